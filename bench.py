@@ -1,0 +1,216 @@
+"""Throughput of the quantized linear-layer path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-extra]
+
+Headline workload: Q4_K decode GEMV, Llama-3-8B FFN shape (14336 x 4096, M = 1). A step is
+one matmul_quant call on device-resident buffers: fp32 -> Q8_0 activation quantization plus
+the GEMV over all 14336 weight rows. The 33 MB weight fits the 256 MB Infinity Cache, so
+steps rotate over enough weight copies (>= 512 MB) that every step reads its weights from
+HBM. value = algorithmic bytes per step / step time, with algorithmic bytes =
+N*(K/256)*144 + 4*K*M + 4*N*M (weights + fp32 x + fp32 y).
+
+roofline: the GEMV kernel alone (pre-quantized activation), timed with HIP events on the
+stream it runs on, against 8 TB/s. cpu_baseline: the reference's own quant.cpp +
+ThreadPool (compiled from its sources into oracle/_ref) running matmul_quant on the same
+workload on this host's cores.
+
+Prints exactly one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5033.0  # 256 CU x 2.4 GHz x 8192 int8 ops / clk / CU (dense)
+ROTATE_BYTES = 512 << 20
+
+
+def algo_bytes(qt, n, k, m):
+    from cllm_inference_amd import synth as S
+    return n * S.row_bytes(qt, k) + 4 * k * m + 4 * n * m
+
+
+def _events():
+    import torch
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_loop(fn, steps, warmup):
+    """Average ms per call of fn(i) over `steps` calls on torch's current stream."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = _events()
+    a.record()
+    for i in range(steps):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def rotated_weights(w_np, copies):
+    import torch
+    base = torch.from_numpy(w_np).cuda()
+    return [base] + [base.clone() for _ in range(copies - 1)]
+
+
+def decode_point(C, S, cfg, label, m, steps, warmup, cold=True):
+    """One decode workload: returns dict with step and GEMV-kernel timings."""
+    import torch
+    qt, n, k, w = S.config_weight(cfg, label)
+    x = torch.from_numpy(S.config_activation(cfg, m, k)).cuda()
+    copies = max(2, -(-ROTATE_BYTES // w.size)) if cold else 1
+    ws = rotated_weights(w, copies)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    qs, sc, bs = C.quantize_q8_0_dev(x)
+
+    def step(i):
+        C.matmul_quant_dev(x, ws[i % copies], qt, None, k, n, y=y)
+
+    def gemv(i):
+        C.gemv_q8_dev(ws[i % copies], qt, k, n, qs, sc, bs, None, y=y)
+
+    ms_step = time_loop(step, steps, warmup)
+    ms_gemv = time_loop(gemv, steps, warmup)
+    nbytes = algo_bytes(qt, n, k, m)
+    del ws
+    torch.cuda.empty_cache()
+    return dict(type=S.TYPE_NAMES[qt], n=n, k=k, m=m, copies=copies, bytes=nbytes,
+                ms_step=ms_step, ms_gemv=ms_gemv,
+                gbs_step=nbytes / ms_step / 1e6, gbs_gemv=nbytes / ms_gemv / 1e6,
+                route=C.matmul_route(qt, k, n, m))
+
+
+def cpu_baseline(S, cfg, label, seconds=10.0):
+    """The reference's matmul_quant (AVX2 + ThreadPool) on this host, bounded sample."""
+    import oracle
+    ref = oracle.reference_or_none()
+    kind = "reference"
+    lib = ref
+    if lib is None:
+        lib, kind = oracle.Oracle(), "port"
+    qt, n, k, w = S.config_weight(cfg, label)
+    x = S.config_activation(cfg, 1, k)
+    threads = min(16, os.cpu_count() or 1)
+    lib.matmul(x, w, qt, None, k, n, 1, threads=threads)  # warm-up
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        lib.matmul(x, w, qt, None, k, n, 1, threads=threads)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    nbytes = algo_bytes(qt, n, k, 1)
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": kind,
+            "sample": f"{len(times)} matmul_quant calls on the same {S.TYPE_NAMES[qt]} {n}x{k} "
+                      f"M=1 workload (activation quantization included), median "
+                      f"{med * 1e3:.2f} ms, {threads} ThreadPool workers"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this path is not sharded across GPUs in this build "
+              "(see the sharding design notes); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import cllm_inference_amd as C
+    from cllm_inference_amd import synth as S
+
+    lib = C.load_library()
+    assert lib.cllm_hip_init(0) == 0, lib.cllm_hip_last_error().decode()
+
+    head = decode_point(C, S, "c1_q4_k_gemv", "ffn", 1, args.steps, args.warmup, cold=True)
+    extra = {}
+    if not args.no_extra:
+        warm = decode_point(C, S, "c1_q4_k_gemv", "ffn", 1, args.steps, args.warmup, cold=False)
+        extra["c1_q4_k_warm_mall_gbs"] = round(warm["gbs_gemv"], 1)
+        c2 = decode_point(C, S, "c2_q6_k_head", "output", 1, max(20, args.steps // 4),
+                          max(3, args.warmup // 4), cold=True)
+        extra["c2_q6_k_head"] = {"gemv_gbs": round(c2["gbs_gemv"], 1),
+                                 "gemv_frac_hbm": round(c2["gbs_gemv"] / HBM_PEAK_GBS, 4),
+                                 "step_gbs": round(c2["gbs_step"], 1),
+                                 "gemv_us": round(c2["ms_gemv"] * 1e3, 2),
+                                 "tokens_per_s": round(1e3 / c2["ms_step"], 1)}
+        c0 = decode_point(C, S, "c0_q8_0_gemv", "w", 1, args.steps, args.warmup, cold=False)
+        extra["c0_q8_0_l2_resident"] = {"gemv_gbs": round(c0["gbs_gemv"], 1),
+                                        "gemv_us": round(c0["ms_gemv"] * 1e3, 2),
+                                        "step_us": round(c0["ms_step"] * 1e3, 2)}
+        sweep = {}
+        for label in ("q5_k", "q8_0"):
+            for m in (1, 4, 16, 64, 256):
+                p = decode_point(C, S, "c4_m_sweep", label, m, max(20, args.steps // 4),
+                                 max(3, args.warmup // 4), cold=True)
+                qt = S.NAME_TO_TYPE[p["type"]]
+                ops = 2.0 * m * p["n"] * p["k"]
+                sweep[f"{label}_m{m}"] = {
+                    "route": p["route"], "us": round(p["ms_step"] * 1e3, 2),
+                    "gbs": round(p["gbs_step"], 1),
+                    "frac_hbm": round(p["gbs_step"] / HBM_PEAK_GBS, 4),
+                    "tops": round(ops / p["ms_step"] / 1e9, 2),
+                    "frac_int8": round(ops / p["ms_step"] / 1e9 / INT8_PEAK_TOPS, 4)}
+        extra["c4_m_sweep"] = sweep
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(S, "c1_q4_k_gemv", "ffn", seconds=args.cpu_seconds)
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_c1_q4_k_gemv.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    out = {
+        "metric": "Q4_K decode GEMV HBM throughput (14336x4096, M=1)",
+        "value": round(head["gbs_step"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded GGUF Q4_K blocks, N(0,1) fp32 activations)",
+        "config": {"workload": "Q4_K decode GEMV 14336x4096 M=1, Llama-3-8B FFN shape; "
+                               f"{head['copies']} rotating weight copies so each step reads HBM",
+                   "type": "Q4_K", "out_dim": 14336, "in_dim": 4096, "n_rows": 1,
+                   "algorithmic_bytes_per_step": head["bytes"]},
+        "frac_of_hbm_peak": round(head["gbs_step"] / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(1e3 / head["ms_step"], 1),
+        "roofline": {"bound": "hbm", "achieved": round(head["gbs_gemv"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs_gemv"] / HBM_PEAK_GBS, 4),
+                     "kernel": "k_gemv<Q4_K> (pre-quantized activation)",
+                     "kernel_us": round(head["ms_gemv"] * 1e3, 3),
+                     "traffic": traffic},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,224 @@
+"""cllm_inference_amd -- the quantized linear-layer path of cllm_inference on MI355X (gfx950).
+
+Python mirror of the reference's Quant API (include/cllm/core/quant.hpp:90-151 in the
+reference) over the C ABI of libcllm_hip.so (include/cllm_hip.h). Same names, argument
+meaning and error behaviour: failures raise RuntimeError with the reference's messages.
+
+Host-array functions take and return numpy arrays and are synchronous, like the reference.
+The *_dev functions take torch tensors already on the GPU and enqueue on torch's current
+stream. There is no CPU fallback: if the HIP library is not built, importing the functions
+works but every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcllm_hip.so")
+QUANT_LIB_PATH = os.path.join(_HERE, "libcllm_quant.so")
+
+
+class GgmlType(enum.IntEnum):
+    """GGUF tensor type ids (reference include/cllm/core/quant.hpp:13-27)."""
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
+    Q8_0 = 8
+    Q8_1 = 9
+    Q2_K = 10
+    Q3_K = 11
+    Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
+
+
+# Every symbol include/cllm_hip.h declares: (name, restype, argtypes).
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_U = ctypes.c_uint32
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+SIGNATURES = {
+    "cllm_hip_init": (_I, [_I]),
+    "cllm_hip_last_error": (ctypes.c_char_p, []),
+    "cllm_hip_block_size": (_I, [_U]),
+    "cllm_hip_type_size": (_SZ, [_U]),
+    "cllm_hip_has_vec_dot": (_I, [_U]),
+    "cllm_hip_quantize_row_q8_0": (_I, [_P, _I64, _I, _P, _P, _P]),
+    "cllm_hip_vec_dot_rows": (_I, [_P, _U, _I64, _I, _P, _P, _P, _P]),
+    "cllm_hip_matmul_quant": (_I, [_P, _P, _U, _P, _I, _I, _P]),
+    "cllm_hip_matmul_quant_batch": (_I, [_P, _P, _U, _P, _I, _I, _I, _P]),
+    "cllm_hip_register_weights": (_I, [_P, _SZ]),
+    "cllm_hip_unregister_weights": (_I, [_P]),
+    "cllm_hip_quantize_q8_0_dev": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
+    "cllm_hip_gemv_q8_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "cllm_hip_matmul_quant_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
+    "cllm_hip_matmul_route": (ctypes.c_char_p, [_U, _I, _I, _I]),
+}
+
+_lib_handle = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads libcllm_hip.so (once) and declares every C-ABI signature."""
+    global _lib_handle
+    if _lib_handle is None:
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"{path} is missing: build it with `python -m cllm_inference_amd.build`")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib_handle = lib
+    return _lib_handle
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        msg = load_library().cllm_hip_last_error().decode()
+        raise RuntimeError(msg)
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def block_size(t: int) -> int:
+    return load_library().cllm_hip_block_size(int(t))
+
+
+def type_size(t: int) -> int:
+    return load_library().cllm_hip_type_size(int(t))
+
+
+def has_vec_dot(t: int) -> bool:
+    return bool(load_library().cllm_hip_has_vec_dot(int(t)))
+
+
+@dataclass
+class QuantizedQ8_0:
+    """Q8_0 activation rows (reference quant.hpp:118-124): fp32 scales, int8 qs, int32
+    per-block sums of qs."""
+    scales: np.ndarray
+    qs: np.ndarray
+    bsums: np.ndarray
+    n: int
+
+
+def quantize_row_q8_0(x: np.ndarray, n: int | None = None) -> QuantizedQ8_0:
+    """fp32 -> Q8_0. x is one row of n floats, or an (m, n) array quantized row by row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows = x.reshape(-1, x.shape[-1]) if x.ndim > 1 else x.reshape(1, -1)
+    n = rows.shape[1] if n is None else int(n)
+    m = rows.shape[0] if x.ndim > 1 else 1
+    qs = np.empty((m, n), dtype=np.int8)
+    sc = np.empty((m, max(n // 32, 0)), dtype=np.float32)
+    bs = np.empty((m, max(n // 32, 0)), dtype=np.int32)
+    _check(load_library().cllm_hip_quantize_row_q8_0(_ptr(rows), n, m, _ptr(qs), _ptr(sc),
+                                                     _ptr(bs)))
+    if x.ndim == 1:
+        qs, sc, bs = qs[0], sc[0], bs[0]
+    return QuantizedQ8_0(scales=sc, qs=qs, bsums=bs, n=n)
+
+
+def vec_dot_rows(w: np.ndarray, t: int, qx: QuantizedQ8_0, n: int, n_w_rows: int = 1) -> np.ndarray:
+    """vec_dot_row over n_w_rows consecutive weight rows starting at w."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    out = np.empty(n_w_rows, dtype=np.float32)
+    _check(load_library().cllm_hip_vec_dot_rows(
+        _ptr(w), int(t), int(n), int(n_w_rows), _ptr(np.ascontiguousarray(qx.qs)),
+        _ptr(np.ascontiguousarray(qx.scales)), _ptr(np.ascontiguousarray(qx.bsums)), _ptr(out)))
+    return out
+
+
+def vec_dot_row(w_row: np.ndarray, t: int, qx: QuantizedQ8_0, n: int) -> float:
+    """Reference quant.hpp:135-136."""
+    return float(vec_dot_rows(w_row, t, qx, n, 1)[0])
+
+
+def matmul_quant(x: np.ndarray, w: np.ndarray, t: int, bias: np.ndarray | None, in_dim: int,
+                 out_dim: int) -> np.ndarray:
+    """y[out_dim] = x . W^T (+ bias) -- reference quant.hpp:143-145."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    y = np.empty(out_dim, dtype=np.float32)
+    _check(load_library().cllm_hip_matmul_quant(_ptr(x), _ptr(w), int(t), _ptr(b), int(in_dim),
+                                                int(out_dim), _ptr(y)))
+    return y
+
+
+def matmul_quant_batch(x: np.ndarray, w: np.ndarray, t: int, bias: np.ndarray | None,
+                       in_dim: int, out_dim: int, n_rows: int) -> np.ndarray:
+    """y[n_rows, out_dim] = X . W^T (+ bias) -- reference quant.hpp:149-151."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    y = np.zeros((max(n_rows, 0), out_dim), dtype=np.float32)
+    _check(load_library().cllm_hip_matmul_quant_batch(_ptr(x), _ptr(w), int(t), _ptr(b),
+                                                      int(in_dim), int(out_dim), int(n_rows),
+                                                      _ptr(y)))
+    return y
+
+
+# ---- device (torch) entry points --------------------------------------------------------
+
+def _tp(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def quantize_q8_0_dev(x, qs=None, scales=None, bsums=None):
+    """x: float32 (m, k) CUDA tensor -> (qs int8 (m, k), scales f32 (m, k/32), bsums i32)."""
+    import torch
+    m, k = x.shape
+    if qs is None:
+        qs = torch.empty((m, k), dtype=torch.int8, device=x.device)
+        scales = torch.empty((m, k // 32), dtype=torch.float32, device=x.device)
+        bsums = torch.empty((m, k // 32), dtype=torch.int32, device=x.device)
+    _check(load_library().cllm_hip_quantize_q8_0_dev(_tp(x), k, m, _tp(qs), _tp(scales),
+                                                     _tp(bsums), _stream()))
+    return qs, scales, bsums
+
+
+def gemv_q8_dev(w, t: int, in_dim: int, out_dim: int, qs, scales, bsums, bias=None, y=None):
+    """vec_dot of every weight row against already-quantized activation rows (device)."""
+    import torch
+    m = qs.shape[0]
+    if y is None:
+        y = torch.empty((m, out_dim), dtype=torch.float32, device=qs.device)
+    _check(load_library().cllm_hip_gemv_q8_dev(_tp(w), int(t), int(in_dim), int(out_dim), int(m),
+                                               _tp(qs), _tp(scales), _tp(bsums), _tp(bias),
+                                               _tp(y), _stream()))
+    return y
+
+
+def matmul_quant_dev(x, w, t: int, bias, in_dim: int, out_dim: int, y=None):
+    """matmul_quant_batch on device tensors: x float32 (m, in_dim), w uint8 GGUF blocks."""
+    import torch
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, out_dim), dtype=torch.float32, device=x.device)
+    _check(load_library().cllm_hip_matmul_quant_dev(_tp(x), _tp(w), int(t), _tp(bias),
+                                                    int(in_dim), int(out_dim), int(m), _tp(y),
+                                                    _stream()))
+    return y
+
+
+def matmul_route(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:
+    return load_library().cllm_hip_matmul_route(int(t), int(in_dim), int(out_dim),
+                                                int(n_rows)).decode()

@@ -1,0 +1,424 @@
+// capi.hip -- the extern "C" boundary of libcllm_hip.so (declared in include/cllm_hip.h).
+//
+// Host-pointer entry points follow the reference's synchronous contract
+// (src/core/quant.cpp:1374-1475): validate in the reference's order with its messages,
+// quantize the activation rows once, run every weight row against them, return with y
+// written. Device-pointer entry points do the same work stream-ordered.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+
+#include "../../include/cllm_hip.h"
+#include "ggml_blocks.h"
+#include "launch.h"
+
+using namespace cllm_hip;
+
+namespace {
+
+thread_local char g_err[512] = "";
+thread_local int g_device = -1;
+
+// Minimum activation rows for the int8-MFMA path; below it the weight-streaming GEMV wins.
+constexpr int kMfmaMinRows = 16;
+
+int set_err(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int set_err(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                        \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return set_err(CLLM_HIP_E_RUNTIME, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+// A device allocation that only grows.
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    // Grows to at least `bytes`. `stream` is synchronised first so no queued kernel still
+    // reads the old allocation.
+    hipError_t ensure(size_t bytes, hipStream_t stream) {
+        if (bytes <= cap) return hipSuccess;
+        size_t want = cap ? cap : (size_t)1 << 20;
+        while (want < bytes) want *= 2;
+        if (p) {
+            hipError_t e = hipStreamSynchronize(stream);
+            if (e != hipSuccess) return e;
+            e = hipFree(p);
+            if (e != hipSuccess) return e;
+            p = nullptr;
+            cap = 0;
+        }
+        hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) return e;
+        cap = want;
+        return hipSuccess;
+    }
+};
+
+// Q8_0 activation workspace: qs[m*k] | scales[m*k/32] | bsums[m*k/32].
+struct Workspace {
+    DevBuf buf;
+    int8_t* qs = nullptr;
+    float* sc = nullptr;
+    int32_t* bs = nullptr;
+    hipError_t ensure(int k, int m, hipStream_t stream) {
+        const size_t n = (size_t)k * (size_t)m;
+        const size_t qs_bytes = (n + 255) & ~(size_t)255;
+        const size_t sc_bytes = ((n / 32) * 4 + 255) & ~(size_t)255;
+        hipError_t e = buf.ensure(qs_bytes + 2 * sc_bytes, stream);
+        if (e != hipSuccess) return e;
+        qs = (int8_t*)buf.p;
+        sc = (float*)((char*)buf.p + qs_bytes);
+        bs = (int32_t*)((char*)buf.p + qs_bytes + sc_bytes);
+        return hipSuccess;
+    }
+};
+
+struct Region {
+    size_t bytes;
+    void* dev;
+};
+
+struct DeviceState {
+    std::mutex mtx;
+    hipStream_t stream = nullptr;
+    DevBuf x, y, bias, wstage, qin;
+    Workspace act;
+    std::map<uintptr_t, Region> regions;  // host base -> device copy
+    std::map<hipStream_t, std::unique_ptr<Workspace>> dev_ws;
+};
+
+std::mutex g_states_mtx;
+std::map<int, std::unique_ptr<DeviceState>> g_states;
+
+int current_device() { return g_device < 0 ? 0 : g_device; }
+
+// Makes the calling thread's device current and returns its state (created on first use).
+int acquire(DeviceState** out) {
+    const int dev = current_device();
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+        (void)hipGetLastError();
+        return set_err(CLLM_HIP_E_NODEV, "cllm_hip: no HIP device available");
+    }
+    if (dev >= count) return set_err(CLLM_HIP_E_NODEV, "cllm_hip: device %d not present", dev);
+    HIP_TRY(hipSetDevice(dev));
+    std::lock_guard<std::mutex> lk(g_states_mtx);
+    auto it = g_states.find(dev);
+    if (it == g_states.end()) {
+        hipDeviceProp_t prop;
+        HIP_TRY(hipGetDeviceProperties(&prop, dev));
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            return set_err(CLLM_HIP_E_NODEV,
+                           "cllm_hip: device %d is %s; this library is built for gfx950 only", dev,
+                           prop.gcnArchName);
+        auto st = std::make_unique<DeviceState>();
+        HIP_TRY(hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking));
+        it = g_states.emplace(dev, std::move(st)).first;
+    }
+    *out = it->second.get();
+    return CLLM_HIP_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+size_t row_bytes(uint32_t type, int in_dim) {
+    return (size_t)(in_dim / block_elems(type)) * block_bytes(type);
+}
+
+// The reference's checks, in its order (quant.cpp:1376-1380 / 1441-1444, 1370).
+int check_matmul(const char* who, uint32_t type, int in_dim, int out_dim) {
+    const int bs = block_elems(type);
+    if (bs <= 0 || in_dim <= 0 || in_dim % bs != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "%s: in_dim not divisible by block size", who);
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if (out_dim < 0) return set_err(CLLM_HIP_E_ARG, "%s: negative out_dim", who);
+    return CLLM_HIP_OK;
+}
+
+bool is_device_ptr(const void* p) {
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return attr.type == hipMemoryTypeDevice;
+}
+
+// Device address of `bytes` of weights at host/device pointer w. Registered regions resolve
+// by offset; device pointers pass through; anything else is copied into a staging buffer.
+int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t** dev) {
+    const uintptr_t a = (uintptr_t)w;
+    auto it = st->regions.upper_bound(a);
+    if (it != st->regions.begin()) {
+        --it;
+        if (a >= it->first && a + bytes <= it->first + it->second.bytes) {
+            *dev = (const uint8_t*)it->second.dev + (a - it->first);
+            if (!aligned16(*dev))
+                return set_err(CLLM_HIP_E_ARG, "cllm_hip: weight pointer is not 16-byte aligned");
+            return CLLM_HIP_OK;
+        }
+    }
+    if (is_device_ptr(w)) {
+        if (!aligned16(w))
+            return set_err(CLLM_HIP_E_ARG, "cllm_hip: weight pointer is not 16-byte aligned");
+        *dev = (const uint8_t*)w;
+        return CLLM_HIP_OK;
+    }
+    HIP_TRY(st->wstage.ensure(bytes, st->stream));
+    HIP_TRY(hipMemcpyAsync(st->wstage.p, w, bytes, hipMemcpyHostToDevice, st->stream));
+    *dev = (const uint8_t*)st->wstage.p;
+    return CLLM_HIP_OK;
+}
+
+bool use_mfma(uint32_t type, int m) { return m >= kMfmaMinRows && gemm_supported(type); }
+
+hipError_t run_linear(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
+                      const float* sc, const int32_t* bs, const float* bias, float* y,
+                      hipStream_t stream) {
+    if (use_mfma(type, m)) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+    return launch_gemv(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+}
+
+// Host-buffer matmul shared by matmul_quant and matmul_quant_batch.
+int host_matmul(const char* who, const float* x, const void* w, uint32_t type, const float* bias,
+                int in_dim, int out_dim, int n_rows, float* y) {
+    int rc = check_matmul(who, type, in_dim, out_dim);
+    if (rc) return rc;
+    if (!x || !w || !y) return set_err(CLLM_HIP_E_ARG, "%s: null pointer", who);
+    if (out_dim == 0) return CLLM_HIP_OK;
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    std::lock_guard<std::mutex> lk(st->mtx);
+    const size_t xb = (size_t)n_rows * in_dim * sizeof(float);
+    const size_t yb = (size_t)n_rows * out_dim * sizeof(float);
+    const uint8_t* wd = nullptr;
+    if ((rc = resolve_weights(st, w, row_bytes(type, in_dim) * (size_t)out_dim, &wd))) return rc;
+    HIP_TRY(st->x.ensure(xb, st->stream));
+    HIP_TRY(st->y.ensure(yb, st->stream));
+    HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
+    HIP_TRY(hipMemcpyAsync(st->x.p, x, xb, hipMemcpyHostToDevice, st->stream));
+    const float* bd = nullptr;
+    if (bias) {
+        HIP_TRY(st->bias.ensure((size_t)out_dim * sizeof(float), st->stream));
+        HIP_TRY(hipMemcpyAsync(st->bias.p, bias, (size_t)out_dim * sizeof(float),
+                               hipMemcpyHostToDevice, st->stream));
+        bd = (const float*)st->bias.p;
+    }
+    HIP_TRY(launch_quantize_q8_0((const float*)st->x.p, (int64_t)n_rows * in_dim / 32,
+                                 st->act.qs, st->act.sc, st->act.bs, st->stream));
+    HIP_TRY(run_linear(type, wd, in_dim, out_dim, n_rows, st->act.qs, st->act.sc, st->act.bs, bd,
+                       (float*)st->y.p, st->stream));
+    HIP_TRY(hipMemcpyAsync(y, st->y.p, yb, hipMemcpyDeviceToHost, st->stream));
+    HIP_TRY(hipStreamSynchronize(st->stream));
+    return CLLM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cllm_hip_init(int device) {
+    if (device < 0) return set_err(CLLM_HIP_E_ARG, "cllm_hip_init: negative device");
+    g_device = device;
+    DeviceState* st;
+    return acquire(&st);
+}
+
+const char* cllm_hip_last_error(void) { return g_err; }
+
+int cllm_hip_block_size(uint32_t type) { return block_elems(type); }
+size_t cllm_hip_type_size(uint32_t type) { return block_bytes(type); }
+int cllm_hip_has_vec_dot(uint32_t type) { return has_kernel(type) ? 1 : 0; }
+
+int cllm_hip_quantize_row_q8_0(const float* x, int64_t n, int n_rows, int8_t* qs, float* scales,
+                               int32_t* bsums) {
+    if (n < 0 || n % 32 != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "quantize_row_q8_0: n not divisible by 32");
+    if (n_rows <= 0 || n == 0) return CLLM_HIP_OK;
+    if (!x || !qs || !scales || !bsums)
+        return set_err(CLLM_HIP_E_ARG, "quantize_row_q8_0: null pointer");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(st->mtx);
+    const size_t total = (size_t)n * n_rows;
+    if (total / 32 > (size_t)INT32_MAX * 32)
+        return set_err(CLLM_HIP_E_ARG, "quantize_row_q8_0: too many elements");
+    HIP_TRY(st->x.ensure(total * sizeof(float), st->stream));
+    HIP_TRY(st->act.ensure((int)n, n_rows, st->stream));
+    HIP_TRY(hipMemcpyAsync(st->x.p, x, total * sizeof(float), hipMemcpyHostToDevice, st->stream));
+    HIP_TRY(launch_quantize_q8_0((const float*)st->x.p, (int64_t)(total / 32), st->act.qs,
+                                 st->act.sc, st->act.bs, st->stream));
+    HIP_TRY(hipMemcpyAsync(qs, st->act.qs, total, hipMemcpyDeviceToHost, st->stream));
+    HIP_TRY(hipMemcpyAsync(scales, st->act.sc, total / 32 * sizeof(float), hipMemcpyDeviceToHost,
+                           st->stream));
+    HIP_TRY(hipMemcpyAsync(bsums, st->act.bs, total / 32 * sizeof(int32_t), hipMemcpyDeviceToHost,
+                           st->stream));
+    HIP_TRY(hipStreamSynchronize(st->stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_vec_dot_rows(const void* w, uint32_t type, int64_t n, int n_w_rows,
+                          const int8_t* qs, const float* scales, const int32_t* bsums,
+                          float* out) {
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if (n <= 0 || n % block_elems(type) != 0 || n > INT32_MAX)
+        return set_err(CLLM_HIP_E_SHAPE, "vec_dot_row: n not divisible by block size");
+    if (n_w_rows <= 0) return CLLM_HIP_OK;
+    if (!w || !qs || !scales || !bsums || !out)
+        return set_err(CLLM_HIP_E_ARG, "vec_dot_row: null pointer");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(st->mtx);
+    const int k = (int)n;
+    const uint8_t* wd = nullptr;
+    if ((rc = resolve_weights(st, w, row_bytes(type, k) * (size_t)n_w_rows, &wd))) return rc;
+    HIP_TRY(st->act.ensure(k, 1, st->stream));
+    HIP_TRY(st->y.ensure((size_t)n_w_rows * sizeof(float), st->stream));
+    HIP_TRY(hipMemcpyAsync(st->act.qs, qs, (size_t)k, hipMemcpyHostToDevice, st->stream));
+    HIP_TRY(hipMemcpyAsync(st->act.sc, scales, (size_t)k / 32 * sizeof(float),
+                           hipMemcpyHostToDevice, st->stream));
+    HIP_TRY(hipMemcpyAsync(st->act.bs, bsums, (size_t)k / 32 * sizeof(int32_t),
+                           hipMemcpyHostToDevice, st->stream));
+    HIP_TRY(launch_gemv(type, wd, k, n_w_rows, 1, st->act.qs, st->act.sc, st->act.bs, nullptr,
+                        (float*)st->y.p, st->stream));
+    HIP_TRY(hipMemcpyAsync(out, st->y.p, (size_t)n_w_rows * sizeof(float), hipMemcpyDeviceToHost,
+                           st->stream));
+    HIP_TRY(hipStreamSynchronize(st->stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_matmul_quant(const float* x, const void* w, uint32_t type, const float* bias,
+                          int in_dim, int out_dim, float* y) {
+    return host_matmul("matmul_quant", x, w, type, bias, in_dim, out_dim, 1, y);
+}
+
+int cllm_hip_matmul_quant_batch(const float* x, const void* w, uint32_t type, const float* bias,
+                                int in_dim, int out_dim, int n_rows, float* y) {
+    if (n_rows <= 0) return CLLM_HIP_OK;  // quant.cpp:1436
+    if (n_rows == 1) return cllm_hip_matmul_quant(x, w, type, bias, in_dim, out_dim, y);
+    return host_matmul("matmul_quant_batch", x, w, type, bias, in_dim, out_dim, n_rows, y);
+}
+
+int cllm_hip_register_weights(const void* host_base, size_t bytes) {
+    if (!host_base || bytes == 0)
+        return set_err(CLLM_HIP_E_ARG, "cllm_hip_register_weights: empty region");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(st->mtx);
+    const uintptr_t a = (uintptr_t)host_base;
+    auto it = st->regions.find(a);
+    if (it != st->regions.end()) {
+        HIP_TRY(hipStreamSynchronize(st->stream));
+        HIP_TRY(hipFree(it->second.dev));
+        st->regions.erase(it);
+    }
+    // Keep the device copy at the same offset modulo 256 as the host base, so host pointers
+    // that are 16-byte aligned stay 16-byte aligned on the device.
+    const size_t lead = a & 255u;
+    void* dev = nullptr;
+    HIP_TRY(hipMalloc(&dev, bytes + lead));
+    HIP_TRY(hipMemcpy((char*)dev + lead, host_base, bytes, hipMemcpyHostToDevice));
+    st->regions[a] = Region{bytes, (char*)dev + lead};
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_unregister_weights(const void* host_base) {
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(st->mtx);
+    auto it = st->regions.find((uintptr_t)host_base);
+    if (it == st->regions.end())
+        return set_err(CLLM_HIP_E_ARG, "cllm_hip_unregister_weights: region not registered");
+    HIP_TRY(hipStreamSynchronize(st->stream));
+    const size_t lead = (uintptr_t)host_base & 255u;
+    HIP_TRY(hipFree((char*)it->second.dev - lead));
+    st->regions.erase(it);
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_quantize_q8_0_dev(const float* x, int64_t n, int n_rows, int8_t* qs, float* scales,
+                               int32_t* bsums, void* stream) {
+    if (n < 0 || n % 32 != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "quantize_row_q8_0: n not divisible by 32");
+    if (n_rows <= 0 || n == 0) return CLLM_HIP_OK;
+    if (!x || !qs || !scales || !bsums)
+        return set_err(CLLM_HIP_E_ARG, "quantize_row_q8_0: null pointer");
+    if (!aligned16(x) || ((uintptr_t)qs & 3u) || ((uintptr_t)scales & 3u) || ((uintptr_t)bsums & 3u))
+        return set_err(CLLM_HIP_E_ARG, "quantize_row_q8_0: misaligned device pointer");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    HIP_TRY(launch_quantize_q8_0(x, n * n_rows / 32, qs, scales, bsums, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, int n_rows,
+                         const int8_t* qs, const float* scales, const int32_t* bsums,
+                         const float* bias, float* y, void* stream) {
+    int rc = check_matmul("matmul_quant", type, in_dim, out_dim);
+    if (rc) return rc;
+    if (n_rows <= 0 || out_dim == 0) return CLLM_HIP_OK;
+    if (!w || !qs || !scales || !bsums || !y)
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(w) || !aligned16(qs) || ((uintptr_t)scales & 7u) || ((uintptr_t)bsums & 7u) ||
+        ((uintptr_t)y & 3u) || ((uintptr_t)bias & 3u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    HIP_TRY(run_linear(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums, bias,
+                       y, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,
+                              int in_dim, int out_dim, int n_rows, float* y, void* stream) {
+    int rc = check_matmul(n_rows > 1 ? "matmul_quant_batch" : "matmul_quant", type, in_dim, out_dim);
+    if (rc) return rc;
+    if (n_rows <= 0 || out_dim == 0) return CLLM_HIP_OK;
+    if (!x || !w || !y) return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(x) || !aligned16(w) || ((uintptr_t)y & 3u) || ((uintptr_t)bias & 3u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    Workspace* ws;
+    {
+        std::lock_guard<std::mutex> lk(st->mtx);
+        auto& slot = st->dev_ws[s];
+        if (!slot) slot = std::make_unique<Workspace>();
+        ws = slot.get();
+        HIP_TRY(ws->ensure(in_dim, n_rows, s));
+    }
+    HIP_TRY(launch_quantize_q8_0(x, (int64_t)n_rows * in_dim / 32, ws->qs, ws->sc, ws->bs, s));
+    HIP_TRY(run_linear(type, (const uint8_t*)w, in_dim, out_dim, n_rows, ws->qs, ws->sc, ws->bs,
+                       bias, y, s));
+    return CLLM_HIP_OK;
+}
+
+const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows) {
+    (void)in_dim;
+    (void)out_dim;
+    if (!has_kernel(type)) return "none";
+    return use_mfma(type, n_rows) ? "mfma" : "gemv";
+}
+
+}  // extern "C"

@@ -1,0 +1,107 @@
+// device_utils.h -- small gfx950 building blocks shared by the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cllm_hip {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// Same vectors with only 4-byte alignment promised: global_load_dwordx{2,4} need dword
+// alignment, not natural alignment.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+    // v_cvt_f32_f16: exact for every fp16 value, subnormals included, like
+    // half_to_float (include/cllm/core/quant.hpp:31-56).
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+__device__ __forceinline__ u32x4 ld_u32x4(const void* p) { return *(const u32x4*)p; }
+__device__ __forceinline__ u32x4 ld_u32x4_nt(const void* p) {
+    return __builtin_nontemporal_load((const u32x4*)p);
+}
+
+// NDW dwords starting at a 2-byte aligned address p, for blocks whose size is not a multiple
+// of 4 (Q8_0 34 B, Q4_0 18 B, Q5_0 22 B, Q6_K 210 B). One dword-aligned vector load of
+// [p - s, p - s + 4*NDW) with s = p & 3 in {0, 2}, plus the 2 bytes at p + 4*NDW - 2, then a
+// funnel shift. Every byte read lies in [p - 2, p + 4*NDW); when s == 2 the two bytes before
+// p exist because p is then at least 2 bytes past a 4-aligned base.
+template <int NDW>
+__device__ __forceinline__ void ld_a2(const uint8_t* p, uint32_t (&out)[NDW]) {
+    const uintptr_t a = (uintptr_t)p;
+    const uint32_t s = (uint32_t)(a & 3u);
+    const uint32_t* q = (const uint32_t*)(a - s);
+    uint32_t v[NDW + 1];
+    if constexpr (NDW % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NDW; i += 4) {
+            const u32x4_a4 t = *(const u32x4_a4*)(q + i);
+            v[i] = t.x; v[i + 1] = t.y; v[i + 2] = t.z; v[i + 3] = t.w;
+        }
+    } else if constexpr (NDW == 2) {
+        const u32x2_a4 t = *(const u32x2_a4*)q;
+        v[0] = t.x; v[1] = t.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < NDW; ++i) v[i] = q[i];
+    }
+    v[NDW] = *(const uint16_t*)(p + 4 * NDW - 2);
+    const uint32_t sel = s;
+#pragma unroll
+    for (int i = 0; i < NDW; ++i) out[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sel);
+}
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *(const uint16_t*)p; }
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// (scale, min) of sub-block j (0..7) from the 12 packed bytes held as dwords s0 = bytes 0-3,
+// s1 = bytes 4-7, s2 = bytes 8-11 (get_scale_min_k4, src/core/quant.cpp:72-80):
+//   j < 4 : sc = q[j] & 63,                          m = q[j+4] & 63
+//   j >= 4: sc = (q[j+4] & 15) | ((q[j-4] >> 6) << 4), m = (q[j+4] >> 4) | ((q[j] >> 6) << 4)
+__device__ __forceinline__ void k4_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                             int& sc, int& m) {
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const uint32_t b0 = (s0 >> sh) & 0xFFu; // q[j & 3]
+    const uint32_t b1 = (s1 >> sh) & 0xFFu; // q[4 + (j & 3)]
+    const uint32_t b2 = (s2 >> sh) & 0xFFu; // q[8 + (j & 3)]
+    const int sc_lo = (int)(b0 & 63u), m_lo = (int)(b1 & 63u);
+    const int sc_hi = (int)((b2 & 15u) | ((b0 >> 6) << 4));
+    const int m_hi = (int)((b2 >> 4) | ((b1 >> 6) << 4));
+    sc = j < 4 ? sc_lo : sc_hi;
+    m = j < 4 ? m_lo : m_hi;
+}
+
+// Cross-lane moves inside a row of 16 lanes (DPP; no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_SWAP1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_SWAP2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+// Sum over all 64 lanes; the result is valid in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<DPP_QUAD_SWAP1>(v);
+    v += dpp_f32<DPP_QUAD_SWAP2>(v);
+    v += dpp_f32<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_f32<DPP_ROW_MIRROR>(v);
+    // four row sums -> all lanes
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+}  // namespace cllm_hip

@@ -1,0 +1,30 @@
+// launch.h -- host-side launchers of the kernels (internal to libcllm_hip.so).
+//
+// Every launcher validates nothing: capi.hip checks shapes, types and alignment before it
+// calls one, so the grid of each launch matches what its kernel indexes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cllm_hip {
+
+// n_blocks consecutive 32-element fp32 blocks -> Q8_0 (qs, fp32 scales, int32 block sums).
+hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* qs, float* scales,
+                                int32_t* bsums, hipStream_t stream);
+
+// y[t, j] = vec_dot(W row j, activation row t) (+ bias[j]) for t < m, j < n.
+// Activation rows are Q8_0: qs[t * k], scales / bsums[t * k / 32]. Any m >= 1.
+hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
+                       const float* scales, const int32_t* bsums, const float* bias, float* y,
+                       hipStream_t stream);
+
+// Same contract as launch_gemv, on the int8 MFMA path (m >= 1, any n; k % 256 == 0 for the
+// K-quants, k % 32 == 0 otherwise). Returns hipErrorNotSupported for types without an MFMA
+// kernel.
+hipError_t launch_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
+                       const float* scales, const int32_t* bsums, const float* bias, float* y,
+                       hipStream_t stream);
+bool gemm_supported(uint32_t type);
+
+}  // namespace cllm_hip

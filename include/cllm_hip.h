@@ -1,0 +1,115 @@
+/*
+ * cllm_hip.h -- C ABI of the MI355X (gfx950) quantized linear-layer path.
+ *
+ * This library replaces the compute behind cllm_inference's Quant API
+ * (include/cllm/core/quant.hpp:90-151, implemented in src/core/quant.cpp:415-1475). Plain
+ * pointers and sizes only: no C++ types, no torch types. The C++20 Quant API itself
+ * (include/cllm/core/quant.hpp in this repository, cllm_inference_amd/csrc/quant_api.cpp)
+ * is a thin wrapper over these functions, and Python reaches them through ctypes.
+ *
+ * Conventions
+ *   - Every function returns CLLM_HIP_OK (0) or one of the CLLM_HIP_E_* codes; the message
+ *     of the last failure on the calling thread is returned by cllm_hip_last_error(). The
+ *     messages of the reference's exceptions are reproduced verbatim where one exists.
+ *   - "type" is a GgmlType id (F32 = 0 ... Q6_K = 14, include/cllm/core/quant.hpp:13-27).
+ *     Only the six types with a vec_dot kernel in the reference (Q4_0, Q5_0, Q8_0, Q4_K,
+ *     Q5_K, Q6_K; src/core/quant.cpp:1347-1357) have GPU kernels here.
+ *   - Weights are GGUF blocks read in place, row-major: out_dim rows of
+ *     (in_dim / block_size) * type_size bytes (src/core/quant.cpp:1381).
+ *   - Functions without the _dev suffix take host pointers and are synchronous, like the
+ *     reference. Functions with the _dev suffix take device pointers, enqueue on the given
+ *     HIP stream (NULL = the null stream) and return without waiting.
+ *   - Device weight pointers must be 16-byte aligned (GGUF data sections are 32-byte
+ *     aligned, gguf.cpp:171-172); device activation and output pointers 16-byte aligned.
+ */
+#ifndef CLLM_HIP_H
+#define CLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CLLM_HIP_OK 0
+#define CLLM_HIP_E_SHAPE 1   /* a dimension is not a multiple of the block size */
+#define CLLM_HIP_E_TYPE 2    /* no kernel for this weight type */
+#define CLLM_HIP_E_ARG 3     /* null or misaligned pointer, negative size */
+#define CLLM_HIP_E_RUNTIME 4 /* HIP runtime failure (allocation, copy, launch) */
+#define CLLM_HIP_E_NODEV 5   /* no usable gfx950 device */
+
+/* Selects the device used by this thread's later calls and builds its per-device state.
+ * Calling it is optional: the first call on a thread uses device 0. No reference
+ * counterpart (the reference is CPU-only). */
+int cllm_hip_init(int device);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* cllm_hip_last_error(void);
+
+/* block_size / type_size: include/cllm/core/quant.hpp:90-93, src/core/quant.cpp:340-369. */
+int cllm_hip_block_size(uint32_t type);
+size_t cllm_hip_type_size(uint32_t type);
+
+/* has_vec_dot: include/cllm/core/quant.hpp:130, src/core/quant.cpp:1347-1357. */
+int cllm_hip_has_vec_dot(uint32_t type);
+
+/* quantize_row_q8_0 over n_rows rows of length n (n % 32 == 0): qs[n_rows * n],
+ * scales[n_rows * n / 32] (fp32), bsums[n_rows * n / 32]. Bit-exact with the reference.
+ * Replaces include/cllm/core/quant.hpp:127 / src/core/quant.cpp:420-452 (which handles one
+ * row; n_rows = 1 is that call). Host buffers. */
+int cllm_hip_quantize_row_q8_0(const float* x, int64_t n, int n_rows, int8_t* qs,
+                               float* scales, int32_t* bsums);
+
+/* vec_dot_row for n_w_rows consecutive weight rows against one Q8_0 activation row:
+ * out[j] = vec_dot_row(w + j * row_bytes, type, qx, n). Replaces
+ * include/cllm/core/quant.hpp:135-136 / src/core/quant.cpp:1359-1372. Host buffers. */
+int cllm_hip_vec_dot_rows(const void* w, uint32_t type, int64_t n, int n_w_rows,
+                          const int8_t* qs, const float* scales, const int32_t* bsums,
+                          float* out);
+
+/* matmul_quant: y[out_dim] = x[in_dim] . W^T (+ bias). Replaces
+ * include/cllm/core/quant.hpp:143-145 / src/core/quant.cpp:1374-1402. Host buffers; w may
+ * also be a device pointer or lie inside a region given to cllm_hip_register_weights. */
+int cllm_hip_matmul_quant(const float* x, const void* w, uint32_t type, const float* bias,
+                          int in_dim, int out_dim, float* y);
+
+/* matmul_quant_batch: y[n_rows, out_dim] row-major. n_rows <= 0 returns without writing y.
+ * Replaces include/cllm/core/quant.hpp:149-151 / src/core/quant.cpp:1433-1469. */
+int cllm_hip_matmul_quant_batch(const float* x, const void* w, uint32_t type,
+                                const float* bias, int in_dim, int out_dim, int n_rows,
+                                float* y);
+
+/* Uploads [host_base, host_base + bytes) -- typically the mmap'd GGUF data section
+ * (gguf.cpp:178-189) -- to the current device once. Later host weight pointers inside the
+ * region resolve to the device copy by offset instead of being copied per call. No
+ * reference counterpart: the reference reads the mmap directly (engine.cpp:189). */
+int cllm_hip_register_weights(const void* host_base, size_t bytes);
+int cllm_hip_unregister_weights(const void* host_base);
+
+/* ---- device-pointer entry points (stream-ordered) ------------------------------------ */
+
+/* quantize_row_q8_0 on device buffers (same layout as cllm_hip_quantize_row_q8_0). */
+int cllm_hip_quantize_q8_0_dev(const float* x, int64_t n, int n_rows, int8_t* qs,
+                               float* scales, int32_t* bsums, void* stream);
+
+/* The vec_dot kernels on an already-quantized activation batch:
+ * y[t, j] = vec_dot_row(w row j, type, qx row t, in_dim) (+ bias[j]), t < n_rows.
+ * This is the inner loop of src/core/quant.cpp:1388-1397 and 1453-1464. */
+int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, int n_rows,
+                         const int8_t* qs, const float* scales, const int32_t* bsums,
+                         const float* bias, float* y, void* stream);
+
+/* matmul_quant_batch on device buffers: quantizes x into a library-owned per-stream
+ * workspace, then runs the GEMV (small n_rows) or the int8-MFMA GEMM (large n_rows). */
+int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,
+                              int in_dim, int out_dim, int n_rows, float* y, void* stream);
+
+/* Name of the kernel family cllm_hip_matmul_quant_dev would run for this shape
+ * ("gemv" or "mfma"); for tests and benchmarks. */
+const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

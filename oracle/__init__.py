@@ -1,0 +1,146 @@
+"""ctypes access to the checkers: the C restatement (liboracle.so) and, where it was built,
+the reference compiled from its own sources (_ref/libcllm_ref.so).
+
+TEST INFRASTRUCTURE ONLY. Imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, always as the checker or the timed CPU baseline, never as the product.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libcllm_ref.so")
+REF_ROOT = "/root/reference"
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_U = ctypes.c_uint32
+_I64 = ctypes.c_int64
+
+
+def build(with_ref: bool = True) -> None:
+    """Compiles liboracle.so, and _ref/libcllm_ref.so when the reference tree is present."""
+    targets = ["all"]
+    if with_ref and os.path.isdir(REF_ROOT):
+        targets.append("ref")
+    subprocess.run(["make", "-s", "-C", HERE, *targets], check=True)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class _Lib:
+    """Common calls of both libraries (prefix 'oracle_' or 'ref_')."""
+
+    def __init__(self, path: str, prefix: str):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        self.lib = ctypes.CDLL(path)
+        self.prefix = prefix
+        sig = {
+            "quantize_row_q8_0": (_I, [_P, _I64, _P, _P, _P]),
+            "matmul_quant": (_I, [_P, _P, _U, _P, _I, _I, _P, _I]),
+            "matmul_quant_batch": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _I]),
+            "dequantize": (_I, [_P, _P, _U, _I64]),
+            "last_error": (ctypes.c_char_p, []),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(self.lib, prefix + name)
+            fn.restype, fn.argtypes = res, args
+
+    def _fn(self, name):
+        return getattr(self.lib, self.prefix + name)
+
+    def _check(self, rc):
+        if rc != 0:
+            raise RuntimeError(self._fn("last_error")().decode())
+
+    def quantize(self, x: np.ndarray):
+        """Row-wise Q8_0 of x (m, k) -> (qs int8 (m, k), scales f32 (m, k/32), bsums i32)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        x2 = x.reshape(-1, x.shape[-1])
+        m, k = x2.shape
+        qs = np.empty((m, k), np.int8)
+        sc = np.empty((m, k // 32), np.float32)
+        bs = np.empty((m, k // 32), np.int32)
+        for t in range(m):
+            self._check(self._fn("quantize_row_q8_0")(_ptr(x2[t]), k, _ptr(qs[t]), _ptr(sc[t]),
+                                                      _ptr(bs[t])))
+        return qs, sc, bs
+
+    def matmul(self, x, w, qtype, bias, k, n, m, threads=0):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        y = np.zeros((max(m, 1), n), np.float32)
+        if m == 1:
+            rc = self._fn("matmul_quant")(_ptr(x), _ptr(w), int(qtype), _ptr(b), int(k), int(n),
+                                          _ptr(y), int(threads))
+        else:
+            rc = self._fn("matmul_quant_batch")(_ptr(x), _ptr(w), int(qtype), _ptr(b), int(k),
+                                                int(n), int(m), _ptr(y), int(threads))
+        self._check(rc)
+        return y
+
+    def dequantize(self, src, qtype, n):
+        out = np.empty(n, np.float32)
+        self._check(self._fn("dequantize")(_ptr(np.ascontiguousarray(src, dtype=np.uint8)),
+                                           _ptr(out), int(qtype), int(n)))
+        return out
+
+
+class Oracle(_Lib):
+    def __init__(self, path: str = ORACLE_SO):
+        super().__init__(path, "oracle_")
+        f = self.lib.oracle_matmul_quant_f64
+        f.restype = _I
+        f.argtypes = [_P, _P, _U, _P, _I, _I, _I, _P, _P]
+
+    def matmul_f64(self, x, w, qtype, bias, k, n, m):
+        """fp64 evaluation and per-output absolute-term sums (tolerance floors)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        y = np.zeros((m, n), np.float64)
+        a = np.zeros((m, n), np.float64)
+        self._check(self.lib.oracle_matmul_quant_f64(_ptr(x), _ptr(w), int(qtype), _ptr(b), int(k),
+                                                     int(n), int(m), _ptr(y), _ptr(a)))
+        return y, a
+
+
+class Reference(_Lib):
+    """The reference's quant.cpp + thread_pool.cpp, compiled unmodified (oracle/Makefile)."""
+
+    def __init__(self, path: str = REF_SO):
+        super().__init__(path, "ref_")
+
+
+def oracle() -> Oracle:
+    return Oracle()
+
+
+def reference_or_none():
+    try:
+        return Reference()
+    except (FileNotFoundError, OSError):
+        return None
+
+
+def rel_err_floored(got: np.ndarray, ref: np.ndarray, abs_sum: np.ndarray, floor_pow: int = -10):
+    """|got - ref| / max(|ref|, 2^floor_pow * abs_sum): the gate used by the parity tests for
+    rows whose output nearly cancels. Returns (max floored relative error, rows that used the
+    floor, max raw relative error)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    floor = abs_sum * 2.0 ** floor_pow
+    denom = np.maximum(np.abs(ref), floor)
+    denom = np.where(denom == 0, 1.0, denom)
+    err = np.abs(got - ref) / denom
+    raw = np.abs(got - ref) / np.where(ref == 0, 1.0, np.abs(ref))
+    return float(err.max(initial=0.0)), int((np.abs(ref) < floor).sum()), float(raw.max(initial=0.0))

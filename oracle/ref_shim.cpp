@@ -1,0 +1,92 @@
+// ref_shim.cpp -- extern "C" entry points over the reference's own Quant API, so that
+// tests/golden/make_golden.py and bench.py's cpu_baseline leg can drive the reference
+// compiled from its unmodified sources (src/core/quant.cpp, src/core/thread_pool.cpp).
+//
+// TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile into oracle/_ref/, never shipped.
+// Interfaces wrapped: include/cllm/core/quant.hpp:90-151, include/cllm/core/thread_pool.hpp:12-24.
+#include "cllm/core/quant.hpp"
+#include "cllm/core/thread_pool.hpp"
+
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <memory>
+#include <mutex>
+
+namespace {
+thread_local char g_err[256];
+std::mutex g_pool_mtx;
+std::unique_ptr<cllm::ThreadPool> g_pool;
+size_t g_pool_threads = 0;
+
+int set_err(const std::exception& e) {
+    std::snprintf(g_err, sizeof g_err, "%s", e.what());
+    return 1;
+}
+
+// n_threads <= 0: no pool (serial, as the reference's tests call it). Otherwise a pool of
+// exactly n_threads workers, kept across calls like the engine keeps its pool.
+cllm::ThreadPool* pool_for(int n_threads) {
+    if (n_threads <= 0) return nullptr;
+    std::lock_guard<std::mutex> lk(g_pool_mtx);
+    if (!g_pool || g_pool_threads != (size_t)n_threads) {
+        g_pool.reset();
+        g_pool = std::make_unique<cllm::ThreadPool>((size_t)n_threads);
+        g_pool_threads = (size_t)n_threads;
+    }
+    return g_pool.get();
+}
+}  // namespace
+
+extern "C" {
+
+const char* ref_last_error(void) { return g_err; }
+
+int ref_block_size(uint32_t t) { return cllm::block_size((cllm::GgmlType)t); }
+size_t ref_type_size(uint32_t t) { return cllm::type_size((cllm::GgmlType)t); }
+int ref_has_vec_dot(uint32_t t) { return cllm::has_vec_dot((cllm::GgmlType)t) ? 1 : 0; }
+
+int ref_quantize_row_q8_0(const float* x, int64_t n, int8_t* qs, float* scales, int32_t* bsums) {
+    try {
+        cllm::QuantizedQ8_0 q;
+        cllm::quantize_row_q8_0(x, q, n);
+        std::memcpy(qs, q.qs.data(), q.qs.size());
+        std::memcpy(scales, q.scales.data(), q.scales.size() * sizeof(float));
+        std::memcpy(bsums, q.bsums.data(), q.bsums.size() * sizeof(int32_t));
+        return 0;
+    } catch (const std::exception& e) {
+        return set_err(e);
+    }
+}
+
+int ref_dequantize(const void* src, float* dst, uint32_t t, int64_t n) {
+    try {
+        cllm::dequantize_block(src, dst, (cllm::GgmlType)t, n);
+        return 0;
+    } catch (const std::exception& e) {
+        return set_err(e);
+    }
+}
+
+int ref_matmul_quant(const float* x, const void* w, uint32_t t, const float* bias, int in_dim,
+                     int out_dim, float* y, int n_threads) {
+    try {
+        cllm::matmul_quant(x, w, (cllm::GgmlType)t, bias, in_dim, out_dim, y, pool_for(n_threads));
+        return 0;
+    } catch (const std::exception& e) {
+        return set_err(e);
+    }
+}
+
+int ref_matmul_quant_batch(const float* x, const void* w, uint32_t t, const float* bias,
+                           int in_dim, int out_dim, int n_rows, float* y, int n_threads) {
+    try {
+        cllm::matmul_quant_batch(x, w, (cllm::GgmlType)t, bias, in_dim, out_dim, n_rows, y,
+                                 pool_for(n_threads));
+        return 0;
+    } catch (const std::exception& e) {
+        return set_err(e);
+    }
+}
+
+}  // extern "C"

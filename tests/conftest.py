@@ -1,0 +1,49 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+def load_golden(name: str) -> dict:
+    with np.load(os.path.join(GOLDEN, name), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def split_cases(data: dict) -> dict:
+    """{'tag__field': arr} -> {tag: {field: arr}}"""
+    out: dict = {}
+    for key, val in data.items():
+        tag, field = key.split("__", 1)
+        out.setdefault(tag, {})[field] = val
+    return out
+
+
+@pytest.fixture(scope="session")
+def orc():
+    import oracle
+    if not os.path.exists(oracle.ORACLE_SO):
+        oracle.build(with_ref=False)
+    return oracle.Oracle()
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The HIP library on device 0; the test fails (never falls back) if it cannot run."""
+    import torch
+    import cllm_inference_amd as C
+    assert torch.cuda.is_available(), "no GPU visible to torch"
+    lib = C.load_library()
+    rc = lib.cllm_hip_init(0)
+    assert rc == 0, lib.cllm_hip_last_error().decode()
+    return C

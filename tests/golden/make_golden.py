@@ -1,0 +1,193 @@
+"""Writes the golden fixtures of tests/golden/ from the reference compiled from its own
+sources (oracle/_ref/libcllm_ref.so, built by `make -C oracle ref`).
+
+Run in a container that has the reference tree:   python tests/golden/make_golden.py
+
+Every fixture holds inputs or the seeds that regenerate them (with a sha256 of the bytes so
+a drift of the generator is caught), and the reference's outputs: Q8_0 activation bytes and
+fp32 y. The GPU parity tests and the oracle tests compare against these files; the
+reference itself never travels.
+"""
+from __future__ import annotations
+
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+import oracle  # noqa: E402
+from cllm_inference_amd import synth as S  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+THREADS = 8
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def special_activation_rows() -> np.ndarray:
+    """Hand-made 32-element blocks for quantize_row_q8_0 edge cases, 4 rows of 128."""
+    rows = np.zeros((4, 128), np.float32)
+    # row 0: amax = 127 -> d = 1, id = 1, q = rint(x): ties go to even
+    rows[0, :32] = [127, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, -1.5, 126.5, -126.5, 0, -0.0,
+                    0.49999997, 0.50000006, 4.5, 5.5, -4.5, 100.25, -100.75, 1, 2, 3, 4, 5, 6, 7,
+                    8, 9, 10, 11, 12]
+    # all-zero block (d = 0, id = 0) and negative zeros
+    rows[0, 32:64] = 0.0
+    rows[0, 64:96] = -0.0
+    # block whose amax is negative
+    rows[0, 96:128] = np.linspace(-3.0, 1.0, 32, dtype=np.float32)
+    # row 1: tiny, subnormal and huge magnitudes
+    rows[1, :32] = np.float32(1e-30) * np.arange(-16, 16, dtype=np.float32)
+    rows[1, 32:64] = np.float32(1e-40) * np.arange(1, 33, dtype=np.float32)
+    rows[1, 64:96] = np.float32(3e37) * np.sin(np.arange(32, dtype=np.float32))
+    rows[1, 96:128] = np.float32(1.0) / np.arange(1, 33, dtype=np.float32)
+    # rows 2-3: random values with exact .5 multiples of a power-of-two scale
+    rng = np.random.default_rng(77)
+    rows[2] = rng.integers(-254, 255, 128).astype(np.float32) * 0.5
+    rows[3] = rng.standard_normal(128).astype(np.float32) * np.float32(1000.0)
+    return rows
+
+
+def quant_fixtures(ref: oracle.Reference) -> None:
+    cases = {
+        "special": special_activation_rows(),
+        "c0": S.config_activation("c0_q8_0_gemv", 1, 896),
+        "c1": S.config_activation("c1_q4_k_gemv", 1, 4096),
+        "c4": S.config_activation("c4_m_sweep", 4, 4096),
+        "c3_down": S.config_activation("c3_q4_k_m_layer", 2, 14336),
+    }
+    data = {}
+    for name, x in cases.items():
+        qs, sc, bs = ref.quantize(x)
+        data[f"{name}__x"] = x
+        data[f"{name}__qs"] = qs
+        data[f"{name}__scales"] = sc
+        data[f"{name}__bsums"] = bs
+    np.savez_compressed(os.path.join(OUT, "q8_act.npz"), **data)
+
+
+def gemv_fixtures(ref: oracle.Reference) -> None:
+    """y of matmul_quant / matmul_quant_batch at the decode workloads."""
+    data = {}
+
+    def add(tag, cfg, label, m, keep_rows):
+        qt, n, k, w = S.config_weight(cfg, label)
+        x = S.config_activation(cfg, m, k)
+        y = ref.matmul(x, w, qt, None, k, n, m, threads=THREADS)
+        data[f"{tag}__meta"] = np.array([qt, n, k, m], np.int64)
+        data[f"{tag}__rows"] = keep_rows(n)
+        data[f"{tag}__y"] = y[:, keep_rows(n)]
+        data[f"{tag}__w_sha"] = np.array(sha(w))
+        data[f"{tag}__x_sha"] = np.array(sha(x))
+        print(tag, qt, n, k, m, flush=True)
+
+    every = lambda n: np.arange(n, dtype=np.int64)  # noqa: E731
+    add("c0", "c0_q8_0_gemv", "w", 1, every)
+    add("c1", "c1_q4_k_gemv", "ffn", 1, every)
+    add("c2", "c2_q6_k_head", "output", 1, lambda n: np.arange(0, n, 16, dtype=np.int64))
+    add("c4_q5_k_m1", "c4_m_sweep", "q5_k", 1, every)
+    add("c4_q5_k_m4", "c4_m_sweep", "q5_k", 4, lambda n: np.arange(0, n, 4, dtype=np.int64))
+    add("c4_q8_0_m1", "c4_m_sweep", "q8_0", 1, every)
+    add("c4_q8_0_m4", "c4_m_sweep", "q8_0", 4, every)
+    np.savez_compressed(os.path.join(OUT, "gemv.npz"), **data)
+
+
+def extra_type_fixtures(ref: oracle.Reference) -> None:
+    """Q4_0 / Q5_0 (in no workload) and odd shapes for every type."""
+    data = {}
+    shapes = [(4096, 4096, 1), (4096, 4096, 4), (1000, 512, 3), (77, 768, 1)]
+    for qt in (S.Q4_0, S.Q5_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K):
+        for (n, k, m) in shapes:
+            if k % S.BLOCK[qt]:
+                continue
+            seed = 900 + qt * 7 + k + m
+            w = S.make_weight(qt, n, k, seed)
+            x = S.make_activation(m, k, seed + 1, outliers=True)
+            bias = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+            y = ref.matmul(x, w, qt, None, k, n, m, threads=THREADS)
+            yb = ref.matmul(x, w, qt, bias, k, n, m, threads=THREADS)
+            tag = f"{S.TYPE_NAMES[qt]}_{n}x{k}_m{m}"
+            data[f"{tag}__meta"] = np.array([qt, n, k, m, seed], np.int64)
+            data[f"{tag}__y"] = y
+            data[f"{tag}__ybias"] = yb
+            data[f"{tag}__w_sha"] = np.array(sha(w))
+            print(tag, flush=True)
+    np.savez_compressed(os.path.join(OUT, "types.npz"), **data)
+
+
+def batch_fixtures(ref: oracle.Reference) -> None:
+    """The prefill layer: first 16 activation rows against the first 512 rows of each
+    matrix (the reference's batch output is row-independent, so slices are exact)."""
+    data = {}
+    cfg = "c3_q4_k_m_layer"
+    for label, qt, n, k in S.CONFIGS[cfg]["mats"]:
+        _, _, _, w = S.config_weight(cfg, label)
+        x = S.config_activation(cfg, 512, k)[:16]
+        rows = min(n, 512)
+        y = ref.matmul(x, w[: rows * S.row_bytes(qt, k)], qt, None, k, rows, 16, threads=THREADS)
+        data[f"{label}__meta"] = np.array([qt, n, k, 16, rows], np.int64)
+        data[f"{label}__y"] = y
+        data[f"{label}__w_sha"] = np.array(sha(w))
+        print(label, flush=True)
+    # M-sweep batch sizes on the Q8_0 4096x4096 matrix: first 512 output rows
+    qt, n, k, w = S.config_weight("c4_m_sweep", "q8_0")
+    for m in (16, 64):
+        x = S.config_activation("c4_m_sweep", m, k)
+        y = ref.matmul(x, w[: 512 * S.row_bytes(qt, k)], qt, None, k, 512, m, threads=THREADS)
+        data[f"c4_q8_0_m{m}__y"] = y
+    qt, n, k, w = S.config_weight("c4_m_sweep", "q5_k")
+    for m in (16, 64):
+        x = S.config_activation("c4_m_sweep", m, k)
+        y = ref.matmul(x, w[: 512 * S.row_bytes(qt, k)], qt, None, k, 512, m, threads=THREADS)
+        data[f"c4_q5_k_m{m}__y"] = y
+    np.savez_compressed(os.path.join(OUT, "batch.npz"), **data)
+
+
+def refkat_fixtures(ref: oracle.Reference) -> None:
+    """Outputs of the reference on the inputs its own tests build (tests/quant_test.cpp:237-361):
+    weight bytes (k + blk + j) % 7 after a leading fp16 1.0, x = ((i % 5) - 2) * 0.5."""
+    data = {}
+    for qt in (S.Q4_0, S.Q5_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K):
+        bs, ts = S.BLOCK[qt], S.TYPE_SIZE[qt]
+        k = 64 if bs <= 32 else 256
+        n = 40
+        rb = (k // bs) * ts
+        w = np.zeros(rb * n, np.uint8)
+        for j in range(n):
+            for blk in range(k // bs):
+                p = j * rb + blk * ts
+                w[p], w[p + 1] = 0x00, 0x3C
+                for kk in range(2, ts):
+                    w[p + kk] = (kk + blk + j) % 7
+        x1 = (((np.arange(k) % 5) - 2) * 0.5).astype(np.float32)
+        x3 = np.stack([((((np.arange(k) + t) % 5) - 2) * 0.5).astype(np.float32) for t in range(3)])
+        name = S.TYPE_NAMES[qt]
+        data[f"{name}__w"] = w
+        data[f"{name}__x1"] = x1
+        data[f"{name}__y1"] = ref.matmul(x1, w, qt, None, k, n, 1)
+        data[f"{name}__x3"] = x3
+        data[f"{name}__y3"] = ref.matmul(x3, w, qt, None, k, n, 3)
+    np.savez_compressed(os.path.join(OUT, "refkat.npz"), **data)
+
+
+def main() -> None:
+    oracle.build(with_ref=True)
+    ref = oracle.Reference()
+    quant_fixtures(ref)
+    refkat_fixtures(ref)
+    extra_type_fixtures(ref)
+    gemv_fixtures(ref)
+    batch_fixtures(ref)
+    for f in sorted(os.listdir(OUT)):
+        if f.endswith(".npz"):
+            print(f, os.path.getsize(os.path.join(OUT, f)))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,91 @@
+"""Independent numpy decoder of the six GGUF block layouts, written from the byte-layout
+descriptions (element order, nibble order, scale packing) rather than from any kernel.
+
+decode(w, qtype, n, k) -> (q, scale, wmin), each (n, k):
+    weight value = scale * q - wmin      (float64 exact; q is the stored integer)
+Q4_0 / Q5_0 / Q6_K return q with their offsets (-8, -16, -32) already applied.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 6, 8, 12, 13, 14
+TS = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BS = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+
+
+def _f16(b: np.ndarray) -> np.ndarray:
+    """(nblk, 2) little-endian fp16 bytes -> (nblk,) float64."""
+    return np.ascontiguousarray(b).view(np.float16)[:, 0].astype(np.float64)
+
+
+def _k4_scales(sc12: np.ndarray):
+    """(nblk, 12) packed bytes -> (nblk, 8) scales and mins, 6 bits each.
+    Sub-blocks 0-3: low 6 bits of bytes 0-3 (scale) and 4-7 (min). Sub-blocks 4-7: low /
+    high nibble of bytes 8-11 give the low 4 bits of scale / min, and the top two bits of
+    bytes 0-3 (scale) and 4-7 (min) give bits 4-5."""
+    s = sc12.astype(np.int64)
+    sc = np.zeros((s.shape[0], 8), np.int64)
+    mn = np.zeros((s.shape[0], 8), np.int64)
+    sc[:, :4] = s[:, 0:4] & 63
+    mn[:, :4] = s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    return sc, mn
+
+
+def decode(w: np.ndarray, qtype: int, n: int, k: int):
+    nb = k // BS[qtype]
+    blk = np.asarray(w, np.uint8)[: n * nb * TS[qtype]].reshape(n * nb, TS[qtype])
+    nblk = blk.shape[0]
+    if qtype == Q8_0:
+        d = _f16(blk[:, 0:2])
+        q = blk[:, 2:34].view(np.int8).astype(np.int64)
+        scale = np.repeat(d[:, None], 32, axis=1)
+        wmin = np.zeros_like(scale)
+    elif qtype in (Q4_0, Q5_0):
+        d = _f16(blk[:, 0:2])
+        qs = blk[:, 6:22] if qtype == Q5_0 else blk[:, 2:18]
+        q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.int64)  # elems 0-15, 16-31
+        if qtype == Q5_0:
+            qh = blk[:, 2:6].astype(np.uint32)
+            bits = qh[:, 0] | (qh[:, 1] << 8) | (qh[:, 2] << 16) | (qh[:, 3] << 24)
+            hb = (bits[:, None] >> np.arange(32, dtype=np.uint32)[None, :]) & 1
+            q = (q | (hb.astype(np.int64) << 4)) - 16
+        else:
+            q = q - 8
+        scale = np.repeat(d[:, None], 32, axis=1)
+        wmin = np.zeros_like(scale)
+    elif qtype in (Q4_K, Q5_K):
+        d = _f16(blk[:, 0:2])
+        dmin = _f16(blk[:, 2:4])
+        sc, mn = _k4_scales(blk[:, 4:16])
+        qs = blk[:, 48:176] if qtype == Q5_K else blk[:, 16:144]
+        q = np.zeros((nblk, 256), np.int64)
+        for c in range(4):  # 32-byte chunk c: low nibbles -> sub-block 2c, high -> 2c + 1
+            q[:, 64 * c: 64 * c + 32] = qs[:, 32 * c: 32 * c + 32] & 15
+            q[:, 64 * c + 32: 64 * c + 64] = qs[:, 32 * c: 32 * c + 32] >> 4
+        if qtype == Q5_K:
+            qh = blk[:, 16:48].astype(np.int64)  # bit j of qh[l] -> bit 4 of elem 32j + l
+            for j in range(8):
+                q[:, 32 * j: 32 * j + 32] |= ((qh >> j) & 1) << 4
+        scale = (d[:, None] * np.repeat(sc, 32, axis=1))
+        wmin = (dmin[:, None] * np.repeat(mn, 32, axis=1))
+    elif qtype == Q6_K:
+        ql = blk[:, 0:128].astype(np.int64)
+        qh = blk[:, 128:192].astype(np.int64)
+        sc = blk[:, 192:208].view(np.int8).astype(np.int64)
+        d = _f16(blk[:, 208:210])
+        q = np.zeros((nblk, 256), np.int64)
+        for g in range(2):      # 128-element halves
+            for i in range(4):  # 32-element sub-blocks
+                low = ql[:, 64 * g + 32 * (i & 1): 64 * g + 32 * (i & 1) + 32]
+                low = (low & 15) if i < 2 else (low >> 4)
+                hi = (qh[:, 32 * g: 32 * g + 32] >> (2 * i)) & 3
+                q[:, 128 * g + 32 * i: 128 * g + 32 * i + 32] = (low | (hi << 4)) - 32
+        scale = d[:, None] * np.repeat(sc, 16, axis=1)
+        wmin = np.zeros_like(scale)
+    else:
+        raise ValueError(qtype)
+    return (q.reshape(n, k), scale.reshape(n, k).astype(np.float64),
+            wmin.reshape(n, k).astype(np.float64))

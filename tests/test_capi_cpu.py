@@ -1,0 +1,76 @@
+"""CPU-only checks of the product libraries: they load, export every declared symbol, and
+reject bad arguments with the reference's messages before touching a device."""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+import cllm_inference_amd as C
+from cllm_inference_amd import synth as S
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "cllm_hip.h")).read()
+    return sorted(set(re.findall(r"\b(cllm_hip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.load_library()
+    declared = header_symbols()
+    assert len(declared) >= 15
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(C.SIGNATURES) == declared
+
+
+def test_quant_api_library_exports_cpp_symbols():
+    assert os.path.exists(C.QUANT_LIB_PATH)
+    nm = shutil.which("nm")
+    out = subprocess.run([nm, "-D", "--defined-only", "-C", C.QUANT_LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    for sym in ["cllm::matmul_quant(", "cllm::matmul_quant_batch(", "cllm::quantize_row_q8_0(",
+                "cllm::vec_dot_row(", "cllm::has_vec_dot(", "cllm::block_size(",
+                "cllm::type_size("]:
+        assert sym in out, sym
+    ctypes.CDLL(C.QUANT_LIB_PATH)
+
+
+def test_sizes_match_reference_tables():
+    for t in C.GgmlType:
+        assert C.block_size(t) == {0: 1, 1: 1}.get(int(t), 32 if int(t) <= 9 else 256)
+    want = {0: 4, 1: 2, 2: 18, 3: 20, 6: 22, 7: 24, 8: 34, 9: 36, 10: 84, 11: 110, 12: 144,
+            13: 176, 14: 210}
+    for t, sz in want.items():
+        assert C.type_size(t) == sz
+    assert {int(t) for t in C.GgmlType if C.has_vec_dot(t)} == {2, 6, 8, 12, 13, 14}
+
+
+def test_argument_errors_before_device_use():
+    x = np.zeros(100, np.float32)
+    w = np.zeros(4096, np.uint8)
+    with pytest.raises(RuntimeError, match=r"^matmul_quant: in_dim not divisible by block size$"):
+        C.matmul_quant(x, w, S.Q4_K, None, 100, 4)
+    with pytest.raises(RuntimeError, match=r"^matmul_quant_batch: in_dim not divisible by block size$"):
+        C.matmul_quant_batch(np.zeros((2, 100), np.float32), w, S.Q8_0, None, 100, 4, 2)
+    with pytest.raises(RuntimeError, match=r"^vec_dot_row: no kernel for this type$"):
+        C.matmul_quant(np.zeros(64, np.float32), w, int(C.GgmlType.Q4_1), None, 64, 4)
+    with pytest.raises(RuntimeError, match=r"^quantize_row_q8_0: n not divisible by 32$"):
+        C.quantize_row_q8_0(np.zeros(48, np.float32))
+    # n_rows <= 0 returns without touching y (quant.cpp:1436)
+    y = C.matmul_quant_batch(np.zeros((0, 64), np.float32), w, S.Q8_0, None, 64, 4, 0)
+    assert y.shape == (0, 4)
+
+
+def test_no_device_is_reported_not_faked():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    lib = C.load_library()
+    assert lib.cllm_hip_init(0) == 5  # CLLM_HIP_E_NODEV
+    assert b"device" in lib.cllm_hip_last_error()

@@ -1,0 +1,209 @@
+"""Parity of the HIP path with the reference, through the C ABI, on an MI355X.
+
+Bars (written into each test):
+  - Q8_0 activation bytes (int8 qs, fp32 scales, int32 block sums): bit-exact.
+  - Outputs: |gpu - ref| <= 1e-4 * max(|ref|, 2^-8 * A) against the reference's own fp32
+    output, where A is the row's sum of absolute per-block terms; and
+    |gpu - exact| <= 1e-4 * max(|exact|, 2^-10 * A) against the fp64 evaluation of the same
+    quantized terms. The reference's sequential fp32 sum is itself up to 1.5e-4 away from
+    exact under the 2^-10 floor on outlier inputs, so the comparison with the reference uses
+    the 2^-8 floor.
+  - Anything the GEMV computes twice the same way (host vs device entry point, batch row vs
+    single row) must agree bit for bit.
+"""
+import numpy as np
+import pytest
+
+from conftest import load_golden, split_cases
+from cllm_inference_amd import synth as S
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+TYPES = [S.Q4_0, S.Q5_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K]
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def check_close(got, ref, exact, abs_sum, what):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    d_ref = np.abs(got - ref) / np.maximum(np.maximum(np.abs(ref), abs_sum * 2.0 ** -8), 1e-30)
+    d_ex = np.abs(got - exact) / np.maximum(np.maximum(np.abs(exact), abs_sum * 2.0 ** -10), 1e-30)
+    assert d_ref.max() <= TOL, f"{what}: vs reference {d_ref.max():.3g} at {np.argmax(d_ref)}"
+    assert d_ex.max() <= TOL, f"{what}: vs exact {d_ex.max():.3g} at {np.argmax(d_ex)}"
+
+
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+# ------------------------------------------------------------------------- quantize
+
+def test_quantize_bit_exact_host_and_device(gpu):
+    for name, c in split_cases(load_golden("q8_act.npz")).items():
+        print("quantize case", name, c["x"].shape, flush=True)
+        q = gpu.quantize_row_q8_0(c["x"])
+        assert np.array_equal(q.qs, c["qs"]), name
+        assert np.array_equal(bits(q.scales), bits(c["scales"])), name
+        assert np.array_equal(q.bsums, c["bsums"]), name
+        qs, sc, bs = gpu.quantize_q8_0_dev(_dev(c["x"]))
+        assert np.array_equal(qs.cpu().numpy(), c["qs"]), name
+        assert np.array_equal(bits(sc.cpu().numpy()), bits(c["scales"])), name
+        assert np.array_equal(bs.cpu().numpy(), c["bsums"]), name
+
+
+def test_quantize_large_random_matches_oracle(gpu, orc):
+    x = S.make_activation(512, 4096, 4242, outliers=True)
+    x[7, 64:96] = 0.0
+    x[9, :32] *= np.float32(1e-38)
+    qs, sc, bs = gpu.quantize_q8_0_dev(_dev(x))
+    oq, osc, obs = orc.quantize(x)
+    assert np.array_equal(qs.cpu().numpy(), oq)
+    assert np.array_equal(bits(sc.cpu().numpy()), bits(osc))
+    assert np.array_equal(bs.cpu().numpy(), obs)
+
+
+# ------------------------------------------------------------------------- GEMV parity
+
+@pytest.mark.parametrize("tag", ["c0", "c1", "c4_q5_k_m1", "c4_q5_k_m4", "c4_q8_0_m1", "c4_q8_0_m4"])
+def test_workload_vs_reference_golden(gpu, orc, tag):
+    c = split_cases(load_golden("gemv.npz"))[tag]
+    qt, n, k, m = (int(v) for v in c["meta"])
+    cfg = {"c0": ("c0_q8_0_gemv", "w"), "c1": ("c1_q4_k_gemv", "ffn")}.get(
+        tag, ("c4_m_sweep", "q5_k" if "q5_k" in tag else "q8_0"))
+    _, _, _, w = S.config_weight(*cfg)
+    x = S.config_activation(cfg[0], m, k)
+    print("workload", tag, S.TYPE_NAMES[qt], n, k, m, flush=True)
+    y_host = gpu.matmul_quant_batch(x, w, qt, None, k, n, m)
+    y_dev = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, None, k, n).cpu().numpy()
+    assert np.array_equal(bits(y_host), bits(y_dev))
+    rows = c["rows"]
+    rb = S.row_bytes(qt, k)
+    exact, abs_sum = orc.matmul_f64(x, w.reshape(n, rb)[rows].reshape(-1), qt, None, k, len(rows), m)
+    check_close(y_host[:, rows], c["y"], exact, abs_sum, tag)
+
+
+def test_q6_k_output_head_full_size(gpu, orc):
+    """128256 x 4096 Q6_K (431 MB): every 16th row against the reference, all rows against
+    the device entry point, and a second call on the same buffers must repeat every bit."""
+    c = split_cases(load_golden("gemv.npz"))["c2"]
+    qt, n, k, m = (int(v) for v in c["meta"])
+    _, _, _, w = S.config_weight("c2_q6_k_head", "output")
+    x = S.config_activation("c2_q6_k_head", 1, k)
+    print("workload c2 Q6_K", n, k, flush=True)
+    wd, xd = _dev(w), _dev(x)
+    y1 = gpu.matmul_quant_dev(xd, wd, qt, None, k, n).cpu().numpy()
+    y2 = gpu.matmul_quant_dev(xd, wd, qt, None, k, n).cpu().numpy()
+    assert np.array_equal(bits(y1), bits(y2))
+    rows = c["rows"]
+    rb = S.row_bytes(qt, k)
+    exact, abs_sum = orc.matmul_f64(x, w.reshape(n, rb)[rows].reshape(-1), qt, None, k, len(rows), 1)
+    check_close(y1[:, rows], c["y"], exact, abs_sum, "c2")
+    # rows the golden file does not hold: against the oracle
+    others = np.arange(1, n, 997)
+    exact, abs_sum = orc.matmul_f64(x, w.reshape(n, rb)[others].reshape(-1), qt, None, k, len(others), 1)
+    yo = orc.matmul(x, w.reshape(n, rb)[others].reshape(-1), qt, None, k, len(others), 1)
+    check_close(y1[:, others], yo, exact, abs_sum, "c2-oracle")
+
+
+def test_all_types_shapes_bias_vs_reference_golden(gpu, orc):
+    cases = split_cases(load_golden("types.npz"))
+    for tag, c in cases.items():
+        qt, n, k, m, seed = (int(v) for v in c["meta"])
+        print("types case", tag, flush=True)
+        w = S.make_weight(qt, n, k, seed)
+        x = S.make_activation(m, k, seed + 1, outliers=True)
+        bias = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+        y = gpu.matmul_quant_batch(x, w, qt, None, k, n, m)
+        yb = gpu.matmul_quant_batch(x, w, qt, bias, k, n, m)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+        check_close(y, c["y"], exact, abs_sum, tag)
+        exact_b, abs_b = orc.matmul_f64(x, w, qt, bias, k, n, m)
+        check_close(yb, c["ybias"], exact_b, abs_b, tag + "+bias")
+        # bias is added after the row's accumulation, like the reference
+        assert np.array_equal(bits(yb), bits((y + bias).astype(np.float32))), tag
+
+
+def test_reference_test_inputs(gpu, orc):
+    """The inputs the reference's own quant_test builds (quant_test.cpp:237-361)."""
+    for name, c in split_cases(load_golden("refkat.npz")).items():
+        qt = S.NAME_TO_TYPE[name]
+        k = 64 if S.BLOCK[qt] == 32 else 256
+        for xk, yk, m in (("x1", "y1", 1), ("x3", "y3", 3)):
+            y = gpu.matmul_quant_batch(c[xk], c["w"], qt, None, k, 40, m)
+            exact, abs_sum = orc.matmul_f64(c[xk], c["w"], qt, None, k, 40, m)
+            check_close(y.reshape(m, 40), c[yk].reshape(m, 40), exact, abs_sum, name + xk)
+
+
+@pytest.mark.parametrize("qt", TYPES)
+def test_batch_rows_equal_single_rows(gpu, qt):
+    k = 1024
+    n = 333
+    w = S.make_weight(qt, n, k, 55)
+    x = S.make_activation(13, k, 56, outliers=True)
+    yb = gpu.matmul_quant_batch(x, w, qt, None, k, n, 13)
+    for t in (0, 5, 12):
+        y1 = gpu.matmul_quant(x[t], w, qt, None, k, n)
+        assert np.array_equal(bits(y1), bits(yb[t])), (S.TYPE_NAMES[qt], t)
+
+
+@pytest.mark.parametrize("qt", TYPES)
+def test_edge_shapes(gpu, orc, qt):
+    bs = S.BLOCK[qt]
+    for (n, k, m) in [(1, bs, 1), (3, bs, 2), (9, 2 * bs, 7), (65, 3 * bs, 5), (130, 14336 if bs == 256 else 96, 1)]:
+        w = S.make_weight(qt, n, k, n + k)
+        x = S.make_activation(m, k, m + k, outliers=True)
+        y = gpu.matmul_quant_batch(x, w, qt, None, k, n, m).reshape(m, n)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+        yo = orc.matmul(x, w, qt, None, k, n, m).reshape(m, n)
+        check_close(y, yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")
+
+
+def test_vec_dot_rows(gpu, orc):
+    for qt in TYPES:
+        k = 2048
+        w = S.make_weight(qt, 10, k, 4)
+        x = S.make_activation(1, k, 5)[0]
+        q = gpu.quantize_row_q8_0(x)
+        got = gpu.vec_dot_rows(w, qt, q, k, 10)
+        want = orc.matmul(x, w, qt, None, k, 10, 1)[0]
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, 10, 1)
+        check_close(got, want, exact[0], abs_sum[0], S.TYPE_NAMES[qt])
+        assert abs(gpu.vec_dot_row(w, qt, q, k) - got[0]) == 0.0
+
+
+def test_registered_weights_resolve_by_offset(gpu):
+    import ctypes
+    qt, k, n = S.Q4_K, 1024, 64
+    region = np.zeros(4096 + 3 * S.row_bytes(qt, k) * n, np.uint8)
+    w = S.make_weight(qt, n, k, 8)
+    off = 4096 + S.row_bytes(qt, k) * n  # 16-aligned offset inside the region
+    region[off: off + w.size] = w
+    x = S.make_activation(1, k, 9)[0]
+    y_plain = gpu.matmul_quant(x, w, qt, None, k, n)
+    lib = gpu.load_library()
+    base = region.ctypes.data
+    assert lib.cllm_hip_register_weights(ctypes.c_void_p(base), region.size) == 0
+    try:
+        view = region[off: off + w.size]
+        assert view.ctypes.data == base + off
+        y_reg = gpu.matmul_quant(x, view, qt, None, k, n)
+        assert np.array_equal(bits(y_plain), bits(y_reg))
+    finally:
+        assert lib.cllm_hip_unregister_weights(ctypes.c_void_p(base)) == 0
+
+
+def test_device_argument_errors(gpu):
+    import torch
+    w = torch.zeros(4096 + 16, dtype=torch.uint8, device="cuda")
+    x = torch.zeros((1, 256), dtype=torch.float32, device="cuda")
+    with pytest.raises(RuntimeError, match="misaligned"):
+        gpu.matmul_quant_dev(x, w[1:], S.Q4_K, None, 256, 4)
+    with pytest.raises(RuntimeError, match="in_dim not divisible by block size"):
+        gpu.matmul_quant_dev(x[:, :100].contiguous(), w, S.Q4_K, None, 100, 4)
+    assert gpu.matmul_route(S.Q4_K, 4096, 4096, 1) == "gemv"

@@ -1,0 +1,255 @@
+"""Pins the CPU oracle (oracle/cllm_oracle.c) before it is trusted as the GPU's checker.
+
+Each check is independent of the oracle's own formulas:
+  - golden vectors produced by the reference compiled from its own sources (bit-exact);
+  - known-answer blocks restated from the reference's tests (tests/quant_test.cpp:58-218);
+  - an independent numpy decode of the byte layouts (tests/np_decode.py);
+  - closed forms: exact integer dots when every scale is 1, ties-to-even at d = 1;
+  - invariants: batch == per-row, y(bias) == y + bias.
+A planted mistake (a swapped nibble order) is shown to fail the integer check.
+"""
+import numpy as np
+import pytest
+
+from conftest import load_golden, split_cases
+import np_decode as D
+from cllm_inference_amd import synth as S
+import oracle as O
+
+TYPES = [S.Q4_0, S.Q5_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K]
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32 if a.dtype.itemsize == 4 else np.uint8)
+
+
+# ------------------------------------------------------------------ quantize_row_q8_0
+
+def test_quantize_matches_reference_golden(orc):
+    cases = split_cases(load_golden("q8_act.npz"))
+    assert set(cases) >= {"special", "c0", "c1", "c4", "c3_down"}
+    for name, c in cases.items():
+        qs, sc, bs = orc.quantize(c["x"])
+        assert np.array_equal(qs, c["qs"]), name
+        assert np.array_equal(bits(sc), bits(c["scales"])), name
+        assert np.array_equal(bs, c["bsums"]), name
+
+
+def test_quantize_closed_forms(orc):
+    # amax = 127 -> d = 1 exactly, id = 1, q = rint(x): ties to even
+    x = np.zeros(64, np.float32)
+    x[:10] = [127, 2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 126.5, -127]
+    qs, sc, bs = orc.quantize(x)
+    assert sc[0, 0] == np.float32(1.0)
+    assert list(qs[0, :10]) == [127, 2, 4, -2, -4, 0, 2, 0, 126, -127]
+    assert bs[0, 0] == int(qs[0, :32].astype(np.int64).sum())
+    # all-zero block
+    assert sc[0, 1] == 0.0 and not qs[0, 32:].any() and bs[0, 1] == 0
+    # the block maximum always maps to +-127 and nothing reaches -128
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((8, 256)).astype(np.float32) * 5
+    qs, sc, bs = orc.quantize(x)
+    blk = qs.reshape(-1, 32).astype(np.int64)
+    assert (np.abs(blk).max(axis=1) == 127).all()
+    assert blk.min() >= -127
+    assert np.array_equal(blk.sum(axis=1), bs.reshape(-1))
+    amax = np.abs(x.reshape(-1, 32)).max(axis=1)
+    assert np.array_equal(bits(sc.reshape(-1)), bits((amax / np.float32(127.0)).astype(np.float32)))
+
+
+def test_quantize_rejects_ragged(orc):
+    with pytest.raises(RuntimeError, match="quantize_row_q8_0: n not divisible by 32"):
+        orc.quantize(np.zeros((1, 48), np.float32))
+
+
+# ------------------------------------------------------------------ block layouts
+
+def _blk(n):
+    return np.zeros(n, np.uint8)
+
+
+def _put_one(b, off):
+    b[off], b[off + 1] = 0x00, 0x3C  # fp16 1.0
+
+
+def test_dequant_known_answers(orc):
+    """The reference's own hand-built blocks (quant_test.cpp:58-218), restated."""
+    b = _blk(18); _put_one(b, 0); b[2] = 0x9A
+    y = orc.dequantize(b, S.Q4_0, 32)
+    assert (y[0], y[16], y[1]) == (2.0, 1.0, -8.0)
+    b = _blk(22); _put_one(b, 0); b[2] = 0x01; b[6] = 0x21
+    y = orc.dequantize(b, S.Q5_0, 32)
+    assert (y[0], y[16]) == (1.0, -14.0)
+    b = _blk(34); _put_one(b, 0); b[2] = 0xFF; b[3] = 0x02
+    y = orc.dequantize(b, S.Q8_0, 32)
+    assert (y[0], y[1]) == (-1.0, 2.0)
+    b = _blk(144); b[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]; b[16] = 0x21; _put_one(b, 0)
+    y = orc.dequantize(b, S.Q4_K, 256)
+    assert (y[0], y[32], y[1]) == (1.0, 2.0, 0.0)
+    b = _blk(176); b[4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]; b[48] = 0x21; _put_one(b, 0)
+    y = orc.dequantize(b, S.Q5_K, 256)
+    assert (y[0], y[32]) == (1.0, 2.0)
+    b[16] = 0x01
+    assert orc.dequantize(b, S.Q5_K, 256)[0] == 17.0
+    b = _blk(210); b[192:208] = 1; b[0] = 0x21; _put_one(b, 208)
+    y = orc.dequantize(b, S.Q6_K, 256)
+    assert (y[0], y[64]) == (-31.0, -30.0)
+
+
+@pytest.mark.parametrize("qt", TYPES)
+def test_dequant_matches_numpy_layout_decode(orc, qt):
+    k = 512
+    w = S.make_weight(qt, 3, k, 11)
+    q, scale, wmin = D.decode(w, qt, 3, k)
+    want = (scale * q - wmin).astype(np.float32)
+    for j in range(3):
+        got = orc.dequantize(w[j * S.row_bytes(qt, k):], qt, k)
+        # fp32 evaluation order of d*sc*q - dmin*m may differ from the float64 one by 1 ulp
+        np.testing.assert_allclose(got, want[j], rtol=2e-7, atol=1e-12)
+
+
+# ------------------------------------------------------------------ vec_dot / matmul
+
+def _int_special_weight(qt, n, k, rng):
+    """Every effective per-element scale is 1 and every min 0: d = 1 (Q6_K sc = 1; K-quants
+    sc = 1, m = 0, dmin = 0), random quant bits. y is then an exact integer dot."""
+    w = S.make_weight(qt, n, k, int(rng.integers(1 << 30)))
+    blk = w.reshape(-1, S.TYPE_SIZE[qt])
+    if qt in (S.Q8_0, S.Q4_0, S.Q5_0):
+        blk[:, 0:2] = [0x00, 0x3C]
+    elif qt in (S.Q4_K, S.Q5_K):
+        blk[:, 0:2] = [0x00, 0x3C]
+        blk[:, 2:4] = 0
+        blk[:, 4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    else:
+        blk[:, 192:208] = 1
+        blk[:, 208:210] = [0x00, 0x3C]
+    return w
+
+
+def _int_special_x(m, k, rng):
+    """Activation blocks with amax = 127 so that d = 1 and q = rint(x)."""
+    x = rng.integers(-127, 128, size=(m, k)).astype(np.float32)
+    x[:, ::32] = 127.0
+    return x
+
+
+@pytest.mark.parametrize("qt", TYPES)
+def test_matmul_exact_integer_case(orc, qt):
+    rng = np.random.default_rng(qt)
+    n, k, m = 37, 512, 2
+    w = _int_special_weight(qt, n, k, rng)
+    x = _int_special_x(m, k, rng)
+    q, scale, wmin = D.decode(w, qt, n, k)
+    assert (scale == 1).all() and (wmin == 0).all()
+    want = x.astype(np.int64) @ q.T
+    got = orc.matmul(x, w, qt, None, k, n, m)
+    assert np.array_equal(got.astype(np.int64), want)
+
+
+def test_planted_nibble_swap_is_caught():
+    """A decoder that swaps the Q4_K nibble order must fail the integer check."""
+    rng = np.random.default_rng(5)
+    n, k = 8, 256
+    w = _int_special_weight(S.Q4_K, n, k, rng)
+    x = _int_special_x(1, k, rng)
+    q, _, _ = D.decode(w, S.Q4_K, n, k)
+    wrong = q.reshape(n, 4, 2, 32)[:, :, ::-1, :].reshape(n, k)  # high/low nibble swapped
+    good = x.astype(np.int64) @ q.T
+    bad = x.astype(np.int64) @ wrong.T
+    assert not np.array_equal(good, bad)
+
+
+@pytest.mark.parametrize("qt", TYPES)
+def test_f64_matches_bruteforce(orc, qt):
+    n, k, m = 19, 512, 3
+    w = S.make_weight(qt, n, k, 123)
+    x = S.make_activation(m, k, 321, outliers=True)
+    qs, sc, _ = orc.quantize(x)
+    xv = qs.astype(np.float64) * np.repeat(sc.astype(np.float64), 32, axis=1)
+    q, scale, wmin = D.decode(w, qt, n, k)
+    wv = scale * q - wmin
+    want = xv @ wv.T
+    got, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12 * abs_sum.max())
+    # and the fp32 oracle is within the gate of its own fp64 evaluation
+    y32 = orc.matmul(x, w, qt, None, k, n, m)
+    err, _, _ = O.rel_err_floored(y32, got, abs_sum)
+    assert err < 1e-4
+
+
+def test_oracle_matches_reference_golden_types(orc):
+    cases = split_cases(load_golden("types.npz"))
+    assert len(cases) >= 20
+    for tag, c in cases.items():
+        qt, n, k, m, seed = (int(v) for v in c["meta"])
+        w = S.make_weight(qt, n, k, seed)
+        assert O_sha(w) == str(c["w_sha"]), f"generator drift for {tag}"
+        x = S.make_activation(m, k, seed + 1, outliers=True)
+        bias = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+        y = orc.matmul(x, w, qt, None, k, n, m)
+        yb = orc.matmul(x, w, qt, bias, k, n, m)
+        assert np.array_equal(bits(y), bits(c["y"])), tag
+        assert np.array_equal(bits(yb), bits(c["ybias"])), tag
+        # reference semantics: bias is added after the row's accumulation
+        assert np.array_equal(bits(yb), bits((y + bias).astype(np.float32))), tag
+
+
+def O_sha(a):
+    import hashlib
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.mark.parametrize("tag", ["c0", "c1", "c4_q5_k_m1", "c4_q5_k_m4", "c4_q8_0_m1", "c4_q8_0_m4"])
+def test_oracle_matches_reference_golden_workloads(orc, tag):
+    c = split_cases(load_golden("gemv.npz"))[tag]
+    qt, n, k, m = (int(v) for v in c["meta"])
+    cfg = {"c0": ("c0_q8_0_gemv", "w"), "c1": ("c1_q4_k_gemv", "ffn")}.get(
+        tag, ("c4_m_sweep", "q5_k" if "q5_k" in tag else "q8_0"))
+    _, _, _, w = S.config_weight(*cfg)
+    x = S.config_activation(cfg[0], m, k)
+    assert O_sha(w) == str(c["w_sha"]) and O_sha(x) == str(c["x_sha"])
+    rows = c["rows"]
+    rb = S.row_bytes(qt, k)
+    wsub = w.reshape(n, rb)[rows].reshape(-1)
+    y = orc.matmul(x, wsub, qt, None, k, len(rows), m)
+    assert np.array_equal(bits(y), bits(c["y"]))
+
+
+def test_oracle_matches_reference_golden_refkat(orc):
+    cases = split_cases(load_golden("refkat.npz"))
+    for name, c in cases.items():
+        qt = S.NAME_TO_TYPE[name]
+        k = 64 if S.BLOCK[qt] == 32 else 256
+        assert np.array_equal(bits(orc.matmul(c["x1"], c["w"], qt, None, k, 40, 1)), bits(c["y1"]))
+        assert np.array_equal(bits(orc.matmul(c["x3"], c["w"], qt, None, k, 40, 3)), bits(c["y3"]))
+
+
+def test_batch_equals_rows_and_bias(orc):
+    qt, n, k, m = S.Q4_K, 300, 1024, 5
+    w = S.make_weight(qt, n, k, 1)
+    x = S.make_activation(m, k, 2, outliers=True)
+    yb = orc.matmul(x, w, qt, None, k, n, m)
+    for t in range(m):
+        assert np.array_equal(bits(orc.matmul(x[t], w, qt, None, k, n, 1)[0]), bits(yb[t]))
+    # threaded row split (ThreadPool chunking) does not change a bit
+    assert np.array_equal(bits(orc.matmul(x, w, qt, None, k, n, m, threads=7)), bits(yb))
+
+
+def test_matmul_shape_error(orc):
+    with pytest.raises(RuntimeError, match="matmul_quant: in_dim not divisible by block size"):
+        orc.matmul(np.zeros(100, np.float32), np.zeros(1000, np.uint8), S.Q4_K, None, 100, 2, 1)
+    with pytest.raises(RuntimeError, match="matmul_quant_batch: in_dim not divisible by block size"):
+        orc.matmul(np.zeros((2, 100), np.float32), np.zeros(1000, np.uint8), S.Q8_0, None, 100, 2, 2)
+
+
+def test_compiled_reference_agrees_when_present(orc):
+    ref = O.reference_or_none()
+    if ref is None:
+        pytest.skip("oracle/_ref/libcllm_ref.so not built (reference tree absent)")
+    for qt in TYPES:
+        k = 512
+        w = S.make_weight(qt, 50, k, 99)
+        x = S.make_activation(3, k, 98, outliers=True)
+        assert np.array_equal(bits(ref.matmul(x, w, qt, None, k, 50, 3)),
+                              bits(orc.matmul(x, w, qt, None, k, 50, 3)))
