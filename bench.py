@@ -86,6 +86,8 @@ def decode_point(C, S, cfg, label, m, steps, warmup, cold=True):
     nbytes = algo_bytes(qt, n, k, m)
     del ws
     torch.cuda.empty_cache()
+    print(f"[bench] {S.TYPE_NAMES[qt]} {n}x{k} m={m} copies={copies}: step {ms_step * 1e3:.2f} us, "
+          f"gemv {ms_gemv * 1e3:.2f} us, {nbytes / ms_gemv / 1e6:.1f} GB/s", file=sys.stderr, flush=True)
     return dict(type=S.TYPE_NAMES[qt], n=n, k=k, m=m, copies=copies, bytes=nbytes,
                 ms_step=ms_step, ms_gemv=ms_gemv,
                 gbs_step=nbytes / ms_step / 1e6, gbs_gemv=nbytes / ms_gemv / 1e6,

@@ -42,7 +42,10 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float r = __builtin_rintf(__fmul_rn(e[i], id));
-        int t = (int)r;
+        // When amax is tiny enough that 1/d overflows, x * id is +-inf (or NaN for 0 * inf).
+        // The reference's (int) conversion of such values is x86's cvttss2si result, INT_MIN,
+        // which the clamp then turns into -128; v_cvt_i32_f32 would saturate instead.
+        int t = (fabsf(r) < 2147483648.0f) ? (int)r : INT32_MIN;
         t = t > 127 ? 127 : t;
         t = t < -128 ? -128 : t;
         q[i] = t;
