@@ -31,9 +31,8 @@ __device__ __forceinline__ u32x4 ld_u32x4_nt(const void* p) {
 // p exist because p is then at least 2 bytes past a 4-aligned base.
 template <int NDW>
 __device__ __forceinline__ void ld_a2(const uint8_t* p, uint32_t (&out)[NDW]) {
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t s = (uint32_t)(a & 3u);
-    const uint32_t* q = (const uint32_t*)(a - s);
+    const uint32_t s = (uint32_t)((uintptr_t)p & 3u);
+    const uint32_t* q = (const uint32_t*)(p - s);  // pointer arithmetic keeps the address space
     uint32_t v[NDW + 1];
     if constexpr (NDW % 4 == 0) {
 #pragma unroll

@@ -4,40 +4,97 @@
 // matmul_quant / matmul_quant_batch (src/core/quant.cpp:1388-1397, 1453-1464) for the six
 // weight types with a vec_dot kernel.
 //
-// Work split. One wave64 owns R consecutive weight rows. A row is cut into "units" that one
-// lane handles at a time:
+// Work split. A row is cut into "units" that one lane handles:
 //   Q4_K, Q5_K : a quarter super-block = one 32-byte qs chunk = sub-blocks 2c and 2c+1
 //   Q6_K       : a quarter super-block = half g, element half h of four sub-blocks
 //   Q8_0, Q4_0, Q5_0 : one 32-element block
-// Lanes stride over the units of the row, so consecutive lanes read consecutive bytes and
-// every weight byte is loaded exactly once, in place, straight from the GGUF blocks. Integer
-// dots use v_dot4_i32_i8; the fp32 per-block terms are the reference's:
-//   acc += (ws * dx) * dot      and, for Q4_K / Q5_K, acc -= (wm * dx) * bsum
-// (quant.cpp:545, 582-583, 621-622, 677-678, 775, 891). Lane partial sums are reduced across
-// the wave, so only the fp32 summation order differs from the reference.
+// Lanes stride over the units of a row, so neighbouring lanes read neighbouring bytes and
+// every weight byte is loaded once, in place, from the GGUF blocks. A row's units form one or
+// more "items" (64 units each) for the wave.
 //
-// Activations (Q8_0 rows: int8 qs, fp32 scales, int32 block sums) are small and re-read from
-// L1/L2 by every wave; for m > 1 each weight unit is dotted with up to MR activation rows
-// while it sits in registers.
+// Streaming. The grid is persistent: each wave walks rows j = wave, wave + n_waves, ... and
+// keeps a ring of P items whose weight loads are in flight while it computes the oldest one
+// (s_waitcnt vmcnt counts in issue order, so only the oldest item's loads are waited for).
+// The Q8_0 activation rows are staged once per workgroup in LDS, together with the
+// activation-only terms the kernels need (dx * bsum for the K-quant minimum, 16-element sums
+// for Q6_K), so no vector-memory load other than the weight ring sits in the wave's queue.
+//
+// Arithmetic. Integer dots use v_dot4_i32_i8 and are exact; the fp32 per-block terms follow
+// the reference (quant.cpp:545, 582-583, 621-622, 677-678, 775, 891):
+//   acc += (ws * dx) * dot       and, for Q4_K / Q5_K, acc -= wm * (dx * bsum)
+// Lane partial sums are reduced across the wave, so only the fp32 summation order (and the
+// association of the minimum term's product) differs from the reference.
 #include "device_utils.h"
 #include "ggml_blocks.h"
 #include "launch.h"
 
 namespace cllm_hip {
 
-struct ActRows {
-    const int8_t* qs;
-    const float* sc;
-    const int32_t* bs;
-    int k;   // elements per activation row
-    int nb;  // 32-element blocks per activation row
+// Activation qs rows in LDS carry 16 bytes of padding after every 256 bytes: the lanes of a
+// wave read 16-byte pieces at strides of 64 B (Q4_K / Q5_K), 32 B (32-element blocks) or
+// 256 B + 32 B (Q6_K), which without padding land on 16 of the 64 banks; with it every access
+// pattern spreads over all banks.
+__host__ __device__ constexpr int lds_qs_off(int off) { return off + ((off >> 8) << 4); }
+__host__ __device__ constexpr int lds_qs_row(int k) { return lds_qs_off(k); }
+
+// Activation rows staged in LDS.
+struct ActLds {
+    const int8_t* qs;  // [MR][lds_qs_row(k)], padded as above
+    const float* xd;   // [MR][nb] dx
+    const float* xm;   // [MR][nb] dx * bsum (K-quants)
+    const int32_t* xb; // [MR][nb] bsum (Q4_0 / Q5_0)
+    const int32_t* hs; // [MR][2][nb] sums of 16 qs (Q6_K): index r*2nb + h*nb + b
+    int k, nb;
 };
 
-__device__ __forceinline__ void ld_act32(const ActRows& a, int r, int b, uint32_t (&x)[8]) {
-    const int8_t* p = a.qs + (size_t)r * a.k + (size_t)b * 32;
-    const u32x4 x0 = ld_u32x4(p), x1 = ld_u32x4(p + 16);
+// 16 activation bytes of row r at element offset e (e % 16 == 0).
+__device__ __forceinline__ u32x4 lds_x16(const ActLds& a, int r, int e) {
+    return *(const u32x4*)(a.qs + r * lds_qs_row(a.k) + lds_qs_off(e));
+}
+
+__device__ __forceinline__ void lds_x32(const ActLds& a, int r, int b, uint32_t (&x)[8]) {
+    const u32x4 x0 = lds_x16(a, r, b * 32), x1 = lds_x16(a, r, b * 32 + 16);
     x[0] = x0.x; x[1] = x0.y; x[2] = x0.z; x[3] = x0.w;
     x[4] = x1.x; x[5] = x1.y; x[6] = x1.z; x[7] = x1.w;
+}
+
+// Raw bytes of a 2-byte-aligned field of NDW dwords: the dword-aligned vector at p & ~3 and
+// the field's last two bytes. Every byte read lies in [p - 2, p + 4 NDW), and p - 2 is inside
+// the buffer whenever p & 3 == 2 (see ld_a2).
+template <int NDW>
+struct A2 {
+    uint32_t v[NDW];
+    uint32_t tail;
+};
+
+template <int NDW>
+__device__ __forceinline__ A2<NDW> load_a2(const uint8_t* p) {
+    // Pointer arithmetic (not an integer round trip) keeps the global address space, so these
+    // stay global_load_* rather than flat loads that would also count against lgkmcnt.
+    const uint32_t* q = (const uint32_t*)(p - ((uintptr_t)p & 3u));
+    A2<NDW> r;
+    if constexpr (NDW % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NDW; i += 4) {
+            const u32x4_a4 t = *(const u32x4_a4*)(q + i);
+            r.v[i] = t.x; r.v[i + 1] = t.y; r.v[i + 2] = t.z; r.v[i + 3] = t.w;
+        }
+    } else if constexpr (NDW == 2) {
+        const u32x2_a4 t = *(const u32x2_a4*)q;
+        r.v[0] = t.x; r.v[1] = t.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < NDW; ++i) r.v[i] = q[i];
+    }
+    r.tail = *(const uint16_t*)(p + 4 * NDW - 2);
+    return r;
+}
+
+template <int NDW>
+__device__ __forceinline__ void align_a2(const A2<NDW>& r, uint32_t sh, uint32_t (&out)[NDW]) {
+#pragma unroll
+    for (int i = 0; i < NDW - 1; ++i) out[i] = __builtin_amdgcn_alignbyte(r.v[i + 1], r.v[i], sh);
+    out[NDW - 1] = __builtin_amdgcn_alignbyte(r.tail, r.v[NDW - 1], sh);
 }
 
 // ------------------------------------------------------------------------------ Q4_K / Q5_K
@@ -46,71 +103,76 @@ __device__ __forceinline__ void ld_act32(const ActRows& a, int r, int b, uint32_
 template <bool Q5>
 struct TraitsK45 {
     static constexpr int UNIT = 64;
-    struct Prep {
-        uint32_t lo[8], hi[8];
-        float ws0, wm0, ws1, wm1;
+    static constexpr bool NEED_XM = true, NEED_XB = false, NEED_HS = false;
+    struct Raw {
+        u32x4 h, qa, qb;
+        u32x4 hha, hhb;  // Q5_K high bits (unused for Q4_K)
     };
-    static __device__ __forceinline__ Prep load(const uint8_t* row, int u) {
+    static __device__ __forceinline__ Raw load(const uint8_t* row, int u) {
         const int s = u >> 2, c = u & 3;
         const uint8_t* blk = row + (size_t)s * (Q5 ? Q5_K_BYTES : Q4_K_BYTES);
-        const u32x4 h = ld_u32x4(blk);
         const uint8_t* qp = blk + (Q5 ? Q5_K_QS : Q4_K_QS) + 32 * c;
-        const u32x4 qa = ld_u32x4(qp), qb = ld_u32x4(qp + 16);
-        const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
-        Prep p;
+        Raw r;
+        r.h = ld_u32x4(blk);
+        r.qa = ld_u32x4(qp);
+        r.qb = ld_u32x4(qp + 16);
         if constexpr (Q5) {
-            const u32x4 ha = ld_u32x4(blk + Q5_K_QH), hb = ld_u32x4(blk + Q5_K_QH + 16);
-            const uint32_t qh[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+            r.hha = ld_u32x4(blk + Q5_K_QH);
+            r.hhb = ld_u32x4(blk + Q5_K_QH + 16);
+        }
+        return r;
+    }
+    template <int MR>
+    static __device__ __forceinline__ void compute(const Raw& r, int u, const ActLds& a,
+                                                   float (&acc)[MR]) {
+        const int c = u & 3;
+        const int b0 = 8 * (u >> 2) + 2 * c;
+        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            lo[i] = q[i] & 0x0F0F0F0Fu;
+            hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+        }
+        if constexpr (Q5) {
+            const uint32_t qh[8] = {r.hha.x, r.hha.y, r.hha.z, r.hha.w,
+                                    r.hhb.x, r.hhb.y, r.hhb.z, r.hhb.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                p.lo[i] = (q[i] & 0x0F0F0F0Fu) | (((qh[i] >> (2 * c)) & 0x01010101u) << 4);
-                p.hi[i] = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                p.lo[i] = q[i] & 0x0F0F0F0Fu;
-                p.hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+                lo[i] |= ((qh[i] >> (2 * c)) & 0x01010101u) << 4;
+                hi[i] |= ((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4;
             }
         }
-        const float d = f16_to_f32(h.x & 0xFFFFu), dmin = f16_to_f32(h.x >> 16);
-        int sc0, m0, sc1, m1;
-        k4_scale_min(h.y, h.z, h.w, 2 * c, sc0, m0);
-        k4_scale_min(h.y, h.z, h.w, 2 * c + 1, sc1, m1);
-        p.ws0 = d * (float)sc0;
-        p.wm0 = dmin * (float)m0;
-        p.ws1 = d * (float)sc1;
-        p.wm1 = dmin * (float)m1;
-        return p;
-    }
-    template <int R, int MR>
-    static __device__ __forceinline__ void accum(const Prep (&p)[R], int u, const ActRows& a,
-                                                 float (&acc)[R][MR]) {
-        const int b0 = 8 * (u >> 2) + 2 * (u & 3);
+        // 6-bit scales / mins of sub-blocks 2c and 2c+1 (get_scale_min_k4, quant.cpp:72-80).
+        // Both use bytes 2(c&1) and 2(c&1)+1 of each packed dword, so they decode as a pair of
+        // bytes: for c < 2 the low 6 bits of bytes 0-3 / 4-7, for c >= 2 a nibble of bytes
+        // 8-11 plus the top two bits of bytes 0-3 / 4-7.
+        const uint32_t sh = 16u * (uint32_t)(c & 1);
+        const uint32_t w0 = r.h.y >> sh, w1 = r.h.z >> sh, w2 = r.h.w >> sh;
+        const uint32_t sc2 = c < 2 ? (w0 & 0x3F3Fu) : ((w2 & 0x0F0Fu) | ((w0 >> 2) & 0x3030u));
+        const uint32_t mn2 = c < 2 ? (w1 & 0x3F3Fu) : (((w2 >> 4) & 0x0F0Fu) | ((w1 >> 2) & 0x3030u));
+        const float d = f16_to_f32(r.h.x & 0xFFFFu), dmin = f16_to_f32(r.h.x >> 16);
+        const float ws0 = d * (float)(sc2 & 0xFFu), ws1 = d * (float)(sc2 >> 8);
+        const float wm0 = dmin * (float)(mn2 & 0xFFu), wm1 = dmin * (float)(mn2 >> 8);
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
+        for (int t = 0; t < MR; ++t) {
             uint32_t x0[8], x1[8];
-            ld_act32(a, r, b0, x0);
-            ld_act32(a, r, b0 + 1, x1);
-            const float* xs = a.sc + (size_t)r * a.nb + b0;
-            const int32_t* xb = a.bs + (size_t)r * a.nb + b0;
-            const float dx0 = xs[0], dx1 = xs[1];
-            const float bs0 = (float)xb[0], bs1 = (float)xb[1];
+            lds_x32(a, t, b0, x0);
+            lds_x32(a, t, b0 + 1, x1);
+            int d0 = 0, d1 = 0;
 #pragma unroll
-            for (int rr = 0; rr < R; ++rr) {
-                int d0 = 0, d1 = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    d0 = sdot4(p[rr].lo[i], x0[i], d0);
-                    d1 = sdot4(p[rr].hi[i], x1[i], d1);
-                }
-                float v = acc[rr][r];
-                v = fmaf(p[rr].ws0 * dx0, (float)d0, v);
-                v = fmaf(-(p[rr].wm0 * dx0), bs0, v);
-                v = fmaf(p[rr].ws1 * dx1, (float)d1, v);
-                v = fmaf(-(p[rr].wm1 * dx1), bs1, v);
-                acc[rr][r] = v;
+            for (int i = 0; i < 8; ++i) {
+                d0 = sdot4(lo[i], x0[i], d0);
+                d1 = sdot4(hi[i], x1[i], d1);
             }
+            const float2 xd = *(const float2*)(a.xd + (size_t)t * a.nb + b0);
+            const float2 xm = *(const float2*)(a.xm + (size_t)t * a.nb + b0);
+            float v = acc[t];
+            v = fmaf(ws0 * xd.x, (float)d0, v);
+            v = fmaf(-wm0, xm.x, v);
+            v = fmaf(ws1 * xd.y, (float)d1, v);
+            v = fmaf(-wm1, xm.y, v);
+            acc[t] = v;
         }
     }
 };
@@ -120,79 +182,78 @@ struct TraitsK45 {
 // (l in [16h, 16h+16)) of its four sub-blocks i. Element l of sub-block i:
 //   low4 = ql[64g + 32(i&1) + l], low nibble for i < 2, high nibble for i >= 2
 //   hi2  = (qh[32g + l] >> 2i) & 3;   q6 = (low4 | hi2 << 4) - 32
-// and it is scaled by sc[8g + 2i + h] (quant.cpp:630-687). The two lanes h = 0, 1 of a
-// sub-block form the reference's exact integer sc_a*dot_a + sc_b*dot_b with one DPP move.
+// scaled by sc[8g + 2i + h] (quant.cpp:630-687). The kernel dots the unsigned 6-bit values and
+// subtracts 32 * (sum of the 16 activation values), which is exact. The two lanes h = 0, 1 of
+// a sub-block form the reference's integer sc_a*dot_a + sc_b*dot_b with one DPP move.
 struct TraitsQ6K {
     static constexpr int UNIT = 64;
-    struct Prep {
-        uint32_t q[4][4];  // [sub-block i][dword]: signed bytes q6 - 32
-        int sc[4];
-        float d;
+    static constexpr bool NEED_XM = false, NEED_XB = false, NEED_HS = true;
+    struct Raw {
+        A2<4> qa, qb, qh;
+        A2<2> sc;
+        uint32_t d;
+        uint32_t sh;
     };
-    static __device__ __forceinline__ Prep load(const uint8_t* row, int u) {
+    static __device__ __forceinline__ Raw load(const uint8_t* row, int u) {
         const int s = u >> 2, g = (u >> 1) & 1, h = u & 1;
         const uint8_t* blk = row + (size_t)s * Q6_K_BYTES;
-        uint32_t qa[4], qb[4], qh[4], sc[2];
-        ld_a2<4>(blk + 64 * g + 16 * h, qa);
-        ld_a2<4>(blk + 64 * g + 32 + 16 * h, qb);
-        ld_a2<4>(blk + Q6_K_QH + 32 * g + 16 * h, qh);
-        ld_a2<2>(blk + Q6_K_SC + 8 * g, sc);
-        const uint32_t dbits = ld_u16(blk + Q6_K_D);
-        Prep p;
+        Raw r;
+        r.qa = load_a2<4>(blk + 64 * g + 16 * h);
+        r.qb = load_a2<4>(blk + 64 * g + 32 + 16 * h);
+        r.qh = load_a2<4>(blk + Q6_K_QH + 32 * g + 16 * h);
+        r.sc = load_a2<2>(blk + Q6_K_SC + 8 * g);
+        r.d = ld_u16(blk + Q6_K_D);
+        r.sh = (uint32_t)((uintptr_t)blk & 3u);  // every field offset is a multiple of 4
+        return r;
+    }
+    template <int MR>
+    static __device__ __forceinline__ void compute(const Raw& r, int u, const ActLds& a,
+                                                   float (&acc)[MR]) {
+        const int g = (u >> 1) & 1, h = u & 1;
+        const int bb = 8 * (u >> 2) + 4 * g;
+        uint32_t la[4], lb[4], qh[4], sc[2];
+        align_a2<4>(r.qa, r.sh, la);
+        align_a2<4>(r.qb, r.sh, lb);
+        align_a2<4>(r.qh, r.sh, qh);
+        align_a2<2>(r.sc, r.sh, sc);
+        uint32_t v[4][4];  // [sub-block i][dword]: unsigned 6-bit values
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const uint32_t l0 = qa[t] & 0x0F0F0F0Fu, l2 = (qa[t] >> 4) & 0x0F0F0F0Fu;
-            const uint32_t l1 = qb[t] & 0x0F0F0F0Fu, l3 = (qb[t] >> 4) & 0x0F0F0F0Fu;
-            const uint32_t h0 = (qh[t] & 0x03030303u) << 4;
-            const uint32_t h1 = (qh[t] & 0x0C0C0C0Cu) << 2;
-            const uint32_t h2 = qh[t] & 0x30303030u;
-            const uint32_t h3 = (qh[t] & 0xC0C0C0C0u) >> 2;
-            // bytes v in [0, 63]: (v + 0x60) ^ 0x80 is the int8 byte of v - 32, no carries.
-            p.q[0][t] = (l0 + h0 + 0x60606060u) ^ 0x80808080u;
-            p.q[1][t] = (l1 + h1 + 0x60606060u) ^ 0x80808080u;
-            p.q[2][t] = (l2 + h2 + 0x60606060u) ^ 0x80808080u;
-            p.q[3][t] = (l3 + h3 + 0x60606060u) ^ 0x80808080u;
+            v[0][t] = (la[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x03030303u) << 4);
+            v[1][t] = (lb[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x0C0C0C0Cu) << 2);
+            v[2][t] = ((la[t] >> 4) & 0x0F0F0F0Fu) | (qh[t] & 0x30303030u);
+            v[3][t] = ((lb[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> 2) & 0x30303030u);
         }
+        // sc[8g + 2i + h]: byte h (i = 0), 2 + h (i = 1) of dword 0, same of dword 1 (i = 2, 3)
+        int scv[4];
+        scv[0] = __builtin_amdgcn_sbfe((int)sc[0], 8 * h, 8);
+        scv[1] = __builtin_amdgcn_sbfe((int)sc[0], 16 + 8 * h, 8);
+        scv[2] = __builtin_amdgcn_sbfe((int)sc[1], 8 * h, 8);
+        scv[3] = __builtin_amdgcn_sbfe((int)sc[1], 16 + 8 * h, 8);
+        const float d = f16_to_f32(r.d);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            p.sc[i] = (int)(int8_t)((sc[i >> 1] >> (8 * (2 * (i & 1) + h))) & 0xFFu);
-        p.d = f16_to_f32(dbits);
-        return p;
-    }
-    template <int R, int MR>
-    static __device__ __forceinline__ void accum(const Prep (&p)[R], int u, const ActRows& a,
-                                                 float (&acc)[R][MR]) {
-        const int s = u >> 2, g = (u >> 1) & 1, h = u & 1;
-        const int bb = 8 * s + 4 * g;
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            uint32_t x[4][4];
+        for (int t = 0; t < MR; ++t) {
+            const u32x4 hs = *(const u32x4*)(a.hs + (size_t)t * 2 * a.nb + (size_t)h * a.nb + bb);
+            const int hsv[4] = {(int)hs.x, (int)hs.y, (int)hs.z, (int)hs.w};
+            int tot[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const u32x4 v = ld_u32x4(a.qs + (size_t)r * a.k + (size_t)(bb + i) * 32 + 16 * h);
-                x[i][0] = v.x; x[i][1] = v.y; x[i][2] = v.z; x[i][3] = v.w;
+                const u32x4 x = lds_x16(a, t, (bb + i) * 32 + 16 * h);
+                int dot = sdot4(v[i][0], x.x, 0);
+                dot = sdot4(v[i][1], x.y, dot);
+                dot = sdot4(v[i][2], x.z, dot);
+                dot = sdot4(v[i][3], x.w, dot);
+                const int part = scv[i] * (dot - 32 * hsv[i]);
+                tot[i] = part + dpp_i32<DPP_QUAD_SWAP1>(part);  // + partner lane h ^ 1
             }
-            const float* xs = a.sc + (size_t)r * a.nb + bb;
-            const float dxa = xs[2 * h], dxb = xs[2 * h + 1];
-#pragma unroll
-            for (int rr = 0; rr < R; ++rr) {
-                int tot[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    int dot = 0;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) dot = sdot4(p[rr].q[i][t], x[i][t], dot);
-                    const int part = p[rr].sc[i] * dot;
-                    tot[i] = part + dpp_i32<DPP_QUAD_SWAP1>(part);  // + partner lane h ^ 1
-                }
-                // lane h finishes sub-blocks 2h and 2h + 1
-                const int ia = h ? tot[2] : tot[0];
-                const int ib = h ? tot[3] : tot[1];
-                float v = acc[rr][r];
-                v = fmaf(p[rr].d * dxa, (float)ia, v);
-                v = fmaf(p[rr].d * dxb, (float)ib, v);
-                acc[rr][r] = v;
-            }
+            // lane h finishes sub-blocks 2h and 2h + 1
+            const int ia = h ? tot[2] : tot[0];
+            const int ib = h ? tot[3] : tot[1];
+            const float2 xd = *(const float2*)(a.xd + (size_t)t * a.nb + bb + 2 * h);
+            float vacc = acc[t];
+            vacc = fmaf(d * xd.x, (float)ia, vacc);
+            vacc = fmaf(d * xd.y, (float)ib, vacc);
+            acc[t] = vacc;
         }
     }
 };
@@ -200,32 +261,33 @@ struct TraitsQ6K {
 // ------------------------------------------------------------------------------------ Q8_0
 struct TraitsQ80 {
     static constexpr int UNIT = 32;
-    struct Prep {
-        uint32_t q[8];
-        float d;
+    static constexpr bool NEED_XM = false, NEED_XB = false, NEED_HS = false;
+    struct Raw {
+        A2<8> q;
+        uint32_t d, sh;
     };
-    static __device__ __forceinline__ Prep load(const uint8_t* row, int b) {
+    static __device__ __forceinline__ Raw load(const uint8_t* row, int b) {
         const uint8_t* blk = row + (size_t)b * Q8_0_BYTES;
-        Prep p;
-        ld_a2<8>(blk + 2, p.q);
-        p.d = f16_to_f32(ld_u16(blk));
-        return p;
+        Raw r;
+        r.q = load_a2<8>(blk + 2);
+        r.d = ld_u16(blk);
+        r.sh = (uint32_t)((uintptr_t)(blk + 2) & 3u);
+        return r;
     }
-    template <int R, int MR>
-    static __device__ __forceinline__ void accum(const Prep (&p)[R], int b, const ActRows& a,
-                                                 float (&acc)[R][MR]) {
+    template <int MR>
+    static __device__ __forceinline__ void compute(const Raw& r, int b, const ActLds& a,
+                                                   float (&acc)[MR]) {
+        uint32_t q[8];
+        align_a2<8>(r.q, r.sh, q);
+        const float d = f16_to_f32(r.d);
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
+        for (int t = 0; t < MR; ++t) {
             uint32_t x[8];
-            ld_act32(a, r, b, x);
-            const float dx = a.sc[(size_t)r * a.nb + b];
+            lds_x32(a, t, b, x);
+            int dot = 0;
 #pragma unroll
-            for (int rr = 0; rr < R; ++rr) {
-                int dot = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) dot = sdot4(p[rr].q[i], x[i], dot);
-                acc[rr][r] = fmaf(p[rr].d * dx, (float)dot, acc[rr][r]);
-            }
+            for (int i = 0; i < 8; ++i) dot = sdot4(q[i], x[i], dot);
+            acc[t] = fmaf(d * a.xd[(size_t)t * a.nb + b], (float)dot, acc[t]);
         }
     }
 };
@@ -237,56 +299,60 @@ struct TraitsQ80 {
 template <bool Q5>
 struct TraitsQ450 {
     static constexpr int UNIT = 32;
-    struct Prep {
-        uint32_t lo[4], hi[4];
-        float d;
+    static constexpr bool NEED_XM = false, NEED_XB = true, NEED_HS = false;
+    struct Raw {
+        A2<4> q;
+        A2<1> qh;
+        uint32_t d, sh;
     };
     // bits 0..3 of x4 -> bit 4 of bytes 0..3
     static __device__ __forceinline__ uint32_t spread4(uint32_t x4) {
         return ((x4 * 0x00204081u) & 0x01010101u) << 4;
     }
-    static __device__ __forceinline__ Prep load(const uint8_t* row, int b) {
+    static __device__ __forceinline__ Raw load(const uint8_t* row, int b) {
         const uint8_t* blk = row + (size_t)b * (Q5 ? Q5_0_BYTES : Q4_0_BYTES);
+        Raw r;
+        r.q = load_a2<4>(blk + (Q5 ? 6 : 2));
+        if constexpr (Q5) r.qh = load_a2<1>(blk + 2);
+        r.d = ld_u16(blk);
+        r.sh = (uint32_t)((uintptr_t)(blk + 2) & 3u);  // qh (+2) and qs (+6) share it
+        return r;
+    }
+    template <int MR>
+    static __device__ __forceinline__ void compute(const Raw& r, int b, const ActLds& a,
+                                                   float (&acc)[MR]) {
         uint32_t q[4];
-        ld_a2<4>(blk + (Q5 ? 6 : 2), q);
-        Prep p;
+        align_a2<4>(r.q, r.sh, q);
+        uint32_t lo[4], hi[4];
         uint32_t qh = 0;
         if constexpr (Q5) {
-            uint32_t t[1];
-            ld_a2<1>(blk + 2, t);
-            qh = t[0];
+            uint32_t t1[1];
+            align_a2<1>(r.qh, r.sh, t1);
+            qh = t1[0];
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            p.lo[t] = q[t] & 0x0F0F0F0Fu;
-            p.hi[t] = (q[t] >> 4) & 0x0F0F0F0Fu;
+            lo[t] = q[t] & 0x0F0F0F0Fu;
+            hi[t] = (q[t] >> 4) & 0x0F0F0F0Fu;
             if constexpr (Q5) {
-                p.lo[t] |= spread4((qh >> (4 * t)) & 0xFu);
-                p.hi[t] |= spread4((qh >> (16 + 4 * t)) & 0xFu);
+                lo[t] |= spread4((qh >> (4 * t)) & 0xFu);
+                hi[t] |= spread4((qh >> (16 + 4 * t)) & 0xFu);
             }
         }
-        p.d = f16_to_f32(ld_u16(blk));
-        return p;
-    }
-    template <int R, int MR>
-    static __device__ __forceinline__ void accum(const Prep (&p)[R], int b, const ActRows& a,
-                                                 float (&acc)[R][MR]) {
+        const float d = f16_to_f32(r.d);
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
+        for (int t = 0; t < MR; ++t) {
             uint32_t x[8];
-            ld_act32(a, r, b, x);
-            const float dx = a.sc[(size_t)r * a.nb + b];
-            const int off = (Q5 ? 16 : 8) * a.bs[(size_t)r * a.nb + b];
+            lds_x32(a, t, b, x);
+            int dot = 0;
 #pragma unroll
-            for (int rr = 0; rr < R; ++rr) {
-                int dot = 0;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    dot = sdot4(p[rr].lo[t], x[t], dot);
-                    dot = sdot4(p[rr].hi[t], x[4 + t], dot);
-                }
-                acc[rr][r] = fmaf(p[rr].d * dx, (float)(dot - off), acc[rr][r]);
+            for (int i = 0; i < 4; ++i) {
+                dot = sdot4(lo[i], x[i], dot);
+                dot = sdot4(hi[i], x[4 + i], dot);
             }
+            const size_t ix = (size_t)t * a.nb + b;
+            const int inner = dot - (Q5 ? 16 : 8) * a.xb[ix];
+            acc[t] = fmaf(d * a.xd[ix], (float)inner, acc[t]);
         }
     }
 };
@@ -299,8 +365,68 @@ template <> struct TraitsOf<T_Q8_0> { using type = TraitsQ80; };
 template <> struct TraitsOf<T_Q4_0> { using type = TraitsQ450<false>; };
 template <> struct TraitsOf<T_Q5_0> { using type = TraitsQ450<true>; };
 
-// One wave per R consecutive weight rows; 4 waves per workgroup.
-template <uint32_t T, int R, int MR>
+__host__ __device__ constexpr size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+// LDS bytes of the staged activation rows: qs | xd | xm or xb | hs.
+template <uint32_t T>
+__host__ __device__ constexpr size_t act_lds_bytes(int mr, int k) {
+    using Tr = typename TraitsOf<T>::type;
+    const size_t nb = (size_t)k / 32;
+    size_t b = align16((size_t)mr * lds_qs_row(k)) + align16((size_t)mr * nb * 4);
+    if (Tr::NEED_XM || Tr::NEED_XB) b += align16((size_t)mr * nb * 4);
+    if (Tr::NEED_HS) b += align16((size_t)mr * 2 * nb * 4);
+    return b;
+}
+
+template <uint32_t T, int MR>
+__device__ __forceinline__ ActLds stage_activations(uint8_t* lds, const int8_t* __restrict__ qs,
+                                                    const float* __restrict__ xs,
+                                                    const int32_t* __restrict__ xb, int k) {
+    using Tr = typename TraitsOf<T>::type;
+    const int nb = k / 32;
+    ActLds a;
+    a.k = k;
+    a.nb = nb;
+    size_t off = 0;
+    int8_t* lqs = (int8_t*)(lds + off);
+    off += align16((size_t)MR * lds_qs_row(k));
+    float* lxd = (float*)(lds + off);
+    off += align16((size_t)MR * nb * 4);
+    float* lxm = (float*)(lds + off);
+    int32_t* lxb = (int32_t*)(lds + off);
+    if (Tr::NEED_XM || Tr::NEED_XB) off += align16((size_t)MR * nb * 4);
+    int32_t* lhs = (int32_t*)(lds + off);
+    a.qs = lqs;
+    a.xd = lxd;
+    a.xm = lxm;
+    a.xb = lxb;
+    a.hs = lhs;
+
+    const int chunks = MR * k / 16;
+    for (int i = threadIdx.x; i < chunks; i += blockDim.x) {
+        const u32x4 v = ld_u32x4(qs + (size_t)i * 16);
+        const int r = i / (k / 16), c = i - r * (k / 16);
+        *(u32x4*)(lqs + r * lds_qs_row(k) + lds_qs_off(c * 16)) = v;
+        if constexpr (Tr::NEED_HS) {
+            int s = sdot4(v.x, 0x01010101u, 0);
+            s = sdot4(v.y, 0x01010101u, s);
+            s = sdot4(v.z, 0x01010101u, s);
+            s = sdot4(v.w, 0x01010101u, s);
+            lhs[(size_t)r * 2 * nb + (size_t)(c & 1) * nb + (c >> 1)] = s;
+        }
+    }
+    for (int i = threadIdx.x; i < MR * nb; i += blockDim.x) {
+        const float d = xs[i];
+        lxd[i] = d;
+        if constexpr (Tr::NEED_XM) lxm[i] = d * (float)xb[i];
+        if constexpr (Tr::NEED_XB) lxb[i] = xb[i];
+    }
+    return a;
+}
+
+// Persistent GEMV: wave w owns rows j = w, w + n_waves, ...; items (row, 64-unit slice) are
+// streamed through a P-deep ring of in-flight weight loads.
+template <uint32_t T, int MR, int P>
 __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ w, int64_t row_bytes,
                                               int k, int n, const int8_t* __restrict__ qs,
                                               const float* __restrict__ xs,
@@ -308,51 +434,151 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ w, int
                                               const float* __restrict__ bias,
                                               float* __restrict__ y) {
     using Tr = typename TraitsOf<T>::type;
+    extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
-    const int j0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-    if (j0 >= n) return;  // wave-uniform
-    const ActRows a{qs, xs, xb, k, k / 32};
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_waves = gridDim.x * 4;
+    const int wid = blockIdx.x * 4 + wave;
     const int units = k / Tr::UNIT;
+    const int iters = (units + 63) / 64;
+    const int my_rows = wid < n ? (n - 1 - wid) / n_waves + 1 : 0;
+    const int n_items = my_rows * iters;
 
-    float acc[R][MR];
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr)
-#pragma unroll
-        for (int r = 0; r < MR; ++r) acc[rr][r] = 0.0f;
+    // Item i of this wave is row wid + (i / iters) * n_waves, unit slice i % iters. Refills are
+    // issued for every slot, with the item and unit clamped to valid memory, so the number of
+    // loads in flight is the same on every path and the compiler's vmcnt waits only ever wait
+    // for the oldest slot.
+    auto slot_addr = [&](int item, const uint8_t*& row, int& u) {
+        const int c = item < n_items ? item : n_items - 1;
+        const int t = c / iters, it = c - t * iters;
+        row = w + (int64_t)(wid + t * n_waves) * row_bytes;
+        u = min(lane + 64 * it, units - 1);
+    };
 
-    for (int u = lane; u < units; u += 64) {
-        typename Tr::Prep p[R];
+    typename Tr::Raw ring[P];
+    if (n_items > 0) {
 #pragma unroll
-        for (int rr = 0; rr < R; ++rr) {
-            const int j = min(j0 + rr, n - 1);  // rows past n repeat row n-1 and are not stored
-            p[rr] = Tr::load(w + (int64_t)j * row_bytes, u);
+        for (int p = 0; p < P; ++p) {
+            const uint8_t* row;
+            int u;
+            slot_addr(p, row, u);
+            ring[p] = Tr::load(row, u);
         }
-        Tr::template accum<R, MR>(p, u, a, acc);
     }
+    // The activations are staged after the first loads are issued, so HBM is busy at once.
+    const ActLds a = stage_activations<T, MR>(lds, qs, xs, xb, k);
+    __syncthreads();
+    if (n_items == 0) return;
 
+    float acc[MR];
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
+    for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
+
+    const int n_pad = ((n_items + P - 1) / P) * P;
+    for (int base = 0; base < n_pad; base += P) {
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
-            float v = wave_sum(acc[rr][r]);
-            const int j = j0 + rr;
-            if (lane == r && j < n) {
-                if (bias) v += bias[j];
-                y[(size_t)r * n + j] = v;
+        for (int p = 0; p < P; ++p) {
+            const int item = base + p;
+            const int t = item / iters, it = item - t * iters;
+            const int u = lane + 64 * it;
+            {
+                // Straight-line for every slot: padded items and lanes past the row's last
+                // unit compute on clamped (valid) data and their result is dropped.
+                float nacc[MR];
+#pragma unroll
+                for (int r = 0; r < MR; ++r) nacc[r] = acc[r];
+                Tr::template compute<MR>(ring[p], min(u, units - 1), a, nacc);
+                const bool keep = item < n_items && u < units;
+#pragma unroll
+                for (int r = 0; r < MR; ++r) acc[r] = keep ? nacc[r] : acc[r];
+            }
+            {
+                const uint8_t* row;
+                int u2;
+                slot_addr(item + P, row, u2);
+                ring[p] = Tr::load(row, u2);
+            }
+            if (item < n_items && it == iters - 1) {
+                const int j = __builtin_amdgcn_readfirstlane(wid + t * n_waves);
+                const float bj = bias ? bias[j] : 0.0f;
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    float v = wave_sum(acc[r]);
+                    if (bias) v += bj;
+                    if (lane == r) y[(size_t)r * n + j] = v;
+                    acc[r] = 0.0f;
+                }
             }
         }
     }
 }
 
-template <uint32_t T, int R, int MR>
+static int g_cu_count = 0;
+
+static int cu_count() {
+    if (g_cu_count == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            cus > 0)
+            g_cu_count = cus;
+        else
+            g_cu_count = 256;
+    }
+    return g_cu_count;
+}
+
+// Launch shape, from sweeps on MI355X (Q4_K 14336x4096 and Q6_K 128256x4096, cold HBM):
+// short streams (a few items per wave even at 8 waves per SIMD) run best with no prefetch
+// ring and as many waves as fit; long streams with a 2-deep ring and 2 waves per SIMD.
+struct GemvShape {
+    int waves;  // persistent waves in the grid
+    bool deep;  // use the 2-deep ring
+};
+
+static GemvShape gemv_shape(int64_t items) {
+    const int64_t simds = (int64_t)cu_count() * 4;
+    GemvShape g;
+    if (items <= simds * 8 * 4) {
+        g.deep = false;
+        g.waves = (int)(items < simds * 8 ? items : simds * 8);
+    } else {
+        g.deep = true;
+        g.waves = (int)(simds * 2);
+    }
+    return g;
+}
+
+template <uint32_t T, int MR, int P>
 static hipError_t launch_t(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
-                           const int32_t* xb, const float* bias, float* y, hipStream_t stream) {
+                           const int32_t* xb, const float* bias, float* y, int waves,
+                           hipStream_t stream) {
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
-    const int waves = (n + R - 1) / R;
+    if (waves > n) waves = n;
     const int grid = (waves + 3) / 4;
-    hipLaunchKernelGGL((k_gemv<T, R, MR>), dim3(grid), dim3(256), 0, stream, w, row_bytes, k, n,
-                       qs, xs, xb, bias, y);
+    const size_t shmem = act_lds_bytes<T>(MR, k);
+    hipLaunchKernelGGL((k_gemv<T, MR, P>), dim3(grid), dim3(256), shmem, stream, w, row_bytes, k,
+                       n, qs, xs, xb, bias, y);
     return hipGetLastError();
+}
+
+// Most activation rows one launch stages in LDS for this type and k (1, 2, 4 or 8).
+template <uint32_t T>
+static int max_rows_per_launch(int k) {
+    constexpr size_t kLdsBudget = 48 * 1024;
+    int mr = 8;
+    while (mr > 1 && act_lds_bytes<T>(mr, k) > kLdsBudget) mr /= 2;
+    return mr;
+}
+
+template <uint32_t T, int MR>
+static hipError_t launch_mr(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
+                            const int32_t* xb, const float* bias, float* y, hipStream_t stream) {
+    using Tr = typename TraitsOf<T>::type;
+    const int iters = (k / Tr::UNIT + 63) / 64;
+    const GemvShape g = gemv_shape((int64_t)n * iters);
+    if (g.deep) return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, g.waves, stream);
+    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, g.waves, stream);
 }
 
 template <uint32_t T>
@@ -360,39 +586,45 @@ static hipError_t launch_rows(const uint8_t* w, int k, int n, int mr, const int8
                               const float* xs, const int32_t* xb, const float* bias, float* y,
                               hipStream_t stream) {
     switch (mr) {
-        case 1: return launch_t<T, 2, 1>(w, k, n, qs, xs, xb, bias, y, stream);
-        case 2: return launch_t<T, 2, 2>(w, k, n, qs, xs, xb, bias, y, stream);
-        case 4: return launch_t<T, 1, 4>(w, k, n, qs, xs, xb, bias, y, stream);
-        default: return launch_t<T, 1, 8>(w, k, n, qs, xs, xb, bias, y, stream);
+        case 1: return launch_mr<T, 1>(w, k, n, qs, xs, xb, bias, y, stream);
+        case 2: return launch_mr<T, 2>(w, k, n, qs, xs, xb, bias, y, stream);
+        case 4: return launch_mr<T, 4>(w, k, n, qs, xs, xb, bias, y, stream);
+        default: return launch_mr<T, 8>(w, k, n, qs, xs, xb, bias, y, stream);
     }
+}
+
+template <uint32_t T>
+static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int8_t* qs,
+                                const float* scales, const int32_t* bsums, const float* bias,
+                                float* y, hipStream_t stream) {
+    const int nb = k / 32;
+    const int cap = max_rows_per_launch<T>(k);
+    int t = 0;
+    while (t < m) {
+        const int left = m - t;
+        int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        while (mr > cap) mr /= 2;
+        const hipError_t e =
+            launch_rows<T>(w, k, n, mr, qs + (size_t)t * k, scales + (size_t)t * nb,
+                           bsums + (size_t)t * nb, bias, y + (size_t)t * n, stream);
+        if (e != hipSuccess) return e;
+        t += mr;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
                        hipStream_t stream) {
-    const int nb = k / 32;
-    int t = 0;
-    while (t < m) {
-        const int left = m - t;
-        const int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
-        const int8_t* q = qs + (size_t)t * k;
-        const float* s = scales + (size_t)t * nb;
-        const int32_t* b = bsums + (size_t)t * nb;
-        float* yy = y + (size_t)t * n;
-        hipError_t e;
-        switch (type) {
-            case T_Q4_K: e = launch_rows<T_Q4_K>(w, k, n, mr, q, s, b, bias, yy, stream); break;
-            case T_Q5_K: e = launch_rows<T_Q5_K>(w, k, n, mr, q, s, b, bias, yy, stream); break;
-            case T_Q6_K: e = launch_rows<T_Q6_K>(w, k, n, mr, q, s, b, bias, yy, stream); break;
-            case T_Q8_0: e = launch_rows<T_Q8_0>(w, k, n, mr, q, s, b, bias, yy, stream); break;
-            case T_Q4_0: e = launch_rows<T_Q4_0>(w, k, n, mr, q, s, b, bias, yy, stream); break;
-            case T_Q5_0: e = launch_rows<T_Q5_0>(w, k, n, mr, q, s, b, bias, yy, stream); break;
-            default: return hipErrorInvalidValue;
-        }
-        if (e != hipSuccess) return e;
-        t += mr;
+    switch (type) {
+        case T_Q4_K: return gemv_all_rows<T_Q4_K>(w, k, n, m, qs, scales, bsums, bias, y, stream);
+        case T_Q5_K: return gemv_all_rows<T_Q5_K>(w, k, n, m, qs, scales, bsums, bias, y, stream);
+        case T_Q6_K: return gemv_all_rows<T_Q6_K>(w, k, n, m, qs, scales, bsums, bias, y, stream);
+        case T_Q8_0: return gemv_all_rows<T_Q8_0>(w, k, n, m, qs, scales, bsums, bias, y, stream);
+        case T_Q4_0: return gemv_all_rows<T_Q4_0>(w, k, n, m, qs, scales, bsums, bias, y, stream);
+        case T_Q5_0: return gemv_all_rows<T_Q5_0>(w, k, n, m, qs, scales, bsums, bias, y, stream);
+        default: return hipErrorInvalidValue;
     }
-    return hipSuccess;
 }
 
 }  // namespace cllm_hip
