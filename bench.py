@@ -110,6 +110,38 @@ def decode_point(C, S, cfg, label, m, steps, warmup, cold=True):
                 route=C.matmul_route(qt, k, n, m))
 
 
+def prefill_layer(C, S, steps, warmup):
+    """The Llama-3-8B layer in the Q4_K_M mix at M = 512: every matrix timed on its own
+    (graph-timed, device-resident inputs), then summed."""
+    import torch
+    cfg = "c3_q4_k_m_layer"
+    per = {}
+    total_ms = 0.0
+    total_ops = 0.0
+    for label, qt, n, k in S.CONFIGS[cfg]["mats"]:
+        _, _, _, w = S.config_weight(cfg, label)
+        x = torch.from_numpy(S.config_activation(cfg, 512, k)).cuda()
+        wd = torch.from_numpy(w).cuda()
+        y = torch.empty((512, n), dtype=torch.float32, device="cuda")
+        ms = time_loop(lambda i: C.matmul_quant_dev(x, wd, qt, None, k, n, y=y), steps, warmup)
+        ops = 2.0 * 512 * n * k
+        per[label] = {"type": S.TYPE_NAMES[qt], "n": n, "k": k, "us": round(ms * 1e3, 1),
+                      "tops": round(ops / ms / 1e9, 1),
+                      "frac_int8": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4),
+                      "route": C.matmul_route(qt, k, n, 512)}
+        print(f"[bench] prefill {label} {S.TYPE_NAMES[qt]} {n}x{k} m=512: {ms * 1e3:.1f} us, "
+              f"{ops / ms / 1e9:.1f} TOPS", file=sys.stderr, flush=True)
+        total_ms += ms
+        total_ops += ops
+        del wd, x, y
+        torch.cuda.empty_cache()
+    return {"layer_us": round(total_ms * 1e3, 1), "tops": round(total_ops / total_ms / 1e9, 1),
+            "frac_int8": round(total_ops / total_ms / 1e9 / INT8_PEAK_TOPS, 4),
+            "tokens_per_s_per_layer": round(512 / (total_ms * 1e-3), 0),
+            "llama3_8b_32_layer_projection_tokens_per_s": round(512 / (32 * total_ms * 1e-3), 0),
+            "matrices": per}
+
+
 def cpu_baseline(S, cfg, label, seconds=10.0):
     """The reference's matmul_quant (AVX2 + ThreadPool) on this host, bounded sample."""
     import oracle
@@ -188,6 +220,8 @@ def main():
                     "tops": round(ops / p["ms_step"] / 1e9, 2),
                     "frac_int8": round(ops / p["ms_step"] / 1e9 / INT8_PEAK_TOPS, 4)}
         extra["c4_m_sweep"] = sweep
+        extra["c3_prefill_layer_m512"] = prefill_layer(C, S, max(5, args.steps // 20),
+                                                        max(2, args.warmup // 10))
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -185,12 +185,15 @@ int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t*
     return CLLM_HIP_OK;
 }
 
-bool use_mfma(uint32_t type, int m) { return m >= kMfmaMinRows && gemm_supported(type); }
+// The MFMA kernel walks K in 256-element steps.
+bool use_mfma(uint32_t type, int k, int m) {
+    return m >= kMfmaMinRows && k % 256 == 0 && gemm_supported(type);
+}
 
 hipError_t run_linear(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                       const float* sc, const int32_t* bs, const float* bias, float* y,
                       hipStream_t stream) {
-    if (use_mfma(type, m)) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+    if (use_mfma(type, k, m)) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
     return launch_gemv(type, w, k, n, m, qs, sc, bs, bias, y, stream);
 }
 
@@ -415,10 +418,9 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
 }
 
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows) {
-    (void)in_dim;
     (void)out_dim;
     if (!has_kernel(type)) return "none";
-    return use_mfma(type, n_rows) ? "mfma" : "gemv";
+    return use_mfma(type, in_dim, n_rows) ? "mfma" : "gemv";
 }
 
 }  // extern "C"

@@ -1,0 +1,103 @@
+"""Parity of the int8-MFMA prefill path (matmul_quant_batch with n_rows >= 16) on an MI355X.
+
+Same bars as the GEMV tests: |gpu - ref| <= 1e-4 * max(|ref|, 2^-8 * A) against the
+reference's fp32 output and |gpu - exact| <= 1e-4 * max(|exact|, 2^-10 * A) against the fp64
+evaluation of the same quantized terms (A = sum of absolute per-block terms).
+"""
+import numpy as np
+import pytest
+
+from conftest import load_golden, split_cases
+from cllm_inference_amd import synth as S
+from test_gpu_parity import check_close, _dev, TYPES
+
+pytestmark = pytest.mark.gpu
+
+
+def test_prefill_layer_slices_vs_reference_golden(gpu, orc):
+    """Q4_K_M layer (wq wk wv wo gate up: Q4_K, down: Q6_K): first 16 activation rows against
+    the first 512 rows of every matrix."""
+    cases = split_cases(load_golden("batch.npz"))
+    for label, qt, n, k in S.CONFIGS["c3_q4_k_m_layer"]["mats"]:
+        c = cases[label]
+        rows = int(c["meta"][4])
+        _, _, _, w = S.config_weight("c3_q4_k_m_layer", label)
+        x = S.config_activation("c3_q4_k_m_layer", 512, k)[:16]
+        wsub = w[: rows * S.row_bytes(qt, k)]
+        assert gpu.matmul_route(qt, k, rows, 16) == "mfma"
+        print("prefill slice", label, S.TYPE_NAMES[qt], rows, k, flush=True)
+        y = gpu.matmul_quant_batch(x, wsub, qt, None, k, rows, 16)
+        exact, abs_sum = orc.matmul_f64(x, wsub, qt, None, k, rows, 16)
+        check_close(y, c["y"], exact, abs_sum, label)
+
+
+@pytest.mark.parametrize("label", ["q5_k", "q8_0"])
+@pytest.mark.parametrize("m", [16, 64])
+def test_m_sweep_batches_vs_reference_golden(gpu, orc, label, m):
+    c = split_cases(load_golden("batch.npz"))[f"c4_{label}_m{m}"]
+    qt, n, k, w = S.config_weight("c4_m_sweep", label)
+    x = S.config_activation("c4_m_sweep", m, k)
+    wsub = w[: 512 * S.row_bytes(qt, k)]
+    print("m sweep", label, m, flush=True)
+    y = gpu.matmul_quant_batch(x, wsub, qt, None, k, 512, m)
+    exact, abs_sum = orc.matmul_f64(x, wsub, qt, None, k, 512, m)
+    check_close(y, c["y"], exact, abs_sum, f"{label} m{m}")
+
+
+@pytest.mark.parametrize("qt", TYPES)
+def test_mfma_matches_gemv_and_oracle(gpu, orc, qt):
+    """Same rows through the MFMA kernel (16 rows at once) and the GEMV kernel (8 + 8)."""
+    import torch
+    k, n, m = 1024, 300, 16
+    w = S.make_weight(qt, n, k, 70 + qt)
+    x = S.make_activation(m, k, 71 + qt, outliers=True)
+    wd, xd = _dev(w), _dev(x)
+    qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+    y_mfma = gpu.gemv_q8_dev(wd, qt, k, n, qs, sc, bs)  # 16 rows -> MFMA route
+    y_gemv = torch.cat([gpu.gemv_q8_dev(wd, qt, k, n, qs[i:i + 8], sc[i:i + 8], bs[i:i + 8])
+                        for i in (0, 8)])
+    assert gpu.matmul_route(qt, k, n, 16) == "mfma" and gpu.matmul_route(qt, k, n, 8) == "gemv"
+    exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+    yo = orc.matmul(x, w, qt, None, k, n, m)
+    check_close(y_mfma.cpu().numpy(), yo, exact, abs_sum, "mfma " + S.TYPE_NAMES[qt])
+    check_close(y_gemv.cpu().numpy(), yo, exact, abs_sum, "gemv " + S.TYPE_NAMES[qt])
+
+
+@pytest.mark.parametrize("qt", TYPES)
+def test_mfma_partial_tiles_and_bias(gpu, orc, qt):
+    for (n, k, m) in [(1, 256, 16), (130, 512, 17), (129, 256, 65), (64, 2048, 100)]:
+        w = S.make_weight(qt, n, k, n * 3 + m)
+        x = S.make_activation(m, k, n + m, outliers=True)
+        bias = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+        print("mfma tile case", S.TYPE_NAMES[qt], n, k, m, flush=True)
+        y = gpu.matmul_quant_batch(x, w, qt, bias, k, n, m)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, bias, k, n, m)
+        yo = orc.matmul(x, w, qt, bias, k, n, m)
+        check_close(y, yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")
+
+
+def test_full_prefill_layer_sampled_rows(gpu, orc):
+    """M = 512 through every matrix of the layer at full size; 8 activation rows (all
+    outputs) checked against the oracle, and every other row against row-wise GEMV."""
+    import torch
+    rng = np.random.default_rng(1)
+    for label, qt, n, k in S.CONFIGS["c3_q4_k_m_layer"]["mats"]:
+        _, _, _, w = S.config_weight("c3_q4_k_m_layer", label)
+        x = S.config_activation("c3_q4_k_m_layer", 512, k)
+        print("full layer", label, n, k, flush=True)
+        wd, xd = _dev(w), _dev(x)
+        y = gpu.matmul_quant_dev(xd, wd, qt, None, k, n)
+        torch.cuda.synchronize()
+        rows = np.sort(rng.choice(512, size=8, replace=False))
+        yo = orc.matmul(x[rows], w, qt, None, k, n, 8, threads=8)
+        exact, abs_sum = orc.matmul_f64(x[rows], w, qt, None, k, n, 8)
+        check_close(y.cpu().numpy()[rows], yo, exact, abs_sum, label)
+        # all 512 rows against the GEMV kernel (a different algorithm, same contract)
+        qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+        yg = torch.cat([gpu.gemv_q8_dev(wd, qt, k, n, qs[i:i + 8], sc[i:i + 8], bs[i:i + 8])
+                        for i in range(0, 512, 8)])
+        d = (y - yg).abs().cpu().numpy().astype(np.float64)
+        scale = np.maximum(np.abs(yg.cpu().numpy()), 1e-3 * np.abs(yg.cpu().numpy()).max(axis=1, keepdims=True))
+        assert (d / scale).max() < 1e-3, (label, (d / scale).max())
+        del wd, xd, y, yg
+        torch.cuda.empty_cache()

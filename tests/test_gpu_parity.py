@@ -3,11 +3,12 @@
 Bars (written into each test):
   - Q8_0 activation bytes (int8 qs, fp32 scales, int32 block sums): bit-exact.
   - Outputs: |gpu - ref| <= 1e-4 * max(|ref|, 2^-8 * A) against the reference's own fp32
-    output, where A is the row's sum of absolute per-block terms; and
-    |gpu - exact| <= 1e-4 * max(|exact|, 2^-10 * A) against the fp64 evaluation of the same
-    quantized terms. The reference's sequential fp32 sum is itself up to 1.5e-4 away from
-    exact under the 2^-10 floor on outlier inputs, so the comparison with the reference uses
-    the 2^-8 floor.
+    output, where A is the row's sum of absolute per-block terms; and, against the fp64
+    evaluation of the same quantized terms,
+    |gpu - exact| <= max(1e-4 * max(|exact|, 2^-10 * A), 2 * |ref - exact|):
+    never further from the exact value than twice the reference's own rounding error. The
+    reference's sequential fp32 sum is itself up to 1.5e-4 away from exact under the 2^-10
+    floor on outlier inputs, which is why neither gate can use that floor alone.
   - Anything the GEMV computes twice the same way (host vs device entry point, batch row vs
     single row) must agree bit for bit.
 """
@@ -31,10 +32,13 @@ def bits(a):
 def check_close(got, ref, exact, abs_sum, what):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
+    exact = np.asarray(exact, np.float64)
     d_ref = np.abs(got - ref) / np.maximum(np.maximum(np.abs(ref), abs_sum * 2.0 ** -8), 1e-30)
-    d_ex = np.abs(got - exact) / np.maximum(np.maximum(np.abs(exact), abs_sum * 2.0 ** -10), 1e-30)
     assert d_ref.max() <= TOL, f"{what}: vs reference {d_ref.max():.3g} at {np.argmax(d_ref)}"
-    assert d_ex.max() <= TOL, f"{what}: vs exact {d_ex.max():.3g} at {np.argmax(d_ex)}"
+    allowed = np.maximum(TOL * np.maximum(np.abs(exact), abs_sum * 2.0 ** -10),
+                         2.0 * np.abs(ref - exact))
+    excess = np.abs(got - exact) - allowed
+    assert excess.max() <= 0, f"{what}: vs exact exceeds the bound at {np.argmax(excess)}"
 
 
 def _dev(a):
