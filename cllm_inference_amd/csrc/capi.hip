@@ -213,7 +213,7 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
     if ((rc = resolve_weights(st, w, row_bytes(type, in_dim) * (size_t)out_dim, &wd))) return rc;
     HIP_TRY(st->x.ensure(xb, st->stream));
     HIP_TRY(st->y.ensure(yb, st->stream));
-    HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
+    if (use_mfma(type, in_dim, n_rows)) HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
     HIP_TRY(hipMemcpyAsync(st->x.p, x, xb, hipMemcpyHostToDevice, st->stream));
     const float* bd = nullptr;
     if (bias) {
@@ -222,10 +222,15 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
                                hipMemcpyHostToDevice, st->stream));
         bd = (const float*)st->bias.p;
     }
-    HIP_TRY(launch_quantize_q8_0((const float*)st->x.p, (int64_t)n_rows * in_dim / 32,
-                                 st->act.qs, st->act.sc, st->act.bs, st->stream));
-    HIP_TRY(run_linear(type, wd, in_dim, out_dim, n_rows, st->act.qs, st->act.sc, st->act.bs, bd,
-                       (float*)st->y.p, st->stream));
+    if (use_mfma(type, in_dim, n_rows)) {
+        HIP_TRY(launch_quantize_q8_0((const float*)st->x.p, (int64_t)n_rows * in_dim / 32,
+                                     st->act.qs, st->act.sc, st->act.bs, st->stream));
+        HIP_TRY(launch_gemm(type, wd, in_dim, out_dim, n_rows, st->act.qs, st->act.sc,
+                            st->act.bs, bd, (float*)st->y.p, st->stream));
+    } else {
+        HIP_TRY(launch_gemv_fused(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
+                                  (float*)st->y.p, st->stream));
+    }
     HIP_TRY(hipMemcpyAsync(y, st->y.p, yb, hipMemcpyDeviceToHost, st->stream));
     HIP_TRY(hipStreamSynchronize(st->stream));
     return CLLM_HIP_OK;
@@ -403,6 +408,11 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
     DeviceState* st;
     if ((rc = acquire(&st))) return rc;
     hipStream_t s = (hipStream_t)stream;
+    if (!use_mfma(type, in_dim, n_rows)) {
+        // decode-sized batch: one launch that quantizes its activation rows in LDS
+        HIP_TRY(launch_gemv_fused(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, s));
+        return CLLM_HIP_OK;
+    }
     Workspace* ws;
     {
         std::lock_guard<std::mutex> lk(st->mtx);

@@ -76,6 +76,35 @@ __device__ __forceinline__ void k4_scale_min(uint32_t s0, uint32_t s1, uint32_t 
     m = j < 4 ? m_lo : m_hi;
 }
 
+// Q8_0 quantization of 4 consecutive elements of a 32-element block whose |x| maximum is
+// amax (quantize_row_q8_0, src/core/quant.cpp:431-450, bit for bit):
+//   d = amax / 127 and id = 1 / d (correctly rounded divisions), q = clamp(rint(x * id)).
+// When amax is tiny enough that 1/d overflows, x * id is +-inf (or NaN for 0 * inf); the
+// reference's (int) conversion of such values is x86's cvttss2si result, INT_MIN, which the
+// clamp turns into -128, so that value is produced here too (v_cvt_i32_f32 would saturate).
+// Returns the four int8 values packed little-endian; `sum` receives their sum.
+__device__ __forceinline__ uint32_t q8_quant4(float x0, float x1, float x2, float x3, float id,
+                                              int& sum) {
+    const float e[4] = {x0, x1, x2, x3};
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float r = __builtin_rintf(__fmul_rn(e[i], id));
+        int t = (fabsf(r) < 2147483648.0f) ? (int)r : INT32_MIN;
+        t = t > 127 ? 127 : t;
+        t = t < -128 ? -128 : t;
+        q[i] = t;
+    }
+    sum = q[0] + q[1] + q[2] + q[3];
+    return (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+           ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+}
+
+__device__ __forceinline__ float q8_scale(float amax) { return __fdiv_rn(amax, 127.0f); }
+__device__ __forceinline__ float q8_inv_scale(float d) {
+    return (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
+}
+
 // Cross-lane moves inside a row of 16 lanes (DPP; no LDS traffic).
 template <int CTRL>
 __device__ __forceinline__ int dpp_i32(int v) {

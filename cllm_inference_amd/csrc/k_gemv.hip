@@ -381,7 +381,8 @@ __host__ __device__ constexpr size_t act_lds_bytes(int mr, int k) {
 template <uint32_t T, int MR>
 __device__ __forceinline__ ActLds stage_activations(uint8_t* lds, const int8_t* __restrict__ qs,
                                                     const float* __restrict__ xs,
-                                                    const int32_t* __restrict__ xb, int k) {
+                                                    const int32_t* __restrict__ xb, int k,
+                                                    bool copy) {
     using Tr = typename TraitsOf<T>::type;
     const int nb = k / 32;
     ActLds a;
@@ -401,6 +402,7 @@ __device__ __forceinline__ ActLds stage_activations(uint8_t* lds, const int8_t* 
     a.xm = lxm;
     a.xb = lxb;
     a.hs = lhs;
+    if (!copy) return a;
 
     const int chunks = MR * k / 16;
     for (int i = threadIdx.x; i < chunks; i += blockDim.x) {
@@ -424,21 +426,74 @@ __device__ __forceinline__ ActLds stage_activations(uint8_t* lds, const int8_t* 
     return a;
 }
 
+// Fused decode: quantize MR fp32 activation rows straight into the LDS layout above, with
+// exactly the arithmetic of k_quantize_q8_0 (q8_scale / q8_inv_scale / q8_quant4). Eight
+// lanes own a 32-element block; the loop trip count is uniform so every shuffle has all 64
+// lanes, and lanes past the last block work on a clamped block and store nothing.
+template <uint32_t T, int MR>
+__device__ __forceinline__ void quantize_activations(const ActLds& a, const float* __restrict__ x) {
+    using Tr = typename TraitsOf<T>::type;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const int nb = a.nb;
+    const int total = MR * nb * 8;
+    int8_t* lqs = const_cast<int8_t*>(a.qs);
+    float* lxd = const_cast<float*>(a.xd);
+    float* lxm = const_cast<float*>(a.xm);
+    int32_t* lxb = const_cast<int32_t*>(a.xb);
+    int32_t* lhs = const_cast<int32_t*>(a.hs);
+    for (int base = 0; base < total; base += blockDim.x) {
+        const int i = base + threadIdx.x;
+        const bool valid = i < total;
+        const int g = (valid ? i : total - 1) >> 3;  // activation block (row-major over rows)
+        const int part = i & 7;
+        const int r = g / nb, b = g - r * nb;
+        const f32x4 v = *(const f32x4*)(x + (size_t)g * 32 + part * 4);
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
+        const float d = q8_scale(amax);
+        const float id = q8_inv_scale(d);
+        int s;
+        const uint32_t packed = q8_quant4(v.x, v.y, v.z, v.w, id, s);
+        if (valid) *(uint32_t*)(lqs + r * lds_qs_row(a.k) + lds_qs_off(b * 32 + part * 4)) = packed;
+        s += __shfl_xor(s, 1, 8);
+        s += __shfl_xor(s, 2, 8);  // now the sum of this lane's 16-element half
+        if constexpr (Tr::NEED_HS) {
+            if (valid && (part & 3) == 0) lhs[(size_t)r * 2 * nb + (size_t)(part >> 2) * nb + b] = s;
+        }
+        s += __shfl_xor(s, 4, 8);  // the block sum
+        if (valid && part == 0) {
+            lxd[g] = d;
+            if constexpr (Tr::NEED_XM) lxm[g] = d * (float)s;
+            if constexpr (Tr::NEED_XB) lxb[g] = s;
+        }
+    }
+}
+
 // Persistent GEMV: wave w owns rows j = w, w + n_waves, ...; items (row, 64-unit slice) are
 // streamed through a P-deep ring of in-flight weight loads.
+// Workgroup size: 16 waves share one staged (or quantized) activation batch for decode-sized
+// batches; with 4 or 8 activation rows the per-wave registers need the 256-VGPR budget of
+// 4-wave workgroups.
+template <int MR>
+constexpr int gemv_threads() { return MR <= 2 ? 1024 : 256; }
+
 template <uint32_t T, int MR, int P>
-__global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ w, int64_t row_bytes,
+__global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __restrict__ w, int64_t row_bytes,
                                               int k, int n, const int8_t* __restrict__ qs,
                                               const float* __restrict__ xs,
                                               const int32_t* __restrict__ xb,
                                               const float* __restrict__ bias,
-                                              float* __restrict__ y) {
+                                              float* __restrict__ y,
+                                              const float* __restrict__ x_f32) {
     using Tr = typename TraitsOf<T>::type;
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n_waves = gridDim.x * 4;
-    const int wid = blockIdx.x * 4 + wave;
+    constexpr int kWaves = gemv_threads<MR>() / 64;
+    const int n_waves = gridDim.x * kWaves;
+    const int wid = blockIdx.x * kWaves + wave;
     const int units = k / Tr::UNIT;
     const int iters = (units + 63) / 64;
     const int my_rows = wid < n ? (n - 1 - wid) / n_waves + 1 : 0;
@@ -466,7 +521,9 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ w, int
         }
     }
     // The activations are staged after the first loads are issued, so HBM is busy at once.
-    const ActLds a = stage_activations<T, MR>(lds, qs, xs, xb, k);
+    // Activations: copied from a Q8_0 batch, or (fused decode, x_f32 != null) quantized here.
+    const ActLds a = stage_activations<T, MR>(lds, qs, xs, xb, k, x_f32 == nullptr);
+    if (x_f32 != nullptr) quantize_activations<T, MR>(a, x_f32);
     __syncthreads();
     if (n_items == 0) return;
 
@@ -551,14 +608,15 @@ static GemvShape gemv_shape(int64_t items) {
 
 template <uint32_t T, int MR, int P>
 static hipError_t launch_t(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
-                           const int32_t* xb, const float* bias, float* y, int waves,
-                           hipStream_t stream) {
+                           const int32_t* xb, const float* bias, float* y, const float* x_f32,
+                           int waves, hipStream_t stream) {
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
     if (waves > n) waves = n;
-    const int grid = (waves + 3) / 4;
+    constexpr int kWaves = gemv_threads<MR>() / 64;
+    const int grid = (waves + kWaves - 1) / kWaves;
     const size_t shmem = act_lds_bytes<T>(MR, k);
-    hipLaunchKernelGGL((k_gemv<T, MR, P>), dim3(grid), dim3(256), shmem, stream, w, row_bytes, k,
-                       n, qs, xs, xb, bias, y);
+    hipLaunchKernelGGL((k_gemv<T, MR, P>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, w, row_bytes, k,
+                       n, qs, xs, xb, bias, y, x_f32);
     return hipGetLastError();
 }
 
@@ -573,30 +631,33 @@ static int max_rows_per_launch(int k) {
 
 template <uint32_t T, int MR>
 static hipError_t launch_mr(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
-                            const int32_t* xb, const float* bias, float* y, hipStream_t stream) {
+                            const int32_t* xb, const float* bias, float* y, const float* x_f32,
+                            hipStream_t stream) {
     using Tr = typename TraitsOf<T>::type;
     const int iters = (k / Tr::UNIT + 63) / 64;
     const GemvShape g = gemv_shape((int64_t)n * iters);
-    if (g.deep) return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, g.waves, stream);
-    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, g.waves, stream);
+    if (g.deep) return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, g.waves, stream);
+    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, g.waves, stream);
 }
 
 template <uint32_t T>
 static hipError_t launch_rows(const uint8_t* w, int k, int n, int mr, const int8_t* qs,
                               const float* xs, const int32_t* xb, const float* bias, float* y,
-                              hipStream_t stream) {
+                              const float* x_f32, hipStream_t stream) {
     switch (mr) {
-        case 1: return launch_mr<T, 1>(w, k, n, qs, xs, xb, bias, y, stream);
-        case 2: return launch_mr<T, 2>(w, k, n, qs, xs, xb, bias, y, stream);
-        case 4: return launch_mr<T, 4>(w, k, n, qs, xs, xb, bias, y, stream);
-        default: return launch_mr<T, 8>(w, k, n, qs, xs, xb, bias, y, stream);
+        case 1: return launch_mr<T, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
+        case 2: return launch_mr<T, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
+        case 4: return launch_mr<T, 4>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
+        default: return launch_mr<T, 8>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
     }
 }
 
+// Runs every activation row through the GEMV, MR rows per launch. With x_f32 set, the rows
+// are fp32 and each launch quantizes its rows itself (qs / scales / bsums unused).
 template <uint32_t T>
 static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int8_t* qs,
                                 const float* scales, const int32_t* bsums, const float* bias,
-                                float* y, hipStream_t stream) {
+                                float* y, const float* x_f32, hipStream_t stream) {
     const int nb = k / 32;
     const int cap = max_rows_per_launch<T>(k);
     int t = 0;
@@ -604,27 +665,40 @@ static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int
         const int left = m - t;
         int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
         while (mr > cap) mr /= 2;
-        const hipError_t e =
-            launch_rows<T>(w, k, n, mr, qs + (size_t)t * k, scales + (size_t)t * nb,
-                           bsums + (size_t)t * nb, bias, y + (size_t)t * n, stream);
+        const hipError_t e = launch_rows<T>(
+            w, k, n, mr, qs ? qs + (size_t)t * k : nullptr, scales ? scales + (size_t)t * nb : nullptr,
+            bsums ? bsums + (size_t)t * nb : nullptr, bias, y + (size_t)t * n,
+            x_f32 ? x_f32 + (size_t)t * k : nullptr, stream);
         if (e != hipSuccess) return e;
         t += mr;
     }
     return hipSuccess;
 }
 
+static hipError_t gemv_dispatch(uint32_t type, const uint8_t* w, int k, int n, int m,
+                                const int8_t* qs, const float* scales, const int32_t* bsums,
+                                const float* bias, float* y, const float* x_f32,
+                                hipStream_t stream) {
+    switch (type) {
+        case T_Q4_K: return gemv_all_rows<T_Q4_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
+        case T_Q5_K: return gemv_all_rows<T_Q5_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
+        case T_Q6_K: return gemv_all_rows<T_Q6_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
+        case T_Q8_0: return gemv_all_rows<T_Q8_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
+        case T_Q4_0: return gemv_all_rows<T_Q4_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
+        case T_Q5_0: return gemv_all_rows<T_Q5_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
                        hipStream_t stream) {
-    switch (type) {
-        case T_Q4_K: return gemv_all_rows<T_Q4_K>(w, k, n, m, qs, scales, bsums, bias, y, stream);
-        case T_Q5_K: return gemv_all_rows<T_Q5_K>(w, k, n, m, qs, scales, bsums, bias, y, stream);
-        case T_Q6_K: return gemv_all_rows<T_Q6_K>(w, k, n, m, qs, scales, bsums, bias, y, stream);
-        case T_Q8_0: return gemv_all_rows<T_Q8_0>(w, k, n, m, qs, scales, bsums, bias, y, stream);
-        case T_Q4_0: return gemv_all_rows<T_Q4_0>(w, k, n, m, qs, scales, bsums, bias, y, stream);
-        case T_Q5_0: return gemv_all_rows<T_Q5_0>(w, k, n, m, qs, scales, bsums, bias, y, stream);
-        default: return hipErrorInvalidValue;
-    }
+    return gemv_dispatch(type, w, k, n, m, qs, scales, bsums, bias, y, nullptr, stream);
+}
+
+hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
+                             const float* x, const float* bias, float* y, hipStream_t stream) {
+    return gemv_dispatch(type, w, k, n, m, nullptr, nullptr, nullptr, bias, y, x, stream);
 }
 
 }  // namespace cllm_hip

@@ -1,12 +1,8 @@
 // k_quantize.hip -- fp32 -> Q8_0 activation quantization on gfx950.
 //
-// Restates quantize_row_q8_0 (src/core/quant.cpp:420-452) bit for bit:
-//   amax = max |x| over the 32-element block
-//   d    = amax / 127.0f          (IEEE division, correctly rounded)
-//   id   = d != 0 ? 1.0f / d : 0  (IEEE division, correctly rounded)
-//   q    = clamp(rint(x * id), -128, 127)   (rint = nearbyint in round-to-nearest-even)
-//   bsum = sum of the block's q
-// amax is a max, so the order of the cross-lane reduction cannot change it.
+// Restates quantize_row_q8_0 (src/core/quant.cpp:420-452) bit for bit (q8_scale,
+// q8_inv_scale and q8_quant4 in device_utils.h hold the arithmetic); bsum is the sum of the
+// block's q. amax is a max, so the order of the cross-lane reduction cannot change it.
 //
 // Mapping: the input is n_blocks contiguous 32-element blocks (M rows of K, K % 32 == 0, are
 // exactly M*K/32 consecutive blocks). Eight lanes own one block, four elements each, loaded as
@@ -34,27 +30,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
     amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
     amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
 
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float id = (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
-
-    int q[4];
-    const float e[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float r = __builtin_rintf(__fmul_rn(e[i], id));
-        // When amax is tiny enough that 1/d overflows, x * id is +-inf (or NaN for 0 * inf).
-        // The reference's (int) conversion of such values is x86's cvttss2si result, INT_MIN,
-        // which the clamp then turns into -128; v_cvt_i32_f32 would saturate instead.
-        int t = (fabsf(r) < 2147483648.0f) ? (int)r : INT32_MIN;
-        t = t > 127 ? 127 : t;
-        t = t < -128 ? -128 : t;
-        q[i] = t;
-    }
-    const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                            ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+    const float d = q8_scale(amax);
+    const float id = q8_inv_scale(d);
+    int s;
+    const uint32_t packed = q8_quant4(v.x, v.y, v.z, v.w, id, s);
     *(uint32_t*)(qs + blk * 32 + part * 4) = packed;
 
-    int s = q[0] + q[1] + q[2] + q[3];
     s += __shfl_xor(s, 1, 8);
     s += __shfl_xor(s, 2, 8);
     s += __shfl_xor(s, 4, 8);

@@ -19,6 +19,12 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, con
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
                        hipStream_t stream);
 
+// Same as launch_gemv with fp32 activation rows x[m][k]: each launch quantizes its rows to
+// Q8_0 in LDS (bit-identical to launch_quantize_q8_0) instead of reading a quantized batch,
+// so a decode step is a single kernel.
+hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
+                             const float* x, const float* bias, float* y, hipStream_t stream);
+
 // Same contract as launch_gemv, on the int8 MFMA path (m >= 1, any n; k % 256 == 0 for the
 // K-quants, k % 32 == 0 otherwise). Returns hipErrorNotSupported for types without an MFMA
 // kernel.

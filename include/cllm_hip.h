@@ -100,8 +100,9 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
                          const int8_t* qs, const float* scales, const int32_t* bsums,
                          const float* bias, float* y, void* stream);
 
-/* matmul_quant_batch on device buffers: quantizes x into a library-owned per-stream
- * workspace, then runs the GEMV (small n_rows) or the int8-MFMA GEMM (large n_rows). */
+/* matmul_quant_batch on device buffers. Small n_rows: one GEMV launch that quantizes its
+ * activation rows itself. Large n_rows: quantizes x into a library-owned per-stream
+ * workspace, then runs the MFMA GEMM. */
 int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,
                               int in_dim, int out_dim, int n_rows, float* y, void* stream);
 
