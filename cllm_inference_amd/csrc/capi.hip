@@ -8,6 +8,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -69,21 +70,28 @@ struct DevBuf {
     }
 };
 
-// Q8_0 activation workspace: qs[m*k] | scales[m*k/32] | bsums[m*k/32].
+// Activation workspace: the Q8_0 batch qs[m*k] | scales[m*k/32] | bsums[m*k/32], and the
+// MFMA path's qh[m*k] (fp16) | px[m*k/32] (dx * bsum).
 struct Workspace {
     DevBuf buf;
     int8_t* qs = nullptr;
     float* sc = nullptr;
     int32_t* bs = nullptr;
+    _Float16* qh = nullptr;
+    float* px = nullptr;
     hipError_t ensure(int k, int m, hipStream_t stream) {
         const size_t n = (size_t)k * (size_t)m;
         const size_t qs_bytes = (n + 255) & ~(size_t)255;
         const size_t sc_bytes = ((n / 32) * 4 + 255) & ~(size_t)255;
-        hipError_t e = buf.ensure(qs_bytes + 2 * sc_bytes, stream);
+        const size_t qh_bytes = (2 * n + 255) & ~(size_t)255;
+        hipError_t e = buf.ensure(qs_bytes + 3 * sc_bytes + qh_bytes, stream);
         if (e != hipSuccess) return e;
-        qs = (int8_t*)buf.p;
-        sc = (float*)((char*)buf.p + qs_bytes);
-        bs = (int32_t*)((char*)buf.p + qs_bytes + sc_bytes);
+        char* p = (char*)buf.p;
+        qs = (int8_t*)p;
+        sc = (float*)(p + qs_bytes);
+        bs = (int32_t*)(p + qs_bytes + sc_bytes);
+        px = (float*)(p + qs_bytes + 2 * sc_bytes);
+        qh = (_Float16*)(p + qs_bytes + 3 * sc_bytes);
         return hipSuccess;
     }
 };
@@ -190,11 +198,46 @@ bool use_mfma(uint32_t type, int k, int m) {
     return m >= kMfmaMinRows && k % 256 == 0 && gemm_supported(type);
 }
 
-hipError_t run_linear(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
-                      const float* sc, const int32_t* bs, const float* bias, float* y,
-                      hipStream_t stream) {
-    if (use_mfma(type, k, m)) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
-    return launch_gemv(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+// The MFMA route runs the int8-MFMA kernel (k_gemm.hip); CLLM_HIP_GEMM=f16 selects the
+// fp16-MFMA kernel (k_gemm16.hip), which has the lower VALU cost per output but not yet the
+// deeper load pipeline it needs to be faster.
+bool int8_gemm_requested() {
+    const char* e = std::getenv("CLLM_HIP_GEMM");
+    return !(e && std::strcmp(e, "f16") == 0);
+}
+
+// MFMA route on a Q8_0 batch already in device memory; ws supplies the fp16 staging.
+hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
+                    const float* sc, const int32_t* bs, const float* bias, float* y,
+                    Workspace* ws, hipStream_t stream) {
+    if (int8_gemm_requested()) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+    hipError_t e = launch_q8_to_mfma(qs, sc, bs, (int64_t)m * k / 32, ws->qh, ws->px, stream);
+    if (e != hipSuccess) return e;
+    return launch_gemm16(type, w, k, n, m, ws->qh, sc, ws->px, bias, y, stream);
+}
+
+// MFMA route from fp32 activations: quantize straight into the format the kernel reads.
+hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
+                        const float* bias, float* y, Workspace* ws, hipStream_t stream) {
+    const int64_t nblk = (int64_t)m * k / 32;
+    if (int8_gemm_requested()) {
+        hipError_t e = launch_quantize_q8_0(x, nblk, ws->qs, ws->sc, ws->bs, stream);
+        if (e != hipSuccess) return e;
+        return launch_gemm(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, stream);
+    }
+    hipError_t e = launch_quantize_mfma(x, nblk, ws->sc, ws->qh, ws->px, stream);
+    if (e != hipSuccess) return e;
+    return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
+}
+
+// The per-stream activation workspace of the device entry points, grown to m x k.
+int stream_workspace(DeviceState* st, hipStream_t s, int k, int m, Workspace** out) {
+    std::lock_guard<std::mutex> lk(st->mtx);
+    auto& slot = st->dev_ws[s];
+    if (!slot) slot = std::make_unique<Workspace>();
+    HIP_TRY(slot->ensure(k, m, s));
+    *out = slot.get();
+    return CLLM_HIP_OK;
 }
 
 // Host-buffer matmul shared by matmul_quant and matmul_quant_batch.
@@ -223,10 +266,8 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
         bd = (const float*)st->bias.p;
     }
     if (use_mfma(type, in_dim, n_rows)) {
-        HIP_TRY(launch_quantize_q8_0((const float*)st->x.p, (int64_t)n_rows * in_dim / 32,
-                                     st->act.qs, st->act.sc, st->act.bs, st->stream));
-        HIP_TRY(launch_gemm(type, wd, in_dim, out_dim, n_rows, st->act.qs, st->act.sc,
-                            st->act.bs, bd, (float*)st->y.p, st->stream));
+        HIP_TRY(run_gemm_f32(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
+                             (float*)st->y.p, &st->act, st->stream));
     } else {
         HIP_TRY(launch_gemv_fused(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
                                   (float*)st->y.p, st->stream));
@@ -392,8 +433,16 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
         return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
     DeviceState* st;
     if ((rc = acquire(&st))) return rc;
-    HIP_TRY(run_linear(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums, bias,
-                       y, (hipStream_t)stream));
+    hipStream_t s = (hipStream_t)stream;
+    if (!use_mfma(type, in_dim, n_rows)) {
+        HIP_TRY(launch_gemv(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums,
+                            bias, y, s));
+        return CLLM_HIP_OK;
+    }
+    Workspace* ws;
+    if ((rc = stream_workspace(st, s, in_dim, n_rows, &ws))) return rc;
+    HIP_TRY(run_gemm(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums, bias, y,
+                     ws, s));
     return CLLM_HIP_OK;
 }
 
@@ -414,16 +463,8 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
         return CLLM_HIP_OK;
     }
     Workspace* ws;
-    {
-        std::lock_guard<std::mutex> lk(st->mtx);
-        auto& slot = st->dev_ws[s];
-        if (!slot) slot = std::make_unique<Workspace>();
-        ws = slot.get();
-        HIP_TRY(ws->ensure(in_dim, n_rows, s));
-    }
-    HIP_TRY(launch_quantize_q8_0(x, (int64_t)n_rows * in_dim / 32, ws->qs, ws->sc, ws->bs, s));
-    HIP_TRY(run_linear(type, (const uint8_t*)w, in_dim, out_dim, n_rows, ws->qs, ws->sc, ws->bs,
-                       bias, y, s));
+    if ((rc = stream_workspace(st, s, in_dim, n_rows, &ws))) return rc;
+    HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws, s));
     return CLLM_HIP_OK;
 }
 

@@ -12,11 +12,16 @@
 
 namespace cllm_hip {
 
+// Besides the Q8_0 row (qs, scales, bsums, any of which may be null), the MFMA path asks for
+// the quantized values as fp16 (qh, exact: |q| <= 128) and dx * bsum (px, the K-quant
+// minimum term's activation factor).
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__ x,
                                                        int64_t n_blocks,
                                                        int8_t* __restrict__ qs,
                                                        float* __restrict__ scales,
-                                                       int32_t* __restrict__ bsums) {
+                                                       int32_t* __restrict__ bsums,
+                                                       _Float16* __restrict__ qh,
+                                                       float* __restrict__ px) {
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gt >> 3;
     const int part = (int)(gt & 7);
@@ -34,15 +39,41 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
     const float id = q8_inv_scale(d);
     int s;
     const uint32_t packed = q8_quant4(v.x, v.y, v.z, v.w, id, s);
-    *(uint32_t*)(qs + blk * 32 + part * 4) = packed;
+    if (qs) *(uint32_t*)(qs + blk * 32 + part * 4) = packed;
+    if (qh) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 hv = {(_Float16)(int8_t)(packed & 0xFF), (_Float16)(int8_t)(packed >> 8),
+                       (_Float16)(int8_t)(packed >> 16), (_Float16)(int8_t)(packed >> 24)};
+        *(h4*)(qh + blk * 32 + part * 4) = hv;
+    }
 
     s += __shfl_xor(s, 1, 8);
     s += __shfl_xor(s, 2, 8);
     s += __shfl_xor(s, 4, 8);
     if (part == 0) {
-        scales[blk] = d;
-        bsums[blk] = s;
+        if (scales) scales[blk] = d;
+        if (bsums) bsums[blk] = s;
+        if (px) px[blk] = d * (float)s;
     }
+}
+
+// int8 qs / fp32 scales / int32 bsums (an already-quantized batch) -> the MFMA path's fp16
+// values and dx * bsum.
+__global__ __launch_bounds__(256) void k_q8_to_mfma(const int8_t* __restrict__ qs,
+                                                    const float* __restrict__ scales,
+                                                    const int32_t* __restrict__ bsums,
+                                                    int64_t n_blocks, _Float16* __restrict__ qh,
+                                                    float* __restrict__ px) {
+    const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t blk = gt >> 3;
+    const int part = (int)(gt & 7);
+    if (blk >= n_blocks) return;
+    const uint32_t packed = *(const uint32_t*)(qs + blk * 32 + part * 4);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 hv = {(_Float16)(int8_t)(packed & 0xFF), (_Float16)(int8_t)(packed >> 8),
+                   (_Float16)(int8_t)(packed >> 16), (_Float16)(int8_t)(packed >> 24)};
+    *(h4*)(qh + blk * 32 + part * 4) = hv;
+    if (part == 0) px[blk] = scales[blk] * (float)bsums[blk];
 }
 
 hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* qs, float* scales,
@@ -51,7 +82,25 @@ hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* qs, fl
     const int64_t threads = n_blocks * 8;
     const int64_t grid = (threads + 255) / 256;
     hipLaunchKernelGGL(k_quantize_q8_0, dim3((unsigned)grid), dim3(256), 0, stream, x, n_blocks,
-                       qs, scales, bsums);
+                       qs, scales, bsums, (_Float16*)nullptr, (float*)nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_mfma(const float* x, int64_t n_blocks, float* scales,
+                                _Float16* qh, float* px, hipStream_t stream) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t grid = (n_blocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(k_quantize_q8_0, dim3((unsigned)grid), dim3(256), 0, stream, x, n_blocks,
+                       (int8_t*)nullptr, scales, (int32_t*)nullptr, qh, px);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_to_mfma(const int8_t* qs, const float* scales, const int32_t* bsums,
+                             int64_t n_blocks, _Float16* qh, float* px, hipStream_t stream) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t grid = (n_blocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(k_q8_to_mfma, dim3((unsigned)grid), dim3(256), 0, stream, qs, scales,
+                       bsums, n_blocks, qh, px);
     return hipGetLastError();
 }
 

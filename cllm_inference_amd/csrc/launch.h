@@ -13,6 +13,14 @@ namespace cllm_hip {
 hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* qs, float* scales,
                                 int32_t* bsums, hipStream_t stream);
 
+// The MFMA path's activation format: fp32 -> Q8_0 as above, kept as dx (scales), the
+// quantized values as exact fp16 (qh[m * k]) and dx * bsum (px[m * k / 32]).
+hipError_t launch_quantize_mfma(const float* x, int64_t n_blocks, float* scales,
+                                _Float16* qh, float* px, hipStream_t stream);
+// Same format from an already-quantized Q8_0 batch.
+hipError_t launch_q8_to_mfma(const int8_t* qs, const float* scales, const int32_t* bsums,
+                             int64_t n_blocks, _Float16* qh, float* px, hipStream_t stream);
+
 // y[t, j] = vec_dot(W row j, activation row t) (+ bias[j]) for t < m, j < n.
 // Activation rows are Q8_0: qs[t * k], scales / bsums[t * k / 32]. Any m >= 1.
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
@@ -32,5 +40,11 @@ hipError_t launch_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, con
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
                        hipStream_t stream);
 bool gemm_supported(uint32_t type);
+
+// The fp16-MFMA GEMM (k_gemm16.hip), same contract, on the MFMA activation format: qh[m*k]
+// fp16 quantized values, xs[m*k/32] dx, xp[m*k/32] dx*bsum. k % 256 == 0.
+hipError_t launch_gemm16(uint32_t type, const uint8_t* w, int k, int n, int m,
+                         const _Float16* qh, const float* xs, const float* xp, const float* bias,
+                         float* y, hipStream_t stream);
 
 }  // namespace cllm_hip
