@@ -1,8 +1,11 @@
-"""Parity of the int8-MFMA prefill path (matmul_quant_batch with n_rows >= 16) on an MI355X.
+"""Parity of the MFMA prefill path (matmul_quant_batch with n_rows >= 16) on an MI355X, for
+both kernels: int8 MFMA with an fp32 per-block epilogue, and fp16 MFMA as an exact integer
+engine.
 
-Same bars as the GEMV tests: |gpu - ref| <= 1e-4 * max(|ref|, 2^-8 * A) against the
-reference's fp32 output and |gpu - exact| <= 1e-4 * max(|exact|, 2^-10 * A) against the fp64
-evaluation of the same quantized terms (A = sum of absolute per-block terms).
+Same bars as the GEMV tests (check_close in test_gpu_parity.py): |gpu - ref| <=
+1e-4 * max(|ref|, 2^-8 * A) against the reference's fp32 output, and no further from the fp64
+evaluation of the same quantized terms than max(1e-4 * max(|exact|, 2^-10 * A),
+2 * |ref - exact|) (A = sum of absolute per-block terms).
 """
 import numpy as np
 import pytest
@@ -12,6 +15,13 @@ from cllm_inference_amd import synth as S
 from test_gpu_parity import check_close, _dev, TYPES
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(params=["int8", "f16"], autouse=True)
+def gemm_kernel(request, monkeypatch):
+    """Every test runs on both MFMA kernels: int8 (k_gemm.hip) and fp16 (k_gemm16.hip)."""
+    monkeypatch.setenv("CLLM_HIP_GEMM", request.param)
+    return request.param
 
 
 def test_prefill_layer_slices_vs_reference_golden(gpu, orc):
