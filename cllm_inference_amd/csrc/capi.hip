@@ -230,6 +230,24 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
     return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
 }
 
+// Batches of at most this many rows take the fused GEMV (quantization inside the kernel, one
+// launch); larger GEMV batches quantize once into the workspace first, because every fused
+// workgroup re-quantizes all of its rows and that redundant work grows with the row count.
+constexpr int kFusedMaxRows = 2;
+
+bool needs_workspace(uint32_t type, int k, int m) {
+    return use_mfma(type, k, m) || m > kFusedMaxRows;
+}
+
+// GEMV route on fp32 activation rows.
+hipError_t run_gemv_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
+                        const float* bias, float* y, Workspace* ws, hipStream_t stream) {
+    if (m <= kFusedMaxRows) return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream);
+    hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws->qs, ws->sc, ws->bs, stream);
+    if (e != hipSuccess) return e;
+    return launch_gemv(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, stream);
+}
+
 // The per-stream activation workspace of the device entry points, grown to m x k.
 int stream_workspace(DeviceState* st, hipStream_t s, int k, int m, Workspace** out) {
     std::lock_guard<std::mutex> lk(st->mtx);
@@ -256,7 +274,7 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
     if ((rc = resolve_weights(st, w, row_bytes(type, in_dim) * (size_t)out_dim, &wd))) return rc;
     HIP_TRY(st->x.ensure(xb, st->stream));
     HIP_TRY(st->y.ensure(yb, st->stream));
-    if (use_mfma(type, in_dim, n_rows)) HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
+    if (needs_workspace(type, in_dim, n_rows)) HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
     HIP_TRY(hipMemcpyAsync(st->x.p, x, xb, hipMemcpyHostToDevice, st->stream));
     const float* bd = nullptr;
     if (bias) {
@@ -269,8 +287,8 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
         HIP_TRY(run_gemm_f32(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
                              (float*)st->y.p, &st->act, st->stream));
     } else {
-        HIP_TRY(launch_gemv_fused(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
-                                  (float*)st->y.p, st->stream));
+        HIP_TRY(run_gemv_f32(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
+                             (float*)st->y.p, &st->act, st->stream));
     }
     HIP_TRY(hipMemcpyAsync(y, st->y.p, yb, hipMemcpyDeviceToHost, st->stream));
     HIP_TRY(hipStreamSynchronize(st->stream));
@@ -457,13 +475,14 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
     DeviceState* st;
     if ((rc = acquire(&st))) return rc;
     hipStream_t s = (hipStream_t)stream;
+    Workspace* ws = nullptr;
+    if (needs_workspace(type, in_dim, n_rows) && (rc = stream_workspace(st, s, in_dim, n_rows, &ws)))
+        return rc;
     if (!use_mfma(type, in_dim, n_rows)) {
-        // decode-sized batch: one launch that quantizes its activation rows in LDS
-        HIP_TRY(launch_gemv_fused(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, s));
+        // decode-sized batch: one or two rows in a single launch that quantizes them in LDS
+        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws, s));
         return CLLM_HIP_OK;
     }
-    Workspace* ws;
-    if ((rc = stream_workspace(st, s, in_dim, n_rows, &ws))) return rc;
     HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws, s));
     return CLLM_HIP_OK;
 }

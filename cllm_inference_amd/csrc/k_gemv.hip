@@ -24,6 +24,9 @@
 //   acc += (ws * dx) * dot       and, for Q4_K / Q5_K, acc -= wm * (dx * bsum)
 // Lane partial sums are reduced across the wave, so only the fp32 summation order (and the
 // association of the minimum term's product) differs from the reference.
+#include <cstdio>
+#include <cstdlib>
+
 #include "device_utils.h"
 #include "ggml_blocks.h"
 #include "launch.h"
@@ -378,97 +381,164 @@ __host__ __device__ constexpr size_t act_lds_bytes(int mr, int k) {
     return b;
 }
 
+// Carves the LDS block into the staged activation arrays (layout of act_lds_bytes).
 template <uint32_t T, int MR>
-__device__ __forceinline__ ActLds stage_activations(uint8_t* lds, const int8_t* __restrict__ qs,
-                                                    const float* __restrict__ xs,
-                                                    const int32_t* __restrict__ xb, int k,
-                                                    bool copy) {
+__device__ __forceinline__ ActLds act_layout(uint8_t* lds, int k) {
     using Tr = typename TraitsOf<T>::type;
     const int nb = k / 32;
     ActLds a;
     a.k = k;
     a.nb = nb;
     size_t off = 0;
-    int8_t* lqs = (int8_t*)(lds + off);
+    a.qs = (const int8_t*)(lds + off);
     off += align16((size_t)MR * lds_qs_row(k));
-    float* lxd = (float*)(lds + off);
+    a.xd = (const float*)(lds + off);
     off += align16((size_t)MR * nb * 4);
-    float* lxm = (float*)(lds + off);
-    int32_t* lxb = (int32_t*)(lds + off);
+    a.xm = (const float*)(lds + off);
+    a.xb = (const int32_t*)(lds + off);
     if (Tr::NEED_XM || Tr::NEED_XB) off += align16((size_t)MR * nb * 4);
-    int32_t* lhs = (int32_t*)(lds + off);
-    a.qs = lqs;
-    a.xd = lxd;
-    a.xm = lxm;
-    a.xb = lxb;
-    a.hs = lhs;
-    if (!copy) return a;
-
-    const int chunks = MR * k / 16;
-    for (int i = threadIdx.x; i < chunks; i += blockDim.x) {
-        const u32x4 v = ld_u32x4(qs + (size_t)i * 16);
-        const int r = i / (k / 16), c = i - r * (k / 16);
-        *(u32x4*)(lqs + r * lds_qs_row(k) + lds_qs_off(c * 16)) = v;
-        if constexpr (Tr::NEED_HS) {
-            int s = sdot4(v.x, 0x01010101u, 0);
-            s = sdot4(v.y, 0x01010101u, s);
-            s = sdot4(v.z, 0x01010101u, s);
-            s = sdot4(v.w, 0x01010101u, s);
-            lhs[(size_t)r * 2 * nb + (size_t)(c & 1) * nb + (c >> 1)] = s;
-        }
-    }
-    for (int i = threadIdx.x; i < MR * nb; i += blockDim.x) {
-        const float d = xs[i];
-        lxd[i] = d;
-        if constexpr (Tr::NEED_XM) lxm[i] = d * (float)xb[i];
-        if constexpr (Tr::NEED_XB) lxb[i] = xb[i];
-    }
+    a.hs = (const int32_t*)(lds + off);
     return a;
 }
 
-// Fused decode: quantize MR fp32 activation rows straight into the LDS layout above, with
-// exactly the arithmetic of k_quantize_q8_0 (q8_scale / q8_inv_scale / q8_quant4). Eight
-// lanes own a 32-element block; the loop trip count is uniform so every shuffle has all 64
-// lanes, and lanes past the last block work on a clamped block and store nothing.
+// Activation staging runs in two phases around the first weight loads. issue() loads the
+// first kPre slots of this thread into registers before the weight ring is filled, so the
+// in-order vmcnt lets them land without waiting for weight bytes; commit() writes them to LDS
+// after the ring loads are out; any slots beyond kPre per thread (long or many rows) are
+// loaded and written by rest(), after the ring loads. Loads are unconditional with clamped
+// indices (so the compiler counts them exactly); only valid slots are stored.
+constexpr int kPre = 2;
+
+// Copy of an already-quantized Q8_0 batch: slot i < MR*k/16 is 16 qs bytes (plus its
+// 16-element sum for Q6_K); slot j < MR*nb is one block's dx and bsum.
 template <uint32_t T, int MR>
-__device__ __forceinline__ void quantize_activations(const ActLds& a, const float* __restrict__ x) {
+struct StageCopy {
+    using Tr = typename TraitsOf<T>::type;
+    const int8_t* __restrict__ qs;
+    const float* __restrict__ xs;
+    const int32_t* __restrict__ xb;
+    int k;
+    u32x4 q[kPre];
+    float d[kPre];
+    int32_t b[kPre];
+
+    __device__ __forceinline__ int chunks() const { return MR * k / 16; }
+    __device__ __forceinline__ int blocks() const { return MR * (k / 32); }
+
+    __device__ __forceinline__ void load_slot(int i, u32x4& qv, float& dv, int32_t& bv) const {
+        const int ic = min(i, chunks() - 1), jc = min(i, blocks() - 1);
+        qv = ld_u32x4(qs + (size_t)ic * 16);
+        dv = xs[jc];
+        bv = Tr::NEED_XM || Tr::NEED_XB ? xb[jc] : 0;
+    }
+    __device__ __forceinline__ void store_slot(const ActLds& a, int i, const u32x4& v, float dv,
+                                               int32_t bv) const {
+        const int nb = k / 32;
+        if (i < chunks()) {
+            const int r = i / (k / 16), c = i - r * (k / 16);
+            *(u32x4*)(const_cast<int8_t*>(a.qs) + r * lds_qs_row(k) + lds_qs_off(c * 16)) = v;
+            if constexpr (Tr::NEED_HS) {
+                int sm = sdot4(v.x, 0x01010101u, 0);
+                sm = sdot4(v.y, 0x01010101u, sm);
+                sm = sdot4(v.z, 0x01010101u, sm);
+                sm = sdot4(v.w, 0x01010101u, sm);
+                const_cast<int32_t*>(a.hs)[(size_t)r * 2 * nb + (size_t)(c & 1) * nb + (c >> 1)] = sm;
+            }
+        }
+        if (i < blocks()) {
+            const_cast<float*>(a.xd)[i] = dv;
+            if constexpr (Tr::NEED_XM) const_cast<float*>(a.xm)[i] = dv * (float)bv;
+            if constexpr (Tr::NEED_XB) const_cast<int32_t*>(a.xb)[i] = bv;
+        }
+    }
+    __device__ __forceinline__ void issue() {
+#pragma unroll
+        for (int p = 0; p < kPre; ++p) load_slot(threadIdx.x + p * blockDim.x, q[p], d[p], b[p]);
+    }
+    __device__ __forceinline__ void commit(const ActLds& a) const {
+#pragma unroll
+        for (int p = 0; p < kPre; ++p) store_slot(a, threadIdx.x + p * blockDim.x, q[p], d[p], b[p]);
+    }
+    __device__ __forceinline__ void rest(const ActLds& a) const {
+        const int n = max(chunks(), blocks());
+        for (int i = threadIdx.x + kPre * blockDim.x; i < n; i += blockDim.x) {
+            u32x4 qv;
+            float dv;
+            int32_t bv;
+            load_slot(i, qv, dv, bv);
+            store_slot(a, i, qv, dv, bv);
+        }
+    }
+};
+
+// Fused decode: quantize MR fp32 activation rows straight into the LDS layout, with exactly
+// the arithmetic of k_quantize_q8_0 (q8_scale / q8_inv_scale / q8_quant4). Eight lanes own a
+// 32-element block (slot i covers elements 4i .. 4i+3); every loop trip is uniform across the
+// workgroup so each shuffle has all 64 lanes, and lanes past the last block work on a clamped
+// block and store nothing.
+template <uint32_t T, int MR>
+struct StageQuant {
     using Tr = typename TraitsOf<T>::type;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
-    const int nb = a.nb;
-    const int total = MR * nb * 8;
-    int8_t* lqs = const_cast<int8_t*>(a.qs);
-    float* lxd = const_cast<float*>(a.xd);
-    float* lxm = const_cast<float*>(a.xm);
-    int32_t* lxb = const_cast<int32_t*>(a.xb);
-    int32_t* lhs = const_cast<int32_t*>(a.hs);
-    for (int base = 0; base < total; base += blockDim.x) {
-        const int i = base + threadIdx.x;
-        const bool valid = i < total;
-        const int g = (valid ? i : total - 1) >> 3;  // activation block (row-major over rows)
+    const float* __restrict__ x;
+    int k;
+    f32x4 v[kPre];
+
+    __device__ __forceinline__ int slots() const { return MR * (k / 32) * 8; }
+    __device__ __forceinline__ f32x4 load_slot(int i) const {
+        return *(const f32x4*)(x + (size_t)min(i, slots() - 1) * 4);
+    }
+    __device__ __forceinline__ void quant_slot(const ActLds& a, int i, const f32x4& xv) const {
+        const int nb = a.nb;
+        const bool valid = i < slots();
+        const int g = (valid ? i : slots() - 1) >> 3;  // activation block, row-major over rows
         const int part = i & 7;
         const int r = g / nb, b = g - r * nb;
-        const f32x4 v = *(const f32x4*)(x + (size_t)g * 32 + part * 4);
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        float amax = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
         amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
         amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
         amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
         const float d = q8_scale(amax);
         const float id = q8_inv_scale(d);
-        int s;
-        const uint32_t packed = q8_quant4(v.x, v.y, v.z, v.w, id, s);
-        if (valid) *(uint32_t*)(lqs + r * lds_qs_row(a.k) + lds_qs_off(b * 32 + part * 4)) = packed;
-        s += __shfl_xor(s, 1, 8);
-        s += __shfl_xor(s, 2, 8);  // now the sum of this lane's 16-element half
+        int sm;
+        const uint32_t packed = q8_quant4(xv.x, xv.y, xv.z, xv.w, id, sm);
+        if (valid)
+            *(uint32_t*)(const_cast<int8_t*>(a.qs) + r * lds_qs_row(a.k) + lds_qs_off(b * 32 + part * 4)) =
+                packed;
+        sm += __shfl_xor(sm, 1, 8);
+        sm += __shfl_xor(sm, 2, 8);  // now the sum of this lane's 16-element half
         if constexpr (Tr::NEED_HS) {
-            if (valid && (part & 3) == 0) lhs[(size_t)r * 2 * nb + (size_t)(part >> 2) * nb + b] = s;
+            if (valid && (part & 3) == 0)
+                const_cast<int32_t*>(a.hs)[(size_t)r * 2 * nb + (size_t)(part >> 2) * nb + b] = sm;
         }
-        s += __shfl_xor(s, 4, 8);  // the block sum
+        sm += __shfl_xor(sm, 4, 8);  // the block sum
         if (valid && part == 0) {
-            lxd[g] = d;
-            if constexpr (Tr::NEED_XM) lxm[g] = d * (float)s;
-            if constexpr (Tr::NEED_XB) lxb[g] = s;
+            const_cast<float*>(a.xd)[g] = d;
+            if constexpr (Tr::NEED_XM) const_cast<float*>(a.xm)[g] = d * (float)sm;
+            if constexpr (Tr::NEED_XB) const_cast<int32_t*>(a.xb)[g] = sm;
         }
     }
+    __device__ __forceinline__ void issue() {
+#pragma unroll
+        for (int p = 0; p < kPre; ++p) v[p] = load_slot(threadIdx.x + p * blockDim.x);
+    }
+    __device__ __forceinline__ void commit(const ActLds& a) const {
+#pragma unroll
+        for (int p = 0; p < kPre; ++p) quant_slot(a, threadIdx.x + p * blockDim.x, v[p]);
+    }
+    __device__ __forceinline__ void rest(const ActLds& a) const {
+        for (int base = kPre * blockDim.x; base < slots(); base += blockDim.x) {
+            const int i = base + threadIdx.x;
+            quant_slot(a, i, load_slot(i));
+        }
+    }
+};
+
+// Workgroup barrier that orders LDS only: the weight loads still in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Persistent GEMV: wave w owns rows j = w, w + n_waves, ...; items (row, 64-unit slice) are
@@ -500,31 +570,46 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __re
     const int n_items = my_rows * iters;
 
     // Item i of this wave is row wid + (i / iters) * n_waves, unit slice i % iters. Refills are
-    // issued for every slot, with the item and unit clamped to valid memory, so the number of
-    // loads in flight is the same on every path and the compiler's vmcnt waits only ever wait
-    // for the oldest slot.
+    // issued for every slot, with the item, row and unit clamped to valid memory (a wave with
+    // no rows reads row n - 1), so the number of loads in flight is the same on every path
+    // and the compiler's vmcnt waits only ever wait for the oldest slot.
     auto slot_addr = [&](int item, const uint8_t*& row, int& u) {
-        const int c = item < n_items ? item : n_items - 1;
+        const int c = max(0, min(item, n_items - 1));
         const int t = c / iters, it = c - t * iters;
-        row = w + (int64_t)(wid + t * n_waves) * row_bytes;
+        row = w + (int64_t)min(wid + t * n_waves, n - 1) * row_bytes;
         u = min(lane + 64 * it, units - 1);
     };
 
+    // Activation loads go out first, then the weight ring; the activations are written to LDS
+    // once their own loads land (vmcnt counts in issue order), and the barrier orders LDS only,
+    // so no wave waits for weight bytes before the first item's compute.
+    const ActLds a = act_layout<T, MR>(lds, k);
+    StageCopy<T, MR> sc{qs, xs, xb, k, {}, {}, {}};
+    StageQuant<T, MR> sq{x_f32, k, {}};
+    const bool fused = x_f32 != nullptr;
+    if (fused)
+        sq.issue();
+    else
+        sc.issue();
+    __builtin_amdgcn_sched_barrier(0);
+
     typename Tr::Raw ring[P];
-    if (n_items > 0) {
 #pragma unroll
-        for (int p = 0; p < P; ++p) {
-            const uint8_t* row;
-            int u;
-            slot_addr(p, row, u);
-            ring[p] = Tr::load(row, u);
-        }
+    for (int p = 0; p < P; ++p) {
+        const uint8_t* row;
+        int u;
+        slot_addr(p, row, u);
+        ring[p] = Tr::load(row, u);
     }
-    // The activations are staged after the first loads are issued, so HBM is busy at once.
-    // Activations: copied from a Q8_0 batch, or (fused decode, x_f32 != null) quantized here.
-    const ActLds a = stage_activations<T, MR>(lds, qs, xs, xb, k, x_f32 == nullptr);
-    if (x_f32 != nullptr) quantize_activations<T, MR>(a, x_f32);
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (fused) {
+        sq.commit(a);
+        sq.rest(a);
+    } else {
+        sc.commit(a);
+        sc.rest(a);
+    }
+    lds_barrier();
     if (n_items == 0) return;
 
     float acc[MR];
@@ -585,23 +670,48 @@ static int cu_count() {
     return g_cu_count;
 }
 
-// Launch shape, from sweeps on MI355X (Q4_K 14336x4096 and Q6_K 128256x4096, cold HBM):
-// short streams (a few items per wave even at 8 waves per SIMD) run best with no prefetch
-// ring and as many waves as fit; long streams with a 2-deep ring and 2 waves per SIMD.
+// Launch shape, from sweeps on MI355X (Q4_K 14336x4096 and Q6_K 128256x4096, cold HBM).
+// Short streams (at most 4 items per wave at full occupancy): one item in flight per wave and
+// as many waves as fit; issuing a wave's two items at once was slower there (1.75 items per
+// wave: 10.4 us against 9.0 us). Long streams: the 2-deep ring with 4 waves per SIMD.
+// CLLM_HIP_GEMV_SHAPE="<short>,<deep>" overrides the waves per SIMD of the two cases (for
+// tuning sweeps; read once per process).
 struct GemvShape {
     int waves;  // persistent waves in the grid
     bool deep;  // use the 2-deep ring
 };
 
+struct GemvTuning {
+    int short_wps = 8;
+    int deep_wps = 4;
+};
+
+static const GemvTuning& gemv_tuning() {
+    static const GemvTuning t = [] {
+        GemvTuning r;
+        if (const char* e = getenv("CLLM_HIP_GEMV_SHAPE")) {
+            int a = 0, b = 0;
+            if (sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && a <= 16 && b >= 1 && b <= 16) {
+                r.short_wps = a;
+                r.deep_wps = b;
+            }
+        }
+        return r;
+    }();
+    return t;
+}
+
 static GemvShape gemv_shape(int64_t items) {
     const int64_t simds = (int64_t)cu_count() * 4;
+    const GemvTuning& tu = gemv_tuning();
     GemvShape g;
     if (items <= simds * 8 * 4) {
         g.deep = false;
-        g.waves = (int)(items < simds * 8 ? items : simds * 8);
+        const int64_t cap = simds * tu.short_wps;
+        g.waves = (int)(items < cap ? items : cap);
     } else {
         g.deep = true;
-        g.waves = (int)(simds * 2);
+        g.waves = (int)(simds * tu.deep_wps);
     }
     return g;
 }
