@@ -198,19 +198,26 @@ bool use_mfma(uint32_t type, int k, int m) {
     return m >= kMfmaMinRows && k % 256 == 0 && gemm_supported(type);
 }
 
-// The MFMA route runs the int8-MFMA kernel (k_gemm.hip); CLLM_HIP_GEMM=f16 selects the
-// fp16-MFMA kernel (k_gemm16.hip), which has the lower VALU cost per output but not yet the
-// deeper load pipeline it needs to be faster.
-bool int8_gemm_requested() {
+// MFMA kernel choice. Default: the weight-row fp16 kernel (k_gemmw.hip) where it has the
+// type, else the int8 kernel (k_gemm.hip). CLLM_HIP_GEMM=int8 or =f16 forces the int8 kernel
+// or the activation-row fp16 kernel (k_gemm16.hip) for every type (tests run all three).
+enum class GemmKind { W16, I8, F16 };
+
+GemmKind gemm_kind(uint32_t type) {
     const char* e = std::getenv("CLLM_HIP_GEMM");
-    return !(e && std::strcmp(e, "f16") == 0);
+    if (e && std::strcmp(e, "f16") == 0) return GemmKind::F16;
+    if (e && std::strcmp(e, "int8") == 0) return GemmKind::I8;
+    return gemmw_supported(type) ? GemmKind::W16 : GemmKind::I8;
 }
 
-// MFMA route on a Q8_0 batch already in device memory; ws supplies the fp16 staging.
+// MFMA route on a Q8_0 batch already in device memory; ws supplies the fp16 staging of the
+// activation-row fp16 kernel.
 hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                     const float* sc, const int32_t* bs, const float* bias, float* y,
                     Workspace* ws, hipStream_t stream) {
-    if (int8_gemm_requested()) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+    const GemmKind kind = gemm_kind(type);
+    if (kind == GemmKind::W16) return launch_gemmw(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+    if (kind == GemmKind::I8) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
     hipError_t e = launch_q8_to_mfma(qs, sc, bs, (int64_t)m * k / 32, ws->qh, ws->px, stream);
     if (e != hipSuccess) return e;
     return launch_gemm16(type, w, k, n, m, ws->qh, sc, ws->px, bias, y, stream);
@@ -220,14 +227,15 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
 hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                         const float* bias, float* y, Workspace* ws, hipStream_t stream) {
     const int64_t nblk = (int64_t)m * k / 32;
-    if (int8_gemm_requested()) {
-        hipError_t e = launch_quantize_q8_0(x, nblk, ws->qs, ws->sc, ws->bs, stream);
+    const GemmKind kind = gemm_kind(type);
+    if (kind == GemmKind::F16) {
+        hipError_t e = launch_quantize_mfma(x, nblk, ws->sc, ws->qh, ws->px, stream);
         if (e != hipSuccess) return e;
-        return launch_gemm(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, stream);
+        return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
     }
-    hipError_t e = launch_quantize_mfma(x, nblk, ws->sc, ws->qh, ws->px, stream);
+    hipError_t e = launch_quantize_q8_0(x, nblk, ws->qs, ws->sc, ws->bs, stream);
     if (e != hipSuccess) return e;
-    return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
+    return run_gemm(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, ws, stream);
 }
 
 // Batches of at most this many rows take the fused GEMV (quantization inside the kernel, one

@@ -47,4 +47,11 @@ hipError_t launch_gemm16(uint32_t type, const uint8_t* w, int k, int n, int m,
                          const _Float16* qh, const float* xs, const float* xp, const float* bias,
                          float* y, hipStream_t stream);
 
+// The weight-row fp16-MFMA GEMM (k_gemmw.hip) on a Q8_0 batch (same contract as launch_gemm).
+// Q4_K only; k % 256 == 0.
+hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
+                        const float* xs, const int32_t* xb, const float* bias, float* y,
+                        hipStream_t stream);
+bool gemmw_supported(uint32_t type);
+
 }  // namespace cllm_hip

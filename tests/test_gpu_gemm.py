@@ -17,10 +17,15 @@ from test_gpu_parity import check_close, _dev, TYPES
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["int8", "f16"], autouse=True)
+@pytest.fixture(params=["default", "int8", "f16"], autouse=True)
 def gemm_kernel(request, monkeypatch):
-    """Every test runs on both MFMA kernels: int8 (k_gemm.hip) and fp16 (k_gemm16.hip)."""
-    monkeypatch.setenv("CLLM_HIP_GEMM", request.param)
+    """Every test runs on each MFMA kernel choice: the default (weight-row fp16 kernel
+    k_gemmw.hip where it has the type, else int8), int8 (k_gemm.hip) and activation-row fp16
+    (k_gemm16.hip)."""
+    if request.param == "default":
+        monkeypatch.delenv("CLLM_HIP_GEMM", raising=False)
+    else:
+        monkeypatch.setenv("CLLM_HIP_GEMM", request.param)
     return request.param
 
 
