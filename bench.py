@@ -49,8 +49,8 @@ def time_loop(fn, steps, warmup):
 
     The `steps` calls are captured once into a HIP graph on a dedicated stream (after
     `warmup` eager calls on that stream, so every per-stream workspace already exists and
-    nothing allocates during capture); one untimed replay warms it, then exactly one replay
-    is timed with HIP events, bracketed by device synchronisation.
+    nothing allocates during capture); one untimed replay warms it, then three replays are
+    timed with HIP events, each bracketed by device synchronisation, and the median is kept.
     """
     import torch
     s = torch.cuda.Stream()
@@ -65,14 +65,16 @@ def time_loop(fn, steps, warmup):
             fn(i)
     g.replay()
     torch.cuda.synchronize()
-    a, b = _events()
-    a.record()
-    g.replay()
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / steps
+    times = []
+    for _ in range(3):
+        a, b = _events()
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / steps)
     del g
-    return ms
+    return sorted(times)[1]
 
 
 def rotated_weights(w_np, copies):

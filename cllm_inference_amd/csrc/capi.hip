@@ -74,6 +74,7 @@ struct DevBuf {
 // MFMA path's qh[m*k] (fp16) | px[m*k/32] (dx * bsum).
 struct Workspace {
     DevBuf buf;
+    DevBuf part;  // split-K partial sums of the weight-row GEMM
     int8_t* qs = nullptr;
     float* sc = nullptr;
     int32_t* bs = nullptr;
@@ -216,7 +217,15 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
                     const float* sc, const int32_t* bs, const float* bias, float* y,
                     Workspace* ws, hipStream_t stream) {
     const GemmKind kind = gemm_kind(type);
-    if (kind == GemmKind::W16) return launch_gemmw(type, w, k, n, m, qs, sc, bs, bias, y, stream);
+    if (kind == GemmKind::W16) {
+        const size_t pb = gemmw_partial_bytes(type, k, n, m);
+        if (pb) {
+            hipError_t e = ws->part.ensure(pb, stream);
+            if (e != hipSuccess) return e;
+        }
+        return launch_gemmw(type, w, k, n, m, qs, sc, bs, bias, y, (float*)ws->part.p,
+                            pb ? ws->part.cap : 0, stream);
+    }
     if (kind == GemmKind::I8) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
     hipError_t e = launch_q8_to_mfma(qs, sc, bs, (int64_t)m * k / 32, ws->qh, ws->px, stream);
     if (e != hipSuccess) return e;

@@ -140,7 +140,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                                                       const float* __restrict__ xs,
                                                       const int32_t* __restrict__ xb,
                                                       const float* __restrict__ bias,
-                                                      float* __restrict__ y) {
+                                                      float* __restrict__ y, int split_stages) {
     using C = Cfg<W, NT, MT>;
     constexpr int BM = C::BM;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -159,7 +159,12 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     const int nblk = lin / mb_count, mblk = lin - nblk * mb_count;
     const int n0 = nblk * C::BN, m0 = mblk * BM;
     const int nb = k / 32;
-    const int stages = k / kKS;
+    // split-K: blockIdx.y owns stages [s_begin, s_end) and writes a partial sum (no bias) to
+    // slice blockIdx.y of y; a reduction adds the slices and the bias
+    const int s_begin = blockIdx.y * split_stages;
+    const int s_end = min(s_begin + split_stages, k / kKS);
+    const bool partial = gridDim.y > 1;
+    float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
 
     // ---- per-lane load offsets (stage 0); each stage adds a uniform step -----------------
     uint32_t a_off[C::A_SLOTS];     // activation chunk: byte offset into qs
@@ -266,17 +271,17 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 
     {
         Pending pd;
-        issue_stage(0, lds, pd);
+        issue_stage(s_begin, lds, pd);
         wait_vm();
         commit_stage(lds, pd);
     }
     __syncthreads();
 
-    for (int s = 0; s < stages; ++s) {
-        uint8_t* cur = lds + (s & 1) * C::STAGE;
-        uint8_t* nxt = lds + ((s + 1) & 1) * C::STAGE;
+    for (int s = s_begin; s < s_end; ++s) {
+        uint8_t* cur = lds + ((s - s_begin) & 1) * C::STAGE;
+        uint8_t* nxt = lds + ((s - s_begin + 1) & 1) * C::STAGE;
         Pending pd;
-        const bool more = s + 1 < stages;
+        const bool more = s + 1 < s_end;
         if (more) issue_stage(s + 1, nxt, pd);
         const int half = s & 1;
 
@@ -369,7 +374,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 #pragma unroll
                     for (int r = 0; r < 16; ++r) yacc[t][mt][r] = fmaf(-dmr[r], fm[r], yacc[t][mt][r]);
                 }
-                if (half == 1) {
+                if (half == 1 || s + 1 == s_end) {
                     float dr[16];
 #pragma unroll
                     for (int q4 = 0; q4 < 4; ++q4) {
@@ -406,19 +411,371 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                 const int row = n0 + (wave * NT + t) * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (row < n) {
                     float v = yacc[t][mt][r];
-                    if (bias) v += bias[row];
-                    y[(size_t)tok * n + row] = v;
+                    if (bias && !partial) v += bias[row];
+                    out[(size_t)tok * n + row] = v;
                 }
             }
         }
 }
 
-bool gemmw_supported(uint32_t type) { return type == T_Q4_K; }
+// ------------------------------------------------------------------------------------ Q6_K
+// Same scheme for Q6_K (src/core/quant.cpp:630-687): the block b = 4g + i of a super-block is
+// elements 128g + 32i + l; with lane half h taking l = 16h .. 16h+15, its 16 values share the
+// one 16-element scale sc[8g + 2i + h]. The weight operand holds sc * (q - 32) as two exact
+// fp16 parts, 16 sc_hi (q - 32) and sc_lo (q - 32) with sc = 16 sc_hi + sc_lo, so a block costs
+// four MFMAs per token tile and F = sc * I (exact while the partial sums stay below 2^24, else
+// within one fp32 rounding). No minimum term; d is applied once per super-block.
+//
+// A stage is half a super-block (g = stage parity). Q6_K blocks are 2-byte aligned, so the raw
+// bytes come through registers (aligned dword loads, realigned with v_alignbyte) into an LDS
+// row of 112 bytes: ql[64 g .. +64] | qh[32 g .. +32] | the half's 8 scales | d.
+constexpr int kQ6Row = 112;
+constexpr int kQ6Pieces = 7;  // 4 ql chunks, 2 qh chunks, 1 scale / d chunk
+
+template <int W, int MT>
+struct Cfg6 {
+    static constexpr int THREADS = 64 * W;
+    static constexpr int BN = 32 * W;
+    static constexpr int BM = 32 * MT;
+    static constexpr int ACT = BM * 256;
+    static constexpr int DX = 4 * BM * 4;
+    static constexpr int WB = BN * kQ6Row;
+    static constexpr int OFF_DX = ACT;
+    static constexpr int OFF_W = OFF_DX + DX;
+    static constexpr int STAGE = OFF_W + WB;
+    static constexpr int SCRATCH = W * 32 * 4;  // per wave: d[32]
+    static constexpr int LDS = 2 * STAGE + SCRATCH;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(BN % 64 == 0, "a wave loads one raw piece type per slot");
+    static constexpr int A_CHUNKS = BM * 8;
+    static constexpr int A_SLOTS = (A_CHUNKS + THREADS - 1) / THREADS;
+    static constexpr int R_CHUNKS = BN * kQ6Pieces;
+    static constexpr int R_SLOTS = (R_CHUNKS + THREADS - 1) / THREADS;
+    static constexpr int DX_VALS = 4 * BM;
+    static constexpr int DX_SLOTS = (DX_VALS + THREADS - 1) / THREADS;
+};
+
+template <int W, int MT>
+__global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict__ w,
+                                                      uint32_t row_bytes, int k, int n, int m,
+                                                      const int8_t* __restrict__ qs,
+                                                      const float* __restrict__ xs,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ y, int split_stages) {
+    using C = Cfg6<W, MT>;
+    constexpr int BM = C::BM;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5;
+    const int r32 = lane & 31;
+
+    const int mb_count = (m + BM - 1) / BM;
+    const int g = gridDim.x;
+    const int bid = blockIdx.x;
+    const int lin = (g % 8 == 0) ? (bid % 8) * (g / 8) + bid / 8 : bid;
+    const int nblk = lin / mb_count, mblk = lin - nblk * mb_count;
+    const int n0 = nblk * C::BN, m0 = mblk * BM;
+    const int nb = k / 32;
+    const int s_begin = blockIdx.y * split_stages;
+    const int s_end = min(s_begin + split_stages, k / kKS);
+    const bool partial = gridDim.y > 1;
+    float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
+
+    // per-lane offsets for stage 0
+    uint32_t a_off[C::A_SLOTS];
+    int a_dst[C::A_SLOTS];
+#pragma unroll
+    for (int j = 0; j < C::A_SLOTS; ++j) {
+        const int i = tid + j * C::THREADS;
+        const int ic = min(i, C::A_CHUNKS - 1);
+        const int tok = ic >> 3, c8 = ic & 7;
+        a_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)k + 16u * c8;
+        a_dst[j] = i < C::A_CHUNKS ? tok * 256 + 16 * ((2 * c8) ^ (tok & 15)) : -1;
+    }
+    uint32_t r_row[C::R_SLOTS];  // byte offset of the row's first super-block
+#pragma unroll
+    for (int j = 0; j < C::R_SLOTS; ++j) {
+        const int i = min(tid + j * C::THREADS, C::R_CHUNKS - 1);
+        r_row[j] = (uint32_t)min(n0 + i % C::BN, n - 1) * row_bytes;
+    }
+    uint32_t dx_off[C::DX_SLOTS];
+#pragma unroll
+    for (int j = 0; j < C::DX_SLOTS; ++j) {
+        const int i = min(tid + j * C::THREADS, C::DX_VALS - 1);
+        const int b = i / BM, tok = i - b * BM;
+        dx_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)nb + b;
+    }
+
+    struct Pending {
+        wu4 a[C::A_SLOTS];
+        uint32_t r[C::R_SLOTS][6];
+        float dx[C::DX_SLOTS];
+    };
+    auto issue_stage = [&](int s, Pending& pd) {
+        const int sb = s >> 1, gh = s & 1;
+#pragma unroll
+        for (int j = 0; j < C::A_SLOTS; ++j)
+            pd.a[j] = *(const wu4*)(qs + a_off[j] + (uint32_t)s * kKS);
+#pragma unroll
+        for (int j = 0; j < C::R_SLOTS; ++j) {
+            const int i = tid + j * C::THREADS;
+            const int piece = __builtin_amdgcn_readfirstlane(min(i, C::R_CHUNKS - 1) / C::BN);
+            const uint8_t* base = w + r_row[j] + (uint32_t)sb * Q6_K_BYTES;
+            if (piece < 6) {
+                // 16 bytes at p (2-byte aligned): dwords at p - (p & 2) .. + 20, all inside the
+                // super-block (p + 18 <= base + 194)
+                const uint8_t* p = piece < 4 ? base + 64 * gh + 16 * piece
+                                             : base + Q6_K_QH + 32 * gh + 16 * (piece - 4);
+                const uint8_t* pa = p - ((uintptr_t)p & 3u);
+                const u32x4_a4 v = *(const u32x4_a4*)pa;
+                pd.r[j][0] = v.x; pd.r[j][1] = v.y; pd.r[j][2] = v.z; pd.r[j][3] = v.w;
+                pd.r[j][4] = *(const uint32_t*)(pa + 16);
+                pd.r[j][5] = (uint32_t)((uintptr_t)p & 3u);
+            } else {
+                // the 16 scales (bytes 192..207) and d (208..209): dwords from 192 - (p & 2),
+                // the fifth only when the region starts 2 bytes into a dword, d by a u16 load
+                const uint8_t* p = base + Q6_K_SC;
+                const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
+                const uint8_t* pa = p - sh;
+                const u32x4_a4 v = *(const u32x4_a4*)pa;
+                pd.r[j][0] = v.x; pd.r[j][1] = v.y; pd.r[j][2] = v.z; pd.r[j][3] = v.w;
+                pd.r[j][4] = *(const uint32_t*)(sh ? pa + 16 : pa);
+                pd.r[j][5] = sh | ((uint32_t)*(const uint16_t*)(base + Q6_K_D) << 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < C::DX_SLOTS; ++j) pd.dx[j] = xs[dx_off[j] + (uint32_t)s * 4];
+    };
+    auto commit_stage = [&](uint8_t* st, int gh, const Pending& pd) {
+#pragma unroll
+        for (int j = 0; j < C::A_SLOTS; ++j) {
+            if (a_dst[j] >= 0) {
+                *(wu4*)(st + a_dst[j]) = int8x8_to_h8(pd.a[j].x, pd.a[j].y);
+                *(wu4*)(st + (a_dst[j] ^ 16)) = int8x8_to_h8(pd.a[j].z, pd.a[j].w);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < C::R_SLOTS; ++j) {
+            const int i = tid + j * C::THREADS;
+            if (i < C::R_CHUNKS) {
+                const int piece = i / C::BN, row = i - piece * C::BN;
+                const uint32_t sh = pd.r[j][5] & 3u;
+                uint8_t* dst = st + C::OFF_W + row * kQ6Row;
+                wu4 o;
+                o.x = __builtin_amdgcn_alignbyte(pd.r[j][1], pd.r[j][0], sh);
+                o.y = __builtin_amdgcn_alignbyte(pd.r[j][2], pd.r[j][1], sh);
+                o.z = __builtin_amdgcn_alignbyte(pd.r[j][3], pd.r[j][2], sh);
+                o.w = __builtin_amdgcn_alignbyte(pd.r[j][4], pd.r[j][3], sh);
+                if (piece < 6) {
+                    *(wu4*)(dst + 16 * piece) = o;
+                } else {
+                    // the 8 scales of this half, then d
+                    *(u32x2*)(dst + 96) = gh ? u32x2{o.z, o.w} : u32x2{o.x, o.y};
+                    *(uint32_t*)(dst + 104) = pd.r[j][5] >> 16;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < C::DX_SLOTS; ++j) {
+            const int i = tid + j * C::THREADS;
+            if (i < C::DX_VALS) ((float*)(st + C::OFF_DX))[i] = pd.dx[j];
+        }
+    };
+
+    wf16 sacc[MT], yacc[MT];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[a][r] = yacc[a][r] = 0.0f;
+
+    float* scratch = (float*)(lds + 2 * C::STAGE) + wave * 32;
+    const int wrow = wave * 32 + r32;
+
+    {
+        Pending pd;
+        issue_stage(s_begin, pd);
+        commit_stage(lds, s_begin & 1, pd);
+    }
+    __syncthreads();
+
+    for (int s = s_begin; s < s_end; ++s) {
+        uint8_t* cur = lds + ((s - s_begin) & 1) * C::STAGE;
+        uint8_t* nxt = lds + ((s - s_begin + 1) & 1) * C::STAGE;
+        Pending pd;
+        const bool more = s + 1 < s_end;
+        if (more) issue_stage(s + 1, pd);
+        const int gh = s & 1;
+        (void)gh;
+
+        const uint8_t* wr = cur + C::OFF_W + wrow * kQ6Row;
+        const wu4 qh = *(const wu4*)(wr + 64 + 16 * h);
+        const u32x2 scv = *(const u32x2*)(wr + 96);  // the 8 scales of this half
+        const uint8_t* act = cur;
+        const float* dxl = (const float*)(cur + C::OFF_DX);
+
+#pragma unroll 1
+        for (int i = 0; i < 4; ++i) {
+            const wu4 ql = *(const wu4*)(wr + 32 * (i & 1) + 16 * h);
+            const uint32_t lsh = i >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)i;
+            uint32_t q6[4];
+            q6[0] = ((ql.x >> lsh) & 0x0F0F0F0Fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
+            q6[1] = ((ql.y >> lsh) & 0x0F0F0F0Fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
+            q6[2] = ((ql.z >> lsh) & 0x0F0F0F0Fu) | (((qh.z >> hsh) & 0x03030303u) << 4);
+            q6[3] = ((ql.w >> lsh) & 0x0F0F0F0Fu) | (((qh.w >> hsh) & 0x03030303u) << 4);
+            // scale of this lane's 16 values: sc[8 g + 2 i + h], local index 2 i + h
+            const int si = 2 * i + h;
+            const uint32_t scw = si < 4 ? scv.x : scv.y;
+            const int sc = (int)(int8_t)((scw >> (8 * (si & 3))) & 0xFFu);
+            const int s_hi = sc >> 4, s_lo = sc & 15;
+            const wh2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+            const wh2 m1 = {(_Float16)(16 * s_hi), (_Float16)(16 * s_hi)};
+            const wh2 m2 = {(_Float16)s_lo, (_Float16)s_lo};
+            wh8 a1[2], a2[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const wh2 v0 = magic_pair(q6[2 * j], 0) + off, v1 = magic_pair(q6[2 * j], 1) + off;
+                const wh2 v2 = magic_pair(q6[2 * j + 1], 0) + off, v3 = magic_pair(q6[2 * j + 1], 1) + off;
+                const wh2 p0 = v0 * m1, p1 = v1 * m1, p2 = v2 * m1, p3 = v3 * m1;
+                const wh2 q0 = v0 * m2, q1 = v1 * m2, q2 = v2 * m2, q3 = v3 * m2;
+                a1[j] = wh8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+                a2[j] = wh8{q0.x, q0.y, q1.x, q1.y, q2.x, q2.y, q3.x, q3.y};
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int tok = mt * 32 + r32;
+                const wh8 b0 = *(const wh8*)(act + tok * 256 + 16 * ((4 * i + 2 * h) ^ (tok & 15)));
+                const wh8 b1 = *(const wh8*)(act + tok * 256 + 16 * ((4 * i + 2 * h + 1) ^ (tok & 15)));
+                const float dxv = dxl[i * BM + tok];
+                wf16 f = {};
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[0], b0, f, 0, 0, 0);
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[1], b1, f, 0, 0, 0);
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[0], b0, f, 0, 0, 0);
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[1], b1, f, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(dxv, f[r], sacc[mt][r]);
+            }
+        }
+        if (gh == 1 || s + 1 == s_end) {
+            // d of the super-block for the lane's 16 output rows
+            if (h == 0) scratch[r32] = f16_to_f32(*(const uint16_t*)(wr + 104));
+            float dr[16];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 dv = *(const float4*)(scratch + 8 * q4 + 4 * h);
+                dr[4 * q4] = dv.x; dr[4 * q4 + 1] = dv.y; dr[4 * q4 + 2] = dv.z; dr[4 * q4 + 3] = dv.w;
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    yacc[mt][r] = fmaf(dr[r], sacc[mt][r], yacc[mt][r]);
+                    sacc[mt][r] = 0.0f;
+                }
+        }
+        if (more) commit_stage(nxt, (s + 1) & 1, pd);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int tok = m0 + mt * 32 + r32;
+        if (tok >= m) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = n0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row < n) {
+                float v = yacc[mt][r];
+                if (bias && !partial) v += bias[row];
+                out[(size_t)tok * n + row] = v;
+            }
+        }
+    }
+}
+
+// y[i] = sum of the split-K slices (+ bias): total = m * n elements.
+__global__ void k_split_reduce(const float* __restrict__ part, int splits, int64_t total,
+                               const float* __restrict__ bias, int n, float* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    float v = part[i];
+    for (int s = 1; s < splits; ++s) v += part[(int64_t)s * total + i];
+    if (bias) v += bias[i % n];
+    y[i] = v;
+}
+
+bool gemmw_supported(uint32_t type) { return type == T_Q4_K || type == T_Q6_K; }
+
+namespace {
+
+int device_cus() {
+    static int cached = 0;
+    if (cached == 0) {
+        int dev = 0, c = 0;
+        cached = (hipGetDevice(&dev) == hipSuccess &&
+                  hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
+                     ? c
+                     : 256;
+    }
+    return cached;
+}
+
+// Split-K factor: workgroups up to `target`, at least 8 stages per split.
+int choose_splits(int tiles, int stages, int target) {
+    int sp = 1;
+    while (sp < 8 && tiles * sp * 2 <= target && stages / (sp * 2) >= 8) sp *= 2;
+    return sp;
+}
+
+struct Plan {
+    int wv, nt, mt, splits;
+};
+
+Plan plan_for(uint32_t type, int k, int n, int m) {
+    Plan p{};
+    int wv = 0, nt = 0, mt = 0;
+    // CLLM_HIP_GEMMW_CFG="<waves>,<weight tiles per wave>,<token tiles>" and
+    // CLLM_HIP_GEMMW_SPLITS=<n> override the Q4_K tile shape and the split-K factor (sweeps).
+    if (const char* e = getenv("CLLM_HIP_GEMMW_CFG")) {
+        if (sscanf(e, "%d,%d,%d", &wv, &nt, &mt) != 3) wv = nt = mt = 0;
+    }
+    const int cus = device_cus();
+    int target = 2 * cus;  // workgroups to aim for
+    if (type == T_Q6_K) {
+        // 128 weight rows x 64 tokens (4 waves, two workgroups per CU)
+        p.wv = 4, p.nt = 1, p.mt = 2;
+    } else if (wv != 0) {
+        p.wv = wv, p.nt = nt, p.mt = mt;
+    } else {
+        // From sweeps on MI355X at m = 512 (us for n = 14336 / 4096 / 1024): 256 x 128 tiles
+        // when they fill the CUs (163), else 256 x 64 tiles split to one workgroup per CU
+        // (4096: 63 against 70 for 128 x 32), else 128 x 32 tiles split to two per CU (1024: 30).
+        const int t84 = ((n + 255) / 256) * ((m + 127) / 128);
+        const int t82 = ((n + 255) / 256) * ((m + 63) / 64);
+        if (t84 >= cus * 3 / 4) {
+            p.wv = 8, p.nt = 1, p.mt = 4;
+        } else if (t82 >= cus / 4) {
+            p.wv = 8, p.nt = 1, p.mt = 2;
+            target = cus;
+        } else {
+            p.wv = 4, p.nt = 1, p.mt = 1;
+        }
+    }
+    const int bn = 32 * p.nt * p.wv, bm = 32 * p.mt;
+    const int tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
+    p.splits = choose_splits(tiles, k / kKS, target);
+    if (const char* e = getenv("CLLM_HIP_GEMMW_SPLITS")) {
+        const int sp = atoi(e);
+        if (sp >= 1 && sp <= 16 && sp <= k / kKS) p.splits = sp;
+    }
+    return p;
+}
 
 template <int W, int NT, int MT>
-static hipError_t launch_cfg(const uint8_t* w, int k, int n, int m, const int8_t* qs,
-                             const float* xs, const int32_t* xb, const float* bias, float* y,
-                             hipStream_t stream) {
+hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const int8_t* qs, const float* xs,
+                     const int32_t* xb, const float* bias, float* out, int splits,
+                     hipStream_t stream) {
     using C = Cfg<W, NT, MT>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -429,50 +786,73 @@ static hipError_t launch_cfg(const uint8_t* w, int k, int n, int m, const int8_t
     }
     const uint32_t row_bytes = (uint32_t)(k / 256) * Q4_K_BYTES;
     const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
-    hipLaunchKernelGGL((k_gemmw_q4k<W, NT, MT>), dim3((unsigned)tiles), dim3(C::THREADS), C::LDS,
-                       stream, w, row_bytes, k, n, m, qs, xs, xb, bias, y);
+    const int stages = k / kKS, per = (stages + splits - 1) / splits;
+    hipLaunchKernelGGL((k_gemmw_q4k<W, NT, MT>), dim3((unsigned)tiles, (unsigned)splits),
+                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qs, xs, xb, bias,
+                       out, per);
     return hipGetLastError();
+}
+
+template <int W, int MT>
+hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const int8_t* qs, const float* xs,
+                     const float* bias, float* out, int splits, hipStream_t stream) {
+    using C = Cfg6<W, MT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemmw_q6k<W, MT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const uint32_t row_bytes = (uint32_t)(k / 256) * Q6_K_BYTES;
+    const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+    const int stages = k / kKS, per = (stages + splits - 1) / splits;
+    hipLaunchKernelGGL((k_gemmw_q6k<W, MT>), dim3((unsigned)tiles, (unsigned)splits),
+                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qs, xs, bias, out,
+                       per);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m) {
+    if (!gemmw_supported(type) || k % 256 != 0) return 0;
+    const Plan p = plan_for(type, k, n, m);
+    return p.splits > 1 ? (size_t)p.splits * (size_t)m * (size_t)n * sizeof(float) : 0;
 }
 
 hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                         const float* xs, const int32_t* xb, const float* bias, float* y,
-                        hipStream_t stream) {
-    if (type != T_Q4_K || k % 256 != 0) return hipErrorNotSupported;
-    // the kernel indexes with 32-bit offsets
-    if ((uint64_t)n * (uint64_t)(k / 256) * Q4_K_BYTES >= (1ull << 32) ||
-        (uint64_t)m * (uint64_t)k >= (1ull << 32))
-        return hipErrorNotSupported;
-    // Tile shape: CLLM_HIP_GEMMW_CFG="<waves>,<weight tiles per wave>,<token tiles>" (for
-    // sweeps), else by the grid size.
-    int wv = 0, nt = 0, mt = 0;
-    if (const char* e = getenv("CLLM_HIP_GEMMW_CFG")) {
-        if (sscanf(e, "%d,%d,%d", &wv, &nt, &mt) != 3) wv = nt = mt = 0;
-    }
-    if (wv == 0) {
-        // Measured on MI355X at m = 512: 256 x 128 tiles (8 waves) when they fill the CUs
-        // (n = 14336: 163 us), else 128 x 32 tiles (4 waves; n = 4096: 74 us against 137 us).
-        int cus = 256, dev = 0, c = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
-            cus = c;
-        const int big = ((n + 255) / 256) * ((m + 127) / 128);
-        if (big >= cus * 3 / 4) {
-            wv = 8, nt = 1, mt = 4;
-        } else {
-            wv = 4, nt = 1, mt = 1;
-        }
-    }
-#define CLLM_GEMMW_CASE(A, B, D) \
-    if (wv == A && nt == B && mt == D) return launch_cfg<A, B, D>(w, k, n, m, qs, xs, xb, bias, y, stream);
-    CLLM_GEMMW_CASE(8, 1, 4)
-    CLLM_GEMMW_CASE(8, 1, 2)
-    CLLM_GEMMW_CASE(8, 2, 2)
-    CLLM_GEMMW_CASE(4, 2, 4)
-    CLLM_GEMMW_CASE(4, 2, 2)
-    CLLM_GEMMW_CASE(4, 1, 2)
-    CLLM_GEMMW_CASE(4, 1, 1)
+                        float* part, size_t part_bytes, hipStream_t stream) {
+    if (!gemmw_supported(type) || k % 256 != 0) return hipErrorNotSupported;
+    const uint64_t wbytes = (uint64_t)n * (uint64_t)(k / 256) * (type == T_Q6_K ? Q6_K_BYTES : Q4_K_BYTES);
+    if (wbytes >= (1ull << 32) || (uint64_t)m * (uint64_t)k >= (1ull << 32))
+        return hipErrorNotSupported;  // the kernels index with 32-bit offsets
+    Plan p = plan_for(type, k, n, m);
+    if (p.splits > 1 && (part == nullptr || part_bytes < (size_t)p.splits * m * n * sizeof(float)))
+        p.splits = 1;
+    float* out = p.splits > 1 ? part : y;
+    hipError_t e = hipErrorNotSupported;
+    if (type == T_Q6_K) {
+        e = launch_q6<4, 2>(w, k, n, m, qs, xs, bias, out, p.splits, stream);
+    } else {
+#define CLLM_GEMMW_CASE(A, B, D)                                                              \
+        if (p.wv == A && p.nt == B && p.mt == D)                                               \
+            e = launch_q4<A, B, D>(w, k, n, m, qs, xs, xb, bias, out, p.splits, stream);
+        CLLM_GEMMW_CASE(8, 1, 4)
+        CLLM_GEMMW_CASE(8, 1, 2)
+        CLLM_GEMMW_CASE(8, 2, 2)
+        CLLM_GEMMW_CASE(4, 2, 4)
+        CLLM_GEMMW_CASE(4, 2, 2)
+        CLLM_GEMMW_CASE(4, 1, 2)
+        CLLM_GEMMW_CASE(4, 1, 1)
 #undef CLLM_GEMMW_CASE
-    return hipErrorNotSupported;
+    }
+    if (e != hipSuccess || p.splits == 1) return e;
+    const int64_t total = (int64_t)m * n;
+    hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)part, p.splits, total, bias, n, y);
+    return hipGetLastError();
 }
 
 }  // namespace cllm_hip

@@ -48,10 +48,12 @@ hipError_t launch_gemm16(uint32_t type, const uint8_t* w, int k, int n, int m,
                          float* y, hipStream_t stream);
 
 // The weight-row fp16-MFMA GEMM (k_gemmw.hip) on a Q8_0 batch (same contract as launch_gemm).
-// Q4_K only; k % 256 == 0.
+// Q4_K and Q6_K; k % 256 == 0. When its plan splits K, it writes partial sums to part (at least
+// gemmw_partial_bytes(type, k, n, m) bytes, else K is not split) and reduces them into y.
 hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                         const float* xs, const int32_t* xb, const float* bias, float* y,
-                        hipStream_t stream);
+                        float* part, size_t part_bytes, hipStream_t stream);
+size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
 bool gemmw_supported(uint32_t type);
 
 }  // namespace cllm_hip
