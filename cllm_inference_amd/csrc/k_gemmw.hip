@@ -20,7 +20,8 @@
 // are shared by all waves. K advances half a super-block (128 elements) per stage through two
 // LDS buffers, filled one stage ahead: the raw Q4_K bytes of the half (header + 64 quant
 // bytes per row) and dx by direct-to-LDS loads (global_load_lds); the int8 activations
-// through registers, widened to fp16 (16-byte chunks XOR-swizzled by token) on the way in;
+// through registers, widened to fp16 on the way in (token rows padded by 16 bytes, so the
+// 16-byte fragment reads of 16 consecutive tokens fall on distinct banks);
 // dx * bsum likewise, split into bf16 parts.
 #include <cstdio>
 #include <cstdlib>
@@ -43,6 +44,7 @@ constexpr int kKS = 128;        // K elements per stage
 constexpr int kWRow = 80;       // LDS bytes per weight row per stage: header + 64 qs bytes
 constexpr int kWChunks = kWRow / 16;
 constexpr int kXpStride = 48;   // bytes per token: hi[4] mid[4] lo[4] 0[4] bf16 + 16 pad
+constexpr int kActRow = 272;    // LDS bytes per token: 128 fp16 + 16 bytes of padding
 
 template <int W, int NT, int MT>
 struct Cfg {
@@ -50,7 +52,7 @@ struct Cfg {
     static constexpr int BN = 32 * NT * W;
     static constexpr int BM = 32 * MT;
     // LDS layout of one stage
-    static constexpr int ACT = BM * 256;          // [token][16 chunks of 8 fp16], swizzled
+    static constexpr int ACT = BM * kActRow;      // [token][16 chunks of 8 fp16] + padding
     static constexpr int DX = 4 * BM * 4;         // [block][token] fp32
     static constexpr int XP = BM * kXpStride;     // [token][...]
     static constexpr int WB = BN * kWRow;         // [row][80]
@@ -175,7 +177,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
         const int ic = min(i, C::A_CHUNKS - 1);
         const int tok = ic >> 3, c8 = ic & 7;
         a_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)k + 16u * c8;
-        a_dst[j] = i < C::A_CHUNKS ? tok * 256 + 16 * ((2 * c8) ^ (tok & 15)) : -1;
+        a_dst[j] = i < C::A_CHUNKS ? tok * kActRow + 32 * c8 : -1;
     }
     uint32_t w_off[C::W_SLOTS];     // raw weight chunk: byte offset into w
     bool w_q[C::W_SLOTS];           // quant bytes (the offset moves with the stage half)
@@ -235,9 +237,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 #pragma unroll
         for (int j = 0; j < C::A_SLOTS; ++j) {
             if (a_dst[j] >= 0) {
-                // logical chunks 2 c8 and 2 c8 + 1 of the token: swizzled indices differ in bit 0
                 *(wu4*)(st + a_dst[j]) = int8x8_to_h8(pd.a[j].x, pd.a[j].y);
-                *(wu4*)(st + (a_dst[j] ^ 16)) = int8x8_to_h8(pd.a[j].z, pd.a[j].w);
+                *(wu4*)(st + a_dst[j] + 16) = int8x8_to_h8(pd.a[j].z, pd.a[j].w);
             }
         }
 #pragma unroll
@@ -299,6 +300,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 #pragma unroll 1
         for (int pc = 0; pc < 2; ++pc) {
             const int c = 2 * half + pc;
+            // the super-block's first block starts the scaled sums (no reset needed)
+            const bool fresh = c == 0;
             // A fragments: sub-block 2c (low nibbles) and 2c+1 (high nibbles), K steps j = 0, 1
             wh8 afr[NT][2][2];
 #pragma unroll
@@ -322,16 +325,21 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const int tok = mt * 32 + r32;
-                    const wh8 b0 = *(const wh8*)(act + tok * 256 + 16 * ((4 * b + 2 * h) ^ (tok & 15)));
-                    const wh8 b1 = *(const wh8*)(act + tok * 256 + 16 * ((4 * b + 2 * h + 1) ^ (tok & 15)));
+                    const wh8 b0 = *(const wh8*)(act + tok * kActRow + 16 * (4 * b + 2 * h));
+                    const wh8 b1 = *(const wh8*)(act + tok * kActRow + 16 * (4 * b + 2 * h + 1));
                     const float dxv = dxl[b * BM + tok];
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         wf16 f = {};
                         f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][blk][0], b0, f, 0, 0, 0);
                         f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][blk][1], b1, f, 0, 0, 0);
+                        if (blk == 0 && fresh) {
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) sacc[t][mt][r] = fmaf(dxv, f[r], sacc[t][mt][r]);
+                            for (int r = 0; r < 16; ++r) sacc[t][mt][r] = dxv * f[r];
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) sacc[t][mt][r] = fmaf(dxv, f[r], sacc[t][mt][r]);
+                        }
                     }
                 }
             }
@@ -384,10 +392,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            yacc[t][mt][r] = fmaf(dr[r], sacc[t][mt][r], yacc[t][mt][r]);
-                            sacc[t][mt][r] = 0.0f;
-                        }
+                        for (int r = 0; r < 16; ++r) yacc[t][mt][r] = fmaf(dr[r], sacc[t][mt][r], yacc[t][mt][r]);
                 }
             }
         }
@@ -437,7 +442,7 @@ struct Cfg6 {
     static constexpr int THREADS = 64 * W;
     static constexpr int BN = 32 * W;
     static constexpr int BM = 32 * MT;
-    static constexpr int ACT = BM * 256;
+    static constexpr int ACT = BM * kActRow;
     static constexpr int DX = 4 * BM * 4;
     static constexpr int WB = BN * kQ6Row;
     static constexpr int OFF_DX = ACT;
@@ -492,7 +497,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         const int ic = min(i, C::A_CHUNKS - 1);
         const int tok = ic >> 3, c8 = ic & 7;
         a_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)k + 16u * c8;
-        a_dst[j] = i < C::A_CHUNKS ? tok * 256 + 16 * ((2 * c8) ^ (tok & 15)) : -1;
+        a_dst[j] = i < C::A_CHUNKS ? tok * kActRow + 32 * c8 : -1;
     }
     uint32_t r_row[C::R_SLOTS];  // byte offset of the row's first super-block
 #pragma unroll
@@ -553,7 +558,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         for (int j = 0; j < C::A_SLOTS; ++j) {
             if (a_dst[j] >= 0) {
                 *(wu4*)(st + a_dst[j]) = int8x8_to_h8(pd.a[j].x, pd.a[j].y);
-                *(wu4*)(st + (a_dst[j] ^ 16)) = int8x8_to_h8(pd.a[j].z, pd.a[j].w);
+                *(wu4*)(st + a_dst[j] + 16) = int8x8_to_h8(pd.a[j].z, pd.a[j].w);
             }
         }
 #pragma unroll
@@ -607,7 +612,6 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         const bool more = s + 1 < s_end;
         if (more) issue_stage(s + 1, pd);
         const int gh = s & 1;
-        (void)gh;
 
         const uint8_t* wr = cur + C::OFF_W + wrow * kQ6Row;
         const wu4 qh = *(const wu4*)(wr + 64 + 16 * h);
@@ -617,6 +621,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
 
 #pragma unroll 1
         for (int i = 0; i < 4; ++i) {
+            const bool fresh = gh == 0 && i == 0;  // first block of the super-block
             const wu4 ql = *(const wu4*)(wr + 32 * (i & 1) + 16 * h);
             const uint32_t lsh = i >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)i;
             uint32_t q6[4];
@@ -645,16 +650,21 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int tok = mt * 32 + r32;
-                const wh8 b0 = *(const wh8*)(act + tok * 256 + 16 * ((4 * i + 2 * h) ^ (tok & 15)));
-                const wh8 b1 = *(const wh8*)(act + tok * 256 + 16 * ((4 * i + 2 * h + 1) ^ (tok & 15)));
+                const wh8 b0 = *(const wh8*)(act + tok * kActRow + 16 * (4 * i + 2 * h));
+                const wh8 b1 = *(const wh8*)(act + tok * kActRow + 16 * (4 * i + 2 * h + 1));
                 const float dxv = dxl[i * BM + tok];
                 wf16 f = {};
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[0], b0, f, 0, 0, 0);
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[1], b1, f, 0, 0, 0);
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[0], b0, f, 0, 0, 0);
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[1], b1, f, 0, 0, 0);
+                if (fresh) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(dxv, f[r], sacc[mt][r]);
+                    for (int r = 0; r < 16; ++r) sacc[mt][r] = dxv * f[r];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(dxv, f[r], sacc[mt][r]);
+                }
             }
         }
         if (gh == 1 || s + 1 == s_end) {
@@ -669,10 +679,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    yacc[mt][r] = fmaf(dr[r], sacc[mt][r], yacc[mt][r]);
-                    sacc[mt][r] = 0.0f;
-                }
+                for (int r = 0; r < 16; ++r) yacc[mt][r] = fmaf(dr[r], sacc[mt][r], yacc[mt][r]);
         }
         if (more) commit_stage(nxt, (s + 1) & 1, pd);
         __syncthreads();
