@@ -31,6 +31,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5033.0  # 256 CU x 2.4 GHz x 8192 int8 ops / clk / CU (dense)
+FP16_PEAK_TFLOPS = 2516.0  # dense fp16 MFMA, the unit the prefill GEMM computes on
 ROTATE_BYTES = 512 << 20
 
 
@@ -139,6 +140,7 @@ def prefill_layer(C, S, steps, warmup):
         torch.cuda.empty_cache()
     return {"layer_us": round(total_ms * 1e3, 1), "tops": round(total_ops / total_ms / 1e9, 1),
             "frac_int8": round(total_ops / total_ms / 1e9 / INT8_PEAK_TOPS, 4),
+            "frac_fp16_mfma": round(total_ops / total_ms / 1e9 / FP16_PEAK_TFLOPS, 4),
             "tokens_per_s_per_layer": round(512 / (total_ms * 1e-3), 0),
             "llama3_8b_32_layer_projection_tokens_per_s": round(512 / (32 * total_ms * 1e-3), 0),
             "matrices": per}
@@ -179,6 +181,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the M=512 Q4_K_M layer (for counter profiles of the GEMM) and "
+                         "print its figures as one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 device copies of 64 MiB (a kernel of known traffic, for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -202,6 +207,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.prefill_only:
+        layer = prefill_layer(C, S, max(5, args.steps // 20), max(2, args.warmup // 10))
+        print(json.dumps({"c3_prefill_layer_m512": layer}))
+        return
 
     head = decode_point(C, S, "c1_q4_k_gemv", "ffn", 1, args.steps, args.warmup, cold=True)
     extra = {}

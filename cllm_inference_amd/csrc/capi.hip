@@ -194,15 +194,28 @@ int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t*
     return CLLM_HIP_OK;
 }
 
-// The MFMA kernel walks K in 256-element steps.
+bool gemm_forced();
+
+// The MFMA kernels walk K in 256-element steps. Crossover from the GEMV (which streams the
+// weights once per 8 activation rows) measured on MI355X: 16 rows for the types the
+// weight-row kernel has; 64 for the others, whose int8 kernel only overtakes the GEMV there
+// (Q5_K 14336 x 4096: 155 us at 16 rows against ~50 us on the GEMV). A forced kernel choice
+// (CLLM_HIP_GEMM) takes the MFMA route from 16 rows for every type.
 bool use_mfma(uint32_t type, int k, int m) {
-    return m >= kMfmaMinRows && k % 256 == 0 && gemm_supported(type);
+    if (k % 256 != 0 || !gemm_supported(type)) return false;
+    const int min_rows = (gemmw_supported(type) || gemm_forced()) ? kMfmaMinRows : 4 * kMfmaMinRows;
+    return m >= min_rows;
 }
 
 // MFMA kernel choice. Default: the weight-row fp16 kernel (k_gemmw.hip) where it has the
 // type, else the int8 kernel (k_gemm.hip). CLLM_HIP_GEMM=int8 or =f16 forces the int8 kernel
 // or the activation-row fp16 kernel (k_gemm16.hip) for every type (tests run all three).
 enum class GemmKind { W16, I8, F16 };
+
+bool gemm_forced() {
+    const char* e = std::getenv("CLLM_HIP_GEMM");
+    return e && (std::strcmp(e, "f16") == 0 || std::strcmp(e, "int8") == 0);
+}
 
 GemmKind gemm_kind(uint32_t type) {
     const char* e = std::getenv("CLLM_HIP_GEMM");

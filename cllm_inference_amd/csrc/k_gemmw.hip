@@ -701,15 +701,31 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     }
 }
 
-// y[i] = sum of the split-K slices (+ bias): total = m * n elements.
+// y[i] = sum of the split-K slices (+ bias): total = m * n elements, four per thread when
+// n % 4 == 0 (16-byte aligned rows), else one.
 __global__ void k_split_reduce(const float* __restrict__ part, int splits, int64_t total,
                                const float* __restrict__ bias, int n, float* __restrict__ y) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    float v = part[i];
-    for (int s = 1; s < splits; ++s) v += part[(int64_t)s * total + i];
-    if (bias) v += bias[i % n];
-    y[i] = v;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (n % 4 == 0) {
+        const int64_t i = 4 * t;
+        if (i >= total) return;
+        float4 v = *(const float4*)(part + i);
+        for (int s = 1; s < splits; ++s) {
+            const float4 u = *(const float4*)(part + (int64_t)s * total + i);
+            v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+        }
+        if (bias) {
+            const int j = (int)(i % n);
+            v.x += bias[j]; v.y += bias[j + 1]; v.z += bias[j + 2]; v.w += bias[j + 3];
+        }
+        *(float4*)(y + i) = v;
+    } else {
+        if (t >= total) return;
+        float v = part[t];
+        for (int s = 1; s < splits; ++s) v += part[(int64_t)s * total + t];
+        if (bias) v += bias[t % n];
+        y[t] = v;
+    }
 }
 
 bool gemmw_supported(uint32_t type) { return type == T_Q4_K || type == T_Q6_K; }
@@ -857,8 +873,9 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     }
     if (e != hipSuccess || p.splits == 1) return e;
     const int64_t total = (int64_t)m * n;
-    hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
-                       (const float*)part, p.splits, total, bias, n, y);
+    const int64_t threads = n % 4 == 0 ? total / 4 : total;
+    hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       stream, (const float*)part, p.splits, total, bias, n, y);
     return hipGetLastError();
 }
 
