@@ -24,6 +24,8 @@
 //   acc += (ws * dx) * dot       and, for Q4_K / Q5_K, acc -= wm * (dx * bsum)
 // Lane partial sums are reduced across the wave, so only the fp32 summation order (and the
 // association of the minimum term's product) differs from the reference.
+#include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 
@@ -471,65 +473,112 @@ struct StageCopy {
     }
 };
 
-// Fused decode: quantize MR fp32 activation rows straight into the LDS layout, with exactly
-// the arithmetic of k_quantize_q8_0 (q8_scale / q8_inv_scale / q8_quant4). Eight lanes own a
-// 32-element block (slot i covers elements 4i .. 4i+3); every loop trip is uniform across the
-// workgroup so each shuffle has all 64 lanes, and lanes past the last block work on a clamped
-// block and store nothing.
+// Fused decode: quantize MR fp32 activation rows straight into the LDS layout, bit for bit as
+// k_quantize_q8_0. Slot i = lanes 4g + p of the workgroup: elements 8p .. 8p+7 of activation
+// block g (row-major over the rows); the four lanes of a block are one DPP quad.
+//
+// Fast path, for blocks with no inf / NaN and a finite 1/d (every real activation): amax is
+// the largest (bits << 1), which orders finite floats by |x|, so it is the reference's amax;
+// since fl(amax * id) < 127.5 bounds every |fl(x * id)|, rint(v) lies in [-127, 127] and is
+// the low byte of fl(v + 1.5 * 2^23) (the sum lands in [2^23, 2^24), where the ulp is 1 and
+// round-to-nearest-even rounds exactly as rint; the clamp cannot act). The four lanes of a
+// block take the same path. Other blocks run q8_quant4, which reproduces the reference's NaN
+// handling of amax and the x86 INT_MIN conversion of out-of-range values.
 template <uint32_t T, int MR>
 struct StageQuant {
     using Tr = typename TraitsOf<T>::type;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     const float* __restrict__ x;
     int k;
-    f32x4 v[kPre];
+    f32x4 v[2];
 
-    __device__ __forceinline__ int slots() const { return MR * (k / 32) * 8; }
-    __device__ __forceinline__ f32x4 load_slot(int i) const {
-        return *(const f32x4*)(x + (size_t)min(i, slots() - 1) * 4);
+    __device__ __forceinline__ int slots() const { return MR * (k / 8); }
+    __device__ __forceinline__ void load_slot(int i, f32x4 (&r)[2]) const {
+        const f32x4* p = (const f32x4*)(x + (size_t)min(i, slots() - 1) * 8);
+        r[0] = p[0];
+        r[1] = p[1];
     }
-    __device__ __forceinline__ void quant_slot(const ActLds& a, int i, const f32x4& xv) const {
+    // Quantizes slot i (the caller keeps i < slots(); slots() is a multiple of 4, so the quad
+    // of a live lane is live).
+    __device__ __forceinline__ void quant_slot(const ActLds& a, int i, const f32x4 (&r)[2]) const {
         const int nb = a.nb;
-        const bool valid = i < slots();
-        const int g = (valid ? i : slots() - 1) >> 3;  // activation block, row-major over rows
-        const int part = i & 7;
-        const int r = g / nb, b = g - r * nb;
-        float amax = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 8));
-        const float d = q8_scale(amax);
-        const float id = q8_inv_scale(d);
-        int sm;
-        const uint32_t packed = q8_quant4(xv.x, xv.y, xv.z, xv.w, id, sm);
-        if (valid)
-            *(uint32_t*)(const_cast<int8_t*>(a.qs) + r * lds_qs_row(a.k) + lds_qs_off(b * 32 + part * 4)) =
-                packed;
-        sm += __shfl_xor(sm, 1, 8);
-        sm += __shfl_xor(sm, 2, 8);  // now the sum of this lane's 16-element half
+        const int g = i >> 2, part = i & 3;
+        const int row = MR == 1 ? 0 : g / nb, b = g - row * nb;
+        const float e[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
+        uint32_t mb = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mb = max(mb, __builtin_bit_cast(uint32_t, e[j]) << 1);
+        mb = max(mb, (uint32_t)dpp_i32<DPP_QUAD_SWAP1>((int)mb));
+        mb = max(mb, (uint32_t)dpp_i32<DPP_QUAD_SWAP2>((int)mb));
+        float d = 0.0f, id = 0.0f;
+        bool fast = mb < 0xFF000000u;  // no inf or NaN in the block
+        if (fast) {
+            const float amax = __builtin_bit_cast(float, mb >> 1);
+            d = q8_scale(amax);
+            id = q8_inv_scale(d);
+            fast = __fmul_rn(amax, id) < 127.5f;  // false when 1/d overflowed to inf
+        }
+        uint32_t q[2];
+        int s8 = 0;
+        if (fast) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                uint32_t rb[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    rb[t] = __builtin_bit_cast(uint32_t, __fadd_rn(__fmul_rn(e[4 * j + t], id), 12582912.0f));
+                const uint32_t lo = __builtin_amdgcn_perm(rb[1], rb[0], 0x0C0C0400u);
+                const uint32_t hi = __builtin_amdgcn_perm(rb[3], rb[2], 0x0C0C0400u);
+                q[j] = lo | (hi << 16);
+                s8 = sdot4(q[j], 0x01010101u, s8);
+            }
+        } else {
+            float amax = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(e[j]));
+            amax = fmaxf(amax, dpp_f32<DPP_QUAD_SWAP1>(amax));
+            amax = fmaxf(amax, dpp_f32<DPP_QUAD_SWAP2>(amax));
+            d = q8_scale(amax);
+            id = q8_inv_scale(d);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                int sm;
+                q[j] = q8_quant4(e[4 * j], e[4 * j + 1], e[4 * j + 2], e[4 * j + 3], id, sm);
+                s8 += sm;
+            }
+        }
+        *(u32x2*)(const_cast<int8_t*>(a.qs) + row * lds_qs_row(a.k) + lds_qs_off(b * 32 + part * 8)) =
+            u32x2{q[0], q[1]};
+        const int s16 = s8 + dpp_i32<DPP_QUAD_SWAP1>(s8);  // this half block's sum
         if constexpr (Tr::NEED_HS) {
-            if (valid && (part & 3) == 0)
-                const_cast<int32_t*>(a.hs)[(size_t)r * 2 * nb + (size_t)(part >> 2) * nb + b] = sm;
+            if ((part & 1) == 0)
+                const_cast<int32_t*>(a.hs)[(size_t)row * 2 * nb + (size_t)(part >> 1) * nb + b] = s16;
         }
-        sm += __shfl_xor(sm, 4, 8);  // the block sum
-        if (valid && part == 0) {
+        const int bsum = s16 + dpp_i32<DPP_QUAD_SWAP2>(s16);
+        if (part == 0) {
             const_cast<float*>(a.xd)[g] = d;
-            if constexpr (Tr::NEED_XM) const_cast<float*>(a.xm)[g] = d * (float)sm;
-            if constexpr (Tr::NEED_XB) const_cast<int32_t*>(a.xb)[g] = sm;
+            if constexpr (Tr::NEED_XM) const_cast<float*>(a.xm)[g] = d * (float)bsum;
+            if constexpr (Tr::NEED_XB) const_cast<int32_t*>(a.xb)[g] = bsum;
         }
+    }
+    // Waves with no slot load nothing; lanes of a partly used wave load a clamped slot.
+    __device__ __forceinline__ bool wave_live() const {
+        return (int)(threadIdx.x & ~63u) < slots();
     }
     __device__ __forceinline__ void issue() {
-#pragma unroll
-        for (int p = 0; p < kPre; ++p) v[p] = load_slot(threadIdx.x + p * blockDim.x);
+        if (wave_live()) load_slot(threadIdx.x, v);
     }
     __device__ __forceinline__ void commit(const ActLds& a) const {
-#pragma unroll
-        for (int p = 0; p < kPre; ++p) quant_slot(a, threadIdx.x + p * blockDim.x, v[p]);
+        if (wave_live() && (int)threadIdx.x < slots()) quant_slot(a, threadIdx.x, v);
     }
     __device__ __forceinline__ void rest(const ActLds& a) const {
-        for (int base = kPre * blockDim.x; base < slots(); base += blockDim.x) {
+        for (int base = blockDim.x; base < slots(); base += blockDim.x) {
             const int i = base + threadIdx.x;
-            quant_slot(a, i, load_slot(i));
+            if (i < slots()) {
+                f32x4 r[2];
+                load_slot(i, r);
+                quant_slot(a, i, r);
+            }
         }
     }
 };
@@ -543,11 +592,12 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Persistent GEMV: wave w owns rows j = w, w + n_waves, ...; items (row, 64-unit slice) are
 // streamed through a P-deep ring of in-flight weight loads.
-// Workgroup size: 16 waves share one staged (or quantized) activation batch for decode-sized
-// batches; with 4 or 8 activation rows the per-wave registers need the 256-VGPR budget of
-// 4-wave workgroups.
+// Workgroup size: 8 waves share one staged (or quantized) activation batch for decode-sized
+// batches (on MI355X 512 threads beat 1024 and 256 on the Q4_K 14336x4096 and Q6_K
+// 128256x4096 decode shapes); with 4 or 8 activation rows the per-wave registers need the
+// 256-VGPR budget of 4-wave workgroups.
 template <int MR>
-constexpr int gemv_threads() { return MR <= 2 ? 1024 : 256; }
+constexpr int gemv_threads() { return MR <= 2 ? 512 : 256; }
 
 template <uint32_t T, int MR, int P>
 __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __restrict__ w, int64_t row_bytes,
@@ -634,7 +684,10 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __re
 #pragma unroll
                 for (int r = 0; r < MR; ++r) acc[r] = keep ? nacc[r] : acc[r];
             }
-            {
+            // With one slot every wait is vmcnt(0) anyway, so the refill is skipped past the
+            // wave's last item instead of re-reading a clamped row (whose return would hold
+            // the wave, and so the kernel's tail, for one more memory round trip).
+            if (P > 1 || item + P < n_items) {
                 const uint8_t* row;
                 int u2;
                 slot_addr(item + P, row, u2);
@@ -670,17 +723,15 @@ static int cu_count() {
     return g_cu_count;
 }
 
-// Launch shape, from sweeps on MI355X (Q4_K 14336x4096 and Q6_K 128256x4096, cold HBM).
-// Short streams (at most 4 items per wave at full occupancy): one item in flight per wave and
-// as many waves as fit; issuing a wave's two items at once was slower there (1.75 items per
-// wave: 10.4 us against 9.0 us). Long streams: the 2-deep ring with 4 waves per SIMD.
-// CLLM_HIP_GEMV_SHAPE="<short>,<deep>" overrides the waves per SIMD of the two cases (for
-// tuning sweeps; read once per process).
-struct GemvShape {
-    int waves;  // persistent waves in the grid
-    bool deep;  // use the 2-deep ring
-};
-
+// Launch shape, from sweeps on MI355X (cold HBM, fused quantization). With one or two
+// activation rows, one item in flight per wave and as many waves as stay resident beat every
+// deeper ring, on the short stream and on the long one: Q4_K 14336x4096 took 8.0 us against
+// 8.8-10.6 us for 2- and 4-deep rings (rows strided or blocked per wave), the Q6_K
+// 128256x4096 head 81 us against 88-96 us for the 2-deep ring at 4 waves per SIMD. More
+// loads in flight per wave lost even when every extra load was useful. With 4 or 8 rows,
+// streams longer than 32 items per SIMD use the 2-deep ring at 4 waves per SIMD.
+// CLLM_HIP_GEMV_SHAPE="<one-deep>,<two-deep>" caps the waves per SIMD of the two rings (for
+// tuning sweeps; read once per process). The grid never exceeds the waves resident at once.
 struct GemvTuning {
     int short_wps = 8;
     int deep_wps = 4;
@@ -701,19 +752,24 @@ static const GemvTuning& gemv_tuning() {
     return t;
 }
 
-static GemvShape gemv_shape(int64_t items) {
-    const int64_t simds = (int64_t)cu_count() * 4;
-    const GemvTuning& tu = gemv_tuning();
-    GemvShape g;
-    if (items <= simds * 8 * 4) {
-        g.deep = false;
-        const int64_t cap = simds * tu.short_wps;
-        g.waves = (int)(items < cap ? items : cap);
+// Waves of k_gemv<T, MR, P> resident on the whole device with `shmem` bytes of LDS per
+// workgroup (cached per instantiation for the last LDS size asked).
+template <uint32_t T, int MR, int P>
+static int64_t resident_waves(size_t shmem) {
+    static std::atomic<uint64_t> cache{0};  // (shmem << 16) | workgroups per CU, 0 = empty
+    uint64_t c = cache.load(std::memory_order_relaxed);
+    int blocks;
+    if (c != 0 && (c >> 16) == shmem) {
+        blocks = (int)(c & 0xFFFFu);
     } else {
-        g.deep = true;
-        g.waves = (int)(simds * tu.deep_wps);
+        blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv<T, MR, P>),
+                                                         gemv_threads<MR>(), shmem) != hipSuccess ||
+            blocks < 1)
+            blocks = 1;
+        cache.store(((uint64_t)shmem << 16) | (uint64_t)(blocks & 0xFFFF), std::memory_order_relaxed);
     }
-    return g;
+    return (int64_t)blocks * (gemv_threads<MR>() / 64) * cu_count();
 }
 
 template <uint32_t T, int MR, int P>
@@ -745,9 +801,16 @@ static hipError_t launch_mr(const uint8_t* w, int k, int n, const int8_t* qs, co
                             hipStream_t stream) {
     using Tr = typename TraitsOf<T>::type;
     const int iters = (k / Tr::UNIT + 63) / 64;
-    const GemvShape g = gemv_shape((int64_t)n * iters);
-    if (g.deep) return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, g.waves, stream);
-    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, g.waves, stream);
+    const int64_t items = (int64_t)n * iters;
+    const int64_t simds = (int64_t)cu_count() * 4;
+    const GemvTuning& tu = gemv_tuning();
+    const size_t shmem = act_lds_bytes<T>(MR, k);
+    if (MR > 2 && items > simds * 32) {
+        const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2>(shmem));
+        return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, (int)waves, stream);
+    }
+    const int64_t waves = std::min({items, simds * tu.short_wps, resident_waves<T, MR, 1>(shmem)});
+    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, (int)waves, stream);
 }
 
 template <uint32_t T>
