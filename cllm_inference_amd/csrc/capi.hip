@@ -71,7 +71,7 @@ struct DevBuf {
 };
 
 // Activation workspace: the Q8_0 batch qs[m*k] | scales[m*k/32] | bsums[m*k/32], and the
-// MFMA path's qh[m*k] (fp16) | px[m*k/32] (dx * bsum).
+// MFMA paths' qh[m*k] (fp16) | px[m*k/32] (dx * bsum) | xq[m*k/8] (dx * bsum as bf16 parts).
 struct Workspace {
     DevBuf buf;
     DevBuf part;  // split-K partial sums of the weight-row GEMM
@@ -80,12 +80,14 @@ struct Workspace {
     int32_t* bs = nullptr;
     _Float16* qh = nullptr;
     float* px = nullptr;
+    uint16_t* xq = nullptr;
     hipError_t ensure(int k, int m, hipStream_t stream) {
         const size_t n = (size_t)k * (size_t)m;
         const size_t qs_bytes = (n + 255) & ~(size_t)255;
         const size_t sc_bytes = ((n / 32) * 4 + 255) & ~(size_t)255;
         const size_t qh_bytes = (2 * n + 255) & ~(size_t)255;
-        hipError_t e = buf.ensure(qs_bytes + 3 * sc_bytes + qh_bytes, stream);
+        const size_t xq_bytes = (n / 4 + 255) & ~(size_t)255;
+        hipError_t e = buf.ensure(qs_bytes + 3 * sc_bytes + qh_bytes + xq_bytes, stream);
         if (e != hipSuccess) return e;
         char* p = (char*)buf.p;
         qs = (int8_t*)p;
@@ -93,6 +95,7 @@ struct Workspace {
         bs = (int32_t*)(p + qs_bytes + sc_bytes);
         px = (float*)(p + qs_bytes + 2 * sc_bytes);
         qh = (_Float16*)(p + qs_bytes + 3 * sc_bytes);
+        xq = (uint16_t*)(p + qs_bytes + 3 * sc_bytes + qh_bytes);
         return hipSuccess;
     }
 };
@@ -236,7 +239,11 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
             hipError_t e = ws->part.ensure(pb, stream);
             if (e != hipSuccess) return e;
         }
-        return launch_gemmw(type, w, k, n, m, qs, sc, bs, bias, y, (float*)ws->part.p,
+        if (type == T_Q4_K) {
+            hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws->qh, ws->xq, stream);
+            if (e != hipSuccess) return e;
+        }
+        return launch_gemmw(type, w, k, n, m, qs, sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,
                             pb ? ws->part.cap : 0, stream);
     }
     if (kind == GemmKind::I8) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
@@ -254,6 +261,17 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
         hipError_t e = launch_quantize_mfma(x, nblk, ws->sc, ws->qh, ws->px, stream);
         if (e != hipSuccess) return e;
         return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
+    }
+    if (kind == GemmKind::W16 && type == T_Q4_K) {
+        hipError_t e = launch_quantize_w(x, nblk, ws->sc, ws->qh, ws->xq, stream);
+        if (e != hipSuccess) return e;
+        const size_t pb = gemmw_partial_bytes(type, k, n, m);
+        if (pb) {
+            e = ws->part.ensure(pb, stream);
+            if (e != hipSuccess) return e;
+        }
+        return launch_gemmw(type, w, k, n, m, nullptr, ws->sc, ws->qh, ws->xq, bias, y,
+                            (float*)ws->part.p, pb ? ws->part.cap : 0, stream);
     }
     hipError_t e = launch_quantize_q8_0(x, nblk, ws->qs, ws->sc, ws->bs, stream);
     if (e != hipSuccess) return e;

@@ -105,6 +105,28 @@ __device__ __forceinline__ float q8_inv_scale(float d) {
     return (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
 }
 
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_val(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+
+// dx * bsum of one Q8_0 block as three bf16 parts hi + mid + lo (24 significant bits: the
+// fp32 value exactly), the token operand of the K-quant minimum term on bf16 MFMA. Stored in
+// a super-block record of 32 bf16: hi at j, mid at 8 + j, lo at 16 + j and 0 at 24 + j for the
+// record's block j.
+__device__ __forceinline__ void xq_store(uint16_t* rec, int j, float pv) {
+    const uint32_t hi = bf16_bits(pv);
+    const float r1 = pv - bf16_val(hi);
+    const uint32_t mid = bf16_bits(r1);
+    const uint32_t lo = bf16_bits(r1 - bf16_val(mid));
+    rec[j] = (uint16_t)hi;
+    rec[8 + j] = (uint16_t)mid;
+    rec[16 + j] = (uint16_t)lo;
+    rec[24 + j] = 0;
+}
+
 // Cross-lane moves inside a row of 16 lanes (DPP; no LDS traffic).
 template <int CTRL>
 __device__ __forceinline__ int dpp_i32(int v) {

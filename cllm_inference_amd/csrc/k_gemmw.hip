@@ -43,35 +43,41 @@ typedef uint32_t wu4 __attribute__((ext_vector_type(4)));
 constexpr int kKS = 128;        // K elements per stage
 constexpr int kWRow = 80;       // LDS bytes per weight row per stage: header + 64 qs bytes
 constexpr int kWChunks = kWRow / 16;
-constexpr int kXpStride = 48;   // bytes per token: hi[4] mid[4] lo[4] 0[4] bf16 + 16 pad
-constexpr int kActRow = 272;    // LDS bytes per token: 128 fp16 + 16 bytes of padding
+constexpr int kActRow = 272;    // Q6_K kernel: LDS bytes per token, 128 fp16 + 16 of padding
+constexpr int kXqRow = 64;      // bytes per token and super-block of the minimum operand
 
+// Q4_K kernel. Every operand reaches LDS by direct-to-LDS loads (no register staging):
+//   ACT  [token][16 chunks of 8 fp16], chunk c of token t stored at slot c ^ (t & 15), so the
+//        16-byte fragment reads of 16 consecutive tokens fall on distinct banks;
+//   DX   [block][token] fp32;
+//   XQ   [token][hi 8 | mid 8 | lo 8 | 0 8] bf16 for the super-block (stages of half 1 only);
+//   W    [row][80] raw Q4_K bytes: 16-byte header, then the half super-block's 64 quant bytes.
 template <int W, int NT, int MT>
 struct Cfg {
     static constexpr int THREADS = 64 * W;
     static constexpr int BN = 32 * NT * W;
     static constexpr int BM = 32 * MT;
-    // LDS layout of one stage
-    static constexpr int ACT = BM * kActRow;      // [token][16 chunks of 8 fp16] + padding
-    static constexpr int DX = 4 * BM * 4;         // [block][token] fp32
-    static constexpr int XP = BM * kXpStride;     // [token][...]
-    static constexpr int WB = BN * kWRow;         // [row][80]
+    static constexpr int ACT = BM * 256;
+    static constexpr int DX = 4 * BM * 4;
+    static constexpr int XQ = BM * kXqRow;
+    static constexpr int WB = BN * kWRow;
     static constexpr int OFF_DX = ACT;
-    static constexpr int OFF_XP = OFF_DX + DX;
-    static constexpr int OFF_W = OFF_XP + XP;
+    static constexpr int OFF_XQ = OFF_DX + DX;
+    static constexpr int OFF_W = OFF_XQ + XQ;
     static constexpr int STAGE = OFF_W + WB;
     static constexpr int SCRATCH = W * NT * 64 * 4;  // per wave and tile: d[32], dmin[32]
     static constexpr int LDS = 2 * STAGE + SCRATCH;
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    // loader work per stage
-    static constexpr int A_CHUNKS = BM * 8;       // 16-byte int8 chunks of activations
-    static constexpr int A_SLOTS = (A_CHUNKS + THREADS - 1) / THREADS;
-    static constexpr int W_LOADS = BN * kWChunks / 64;   // wave-loads of raw weights
+    // wave-loads (64 lanes x 16 or 4 bytes) per stage, spread over the W waves
+    static constexpr int A_LOADS = ACT / 1024;
+    static constexpr int A_SLOTS = (A_LOADS + W - 1) / W;
+    static constexpr int W_LOADS = WB / 1024;
+    static_assert(WB % 1024 == 0, "whole wave-loads of weight chunks");
     static constexpr int W_SLOTS = (W_LOADS + W - 1) / W;
-    static constexpr int DX_LOADS = 4 * BM / 64;          // wave-loads of dx
+    static constexpr int DX_LOADS = DX / 256;
     static constexpr int DX_SLOTS = (DX_LOADS + W - 1) / W;
-    static constexpr int P_VALS = 4 * BM;                 // dx * bsum values
-    static constexpr int P_SLOTS = (P_VALS + THREADS - 1) / THREADS;
+    static constexpr int XQ_LOADS = XQ / 1024;
+    static constexpr int XQ_SLOTS = (XQ_LOADS + W - 1) / W;
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -86,12 +92,15 @@ __device__ __forceinline__ void lds_load4(const void* g, uint8_t* lds_base) {
 // Waits for this wave's outstanding vector-memory loads (including direct-to-LDS ones).
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// fp32 -> bf16 bits, round to nearest even (finite inputs).
-__device__ __forceinline__ uint32_t bf16_bits(float f) {
-    const uint32_t u = __builtin_bit_cast(uint32_t, f);
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+// Returns v unchanged, but opaque to the optimizer: arithmetic on a value loaded for the next
+// stage cannot be hoisted to where its load is issued, which would make the wave wait there
+// for all of that stage's loads instead of after the current stage's MFMA work.
+template <typename T>
+__device__ __forceinline__ T pinned(T v) {
+    asm volatile("" : "+v"(v));
+    return v;
 }
-__device__ __forceinline__ float bf16_val(uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+
 
 // fp16 pairs (1024 + b0, 1024 + b1) from bytes 0,1 (pair 0) or 2,3 (pair 1) of x.
 __device__ __forceinline__ wh2 magic_pair(uint32_t x, int pair) {
@@ -138,17 +147,16 @@ __device__ __forceinline__ void k4_sm(int j, uint32_t s0, uint32_t s1, uint32_t 
 template <int W, int NT, int MT>
 __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict__ w,
                                                       uint32_t row_bytes, int k, int n, int m,
-                                                      const int8_t* __restrict__ qs,
+                                                      const _Float16* __restrict__ qh,
                                                       const float* __restrict__ xs,
-                                                      const int32_t* __restrict__ xb,
+                                                      const uint16_t* __restrict__ xq,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int split_stages) {
     using C = Cfg<W, NT, MT>;
     constexpr int BM = C::BM;
     extern __shared__ __align__(16) uint8_t lds[];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = lane >> 5;
     const int r32 = lane & 31;
 
@@ -168,94 +176,73 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     const bool partial = gridDim.y > 1;
     float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
 
-    // ---- per-lane load offsets (stage 0); each stage adds a uniform step -----------------
-    uint32_t a_off[C::A_SLOTS];     // activation chunk: byte offset into qs
-    int a_dst[C::A_SLOTS];          // LDS byte offset of its low fp16 chunk (-1: none)
+    // ---- per-lane source offsets of this wave's load slots (stage 0; stages add a step) ----
+    // Rows and tokens past the matrix are clamped to the last one (their results are dropped).
+    uint32_t a_off[C::A_SLOTS];   // bytes into qh: token, swizzled 16-byte chunk
 #pragma unroll
     for (int j = 0; j < C::A_SLOTS; ++j) {
-        const int i = tid + j * C::THREADS;
-        const int ic = min(i, C::A_CHUNKS - 1);
-        const int tok = ic >> 3, c8 = ic & 7;
-        a_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)k + 16u * c8;
-        a_dst[j] = i < C::A_CHUNKS ? tok * kActRow + 32 * c8 : -1;
+        const int L = min(wave + j * W, C::A_LOADS - 1);
+        const int t = 4 * L + (lane >> 4);                 // 4 tokens per wave-load
+        const int c = (lane & 15) ^ (t & 15);              // chunk stored at slot lane & 15
+        a_off[j] = ((uint32_t)min(m0 + t, m - 1) * (uint32_t)k + 8u * (uint32_t)c) * 2u;
     }
-    uint32_t w_off[C::W_SLOTS];     // raw weight chunk: byte offset into w
-    bool w_q[C::W_SLOTS];           // quant bytes (the offset moves with the stage half)
+    uint32_t w_off[C::W_SLOTS];   // bytes into w
+    bool w_q[C::W_SLOTS];         // quant bytes (the offset moves with the stage half)
 #pragma unroll
     for (int j = 0; j < C::W_SLOTS; ++j) {
-        const int p = min((wave * C::W_SLOTS + j) * 64 + lane, C::W_LOADS * 64 - 1);
+        const int L = min(wave + j * W, C::W_LOADS - 1);
+        const int p = L * 64 + lane;
         const int row = p / kWChunks, piece = p - row * kWChunks;
         w_off[j] = (uint32_t)min(n0 + row, n - 1) * row_bytes +
                    (piece == 0 ? 0u : (uint32_t)(Q4_K_QS + 16 * (piece - 1)));
         w_q[j] = piece != 0;
     }
-    uint32_t dx_off[C::DX_SLOTS];   // dx: [block][token], wave-load wave + j W
+    uint32_t dx_off[C::DX_SLOTS];  // elements into xs: [block][token] in LDS
 #pragma unroll
     for (int j = 0; j < C::DX_SLOTS; ++j) {
         const int p = min(wave + j * W, C::DX_LOADS - 1) * 64 + lane;
         const int b = p / BM, tok = p - b * BM;
         dx_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)nb + b;
     }
-    uint32_t p_off[C::P_SLOTS];     // dx * bsum value: element offset into xs / xb
+    uint32_t q_off[C::XQ_SLOTS];   // bytes into xq: 16 tokens x 64 bytes per wave-load
 #pragma unroll
-    for (int j = 0; j < C::P_SLOTS; ++j) {
-        const int i = min(tid + j * C::THREADS, C::P_VALS - 1);
-        const int tok = i >> 2, b = i & 3;
-        p_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)nb + b;
+    for (int j = 0; j < C::XQ_SLOTS; ++j) {
+        const int L = min(wave + j * W, C::XQ_LOADS - 1);
+        const int t = 16 * L + (lane >> 2);
+        q_off[j] = (uint32_t)min(m0 + t, m - 1) * (uint32_t)(k / 256) * (uint32_t)kXqRow + 16u * (lane & 3);
     }
 
-    struct Pending {
-        wu4 a[C::A_SLOTS];
-        float d[C::P_SLOTS];
-        int32_t bs[C::P_SLOTS];
+    // A stage's direct-to-LDS loads: the activations, then weights, dx and (for the second half
+    // of a super-block) the minimum operand.
+    auto issue_act = [&](int s, uint8_t* st) {
+#pragma unroll
+        for (int j = 0; j < C::A_SLOTS; ++j) {
+            const int L = wave + j * W;
+            if (C::A_LOADS % W == 0 || L < C::A_LOADS)
+                lds_load16((const uint8_t*)qh + a_off[j] + (uint32_t)s * (2u * kKS), st + L * 1024);
+        }
     };
-    auto issue_stage = [&](int s, uint8_t* st, Pending& pd) {
+    auto issue_rest = [&](int s, uint8_t* st) {
         const int sb = s >> 1, half = s & 1;
 #pragma unroll
-        for (int j = 0; j < C::A_SLOTS; ++j)
-            pd.a[j] = *(const wu4*)(qs + a_off[j] + (uint32_t)s * kKS);
-#pragma unroll
         for (int j = 0; j < C::W_SLOTS; ++j) {
-            const int slot = wave * C::W_SLOTS + j;
-            if (C::W_LOADS % W == 0 || slot < C::W_LOADS)
+            const int L = wave + j * W;
+            if (C::W_LOADS % W == 0 || L < C::W_LOADS)
                 lds_load16(w + w_off[j] + (uint32_t)sb * Q4_K_BYTES + (w_q[j] ? 64u * half : 0u),
-                           st + C::OFF_W + slot * 1024);
+                           st + C::OFF_W + L * 1024);
         }
 #pragma unroll
         for (int j = 0; j < C::DX_SLOTS; ++j) {
-            const int wl = wave + j * W;
-            if (C::DX_LOADS % W == 0 || wl < C::DX_LOADS)
-                lds_load4(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + wl * 256);
+            const int L = wave + j * W;
+            if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
+                lds_load4(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + L * 256);
         }
+        if (half == 1) {
 #pragma unroll
-        for (int j = 0; j < C::P_SLOTS; ++j) {
-            pd.d[j] = xs[p_off[j] + (uint32_t)s * 4];
-            pd.bs[j] = xb[p_off[j] + (uint32_t)s * 4];
-        }
-    };
-    auto commit_stage = [&](uint8_t* st, const Pending& pd) {
-#pragma unroll
-        for (int j = 0; j < C::A_SLOTS; ++j) {
-            if (a_dst[j] >= 0) {
-                *(wu4*)(st + a_dst[j]) = int8x8_to_h8(pd.a[j].x, pd.a[j].y);
-                *(wu4*)(st + a_dst[j] + 16) = int8x8_to_h8(pd.a[j].z, pd.a[j].w);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < C::P_SLOTS; ++j) {
-            const int i = tid + j * C::THREADS;
-            if (i < C::P_VALS) {
-                const int tok = i >> 2, b = i & 3;
-                const float pv = pd.d[j] * (float)pd.bs[j];
-                const uint32_t hi = bf16_bits(pv);
-                const float r1 = pv - bf16_val(hi);
-                const uint32_t mid = bf16_bits(r1);
-                const uint32_t lo = bf16_bits(r1 - bf16_val(mid));
-                uint16_t* p = (uint16_t*)(st + C::OFF_XP + tok * kXpStride);
-                p[b] = (uint16_t)hi;
-                p[4 + b] = (uint16_t)mid;
-                p[8 + b] = (uint16_t)lo;
-                p[12 + b] = 0;
+            for (int j = 0; j < C::XQ_SLOTS; ++j) {
+                const int L = wave + j * W;
+                if (C::XQ_LOADS % W == 0 || L < C::XQ_LOADS)
+                    lds_load16((const uint8_t*)xq + q_off[j] + (uint32_t)sb * kXqRow, st + C::OFF_XQ + L * 1024);
             }
         }
     };
@@ -270,38 +257,41 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 
     float* scratch = (float*)(lds + 2 * C::STAGE) + wave * NT * 64;
 
-    {
-        Pending pd;
-        issue_stage(s_begin, lds, pd);
-        wait_vm();
-        commit_stage(lds, pd);
-    }
-    __syncthreads();
+    // One stage: half HALF = s & 1 of a super-block. The host keeps every split's stage range
+    // even and super-block aligned, so stage s sits in LDS buffer HALF; the scaled sums are
+    // folded into the output sums (times d) and cleared at the end of each super-block.
+    auto run_stage = [&](int s) {
+        const int HALF = s & 1;
+        uint8_t* cur = lds + HALF * C::STAGE;
+        uint8_t* nxt = lds + (1 - HALF) * C::STAGE;
 
-    for (int s = s_begin; s < s_end; ++s) {
-        uint8_t* cur = lds + ((s - s_begin) & 1) * C::STAGE;
-        uint8_t* nxt = lds + ((s - s_begin + 1) & 1) * C::STAGE;
-        Pending pd;
-        const bool more = s + 1 < s_end;
-        if (more) issue_stage(s + 1, nxt, pd);
-        const int half = s & 1;
-
-        // this lane's weight rows: row r32 of each of the wave's NT tiles
+        // this lane's weight rows: row r32 of each of the wave's NT tiles. The rows' d and dmin
+        // go to this wave's scratch before the next stage's direct-to-LDS loads are issued: an
+        // LDS store while those are in flight would make the compiler wait for all of them.
         const uint8_t* wr[NT];
         wu4 hdr[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             wr[t] = cur + C::OFF_W + ((wave * NT + t) * 32 + r32) * kWRow;
             hdr[t] = *(const wu4*)wr[t];
+            if (h == 0 && HALF == 1) {
+                float* sc_t = scratch + t * 64;
+                sc_t[r32] = f16_to_f32(hdr[t].x & 0xFFFFu);
+                sc_t[32 + r32] = f16_to_f32(hdr[t].x >> 16);
+            }
         }
+        const bool more = s + 1 < s_end;
+        if (more) {
+            issue_act(s + 1, nxt);
+            issue_rest(s + 1, nxt);
+        }
+
         const uint8_t* act = cur;
         const float* dxl = (const float*)(cur + C::OFF_DX);
 
-#pragma unroll 1
-        for (int pc = 0; pc < 2; ++pc) {
-            const int c = 2 * half + pc;
-            // the super-block's first block starts the scaled sums (no reset needed)
-            const bool fresh = c == 0;
+        // blocks 2 pc and 2 pc + 1 of the stage (sub-blocks 2c and 2c + 1, c = 2 HALF + pc)
+        auto blocks = [&](int pc) {
+            const int c = 2 * HALF + pc;
             // A fragments: sub-block 2c (low nibbles) and 2c+1 (high nibbles), K steps j = 0, 1
             wh8 afr[NT][2][2];
 #pragma unroll
@@ -325,83 +315,86 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const int tok = mt * 32 + r32;
-                    const wh8 b0 = *(const wh8*)(act + tok * kActRow + 16 * (4 * b + 2 * h));
-                    const wh8 b1 = *(const wh8*)(act + tok * kActRow + 16 * (4 * b + 2 * h + 1));
+                    const uint8_t* arow = act + tok * 256;
+                    const int sw = tok & 15;
+                    const wh8 b0 = *(const wh8*)(arow + (((4 * b + 2 * h) ^ sw) << 4));
+                    const wh8 b1 = *(const wh8*)(arow + (((4 * b + 2 * h + 1) ^ sw) << 4));
                     const float dxv = dxl[b * BM + tok];
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         wf16 f = {};
                         f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][blk][0], b0, f, 0, 0, 0);
                         f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][blk][1], b1, f, 0, 0, 0);
-                        if (blk == 0 && fresh) {
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) sacc[t][mt][r] = dxv * f[r];
-                        } else {
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) sacc[t][mt][r] = fmaf(dxv, f[r], sacc[t][mt][r]);
-                        }
+                        for (int r = 0; r < 16; ++r) sacc[t][mt][r] = fmaf(dxv, f[r], sacc[t][mt][r]);
                     }
                 }
             }
-        }
+        };
+#pragma unroll 1
+        for (int pc = 0; pc < 2; ++pc) blocks(pc);
 
-        // minimum term of this half: minima of sub-blocks 4 half .. 4 half + 3; d at the end
-        // of the super-block
-        {
-            const uint8_t* xpl = cur + C::OFF_XP;
-            wbf8 xbv[MT];
+        // The next stage's loads have landed before the scratch is read (an LDS read while
+        // direct-to-LDS loads are in flight waits for all of them anyway).
+        if (more) wait_vm();
+
+        // End of the super-block: the minimum term of its 8 sub-blocks, then d.
+        //   fm = sum_b mn_b * (hi_b + mid_b + lo_b) as two bf16 MFMAs: the weight operand holds
+        //   the 8 minima in both K halves, the token operand hi | mid, then lo | 0.
+        if (HALF == 1) {
+            const uint8_t* xql = cur + C::OFF_XQ;
+            wbf8 xa[MT], xb2[MT];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                xbv[mt] = *(const wbf8*)(xpl + (mt * 32 + r32) * kXpStride + 16 * h);
+            for (int mt = 0; mt < MT; ++mt) {
+                const uint8_t* q = xql + (mt * 32 + r32) * kXqRow + 16 * h;
+                xa[mt] = *(const wbf8*)q;
+                xb2[mt] = *(const wbf8*)(q + 32);
+            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                uint32_t mq[4];
+                uint32_t mq[8];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int j = 0; j < 8; ++j) {
                     int scj, mnj;
-                    k4_sm(4 * half + j, hdr[t].y, hdr[t].z, hdr[t].w, scj, mnj);
+                    k4_sm(j, hdr[t].y, hdr[t].z, hdr[t].w, scj, mnj);
                     mq[j] = bf16_bits((float)mnj);
                 }
-                const uint32_t m01 = mq[0] | (mq[1] << 16), m23 = mq[2] | (mq[3] << 16);
-                const wbf8 amq = __builtin_bit_cast(wbf8, wu4{m01, m23, m01, m23});
-                float* sc_t = scratch + t * 64;
-                if (h == 0) {
-                    sc_t[r32] = f16_to_f32(hdr[t].x & 0xFFFFu);
-                    sc_t[32 + r32] = f16_to_f32(hdr[t].x >> 16);
-                }
-                float dmr[16];
+                const wbf8 amq = __builtin_bit_cast(
+                    wbf8, wu4{mq[0] | (mq[1] << 16), mq[2] | (mq[3] << 16), mq[4] | (mq[5] << 16),
+                              mq[6] | (mq[7] << 16)});
+                const float* sc_t = scratch + t * 64;
+                float dr[16], dmr[16];
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 dv = *(const float4*)(sc_t + 8 * q4 + 4 * h);
                     const float4 mv = *(const float4*)(sc_t + 32 + 8 * q4 + 4 * h);
+                    dr[4 * q4] = dv.x; dr[4 * q4 + 1] = dv.y; dr[4 * q4 + 2] = dv.z; dr[4 * q4 + 3] = dv.w;
                     dmr[4 * q4] = mv.x; dmr[4 * q4 + 1] = mv.y; dmr[4 * q4 + 2] = mv.z; dmr[4 * q4 + 3] = mv.w;
                 }
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     wf16 fm = {};
-                    fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, xbv[mt], fm, 0, 0, 0);
+                    fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, xa[mt], fm, 0, 0, 0);
+                    fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, xb2[mt], fm, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) yacc[t][mt][r] = fmaf(-dmr[r], fm[r], yacc[t][mt][r]);
-                }
-                if (half == 1 || s + 1 == s_end) {
-                    float dr[16];
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; ++q4) {
-                        const float4 dv = *(const float4*)(sc_t + 8 * q4 + 4 * h);
-                        dr[4 * q4] = dv.x; dr[4 * q4 + 1] = dv.y; dr[4 * q4 + 2] = dv.z; dr[4 * q4 + 3] = dv.w;
+                    for (int r = 0; r < 16; ++r) {
+                        yacc[t][mt][r] = fmaf(-dmr[r], fm[r], fmaf(dr[r], sacc[t][mt][r], yacc[t][mt][r]));
+                        sacc[t][mt][r] = 0.0f;
                     }
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) yacc[t][mt][r] = fmaf(dr[r], sacc[t][mt][r], yacc[t][mt][r]);
                 }
             }
         }
-
-        if (more) {
-            wait_vm();
-            commit_stage(nxt, pd);
-        }
         __syncthreads();
+    };
+
+    // An empty split range (the host rounds the stages per split up to whole super-blocks)
+    // loads nothing and contributes zeros.
+    if (s_begin < s_end) {
+        issue_act(s_begin, lds);
+        issue_rest(s_begin, lds);
+        wait_vm();
+        __syncthreads();
+        for (int s = s_begin; s < s_end; ++s) run_stage(s);
     }
 
     // ---- output: lane holds rows 8q + 4h + (0..3) of each tile, token column r32 ----------
@@ -556,36 +549,41 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     auto commit_stage = [&](uint8_t* st, int gh, const Pending& pd) {
 #pragma unroll
         for (int j = 0; j < C::A_SLOTS; ++j) {
+            const wu4 av = pinned(pd.a[j]);
             if (a_dst[j] >= 0) {
-                *(wu4*)(st + a_dst[j]) = int8x8_to_h8(pd.a[j].x, pd.a[j].y);
-                *(wu4*)(st + a_dst[j] + 16) = int8x8_to_h8(pd.a[j].z, pd.a[j].w);
+                *(wu4*)(st + a_dst[j]) = int8x8_to_h8(av.x, av.y);
+                *(wu4*)(st + a_dst[j] + 16) = int8x8_to_h8(av.z, av.w);
             }
         }
 #pragma unroll
         for (int j = 0; j < C::R_SLOTS; ++j) {
             const int i = tid + j * C::THREADS;
+            uint32_t r[6];
+#pragma unroll
+            for (int e = 0; e < 6; ++e) r[e] = pinned(pd.r[j][e]);
             if (i < C::R_CHUNKS) {
                 const int piece = i / C::BN, row = i - piece * C::BN;
-                const uint32_t sh = pd.r[j][5] & 3u;
+                const uint32_t sh = r[5] & 3u;
                 uint8_t* dst = st + C::OFF_W + row * kQ6Row;
                 wu4 o;
-                o.x = __builtin_amdgcn_alignbyte(pd.r[j][1], pd.r[j][0], sh);
-                o.y = __builtin_amdgcn_alignbyte(pd.r[j][2], pd.r[j][1], sh);
-                o.z = __builtin_amdgcn_alignbyte(pd.r[j][3], pd.r[j][2], sh);
-                o.w = __builtin_amdgcn_alignbyte(pd.r[j][4], pd.r[j][3], sh);
+                o.x = __builtin_amdgcn_alignbyte(r[1], r[0], sh);
+                o.y = __builtin_amdgcn_alignbyte(r[2], r[1], sh);
+                o.z = __builtin_amdgcn_alignbyte(r[3], r[2], sh);
+                o.w = __builtin_amdgcn_alignbyte(r[4], r[3], sh);
                 if (piece < 6) {
                     *(wu4*)(dst + 16 * piece) = o;
                 } else {
                     // the 8 scales of this half, then d
                     *(u32x2*)(dst + 96) = gh ? u32x2{o.z, o.w} : u32x2{o.x, o.y};
-                    *(uint32_t*)(dst + 104) = pd.r[j][5] >> 16;
+                    *(uint32_t*)(dst + 104) = r[5] >> 16;
                 }
             }
         }
 #pragma unroll
         for (int j = 0; j < C::DX_SLOTS; ++j) {
             const int i = tid + j * C::THREADS;
-            if (i < C::DX_VALS) ((float*)(st + C::OFF_DX))[i] = pd.dx[j];
+            const float dv = pinned(pd.dx[j]);
+            if (i < C::DX_VALS) ((float*)(st + C::OFF_DX))[i] = dv;
         }
     };
 
@@ -598,20 +596,14 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     float* scratch = (float*)(lds + 2 * C::STAGE) + wave * 32;
     const int wrow = wave * 32 + r32;
 
-    {
-        Pending pd;
-        issue_stage(s_begin, pd);
-        commit_stage(lds, s_begin & 1, pd);
-    }
-    __syncthreads();
-
-    for (int s = s_begin; s < s_end; ++s) {
-        uint8_t* cur = lds + ((s - s_begin) & 1) * C::STAGE;
-        uint8_t* nxt = lds + ((s - s_begin + 1) & 1) * C::STAGE;
+    // One stage: half GH of a super-block (stage ranges are even and super-block aligned, so
+    // stage s sits in LDS buffer GH and the first block of GH = 0 starts the scaled sums).
+    auto run_stage = [&]<int GH>(int s) {
+        uint8_t* cur = lds + GH * C::STAGE;
+        uint8_t* nxt = lds + (1 - GH) * C::STAGE;
         Pending pd;
         const bool more = s + 1 < s_end;
         if (more) issue_stage(s + 1, pd);
-        const int gh = s & 1;
 
         const uint8_t* wr = cur + C::OFF_W + wrow * kQ6Row;
         const wu4 qh = *(const wu4*)(wr + 64 + 16 * h);
@@ -619,9 +611,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         const uint8_t* act = cur;
         const float* dxl = (const float*)(cur + C::OFF_DX);
 
-#pragma unroll 1
-        for (int i = 0; i < 4; ++i) {
-            const bool fresh = gh == 0 && i == 0;  // first block of the super-block
+        auto block = [&]<bool FRESH>(int i) {
             const wu4 ql = *(const wu4*)(wr + 32 * (i & 1) + 16 * h);
             const uint32_t lsh = i >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)i;
             uint32_t q6[4];
@@ -658,7 +648,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[1], b1, f, 0, 0, 0);
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[0], b0, f, 0, 0, 0);
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2[1], b1, f, 0, 0, 0);
-                if (fresh) {
+                if constexpr (FRESH) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) sacc[mt][r] = dxv * f[r];
                 } else {
@@ -666,8 +656,14 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
                     for (int r = 0; r < 16; ++r) sacc[mt][r] = fmaf(dxv, f[r], sacc[mt][r]);
                 }
             }
-        }
-        if (gh == 1 || s + 1 == s_end) {
+        };
+        if constexpr (GH == 0) {
+            block.template operator()<true>(0);
+#pragma unroll 1
+            for (int i = 1; i < 4; ++i) block.template operator()<false>(i);
+        } else {
+#pragma unroll 1
+            for (int i = 0; i < 4; ++i) block.template operator()<false>(i);
             // d of the super-block for the lane's 16 output rows
             if (h == 0) scratch[r32] = f16_to_f32(*(const uint16_t*)(wr + 104));
             float dr[16];
@@ -683,6 +679,21 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         }
         if (more) commit_stage(nxt, (s + 1) & 1, pd);
         __syncthreads();
+    };
+
+    // An empty split range (stages per split are rounded up to whole super-blocks) loads
+    // nothing and contributes zeros.
+    if (s_begin < s_end) {
+        {
+            Pending pd;
+            issue_stage(s_begin, pd);
+            commit_stage(lds, s_begin & 1, pd);
+        }
+        __syncthreads();
+        for (int s = s_begin; s < s_end; s += 2) {
+            run_stage.template operator()<0>(s);
+            run_stage.template operator()<1>(s + 1);
+        }
     }
 
 #pragma unroll
@@ -796,8 +807,8 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
 }
 
 template <int W, int NT, int MT>
-hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const int8_t* qs, const float* xs,
-                     const int32_t* xb, const float* bias, float* out, int splits,
+hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
+                     const uint16_t* xq, const float* bias, float* out, int splits,
                      hipStream_t stream) {
     using C = Cfg<W, NT, MT>;
     static bool attr_set = false;
@@ -809,9 +820,9 @@ hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const int8_t* qs, co
     }
     const uint32_t row_bytes = (uint32_t)(k / 256) * Q4_K_BYTES;
     const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
-    const int stages = k / kKS, per = (stages + splits - 1) / splits;
+    const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
     hipLaunchKernelGGL((k_gemmw_q4k<W, NT, MT>), dim3((unsigned)tiles, (unsigned)splits),
-                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qs, xs, xb, bias,
+                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, xq, bias,
                        out, per);
     return hipGetLastError();
 }
@@ -829,7 +840,7 @@ hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const int8_t* qs, co
     }
     const uint32_t row_bytes = (uint32_t)(k / 256) * Q6_K_BYTES;
     const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
-    const int stages = k / kKS, per = (stages + splits - 1) / splits;
+    const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
     hipLaunchKernelGGL((k_gemmw_q6k<W, MT>), dim3((unsigned)tiles, (unsigned)splits),
                        dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qs, xs, bias, out,
                        per);
@@ -845,12 +856,13 @@ size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m) {
 }
 
 hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
-                        const float* xs, const int32_t* xb, const float* bias, float* y,
-                        float* part, size_t part_bytes, hipStream_t stream) {
+                        const float* xs, const _Float16* qh, const uint16_t* xq,
+                        const float* bias, float* y, float* part, size_t part_bytes,
+                        hipStream_t stream) {
     if (!gemmw_supported(type) || k % 256 != 0) return hipErrorNotSupported;
     const uint64_t wbytes = (uint64_t)n * (uint64_t)(k / 256) * (type == T_Q6_K ? Q6_K_BYTES : Q4_K_BYTES);
-    if (wbytes >= (1ull << 32) || (uint64_t)m * (uint64_t)k >= (1ull << 32))
-        return hipErrorNotSupported;  // the kernels index with 32-bit offsets
+    if (wbytes >= (1ull << 32) || 2ull * (uint64_t)m * (uint64_t)k >= (1ull << 32))
+        return hipErrorNotSupported;  // the kernels index with 32-bit byte offsets
     Plan p = plan_for(type, k, n, m);
     if (p.splits > 1 && (part == nullptr || part_bytes < (size_t)p.splits * m * n * sizeof(float)))
         p.splits = 1;
@@ -861,7 +873,7 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     } else {
 #define CLLM_GEMMW_CASE(A, B, D)                                                              \
         if (p.wv == A && p.nt == B && p.mt == D)                                               \
-            e = launch_q4<A, B, D>(w, k, n, m, qs, xs, xb, bias, out, p.splits, stream);
+            e = launch_q4<A, B, D>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
         CLLM_GEMMW_CASE(8, 1, 4)
         CLLM_GEMMW_CASE(8, 1, 2)
         CLLM_GEMMW_CASE(8, 2, 2)

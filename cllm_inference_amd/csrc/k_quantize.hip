@@ -12,16 +12,18 @@
 
 namespace cllm_hip {
 
-// Besides the Q8_0 row (qs, scales, bsums, any of which may be null), the MFMA path asks for
-// the quantized values as fp16 (qh, exact: |q| <= 128) and dx * bsum (px, the K-quant
-// minimum term's activation factor).
+// Besides the Q8_0 row (qs, scales, bsums, any of which may be null), the MFMA paths ask for
+// the quantized values as fp16 (qh, exact: |q| <= 128) and dx * bsum, the K-quant minimum
+// term's activation factor, as fp32 (px) or split into bf16 parts per super-block (xq, see
+// xq_store; its record of block blk is xq + 32 (blk / 8), rows of k % 256 == 0 elements).
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__ x,
                                                        int64_t n_blocks,
                                                        int8_t* __restrict__ qs,
                                                        float* __restrict__ scales,
                                                        int32_t* __restrict__ bsums,
                                                        _Float16* __restrict__ qh,
-                                                       float* __restrict__ px) {
+                                                       float* __restrict__ px,
+                                                       uint16_t* __restrict__ xq) {
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gt >> 3;
     const int part = (int)(gt & 7);
@@ -54,6 +56,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
         if (scales) scales[blk] = d;
         if (bsums) bsums[blk] = s;
         if (px) px[blk] = d * (float)s;
+        if (xq) xq_store(xq + (blk >> 3) * 32, (int)(blk & 7), d * (float)s);
     }
 }
 
@@ -63,7 +66,8 @@ __global__ __launch_bounds__(256) void k_q8_to_mfma(const int8_t* __restrict__ q
                                                     const float* __restrict__ scales,
                                                     const int32_t* __restrict__ bsums,
                                                     int64_t n_blocks, _Float16* __restrict__ qh,
-                                                    float* __restrict__ px) {
+                                                    float* __restrict__ px,
+                                                    uint16_t* __restrict__ xq) {
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gt >> 3;
     const int part = (int)(gt & 7);
@@ -73,7 +77,11 @@ __global__ __launch_bounds__(256) void k_q8_to_mfma(const int8_t* __restrict__ q
     const h4 hv = {(_Float16)(int8_t)(packed & 0xFF), (_Float16)(int8_t)(packed >> 8),
                    (_Float16)(int8_t)(packed >> 16), (_Float16)(int8_t)(packed >> 24)};
     *(h4*)(qh + blk * 32 + part * 4) = hv;
-    if (part == 0) px[blk] = scales[blk] * (float)bsums[blk];
+    if (part == 0) {
+        const float pv = scales[blk] * (float)bsums[blk];
+        if (px) px[blk] = pv;
+        if (xq) xq_store(xq + (blk >> 3) * 32, (int)(blk & 7), pv);
+    }
 }
 
 hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* qs, float* scales,
@@ -82,7 +90,7 @@ hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* qs, fl
     const int64_t threads = n_blocks * 8;
     const int64_t grid = (threads + 255) / 256;
     hipLaunchKernelGGL(k_quantize_q8_0, dim3((unsigned)grid), dim3(256), 0, stream, x, n_blocks,
-                       qs, scales, bsums, (_Float16*)nullptr, (float*)nullptr);
+                       qs, scales, bsums, (_Float16*)nullptr, (float*)nullptr, (uint16_t*)nullptr);
     return hipGetLastError();
 }
 
@@ -91,7 +99,7 @@ hipError_t launch_quantize_mfma(const float* x, int64_t n_blocks, float* scales,
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks * 8 + 255) / 256;
     hipLaunchKernelGGL(k_quantize_q8_0, dim3((unsigned)grid), dim3(256), 0, stream, x, n_blocks,
-                       (int8_t*)nullptr, scales, (int32_t*)nullptr, qh, px);
+                       (int8_t*)nullptr, scales, (int32_t*)nullptr, qh, px, (uint16_t*)nullptr);
     return hipGetLastError();
 }
 
@@ -100,7 +108,25 @@ hipError_t launch_q8_to_mfma(const int8_t* qs, const float* scales, const int32_
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks * 8 + 255) / 256;
     hipLaunchKernelGGL(k_q8_to_mfma, dim3((unsigned)grid), dim3(256), 0, stream, qs, scales,
-                       bsums, n_blocks, qh, px);
+                       bsums, n_blocks, qh, px, (uint16_t*)nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_w(const float* x, int64_t n_blocks, float* scales, _Float16* qh,
+                             uint16_t* xq, hipStream_t stream) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t grid = (n_blocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(k_quantize_q8_0, dim3((unsigned)grid), dim3(256), 0, stream, x, n_blocks,
+                       (int8_t*)nullptr, scales, (int32_t*)nullptr, qh, (float*)nullptr, xq);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_to_w(const int8_t* qs, const float* scales, const int32_t* bsums,
+                          int64_t n_blocks, _Float16* qh, uint16_t* xq, hipStream_t stream) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t grid = (n_blocks * 8 + 255) / 256;
+    hipLaunchKernelGGL(k_q8_to_mfma, dim3((unsigned)grid), dim3(256), 0, stream, qs, scales,
+                       bsums, n_blocks, qh, (float*)nullptr, xq);
     return hipGetLastError();
 }
 

@@ -21,6 +21,14 @@ hipError_t launch_quantize_mfma(const float* x, int64_t n_blocks, float* scales,
 hipError_t launch_q8_to_mfma(const int8_t* qs, const float* scales, const int32_t* bsums,
                              int64_t n_blocks, _Float16* qh, float* px, hipStream_t stream);
 
+// The Q4_K weight-row GEMM's activation format: dx (scales), the quantized values as exact
+// fp16 (qh[m * k]) and dx * bsum split into bf16 parts, one 64-byte record per 8 blocks
+// (xq[m * k / 8]); rows of k % 256 == 0 elements. From fp32 or from a Q8_0 batch.
+hipError_t launch_quantize_w(const float* x, int64_t n_blocks, float* scales, _Float16* qh,
+                             uint16_t* xq, hipStream_t stream);
+hipError_t launch_q8_to_w(const int8_t* qs, const float* scales, const int32_t* bsums,
+                          int64_t n_blocks, _Float16* qh, uint16_t* xq, hipStream_t stream);
+
 // y[t, j] = vec_dot(W row j, activation row t) (+ bias[j]) for t < m, j < n.
 // Activation rows are Q8_0: qs[t * k], scales / bsums[t * k / 32]. Any m >= 1.
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
@@ -47,12 +55,14 @@ hipError_t launch_gemm16(uint32_t type, const uint8_t* w, int k, int n, int m,
                          const _Float16* qh, const float* xs, const float* xp, const float* bias,
                          float* y, hipStream_t stream);
 
-// The weight-row fp16-MFMA GEMM (k_gemmw.hip) on a Q8_0 batch (same contract as launch_gemm).
-// Q4_K and Q6_K; k % 256 == 0. When its plan splits K, it writes partial sums to part (at least
+// The weight-row fp16-MFMA GEMM (k_gemmw.hip), same contract as launch_gemm. Q4_K reads the
+// activation format of launch_quantize_w (qh, xs, xq), Q6_K the Q8_0 batch (qs, xs).
+// k % 256 == 0. When its plan splits K, it writes partial sums to part (at least
 // gemmw_partial_bytes(type, k, n, m) bytes, else K is not split) and reduces them into y.
 hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
-                        const float* xs, const int32_t* xb, const float* bias, float* y,
-                        float* part, size_t part_bytes, hipStream_t stream);
+                        const float* xs, const _Float16* qh, const uint16_t* xq,
+                        const float* bias, float* y, float* part, size_t part_bytes,
+                        hipStream_t stream);
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
 bool gemmw_supported(uint32_t type);
 
