@@ -239,11 +239,10 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
             hipError_t e = ws->part.ensure(pb, stream);
             if (e != hipSuccess) return e;
         }
-        if (type == T_Q4_K) {
-            hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws->qh, ws->xq, stream);
-            if (e != hipSuccess) return e;
-        }
-        return launch_gemmw(type, w, k, n, m, qs, sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,
+        hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws->sc, ws->qh,
+                                      type == T_Q4_K ? ws->xq : nullptr, stream);
+        if (e != hipSuccess) return e;
+        return launch_gemmw(type, w, k, n, m, ws->sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,
                             pb ? ws->part.cap : 0, stream);
     }
     if (kind == GemmKind::I8) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
@@ -262,16 +261,17 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
         if (e != hipSuccess) return e;
         return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
     }
-    if (kind == GemmKind::W16 && type == T_Q4_K) {
-        hipError_t e = launch_quantize_w(x, nblk, ws->sc, ws->qh, ws->xq, stream);
+    if (kind == GemmKind::W16) {
+        hipError_t e = launch_quantize_w(x, nblk, ws->sc, ws->qh, type == T_Q4_K ? ws->xq : nullptr,
+                                         stream);
         if (e != hipSuccess) return e;
         const size_t pb = gemmw_partial_bytes(type, k, n, m);
         if (pb) {
             e = ws->part.ensure(pb, stream);
             if (e != hipSuccess) return e;
         }
-        return launch_gemmw(type, w, k, n, m, nullptr, ws->sc, ws->qh, ws->xq, bias, y,
-                            (float*)ws->part.p, pb ? ws->part.cap : 0, stream);
+        return launch_gemmw(type, w, k, n, m, ws->sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,
+                            pb ? ws->part.cap : 0, stream);
     }
     hipError_t e = launch_quantize_q8_0(x, nblk, ws->qs, ws->sc, ws->bs, stream);
     if (e != hipSuccess) return e;

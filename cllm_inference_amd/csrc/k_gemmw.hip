@@ -49,7 +49,7 @@ constexpr int kXqRow = 64;      // bytes per token and super-block of the minimu
 // Q4_K kernel. Every operand reaches LDS by direct-to-LDS loads (no register staging):
 //   ACT  [token][16 chunks of 8 fp16], chunk c of token t stored at slot c ^ (t & 15), so the
 //        16-byte fragment reads of 16 consecutive tokens fall on distinct banks;
-//   DX   [block][token] fp32;
+//   DX   [token][4 blocks] fp32 (at least one wave-load);
 //   XQ   [token][hi 8 | mid 8 | lo 8 | 0 8] bf16 for the super-block (stages of half 1 only);
 //   W    [row][80] raw Q4_K bytes: 16-byte header, then the half super-block's 64 quant bytes.
 template <int W, int NT, int MT>
@@ -58,7 +58,7 @@ struct Cfg {
     static constexpr int BN = 32 * NT * W;
     static constexpr int BM = 32 * MT;
     static constexpr int ACT = BM * 256;
-    static constexpr int DX = 4 * BM * 4;
+    static constexpr int DX = BM * 16 < 1024 ? 1024 : BM * 16;
     static constexpr int XQ = BM * kXqRow;
     static constexpr int WB = BN * kWRow;
     static constexpr int OFF_DX = ACT;
@@ -74,7 +74,7 @@ struct Cfg {
     static constexpr int W_LOADS = WB / 1024;
     static_assert(WB % 1024 == 0, "whole wave-loads of weight chunks");
     static constexpr int W_SLOTS = (W_LOADS + W - 1) / W;
-    static constexpr int DX_LOADS = DX / 256;
+    static constexpr int DX_LOADS = DX / 1024;
     static constexpr int DX_SLOTS = (DX_LOADS + W - 1) / W;
     static constexpr int XQ_LOADS = XQ / 1024;
     static constexpr int XQ_SLOTS = (XQ_LOADS + W - 1) / W;
@@ -197,12 +197,11 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                    (piece == 0 ? 0u : (uint32_t)(Q4_K_QS + 16 * (piece - 1)));
         w_q[j] = piece != 0;
     }
-    uint32_t dx_off[C::DX_SLOTS];  // elements into xs: [block][token] in LDS
+    uint32_t dx_off[C::DX_SLOTS];  // elements into xs: a token's 4 blocks of the stage
 #pragma unroll
     for (int j = 0; j < C::DX_SLOTS; ++j) {
-        const int p = min(wave + j * W, C::DX_LOADS - 1) * 64 + lane;
-        const int b = p / BM, tok = p - b * BM;
-        dx_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)nb + b;
+        const int t = min(wave + j * W, C::DX_LOADS - 1) * 64 + lane;
+        dx_off[j] = (uint32_t)min(m0 + t, m - 1) * (uint32_t)nb;
     }
     uint32_t q_off[C::XQ_SLOTS];   // bytes into xq: 16 tokens x 64 bytes per wave-load
 #pragma unroll
@@ -212,37 +211,41 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
         q_off[j] = (uint32_t)min(m0 + t, m - 1) * (uint32_t)(k / 256) * (uint32_t)kXqRow + 16u * (lane & 3);
     }
 
-    // A stage's direct-to-LDS loads: the activations, then weights, dx and (for the second half
-    // of a super-block) the minimum operand.
-    auto issue_act = [&](int s, uint8_t* st) {
+    // A stage's direct-to-LDS loads, in two parts issued before each half of the stage's MFMA
+    // work: a wave's address unit accepts about one 16-byte wave-load per 16 cycles, so the
+    // whole stage issued at once (right after a barrier, by every wave) stalls the waves for
+    // ~1000 cycles. Offsets pass through pinned() so their address arithmetic is not hoisted
+    // out of the MFMA loop (where it would hold registers the loop needs).
+    auto issue_part = [&](int s, uint8_t* st, int part) {
+        const int sb = s >> 1, half = s & 1;
+        constexpr int AH = (C::A_SLOTS + 1) / 2, WH = (C::W_SLOTS + 1) / 2;
 #pragma unroll
         for (int j = 0; j < C::A_SLOTS; ++j) {
             const int L = wave + j * W;
-            if (C::A_LOADS % W == 0 || L < C::A_LOADS)
-                lds_load16((const uint8_t*)qh + a_off[j] + (uint32_t)s * (2u * kKS), st + L * 1024);
+            if ((j < AH) == (part == 0) && (C::A_LOADS % W == 0 || L < C::A_LOADS))
+                lds_load16((const uint8_t*)qh + pinned(a_off[j]) + (uint32_t)s * (2u * kKS), st + L * 1024);
         }
-    };
-    auto issue_rest = [&](int s, uint8_t* st) {
-        const int sb = s >> 1, half = s & 1;
 #pragma unroll
         for (int j = 0; j < C::W_SLOTS; ++j) {
             const int L = wave + j * W;
-            if (C::W_LOADS % W == 0 || L < C::W_LOADS)
-                lds_load16(w + w_off[j] + (uint32_t)sb * Q4_K_BYTES + (w_q[j] ? 64u * half : 0u),
+            if ((j < WH) == (part == 0) && (C::W_LOADS % W == 0 || L < C::W_LOADS))
+                lds_load16(w + pinned(w_off[j]) + (uint32_t)sb * Q4_K_BYTES + (w_q[j] ? 64u * half : 0u),
                            st + C::OFF_W + L * 1024);
         }
+        if (part == 0) {
 #pragma unroll
-        for (int j = 0; j < C::DX_SLOTS; ++j) {
-            const int L = wave + j * W;
-            if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
-                lds_load4(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + L * 256);
-        }
-        if (half == 1) {
+            for (int j = 0; j < C::DX_SLOTS; ++j) {
+                const int L = wave + j * W;
+                if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
+                    lds_load16(xs + pinned(dx_off[j]) + (uint32_t)s * 4, st + C::OFF_DX + L * 1024);
+            }
+        } else if (half == 1) {
 #pragma unroll
             for (int j = 0; j < C::XQ_SLOTS; ++j) {
                 const int L = wave + j * W;
                 if (C::XQ_LOADS % W == 0 || L < C::XQ_LOADS)
-                    lds_load16((const uint8_t*)xq + q_off[j] + (uint32_t)sb * kXqRow, st + C::OFF_XQ + L * 1024);
+                    lds_load16((const uint8_t*)xq + pinned(q_off[j]) + (uint32_t)sb * kXqRow,
+                               st + C::OFF_XQ + L * 1024);
             }
         }
     };
@@ -281,10 +284,6 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
             }
         }
         const bool more = s + 1 < s_end;
-        if (more) {
-            issue_act(s + 1, nxt);
-            issue_rest(s + 1, nxt);
-        }
 
         const uint8_t* act = cur;
         const float* dxl = (const float*)(cur + C::OFF_DX);
@@ -319,7 +318,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                     const int sw = tok & 15;
                     const wh8 b0 = *(const wh8*)(arow + (((4 * b + 2 * h) ^ sw) << 4));
                     const wh8 b1 = *(const wh8*)(arow + (((4 * b + 2 * h + 1) ^ sw) << 4));
-                    const float dxv = dxl[b * BM + tok];
+                    const float dxv = dxl[tok * 4 + b];
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         wf16 f = {};
@@ -332,7 +331,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
             }
         };
 #pragma unroll 1
-        for (int pc = 0; pc < 2; ++pc) blocks(pc);
+        for (int pc = 0; pc < 2; ++pc) {
+            if (more) issue_part(s + 1, nxt, pc);
+            blocks(pc);
+        }
 
         // The next stage's loads have landed before the scratch is read (an LDS read while
         // direct-to-LDS loads are in flight waits for all of them anyway).
@@ -343,13 +345,6 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
         //   the 8 minima in both K halves, the token operand hi | mid, then lo | 0.
         if (HALF == 1) {
             const uint8_t* xql = cur + C::OFF_XQ;
-            wbf8 xa[MT], xb2[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const uint8_t* q = xql + (mt * 32 + r32) * kXqRow + 16 * h;
-                xa[mt] = *(const wbf8*)q;
-                xb2[mt] = *(const wbf8*)(q + 32);
-            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 uint32_t mq[8];
@@ -373,9 +368,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                 }
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
+                    const uint8_t* q = xql + (mt * 32 + r32) * kXqRow + 16 * h;
                     wf16 fm = {};
-                    fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, xa[mt], fm, 0, 0, 0);
-                    fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, xb2[mt], fm, 0, 0, 0);
+                    fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, *(const wbf8*)q, fm, 0, 0, 0);
+                    fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, *(const wbf8*)(q + 32), fm, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         yacc[t][mt][r] = fmaf(-dmr[r], fm[r], fmaf(dr[r], sacc[t][mt][r], yacc[t][mt][r]));
@@ -390,8 +386,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     // An empty split range (the host rounds the stages per split up to whole super-blocks)
     // loads nothing and contributes zeros.
     if (s_begin < s_end) {
-        issue_act(s_begin, lds);
-        issue_rest(s_begin, lds);
+        issue_part(s_begin, lds, 0);
+        issue_part(s_begin, lds, 1);
         wait_vm();
         __syncthreads();
         for (int s = s_begin; s < s_end; ++s) run_stage(s);
@@ -435,7 +431,7 @@ struct Cfg6 {
     static constexpr int THREADS = 64 * W;
     static constexpr int BN = 32 * W;
     static constexpr int BM = 32 * MT;
-    static constexpr int ACT = BM * kActRow;
+    static constexpr int ACT = BM * 256;          // swizzled fp16 activations, as for Q4_K
     static constexpr int DX = 4 * BM * 4;
     static constexpr int WB = BN * kQ6Row;
     static constexpr int OFF_DX = ACT;
@@ -445,18 +441,18 @@ struct Cfg6 {
     static constexpr int LDS = 2 * STAGE + SCRATCH;
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(BN % 64 == 0, "a wave loads one raw piece type per slot");
-    static constexpr int A_CHUNKS = BM * 8;
-    static constexpr int A_SLOTS = (A_CHUNKS + THREADS - 1) / THREADS;
-    static constexpr int R_CHUNKS = BN * kQ6Pieces;
+    static constexpr int A_LOADS = ACT / 1024;    // direct-to-LDS wave-loads
+    static constexpr int A_SLOTS = (A_LOADS + W - 1) / W;
+    static constexpr int DX_LOADS = DX / 256;
+    static constexpr int DX_SLOTS = (DX_LOADS + W - 1) / W;
+    static constexpr int R_CHUNKS = BN * kQ6Pieces;  // raw weight pieces through registers
     static constexpr int R_SLOTS = (R_CHUNKS + THREADS - 1) / THREADS;
-    static constexpr int DX_VALS = 4 * BM;
-    static constexpr int DX_SLOTS = (DX_VALS + THREADS - 1) / THREADS;
 };
 
 template <int W, int MT>
 __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict__ w,
                                                       uint32_t row_bytes, int k, int n, int m,
-                                                      const int8_t* __restrict__ qs,
+                                                      const _Float16* __restrict__ qh,
                                                       const float* __restrict__ xs,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int split_stages) {
@@ -481,16 +477,14 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     const bool partial = gridDim.y > 1;
     float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
 
-    // per-lane offsets for stage 0
-    uint32_t a_off[C::A_SLOTS];
-    int a_dst[C::A_SLOTS];
+    // per-lane offsets for stage 0 (rows and tokens past the matrix are clamped to the last one)
+    uint32_t a_off[C::A_SLOTS];   // bytes into qh: token, swizzled 16-byte chunk
 #pragma unroll
     for (int j = 0; j < C::A_SLOTS; ++j) {
-        const int i = tid + j * C::THREADS;
-        const int ic = min(i, C::A_CHUNKS - 1);
-        const int tok = ic >> 3, c8 = ic & 7;
-        a_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)k + 16u * c8;
-        a_dst[j] = i < C::A_CHUNKS ? tok * kActRow + 32 * c8 : -1;
+        const int L = min(wave + j * W, C::A_LOADS - 1);
+        const int t = 4 * L + (lane >> 4);
+        const int c = (lane & 15) ^ (t & 15);
+        a_off[j] = ((uint32_t)min(m0 + t, m - 1) * (uint32_t)k + 8u * (uint32_t)c) * 2u;
     }
     uint32_t r_row[C::R_SLOTS];  // byte offset of the row's first super-block
 #pragma unroll
@@ -498,24 +492,33 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         const int i = min(tid + j * C::THREADS, C::R_CHUNKS - 1);
         r_row[j] = (uint32_t)min(n0 + i % C::BN, n - 1) * row_bytes;
     }
-    uint32_t dx_off[C::DX_SLOTS];
+    uint32_t dx_off[C::DX_SLOTS];  // elements into xs: [block][token] in LDS
 #pragma unroll
     for (int j = 0; j < C::DX_SLOTS; ++j) {
-        const int i = min(tid + j * C::THREADS, C::DX_VALS - 1);
-        const int b = i / BM, tok = i - b * BM;
+        const int p = min(wave + j * W, C::DX_LOADS - 1) * 64 + lane;
+        const int b = p / BM, tok = p - b * BM;
         dx_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)nb + b;
     }
 
     struct Pending {
-        wu4 a[C::A_SLOTS];
         uint32_t r[C::R_SLOTS][6];
-        float dx[C::DX_SLOTS];
     };
-    auto issue_stage = [&](int s, Pending& pd) {
+    // activations and dx go straight to LDS; the 2-byte-aligned weight pieces come through
+    // registers and are realigned by commit_stage
+    auto issue_stage = [&](int s, uint8_t* st, Pending& pd) {
         const int sb = s >> 1, gh = s & 1;
 #pragma unroll
-        for (int j = 0; j < C::A_SLOTS; ++j)
-            pd.a[j] = *(const wu4*)(qs + a_off[j] + (uint32_t)s * kKS);
+        for (int j = 0; j < C::A_SLOTS; ++j) {
+            const int L = wave + j * W;
+            if (C::A_LOADS % W == 0 || L < C::A_LOADS)
+                lds_load16((const uint8_t*)qh + a_off[j] + (uint32_t)s * (2u * kKS), st + L * 1024);
+        }
+#pragma unroll
+        for (int j = 0; j < C::DX_SLOTS; ++j) {
+            const int L = wave + j * W;
+            if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
+                lds_load4(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + L * 256);
+        }
 #pragma unroll
         for (int j = 0; j < C::R_SLOTS; ++j) {
             const int i = tid + j * C::THREADS;
@@ -543,18 +546,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
                 pd.r[j][5] = sh | ((uint32_t)*(const uint16_t*)(base + Q6_K_D) << 16);
             }
         }
-#pragma unroll
-        for (int j = 0; j < C::DX_SLOTS; ++j) pd.dx[j] = xs[dx_off[j] + (uint32_t)s * 4];
     };
     auto commit_stage = [&](uint8_t* st, int gh, const Pending& pd) {
-#pragma unroll
-        for (int j = 0; j < C::A_SLOTS; ++j) {
-            const wu4 av = pinned(pd.a[j]);
-            if (a_dst[j] >= 0) {
-                *(wu4*)(st + a_dst[j]) = int8x8_to_h8(av.x, av.y);
-                *(wu4*)(st + a_dst[j] + 16) = int8x8_to_h8(av.z, av.w);
-            }
-        }
 #pragma unroll
         for (int j = 0; j < C::R_SLOTS; ++j) {
             const int i = tid + j * C::THREADS;
@@ -579,12 +572,6 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
                 }
             }
         }
-#pragma unroll
-        for (int j = 0; j < C::DX_SLOTS; ++j) {
-            const int i = tid + j * C::THREADS;
-            const float dv = pinned(pd.dx[j]);
-            if (i < C::DX_VALS) ((float*)(st + C::OFF_DX))[i] = dv;
-        }
     };
 
     wf16 sacc[MT], yacc[MT];
@@ -601,12 +588,16 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     auto run_stage = [&]<int GH>(int s) {
         uint8_t* cur = lds + GH * C::STAGE;
         uint8_t* nxt = lds + (1 - GH) * C::STAGE;
+        const uint8_t* wr = cur + C::OFF_W + wrow * kQ6Row;
+        // d of the super-block for the lane's output rows goes to the wave's scratch before the
+        // next stage's direct-to-LDS loads are issued (an LDS store while they are in flight
+        // would make the compiler wait for all of them)
+        if (GH == 1 && h == 0) scratch[r32] = f16_to_f32(*(const uint16_t*)(wr + 104));
         Pending pd;
         const bool more = s + 1 < s_end;
-        if (more) issue_stage(s + 1, pd);
+        if (more) issue_stage(s + 1, nxt, pd);
 
-        const uint8_t* wr = cur + C::OFF_W + wrow * kQ6Row;
-        const wu4 qh = *(const wu4*)(wr + 64 + 16 * h);
+        const wu4 qhb = *(const wu4*)(wr + 64 + 16 * h);
         const u32x2 scv = *(const u32x2*)(wr + 96);  // the 8 scales of this half
         const uint8_t* act = cur;
         const float* dxl = (const float*)(cur + C::OFF_DX);
@@ -615,10 +606,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
             const wu4 ql = *(const wu4*)(wr + 32 * (i & 1) + 16 * h);
             const uint32_t lsh = i >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)i;
             uint32_t q6[4];
-            q6[0] = ((ql.x >> lsh) & 0x0F0F0F0Fu) | (((qh.x >> hsh) & 0x03030303u) << 4);
-            q6[1] = ((ql.y >> lsh) & 0x0F0F0F0Fu) | (((qh.y >> hsh) & 0x03030303u) << 4);
-            q6[2] = ((ql.z >> lsh) & 0x0F0F0F0Fu) | (((qh.z >> hsh) & 0x03030303u) << 4);
-            q6[3] = ((ql.w >> lsh) & 0x0F0F0F0Fu) | (((qh.w >> hsh) & 0x03030303u) << 4);
+            q6[0] = ((ql.x >> lsh) & 0x0F0F0F0Fu) | (((qhb.x >> hsh) & 0x03030303u) << 4);
+            q6[1] = ((ql.y >> lsh) & 0x0F0F0F0Fu) | (((qhb.y >> hsh) & 0x03030303u) << 4);
+            q6[2] = ((ql.z >> lsh) & 0x0F0F0F0Fu) | (((qhb.z >> hsh) & 0x03030303u) << 4);
+            q6[3] = ((ql.w >> lsh) & 0x0F0F0F0Fu) | (((qhb.w >> hsh) & 0x03030303u) << 4);
             // scale of this lane's 16 values: sc[8 g + 2 i + h], local index 2 i + h
             const int si = 2 * i + h;
             const uint32_t scw = si < 4 ? scv.x : scv.y;
@@ -640,8 +631,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int tok = mt * 32 + r32;
-                const wh8 b0 = *(const wh8*)(act + tok * kActRow + 16 * (4 * i + 2 * h));
-                const wh8 b1 = *(const wh8*)(act + tok * kActRow + 16 * (4 * i + 2 * h + 1));
+                const uint8_t* arow = act + tok * 256;
+                const int sw = tok & 15;
+                const wh8 b0 = *(const wh8*)(arow + (((4 * i + 2 * h) ^ sw) << 4));
+                const wh8 b1 = *(const wh8*)(arow + (((4 * i + 2 * h + 1) ^ sw) << 4));
                 const float dxv = dxl[i * BM + tok];
                 wf16 f = {};
                 f = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[0], b0, f, 0, 0, 0);
@@ -664,8 +657,9 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         } else {
 #pragma unroll 1
             for (int i = 0; i < 4; ++i) block.template operator()<false>(i);
-            // d of the super-block for the lane's 16 output rows
-            if (h == 0) scratch[r32] = f16_to_f32(*(const uint16_t*)(wr + 104));
+        }
+        if (more) wait_vm();
+        if constexpr (GH == 1) {
             float dr[16];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
@@ -686,7 +680,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     if (s_begin < s_end) {
         {
             Pending pd;
-            issue_stage(s_begin, pd);
+            issue_stage(s_begin, lds, pd);
+            wait_vm();
             commit_stage(lds, s_begin & 1, pd);
         }
         __syncthreads();
@@ -828,7 +823,7 @@ hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const _Float16* qh, 
 }
 
 template <int W, int MT>
-hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const int8_t* qs, const float* xs,
+hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
                      const float* bias, float* out, int splits, hipStream_t stream) {
     using C = Cfg6<W, MT>;
     static bool attr_set = false;
@@ -842,7 +837,7 @@ hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const int8_t* qs, co
     const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
     const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
     hipLaunchKernelGGL((k_gemmw_q6k<W, MT>), dim3((unsigned)tiles, (unsigned)splits),
-                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qs, xs, bias, out,
+                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, bias, out,
                        per);
     return hipGetLastError();
 }
@@ -855,8 +850,8 @@ size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m) {
     return p.splits > 1 ? (size_t)p.splits * (size_t)m * (size_t)n * sizeof(float) : 0;
 }
 
-hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
-                        const float* xs, const _Float16* qh, const uint16_t* xq,
+hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const float* xs,
+                        const _Float16* qh, const uint16_t* xq,
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream) {
     if (!gemmw_supported(type) || k % 256 != 0) return hipErrorNotSupported;
@@ -869,7 +864,7 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     float* out = p.splits > 1 ? part : y;
     hipError_t e = hipErrorNotSupported;
     if (type == T_Q6_K) {
-        e = launch_q6<4, 2>(w, k, n, m, qs, xs, bias, out, p.splits, stream);
+        e = launch_q6<4, 2>(w, k, n, m, qh, xs, bias, out, p.splits, stream);
     } else {
 #define CLLM_GEMMW_CASE(A, B, D)                                                              \
         if (p.wv == A && p.nt == B && p.mt == D)                                               \

@@ -60,14 +60,15 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
     }
 }
 
-// int8 qs / fp32 scales / int32 bsums (an already-quantized batch) -> the MFMA path's fp16
-// values and dx * bsum.
+// int8 qs / fp32 scales / int32 bsums (an already-quantized batch) -> the MFMA paths' fp16
+// values and dx * bsum, and (scales_out, may be null) a copy of the scales.
 __global__ __launch_bounds__(256) void k_q8_to_mfma(const int8_t* __restrict__ qs,
                                                     const float* __restrict__ scales,
                                                     const int32_t* __restrict__ bsums,
                                                     int64_t n_blocks, _Float16* __restrict__ qh,
                                                     float* __restrict__ px,
-                                                    uint16_t* __restrict__ xq) {
+                                                    uint16_t* __restrict__ xq,
+                                                    float* __restrict__ scales_out) {
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gt >> 3;
     const int part = (int)(gt & 7);
@@ -79,6 +80,7 @@ __global__ __launch_bounds__(256) void k_q8_to_mfma(const int8_t* __restrict__ q
     *(h4*)(qh + blk * 32 + part * 4) = hv;
     if (part == 0) {
         const float pv = scales[blk] * (float)bsums[blk];
+        if (scales_out) scales_out[blk] = scales[blk];
         if (px) px[blk] = pv;
         if (xq) xq_store(xq + (blk >> 3) * 32, (int)(blk & 7), pv);
     }
@@ -108,7 +110,7 @@ hipError_t launch_q8_to_mfma(const int8_t* qs, const float* scales, const int32_
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks * 8 + 255) / 256;
     hipLaunchKernelGGL(k_q8_to_mfma, dim3((unsigned)grid), dim3(256), 0, stream, qs, scales,
-                       bsums, n_blocks, qh, px, (uint16_t*)nullptr);
+                       bsums, n_blocks, qh, px, (uint16_t*)nullptr, (float*)nullptr);
     return hipGetLastError();
 }
 
@@ -122,11 +124,12 @@ hipError_t launch_quantize_w(const float* x, int64_t n_blocks, float* scales, _F
 }
 
 hipError_t launch_q8_to_w(const int8_t* qs, const float* scales, const int32_t* bsums,
-                          int64_t n_blocks, _Float16* qh, uint16_t* xq, hipStream_t stream) {
+                          int64_t n_blocks, float* scales_out, _Float16* qh, uint16_t* xq,
+                          hipStream_t stream) {
     if (n_blocks <= 0) return hipSuccess;
     const int64_t grid = (n_blocks * 8 + 255) / 256;
     hipLaunchKernelGGL(k_q8_to_mfma, dim3((unsigned)grid), dim3(256), 0, stream, qs, scales,
-                       bsums, n_blocks, qh, (float*)nullptr, xq);
+                       bsums, n_blocks, qh, (float*)nullptr, xq, scales_out);
     return hipGetLastError();
 }
 

@@ -21,13 +21,16 @@ hipError_t launch_quantize_mfma(const float* x, int64_t n_blocks, float* scales,
 hipError_t launch_q8_to_mfma(const int8_t* qs, const float* scales, const int32_t* bsums,
                              int64_t n_blocks, _Float16* qh, float* px, hipStream_t stream);
 
-// The Q4_K weight-row GEMM's activation format: dx (scales), the quantized values as exact
-// fp16 (qh[m * k]) and dx * bsum split into bf16 parts, one 64-byte record per 8 blocks
-// (xq[m * k / 8]); rows of k % 256 == 0 elements. From fp32 or from a Q8_0 batch.
+// The weight-row GEMM's activation format: dx (scales), the quantized values as exact fp16
+// (qh[m * k]) and (xq, may be null) dx * bsum split into bf16 parts, one 64-byte record per
+// 8 blocks (xq[m * k / 8]); rows of k % 256 == 0 elements. From fp32 or from a Q8_0 batch.
 hipError_t launch_quantize_w(const float* x, int64_t n_blocks, float* scales, _Float16* qh,
                              uint16_t* xq, hipStream_t stream);
+// (The Q8_0 variant also copies the scales to scales_out: the GEMM loads them 16 bytes at a
+// time, so they must sit in a 16-byte-aligned buffer of the library's own.)
 hipError_t launch_q8_to_w(const int8_t* qs, const float* scales, const int32_t* bsums,
-                          int64_t n_blocks, _Float16* qh, uint16_t* xq, hipStream_t stream);
+                          int64_t n_blocks, float* scales_out, _Float16* qh, uint16_t* xq,
+                          hipStream_t stream);
 
 // y[t, j] = vec_dot(W row j, activation row t) (+ bias[j]) for t < m, j < n.
 // Activation rows are Q8_0: qs[t * k], scales / bsums[t * k / 32]. Any m >= 1.
@@ -55,12 +58,13 @@ hipError_t launch_gemm16(uint32_t type, const uint8_t* w, int k, int n, int m,
                          const _Float16* qh, const float* xs, const float* xp, const float* bias,
                          float* y, hipStream_t stream);
 
-// The weight-row fp16-MFMA GEMM (k_gemmw.hip), same contract as launch_gemm. Q4_K reads the
-// activation format of launch_quantize_w (qh, xs, xq), Q6_K the Q8_0 batch (qs, xs).
-// k % 256 == 0. When its plan splits K, it writes partial sums to part (at least
-// gemmw_partial_bytes(type, k, n, m) bytes, else K is not split) and reduces them into y.
-hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
-                        const float* xs, const _Float16* qh, const uint16_t* xq,
+// The weight-row fp16-MFMA GEMM (k_gemmw.hip), same contract as launch_gemm, on the activation
+// format of launch_quantize_w: dx (xs), fp16 values (qh) and, for Q4_K, the minimum operand
+// (xq). Q4_K and Q6_K; k % 256 == 0. When its plan splits K, it writes partial sums to part
+// (at least gemmw_partial_bytes(type, k, n, m) bytes, else K is not split) and reduces them
+// into y.
+hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const float* xs,
+                        const _Float16* qh, const uint16_t* xq,
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream);
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
