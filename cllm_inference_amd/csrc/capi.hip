@@ -240,7 +240,7 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
             if (e != hipSuccess) return e;
         }
         hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws->sc, ws->qh,
-                                      type == T_Q4_K ? ws->xq : nullptr, stream);
+                                      (type == T_Q4_K || type == T_Q5_K) ? ws->xq : nullptr, stream);
         if (e != hipSuccess) return e;
         return launch_gemmw(type, w, k, n, m, ws->sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,
                             pb ? ws->part.cap : 0, stream);
@@ -262,7 +262,7 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
         return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
     }
     if (kind == GemmKind::W16) {
-        hipError_t e = launch_quantize_w(x, nblk, ws->sc, ws->qh, type == T_Q4_K ? ws->xq : nullptr,
+        hipError_t e = launch_quantize_w(x, nblk, ws->sc, ws->qh, (type == T_Q4_K || type == T_Q5_K) ? ws->xq : nullptr,
                                          stream);
         if (e != hipSuccess) return e;
         const size_t pb = gemmw_partial_bytes(type, k, n, m);

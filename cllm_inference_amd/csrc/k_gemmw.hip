@@ -41,8 +41,10 @@ typedef float wf16 __attribute__((ext_vector_type(16)));
 typedef uint32_t wu4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKS = 128;        // K elements per stage
-constexpr int kWRow = 80;       // LDS bytes per weight row per stage: header + 64 qs bytes
-constexpr int kWChunks = kWRow / 16;
+// LDS bytes per weight row per stage: the 16-byte header, for Q5_K the super-block's 32 qh
+// bytes, and the half super-block's 64 qs bytes
+template <bool Q5>
+constexpr int wrow_bytes() { return Q5 ? 112 : 80; }
 constexpr int kActRow = 272;    // Q6_K kernel: LDS bytes per token, 128 fp16 + 16 of padding
 constexpr int kXqRow = 64;      // bytes per token and super-block of the minimum operand
 
@@ -51,8 +53,9 @@ constexpr int kXqRow = 64;      // bytes per token and super-block of the minimu
 //        16-byte fragment reads of 16 consecutive tokens fall on distinct banks;
 //   DX   [token][4 blocks] fp32 (at least one wave-load);
 //   XQ   [token][hi 8 | mid 8 | lo 8 | 0 8] bf16 for the super-block (stages of half 1 only);
-//   W    [row][80] raw Q4_K bytes: 16-byte header, then the half super-block's 64 quant bytes.
-template <int W, int NT, int MT>
+//   W    [row][80] raw Q4_K bytes: 16-byte header, then the half super-block's 64 quant bytes
+//        (Q5_K: [row][112], the 32 qh bytes between the two).
+template <int W, int NT, int MT, bool Q5>
 struct Cfg {
     static constexpr int THREADS = 64 * W;
     static constexpr int BN = 32 * NT * W;
@@ -60,7 +63,8 @@ struct Cfg {
     static constexpr int ACT = BM * 256;
     static constexpr int DX = BM * 16 < 1024 ? 1024 : BM * 16;
     static constexpr int XQ = BM * kXqRow;
-    static constexpr int WB = BN * kWRow;
+    static constexpr int WROW = wrow_bytes<Q5>();
+    static constexpr int WB = BN * WROW;
     static constexpr int OFF_DX = ACT;
     static constexpr int OFF_XQ = OFF_DX + DX;
     static constexpr int OFF_W = OFF_XQ + XQ;
@@ -144,7 +148,7 @@ __device__ __forceinline__ void k4_sm(int j, uint32_t s0, uint32_t s1, uint32_t 
 
 }  // namespace
 
-template <int W, int NT, int MT>
+template <int W, int NT, int MT, bool Q5>
 __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict__ w,
                                                       uint32_t row_bytes, int k, int n, int m,
                                                       const _Float16* __restrict__ qh,
@@ -152,8 +156,11 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                                                       const uint16_t* __restrict__ xq,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int split_stages) {
-    using C = Cfg<W, NT, MT>;
+    using C = Cfg<W, NT, MT, Q5>;
     constexpr int BM = C::BM;
+    constexpr int WCH = C::WROW / 16;             // 16-byte pieces per weight row and stage
+    constexpr int QS_AT = Q5 ? 48 : 16;           // qs bytes within an LDS row
+    constexpr uint32_t SB_BYTES = Q5 ? Q5_K_BYTES : Q4_K_BYTES;
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -192,10 +199,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     for (int j = 0; j < C::W_SLOTS; ++j) {
         const int L = min(wave + j * W, C::W_LOADS - 1);
         const int p = L * 64 + lane;
-        const int row = p / kWChunks, piece = p - row * kWChunks;
-        w_off[j] = (uint32_t)min(n0 + row, n - 1) * row_bytes +
-                   (piece == 0 ? 0u : (uint32_t)(Q4_K_QS + 16 * (piece - 1)));
-        w_q[j] = piece != 0;
+        const int row = p / WCH, piece = p - row * WCH;
+        // header, (Q5_K) qh, then the qs bytes, which move with the stage half
+        w_off[j] = (uint32_t)min(n0 + row, n - 1) * row_bytes + 16u * (uint32_t)piece;
+        w_q[j] = 16 * piece >= QS_AT;
     }
     uint32_t dx_off[C::DX_SLOTS];  // elements into xs: a token's 4 blocks of the stage
 #pragma unroll
@@ -229,7 +236,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
         for (int j = 0; j < C::W_SLOTS; ++j) {
             const int L = wave + j * W;
             if ((j < WH) == (part == 0) && (C::W_LOADS % W == 0 || L < C::W_LOADS))
-                lds_load16(w + pinned(w_off[j]) + (uint32_t)sb * Q4_K_BYTES + (w_q[j] ? 64u * half : 0u),
+                lds_load16(w + pinned(w_off[j]) + (uint32_t)sb * SB_BYTES + (w_q[j] ? 64u * half : 0u),
                            st + C::OFF_W + L * 1024);
         }
         if (part == 0) {
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
         wu4 hdr[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            wr[t] = cur + C::OFF_W + ((wave * NT + t) * 32 + r32) * kWRow;
+            wr[t] = cur + C::OFF_W + ((wave * NT + t) * 32 + r32) * C::WROW;
             hdr[t] = *(const wu4*)wr[t];
             if (h == 0 && HALF == 1) {
                 float* sc_t = scratch + t * 64;
@@ -295,18 +302,41 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
             wh8 afr[NT][2][2];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const wu4 q = *(const wu4*)(wr[t] + 16 * (1 + 2 * pc + h));
+                const wu4 q = *(const wu4*)(wr[t] + QS_AT + 32 * pc + 16 * h);
                 int sa, ma, sb, mb;
                 k4_sm(2 * c, hdr[t].y, hdr[t].z, hdr[t].w, sa, ma);
                 k4_sm(2 * c + 1, hdr[t].y, hdr[t].z, hdr[t].w, sb, mb);
-                const _Float16 fa = (_Float16)sa, fb = (_Float16)(sb * 0.0625f);
-                const _Float16 ca = (_Float16)(-1024.0f * sa), cb = (_Float16)(-64.0f * sb);
-                const wh2 s_lo = {fa, fa}, c_lo = {ca, ca};
-                const wh2 s_hi = {fb, fb}, c_hi = {cb, cb};
-                afr[t][0][0] = scaled8(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, s_lo, c_lo);
-                afr[t][0][1] = scaled8(q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu, s_lo, c_lo);
-                afr[t][1][0] = scaled8(q.x & 0xF0F0F0F0u, q.y & 0xF0F0F0F0u, s_hi, c_hi);
-                afr[t][1][1] = scaled8(q.z & 0xF0F0F0F0u, q.w & 0xF0F0F0F0u, s_hi, c_hi);
+                const _Float16 fa = (_Float16)sa;
+                const wh2 s_lo = {fa, fa};
+                if constexpr (Q5) {
+                    // 5-bit values: bit 2c (sub-block 2c) or 2c+1 of qh[l] above the nibble;
+                    // sc * q <= 63 * 31 stays exact in fp16
+                    const wu4 hb = *(const wu4*)(wr[t] + 16 + 16 * h);
+                    const uint32_t q4[4] = {q.x, q.y, q.z, q.w}, h4[4] = {hb.x, hb.y, hb.z, hb.w};
+                    uint32_t lo[4], hi[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        lo[e] = (q4[e] & 0x0F0F0F0Fu) | (((h4[e] >> (2 * c)) & 0x01010101u) << 4);
+                        hi[e] = ((q4[e] >> 4) & 0x0F0F0F0Fu) | (((h4[e] >> (2 * c + 1)) & 0x01010101u) << 4);
+                    }
+                    const _Float16 fb = (_Float16)sb;
+                    const wh2 s_hi = {fb, fb};
+                    const wh2 c_lo = {(_Float16)(-1024.0f * sa), (_Float16)(-1024.0f * sa)};
+                    const wh2 c_hi = {(_Float16)(-1024.0f * sb), (_Float16)(-1024.0f * sb)};
+                    afr[t][0][0] = scaled8(lo[0], lo[1], s_lo, c_lo);
+                    afr[t][0][1] = scaled8(lo[2], lo[3], s_lo, c_lo);
+                    afr[t][1][0] = scaled8(hi[0], hi[1], s_hi, c_hi);
+                    afr[t][1][1] = scaled8(hi[2], hi[3], s_hi, c_hi);
+                } else {
+                    const _Float16 fb = (_Float16)(sb * 0.0625f);
+                    const _Float16 ca = (_Float16)(-1024.0f * sa), cb = (_Float16)(-64.0f * sb);
+                    const wh2 c_lo = {ca, ca};
+                    const wh2 s_hi = {fb, fb}, c_hi = {cb, cb};
+                    afr[t][0][0] = scaled8(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, s_lo, c_lo);
+                    afr[t][0][1] = scaled8(q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu, s_lo, c_lo);
+                    afr[t][1][0] = scaled8(q.x & 0xF0F0F0F0u, q.y & 0xF0F0F0F0u, s_hi, c_hi);
+                    afr[t][1][1] = scaled8(q.z & 0xF0F0F0F0u, q.w & 0xF0F0F0F0u, s_hi, c_hi);
+                }
             }
 #pragma unroll
             for (int blk = 0; blk < 2; ++blk) {
@@ -707,6 +737,244 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     }
 }
 
+// ------------------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
+// 32-element blocks with one fp16 scale d each (quant.cpp: Q8_0 and Q4_0 vec_dot 706-724,
+// Q5_0 its analogue). The weight operand holds the block's integers (q, q - 8 or q - 16, exact
+// in fp16), so a block's MFMA pair returns the reference's integer dot I exactly and
+//   y += dx * (d * I)
+// costs two VALU operations per output and block (d belongs to the weight row, dx to the
+// token). A stage is 4 blocks (128 elements); the rows' stage bytes (4 blocks of 34 / 18 / 22
+// bytes, 4-byte aligned because k % 256 == 0) arrive by 4-byte direct-to-LDS loads in the
+// blocks' own layout, and each lane realigns its 2-byte-aligned fields from 4-byte LDS reads.
+template <uint32_t T>
+constexpr int b32_bytes() { return T == T_Q8_0 ? Q8_0_BYTES : T == T_Q4_0 ? Q4_0_BYTES : Q5_0_BYTES; }
+
+template <uint32_t T, int W, int MT>
+struct CfgB {
+    static constexpr int THREADS = 64 * W;
+    static constexpr int BN = 32 * W;
+    static constexpr int BM = 32 * MT;
+    static constexpr int SROW = 4 * b32_bytes<T>();   // bytes per weight row per stage
+    static constexpr int SDW = SROW / 4;
+    static constexpr int ACT = BM * 256;                // swizzled fp16, as for the K-quants
+    static constexpr int DX = BM * 16 < 1024 ? 1024 : BM * 16;
+    static constexpr int WB = (BN * SROW + 255) / 256 * 256 + 64;  // + slack for the last lane's 5th dword
+    static constexpr int OFF_DX = ACT;
+    static constexpr int OFF_W = OFF_DX + DX;
+    static constexpr int STAGE = OFF_W + WB;
+    static constexpr int SCRATCH = W * 4 * 32 * 4;      // per wave: d[4 blocks][32 rows]
+    static constexpr int LDS = 2 * STAGE + SCRATCH;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static constexpr int A_LOADS = ACT / 1024;
+    static constexpr int A_SLOTS = (A_LOADS + W - 1) / W;
+    static constexpr int DX_LOADS = DX / 1024;
+    static constexpr int DX_SLOTS = (DX_LOADS + W - 1) / W;
+    static constexpr int W_DW = BN * SDW;               // weight dwords per stage
+    static constexpr int W_LOADS = (W_DW + 63) / 64;    // 4-byte wave-loads
+    static constexpr int W_SLOTS = (W_LOADS + W - 1) / W;
+};
+
+// Bytes [o, o + 4 N) of an LDS row whose base is 4-byte aligned, o even: N + 1 aligned dword
+// reads and a funnel shift.
+template <int N>
+__device__ __forceinline__ void lds_unaligned(const uint8_t* row, int o, uint32_t (&out)[N]) {
+    const uint32_t* p = (const uint32_t*)(row + (o & ~3));
+    const uint32_t sh = (uint32_t)(o & 3);
+    uint32_t v[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; ++i) v[i] = p[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
+}
+
+// Four bits b0..b3 of x (at bit positions 0..3) moved to bit 4 of bytes 0..3.
+__device__ __forceinline__ uint32_t bits_to_byte_bit4(uint32_t x) {
+    x &= 0xFu;
+    return ((x | (x << 7) | (x << 14) | (x << 21)) & 0x01010101u) << 4;
+}
+
+template <uint32_t T, int W, int MT>
+__global__ __launch_bounds__(64 * W) void k_gemmw_b32(const uint8_t* __restrict__ w,
+                                                      uint32_t row_bytes, int k, int n, int m,
+                                                      const _Float16* __restrict__ qh,
+                                                      const float* __restrict__ xs,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ y, int split_stages) {
+    using C = CfgB<T, W, MT>;
+    constexpr int BM = C::BM;
+    constexpr int BS = b32_bytes<T>();
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane >> 5;
+    const int r32 = lane & 31;
+
+    const int mb_count = (m + BM - 1) / BM;
+    const int g = gridDim.x;
+    const int bid = blockIdx.x;
+    const int lin = (g % 8 == 0) ? (bid % 8) * (g / 8) + bid / 8 : bid;
+    const int nblk = lin / mb_count, mblk = lin - nblk * mb_count;
+    const int n0 = nblk * C::BN, m0 = mblk * BM;
+    const int nb = k / 32;
+    const int s_begin = blockIdx.y * split_stages;
+    const int s_end = min(s_begin + split_stages, k / kKS);
+    const bool partial = gridDim.y > 1;
+    float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
+
+    // per-lane source offsets (stage 0); rows and tokens past the matrix are clamped
+    uint32_t a_off[C::A_SLOTS];
+#pragma unroll
+    for (int j = 0; j < C::A_SLOTS; ++j) {
+        const int L = min(wave + j * W, C::A_LOADS - 1);
+        const int t = 4 * L + (lane >> 4);
+        const int c = (lane & 15) ^ (t & 15);
+        a_off[j] = ((uint32_t)min(m0 + t, m - 1) * (uint32_t)k + 8u * (uint32_t)c) * 2u;
+    }
+    uint32_t dx_off[C::DX_SLOTS];
+#pragma unroll
+    for (int j = 0; j < C::DX_SLOTS; ++j) {
+        const int t = min(wave + j * W, C::DX_LOADS - 1) * 64 + lane;
+        dx_off[j] = (uint32_t)min(m0 + t, m - 1) * (uint32_t)nb;
+    }
+    uint32_t w_off[C::W_SLOTS];   // flat dword f of [row][SDW]: row f / SDW, dword f % SDW
+#pragma unroll
+    for (int j = 0; j < C::W_SLOTS; ++j) {
+        const int f = min(min(wave + j * W, C::W_LOADS - 1) * 64 + lane, C::W_DW - 1);
+        const int row = f / C::SDW, dw = f - row * C::SDW;
+        w_off[j] = (uint32_t)min(n0 + row, n - 1) * row_bytes + 4u * (uint32_t)dw;
+    }
+
+    auto issue_stage = [&](int s, uint8_t* st) {
+#pragma unroll
+        for (int j = 0; j < C::A_SLOTS; ++j) {
+            const int L = wave + j * W;
+            if (C::A_LOADS % W == 0 || L < C::A_LOADS)
+                lds_load16((const uint8_t*)qh + a_off[j] + (uint32_t)s * (2u * kKS), st + L * 1024);
+        }
+#pragma unroll
+        for (int j = 0; j < C::DX_SLOTS; ++j) {
+            const int L = wave + j * W;
+            if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
+                lds_load16(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + L * 1024);
+        }
+#pragma unroll
+        for (int j = 0; j < C::W_SLOTS; ++j) {
+            const int L = wave + j * W;
+            if (C::W_LOADS % W == 0 || L < C::W_LOADS)
+                lds_load4(w + w_off[j] + (uint32_t)s * (uint32_t)C::SROW, st + C::OFF_W + L * 256);
+        }
+    };
+
+    wf16 yacc[MT];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) yacc[a][r] = 0.0f;
+
+    float* scratch = (float*)(lds + 2 * C::STAGE) + wave * 128;
+    const int wrow = wave * 32 + r32;
+
+    auto run_stage = [&](int s) {
+        const int buf = (s - s_begin) & 1;
+        uint8_t* cur = lds + buf * C::STAGE;
+        uint8_t* nxt = lds + (1 - buf) * C::STAGE;
+        const uint8_t* wr = cur + C::OFF_W + wrow * C::SROW;
+
+        // d of blocks 2h and 2h + 1 of this lane's row -> scratch, then each lane's 16 output
+        // rows' d for all 4 blocks into registers, before the next stage's direct-to-LDS loads
+        // are issued (LDS accesses while they fly would make the compiler wait for them)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int b = 2 * h + e;
+            const uint32_t dw = *(const uint32_t*)(wr + ((b * BS) & ~3));
+            scratch[b * 32 + r32] = f16_to_f32(((b * BS) & 2) ? (dw >> 16) : (dw & 0xFFFFu));
+        }
+        float dr[4][16];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 dv = *(const float4*)(scratch + b * 32 + 8 * q4 + 4 * h);
+                dr[b][4 * q4] = dv.x; dr[b][4 * q4 + 1] = dv.y; dr[b][4 * q4 + 2] = dv.z; dr[b][4 * q4 + 3] = dv.w;
+            }
+        const bool more = s + 1 < s_end;
+        if (more) issue_stage(s + 1, nxt);
+
+        const uint8_t* act = cur;
+        const float* dxl = (const float*)(cur + C::OFF_DX);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            // A fragments: elements 16h + 8j + e of block b (K steps j = 0, 1)
+            wh8 afr[2];
+            if constexpr (T == T_Q8_0) {
+                uint32_t u[4];
+                lds_unaligned<4>(wr, b * BS + 2 + 16 * h, u);
+                afr[0] = __builtin_bit_cast(wh8, int8x8_to_h8(u[0], u[1]));
+                afr[1] = __builtin_bit_cast(wh8, int8x8_to_h8(u[2], u[3]));
+            } else {
+                uint32_t u[4], hb = 0;
+                if constexpr (T == T_Q4_0) {
+                    lds_unaligned<4>(wr, b * BS + 2, u);
+                } else {
+                    uint32_t v[5];
+                    lds_unaligned<5>(wr, b * BS + 2, v);
+                    hb = v[0] >> (16 * h);
+                    u[0] = v[1]; u[1] = v[2]; u[2] = v[3]; u[3] = v[4];
+                }
+                // byte j: low nibble = element j, high nibble = element 16 + j
+                uint32_t q[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    q[e] = h ? ((u[e] >> 4) & 0x0F0F0F0Fu) : (u[e] & 0x0F0F0F0Fu);
+                    if constexpr (T == T_Q5_0) q[e] |= bits_to_byte_bit4(hb >> (4 * e));
+                }
+                const _Float16 off = (_Float16)(T == T_Q4_0 ? -1032.0f : -1040.0f);
+                const wh2 one = {(_Float16)1.0f, (_Float16)1.0f}, c = {off, off};
+                afr[0] = scaled8(q[0], q[1], one, c);
+                afr[1] = scaled8(q[2], q[3], one, c);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int tok = mt * 32 + r32;
+                const uint8_t* arow = act + tok * 256;
+                const int sw = tok & 15;
+                const wh8 b0 = *(const wh8*)(arow + (((4 * b + 2 * h) ^ sw) << 4));
+                const wh8 b1 = *(const wh8*)(arow + (((4 * b + 2 * h + 1) ^ sw) << 4));
+                const float dxv = dxl[tok * 4 + b];
+                wf16 f = {};
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[0], b0, f, 0, 0, 0);
+                f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[1], b1, f, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) yacc[mt][r] = fmaf(dxv, dr[b][r] * f[r], yacc[mt][r]);
+            }
+        }
+        if (more) wait_vm();
+        __syncthreads();
+    };
+
+    if (s_begin < s_end) {
+        issue_stage(s_begin, lds);
+        wait_vm();
+        __syncthreads();
+        for (int s = s_begin; s < s_end; ++s) run_stage(s);
+    }
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int tok = m0 + mt * 32 + r32;
+        if (tok >= m) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = n0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row < n) {
+                float v = yacc[mt][r];
+                if (bias && !partial) v += bias[row];
+                out[(size_t)tok * n + row] = v;
+            }
+        }
+    }
+}
+
 // y[i] = sum of the split-K slices (+ bias): total = m * n elements, four per thread when
 // n % 4 == 0 (16-byte aligned rows), else one.
 __global__ void k_split_reduce(const float* __restrict__ part, int splits, int64_t total,
@@ -734,7 +1002,12 @@ __global__ void k_split_reduce(const float* __restrict__ part, int splits, int64
     }
 }
 
-bool gemmw_supported(uint32_t type) { return type == T_Q4_K || type == T_Q6_K; }
+bool gemmw_supported(uint32_t type) {
+    return type == T_Q4_K || type == T_Q5_K || type == T_Q6_K || type == T_Q8_0 || type == T_Q4_0 ||
+           type == T_Q5_0;
+}
+
+bool is_b32(uint32_t type) { return type == T_Q8_0 || type == T_Q4_0 || type == T_Q5_0; }
 
 namespace {
 
@@ -771,10 +1044,15 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
     }
     const int cus = device_cus();
     int target = 2 * cus;  // workgroups to aim for
-    if (type == T_Q6_K) {
+    if (is_b32(type)) {
+        // 32-element block types: 128 x 32 tiles up to 32 rows, else 128 x 64 (the per-block
+        // d of the 16 output rows a lane holds stays in registers, which larger token tiles
+        // would spill); split K to about two workgroups per CU
+        p.wv = 4, p.nt = 1, p.mt = m <= 32 ? 1 : 2;
+    } else if (type == T_Q6_K) {
         // 128 weight rows x 64 tokens (4 waves, two workgroups per CU)
         p.wv = 4, p.nt = 1, p.mt = 2;
-    } else if (wv != 0) {
+    } else if (wv != 0 && type == T_Q4_K) {
         p.wv = wv, p.nt = nt, p.mt = mt;
     } else {
         // From sweeps on MI355X at m = 512 (us for n = 14336 / 4096 / 1024): 256 x 128 tiles
@@ -801,22 +1079,22 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
     return p;
 }
 
-template <int W, int NT, int MT>
+template <int W, int NT, int MT, bool Q5>
 hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
                      const uint16_t* xq, const float* bias, float* out, int splits,
                      hipStream_t stream) {
-    using C = Cfg<W, NT, MT>;
+    using C = Cfg<W, NT, MT, Q5>;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemmw_q4k<W, NT, MT>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemmw_q4k<W, NT, MT, Q5>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    const uint32_t row_bytes = (uint32_t)(k / 256) * Q4_K_BYTES;
+    const uint32_t row_bytes = (uint32_t)(k / 256) * (Q5 ? Q5_K_BYTES : Q4_K_BYTES);
     const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
     const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
-    hipLaunchKernelGGL((k_gemmw_q4k<W, NT, MT>), dim3((unsigned)tiles, (unsigned)splits),
+    hipLaunchKernelGGL((k_gemmw_q4k<W, NT, MT, Q5>), dim3((unsigned)tiles, (unsigned)splits),
                        dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, xq, bias,
                        out, per);
     return hipGetLastError();
@@ -842,6 +1120,25 @@ hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const _Float16* qh, 
     return hipGetLastError();
 }
 
+template <uint32_t T, int W, int MT>
+hipError_t launch_b32(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
+                      const float* bias, float* out, int splits, hipStream_t stream) {
+    using C = CfgB<T, W, MT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemmw_b32<T, W, MT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const uint32_t row_bytes = (uint32_t)(k / 32) * (uint32_t)b32_bytes<T>();
+    const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+    const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
+    hipLaunchKernelGGL((k_gemmw_b32<T, W, MT>), dim3((unsigned)tiles, (unsigned)splits),
+                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, bias, out, per);
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m) {
@@ -855,7 +1152,7 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream) {
     if (!gemmw_supported(type) || k % 256 != 0) return hipErrorNotSupported;
-    const uint64_t wbytes = (uint64_t)n * (uint64_t)(k / 256) * (type == T_Q6_K ? Q6_K_BYTES : Q4_K_BYTES);
+    const uint64_t wbytes = (uint64_t)n * (uint64_t)(k / block_elems(type)) * (uint64_t)block_bytes(type);
     if (wbytes >= (1ull << 32) || 2ull * (uint64_t)m * (uint64_t)k >= (1ull << 32))
         return hipErrorNotSupported;  // the kernels index with 32-bit byte offsets
     Plan p = plan_for(type, k, n, m);
@@ -865,10 +1162,30 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     hipError_t e = hipErrorNotSupported;
     if (type == T_Q6_K) {
         e = launch_q6<4, 2>(w, k, n, m, qh, xs, bias, out, p.splits, stream);
+    } else if (is_b32(type)) {
+#define CLLM_GEMMW_B32(TT)                                                                    \
+        if (type == TT) {                                                                      \
+            if (p.mt == 2)                                                                     \
+                e = launch_b32<TT, 4, 2>(w, k, n, m, qh, xs, bias, out, p.splits, stream);     \
+            else                                                                               \
+                e = launch_b32<TT, 4, 1>(w, k, n, m, qh, xs, bias, out, p.splits, stream);     \
+        }
+        CLLM_GEMMW_B32(T_Q8_0)
+        CLLM_GEMMW_B32(T_Q4_0)
+        CLLM_GEMMW_B32(T_Q5_0)
+#undef CLLM_GEMMW_B32
+    } else if (type == T_Q5_K) {
+        // the three shapes of the default plan (tuning overrides apply to Q4_K only)
+        if (p.wv == 8 && p.nt == 1 && p.mt == 4)
+            e = launch_q4<8, 1, 4, true>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
+        else if (p.wv == 8 && p.nt == 1 && p.mt == 2)
+            e = launch_q4<8, 1, 2, true>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
+        else
+            e = launch_q4<4, 1, 1, true>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
     } else {
 #define CLLM_GEMMW_CASE(A, B, D)                                                              \
         if (p.wv == A && p.nt == B && p.mt == D)                                               \
-            e = launch_q4<A, B, D>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
+            e = launch_q4<A, B, D, false>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
         CLLM_GEMMW_CASE(8, 1, 4)
         CLLM_GEMMW_CASE(8, 1, 2)
         CLLM_GEMMW_CASE(8, 2, 2)

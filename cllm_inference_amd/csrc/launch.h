@@ -60,7 +60,7 @@ hipError_t launch_gemm16(uint32_t type, const uint8_t* w, int k, int n, int m,
 
 // The weight-row fp16-MFMA GEMM (k_gemmw.hip), same contract as launch_gemm, on the activation
 // format of launch_quantize_w: dx (xs), fp16 values (qh) and, for Q4_K, the minimum operand
-// (xq). Q4_K and Q6_K; k % 256 == 0. When its plan splits K, it writes partial sums to part
+// (xq). Q4_K, Q5_K and Q6_K; k % 256 == 0. When its plan splits K, it writes partial sums to part
 // (at least gemmw_partial_bytes(type, k, n, m) bytes, else K is not split) and reduces them
 // into y.
 hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const float* xs,

@@ -73,7 +73,7 @@ def test_mfma_matches_gemv_and_oracle(gpu, orc, qt, gemm_kernel):
     y_gemv = torch.cat([gpu.gemv_q8_dev(wd, qt, k, n, qs[i:i + 8], sc[i:i + 8], bs[i:i + 8])
                         for i in (0, 8)])
     assert gpu.matmul_route(qt, k, n, 8) == "gemv"
-    if gemm_kernel != "default" or qt in (S.Q4_K, S.Q6_K):
+    if gemm_kernel != "default" or qt in (S.Q4_K, S.Q5_K, S.Q6_K):
         assert gpu.matmul_route(qt, k, n, 16) == "mfma"
     exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
     yo = orc.matmul(x, w, qt, None, k, n, m)
