@@ -61,8 +61,7 @@ def test_m_sweep_batches_vs_reference_golden(gpu, orc, label, m):
 
 @pytest.mark.parametrize("qt", TYPES)
 def test_mfma_matches_gemv_and_oracle(gpu, orc, qt, gemm_kernel):
-    """Same rows through the MFMA kernel (16 rows at once; by default only the weight-row
-    kernel's types take that route at 16 rows) and the GEMV kernel (8 + 8)."""
+    """Same rows through the MFMA kernel (16 rows at once) and the GEMV kernel (8 + 8)."""
     import torch
     k, n, m = 1024, 300, 16
     w = S.make_weight(qt, n, k, 70 + qt)
@@ -73,8 +72,7 @@ def test_mfma_matches_gemv_and_oracle(gpu, orc, qt, gemm_kernel):
     y_gemv = torch.cat([gpu.gemv_q8_dev(wd, qt, k, n, qs[i:i + 8], sc[i:i + 8], bs[i:i + 8])
                         for i in (0, 8)])
     assert gpu.matmul_route(qt, k, n, 8) == "gemv"
-    if gemm_kernel != "default" or qt in (S.Q4_K, S.Q5_K, S.Q6_K):
-        assert gpu.matmul_route(qt, k, n, 16) == "mfma"
+    assert gpu.matmul_route(qt, k, n, 16) == "mfma"
     exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
     yo = orc.matmul(x, w, qt, None, k, n, m)
     check_close(y_mfma.cpu().numpy(), yo, exact, abs_sum, "mfma " + S.TYPE_NAMES[qt])
@@ -119,3 +117,23 @@ def test_full_prefill_layer_sampled_rows(gpu, orc):
         assert (d / scale).max() < 1e-3, (label, (d / scale).max())
         del wd, xd, y, yg
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("splits", [None, "4"])
+@pytest.mark.parametrize("qt", TYPES)
+def test_mfma_tails_and_split_k(gpu, orc, qt, splits, gemm_kernel, monkeypatch):
+    """Output rows and activation rows that end inside a tile (n = 520, m = 80), K = 2048, with
+    the planned K split and with K forced into 4 splits (partial sums plus the reduction)."""
+    if splits:
+        monkeypatch.setenv("CLLM_HIP_GEMMW_SPLITS", splits)
+    else:
+        monkeypatch.delenv("CLLM_HIP_GEMMW_SPLITS", raising=False)
+    k, n, m = 2048, 520, 80
+    w = S.make_weight(qt, n, k, 90 + qt)
+    x = S.make_activation(m, k, 91 + qt, outliers=True)
+    bias = np.linspace(-1.0, 1.0, n).astype(np.float32)
+    print("tails", S.TYPE_NAMES[qt], "splits", splits, flush=True)
+    y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, _dev(bias), k, n).cpu().numpy()
+    exact, abs_sum = orc.matmul_f64(x, w, qt, bias, k, n, m)
+    yo = orc.matmul(x, w, qt, bias, k, n, m)
+    check_close(y, yo, exact, abs_sum, f"tails {S.TYPE_NAMES[qt]} splits={splits}")
