@@ -98,6 +98,14 @@ struct Workspace {
         xq = (uint16_t*)(p + qs_bytes + 3 * sc_bytes + qh_bytes);
         return hipSuccess;
     }
+    // The weight-row GEMM's split-K workspace; a new allocation is zeroed (its tile counters
+    // must start at zero; every launch leaves them zero).
+    hipError_t ensure_part(size_t bytes, hipStream_t stream) {
+        const void* before = part.p;
+        hipError_t e = part.ensure(bytes, stream);
+        if (e != hipSuccess || part.p == before) return e;
+        return gemmw_workspace_init(part.p, part.cap, stream);
+    }
 };
 
 struct Region {
@@ -236,7 +244,7 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
     if (kind == GemmKind::W16) {
         const size_t pb = gemmw_partial_bytes(type, k, n, m);
         if (pb) {
-            hipError_t e = ws->part.ensure(pb, stream);
+            hipError_t e = ws->ensure_part(pb, stream);
             if (e != hipSuccess) return e;
         }
         hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws->sc, ws->qh,
@@ -267,7 +275,7 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
         if (e != hipSuccess) return e;
         const size_t pb = gemmw_partial_bytes(type, k, n, m);
         if (pb) {
-            e = ws->part.ensure(pb, stream);
+            e = ws->ensure_part(pb, stream);
             if (e != hipSuccess) return e;
         }
         return launch_gemmw(type, w, k, n, m, ws->sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,

@@ -146,6 +146,105 @@ __device__ __forceinline__ void k4_sm(int j, uint32_t s0, uint32_t s1, uint32_t 
     }
 }
 
+// Output of a workgroup's tile: lane values val(i, r) for token tok(i) and weight row row(i, r),
+// i < NI, r < 16. Without split-K they go to y (plus the bias). With split-K (gridDim.y > 1)
+// each wave writes its whole share of the tile, bounds ignored, to its slot of split
+// blockIdx.y in part, laid out [i][r / 2][lane] in 8-byte pairs so that every store
+// instruction covers 512 contiguous bytes; the last split to finish the tile, found by a
+// per-tile arrival counter that it resets, adds the slots in split order (its own from
+// registers, so the sum does not depend on which split finished last), plus the bias, into y.
+// No split waits for another.
+//
+// The slots cross XCDs, whose L2 caches are not coherent with each other. They are written
+// and read as relaxed agent-scope atomics (loads and stores that are coherent device-wide by
+// themselves), so no agent-scope fence is needed: such a fence writes back and invalidates
+// the whole L2 of the XCD, under the feet of every other workgroup streaming through it.
+// Each wave waits for its slot stores to complete before the workgroup barrier, and the
+// counter is bumped after that barrier; the workgroup's LDS (free once every wave has left
+// its main loop) carries the verdict.
+template <int NI, int W, class Val, class Tok, class Row>
+__device__ __forceinline__ void store_tile(int n, int m, const float* __restrict__ bias,
+                                           float* __restrict__ y, float* __restrict__ part,
+                                           int* __restrict__ counters, uint8_t* lds, int wave,
+                                           Val val, Tok tok, Row row) {
+    const int splits = (int)gridDim.y;
+    if (splits == 1) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int t = tok(i);
+            if (t >= m) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int j = row(i, r);
+                if (j < n) {
+                    float v = val(i, r);
+                    if (bias) v += bias[j];
+                    y[(size_t)t * n + j] = v;
+                }
+            }
+        }
+        return;
+    }
+    constexpr int SLOT = NI * 8 * 64;  // 8-byte pairs per wave slot
+    const size_t split_pairs = (size_t)gridDim.x * W * SLOT;
+    const size_t slot = ((size_t)blockIdx.x * W + wave) * SLOT + (threadIdx.x & 63);
+    uint64_t* __restrict__ pairs = (uint64_t*)part;
+    auto pack = [&](int i, int r2) {
+        return (uint64_t)__float_as_uint(val(i, 2 * r2)) |
+               ((uint64_t)__float_as_uint(val(i, 2 * r2 + 1)) << 32);
+    };
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int r2 = 0; r2 < 8; ++r2)
+            __hip_atomic_store(pairs + blockIdx.y * split_pairs + slot + (i * 8 + r2) * 64,
+                               pack(i, r2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's slot stores have completed
+    __syncthreads();
+    int* last = (int*)lds;
+    if (threadIdx.x == 0) {
+        const int arrived = __hip_atomic_fetch_add(&counters[blockIdx.x], 1, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+        *last = arrived == splits - 1;
+        if (arrived == splits - 1)
+            __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!*last) return;
+    float acc[NI][16];
+    for (int sp = 0; sp < splits; ++sp) {
+        const bool own = sp == (int)blockIdx.y;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+#pragma unroll
+            for (int r2 = 0; r2 < 8; ++r2) {
+                float x0, x1;
+                if (own) {
+                    x0 = val(i, 2 * r2);
+                    x1 = val(i, 2 * r2 + 1);
+                } else {
+                    const uint64_t b = __hip_atomic_load(
+                        pairs + sp * split_pairs + slot + (i * 8 + r2) * 64, __ATOMIC_RELAXED,
+                        __HIP_MEMORY_SCOPE_AGENT);
+                    x0 = __uint_as_float((uint32_t)b);
+                    x1 = __uint_as_float((uint32_t)(b >> 32));
+                }
+                acc[i][2 * r2] = sp == 0 ? x0 : acc[i][2 * r2] + x0;
+                acc[i][2 * r2 + 1] = sp == 0 ? x1 : acc[i][2 * r2 + 1] + x1;
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int t = tok(i);
+        if (t >= m) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int j = row(i, r);
+            if (j < n) y[(size_t)t * n + j] = bias ? acc[i][r] + bias[j] : acc[i][r];
+        }
+    }
+}
+
 }  // namespace
 
 template <int W, int NT, int MT, bool Q5>
@@ -155,7 +254,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                                                       const float* __restrict__ xs,
                                                       const uint16_t* __restrict__ xq,
                                                       const float* __restrict__ bias,
-                                                      float* __restrict__ y, int split_stages) {
+                                                      float* __restrict__ y, float* __restrict__ part,
+                                                      int* __restrict__ counters, int split_stages) {
     using C = Cfg<W, NT, MT, Q5>;
     constexpr int BM = C::BM;
     constexpr int WCH = C::WROW / 16;             // 16-byte pieces per weight row and stage
@@ -180,8 +280,6 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     // slice blockIdx.y of y; a reduction adds the slices and the bias
     const int s_begin = blockIdx.y * split_stages;
     const int s_end = min(s_begin + split_stages, k / kKS);
-    const bool partial = gridDim.y > 1;
-    float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
 
     // ---- per-lane source offsets of this wave's load slots (stage 0; stages add a step) ----
     // Rows and tokens past the matrix are clamped to the last one (their results are dropped).
@@ -424,22 +522,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     }
 
     // ---- output: lane holds rows 8q + 4h + (0..3) of each tile, token column r32 ----------
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const int tok = m0 + mt * 32 + r32;
-            if (tok >= m) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = n0 + (wave * NT + t) * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < n) {
-                    float v = yacc[t][mt][r];
-                    if (bias && !partial) v += bias[row];
-                    out[(size_t)tok * n + row] = v;
-                }
-            }
-        }
+    store_tile<NT * MT, W>(
+        n, m, bias, y, part, counters, lds, wave, [&](int i, int r) { return yacc[i / MT][i % MT][r]; },
+        [&](int i) { return m0 + (i % MT) * 32 + r32; },
+        [&](int i, int r) { return n0 + (wave * NT + i / MT) * 32 + 8 * (r >> 2) + 4 * h + (r & 3); });
 }
 
 // ------------------------------------------------------------------------------------ Q6_K
@@ -485,7 +571,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
                                                       const _Float16* __restrict__ qh,
                                                       const float* __restrict__ xs,
                                                       const float* __restrict__ bias,
-                                                      float* __restrict__ y, int split_stages) {
+                                                      float* __restrict__ y, float* __restrict__ part,
+                                                      int* __restrict__ counters, int split_stages) {
     using C = Cfg6<W, MT>;
     constexpr int BM = C::BM;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -504,8 +591,6 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     const int nb = k / 32;
     const int s_begin = blockIdx.y * split_stages;
     const int s_end = min(s_begin + split_stages, k / kKS);
-    const bool partial = gridDim.y > 1;
-    float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
 
     // per-lane offsets for stage 0 (rows and tokens past the matrix are clamped to the last one)
     uint32_t a_off[C::A_SLOTS];   // bytes into qh: token, swizzled 16-byte chunk
@@ -721,20 +806,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         }
     }
 
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int tok = m0 + mt * 32 + r32;
-        if (tok >= m) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = n0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (row < n) {
-                float v = yacc[mt][r];
-                if (bias && !partial) v += bias[row];
-                out[(size_t)tok * n + row] = v;
-            }
-        }
-    }
+    store_tile<MT, W>(
+        n, m, bias, y, part, counters, lds, wave, [&](int i, int r) { return yacc[i][r]; },
+        [&](int i) { return m0 + i * 32 + r32; },
+        [&](int i, int r) { return n0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3); });
 }
 
 // ------------------------------------------------------------------ Q8_0 / Q4_0 / Q5_0
@@ -799,7 +874,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_b32(const uint8_t* __restrict_
                                                       const _Float16* __restrict__ qh,
                                                       const float* __restrict__ xs,
                                                       const float* __restrict__ bias,
-                                                      float* __restrict__ y, int split_stages) {
+                                                      float* __restrict__ y, float* __restrict__ part,
+                                                      int* __restrict__ counters, int split_stages) {
     using C = CfgB<T, W, MT>;
     constexpr int BM = C::BM;
     constexpr int BS = b32_bytes<T>();
@@ -818,8 +894,6 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_b32(const uint8_t* __restrict_
     const int nb = k / 32;
     const int s_begin = blockIdx.y * split_stages;
     const int s_end = min(s_begin + split_stages, k / kKS);
-    const bool partial = gridDim.y > 1;
-    float* __restrict__ out = y + (size_t)blockIdx.y * (size_t)m * (size_t)n;
 
     // per-lane source offsets (stage 0); rows and tokens past the matrix are clamped
     uint32_t a_off[C::A_SLOTS];
@@ -959,47 +1033,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_b32(const uint8_t* __restrict_
         for (int s = s_begin; s < s_end; ++s) run_stage(s);
     }
 
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int tok = m0 + mt * 32 + r32;
-        if (tok >= m) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = n0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (row < n) {
-                float v = yacc[mt][r];
-                if (bias && !partial) v += bias[row];
-                out[(size_t)tok * n + row] = v;
-            }
-        }
-    }
-}
-
-// y[i] = sum of the split-K slices (+ bias): total = m * n elements, four per thread when
-// n % 4 == 0 (16-byte aligned rows), else one.
-__global__ void k_split_reduce(const float* __restrict__ part, int splits, int64_t total,
-                               const float* __restrict__ bias, int n, float* __restrict__ y) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (n % 4 == 0) {
-        const int64_t i = 4 * t;
-        if (i >= total) return;
-        float4 v = *(const float4*)(part + i);
-        for (int s = 1; s < splits; ++s) {
-            const float4 u = *(const float4*)(part + (int64_t)s * total + i);
-            v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
-        }
-        if (bias) {
-            const int j = (int)(i % n);
-            v.x += bias[j]; v.y += bias[j + 1]; v.z += bias[j + 2]; v.w += bias[j + 3];
-        }
-        *(float4*)(y + i) = v;
-    } else {
-        if (t >= total) return;
-        float v = part[t];
-        for (int s = 1; s < splits; ++s) v += part[(int64_t)s * total + t];
-        if (bias) v += bias[t % n];
-        y[t] = v;
-    }
+    store_tile<MT, W>(
+        n, m, bias, y, part, counters, lds, wave, [&](int i, int r) { return yacc[i][r]; },
+        [&](int i) { return m0 + i * 32 + r32; },
+        [&](int i, int r) { return n0 + wave * 32 + 8 * (r >> 2) + 4 * h + (r & 3); });
 }
 
 bool gemmw_supported(uint32_t type) {
@@ -1081,8 +1118,8 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
 
 template <int W, int NT, int MT, bool Q5>
 hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
-                     const uint16_t* xq, const float* bias, float* out, int splits,
-                     hipStream_t stream) {
+                     const uint16_t* xq, const float* bias, float* y, float* part, int* counters,
+                     int splits, hipStream_t stream) {
     using C = Cfg<W, NT, MT, Q5>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -1096,13 +1133,14 @@ hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const _Float16* qh, 
     const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
     hipLaunchKernelGGL((k_gemmw_q4k<W, NT, MT, Q5>), dim3((unsigned)tiles, (unsigned)splits),
                        dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, xq, bias,
-                       out, per);
+                       y, part, counters, per);
     return hipGetLastError();
 }
 
 template <int W, int MT>
 hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
-                     const float* bias, float* out, int splits, hipStream_t stream) {
+                     const float* bias, float* y, float* part, int* counters, int splits,
+                     hipStream_t stream) {
     using C = Cfg6<W, MT>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -1115,14 +1153,15 @@ hipError_t launch_q6(const uint8_t* w, int k, int n, int m, const _Float16* qh, 
     const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
     const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
     hipLaunchKernelGGL((k_gemmw_q6k<W, MT>), dim3((unsigned)tiles, (unsigned)splits),
-                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, bias, out,
-                       per);
+                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, bias, y,
+                       part, counters, per);
     return hipGetLastError();
 }
 
 template <uint32_t T, int W, int MT>
 hipError_t launch_b32(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
-                      const float* bias, float* out, int splits, hipStream_t stream) {
+                      const float* bias, float* y, float* part, int* counters, int splits,
+                      hipStream_t stream) {
     using C = CfgB<T, W, MT>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -1135,16 +1174,44 @@ hipError_t launch_b32(const uint8_t* w, int k, int n, int m, const _Float16* qh,
     const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
     const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
     hipLaunchKernelGGL((k_gemmw_b32<T, W, MT>), dim3((unsigned)tiles, (unsigned)splits),
-                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, bias, out, per);
+                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, bias, y, part,
+                       counters, per);
     return hipGetLastError();
 }
 
 }  // namespace
 
+// Split-K workspace: one arrival counter per tile at its start (a fixed block of ints that must
+// be zero before the first launch; each launch leaves it zero, and no launch writes anything
+// else there whatever its shape), then the partial sums: per split, one whole tile of fp32 per
+// workgroup (rows and tokens past the matrix included).
+int64_t plan_tiles(const Plan& p, int n, int m) {
+    return (int64_t)((n + 32 * p.nt * p.wv - 1) / (32 * p.nt * p.wv)) *
+           ((m + 32 * p.mt - 1) / (32 * p.mt));
+}
+size_t slices_bytes(const Plan& p, int n, int m) {
+    const size_t tile = (size_t)(32 * p.nt * p.wv) * (size_t)(32 * p.mt) * sizeof(float);
+    return (size_t)p.splits * (size_t)plan_tiles(p, n, m) * tile;
+}
+constexpr size_t kCounterBytes = 64 * 1024;  // 16384 tiles
+
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m) {
     if (!gemmw_supported(type) || k % 256 != 0) return 0;
     const Plan p = plan_for(type, k, n, m);
-    return p.splits > 1 ? (size_t)p.splits * (size_t)m * (size_t)n * sizeof(float) : 0;
+    return p.splits > 1 ? slices_bytes(p, n, m) + kCounterBytes : 0;
+}
+
+__global__ void k_zero_words(uint32_t* __restrict__ p, size_t words) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < words) p[i] = 0;
+}
+
+hipError_t gemmw_workspace_init(void* part, size_t bytes, hipStream_t stream) {
+    const size_t words = bytes / 4;
+    if (words == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_zero_words, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                       (uint32_t*)part, words);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const float* xs,
@@ -1156,19 +1223,21 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     if (wbytes >= (1ull << 32) || 2ull * (uint64_t)m * (uint64_t)k >= (1ull << 32))
         return hipErrorNotSupported;  // the kernels index with 32-bit byte offsets
     Plan p = plan_for(type, k, n, m);
-    if (p.splits > 1 && (part == nullptr || part_bytes < (size_t)p.splits * m * n * sizeof(float)))
+    if (p.splits > 1 && (part == nullptr || part_bytes < slices_bytes(p, n, m) + kCounterBytes ||
+                         plan_tiles(p, n, m) * 4 > (int64_t)kCounterBytes))
         p.splits = 1;
-    float* out = p.splits > 1 ? part : y;
+    int* counters = p.splits > 1 ? (int*)part : nullptr;
+    part = p.splits > 1 ? (float*)((char*)part + kCounterBytes) : nullptr;
     hipError_t e = hipErrorNotSupported;
     if (type == T_Q6_K) {
-        e = launch_q6<4, 2>(w, k, n, m, qh, xs, bias, out, p.splits, stream);
+        e = launch_q6<4, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
     } else if (is_b32(type)) {
 #define CLLM_GEMMW_B32(TT)                                                                    \
         if (type == TT) {                                                                      \
             if (p.mt == 2)                                                                     \
-                e = launch_b32<TT, 4, 2>(w, k, n, m, qh, xs, bias, out, p.splits, stream);     \
+                e = launch_b32<TT, 4, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream); \
             else                                                                               \
-                e = launch_b32<TT, 4, 1>(w, k, n, m, qh, xs, bias, out, p.splits, stream);     \
+                e = launch_b32<TT, 4, 1>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream); \
         }
         CLLM_GEMMW_B32(T_Q8_0)
         CLLM_GEMMW_B32(T_Q4_0)
@@ -1177,15 +1246,15 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     } else if (type == T_Q5_K) {
         // the three shapes of the default plan (tuning overrides apply to Q4_K only)
         if (p.wv == 8 && p.nt == 1 && p.mt == 4)
-            e = launch_q4<8, 1, 4, true>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
+            e = launch_q4<8, 1, 4, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
         else if (p.wv == 8 && p.nt == 1 && p.mt == 2)
-            e = launch_q4<8, 1, 2, true>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
+            e = launch_q4<8, 1, 2, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
         else
-            e = launch_q4<4, 1, 1, true>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
+            e = launch_q4<4, 1, 1, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
     } else {
 #define CLLM_GEMMW_CASE(A, B, D)                                                              \
         if (p.wv == A && p.nt == B && p.mt == D)                                               \
-            e = launch_q4<A, B, D, false>(w, k, n, m, qh, xs, xq, bias, out, p.splits, stream);
+            e = launch_q4<A, B, D, false>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
         CLLM_GEMMW_CASE(8, 1, 4)
         CLLM_GEMMW_CASE(8, 1, 2)
         CLLM_GEMMW_CASE(8, 2, 2)
@@ -1195,12 +1264,7 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
         CLLM_GEMMW_CASE(4, 1, 1)
 #undef CLLM_GEMMW_CASE
     }
-    if (e != hipSuccess || p.splits == 1) return e;
-    const int64_t total = (int64_t)m * n;
-    const int64_t threads = n % 4 == 0 ? total / 4 : total;
-    hipLaunchKernelGGL(k_split_reduce, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                       stream, (const float*)part, p.splits, total, bias, n, y);
-    return hipGetLastError();
+    return e;
 }
 
 }  // namespace cllm_hip

@@ -60,14 +60,16 @@ hipError_t launch_gemm16(uint32_t type, const uint8_t* w, int k, int n, int m,
 
 // The weight-row fp16-MFMA GEMM (k_gemmw.hip), same contract as launch_gemm, on the activation
 // format of launch_quantize_w: dx (xs), fp16 values (qh) and, for Q4_K, the minimum operand
-// (xq). Q4_K, Q5_K and Q6_K; k % 256 == 0. When its plan splits K, it writes partial sums to part
-// (at least gemmw_partial_bytes(type, k, n, m) bytes, else K is not split) and reduces them
-// into y.
+// (xq). All six types; k % 256 == 0. When its plan splits K it needs a workspace part of at
+// least gemmw_partial_bytes(type, k, n, m) bytes (else K is not split), zeroed once by
+// gemmw_workspace_init when allocated: the splits write partial sums there and the last split
+// of each tile adds them into y inside the same launch.
 hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const float* xs,
                         const _Float16* qh, const uint16_t* xq,
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream);
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
+hipError_t gemmw_workspace_init(void* part, size_t bytes, hipStream_t stream);
 bool gemmw_supported(uint32_t type);
 
 }  // namespace cllm_hip
