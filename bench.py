@@ -113,6 +113,37 @@ def decode_point(C, S, cfg, label, m, steps, warmup, cold=True):
                 route=C.matmul_route(qt, k, n, m))
 
 
+def float_dot_points(C, S, steps, warmup):
+    """The types without vec_dot (float-dot kernels): decode GEMV at the Llama-3-8B FFN shape
+    14336 x 4096 for each type, M = 1 and 4, plus an F16 output head of Qwen2.5-0.5B's shape
+    (151936 x 896), all with rotating cold weight copies."""
+    import torch
+    out = {}
+    shapes = [(qt, 14336, 4096) for qt in S.FLOAT_DOT_TYPES] + [(S.F16, 151936, 896)]
+    for qt, n, k in shapes:
+        w = S.make_weight(qt, n, k, 5150 + qt)
+        copies = max(2, -(-ROTATE_BYTES // w.size))
+        ws = rotated_weights(w, copies)
+        for m in (1, 4):
+            x = torch.from_numpy(S.make_activation(m, k, 5151)).cuda()
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+
+            def step(i):
+                C.matmul_quant_dev(x, ws[i % copies], qt, None, k, n, y=y)
+
+            ms = time_loop(step, steps, warmup)
+            nbytes = algo_bytes(qt, n, k, m)
+            tag = f"{S.TYPE_NAMES[qt]}_{n}x{k}_m{m}"
+            out[tag] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / ms / 1e6, 1),
+                        "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                        "route": C.matmul_route(qt, k, n, m)}
+            print(f"[bench] float-dot {tag}: {ms * 1e3:.2f} us, {nbytes / ms / 1e6:.1f} GB/s",
+                  file=sys.stderr, flush=True)
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def prefill_layer(C, S, steps, warmup):
     """The Llama-3-8B layer in the Q4_K_M mix at M = 512: every matrix timed on its own
     (graph-timed, device-resident inputs), then summed."""
@@ -184,6 +215,9 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the M=512 Q4_K_M layer (for counter profiles of the GEMM) and "
                          "print its figures as one JSON line")
+    ap.add_argument("--float-dot-only", action="store_true",
+                    help="run only the float-dot types' decode GEMVs and print them as one "
+                         "JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 device copies of 64 MiB (a kernel of known traffic, for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -207,6 +241,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.float_dot_only:
+        print(json.dumps({"f3_float_dot_types": float_dot_points(C, S, max(20, args.steps // 4),
+                                                                 max(3, args.warmup // 4))}))
+        return
 
     if args.prefill_only:
         layer = prefill_layer(C, S, max(5, args.steps // 20), max(2, args.warmup // 10))
@@ -245,6 +284,8 @@ def main():
         extra["c4_m_sweep"] = sweep
         extra["c3_prefill_layer_m512"] = prefill_layer(C, S, max(5, args.steps // 20),
                                                         max(2, args.warmup // 10))
+        extra["f3_float_dot_types"] = float_dot_points(C, S, max(20, args.steps // 4),
+                                                       max(3, args.warmup // 4))
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -160,12 +160,15 @@ size_t row_bytes(uint32_t type, int in_dim) {
     return (size_t)(in_dim / block_elems(type)) * block_bytes(type);
 }
 
-// The reference's checks, in its order (quant.cpp:1376-1380 / 1441-1444, 1370).
+// The reference's checks, in its order (quant.cpp:1376-1380 / 1441-1444). Types without a
+// vec_dot kernel take the float-dot kernels (the reference's dequantize fallback,
+// 1404-1430), which fail only for an id that is no GGML type (dequantize_block, 387).
 int check_matmul(const char* who, uint32_t type, int in_dim, int out_dim) {
     const int bs = block_elems(type);
     if (bs <= 0 || in_dim <= 0 || in_dim % bs != 0)
         return set_err(CLLM_HIP_E_SHAPE, "%s: in_dim not divisible by block size", who);
-    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if (!has_kernel(type) && !gemv_f_supported(type))
+        return set_err(CLLM_HIP_E_TYPE, "unsupported ggml type for dequantize");
     if (out_dim < 0) return set_err(CLLM_HIP_E_ARG, "%s: negative out_dim", who);
     return CLLM_HIP_OK;
 }
@@ -292,6 +295,7 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
 constexpr int kFusedMaxRows = 2;
 
 bool needs_workspace(uint32_t type, int k, int m) {
+    if (!has_kernel(type)) return false;  // the float-dot kernels read fp32 rows directly
     return use_mfma(type, k, m) || m > kFusedMaxRows;
 }
 
@@ -339,7 +343,10 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
                                hipMemcpyHostToDevice, st->stream));
         bd = (const float*)st->bias.p;
     }
-    if (use_mfma(type, in_dim, n_rows)) {
+    if (!has_kernel(type)) {
+        HIP_TRY(launch_gemv_f(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
+                              (float*)st->y.p, st->stream));
+    } else if (use_mfma(type, in_dim, n_rows)) {
         HIP_TRY(run_gemm_f32(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
                              (float*)st->y.p, &st->act, st->stream));
     } else {
@@ -499,6 +506,7 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
                          const float* bias, float* y, void* stream) {
     int rc = check_matmul("matmul_quant", type, in_dim, out_dim);
     if (rc) return rc;
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
     if (n_rows <= 0 || out_dim == 0) return CLLM_HIP_OK;
     if (!w || !qs || !scales || !bsums || !y)
         return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
@@ -531,6 +539,10 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
     DeviceState* st;
     if ((rc = acquire(&st))) return rc;
     hipStream_t s = (hipStream_t)stream;
+    if (!has_kernel(type)) {
+        HIP_TRY(launch_gemv_f(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, s));
+        return CLLM_HIP_OK;
+    }
     Workspace* ws = nullptr;
     if (needs_workspace(type, in_dim, n_rows) && (rc = stream_workspace(st, s, in_dim, n_rows, &ws)))
         return rc;
@@ -545,6 +557,7 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
 
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows) {
     (void)out_dim;
+    if (gemv_f_supported(type)) return "fdot";
     if (!has_kernel(type)) return "none";
     return use_mfma(type, in_dim, n_rows) ? "mfma" : "gemv";
 }

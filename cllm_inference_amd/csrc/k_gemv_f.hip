@@ -1,0 +1,447 @@
+// k_gemv_f.hip -- float-dot GEMV for the weight types without a vec_dot kernel: F32, F16,
+// Q4_1, Q5_1, Q8_1, Q2_K and Q3_K.
+//
+// The reference routes these through the fallback of matmul_quant (src/core/quant.cpp:
+// 1404-1430; matmul_quant_batch runs it row by row, 1471-1474): each weight row is
+// dequantized to fp32 and dotted with the fp32 activation row, which is NOT quantized to
+// Q8_0. So here
+//     y[t, j] = bias[j] + sum_i x[t, i] * deq(W[j, i])
+// in fp32, with every dequantized value computed exactly as the reference's deq_* functions
+// compute it (quant.cpp:28-298: each is a product that fp32 holds exactly, or one rounding of
+// d * q + m), and one fma per element and activation row. Only the summation order differs:
+// lanes own 32-element units of a row and the partial sums are added across lanes.
+//
+// Work split. A unit is 32 consecutive elements of a row: 32 fp32 or fp16 values, one
+// Q4_1 / Q5_1 / Q8_1 block, or one eighth of a Q2_K / Q3_K super-block. A row's units are
+// spread over L lanes (L = 64, or the power of two covering the units of a short row, so a
+// wave then works on 64 / L rows at once); each lane loads the raw bytes of two units before
+// decoding the first, and many waves per CU keep the HBM stream busy.
+//
+// Activations. The MR activation rows of a workgroup's token group are staged in LDS as fp32
+// with 16 bytes of padding after every 32 values, so the 16-byte reads of the lanes (units at
+// a stride of 144 bytes) spread over all 64 banks. Rows too long for the LDS budget are read
+// from global memory instead (they stay in L2).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "device_utils.h"
+#include "ggml_blocks.h"
+#include "launch.h"
+
+namespace cllm_hip {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr size_t kLdsBudget = 64 * 1024;
+
+// byte b (0..3) of dword v as a float: v_cvt_f32_ubyte{0..3}
+__device__ __forceinline__ float ubyte_f(uint32_t v, int b) {
+    return (float)((v >> (8 * b)) & 0xFFu);
+}
+
+// ------------------------------------------------------------------------- unit decoders
+// Each FUnit<T> loads the raw bytes of unit u of a row (load) and turns them into the 32
+// fp32 weights of that unit, in element order (decode).
+
+template <uint32_t T> struct FUnit;
+
+// F32: 128 bytes (quant.cpp:29-31)
+template <> struct FUnit<T_F32> {
+    struct Raw { u32x4 v[8]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        Raw r;
+        const u32x4* p = (const u32x4*)(row + (size_t)u * 128);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.v[i] = p[i];
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            // element values are copied out first: __builtin_bit_cast applied to a vector
+            // element expression reads element 0 with this compiler
+            const uint32_t e[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) w[4 * i + c] = __builtin_bit_cast(float, e[c]);
+        }
+    }
+};
+
+// F16: 64 bytes, exact conversion (quant.cpp:34-37)
+template <> struct FUnit<T_F16> {
+    struct Raw { u32x4 v[4]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        Raw r;
+        const u32x4* p = (const u32x4*)(row + (size_t)u * 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.v[i] = p[i];
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d[4] = {r.v[i].x, r.v[i].y, r.v[i].z, r.v[i].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                w[8 * i + 2 * k] = f16_to_f32(d[k] & 0xFFFFu);
+                w[8 * i + 2 * k + 1] = f16_to_f32(d[k] >> 16);
+            }
+        }
+    }
+};
+
+// Q8_1: [d f16][s f16][qs i8 x32], 36 bytes, value d * q; s is not used (quant.cpp:203-214)
+template <> struct FUnit<T_Q8_1> {
+    struct Raw { u32x4_a4 a, b; uint32_t c; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + (size_t)u * 36;
+        Raw r;
+        r.a = *(const u32x4_a4*)p;
+        r.b = *(const u32x4_a4*)(p + 16);
+        r.c = *(const uint32_t*)(p + 32);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+        const float d = f16_to_f32(r.a.x & 0xFFFFu);
+        const uint32_t q[8] = {r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                w[4 * i + b] = d * (float)(int8_t)((q[i] >> (8 * b)) & 0xFFu);
+    }
+};
+
+// Q4_1: [d][m][qs 16 B], 20 bytes; byte j: low nibble = element j, high = element j + 16;
+// value d * q + m (quant.cpp:164-177)
+template <> struct FUnit<T_Q4_1> {
+    struct Raw { uint32_t dm; u32x4_a4 qs; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + (size_t)u * 20;
+        Raw r;
+        r.dm = *(const uint32_t*)p;
+        r.qs = *(const u32x4_a4*)(p + 4);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+        const float d = f16_to_f32(r.dm & 0xFFFFu), m = f16_to_f32(r.dm >> 16);
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = q[i] & 0x0F0F0F0Fu, hi = (q[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[4 * i + b] = __builtin_fmaf(d, ubyte_f(lo, b), m);
+                w[16 + 4 * i + b] = __builtin_fmaf(d, ubyte_f(hi, b), m);
+            }
+        }
+    }
+};
+
+// Q5_1: [d][m][qh u32][qs 16 B], 24 bytes; bit j of qh is bit 4 of element j
+// (quant.cpp:182-200)
+template <> struct FUnit<T_Q5_1> {
+    struct Raw { u32x2_a4 dmh; u32x4_a4 qs; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* p = row + (size_t)u * 24;
+        Raw r;
+        r.dmh = *(const u32x2_a4*)p;
+        r.qs = *(const u32x4_a4*)(p + 8);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+        const float d = f16_to_f32(r.dmh.x & 0xFFFFu), m = f16_to_f32(r.dmh.x >> 16);
+        const uint32_t qh = r.dmh.y;
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // bit 4 of elements 4i..4i+3 and 16+4i..: qh bits 4i.. and 16+4i.. moved to bit 4
+            // of each byte
+            const uint32_t h0 = (qh >> (4 * i)) & 0xFu, h1 = (qh >> (16 + 4 * i)) & 0xFu;
+            const uint32_t s0 = ((h0 & 1u) | ((h0 & 2u) << 7) | ((h0 & 4u) << 14) | ((h0 & 8u) << 21)) << 4;
+            const uint32_t s1 = ((h1 & 1u) | ((h1 & 2u) << 7) | ((h1 & 4u) << 14) | ((h1 & 8u) << 21)) << 4;
+            const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | s0, hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | s1;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[4 * i + b] = __builtin_fmaf(d, ubyte_f(lo, b), m);
+                w[16 + 4 * i + b] = __builtin_fmaf(d, ubyte_f(hi, b), m);
+            }
+        }
+    }
+};
+
+// Q2_K: [scales 16][qs 64][d][dmin], 84 bytes. Unit v = 4 h + j of a super-block: elements
+// 32 v + l take bits 2j..2j+1 of qs[32 h + l], with scale byte 8 h + 2 j for l < 16 and
+// 8 h + 2 j + 1 for l >= 16 (low nibble scale, high nibble min); value
+// d * sc * q - dmin * m (quant.cpp:218-248).
+template <> struct FUnit<T_Q2_K> {
+    struct Raw { u32x4_a4 q0, q1; uint32_t sc; uint32_t dd; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 3) * 84;
+        const int v = u & 7, h = v >> 2, j = v & 3;
+        Raw r;
+        r.q0 = *(const u32x4_a4*)(blk + 16 + 32 * h);
+        r.q1 = *(const u32x4_a4*)(blk + 32 + 32 * h);
+        r.sc = ld_u16(blk + 8 * h + 2 * j);
+        r.dd = *(const uint32_t*)(blk + 80);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int u, float (&w)[32]) {
+        const int sh = 2 * (u & 3);
+        const float d = f16_to_f32(r.dd & 0xFFFFu), dmin = f16_to_f32(r.dd >> 16);
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t scb = (r.sc >> (8 * g)) & 0xFFu;
+            const float dl = d * (float)(scb & 0xFu), ml = dmin * (float)(scb >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t v = (q[4 * g + i] >> sh) & 0x03030303u;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w[16 * g + 4 * i + b] = __builtin_fmaf(dl, ubyte_f(v, b), -ml);
+            }
+        }
+    }
+};
+
+// Q3_K: [hmask 32][qs 64][scales 12][d], 110 bytes (2-byte aligned blocks). Unit v = 4 h + j:
+// elements 32 v + l take bits 2j..2j+1 of qs[32 h + l] minus 4 unless bit 4h + j of
+// hmask[l] is set, with the signed 6-bit scale 8 h + 2 j (l < 16) or 8 h + 2 j + 1 (l >= 16);
+// value d * (scale - 32) * q (quant.cpp:252-298).
+template <> struct FUnit<T_Q3_K> {
+    struct Raw { uint32_t hm[8], q[8], sc[3], d; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 3) * 110;
+        const int h = (u & 7) >> 2;
+        Raw r;
+        ld_a2<8>(blk, r.hm);
+        ld_a2<8>(blk + 32 + 32 * h, r.q);
+        ld_a2<3>(blk + 96, r.sc);
+        r.d = ld_u16(blk + 108);
+        return r;
+    }
+    // Scale i (0..15) of the 12 packed bytes b (as dwords s[0..2]): low four bits from byte
+    // i (i < 8, low nibble) or byte i - 8 (i >= 8, high nibble), top two bits from byte
+    // 8 + i % 4 at bit 2 (i / 4) (the aux shuffle of quant.cpp:259-265).
+    __device__ __forceinline__ static int scale(const uint32_t (&s)[3], int i) {
+        const int grp = i >> 2, ii = i & 3;
+        // bytes 0-7 as one 64-bit value, shifted (an indexed pick of s[0] / s[1] would be
+        // lowered to a scratch-memory load)
+        const uint64_t s01 = (uint64_t)s[0] | ((uint64_t)s[1] << 32);
+        const uint32_t src = (uint32_t)(s01 >> (32 * (grp & 1) + 8 * ii));
+        const uint32_t lo = (grp < 2 ? src : src >> 4) & 0xFu;
+        const uint32_t hi = (s[2] >> (8 * ii + 2 * grp)) & 3u;
+        return (int)(lo | (hi << 4)) - 32;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int u, float (&w)[32]) {
+        const int v = u & 7, h = v >> 2, j = v & 3;
+        const float d = f16_to_f32(r.d);
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const float dl = d * (float)scale(r.sc, 8 * h + 2 * j + g);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // q2 | hbit << 2 per byte, so value = byte - 4
+                const uint32_t q2 = (r.q[4 * g + i] >> (2 * j)) & 0x03030303u;
+                const uint32_t hb = ((r.hm[4 * g + i] >> (4 * h + j)) & 0x01010101u) << 2;
+                const uint32_t qv = q2 | hb;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w[16 * g + 4 * i + b] = dl * (ubyte_f(qv, b) - 4.0f);
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------------------ kernel
+
+__host__ __device__ constexpr int xpad_row(int k) { return k + k / 8; }  // floats per LDS row
+
+template <int MR>
+__device__ __forceinline__ void fma_unit(const float (&w)[32], const float* xp, int xstride,
+                                         float (&acc)[MR]) {
+#pragma unroll
+    for (int t = 0; t < MR; ++t) {
+        const float4* p = (const float4*)(xp + (size_t)t * xstride);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 xv = p[q];
+            acc[t] = __builtin_fmaf(xv.x, w[4 * q], acc[t]);
+            acc[t] = __builtin_fmaf(xv.y, w[4 * q + 1], acc[t]);
+            acc[t] = __builtin_fmaf(xv.z, w[4 * q + 2], acc[t]);
+            acc[t] = __builtin_fmaf(xv.w, w[4 * q + 3], acc[t]);
+        }
+    }
+}
+
+// grid (row workgroups, token groups of MR), 256 threads. lpr_log2 = log2(lanes per row).
+template <uint32_t T, int MR, bool XG>
+__global__ __launch_bounds__(kThreads) void k_gemv_f(const uint8_t* __restrict__ w,
+                                                     size_t row_bytes, int k, int n, int m,
+                                                     const float* __restrict__ x,
+                                                     const float* __restrict__ bias,
+                                                     float* __restrict__ y, int lpr_log2) {
+    using U = FUnit<T>;
+    extern __shared__ __align__(16) float xs[];
+    const int t0 = blockIdx.y * MR;
+    const int units = k / 32;
+    const int srow = xpad_row(k);
+    if constexpr (!XG) {
+        // stage the token group's rows (zeros past m) with the 16-byte pad per 32 values
+        const int q4 = k / 4;
+        for (int i = threadIdx.x; i < MR * q4; i += kThreads) {
+            const int t = i / q4, e = 4 * (i - t * q4);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t0 + t < m) v = *(const float4*)(x + (size_t)(t0 + t) * k + e);
+            *(float4*)(xs + t * srow + e + (e >> 5) * 4) = v;
+        }
+        __syncthreads();
+    }
+    const int lane = threadIdx.x & 63;
+    const int lpr = 1 << lpr_log2;
+    const int sub = lane & (lpr - 1);
+    const int rpw = 64 >> lpr_log2;  // rows per wave
+    const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int nw = gridDim.x * kWaves;
+    // activation source: LDS rows, or global rows clamped to the last valid one
+    const float* xbase = XG ? x + (size_t)min(t0, m - 1) * k : xs;
+    const int xstride = XG ? k : srow;
+    auto xptr = [&](int u) { return XG ? xbase + 32 * u : xbase + 36 * u; };
+
+    for (int rb = gw * rpw; rb < n; rb += nw * rpw) {
+        const int j = rb + (lane >> lpr_log2);
+        const uint8_t* row = w + (size_t)min(j, n - 1) * row_bytes;
+        float acc[MR];
+#pragma unroll
+        for (int t = 0; t < MR; ++t) acc[t] = 0.0f;
+        for (int u = sub; u < units; u += 2 * lpr) {
+            const bool two = u + lpr < units;
+            const typename U::Raw r0 = U::load(row, u);
+            const typename U::Raw r1 = U::load(row, two ? u + lpr : u);
+            float wv[32];
+            U::decode(r0, u, wv);
+            fma_unit<MR>(wv, xptr(u), xstride, acc);
+            if (two) {
+                U::decode(r1, u + lpr, wv);
+                fma_unit<MR>(wv, xptr(u + lpr), xstride, acc);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MR; ++t)
+            for (int off = lpr >> 1; off > 0; off >>= 1) acc[t] += __shfl_xor(acc[t], off, 64);
+        if (sub == 0 && j < n) {
+            const float b = bias ? bias[j] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < MR; ++t)
+                if (t0 + t < m) y[(size_t)(t0 + t) * n + j] = acc[t] + b;
+        }
+    }
+}
+
+// F32 / F16 rows whose length is not a multiple of 32: one wave per row, lanes stride over
+// the elements, activations from global memory, every token of the batch in turn.
+template <uint32_t T>
+__global__ __launch_bounds__(kThreads) void k_gemv_f_any(const uint8_t* __restrict__ w,
+                                                         size_t row_bytes, int k, int n, int m,
+                                                         const float* __restrict__ x,
+                                                         const float* __restrict__ bias,
+                                                         float* __restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int nw = gridDim.x * kWaves;
+    for (int j = gw; j < n; j += nw) {
+        const uint8_t* row = w + (size_t)j * row_bytes;
+        for (int t = 0; t < m; ++t) {
+            const float* xt = x + (size_t)t * k;
+            float acc = 0.0f;
+            for (int e = lane; e < k; e += 64) {
+                const float wv = T == T_F32 ? ((const float*)row)[e]
+                                            : f16_to_f32(((const uint16_t*)row)[e]);
+                acc = __builtin_fmaf(xt[e], wv, acc);
+            }
+            acc = wave_sum(acc);
+            if (lane == 0) y[(size_t)t * n + j] = acc + (bias ? bias[j] : 0.0f);
+        }
+    }
+}
+
+int device_cus_f() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            cus = v;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+template <uint32_t T, int MR, bool XG>
+hipError_t launch_mr(const uint8_t* w, size_t row_bytes, int k, int n, int m, const float* x,
+                     const float* bias, float* y, hipStream_t stream) {
+    const int units = k / 32;
+    int lpr_log2 = 6;
+    while (lpr_log2 > 0 && (1 << (lpr_log2 - 1)) >= units) --lpr_log2;
+    const int rpw = 64 >> lpr_log2;
+    const int64_t row_groups = ((int64_t)n + rpw - 1) / rpw;
+    const int64_t wgs = std::min<int64_t>((row_groups + kWaves - 1) / kWaves,
+                                          (int64_t)device_cus_f() * 8);
+    const int groups = (m + MR - 1) / MR;
+    if (groups > 65535) return hipErrorInvalidConfiguration;
+    const size_t lds = XG ? 0 : (size_t)MR * xpad_row(k) * sizeof(float);
+    hipLaunchKernelGGL((k_gemv_f<T, MR, XG>), dim3((unsigned)wgs, (unsigned)groups),
+                       dim3(kThreads), lds, stream, w, row_bytes, k, n, m, x, bias, y, lpr_log2);
+    return hipGetLastError();
+}
+
+template <uint32_t T>
+hipError_t launch_type(const uint8_t* w, int k, int n, int m, const float* x, const float* bias,
+                       float* y, hipStream_t stream) {
+    const size_t row_bytes = (size_t)(k / block_elems(T)) * block_bytes(T);
+    if constexpr (T == T_F32 || T == T_F16) {
+        if (k % 32 != 0) {
+            const int64_t wgs = std::min<int64_t>(((int64_t)n + kWaves - 1) / kWaves,
+                                                  (int64_t)device_cus_f() * 8);
+            hipLaunchKernelGGL((k_gemv_f_any<T>), dim3((unsigned)wgs), dim3(kThreads), 0, stream,
+                               w, row_bytes, k, n, m, x, bias, y);
+            return hipGetLastError();
+        }
+    }
+    const size_t row_lds = (size_t)xpad_row(k) * sizeof(float);
+    if (m >= 3 && 4 * row_lds <= kLdsBudget)
+        return launch_mr<T, 4, false>(w, row_bytes, k, n, m, x, bias, y, stream);
+    if (m >= 2 && 2 * row_lds <= kLdsBudget)
+        return launch_mr<T, 2, false>(w, row_bytes, k, n, m, x, bias, y, stream);
+    if (row_lds <= kLdsBudget)
+        return launch_mr<T, 1, false>(w, row_bytes, k, n, m, x, bias, y, stream);
+    if (m >= 3) return launch_mr<T, 4, true>(w, row_bytes, k, n, m, x, bias, y, stream);
+    return launch_mr<T, 1, true>(w, row_bytes, k, n, m, x, bias, y, stream);
+}
+
+}  // namespace
+
+bool gemv_f_supported(uint32_t type) {
+    return type == T_F32 || type == T_F16 || type == T_Q4_1 || type == T_Q5_1 ||
+           type == T_Q8_1 || type == T_Q2_K || type == T_Q3_K;
+}
+
+hipError_t launch_gemv_f(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
+                         const float* bias, float* y, hipStream_t stream) {
+    if (n <= 0 || m <= 0) return hipSuccess;
+    if (k <= 0 || k % block_elems(type) != 0) return hipErrorInvalidValue;
+    switch (type) {
+        case T_F32: return launch_type<T_F32>(w, k, n, m, x, bias, y, stream);
+        case T_F16: return launch_type<T_F16>(w, k, n, m, x, bias, y, stream);
+        case T_Q4_1: return launch_type<T_Q4_1>(w, k, n, m, x, bias, y, stream);
+        case T_Q5_1: return launch_type<T_Q5_1>(w, k, n, m, x, bias, y, stream);
+        case T_Q8_1: return launch_type<T_Q8_1>(w, k, n, m, x, bias, y, stream);
+        case T_Q2_K: return launch_type<T_Q2_K>(w, k, n, m, x, bias, y, stream);
+        case T_Q3_K: return launch_type<T_Q3_K>(w, k, n, m, x, bias, y, stream);
+        default: return hipErrorNotSupported;
+    }
+}
+
+}  // namespace cllm_hip

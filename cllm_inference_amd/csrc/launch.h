@@ -69,6 +69,13 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream);
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
+
+// Float-dot GEMV (k_gemv_f.hip) for the types without a vec_dot kernel (F32, F16, Q4_1,
+// Q5_1, Q8_1, Q2_K, Q3_K): y[t, j] = bias[j] + sum_i x[t, i] * deq(W[j, i]) on fp32
+// activation rows x[m][k], as the reference's dequantize fallback computes it.
+bool gemv_f_supported(uint32_t type);
+hipError_t launch_gemv_f(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
+                         const float* bias, float* y, hipStream_t stream);
 hipError_t gemmw_workspace_init(void* part, size_t bytes, hipStream_t stream);
 bool gemmw_supported(uint32_t type);
 

@@ -14,13 +14,21 @@ import numpy as np
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K = (
     0, 1, 2, 3, 6, 7, 8, 9, 10, 11, 12, 13, 14)
 
-TYPE_NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K",
-              Q6_K: "Q6_K"}
+TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1",
+              Q8_0: "Q8_0", Q8_1: "Q8_1", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K",
+              Q5_K: "Q5_K", Q6_K: "Q6_K"}
 NAME_TO_TYPE = {v: k for k, v in TYPE_NAMES.items()}
 
+# The six types with a vec_dot kernel (src/core/quant.cpp:1347-1357); the others take the
+# reference's dequantize-and-float-dot fallback (1404-1430).
+VEC_DOT_TYPES = (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K)
+FLOAT_DOT_TYPES = (F32, F16, Q4_1, Q5_1, Q8_1, Q2_K, Q3_K)
+
 # elements per block and bytes per block, src/core/quant.cpp:340-369
-BLOCK = {Q4_0: 32, Q5_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-TYPE_SIZE = {Q4_0: 18, Q5_0: 22, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLOCK = {F32: 1, F16: 1, Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32, Q8_1: 32,
+         Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+TYPE_SIZE = {F32: 4, F16: 2, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34, Q8_1: 36,
+             Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 
 
 def row_bytes(qtype: int, k: int) -> int:
@@ -43,6 +51,11 @@ def make_weight(qtype: int, n: int, k: int, seed: int) -> np.ndarray:
             scale and min then decodes uniform on [0, 63]), qs random bytes
       Q5_K: as Q4_K plus 32 random qh bytes
       Q6_K: ql, qh random bytes, sc int8 ~ U[-32, 31], d ~ U(1e-3, 1e-2)
+      F32, F16: values ~ N(0, 0.02)
+      Q4_1, Q5_1: d ~ U(0.002, 0.02), m ~ U(-0.15, -0.01), qh and qs random bytes
+      Q8_1: d ~ U(0.002, 0.02), s = d * (sum of the block's qs) as fp16, qs ~ U[-127, 127]
+      Q2_K: 16 random scale bytes, qs random, d ~ U(1e-3, 1e-2), dmin ~ U(1e-4, 1e-3)
+      Q3_K: hmask, qs and the 12 scale bytes random, d ~ U(1e-3, 1e-2)
     """
     if k % BLOCK[qtype]:
         raise ValueError("k must be a multiple of the block size")
@@ -62,8 +75,28 @@ def make_weight(qtype: int, n: int, k: int, seed: int) -> np.ndarray:
     elif qtype == Q6_K:
         blk[:, 192:208] = rng.integers(-32, 32, size=(nblk, 16), dtype=np.int8).view(np.uint8)
         blk[:, 208:210] = _f16_bytes(rng, nblk, 1e-3, 1e-2)
+    elif qtype == F32:
+        raw[:] = (rng.standard_normal(nblk, dtype=np.float32) * np.float32(0.02)).view(np.uint8)
+    elif qtype == F16:
+        raw[:] = (rng.standard_normal(nblk, dtype=np.float32) * np.float32(0.02)).astype(
+            np.float16).view(np.uint8)
+    elif qtype in (Q4_1, Q5_1):
+        blk[:, 0:2] = _f16_bytes(rng, nblk, 0.002, 0.02)
+        blk[:, 2:4] = _f16_bytes(rng, nblk, -0.15, -0.01)
+    elif qtype == Q8_1:
+        d = rng.uniform(0.002, 0.02, size=nblk).astype(np.float16)
+        q = rng.integers(-127, 128, size=(nblk, 32), dtype=np.int8)
+        blk[:, 0:2] = d.view(np.uint8).reshape(nblk, 2)
+        blk[:, 2:4] = (d.astype(np.float32) * q.sum(axis=1, dtype=np.int32)).astype(
+            np.float16).view(np.uint8).reshape(nblk, 2)
+        blk[:, 4:36] = q.view(np.uint8)
+    elif qtype == Q2_K:
+        blk[:, 80:82] = _f16_bytes(rng, nblk, 1e-3, 1e-2)
+        blk[:, 82:84] = _f16_bytes(rng, nblk, 1e-4, 1e-3)
+    elif qtype == Q3_K:
+        blk[:, 108:110] = _f16_bytes(rng, nblk, 1e-3, 1e-2)
     else:
-        raise ValueError(f"no vec_dot kernel for type {qtype}")
+        raise ValueError(f"unknown ggml type {qtype}")
     return raw
 
 

@@ -8,10 +8,10 @@
 //
 // Differences a caller can observe:
 //   - The ThreadPool* argument is accepted and ignored; the GPU grid replaces the pool.
-//   - Only the six types with a vec_dot kernel (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K) are
-//     computed. matmul_quant / matmul_quant_batch on other types throw std::runtime_error
-//     instead of taking the reference's dequantize-and-float-dot fallback, which has no GPU
-//     kernel here. dequantize_block / dequantize_block_f16 are not part of this library.
+//   - All thirteen types are computed on the GPU: the six with a vec_dot kernel (Q4_0, Q5_0,
+//     Q8_0, Q4_K, Q5_K, Q6_K) on Q8_0 activations, the others (F32, F16, Q4_1, Q5_1, Q8_1,
+//     Q2_K, Q3_K) as the reference's dequantize-and-float-dot fallback, on fp32 activations.
+//     dequantize_block / dequantize_block_f16 are not part of this library.
 //   - Failures of the GPU runtime also surface as std::runtime_error.
 #pragma once
 

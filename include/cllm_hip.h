@@ -12,8 +12,12 @@
  *     of the last failure on the calling thread is returned by cllm_hip_last_error(). The
  *     messages of the reference's exceptions are reproduced verbatim where one exists.
  *   - "type" is a GgmlType id (F32 = 0 ... Q6_K = 14, include/cllm/core/quant.hpp:13-27).
- *     Only the six types with a vec_dot kernel in the reference (Q4_0, Q5_0, Q8_0, Q4_K,
- *     Q5_K, Q6_K; src/core/quant.cpp:1347-1357) have GPU kernels here.
+ *     The six types with a vec_dot kernel in the reference (Q4_0, Q5_0, Q8_0, Q4_K, Q5_K,
+ *     Q6_K; src/core/quant.cpp:1347-1357) are computed on Q8_0-quantized activations, like
+ *     the reference's fast path; the other seven (F32, F16, Q4_1, Q5_1, Q8_1, Q2_K, Q3_K) on
+ *     the fp32 activations, like its dequantize-and-float-dot fallback (1404-1430). The
+ *     vec_dot and Q8_0 entry points (cllm_hip_vec_dot_rows, cllm_hip_gemv_q8_dev) take
+ *     the six types only.
  *   - Weights are GGUF blocks read in place, row-major: out_dim rows of
  *     (in_dim / block_size) * type_size bytes (src/core/quant.cpp:1381).
  *   - Functions without the _dev suffix take host pointers and are synchronous, like the
@@ -100,14 +104,15 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
                          const int8_t* qs, const float* scales, const int32_t* bsums,
                          const float* bias, float* y, void* stream);
 
-/* matmul_quant_batch on device buffers. Small n_rows: one GEMV launch that quantizes its
- * activation rows itself. Large n_rows: quantizes x into a library-owned per-stream
- * workspace, then runs the MFMA GEMM. */
+/* matmul_quant_batch on device buffers. vec_dot types, small n_rows: one GEMV launch that
+ * quantizes its activation rows itself; large n_rows: quantizes x into a library-owned
+ * per-stream workspace, then runs the MFMA GEMM. Other types: the float-dot GEMV on x. */
 int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,
                               int in_dim, int out_dim, int n_rows, float* y, void* stream);
 
-/* Name of the kernel family cllm_hip_matmul_quant_dev would run for this shape
- * ("gemv" or "mfma"); for tests and benchmarks. */
+/* Name of the kernel family cllm_hip_matmul_quant_dev would run for this shape: "gemv" or
+ * "mfma" (vec_dot types), "fdot" (the float-dot kernels of the other types), "none" (no
+ * GGML type); for tests and benchmarks. */
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows);
 
 #ifdef __cplusplus

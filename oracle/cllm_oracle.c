@@ -120,15 +120,103 @@ static inline void scale_min_k4(int j, const uint8_t* q, int* sc, int* m) {
 }
 
 /* ---- dequantization: the layout oracle ------------------------------------------------- */
+static int known_type(uint32_t t) { return oracle_type_size(t) != 0; }
+
+/* 16 signed 6-bit Q3_K scales (value - 32) from the 12 packed bytes: scale i takes its low
+ * four bits from byte i (i < 8, low nibble) or byte i - 8 (i >= 8, high nibble) and its top
+ * two bits from byte 8 + i % 4, at bit 2 * (i / 4) (src/core/quant.cpp:259-265). */
+static void q3_k_scales(const uint8_t* b, int* out) {
+    for (int i = 0; i < 16; ++i) {
+        const int grp = i / 4, ii = i % 4;
+        const int lo = grp < 2 ? (b[4 * grp + ii] & 0x0F) : (b[4 * (grp - 2) + ii] >> 4);
+        const int hi = (b[8 + ii] >> (2 * grp)) & 3;
+        out[i] = (lo | (hi << 4)) - 32;
+    }
+}
+
 int oracle_dequantize(const void* src, float* dst, uint32_t t, int64_t n) {
     const uint8_t* s = (const uint8_t*)src;
     const int bs = oracle_block_size(t);
-    if (!oracle_has_vec_dot(t)) return fail(ORACLE_ERR_TYPE, "unsupported ggml type for dequantize");
+    if (!known_type(t)) return fail(ORACLE_ERR_TYPE, "unsupported ggml type for dequantize");
     if (n % bs != 0) return fail(ORACLE_ERR_SHAPE, "dequantize: n not a multiple of the block size");
     const int64_t nb = n / bs;
     for (int64_t b = 0; b < nb; ++b) {
         float* o = dst + b * bs;
         switch (t) {
+            case ORACLE_F32: /* quant.cpp:29-31 */
+                memcpy(o, s, 4);
+                s += 4;
+                break;
+            case ORACLE_F16: /* quant.cpp:34-37 */
+                o[0] = ld_f16(s);
+                s += 2;
+                break;
+            case ORACLE_Q8_1: { /* [d f16][s f16][qs i8 x32], value = d*q (quant.cpp:203-214) */
+                const float d = ld_f16(s);
+                for (int j = 0; j < 32; ++j) o[j] = d * (float)(int8_t)s[4 + j];
+                s += 36;
+                break;
+            }
+            case ORACLE_Q4_1: { /* [d][m][16 B], value = d*q + m (quant.cpp:164-177) */
+                const float d = ld_f16(s), m = ld_f16(s + 2);
+                for (int j = 0; j < 16; ++j) {
+                    o[j] = d * (float)(s[4 + j] & 0x0F) + m;
+                    o[j + 16] = d * (float)(s[4 + j] >> 4) + m;
+                }
+                s += 20;
+                break;
+            }
+            case ORACLE_Q5_1: { /* [d][m][qh u32 LE][qs 16 B] (quant.cpp:182-200) */
+                const float d = ld_f16(s), m = ld_f16(s + 2);
+                const uint32_t qh = (uint32_t)s[4] | ((uint32_t)s[5] << 8) |
+                                    ((uint32_t)s[6] << 16) | ((uint32_t)s[7] << 24);
+                for (int j = 0; j < 16; ++j) {
+                    const int q0 = (s[8 + j] & 0x0F) | (int)(((qh >> j) & 1u) << 4);
+                    const int q1 = (s[8 + j] >> 4) | (int)(((qh >> (j + 16)) & 1u) << 4);
+                    o[j] = d * (float)q0 + m;
+                    o[j + 16] = d * (float)q1 + m;
+                }
+                s += 24;
+                break;
+            }
+            case ORACLE_Q2_K: { /* [scales 16][qs 64][d][dmin] (quant.cpp:218-248) */
+                const uint8_t* sc = s;
+                const float d = ld_f16(s + 80), dmin = ld_f16(s + 82);
+                /* 32-element group u = 4 h + j of half h: qs[32 h + l] >> 2 j, scale bytes
+                 * 8 h + 2 j (elements 0-15) and 8 h + 2 j + 1 (16-31) */
+                for (int u = 0; u < 8; ++u) {
+                    const int h = u / 4, j = u % 4;
+                    for (int half16 = 0; half16 < 2; ++half16) {
+                        const uint8_t scb = sc[8 * h + 2 * j + half16];
+                        const float dl = d * (float)(scb & 0x0F), ml = dmin * (float)(scb >> 4);
+                        for (int l = 0; l < 16; ++l) {
+                            const int q = (s[16 + 32 * h + 16 * half16 + l] >> (2 * j)) & 3;
+                            o[32 * u + 16 * half16 + l] = dl * (float)q - ml;
+                        }
+                    }
+                }
+                s += 84;
+                break;
+            }
+            case ORACLE_Q3_K: { /* [hmask 32][qs 64][scales 12][d] (quant.cpp:252-298) */
+                int scv[16];
+                q3_k_scales(s + 96, scv);
+                const float d = ld_f16(s + 108);
+                for (int u = 0; u < 8; ++u) {
+                    const int h = u / 4, j = u % 4;
+                    const int mbit = 1 << (4 * h + j);
+                    for (int half16 = 0; half16 < 2; ++half16) {
+                        const float dl = d * (float)scv[8 * h + 2 * j + half16];
+                        for (int l = 0; l < 16; ++l) {
+                            const int e = 16 * half16 + l;
+                            const int q = ((s[32 + 32 * h + e] >> (2 * j)) & 3) - ((s[e] & mbit) ? 0 : 4);
+                            o[32 * u + e] = dl * (float)q;
+                        }
+                    }
+                }
+                s += 110;
+                break;
+            }
             case ORACLE_Q8_0: { /* [d f16][qs i8 x32], value = d*q */
                 const float d = ld_f16(s);
                 for (int j = 0; j < 32; ++j) o[j] = d * (float)(int8_t)s[2 + j];
@@ -428,9 +516,37 @@ typedef struct {
     const float* bias;
     float* y;
     size_t j0, j1;
+    const float* x;  /* fp32 activations (types without vec_dot) */
+    float* buf;      /* per-job dequantization chunk (types without vec_dot) */
 } job_t;
 
+/* Types without a vec_dot kernel (src/core/quant.cpp:1404-1430): the row is dequantized in
+ * chunks of (512 / bs) * bs elements and accumulated in order into acc, which starts at the
+ * bias; clang contracts "acc += xp[i] * buf[i]" into one fma per element. */
+static void run_rows_float(const job_t* jb) {
+    const int bs = oracle_block_size(jb->type);
+    const int chunk = (512 / bs) * bs;
+    const size_t ts = oracle_type_size(jb->type);
+    for (size_t j = jb->j0; j < jb->j1; ++j) {
+        const uint8_t* rp = jb->w + j * jb->row_bytes;
+        for (int t = 0; t < jb->n_rows; ++t) {
+            const float* x = jb->x + (size_t)t * jb->in_dim;
+            float acc = jb->bias ? jb->bias[j] : 0.0f;
+            for (int off = 0; off < jb->in_dim; off += chunk) {
+                const int len = jb->in_dim - off < chunk ? jb->in_dim - off : chunk;
+                oracle_dequantize(rp + (size_t)(off / bs) * ts, jb->buf, jb->type, len);
+                for (int i = 0; i < len; ++i) acc = fmaf(x[off + i], jb->buf[i], acc);
+            }
+            jb->y[(size_t)t * jb->out_dim + j] = acc;
+        }
+    }
+}
+
 static void run_rows(const job_t* jb) {
+    if (jb->x) {
+        run_rows_float(jb);
+        return;
+    }
     const int nb = jb->in_dim / 32;
     for (size_t j = jb->j0; j < jb->j1; ++j) {
         const uint8_t* rp = jb->w + j * jb->row_bytes;
@@ -451,10 +567,15 @@ static void* run_rows_thread(void* p) {
 
 static int run_all(job_t base, int n_threads) {
     const size_t total = (size_t)base.out_dim;
+    const int chunk_floats = 512;
     if (n_threads <= 1 || base.out_dim < 256) {
         base.j0 = 0;
         base.j1 = total;
+        float* buf = base.x ? (float*)malloc(sizeof(float) * chunk_floats) : NULL;
+        if (base.x && !buf) return fail(ORACLE_ERR_SYS, "out of memory");
+        base.buf = buf;
         run_rows(&base);
+        free(buf);
         return ORACLE_OK;
     }
     /* chunk = ceil(total / workers); one task per chunk */
@@ -462,20 +583,24 @@ static int run_all(job_t base, int n_threads) {
     const size_t n_chunks = (total + chunk - 1) / chunk;
     job_t* jobs = (job_t*)calloc(n_chunks, sizeof(job_t));
     pthread_t* th = (pthread_t*)calloc(n_chunks, sizeof(pthread_t));
-    if (!jobs || !th) {
+    float* bufs = base.x ? (float*)malloc(sizeof(float) * chunk_floats * n_chunks) : NULL;
+    if (!jobs || !th || (base.x && !bufs)) {
         free(jobs);
         free(th);
+        free(bufs);
         return fail(ORACLE_ERR_SYS, "out of memory");
     }
     for (size_t c = 0; c < n_chunks; ++c) {
         jobs[c] = base;
         jobs[c].j0 = c * chunk;
         jobs[c].j1 = (c + 1) * chunk < total ? (c + 1) * chunk : total;
+        jobs[c].buf = bufs ? bufs + c * chunk_floats : NULL;
         pthread_create(&th[c], NULL, run_rows_thread, &jobs[c]);
     }
     for (size_t c = 0; c < n_chunks; ++c) pthread_join(th[c], NULL);
     free(jobs);
     free(th);
+    free(bufs);
     return ORACLE_OK;
 }
 
@@ -503,7 +628,26 @@ static int matmul_impl(const char* who, const float* x, const void* w, uint32_t 
         snprintf(msg, sizeof msg, "%s: in_dim not divisible by block size", who);
         return fail(ORACLE_ERR_SHAPE, msg);
     }
-    if (!oracle_has_vec_dot(type)) return fail(ORACLE_ERR_TYPE, "vec_dot_row: no kernel for this type");
+    if (!oracle_has_vec_dot(type)) {
+        /* quant.cpp:1404-1430 (matmul_quant_batch runs it row by row, 1471-1474) */
+        if (!known_type(type)) {
+            if (out_dim > 0 && in_dim > 0)
+                return fail(ORACLE_ERR_TYPE, "unsupported ggml type for dequantize");
+            return ORACLE_OK;
+        }
+        job_t jb;
+        memset(&jb, 0, sizeof jb);
+        jb.w = (const uint8_t*)w;
+        jb.type = type;
+        jb.row_bytes = (size_t)(in_dim / bs) * oracle_type_size(type);
+        jb.in_dim = in_dim;
+        jb.out_dim = out_dim;
+        jb.n_rows = n_rows;
+        jb.bias = bias;
+        jb.y = y;
+        jb.x = x;
+        return run_all(jb, n_threads);
+    }
     int8_t* qs = NULL;
     float* sc = NULL;
     int32_t* bsum = NULL;
@@ -626,8 +770,30 @@ int oracle_matmul_quant_f64(const float* x, const void* w, uint32_t type, const 
                             int in_dim, int out_dim, int n_rows, double* y, double* abs_sum) {
     const int bs = oracle_block_size(type);
     if (bs <= 0 || in_dim % bs != 0) return fail(ORACLE_ERR_SHAPE, "matmul_quant: in_dim not divisible by block size");
-    if (!oracle_has_vec_dot(type)) return fail(ORACLE_ERR_TYPE, "vec_dot_row: no kernel for this type");
+    if (!known_type(type)) return fail(ORACLE_ERR_TYPE, "unsupported ggml type for dequantize");
     if (n_rows <= 0) return ORACLE_OK;
+    if (!oracle_has_vec_dot(type)) {
+        /* dequantized fp32 weights times fp32 activations, summed exactly in fp64 */
+        const size_t rb = (size_t)(in_dim / bs) * oracle_type_size(type);
+        float* wrow = (float*)malloc(sizeof(float) * (size_t)in_dim);
+        if (!wrow) return fail(ORACLE_ERR_SYS, "out of memory");
+        for (int j = 0; j < out_dim; ++j) {
+            oracle_dequantize((const uint8_t*)w + (size_t)j * rb, wrow, type, in_dim);
+            for (int t = 0; t < n_rows; ++t) {
+                const float* xt = x + (size_t)t * in_dim;
+                double acc = bias ? (double)bias[j] : 0.0, aab = bias ? fabs((double)bias[j]) : 0.0;
+                for (int i = 0; i < in_dim; ++i) {
+                    const double p = (double)xt[i] * (double)wrow[i];
+                    acc += p;
+                    aab += fabs(p);
+                }
+                y[(size_t)t * out_dim + j] = acc;
+                if (abs_sum) abs_sum[(size_t)t * out_dim + j] = aab;
+            }
+        }
+        free(wrow);
+        return ORACLE_OK;
+    }
     int8_t* qs = NULL;
     float* sc = NULL;
     int32_t* bsum = NULL;

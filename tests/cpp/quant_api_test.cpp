@@ -109,9 +109,24 @@ std::vector<uint8_t> random_weights(GgmlType t, int in_dim, int out_dim, uint64_
         };
         if (t == GgmlType::Q6_K) {
             put(208, 0);
-        } else if (t == GgmlType::Q4_K || t == GgmlType::Q5_K) {
+        } else if (t == GgmlType::Q4_K || t == GgmlType::Q5_K || t == GgmlType::Q4_1 ||
+                   t == GgmlType::Q5_1) {
             put(0, 0);
             put(2, 2);
+        } else if (t == GgmlType::Q2_K) {
+            put(80, 0);
+            put(82, 2);
+        } else if (t == GgmlType::Q3_K) {
+            put(108, 0);
+        } else if (t == GgmlType::F16) {
+            // fp16 values of either sign with exponent field 6..13
+            const uint16_t h = (uint16_t)(((sc[4 * b] & 1) << 15) | ((6 + sc[4 * b + 1] % 8) << 10) |
+                                          ((sc[4 * b + 2] << 2) & 0x3FF));
+            p[0] = (uint8_t)(h & 0xFF);
+            p[1] = (uint8_t)(h >> 8);
+        } else if (t == GgmlType::F32) {
+            const float v = (float)((int)(sc[4 * b] | (sc[4 * b + 1] << 8)) - 32768) * (1.0f / 65536.0f);
+            std::memcpy(p, &v, 4);
         } else {
             put(0, 0);
         }
@@ -289,6 +304,28 @@ void test_matmul_quant_patterns() {
     }
 }
 
+// The types without vec_dot: the reference dequantizes each row and dots it with the fp32
+// activations (quant.cpp:1404-1430); the bar is the same 1e-4 of the fp64 result.
+void test_matmul_float_dot_types() {
+    const TypeCase types[] = {{"F32", GgmlType::F32},   {"F16", GgmlType::F16},
+                              {"Q4_1", GgmlType::Q4_1}, {"Q5_1", GgmlType::Q5_1},
+                              {"Q8_1", GgmlType::Q8_1}, {"Q2_K", GgmlType::Q2_K},
+                              {"Q3_K", GgmlType::Q3_K}};
+    for (const TypeCase& c : types) {
+        std::printf("[matmul_quant %s (float dot)]\n", c.name);
+        const int in_dim = 512, out_dim = 300, n_rows = 3;
+        std::vector<uint8_t> w = random_weights(c.type, in_dim, out_dim, 5 + (uint64_t)c.type);
+        std::vector<float> x = activations(n_rows, in_dim, 2);
+        std::vector<float> y((size_t)n_rows * out_dim), y1(out_dim);
+        matmul_quant_batch(x.data(), w.data(), c.type, nullptr, in_dim, out_dim, n_rows, y.data());
+        expect(floored_rel_err(y, x.data(), w.data(), c.type, nullptr, in_dim, out_dim, n_rows) <= 1e-4,
+               "batch within 1e-4 of the fp64 result");
+        matmul_quant(x.data() + in_dim, w.data(), c.type, nullptr, in_dim, out_dim, y1.data());
+        expect(std::memcmp(y1.data(), y.data() + out_dim, out_dim * sizeof(float)) == 0,
+               "batch row == single row, bit for bit");
+    }
+}
+
 void test_matmul_quant_bias() {
     std::printf("[matmul_quant bias]\n");
     const int in_dim = 64, out_dim = 40;
@@ -350,6 +387,7 @@ int main(int argc, char** argv) {
             test_quantize_bit_exact();
             test_vec_dot_row();
             test_matmul_quant_patterns();
+            test_matmul_float_dot_types();
             test_matmul_quant_bias();
             test_matmul_quant_batch();
         }

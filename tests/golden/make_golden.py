@@ -149,11 +149,38 @@ def batch_fixtures(ref: oracle.Reference) -> None:
     np.savez_compressed(os.path.join(OUT, "batch.npz"), **data)
 
 
+def fdot_fixtures(ref: oracle.Reference) -> None:
+    """The types without a vec_dot kernel (the reference's dequantize-and-float-dot fallback,
+    src/core/quant.cpp:1404-1430): short and long rows, batches of 1-5 rows, rows too long
+    for one LDS-resident activation row, and F16 / F32 rows whose length is not a multiple
+    of 32."""
+    data = {}
+    shapes = [(300, 256, 1), (64, 4096, 1), (257, 4096, 3), (100, 1024, 5), (16, 16640, 1),
+              (16, 16640, 3), (50, 33, 2), (40, 100, 1)]
+    for qt in S.FLOAT_DOT_TYPES:
+        for (n, k, m) in shapes:
+            if k % S.BLOCK[qt]:
+                continue
+            seed = 4200 + qt * 11 + k + m
+            w = S.make_weight(qt, n, k, seed)
+            x = S.make_activation(m, k, seed + 1, outliers=True)
+            bias = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+            y = ref.matmul(x, w, qt, None, k, n, m, threads=THREADS)
+            yb = ref.matmul(x, w, qt, bias, k, n, m, threads=THREADS)
+            tag = f"{S.TYPE_NAMES[qt]}_{n}x{k}_m{m}"
+            data[f"{tag}__meta"] = np.array([qt, n, k, m, seed], np.int64)
+            data[f"{tag}__y"] = y
+            data[f"{tag}__ybias"] = yb
+            data[f"{tag}__w_sha"] = np.array(sha(w))
+            print(tag, flush=True)
+    np.savez_compressed(os.path.join(OUT, "fdot.npz"), **data)
+
+
 def refkat_fixtures(ref: oracle.Reference) -> None:
     """Outputs of the reference on the inputs its own tests build (tests/quant_test.cpp:237-361):
     weight bytes (k + blk + j) % 7 after a leading fp16 1.0, x = ((i % 5) - 2) * 0.5."""
     data = {}
-    for qt in (S.Q4_0, S.Q5_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K):
+    for qt in sorted(S.TYPE_NAMES):
         bs, ts = S.BLOCK[qt], S.TYPE_SIZE[qt]
         k = 64 if bs <= 32 else 256
         n = 40
@@ -176,14 +203,16 @@ def refkat_fixtures(ref: oracle.Reference) -> None:
     np.savez_compressed(os.path.join(OUT, "refkat.npz"), **data)
 
 
+FIXTURES = {"quant": quant_fixtures, "refkat": refkat_fixtures, "types": extra_type_fixtures,
+            "gemv": gemv_fixtures, "batch": batch_fixtures, "fdot": fdot_fixtures}
+
+
 def main() -> None:
+    """Writes every fixture set, or only those named on the command line."""
     oracle.build(with_ref=True)
     ref = oracle.Reference()
-    quant_fixtures(ref)
-    refkat_fixtures(ref)
-    extra_type_fixtures(ref)
-    gemv_fixtures(ref)
-    batch_fixtures(ref)
+    for name in sys.argv[1:] or list(FIXTURES):
+        FIXTURES[name](ref)
     for f in sorted(os.listdir(OUT)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(OUT, f)))

@@ -58,8 +58,14 @@ def test_argument_errors_before_device_use():
         C.matmul_quant(x, w, S.Q4_K, None, 100, 4)
     with pytest.raises(RuntimeError, match=r"^matmul_quant_batch: in_dim not divisible by block size$"):
         C.matmul_quant_batch(np.zeros((2, 100), np.float32), w, S.Q8_0, None, 100, 4, 2)
+    # an id that is no GGML type fails like the reference's dequantize fallback
+    # (quant.cpp:387); Q4_1 and the other types without vec_dot have float-dot kernels
+    with pytest.raises(RuntimeError, match=r"^unsupported ggml type for dequantize$"):
+        C.matmul_quant(np.zeros(64, np.float32), w, 5, None, 64, 4)
     with pytest.raises(RuntimeError, match=r"^vec_dot_row: no kernel for this type$"):
-        C.matmul_quant(np.zeros(64, np.float32), w, int(C.GgmlType.Q4_1), None, 64, 4)
+        qx = C.QuantizedQ8_0(scales=np.zeros(2, np.float32), qs=np.zeros(64, np.int8),
+                             bsums=np.zeros(2, np.int32), n=64)
+        C.vec_dot_rows(w, int(C.GgmlType.Q4_1), qx, 64, 4)
     with pytest.raises(RuntimeError, match=r"^quantize_row_q8_0: n not divisible by 32$"):
         C.quantize_row_q8_0(np.zeros(48, np.float32))
     # n_rows <= 0 returns without touching y (quant.cpp:1436)

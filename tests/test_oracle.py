@@ -6,7 +6,8 @@ Each check is independent of the oracle's own formulas:
   - an independent numpy decode of the byte layouts (tests/np_decode.py);
   - closed forms: exact integer dots when every scale is 1, ties-to-even at d = 1;
   - invariants: batch == per-row, y(bias) == y + bias.
-A planted mistake (a swapped nibble order) is shown to fail the integer check.
+A planted mistake (a swapped nibble order) is shown to fail the integer check, and a sum
+without the reference's fma contraction is shown to miss the float-dot golden vectors.
 """
 import numpy as np
 import pytest
@@ -17,6 +18,8 @@ from cllm_inference_amd import synth as S
 import oracle as O
 
 TYPES = [S.Q4_0, S.Q5_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K]
+FD_TYPES = list(S.FLOAT_DOT_TYPES)
+ALL_TYPES = TYPES + FD_TYPES
 
 
 def bits(a):
@@ -96,7 +99,44 @@ def test_dequant_known_answers(orc):
     assert (y[0], y[64]) == (-31.0, -30.0)
 
 
-@pytest.mark.parametrize("qt", TYPES)
+def _put_f16(b, off, v):
+    b[off:off + 2] = np.array([v], np.float16).view(np.uint8)
+
+
+def test_dequant_known_answers_float_dot_types(orc):
+    """The reference's hand-built blocks for the types without vec_dot
+    (quant_test.cpp:42-55, 70-80, 95-105, 120-130, 133-149, 152-170), restated."""
+    f = np.array([1.5, -2.25, 0.0, 3.0], np.float32)
+    y = orc.dequantize(f.view(np.uint8), S.F32, 4)
+    assert (y[0], y[1]) == (1.5, -2.25)
+    b = np.array([0x00, 0x3C, 0x00, 0x38, 0x00, 0x00, 0x00, 0xC0], np.uint8)  # 1, .5, 0, -2
+    assert tuple(orc.dequantize(b, S.F16, 4)) == (1.0, 0.5, 0.0, -2.0)
+    b = _blk(20); _put_one(b, 0); _put_f16(b, 2, 0.5); b[4] = 0x21
+    y = orc.dequantize(b, S.Q4_1, 32)
+    assert (y[0], y[16], y[1]) == (1.5, 2.5, 0.5)
+    b = _blk(24); _put_one(b, 0); b[4] = 0x01; b[8] = 0x21
+    y = orc.dequantize(b, S.Q5_1, 32)
+    assert (y[0], y[16]) == (17.0, 2.0)
+    b = _blk(36); _put_one(b, 0); b[4] = 0xFF; b[5] = 0x02
+    y = orc.dequantize(b, S.Q8_1, 32)
+    assert (y[0], y[1]) == (-1.0, 2.0)
+    b = _blk(84); b[0:16] = 0x01; b[16] = 0x03; b[32] = 0x03; _put_one(b, 80)
+    y = orc.dequantize(b, S.Q2_K, 256)
+    assert (y[0], y[16], y[32], y[128]) == (3.0, 3.0, 0.0, 0.0)
+    b = _blk(110); b[96:104] = 0x11; b[104:108] = 0xAA; _put_one(b, 108)
+    y = orc.dequantize(b, S.Q3_K, 256)
+    assert (y[0], y[255]) == (-4.0, -4.0)
+    b[0:32] = 0xFF
+    y = orc.dequantize(b, S.Q3_K, 256)
+    assert (y[0], y[255]) == (0.0, 0.0)
+
+
+def test_dequant_unknown_type_fails(orc):
+    with pytest.raises(RuntimeError, match="unsupported ggml type for dequantize"):
+        orc.dequantize(_blk(64), 999, 32)
+
+
+@pytest.mark.parametrize("qt", ALL_TYPES)
 def test_dequant_matches_numpy_layout_decode(orc, qt):
     k = 512
     w = S.make_weight(qt, 3, k, 11)
@@ -218,9 +258,10 @@ def test_oracle_matches_reference_golden_workloads(orc, tag):
 
 def test_oracle_matches_reference_golden_refkat(orc):
     cases = split_cases(load_golden("refkat.npz"))
+    assert len(cases) == 13
     for name, c in cases.items():
         qt = S.NAME_TO_TYPE[name]
-        k = 64 if S.BLOCK[qt] == 32 else 256
+        k = 64 if S.BLOCK[qt] <= 32 else 256
         assert np.array_equal(bits(orc.matmul(c["x1"], c["w"], qt, None, k, 40, 1)), bits(c["y1"]))
         assert np.array_equal(bits(orc.matmul(c["x3"], c["w"], qt, None, k, 40, 3)), bits(c["y3"]))
 
@@ -253,3 +294,78 @@ def test_compiled_reference_agrees_when_present(orc):
         x = S.make_activation(3, k, 98, outliers=True)
         assert np.array_equal(bits(ref.matmul(x, w, qt, None, k, 50, 3)),
                               bits(orc.matmul(x, w, qt, None, k, 50, 3)))
+
+
+# ------------------------------------------------------------ types without vec_dot
+
+def _fdot_case(c):
+    qt, n, k, m, seed = (int(v) for v in c["meta"])
+    w = S.make_weight(qt, n, k, seed)
+    x = S.make_activation(m, k, seed + 1, outliers=True)
+    bias = np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+    return qt, n, k, m, w, x, bias
+
+
+def test_fdot_oracle_matches_reference_golden(orc):
+    cases = split_cases(load_golden("fdot.npz"))
+    assert {int(c["meta"][0]) for c in cases.values()} == set(FD_TYPES)
+    for tag, c in cases.items():
+        qt, n, k, m, w, x, bias = _fdot_case(c)
+        assert O_sha(w) == str(c["w_sha"]), f"generator drift for {tag}"
+        assert np.array_equal(bits(orc.matmul(x, w, qt, None, k, n, m)), bits(c["y"])), tag
+        assert np.array_equal(bits(orc.matmul(x, w, qt, bias, k, n, m, threads=5)),
+                              bits(c["ybias"])), tag
+
+
+def test_fdot_golden_pins_fma_contraction():
+    """The reference accumulates acc = fma(x, w, acc) from acc = bias; the same sum with a
+    separately rounded product misses the golden bits."""
+    c = split_cases(load_golden("fdot.npz"))["F16_64x4096_m1"]
+    qt, n, k, m, w, x, bias = _fdot_case(c)
+    q, scale, wmin = D.decode(w, qt, n, k)
+    wv = (scale * q - wmin).astype(np.float32)
+    y = np.zeros(n, np.float32)
+    for i in range(k):
+        y = (y + x[0, i] * wv[:, i]).astype(np.float32)
+    assert not np.array_equal(bits(y), bits(c["y"][0]))
+    np.testing.assert_allclose(y, c["y"][0], rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("qt", FD_TYPES)
+def test_fdot_f64_matches_bruteforce(orc, qt):
+    n, k, m = 19, 512, 3
+    w = S.make_weight(qt, n, k, 123)
+    x = S.make_activation(m, k, 321, outliers=True)
+    q, scale, wmin = D.decode(w, qt, n, k)
+    want = x.astype(np.float64) @ (scale * q - wmin).T
+    got, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12 * abs_sum.max())
+    y32 = orc.matmul(x, w, qt, None, k, n, m)
+    err, _, _ = O.rel_err_floored(y32, got, abs_sum)
+    assert err < 1e-4
+
+
+@pytest.mark.parametrize("qt", FD_TYPES)
+def test_fdot_batch_equals_rows_and_exact_cases(orc, qt):
+    n, k, m = 33, 512, 4
+    w = S.make_weight(qt, n, k, 7)
+    x = S.make_activation(m, k, 8, outliers=True)
+    yb = orc.matmul(x, w, qt, None, k, n, m)
+    for t in range(m):
+        assert np.array_equal(bits(orc.matmul(x[t], w, qt, None, k, n, 1)[0]), bits(yb[t]))
+    # integer activations against integer-valued weights: every product and partial sum is
+    # exact, so any order of summation gives the exact integer dot
+    q, scale, wmin = D.decode(w, qt, n, k)
+    wv = scale * q - wmin
+    xi = np.random.default_rng(qt).integers(-3, 4, size=(2, k)).astype(np.float32)
+    if qt in (S.F32, S.F16):
+        wi = np.round(wv * 64)
+        wb = (wi.astype(np.float32) if qt == S.F32 else wi.astype(np.float16)).view(np.uint8).copy()
+        want = xi.astype(np.float64) @ wi.T
+        assert np.array_equal(orc.matmul(xi, wb.reshape(-1), qt, None, k, n, 2).astype(np.float64),
+                              want)
+
+
+def test_fdot_unknown_type_fails(orc):
+    with pytest.raises(RuntimeError, match="unsupported ggml type for dequantize"):
+        orc.matmul(np.zeros(64, np.float32), np.zeros(1000, np.uint8), 5, None, 64, 3, 1)
