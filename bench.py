@@ -144,6 +144,68 @@ def float_dot_points(C, S, steps, warmup):
     return out
 
 
+def decode_layer_device(C, S, steps, warmup, copies=4):
+    """The linear path of one Llama-3-8B decode layer in the Q4_K_M mix, device-resident:
+    RMSNorm+Q8_0 -> q/k/v GEMVs; Q8_0 of the attention output (a fixed synthetic vector:
+    attention itself is not part of this path) -> wo GEMV -> residual add; RMSNorm+Q8_0 ->
+    gate/up GEMVs -> SwiGLU+Q8_0 -> down GEMV -> residual add (engine.cpp:475-513). Thirteen
+    launches per layer. `copies` distinct copies of the layer's weights rotate so that each
+    step streams its weights from HBM, as the 32 different layers of a model would."""
+    import torch
+    cfg = "c3_q4_k_m_layer"
+    mats = {label: (qt, n, k) for label, qt, n, k in S.CONFIGS[cfg]["mats"]}
+    layers = []
+    for c in range(copies):
+        layer = {}
+        for label in mats:
+            _, _, _, w = S.config_weight(cfg, label)
+            t = torch.from_numpy(w).cuda()
+            layer[label] = t if c == 0 else t.clone()
+        layers.append(layer)
+    wbytes = sum(layers[0][l].numel() for l in mats)
+    n_embd, n_ff = 4096, 14336
+    rng = np.random.default_rng(20265)
+    x0 = torch.from_numpy(rng.standard_normal((1, n_embd)).astype(np.float32)).cuda()
+    x = x0.clone()
+    wn1 = torch.from_numpy((1 + 0.1 * rng.standard_normal(n_embd)).astype(np.float32)).cuda()
+    wn2 = torch.from_numpy((1 + 0.1 * rng.standard_normal(n_embd)).astype(np.float32)).cuda()
+    attn = torch.from_numpy(rng.standard_normal((1, n_embd)).astype(np.float32)).cuda()
+    outs = {l: torch.empty((1, n), dtype=torch.float32, device="cuda")
+            for l, (_, n, _) in mats.items()}
+
+    def step(i):
+        L = layers[i % copies]
+        _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn1, 1e-5, h=False)
+        for l in ("wq", "wk", "wv"):
+            qt, n, k = mats[l]
+            C.gemv_q8_dev(L[l], qt, k, n, qs, sc, bs, y=outs[l])
+        qa, sa, ba = C.quantize_q8_0_dev(attn)
+        qt, n, k = mats["wo"]
+        C.gemv_q8_dev(L["wo"], qt, k, n, qa, sa, ba, y=outs["wo"])
+        C.add_dev(x, outs["wo"])
+        _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn2, 1e-5, h=False)
+        for l in ("gate", "up"):
+            qt, n, k = mats[l]
+            C.gemv_q8_dev(L[l], qt, k, n, qs, sc, bs, y=outs[l])
+        _, qs, sc, bs = C.swiglu_q8_0_dev(outs["gate"], outs["up"], h=False)
+        qt, n, k = mats["down"]
+        C.gemv_q8_dev(L["down"], qt, k, n, qs, sc, bs, y=outs["down"])
+        C.add_dev(x, outs["down"])
+
+    ms = time_loop(step, steps, warmup)
+    x.copy_(x0)
+    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 13,
+           "gbs": round(wbytes / ms / 1e6, 1),
+           "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+           "projected_tokens_per_s_32_layers_linear_only": round(1e3 / (32 * ms), 1),
+           "weight_copies_rotated": copies}
+    print(f"[bench] device-resident decode layer (linear path): {ms * 1e3:.2f} us, "
+          f"{wbytes / ms / 1e6:.1f} GB/s", file=sys.stderr, flush=True)
+    del layers
+    torch.cuda.empty_cache()
+    return per
+
+
 def prefill_layer(C, S, steps, warmup):
     """The Llama-3-8B layer in the Q4_K_M mix at M = 512: every matrix timed on its own
     (graph-timed, device-resident inputs), then summed."""
@@ -215,6 +277,9 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the M=512 Q4_K_M layer (for counter profiles of the GEMM) and "
                          "print its figures as one JSON line")
+    ap.add_argument("--layer-only", action="store_true",
+                    help="run only the device-resident decode layer and print it as one JSON "
+                         "line")
     ap.add_argument("--float-dot-only", action="store_true",
                     help="run only the float-dot types' decode GEMVs and print them as one "
                          "JSON line")
@@ -241,6 +306,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.layer_only:
+        print(json.dumps({"f1_decode_layer_device": decode_layer_device(
+            C, S, max(20, args.steps // 4), max(3, args.warmup // 4))}))
+        return
 
     if args.float_dot_only:
         print(json.dumps({"f3_float_dot_types": float_dot_points(C, S, max(20, args.steps // 4),
@@ -286,6 +356,8 @@ def main():
                                                         max(2, args.warmup // 10))
         extra["f3_float_dot_types"] = float_dot_points(C, S, max(20, args.steps // 4),
                                                        max(3, args.warmup // 4))
+        extra["f1_decode_layer_device"] = decode_layer_device(C, S, max(20, args.steps // 4),
+                                                              max(3, args.warmup // 4))
 
     cpu = None
     if not args.no_cpu_baseline:

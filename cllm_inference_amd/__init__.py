@@ -62,6 +62,9 @@ SIGNATURES = {
     "cllm_hip_gemv_q8_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_matmul_quant_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
     "cllm_hip_matmul_route": (ctypes.c_char_p, [_U, _I, _I, _I]),
+    "cllm_hip_rmsnorm_q8_0_dev": (_I, [_P, _P, ctypes.c_float, _I, _I, _P, _P, _P, _P, _P]),
+    "cllm_hip_swiglu_q8_0_dev": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P]),
+    "cllm_hip_add_dev": (_I, [_P, _P, _I64, _P]),
 }
 
 _lib_handle = None
@@ -222,3 +225,46 @@ def matmul_quant_dev(x, w, t: int, bias, in_dim: int, out_dim: int, y=None):
 def matmul_route(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:
     return load_library().cllm_hip_matmul_route(int(t), int(in_dim), int(out_dim),
                                                 int(n_rows)).decode()
+
+
+# ---- producers of a device-resident layer ------------------------------------------------
+
+def _q8_buffers(m, n, device, want):
+    import torch
+    if not want:
+        return None, None, None
+    return (torch.empty((m, n), dtype=torch.int8, device=device),
+            torch.empty((m, n // 32), dtype=torch.float32, device=device),
+            torch.empty((m, n // 32), dtype=torch.int32, device=device))
+
+
+def rmsnorm_q8_0_dev(x, w, eps: float, h=True, quantize=True):
+    """RMSNorm of each row of x (float32 (m, n) CUDA tensor) with weight w (n,), fused with
+    Q8_0 quantization -- engine.cpp:23-28 then quant.cpp:420-452. Returns (h, qs, scales,
+    bsums); h is None when h=False, the Q8_0 triple None when quantize=False."""
+    import torch
+    m, n = x.shape
+    hb = torch.empty_like(x) if h else None
+    qs, sc, bs = _q8_buffers(m, n, x.device, quantize)
+    _check(load_library().cllm_hip_rmsnorm_q8_0_dev(_tp(x), _tp(w), float(eps), int(n), int(m),
+                                                    _tp(hb), _tp(qs), _tp(sc), _tp(bs),
+                                                    _stream()))
+    return hb, qs, sc, bs
+
+
+def swiglu_q8_0_dev(gate, up, h=True, quantize=True):
+    """silu(gate) * up (engine.cpp:38, 511, 596) fused with Q8_0 quantization; gate and up
+    are float32 (m, n) CUDA tensors. Returns (h, qs, scales, bsums) like rmsnorm_q8_0_dev."""
+    import torch
+    m, n = gate.shape
+    hb = torch.empty_like(gate) if h else None
+    qs, sc, bs = _q8_buffers(m, n, gate.device, quantize)
+    _check(load_library().cllm_hip_swiglu_q8_0_dev(_tp(gate), _tp(up), int(n), int(m), _tp(hb),
+                                                   _tp(qs), _tp(sc), _tp(bs), _stream()))
+    return hb, qs, sc, bs
+
+
+def add_dev(x, d):
+    """x += d in place (the residual adds, engine.cpp:506, 513)."""
+    _check(load_library().cllm_hip_add_dev(_tp(x), _tp(d), int(x.numel()), _stream()))
+    return x

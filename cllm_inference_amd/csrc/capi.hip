@@ -555,6 +555,56 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
     return CLLM_HIP_OK;
 }
 
+int cllm_hip_rmsnorm_q8_0_dev(const float* x, const float* w, float eps, int n, int n_rows,
+                              float* h, int8_t* qs, float* scales, int32_t* bsums,
+                              void* stream) {
+    if (n <= 0 || n_rows < 0) return set_err(CLLM_HIP_E_ARG, "rms_norm: bad shape");
+    if (qs && n % 32 != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "quantize_row_q8_0: n not divisible by 32");
+    if (!x || !w || (!h && !qs) || (qs && (!scales || !bsums)))
+        return set_err(CLLM_HIP_E_ARG, "rms_norm: null pointer");
+    if (!aligned16(x) || !aligned16(w) || (h && !aligned16(h)) || ((uintptr_t)qs & 3u) ||
+        ((uintptr_t)scales & 3u) || ((uintptr_t)bsums & 3u))
+        return set_err(CLLM_HIP_E_ARG, "rms_norm: misaligned device pointer");
+    if (n_rows == 0) return CLLM_HIP_OK;
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    HIP_TRY(launch_rmsnorm_q8_0(x, w, eps, n, n_rows, h, qs, scales, bsums, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_swiglu_q8_0_dev(const float* gate, const float* up, int n, int n_rows, float* h,
+                             int8_t* qs, float* scales, int32_t* bsums, void* stream) {
+    if (n <= 0 || n_rows < 0) return set_err(CLLM_HIP_E_ARG, "swiglu: bad shape");
+    if (qs && n % 32 != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "quantize_row_q8_0: n not divisible by 32");
+    if (!gate || !up || (!h && !qs) || (qs && (!scales || !bsums)))
+        return set_err(CLLM_HIP_E_ARG, "swiglu: null pointer");
+    if (!aligned16(gate) || !aligned16(up) || (h && !aligned16(h)) || ((uintptr_t)qs & 3u) ||
+        ((uintptr_t)scales & 3u) || ((uintptr_t)bsums & 3u))
+        return set_err(CLLM_HIP_E_ARG, "swiglu: misaligned device pointer");
+    if (n_rows == 0) return CLLM_HIP_OK;
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    HIP_TRY(launch_swiglu_q8_0(gate, up, (int64_t)n * n_rows, h, qs, scales, bsums,
+                               (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream) {
+    if (n < 0) return set_err(CLLM_HIP_E_ARG, "add: negative length");
+    if (n == 0) return CLLM_HIP_OK;
+    if (!x || !d) return set_err(CLLM_HIP_E_ARG, "add: null pointer");
+    if (!aligned16(x) || !aligned16(d)) return set_err(CLLM_HIP_E_ARG, "add: misaligned device pointer");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    HIP_TRY(launch_add(x, d, n, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows) {
     (void)out_dim;
     if (gemv_f_supported(type)) return "fdot";

@@ -70,6 +70,16 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         hipStream_t stream);
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
 
+// Producers of the linear layers' activations (k_producers.hip): RMSNorm of `rows` rows of n
+// and SwiGLU (silu(gate) * up) over `total` elements, each writing h (fp32, may be null)
+// and, when qs is not null and n (total) is a multiple of 32, its Q8_0 blocks; x += d.
+hipError_t launch_rmsnorm_q8_0(const float* x, const float* w, float eps, int n, int rows,
+                               float* h, int8_t* qs, float* scales, int32_t* bsums,
+                               hipStream_t stream);
+hipError_t launch_swiglu_q8_0(const float* gate, const float* up, int64_t total, float* h,
+                              int8_t* qs, float* scales, int32_t* bsums, hipStream_t stream);
+hipError_t launch_add(float* x, const float* d, int64_t n, hipStream_t stream);
+
 // Float-dot GEMV (k_gemv_f.hip) for the types without a vec_dot kernel (F32, F16, Q4_1,
 // Q5_1, Q8_1, Q2_K, Q3_K): y[t, j] = bias[j] + sum_i x[t, i] * deq(W[j, i]) on fp32
 // activation rows x[m][k], as the reference's dequantize fallback computes it.

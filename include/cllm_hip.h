@@ -110,6 +110,27 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
 int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,
                               int in_dim, int out_dim, int n_rows, float* y, void* stream);
 
+/* ---- producers of a device-resident layer's activations (stream-ordered) -------------- */
+
+/* RMSNorm of n_rows rows of n floats fused with the Q8_0 quantization matmul_quant applies
+ * to its input: h = x * (1 / sqrt(sum(x^2) / n + eps)) * w (rms_norm_ptr,
+ * src/core/engine.cpp:23-28), then quantize_row_q8_0(h) (src/core/quant.cpp:420-452) into
+ * qs / scales / bsums (the layout of cllm_hip_quantize_q8_0_dev). h (fp32) may be null, or
+ * qs, scales and bsums may all be null; n % 32 == 0 when they are given. The Q8_0 blocks are
+ * exactly those of h; the sum of squares is reduced in parallel, so h can differ from the
+ * reference's in the last bits. Feed qs/scales/bsums to cllm_hip_gemv_q8_dev. */
+int cllm_hip_rmsnorm_q8_0_dev(const float* x, const float* w, float eps, int n, int n_rows,
+                              float* h, int8_t* qs, float* scales, int32_t* bsums,
+                              void* stream);
+
+/* h = silu(gate) * up, silu(v) = v / (1 + exp(-v)) (src/core/engine.cpp:38, 511, 596),
+ * over n_rows rows of n, fused with its Q8_0 quantization as above. */
+int cllm_hip_swiglu_q8_0_dev(const float* gate, const float* up, int n, int n_rows, float* h,
+                             int8_t* qs, float* scales, int32_t* bsums, void* stream);
+
+/* x[i] += d[i], i < n: the residual adds (src/core/engine.cpp:506, 513, 587, 598). */
+int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream);
+
 /* Name of the kernel family cllm_hip_matmul_quant_dev would run for this shape: "gemv" or
  * "mfma" (vec_dot types), "fdot" (the float-dot kernels of the other types), "none" (no
  * GGML type); for tests and benchmarks. */

@@ -102,6 +102,27 @@ class Oracle(_Lib):
         f.restype = _I
         f.argtypes = [_P, _P, _U, _P, _I, _I, _I, _P, _P]
 
+    def rms_norm(self, x, w, eps):
+        """rms_norm_ptr of each row of x (m, n) with weight w (n,)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        x2 = x.reshape(-1, x.shape[-1])
+        out = np.empty_like(x2)
+        f = self.lib.oracle_rms_norm
+        f.restype, f.argtypes = _I, [_P, _P, _I, _I, ctypes.c_float, _P]
+        self._check(f(_ptr(x2), _ptr(np.ascontiguousarray(w, dtype=np.float32)), x2.shape[1],
+                      x2.shape[0], float(eps), _ptr(out)))
+        return out.reshape(x.shape)
+
+    def swiglu(self, gate, up):
+        """silu(gate) * up element-wise."""
+        g = np.ascontiguousarray(gate, dtype=np.float32)
+        u = np.ascontiguousarray(up, dtype=np.float32)
+        out = np.empty_like(g)
+        f = self.lib.oracle_swiglu
+        f.restype, f.argtypes = _I, [_P, _P, _I64, _P]
+        self._check(f(_ptr(g), _ptr(u), g.size, _ptr(out)))
+        return out
+
     def matmul_f64(self, x, w, qtype, bias, k, n, m):
         """fp64 evaluation and per-output absolute-term sums (tolerance floors)."""
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -835,3 +835,27 @@ int oracle_matmul_quant_f64(const float* x, const void* w, uint32_t type, const 
     free(bsum);
     return rc;
 }
+
+/* ---- producers of the linear layers' activations (src/core/engine.cpp) ----------------- */
+
+/* rms_norm_ptr (engine.cpp:23-28) on each of `rows` rows: a sequential sum of squares, which
+ * clang contracts into one fma per element, then rms = 1 / sqrt(sum / n + eps) and
+ * out = (x * rms) * w. */
+int oracle_rms_norm(const float* x, const float* w, int n, int rows, float eps, float* out) {
+    if (n <= 0 || rows < 0) return fail(ORACLE_ERR_SHAPE, "rms_norm: bad shape");
+    for (int r = 0; r < rows; ++r) {
+        const float* xr = x + (size_t)r * n;
+        float* o = out + (size_t)r * n;
+        float sum = 0.0f;
+        for (int i = 0; i < n; ++i) sum = fmaf(xr[i], xr[i], sum);
+        const float rms = 1.0f / sqrtf(sum / (float)n + eps);
+        for (int i = 0; i < n; ++i) o[i] = xr[i] * rms * w[i];
+    }
+    return ORACLE_OK;
+}
+
+/* silu(gate) * up element-wise, silu(v) = v / (1 + exp(-v)) (engine.cpp:38, 511, 596). */
+int oracle_swiglu(const float* gate, const float* up, int64_t n, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = gate[i] / (1.0f + expf(-gate[i])) * up[i];
+    return ORACLE_OK;
+}

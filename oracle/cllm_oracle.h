@@ -77,6 +77,12 @@ int oracle_matmul_quant_f64(const float* x, const void* w, uint32_t type, const 
 
 const char* oracle_last_error(void);
 
+/* Producers of the linear layers' inputs in the reference engine (next to the path):
+ *   oracle_rms_norm   src/core/engine.cpp:23-28 (rms_norm_ptr), row by row
+ *   oracle_swiglu     src/core/engine.cpp:38 (silu) and 511 / 596 (gate * up) */
+int oracle_rms_norm(const float* x, const float* w, int n, int rows, float eps, float* out);
+int oracle_swiglu(const float* gate, const float* up, int64_t n, float* out);
+
 #ifdef __cplusplus
 }
 #endif

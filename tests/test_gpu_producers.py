@@ -1,0 +1,123 @@
+"""GPU parity of the fused producers of a device-resident layer: RMSNorm and SwiGLU, each
+fused with the Q8_0 quantization matmul_quant applies to its input, and the residual add.
+
+Bars (written into each test):
+  - h (fp32) against the reference's arithmetic (the oracle's restatement of
+    rms_norm_ptr / silu, src/core/engine.cpp:23-28, 38): within 2e-6 relative, and never
+    further from the fp64 value than the reference's own h is, plus 4 ulp (the sum of
+    squares is reduced in parallel rather than sequentially; silu uses the device's expf);
+  - the Q8_0 blocks equal quantize_row_q8_0 of the GPU's own h, bit for bit;
+  - against quantize_row_q8_0 of the reference's h, codes differ only at rounding
+    boundaries: by at most 1, in under 0.1 % of the elements;
+  - a whole decode sub-layer (RMSNorm -> Q8_0 -> GEMV) meets the GEMV's own 1e-4 bar
+    against the reference's matmul_quant of the reference's h.
+"""
+import numpy as np
+import pytest
+
+from cllm_inference_amd import synth as S
+from test_gpu_parity import bits, check_close, _dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_h(got, ref, exact, what):
+    got = np.asarray(got, np.float64)
+    ref32 = np.asarray(ref, np.float32)
+    ref = ref32.astype(np.float64)
+    rel = np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert rel.max() <= 2e-6, f"{what}: {rel.max():.3g} relative to the reference"
+    ulp = np.spacing(np.abs(ref32)).astype(np.float64)
+    excess = np.abs(got - exact) - (np.abs(ref - exact) + 4 * ulp)
+    assert excess.max() <= 0, f"{what}: further from fp64 than the reference + 4 ulp"
+
+
+def _check_q8(gpu, orc, h_gpu, h_ref, qs, sc, bs, what):
+    n = h_gpu.shape[1]
+    q_own, s_own, b_own = orc.quantize(h_gpu)
+    assert np.array_equal(qs, q_own), what
+    assert np.array_equal(bits(sc), bits(s_own)), what
+    assert np.array_equal(bs, b_own), what
+    q_ref, _, _ = orc.quantize(h_ref)
+    diff = qs.astype(np.int32) - q_ref.astype(np.int32)
+    assert np.abs(diff).max() <= 1, what
+    assert np.count_nonzero(diff) <= max(1, int(1e-3 * diff.size)), what
+
+
+@pytest.mark.parametrize("n,m", [(896, 1), (4096, 1), (4096, 5), (14336, 2), (5120, 3)])
+def test_rmsnorm_q8_0(gpu, orc, n, m):
+    rng = np.random.default_rng(n + m)
+    x = (rng.standard_normal((m, n)) * 2).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    eps = 1e-5
+    print("rmsnorm", n, m, flush=True)
+    h, qs, sc, bs = gpu.rmsnorm_q8_0_dev(_dev(x), _dev(w), eps)
+    h = h.cpu().numpy()
+    h_ref = orc.rms_norm(x, w, eps)
+    x64 = x.astype(np.float64)
+    exact = x64 / np.sqrt((x64 ** 2).sum(axis=1, keepdims=True) / n + eps) * w
+    _check_h(h, h_ref, exact, f"rmsnorm {n}x{m}")
+    _check_q8(gpu, orc, h, h_ref, qs.cpu().numpy(), sc.cpu().numpy(), bs.cpu().numpy(),
+              f"rmsnorm {n}x{m}")
+    # h alone, and the Q8_0 blocks alone, are the same values
+    h2, _, _, _ = gpu.rmsnorm_q8_0_dev(_dev(x), _dev(w), eps, quantize=False)
+    _, qs2, _, _ = gpu.rmsnorm_q8_0_dev(_dev(x), _dev(w), eps, h=False)
+    assert np.array_equal(bits(h2.cpu().numpy()), bits(h))
+    assert np.array_equal(qs2.cpu().numpy(), qs.cpu().numpy())
+
+
+@pytest.mark.parametrize("n,m", [(14336, 1), (14336, 3), (4864, 2), (96, 7)])
+def test_swiglu_q8_0(gpu, orc, n, m):
+    rng = np.random.default_rng(7 * n + m)
+    g = (rng.standard_normal((m, n)) * 3).astype(np.float32)
+    u = rng.standard_normal((m, n)).astype(np.float32)
+    g[0, :4] = [0.0, 100.0, -100.0, -0.0]
+    print("swiglu", n, m, flush=True)
+    h, qs, sc, bs = gpu.swiglu_q8_0_dev(_dev(g), _dev(u))
+    h = h.cpu().numpy()
+    h_ref = orc.swiglu(g, u)
+    g64 = g.astype(np.float64)
+    with np.errstate(over="ignore"):
+        exact = g64 / (1 + np.exp(-g64)) * u
+    _check_h(h, h_ref, exact, f"swiglu {n}x{m}")
+    assert h[0, 1] == h_ref[0, 1] and np.signbit(h[0, 2]) == np.signbit(h_ref[0, 2])
+    _check_q8(gpu, orc, h, h_ref, qs.cpu().numpy(), sc.cpu().numpy(), bs.cpu().numpy(),
+              f"swiglu {n}x{m}")
+
+
+def test_add(gpu):
+    rng = np.random.default_rng(9)
+    for n in (4096, 4099, 3):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        ad = _dev(a)
+        gpu.add_dev(ad, _dev(b))
+        assert np.array_equal(bits(ad.cpu().numpy()), bits((a + b).astype(np.float32)))
+
+
+@pytest.mark.parametrize("qt", [S.Q4_K, S.Q6_K, S.Q8_0])
+def test_rmsnorm_then_gemv_meets_the_gemv_bar(gpu, orc, qt):
+    """RMSNorm -> Q8_0 -> GEMV on device against the reference's rms_norm then matmul_quant."""
+    n_out, k = 1024, 4096
+    rng = np.random.default_rng(qt)
+    x = (rng.standard_normal((1, k)) * 2).astype(np.float32)
+    wn = (1 + 0.2 * rng.standard_normal(k)).astype(np.float32)
+    w = S.make_weight(qt, n_out, k, 11)
+    _, qs, sc, bs = gpu.rmsnorm_q8_0_dev(_dev(x), _dev(wn), 1e-5, h=False)
+    y = gpu.gemv_q8_dev(_dev(w), qt, k, n_out, qs, sc, bs).cpu().numpy()
+    h_ref = orc.rms_norm(x, wn, 1e-5)
+    yo = orc.matmul(h_ref, w, qt, None, k, n_out, 1).reshape(1, n_out)
+    exact, abs_sum = orc.matmul_f64(h_ref, w, qt, None, k, n_out, 1)
+    check_close(y, yo, exact, abs_sum, f"rmsnorm+gemv {S.TYPE_NAMES[qt]}")
+
+
+def test_producer_argument_errors(gpu):
+    import torch
+    x = torch.zeros((1, 48), dtype=torch.float32, device="cuda")
+    w = torch.zeros(48, dtype=torch.float32, device="cuda")
+    with pytest.raises(RuntimeError, match="quantize_row_q8_0: n not divisible by 32"):
+        gpu.rmsnorm_q8_0_dev(x, w, 1e-5)
+    h, _, _, _ = gpu.rmsnorm_q8_0_dev(x, w, 1e-5, quantize=False)  # fp32 output is fine
+    assert h.shape == (1, 48)
+    with pytest.raises(RuntimeError, match="misaligned"):
+        gpu.add_dev(torch.zeros(9, device="cuda")[1:], torch.zeros(8, device="cuda"))

@@ -369,3 +369,49 @@ def test_fdot_batch_equals_rows_and_exact_cases(orc, qt):
 def test_fdot_unknown_type_fails(orc):
     with pytest.raises(RuntimeError, match="unsupported ggml type for dequantize"):
         orc.matmul(np.zeros(64, np.float32), np.zeros(1000, np.uint8), 5, None, 64, 3, 1)
+
+
+# ------------------------------------------------- producers of the linear layers' inputs
+
+def test_rms_norm_closed_form(orc):
+    """Inputs whose squares and running sums are exact in fp32 (multiples of 1/2 up to 8),
+    so the sequential sum equals the exact one whatever the contraction; rms and the output
+    then follow from single IEEE operations, restated in numpy float32."""
+    rng = np.random.default_rng(3)
+    n, rows, eps = 896, 3, np.float32(1e-6)
+    x = (rng.integers(-16, 17, size=(rows, n)) * 0.5).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    got = orc.rms_norm(x, w, eps)
+    for r in range(rows):
+        s = np.float32(np.sum(x[r].astype(np.float64) ** 2))      # exact
+        rms = np.float32(1.0) / np.sqrt(np.float32(s / np.float32(n)) + eps)
+        want = (x[r] * rms).astype(np.float32) * w
+        assert np.array_equal(bits(got[r]), bits(want.astype(np.float32)))
+    # a plausible slip (mean over n - 1, or eps dropped) changes the bits
+    s = np.float32(np.sum(x[0].astype(np.float64) ** 2))
+    bad = np.float32(1.0) / np.sqrt(np.float32(s / np.float32(n - 1)) + eps)
+    assert not np.array_equal(bits(got[0]), bits((x[0] * bad).astype(np.float32) * w))
+
+
+def test_rms_norm_general_inputs_close_to_f64(orc):
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((4, 4096)).astype(np.float32) * 3
+    w = (1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)
+    got = orc.rms_norm(x, w, 1e-5)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-5) * w
+    np.testing.assert_allclose(got, want, rtol=2e-6)
+
+
+def test_swiglu_closed_forms_and_f64(orc):
+    g = np.array([0.0, -0.0, 100.0, -100.0, 1.0, -1.0, 20.0, -20.0], np.float32)
+    u = np.array([3.0, 3.0, 0.5, 2.0, 1.0, 1.0, 1.0, 1.0], np.float32)
+    h = orc.swiglu(g, u)
+    assert h[0] == 0.0 and h[2] == 50.0           # silu(0) = 0; exp(-100) is lost in 1 + e
+    assert h[3] == 0.0 and np.signbit(h[3])       # -100 / (1 + inf) = -0
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(10000) * 4).astype(np.float32)
+    u = rng.standard_normal(10000).astype(np.float32)
+    g64 = g.astype(np.float64)
+    want = g64 / (1 + np.exp(-g64)) * u
+    np.testing.assert_allclose(orc.swiglu(g, u), want, rtol=1e-6, atol=1e-30)
