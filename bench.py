@@ -148,9 +148,10 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
     """The linear path of one Llama-3-8B decode layer in the Q4_K_M mix, device-resident:
     RMSNorm+Q8_0 -> q/k/v GEMVs; Q8_0 of the attention output (a fixed synthetic vector:
     attention itself is not part of this path) -> wo GEMV -> residual add; RMSNorm+Q8_0 ->
-    gate/up GEMVs -> SwiGLU+Q8_0 -> down GEMV -> residual add (engine.cpp:475-513). Thirteen
-    launches per layer. `copies` distinct copies of the layer's weights rotate so that each
-    step streams its weights from HBM, as the 32 different layers of a model would."""
+    gate/up GEMVs -> SwiGLU+Q8_0 -> down GEMV -> residual add (engine.cpp:475-513). Eleven
+    launches per layer (the residual adds ride in the wo and down GEMVs). `copies` distinct
+    copies of the layer's weights rotate so that each step streams its weights from HBM, as
+    the 32 different layers of a model would."""
     import torch
     cfg = "c3_q4_k_m_layer"
     mats = {label: (qt, n, k) for label, qt, n, k in S.CONFIGS[cfg]["mats"]}
@@ -181,20 +182,18 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
             C.gemv_q8_dev(L[l], qt, k, n, qs, sc, bs, y=outs[l])
         qa, sa, ba = C.quantize_q8_0_dev(attn)
         qt, n, k = mats["wo"]
-        C.gemv_q8_dev(L["wo"], qt, k, n, qa, sa, ba, y=outs["wo"])
-        C.add_dev(x, outs["wo"])
+        C.gemv_q8_residual_dev(L["wo"], qt, k, n, qa, sa, ba, x)
         _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn2, 1e-5, h=False)
         for l in ("gate", "up"):
             qt, n, k = mats[l]
             C.gemv_q8_dev(L[l], qt, k, n, qs, sc, bs, y=outs[l])
         _, qs, sc, bs = C.swiglu_q8_0_dev(outs["gate"], outs["up"], h=False)
         qt, n, k = mats["down"]
-        C.gemv_q8_dev(L["down"], qt, k, n, qs, sc, bs, y=outs["down"])
-        C.add_dev(x, outs["down"])
+        C.gemv_q8_residual_dev(L["down"], qt, k, n, qs, sc, bs, x)
 
     ms = time_loop(step, steps, warmup)
     x.copy_(x0)
-    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 13,
+    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 11,
            "gbs": round(wbytes / ms / 1e6, 1),
            "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
            "projected_tokens_per_s_32_layers_linear_only": round(1e3 / (32 * ms), 1),

@@ -65,6 +65,7 @@ SIGNATURES = {
     "cllm_hip_rmsnorm_q8_0_dev": (_I, [_P, _P, ctypes.c_float, _I, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_swiglu_q8_0_dev": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_add_dev": (_I, [_P, _P, _I64, _P]),
+    "cllm_hip_gemv_q8_residual_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
 }
 
 _lib_handle = None
@@ -207,6 +208,16 @@ def gemv_q8_dev(w, t: int, in_dim: int, out_dim: int, qs, scales, bsums, bias=No
     _check(load_library().cllm_hip_gemv_q8_dev(_tp(w), int(t), int(in_dim), int(out_dim), int(m),
                                                _tp(qs), _tp(scales), _tp(bsums), _tp(bias),
                                                _tp(y), _stream()))
+    return y
+
+
+def gemv_q8_residual_dev(w, t: int, in_dim: int, out_dim: int, qs, scales, bsums, y, bias=None):
+    """y += vec_dot of every weight row against the quantized rows (device): a matmul and
+    the residual add after it (engine.cpp:505-506, 512-513) in one launch."""
+    m = qs.shape[0]
+    _check(load_library().cllm_hip_gemv_q8_residual_dev(
+        _tp(w), int(t), int(in_dim), int(out_dim), int(m), _tp(qs), _tp(scales), _tp(bsums),
+        _tp(bias), _tp(y), _stream()))
     return y
 
 

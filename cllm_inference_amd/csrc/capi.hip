@@ -528,6 +528,26 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
     return CLLM_HIP_OK;
 }
 
+int cllm_hip_gemv_q8_residual_dev(const void* w, uint32_t type, int in_dim, int out_dim,
+                                  int n_rows, const int8_t* qs, const float* scales,
+                                  const int32_t* bsums, const float* bias, float* y,
+                                  void* stream) {
+    int rc = check_matmul("matmul_quant", type, in_dim, out_dim);
+    if (rc) return rc;
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if (n_rows <= 0 || out_dim == 0) return CLLM_HIP_OK;
+    if (!w || !qs || !scales || !bsums || !y)
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(w) || !aligned16(qs) || ((uintptr_t)scales & 7u) || ((uintptr_t)bsums & 7u) ||
+        ((uintptr_t)y & 3u) || ((uintptr_t)bias & 3u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    HIP_TRY(launch_gemv(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums, bias,
+                        y, (hipStream_t)stream, true));
+    return CLLM_HIP_OK;
+}
+
 int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,
                               int in_dim, int out_dim, int n_rows, float* y, void* stream) {
     int rc = check_matmul(n_rows > 1 ? "matmul_quant_batch" : "matmul_quant", type, in_dim, out_dim);

@@ -606,7 +606,7 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __re
                                               const int32_t* __restrict__ xb,
                                               const float* __restrict__ bias,
                                               float* __restrict__ y,
-                                              const float* __restrict__ x_f32) {
+                                              const float* __restrict__ x_f32, int accumulate) {
     using Tr = typename TraitsOf<T>::type;
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
@@ -700,7 +700,10 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __re
                 for (int r = 0; r < MR; ++r) {
                     float v = wave_sum(acc[r]);
                     if (bias) v += bj;
-                    if (lane == r) y[(size_t)r * n + j] = v;
+                    if (lane == r) {
+                        float* yp = y + (size_t)r * n + j;
+                        *yp = accumulate ? *yp + v : v;  // residual add: x += (W a + b)
+                    }
                     acc[r] = 0.0f;
                 }
             }
@@ -775,14 +778,14 @@ static int64_t resident_waves(size_t shmem) {
 template <uint32_t T, int MR, int P>
 static hipError_t launch_t(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
                            const int32_t* xb, const float* bias, float* y, const float* x_f32,
-                           int waves, hipStream_t stream) {
+                           int accumulate, int waves, hipStream_t stream) {
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
     if (waves > n) waves = n;
     constexpr int kWaves = gemv_threads<MR>() / 64;
     const int grid = (waves + kWaves - 1) / kWaves;
     const size_t shmem = act_lds_bytes<T>(MR, k);
     hipLaunchKernelGGL((k_gemv<T, MR, P>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, w, row_bytes, k,
-                       n, qs, xs, xb, bias, y, x_f32);
+                       n, qs, xs, xb, bias, y, x_f32, accumulate);
     return hipGetLastError();
 }
 
@@ -798,7 +801,7 @@ static int max_rows_per_launch(int k) {
 template <uint32_t T, int MR>
 static hipError_t launch_mr(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
                             const int32_t* xb, const float* bias, float* y, const float* x_f32,
-                            hipStream_t stream) {
+                            int accumulate, hipStream_t stream) {
     using Tr = typename TraitsOf<T>::type;
     const int iters = (k / Tr::UNIT + 63) / 64;
     const int64_t items = (int64_t)n * iters;
@@ -807,21 +810,22 @@ static hipError_t launch_mr(const uint8_t* w, int k, int n, const int8_t* qs, co
     const size_t shmem = act_lds_bytes<T>(MR, k);
     if (MR > 2 && items > simds * 32) {
         const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2>(shmem));
-        return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, (int)waves, stream);
+        return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, accumulate, (int)waves,
+                                  stream);
     }
     const int64_t waves = std::min({items, simds * tu.short_wps, resident_waves<T, MR, 1>(shmem)});
-    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, (int)waves, stream);
+    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, accumulate, (int)waves, stream);
 }
 
 template <uint32_t T>
 static hipError_t launch_rows(const uint8_t* w, int k, int n, int mr, const int8_t* qs,
                               const float* xs, const int32_t* xb, const float* bias, float* y,
-                              const float* x_f32, hipStream_t stream) {
+                              const float* x_f32, int acc, hipStream_t stream) {
     switch (mr) {
-        case 1: return launch_mr<T, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
-        case 2: return launch_mr<T, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
-        case 4: return launch_mr<T, 4>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
-        default: return launch_mr<T, 8>(w, k, n, qs, xs, xb, bias, y, x_f32, stream);
+        case 1: return launch_mr<T, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
+        case 2: return launch_mr<T, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
+        case 4: return launch_mr<T, 4>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
+        default: return launch_mr<T, 8>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
     }
 }
 
@@ -830,7 +834,7 @@ static hipError_t launch_rows(const uint8_t* w, int k, int n, int mr, const int8
 template <uint32_t T>
 static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int8_t* qs,
                                 const float* scales, const int32_t* bsums, const float* bias,
-                                float* y, const float* x_f32, hipStream_t stream) {
+                                float* y, const float* x_f32, int acc, hipStream_t stream) {
     const int nb = k / 32;
     const int cap = max_rows_per_launch<T>(k);
     int t = 0;
@@ -841,7 +845,7 @@ static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int
         const hipError_t e = launch_rows<T>(
             w, k, n, mr, qs ? qs + (size_t)t * k : nullptr, scales ? scales + (size_t)t * nb : nullptr,
             bsums ? bsums + (size_t)t * nb : nullptr, bias, y + (size_t)t * n,
-            x_f32 ? x_f32 + (size_t)t * k : nullptr, stream);
+            x_f32 ? x_f32 + (size_t)t * k : nullptr, acc, stream);
         if (e != hipSuccess) return e;
         t += mr;
     }
@@ -850,28 +854,29 @@ static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int
 
 static hipError_t gemv_dispatch(uint32_t type, const uint8_t* w, int k, int n, int m,
                                 const int8_t* qs, const float* scales, const int32_t* bsums,
-                                const float* bias, float* y, const float* x_f32,
+                                const float* bias, float* y, const float* x_f32, int acc,
                                 hipStream_t stream) {
     switch (type) {
-        case T_Q4_K: return gemv_all_rows<T_Q4_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
-        case T_Q5_K: return gemv_all_rows<T_Q5_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
-        case T_Q6_K: return gemv_all_rows<T_Q6_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
-        case T_Q8_0: return gemv_all_rows<T_Q8_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
-        case T_Q4_0: return gemv_all_rows<T_Q4_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
-        case T_Q5_0: return gemv_all_rows<T_Q5_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, stream);
+        case T_Q4_K: return gemv_all_rows<T_Q4_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
+        case T_Q5_K: return gemv_all_rows<T_Q5_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
+        case T_Q6_K: return gemv_all_rows<T_Q6_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
+        case T_Q8_0: return gemv_all_rows<T_Q8_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
+        case T_Q4_0: return gemv_all_rows<T_Q4_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
+        case T_Q5_0: return gemv_all_rows<T_Q5_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
-                       hipStream_t stream) {
-    return gemv_dispatch(type, w, k, n, m, qs, scales, bsums, bias, y, nullptr, stream);
+                       hipStream_t stream, bool accumulate) {
+    return gemv_dispatch(type, w, k, n, m, qs, scales, bsums, bias, y, nullptr, accumulate ? 1 : 0,
+                         stream);
 }
 
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
                              const float* x, const float* bias, float* y, hipStream_t stream) {
-    return gemv_dispatch(type, w, k, n, m, nullptr, nullptr, nullptr, bias, y, x, stream);
+    return gemv_dispatch(type, w, k, n, m, nullptr, nullptr, nullptr, bias, y, x, 0, stream);
 }
 
 }  // namespace cllm_hip

@@ -105,6 +105,58 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_q8_0(const float* __restri
     }
 }
 
+// The same with the row held in registers: 1024 threads, CPT 16-byte chunks per thread
+// (n <= 4096 * CPT, n % 32 == 0), so the row is read once and no thread loops long.
+// Chunk c = t + 1024 i of the row; the 8 consecutive lanes of a group share t / 8 and hold
+// the 8 chunks of one 32-element block.
+constexpr int kRegThreads = 1024;
+
+template <int CPT>
+__global__ __launch_bounds__(kRegThreads) void k_rmsnorm_q8_0_reg(const float* __restrict__ x,
+                                                                  const float* __restrict__ w,
+                                                                  float eps, int n,
+                                                                  float* __restrict__ h,
+                                                                  int8_t* __restrict__ qs,
+                                                                  float* __restrict__ scales,
+                                                                  int32_t* __restrict__ bsums) {
+    __shared__ float part_sums[kRegThreads / 64];
+    const int row = blockIdx.x;
+    const float* xr = x + (size_t)row * n;
+    const int chunks = n / 4;
+    f32x4 v[CPT];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = threadIdx.x + kRegThreads * i;
+        v[i] = c < chunks ? *(const f32x4*)(xr + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+        ss = __builtin_fmaf(v[i].x, v[i].x, ss);
+        ss = __builtin_fmaf(v[i].y, v[i].y, ss);
+        ss = __builtin_fmaf(v[i].z, v[i].z, ss);
+        ss = __builtin_fmaf(v[i].w, v[i].w, ss);
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) part_sums[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRegThreads / 64; ++i) sum += part_sums[i];
+    const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sum, (float)n) + eps));
+    const int part = threadIdx.x & 7;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+        const int c = threadIdx.x + kRegThreads * i;
+        if (c >= chunks) break;  // whole 8-lane groups (chunks % 8 == 0)
+        const f32x4 wv = *(const f32x4*)(w + 4 * c);
+        f32x4 hv;
+        hv.x = __fmul_rn(__fmul_rn(v[i].x, rms), wv.x);
+        hv.y = __fmul_rn(__fmul_rn(v[i].y, rms), wv.y);
+        hv.z = __fmul_rn(__fmul_rn(v[i].z, rms), wv.z);
+        hv.w = __fmul_rn(__fmul_rn(v[i].w, rms), wv.w);
+        if (h) *(f32x4*)(h + (size_t)row * n + 4 * c) = hv;
+        if (qs) quantize_block8(hv, part, (int64_t)row * (n / 32) + c / 8, qs, scales, bsums);
+    }
+}
+
 // silu(g) * u over n_blocks 32-element blocks, eight lanes per block.
 __global__ __launch_bounds__(kThreads) void k_swiglu_q8_0(const float* __restrict__ gate,
                                                           const float* __restrict__ up,
@@ -113,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_q8_0(const float* __restric
                                                           int8_t* __restrict__ qs,
                                                           float* __restrict__ scales,
                                                           int32_t* __restrict__ bsums) {
-    const int64_t gt = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gt >> 3;
     const int part = (int)(gt & 7);
     if (blk >= n_blocks) return;  // whole 8-lane groups leave together
@@ -160,6 +212,19 @@ hipError_t launch_rmsnorm_q8_0(const float* x, const float* w, float eps, int n,
                                float* h, int8_t* qs, float* scales, int32_t* bsums,
                                hipStream_t stream) {
     if (rows <= 0 || n <= 0) return hipSuccess;
+    if (n % 32 == 0 && n <= 4 * 4 * kRegThreads) {
+        const int cpt = (n + 4 * kRegThreads - 1) / (4 * kRegThreads);
+        if (cpt == 1)
+            hipLaunchKernelGGL(k_rmsnorm_q8_0_reg<1>, dim3((unsigned)rows), dim3(kRegThreads), 0,
+                               stream, x, w, eps, n, h, qs, scales, bsums);
+        else if (cpt == 2)
+            hipLaunchKernelGGL(k_rmsnorm_q8_0_reg<2>, dim3((unsigned)rows), dim3(kRegThreads), 0,
+                               stream, x, w, eps, n, h, qs, scales, bsums);
+        else
+            hipLaunchKernelGGL(k_rmsnorm_q8_0_reg<4>, dim3((unsigned)rows), dim3(kRegThreads), 0,
+                               stream, x, w, eps, n, h, qs, scales, bsums);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_rmsnorm_q8_0, dim3((unsigned)rows), dim3(kThreads), 0, stream, x, w, eps,
                        n, h, qs, scales, bsums);
     return hipGetLastError();
@@ -173,9 +238,10 @@ hipError_t launch_swiglu_q8_0(const float* gate, const float* up, int64_t total,
                            dim3(kThreads), 0, stream, gate, up, total, h);
         return hipGetLastError();
     }
+    // one wave per workgroup: a decode row (14336 elements) then spreads over 224 CUs
     const int64_t n_blocks = total / 32;
-    hipLaunchKernelGGL(k_swiglu_q8_0, dim3((unsigned)((n_blocks * 8 + kThreads - 1) / kThreads)),
-                       dim3(kThreads), 0, stream, gate, up, n_blocks, h, qs, scales, bsums);
+    hipLaunchKernelGGL(k_swiglu_q8_0, dim3((unsigned)((n_blocks * 8 + 63) / 64)), dim3(64), 0,
+                       stream, gate, up, n_blocks, h, qs, scales, bsums);
     return hipGetLastError();
 }
 

@@ -34,9 +34,11 @@ hipError_t launch_q8_to_w(const int8_t* qs, const float* scales, const int32_t* 
 
 // y[t, j] = vec_dot(W row j, activation row t) (+ bias[j]) for t < m, j < n.
 // Activation rows are Q8_0: qs[t * k], scales / bsums[t * k / 32]. Any m >= 1.
+// With accumulate, y[t, j] += vec_dot (+ bias[j]) instead of y[t, j] = ... (the residual add
+// that follows a matmul in the engine, fused).
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
-                       hipStream_t stream);
+                       hipStream_t stream, bool accumulate = false);
 
 // Same as launch_gemv with fp32 activation rows x[m][k]: each launch quantizes its rows to
 // Q8_0 in LDS (bit-identical to launch_quantize_q8_0) instead of reading a quantized batch,

@@ -104,6 +104,15 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
                          const int8_t* qs, const float* scales, const int32_t* bsums,
                          const float* bias, float* y, void* stream);
 
+/* cllm_hip_gemv_q8_dev fused with the residual add that follows the matmul in the engine
+ * (x += mm(...), src/core/engine.cpp:505-506, 512-513): y[t, j] += vec_dot_row(...)
+ * (+ bias[j]), so y holds the residual stream on entry. Always the GEMV kernels (meant for
+ * decode and small batches). */
+int cllm_hip_gemv_q8_residual_dev(const void* w, uint32_t type, int in_dim, int out_dim,
+                                  int n_rows, const int8_t* qs, const float* scales,
+                                  const int32_t* bsums, const float* bias, float* y,
+                                  void* stream);
+
 /* matmul_quant_batch on device buffers. vec_dot types, small n_rows: one GEMV launch that
  * quantizes its activation rows itself; large n_rows: quantizes x into a library-owned
  * per-stream workspace, then runs the MFMA GEMM. Other types: the float-dot GEMV on x. */

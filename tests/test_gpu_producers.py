@@ -121,3 +121,21 @@ def test_producer_argument_errors(gpu):
     assert h.shape == (1, 48)
     with pytest.raises(RuntimeError, match="misaligned"):
         gpu.add_dev(torch.zeros(9, device="cuda")[1:], torch.zeros(8, device="cuda"))
+
+
+@pytest.mark.parametrize("qt", [S.Q4_K, S.Q6_K, S.Q5_0])
+def test_gemv_residual_equals_gemv_then_add(gpu, qt):
+    """y += W a (+ b) in one launch gives the bits of the separate matmul and add."""
+    import torch
+    n_out, k, m = 4096, 4096, 3
+    rng = np.random.default_rng(qt + 100)
+    w = _dev(S.make_weight(qt, n_out, k, 12))
+    a = _dev(S.make_activation(m, k, 13))
+    bias = _dev(rng.standard_normal(n_out).astype(np.float32))
+    resid = rng.standard_normal((m, n_out)).astype(np.float32)
+    qs, sc, bs = gpu.quantize_q8_0_dev(a)
+    mm = gpu.gemv_q8_dev(w, qt, k, n_out, qs, sc, bs, bias=bias).cpu().numpy()
+    y = _dev(resid)
+    gpu.gemv_q8_residual_dev(w, qt, k, n_out, qs, sc, bs, y, bias=bias)
+    assert np.array_equal(bits(y.cpu().numpy()), bits((resid + mm).astype(np.float32)))
+    torch.cuda.synchronize()
