@@ -146,10 +146,11 @@ def float_dot_points(C, S, steps, warmup):
 
 def decode_layer_device(C, S, steps, warmup, copies=4):
     """The linear path of one Llama-3-8B decode layer in the Q4_K_M mix, device-resident:
-    RMSNorm+Q8_0 -> q/k/v GEMVs; Q8_0 of the attention output (a fixed synthetic vector:
-    attention itself is not part of this path) -> wo GEMV -> residual add; RMSNorm+Q8_0 ->
-    gate/up GEMVs -> SwiGLU+Q8_0 -> down GEMV -> residual add (engine.cpp:475-513). Eleven
-    launches per layer (the residual adds ride in the wo and down GEMVs). `copies` distinct
+    RMSNorm+Q8_0 -> one GEMV launch for q/k/v; Q8_0 of the attention output (a fixed
+    synthetic vector: attention itself is not part of this path) -> wo GEMV + residual add;
+    RMSNorm+Q8_0 -> one launch for gate/up -> SwiGLU+Q8_0 -> down GEMV + residual add
+    (engine.cpp:475-513). Eight launches per layer (the residual adds ride in the wo and
+    down GEMVs). `copies` distinct
     copies of the layer's weights rotate so that each step streams its weights from HBM, as
     the 32 different layers of a model would."""
     import torch
@@ -174,26 +175,29 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
     outs = {l: torch.empty((1, n), dtype=torch.float32, device="cuda")
             for l, (_, n, _) in mats.items()}
 
+    qkv, gu = ("wq", "wk", "wv"), ("gate", "up")
+    assert len({mats[l][0] for l in qkv}) == 1 and len({mats[l][0] for l in gu}) == 1
+
     def step(i):
         L = layers[i % copies]
         _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn1, 1e-5, h=False)
-        for l in ("wq", "wk", "wv"):
-            qt, n, k = mats[l]
-            C.gemv_q8_dev(L[l], qt, k, n, qs, sc, bs, y=outs[l])
+        qt, _, k = mats["wq"]
+        C.gemv_q8_multi_dev([L[l] for l in qkv], qt, k, [mats[l][1] for l in qkv], qs, sc, bs,
+                            ys=[outs[l] for l in qkv])
         qa, sa, ba = C.quantize_q8_0_dev(attn)
         qt, n, k = mats["wo"]
         C.gemv_q8_residual_dev(L["wo"], qt, k, n, qa, sa, ba, x)
         _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn2, 1e-5, h=False)
-        for l in ("gate", "up"):
-            qt, n, k = mats[l]
-            C.gemv_q8_dev(L[l], qt, k, n, qs, sc, bs, y=outs[l])
+        qt, _, k = mats["gate"]
+        C.gemv_q8_multi_dev([L[l] for l in gu], qt, k, [mats[l][1] for l in gu], qs, sc, bs,
+                            ys=[outs[l] for l in gu])
         _, qs, sc, bs = C.swiglu_q8_0_dev(outs["gate"], outs["up"], h=False)
         qt, n, k = mats["down"]
         C.gemv_q8_residual_dev(L["down"], qt, k, n, qs, sc, bs, x)
 
     ms = time_loop(step, steps, warmup)
     x.copy_(x0)
-    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 11,
+    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 8,
            "gbs": round(wbytes / ms / 1e6, 1),
            "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
            "projected_tokens_per_s_32_layers_linear_only": round(1e3 / (32 * ms), 1),

@@ -66,6 +66,7 @@ SIGNATURES = {
     "cllm_hip_swiglu_q8_0_dev": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_add_dev": (_I, [_P, _P, _I64, _P]),
     "cllm_hip_gemv_q8_residual_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "cllm_hip_gemv_q8_multi_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
 }
 
 _lib_handle = None
@@ -209,6 +210,27 @@ def gemv_q8_dev(w, t: int, in_dim: int, out_dim: int, qs, scales, bsums, bias=No
                                                _tp(qs), _tp(scales), _tp(bsums), _tp(bias),
                                                _tp(y), _stream()))
     return y
+
+
+def gemv_q8_multi_dev(ws, t: int, in_dim: int, out_dims, qs, scales, bsums, ys=None,
+                      biases=None):
+    """One launch over up to three matrices sharing the quantized activation rows (q/k/v,
+    gate/up). Returns the list of outputs [n_rows, out_dims[i]]."""
+    import torch
+    m = qs.shape[0]
+    n_mats = len(ws)
+    if ys is None:
+        ys = [torch.empty((m, int(n)), dtype=torch.float32, device=qs.device) for n in out_dims]
+    wa = (ctypes.c_void_p * n_mats)(*[w.data_ptr() for w in ws])
+    ya = (ctypes.c_void_p * n_mats)(*[y.data_ptr() for y in ys])
+    na = (ctypes.c_int * n_mats)(*[int(n) for n in out_dims])
+    ba = None
+    if biases is not None:
+        ba = (ctypes.c_void_p * n_mats)(*[0 if b is None else b.data_ptr() for b in biases])
+    _check(load_library().cllm_hip_gemv_q8_multi_dev(
+        int(t), int(in_dim), n_mats, wa, na, ba, ya, int(m), _tp(qs), _tp(scales), _tp(bsums),
+        _stream()))
+    return ys
 
 
 def gemv_q8_residual_dev(w, t: int, in_dim: int, out_dim: int, qs, scales, bsums, y, bias=None):

@@ -528,6 +528,32 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
     return CLLM_HIP_OK;
 }
 
+int cllm_hip_gemv_q8_multi_dev(uint32_t type, int in_dim, int n_mats, const void* const* w,
+                               const int* out_dims, const float* const* bias, float* const* y,
+                               int n_rows, const int8_t* qs, const float* scales,
+                               const int32_t* bsums, void* stream) {
+    if (n_mats < 1 || n_mats > 3 || !w || !out_dims || !y)
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: 1 to 3 matrices expected");
+    int rc;
+    for (int i = 0; i < n_mats; ++i)
+        if ((rc = check_matmul("matmul_quant", type, in_dim, out_dims[i]))) return rc;
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if (n_rows <= 0) return CLLM_HIP_OK;
+    if (!qs || !scales || !bsums) return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(qs) || ((uintptr_t)scales & 7u) || ((uintptr_t)bsums & 7u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    for (int i = 0; i < n_mats; ++i) {
+        if (!w[i] || !y[i]) return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+        if (!aligned16(w[i]) || ((uintptr_t)y[i] & 3u) || (bias && ((uintptr_t)bias[i] & 3u)))
+            return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    }
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    HIP_TRY(launch_gemv_multi(type, in_dim, n_mats, (const uint8_t* const*)w, out_dims, bias, y,
+                              n_rows, qs, scales, bsums, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
 int cllm_hip_gemv_q8_residual_dev(const void* w, uint32_t type, int in_dim, int out_dim,
                                   int n_rows, const int8_t* qs, const float* scales,
                                   const int32_t* bsums, const float* bias, float* y,

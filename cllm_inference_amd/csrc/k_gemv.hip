@@ -25,6 +25,7 @@
 // Lane partial sums are reduced across the wave, so only the fp32 summation order (and the
 // association of the minimum term's product) differs from the reference.
 #include <algorithm>
+#include <climits>
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
@@ -590,6 +591,28 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Up to three weight matrices of one type and row length that read the same activation rows
+// (q, k and v; gate and up) run as one launch: virtual row j belongs to segment s with
+// start[s] <= j < start[s + 1] and is row j - start[s] of w[s], its results going to y[s]
+// (row stride rows[s]) plus bias[s]. Unused segments start at INT_MAX. The segment of a row
+// is wave-uniform, so the picks below are scalar selects (an indexed read of the argument
+// arrays would go through scratch memory).
+struct GemvSegs {
+    const uint8_t* w[3];
+    float* y[3];
+    const float* bias[3];
+    int start[3];
+    int rows[3];
+};
+
+__device__ __forceinline__ int seg_of(const GemvSegs& sg, int j) {
+    return (j >= sg.start[1] ? 1 : 0) + (j >= sg.start[2] ? 1 : 0);
+}
+template <class V>
+__device__ __forceinline__ V seg_pick(int s, V a, V b, V c) {
+    return s == 0 ? a : (s == 1 ? b : c);
+}
+
 // Persistent GEMV: wave w owns rows j = w, w + n_waves, ...; items (row, 64-unit slice) are
 // streamed through a P-deep ring of in-flight weight loads.
 // Workgroup size: 8 waves share one staged (or quantized) activation batch for decode-sized
@@ -600,12 +623,10 @@ template <int MR>
 constexpr int gemv_threads() { return MR <= 2 ? 512 : 256; }
 
 template <uint32_t T, int MR, int P>
-__global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __restrict__ w, int64_t row_bytes,
+__global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_t row_bytes,
                                               int k, int n, const int8_t* __restrict__ qs,
                                               const float* __restrict__ xs,
                                               const int32_t* __restrict__ xb,
-                                              const float* __restrict__ bias,
-                                              float* __restrict__ y,
                                               const float* __restrict__ x_f32, int accumulate) {
     using Tr = typename TraitsOf<T>::type;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -626,7 +647,10 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __re
     auto slot_addr = [&](int item, const uint8_t*& row, int& u) {
         const int c = max(0, min(item, n_items - 1));
         const int t = c / iters, it = c - t * iters;
-        row = w + (int64_t)min(wid + t * n_waves, n - 1) * row_bytes;
+        const int jr = min(wid + t * n_waves, n - 1);
+        const int s = seg_of(sg, jr);
+        row = seg_pick(s, sg.w[0], sg.w[1], sg.w[2]) +
+              (int64_t)(jr - seg_pick(s, sg.start[0], sg.start[1], sg.start[2])) * row_bytes;
         u = min(lane + 64 * it, units - 1);
     };
 
@@ -694,14 +718,19 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(const uint8_t* __re
                 ring[p] = Tr::load(row, u2);
             }
             if (item < n_items && it == iters - 1) {
-                const int j = __builtin_amdgcn_readfirstlane(wid + t * n_waves);
+                const int jv = __builtin_amdgcn_readfirstlane(wid + t * n_waves);
+                const int s = seg_of(sg, jv);
+                const int j = jv - seg_pick(s, sg.start[0], sg.start[1], sg.start[2]);
+                const float* bias = seg_pick(s, sg.bias[0], sg.bias[1], sg.bias[2]);
+                float* y = seg_pick(s, sg.y[0], sg.y[1], sg.y[2]);
+                const int ny = seg_pick(s, sg.rows[0], sg.rows[1], sg.rows[2]);
                 const float bj = bias ? bias[j] : 0.0f;
 #pragma unroll
                 for (int r = 0; r < MR; ++r) {
                     float v = wave_sum(acc[r]);
                     if (bias) v += bj;
                     if (lane == r) {
-                        float* yp = y + (size_t)r * n + j;
+                        float* yp = y + (size_t)r * ny + j;
                         *yp = accumulate ? *yp + v : v;  // residual add: x += (W a + b)
                     }
                     acc[r] = 0.0f;
@@ -776,16 +805,16 @@ static int64_t resident_waves(size_t shmem) {
 }
 
 template <uint32_t T, int MR, int P>
-static hipError_t launch_t(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
-                           const int32_t* xb, const float* bias, float* y, const float* x_f32,
-                           int accumulate, int waves, hipStream_t stream) {
+static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
+                           const int32_t* xb, const float* x_f32, int accumulate, int waves,
+                           hipStream_t stream) {
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
     if (waves > n) waves = n;
     constexpr int kWaves = gemv_threads<MR>() / 64;
     const int grid = (waves + kWaves - 1) / kWaves;
     const size_t shmem = act_lds_bytes<T>(MR, k);
-    hipLaunchKernelGGL((k_gemv<T, MR, P>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, w, row_bytes, k,
-                       n, qs, xs, xb, bias, y, x_f32, accumulate);
+    hipLaunchKernelGGL((k_gemv<T, MR, P>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, sg,
+                       row_bytes, k, n, qs, xs, xb, x_f32, accumulate);
     return hipGetLastError();
 }
 
@@ -799,9 +828,9 @@ static int max_rows_per_launch(int k) {
 }
 
 template <uint32_t T, int MR>
-static hipError_t launch_mr(const uint8_t* w, int k, int n, const int8_t* qs, const float* xs,
-                            const int32_t* xb, const float* bias, float* y, const float* x_f32,
-                            int accumulate, hipStream_t stream) {
+static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
+                            const int32_t* xb, const float* x_f32, int accumulate,
+                            hipStream_t stream) {
     using Tr = typename TraitsOf<T>::type;
     const int iters = (k / Tr::UNIT + 63) / 64;
     const int64_t items = (int64_t)n * iters;
@@ -810,31 +839,30 @@ static hipError_t launch_mr(const uint8_t* w, int k, int n, const int8_t* qs, co
     const size_t shmem = act_lds_bytes<T>(MR, k);
     if (MR > 2 && items > simds * 32) {
         const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2>(shmem));
-        return launch_t<T, MR, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, accumulate, (int)waves,
-                                  stream);
+        return launch_t<T, MR, 2>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);
     }
     const int64_t waves = std::min({items, simds * tu.short_wps, resident_waves<T, MR, 1>(shmem)});
-    return launch_t<T, MR, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, accumulate, (int)waves, stream);
+    return launch_t<T, MR, 1>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);
 }
 
 template <uint32_t T>
-static hipError_t launch_rows(const uint8_t* w, int k, int n, int mr, const int8_t* qs,
-                              const float* xs, const int32_t* xb, const float* bias, float* y,
-                              const float* x_f32, int acc, hipStream_t stream) {
+static hipError_t launch_rows(const GemvSegs& sg, int k, int n, int mr, const int8_t* qs,
+                              const float* xs, const int32_t* xb, const float* x_f32, int acc,
+                              hipStream_t stream) {
     switch (mr) {
-        case 1: return launch_mr<T, 1>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
-        case 2: return launch_mr<T, 2>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
-        case 4: return launch_mr<T, 4>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
-        default: return launch_mr<T, 8>(w, k, n, qs, xs, xb, bias, y, x_f32, acc, stream);
+        case 1: return launch_mr<T, 1>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 2: return launch_mr<T, 2>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 4: return launch_mr<T, 4>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        default: return launch_mr<T, 8>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
     }
 }
 
 // Runs every activation row through the GEMV, MR rows per launch. With x_f32 set, the rows
 // are fp32 and each launch quantizes its rows itself (qs / scales / bsums unused).
 template <uint32_t T>
-static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int8_t* qs,
-                                const float* scales, const int32_t* bsums, const float* bias,
-                                float* y, const float* x_f32, int acc, hipStream_t stream) {
+static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const int8_t* qs,
+                                const float* scales, const int32_t* bsums, const float* x_f32,
+                                int acc, hipStream_t stream) {
     const int nb = k / 32;
     const int cap = max_rows_per_launch<T>(k);
     int t = 0;
@@ -842,41 +870,75 @@ static hipError_t gemv_all_rows(const uint8_t* w, int k, int n, int m, const int
         const int left = m - t;
         int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
         while (mr > cap) mr /= 2;
+        GemvSegs sg = sg0;
+        for (int i = 0; i < 3; ++i) sg.y[i] = sg0.y[i] + (size_t)t * sg0.rows[i];
         const hipError_t e = launch_rows<T>(
-            w, k, n, mr, qs ? qs + (size_t)t * k : nullptr, scales ? scales + (size_t)t * nb : nullptr,
-            bsums ? bsums + (size_t)t * nb : nullptr, bias, y + (size_t)t * n,
-            x_f32 ? x_f32 + (size_t)t * k : nullptr, acc, stream);
+            sg, k, n, mr, qs ? qs + (size_t)t * k : nullptr, scales ? scales + (size_t)t * nb : nullptr,
+            bsums ? bsums + (size_t)t * nb : nullptr, x_f32 ? x_f32 + (size_t)t * k : nullptr, acc,
+            stream);
         if (e != hipSuccess) return e;
         t += mr;
     }
     return hipSuccess;
 }
 
-static hipError_t gemv_dispatch(uint32_t type, const uint8_t* w, int k, int n, int m,
+static hipError_t gemv_dispatch(uint32_t type, const GemvSegs& sg, int k, int n, int m,
                                 const int8_t* qs, const float* scales, const int32_t* bsums,
-                                const float* bias, float* y, const float* x_f32, int acc,
-                                hipStream_t stream) {
+                                const float* x_f32, int acc, hipStream_t stream) {
     switch (type) {
-        case T_Q4_K: return gemv_all_rows<T_Q4_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
-        case T_Q5_K: return gemv_all_rows<T_Q5_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
-        case T_Q6_K: return gemv_all_rows<T_Q6_K>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
-        case T_Q8_0: return gemv_all_rows<T_Q8_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
-        case T_Q4_0: return gemv_all_rows<T_Q4_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
-        case T_Q5_0: return gemv_all_rows<T_Q5_0>(w, k, n, m, qs, scales, bsums, bias, y, x_f32, acc, stream);
+        case T_Q4_K: return gemv_all_rows<T_Q4_K>(sg, k, n, m, qs, scales, bsums, x_f32, acc, stream);
+        case T_Q5_K: return gemv_all_rows<T_Q5_K>(sg, k, n, m, qs, scales, bsums, x_f32, acc, stream);
+        case T_Q6_K: return gemv_all_rows<T_Q6_K>(sg, k, n, m, qs, scales, bsums, x_f32, acc, stream);
+        case T_Q8_0: return gemv_all_rows<T_Q8_0>(sg, k, n, m, qs, scales, bsums, x_f32, acc, stream);
+        case T_Q4_0: return gemv_all_rows<T_Q4_0>(sg, k, n, m, qs, scales, bsums, x_f32, acc, stream);
+        case T_Q5_0: return gemv_all_rows<T_Q5_0>(sg, k, n, m, qs, scales, bsums, x_f32, acc, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+static GemvSegs one_segment(const uint8_t* w, int n, const float* bias, float* y) {
+    GemvSegs sg;
+    for (int i = 0; i < 3; ++i) {
+        sg.w[i] = w;
+        sg.y[i] = y;
+        sg.bias[i] = bias;
+        sg.start[i] = i == 0 ? 0 : INT_MAX;
+        sg.rows[i] = n;
+    }
+    return sg;
 }
 
 hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
                        hipStream_t stream, bool accumulate) {
-    return gemv_dispatch(type, w, k, n, m, qs, scales, bsums, bias, y, nullptr, accumulate ? 1 : 0,
-                         stream);
+    return gemv_dispatch(type, one_segment(w, n, bias, y), k, n, m, qs, scales, bsums, nullptr,
+                         accumulate ? 1 : 0, stream);
+}
+
+hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* const* w,
+                             const int* n, const float* const* bias, float* const* y, int m,
+                             const int8_t* qs, const float* scales, const int32_t* bsums,
+                             hipStream_t stream) {
+    if (n_mats < 1 || n_mats > 3) return hipErrorInvalidValue;
+    GemvSegs sg = one_segment(w[0], n[0], bias ? bias[0] : nullptr, y[0]);
+    int total = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        sg.w[i] = w[i];
+        sg.y[i] = y[i];
+        sg.bias[i] = bias ? bias[i] : nullptr;
+        sg.start[i] = total;
+        sg.rows[i] = n[i];
+        if (n[i] < 0 || (int64_t)total + n[i] > INT_MAX / 2) return hipErrorInvalidValue;
+        total += n[i];
+    }
+    if (total == 0) return hipSuccess;
+    return gemv_dispatch(type, sg, k, total, m, qs, scales, bsums, nullptr, 0, stream);
 }
 
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
                              const float* x, const float* bias, float* y, hipStream_t stream) {
-    return gemv_dispatch(type, w, k, n, m, nullptr, nullptr, nullptr, bias, y, x, 0, stream);
+    return gemv_dispatch(type, one_segment(w, n, bias, y), k, n, m, nullptr, nullptr, nullptr, x, 0,
+                         stream);
 }
 
 }  // namespace cllm_hip

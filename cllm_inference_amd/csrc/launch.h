@@ -40,6 +40,14 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, con
                        const float* scales, const int32_t* bsums, const float* bias, float* y,
                        hipStream_t stream, bool accumulate = false);
 
+// launch_gemv over up to three matrices of one type and row length k that read the same
+// activation rows (q / k / v, gate / up), in one launch: matrix i has n[i] rows, results
+// go to y[i] ([m][n[i]]) plus bias[i] (bias may be null, as may its entries).
+hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* const* w,
+                             const int* n, const float* const* bias, float* const* y, int m,
+                             const int8_t* qs, const float* scales, const int32_t* bsums,
+                             hipStream_t stream);
+
 // Same as launch_gemv with fp32 activation rows x[m][k]: each launch quantizes its rows to
 // Q8_0 in LDS (bit-identical to launch_quantize_q8_0) instead of reading a quantized batch,
 // so a decode step is a single kernel.

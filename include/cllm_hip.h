@@ -104,6 +104,16 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
                          const int8_t* qs, const float* scales, const int32_t* bsums,
                          const float* bias, float* y, void* stream);
 
+/* cllm_hip_gemv_q8_dev over n_mats (1 to 3) matrices of one type and in_dim that read the
+ * same quantized activation rows, in one launch: the q, k and v projections of one norm's
+ * output (src/core/engine.cpp:476-478), or gate and up (509-510). Matrix i has
+ * out_dims[i] rows, writes y[i] ([n_rows][out_dims[i]]) and adds bias[i] when bias and
+ * bias[i] are not null. */
+int cllm_hip_gemv_q8_multi_dev(uint32_t type, int in_dim, int n_mats, const void* const* w,
+                               const int* out_dims, const float* const* bias, float* const* y,
+                               int n_rows, const int8_t* qs, const float* scales,
+                               const int32_t* bsums, void* stream);
+
 /* cllm_hip_gemv_q8_dev fused with the residual add that follows the matmul in the engine
  * (x += mm(...), src/core/engine.cpp:505-506, 512-513): y[t, j] += vec_dot_row(...)
  * (+ bias[j]), so y holds the residual stream on entry. Always the GEMV kernels (meant for

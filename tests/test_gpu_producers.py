@@ -139,3 +139,21 @@ def test_gemv_residual_equals_gemv_then_add(gpu, qt):
     gpu.gemv_q8_residual_dev(w, qt, k, n_out, qs, sc, bs, y, bias=bias)
     assert np.array_equal(bits(y.cpu().numpy()), bits((resid + mm).astype(np.float32)))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("qt", [S.Q4_K, S.Q6_K, S.Q8_0])
+def test_gemv_multi_equals_separate_launches(gpu, qt):
+    """q/k/v (and gate/up) in one launch give the bits of one launch per matrix."""
+    rng = np.random.default_rng(qt + 200)
+    k, m = 4096, 2
+    dims = [4096, 1024, 1000]
+    ws = [_dev(S.make_weight(qt, n, k, 20 + i)) for i, n in enumerate(dims)]
+    biases = [_dev(rng.standard_normal(dims[0]).astype(np.float32)), None,
+              _dev(rng.standard_normal(dims[2]).astype(np.float32))]
+    qs, sc, bs = gpu.quantize_q8_0_dev(_dev(S.make_activation(m, k, 21)))
+    for n_mats in (3, 2):
+        ys = gpu.gemv_q8_multi_dev(ws[:n_mats], qt, k, dims[:n_mats], qs, sc, bs,
+                                   biases=biases[:n_mats])
+        for i in range(n_mats):
+            one = gpu.gemv_q8_dev(ws[i], qt, k, dims[i], qs, sc, bs, bias=biases[i])
+            assert np.array_equal(bits(ys[i].cpu().numpy()), bits(one.cpu().numpy())), (n_mats, i)
