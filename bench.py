@@ -209,6 +209,37 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
     return per
 
 
+def gguf_upload(C, S, gib=1.0):
+    """f2: the GGUF data section's one-time upload (parse, map, pinned double-buffered H2D,
+    registration) for a synthetic file of `gib` GiB written to local temporary storage."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_writer as G
+    n, k = int(gib * (1 << 30)) // S.row_bytes(S.Q4_K, 4096), 4096
+    raw = np.random.default_rng(5).integers(0, 256, size=n * S.row_bytes(S.Q4_K, k),
+                                            dtype=np.uint8).tobytes()
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "upload.gguf")
+        G.write_gguf(path, [("general.architecture", G.STR, "llama")],
+                     [("blob.weight", (n, k), S.Q4_K, raw)])
+        del raw
+        with open(path, "rb") as f:  # page cache warm, as after the engine's own load
+            while f.read(64 << 20):
+                pass
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            g = C.GgufFile(path, upload=True)
+            times.append(time.perf_counter() - t0)
+            nbytes = g.config().data_bytes
+            g.close()
+    t = sorted(times)[1]
+    out = {"bytes": int(nbytes), "seconds": round(t, 4), "gbs": round(nbytes / t / 1e9, 2)}
+    print(f"[bench] GGUF upload {nbytes / 2**30:.2f} GiB: {t * 1e3:.1f} ms, "
+          f"{nbytes / t / 1e9:.2f} GB/s", file=sys.stderr, flush=True)
+    return out
+
+
 def prefill_layer(C, S, steps, warmup):
     """The Llama-3-8B layer in the Q4_K_M mix at M = 512: every matrix timed on its own
     (graph-timed, device-resident inputs), then summed."""
@@ -280,6 +311,8 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the M=512 Q4_K_M layer (for counter profiles of the GEMM) and "
                          "print its figures as one JSON line")
+    ap.add_argument("--upload-only", action="store_true",
+                    help="run only the GGUF upload measurement and print it as one JSON line")
     ap.add_argument("--layer-only", action="store_true",
                     help="run only the device-resident decode layer and print it as one JSON "
                          "line")
@@ -309,6 +342,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.upload_only:
+        print(json.dumps({"f2_gguf_upload": gguf_upload(C, S)}))
+        return
 
     if args.layer_only:
         print(json.dumps({"f1_decode_layer_device": decode_layer_device(
@@ -361,6 +398,7 @@ def main():
                                                        max(3, args.warmup // 4))
         extra["f1_decode_layer_device"] = decode_layer_device(C, S, max(20, args.steps // 4),
                                                               max(3, args.warmup // 4))
+        extra["f2_gguf_upload"] = gguf_upload(C, S)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -67,7 +67,26 @@ SIGNATURES = {
     "cllm_hip_add_dev": (_I, [_P, _P, _I64, _P]),
     "cllm_hip_gemv_q8_residual_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_multi_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
+    "cllm_hip_gguf_open": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_P)]),
+    "cllm_hip_gguf_close": (_I, [_P]),
+    "cllm_hip_gguf_tensor_count": (_I, [_P]),
+    "cllm_hip_gguf_find": (_I, [_P, ctypes.c_char_p]),
+    "cllm_hip_gguf_tensor": (_I, [_P, _I, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U),
+                                  ctypes.POINTER(_I), ctypes.POINTER(ctypes.c_uint64),
+                                  ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(_P),
+                                  ctypes.POINTER(_P)]),
+    "cllm_hip_gguf_config": (_I, [_P, _P]),
 }
+
+
+class ModelConfig(ctypes.Structure):
+    """cllm_hip_model_config: ModelConfig (reference gguf.hpp:13-34) plus the file layout."""
+    _fields_ = [("arch", ctypes.c_char * 64)] + [
+        (n, ctypes.c_uint32) for n in ("n_layers", "n_embd", "n_head", "n_head_kv", "n_ctx",
+                                        "n_ff", "vocab_size", "head_dim")] + [
+        ("rope_theta", ctypes.c_float), ("norm_eps", ctypes.c_float),
+        ("version", ctypes.c_uint32), ("data_offset", ctypes.c_uint64),
+        ("data_bytes", ctypes.c_uint64)]
 
 _lib_handle = None
 
@@ -301,3 +320,64 @@ def add_dev(x, d):
     """x += d in place (the residual adds, engine.cpp:506, 513)."""
     _check(load_library().cllm_hip_add_dev(_tp(x), _tp(d), int(x.numel()), _stream()))
     return x
+
+
+# ---- GGUF files ---------------------------------------------------------------------------
+
+@dataclass
+class GgufTensorInfo:
+    name: str
+    type: int
+    shape: tuple          # rows first
+    offset: int           # in the data section
+    host: int             # address in the mapping
+    dev: int              # device address (0 without upload)
+
+
+class GgufFile:
+    """A GGUF file parsed by the library (reference GgufLoader::load, gguf.cpp:122-275);
+    with upload=True its data section lives on the device and host tensor pointers into the
+    mapping resolve to it in every matmul call."""
+
+    def __init__(self, path: str, upload: bool = False):
+        lib = load_library()
+        h = ctypes.c_void_p()
+        _check(lib.cllm_hip_gguf_open(str(path).encode(), 1 if upload else 0, ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            _check(load_library().cllm_hip_gguf_close(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __len__(self):
+        return load_library().cllm_hip_gguf_tensor_count(self._h)
+
+    def tensor(self, i: int) -> GgufTensorInfo:
+        name = ctypes.c_char_p()
+        t = ctypes.c_uint32()
+        nd = ctypes.c_int()
+        dims = (ctypes.c_uint64 * 4)()
+        off = ctypes.c_uint64()
+        host = ctypes.c_void_p()
+        dev = ctypes.c_void_p()
+        _check(load_library().cllm_hip_gguf_tensor(self._h, int(i), ctypes.byref(name),
+                                                   ctypes.byref(t), ctypes.byref(nd), dims,
+                                                   ctypes.byref(off), ctypes.byref(host),
+                                                   ctypes.byref(dev)))
+        return GgufTensorInfo(name.value.decode(), t.value, tuple(dims[:min(nd.value, 4)]),
+                              off.value, host.value or 0, dev.value or 0)
+
+    def find(self, name: str) -> int:
+        return load_library().cllm_hip_gguf_find(self._h, name.encode())
+
+    def config(self) -> ModelConfig:
+        c = ModelConfig()
+        _check(load_library().cllm_hip_gguf_config(self._h, ctypes.byref(c)))
+        return c

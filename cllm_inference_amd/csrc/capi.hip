@@ -6,6 +6,7 @@
 // written. Device-pointer entry points do the same work stream-ordered.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -17,6 +18,7 @@
 
 #include "../../include/cllm_hip.h"
 #include "ggml_blocks.h"
+#include "gguf_file.h"
 #include "launch.h"
 
 using namespace cllm_hip;
@@ -110,7 +112,8 @@ struct Workspace {
 
 struct Region {
     size_t bytes;
-    void* dev;
+    void* dev;    // device address of the region's first byte
+    void* alloc;  // the allocation to free
 };
 
 struct DeviceState {
@@ -457,7 +460,7 @@ int cllm_hip_register_weights(const void* host_base, size_t bytes) {
     auto it = st->regions.find(a);
     if (it != st->regions.end()) {
         HIP_TRY(hipStreamSynchronize(st->stream));
-        HIP_TRY(hipFree(it->second.dev));
+        HIP_TRY(hipFree(it->second.alloc));
         st->regions.erase(it);
     }
     // Keep the device copy at the same offset modulo 256 as the host base, so host pointers
@@ -466,7 +469,7 @@ int cllm_hip_register_weights(const void* host_base, size_t bytes) {
     void* dev = nullptr;
     HIP_TRY(hipMalloc(&dev, bytes + lead));
     HIP_TRY(hipMemcpy((char*)dev + lead, host_base, bytes, hipMemcpyHostToDevice));
-    st->regions[a] = Region{bytes, (char*)dev + lead};
+    st->regions[a] = Region{bytes, (char*)dev + lead, dev};
     return CLLM_HIP_OK;
 }
 
@@ -479,8 +482,7 @@ int cllm_hip_unregister_weights(const void* host_base) {
     if (it == st->regions.end())
         return set_err(CLLM_HIP_E_ARG, "cllm_hip_unregister_weights: region not registered");
     HIP_TRY(hipStreamSynchronize(st->stream));
-    const size_t lead = (uintptr_t)host_base & 255u;
-    HIP_TRY(hipFree((char*)it->second.dev - lead));
+    HIP_TRY(hipFree(it->second.alloc));
     st->regions.erase(it);
     return CLLM_HIP_OK;
 }
@@ -648,6 +650,136 @@ int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream) {
     int rc = acquire(&st);
     if (rc) return rc;
     HIP_TRY(launch_add(x, d, n, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+// ---- GGUF files (gguf.cpp:122-275 of the reference) ---------------------------------------
+
+struct cllm_hip_gguf {
+    cllm_hip::GgufFile file;
+    int device = -1;        // device holding the upload, -1 if not uploaded
+    void* dev = nullptr;    // device copy of the data section
+    size_t dev_bytes = 0;
+};
+
+int cllm_hip_gguf_open(const char* path, int upload, cllm_hip_gguf** out) {
+    if (!path || !out) return set_err(CLLM_HIP_E_ARG, "cllm_hip_gguf_open: null pointer");
+    *out = nullptr;
+    auto g = std::make_unique<cllm_hip_gguf>();
+    std::string err;
+    if (!cllm_hip::gguf_open(path, g->file, err)) return set_err(CLLM_HIP_E_ARG, "%s", err.c_str());
+    if (upload) {
+        DeviceState* st;
+        int rc = acquire(&st);
+        if (rc) return rc;
+        const cllm_hip::GgufFile& f = g->file;
+        const size_t bytes = f.map_bytes > f.data_offset ? f.map_bytes - f.data_offset : 0;
+        if (bytes > 0) {
+            // One pass over the data section through two pinned staging buffers: the host
+            // copy into one buffer overlaps the DMA out of the other.
+            constexpr size_t kChunk = 32u << 20;
+            void* stage[2] = {nullptr, nullptr};
+            hipEvent_t done[2] = {nullptr, nullptr};
+            std::lock_guard<std::mutex> lk(st->mtx);
+            hipError_t e = hipMalloc(&g->dev, bytes);
+            for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+                e = hipHostMalloc(&stage[i], kChunk, hipHostMallocDefault);
+                if (e == hipSuccess) e = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
+            }
+            const uint8_t* src = (const uint8_t*)f.map + f.data_offset;
+            for (size_t off = 0, i = 0; e == hipSuccess && off < bytes; off += kChunk, ++i) {
+                const size_t len = std::min(kChunk, bytes - off);
+                const int b = (int)(i & 1);
+                if (i >= 2) e = hipEventSynchronize(done[b]);
+                if (e != hipSuccess) break;
+                std::memcpy(stage[b], src + off, len);
+                e = hipMemcpyAsync((char*)g->dev + off, stage[b], len, hipMemcpyHostToDevice,
+                                   st->stream);
+                if (e == hipSuccess) e = hipEventRecord(done[b], st->stream);
+            }
+            if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
+            for (int i = 0; i < 2; ++i) {
+                if (done[i]) (void)hipEventDestroy(done[i]);
+                if (stage[i]) (void)hipHostFree(stage[i]);
+            }
+            if (e != hipSuccess) {
+                if (g->dev) (void)hipFree(g->dev);
+                return set_err(CLLM_HIP_E_RUNTIME, "cllm_hip_gguf_open: upload failed: %s",
+                               hipGetErrorString(e));
+            }
+            g->dev_bytes = bytes;
+            g->device = current_device();
+            // host pointers into the data section now resolve to the device copy
+            st->regions[(uintptr_t)src] = Region{bytes, g->dev, g->dev};
+        }
+    }
+    *out = g.release();
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_gguf_close(cllm_hip_gguf* g) {
+    if (!g) return CLLM_HIP_OK;
+    std::unique_ptr<cllm_hip_gguf> own(g);
+    if (g->dev) {
+        const int saved = g_device;
+        g_device = g->device;
+        DeviceState* st;
+        int rc = acquire(&st);
+        g_device = saved;
+        if (rc) return rc;
+        std::lock_guard<std::mutex> lk(st->mtx);
+        st->regions.erase((uintptr_t)g->file.map + g->file.data_offset);
+        HIP_TRY(hipStreamSynchronize(st->stream));
+        HIP_TRY(hipFree(g->dev));
+        g->dev = nullptr;
+    }
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_gguf_tensor_count(const cllm_hip_gguf* g) { return g ? (int)g->file.tensors.size() : 0; }
+
+int cllm_hip_gguf_find(const cllm_hip_gguf* g, const char* name) {
+    if (!g || !name) return -1;
+    auto it = g->file.index.find(name);
+    return it == g->file.index.end() ? -1 : it->second;
+}
+
+int cllm_hip_gguf_tensor(const cllm_hip_gguf* g, int i, const char** name, uint32_t* type,
+                         int* n_dims, uint64_t* dims, uint64_t* offset, const void** host,
+                         const void** dev) {
+    if (!g || i < 0 || i >= (int)g->file.tensors.size())
+        return set_err(CLLM_HIP_E_ARG, "cllm_hip_gguf_tensor: no tensor %d", i);
+    const cllm_hip::GgufTensor& t = g->file.tensors[(size_t)i];
+    if (name) *name = t.name.c_str();
+    if (type) *type = t.type;
+    if (n_dims) *n_dims = (int)t.shape.size();
+    if (dims)
+        for (size_t d = 0; d < t.shape.size() && d < 4; ++d) dims[d] = t.shape[d];
+    if (offset) *offset = t.offset;
+    const size_t at = g->file.data_offset + t.offset;
+    if (host) *host = (const uint8_t*)g->file.map + at;
+    if (dev) *dev = g->dev ? (const uint8_t*)g->dev + t.offset : nullptr;
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_gguf_config(const cllm_hip_gguf* g, cllm_hip_model_config* c) {
+    if (!g || !c) return set_err(CLLM_HIP_E_ARG, "cllm_hip_gguf_config: null pointer");
+    const cllm_hip::GgufConfig& f = g->file.config;
+    std::memset(c, 0, sizeof *c);
+    std::snprintf(c->arch, sizeof c->arch, "%s", f.arch.c_str());
+    c->n_layers = f.n_layers;
+    c->n_embd = f.n_embd;
+    c->n_head = f.n_head;
+    c->n_head_kv = f.n_head_kv;
+    c->n_ctx = f.n_ctx;
+    c->n_ff = f.n_ff;
+    c->vocab_size = f.vocab_size;
+    c->head_dim = f.head_dim_explicit > 0 ? f.head_dim_explicit : (f.n_head ? f.n_embd / f.n_head : 0);
+    c->rope_theta = f.rope_theta;
+    c->norm_eps = f.norm_eps;
+    c->version = g->file.version;
+    c->data_offset = g->file.data_offset;
+    c->data_bytes = g->file.map_bytes > g->file.data_offset ? g->file.map_bytes - g->file.data_offset : 0;
     return CLLM_HIP_OK;
 }
 

@@ -150,6 +150,42 @@ int cllm_hip_swiglu_q8_0_dev(const float* gate, const float* up, int n, int n_ro
 /* x[i] += d[i], i < n: the residual adds (src/core/engine.cpp:506, 513, 587, 598). */
 int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream);
 
+/* ---- GGUF files ------------------------------------------------------------------------ */
+
+/* A GGUF file mapped read-only, parsed like GgufLoader::load (src/core/gguf.cpp:122-275):
+ * version 2 or 3, the tensor table, the data section at the next multiple of 32 bytes after
+ * the table, and the hyper-parameters under "<arch>." (falling back to "llama.").
+ * Errors carry the reference's messages ("cannot open model file: ...", "invalid GGUF
+ * magic", "unsupported GGUF version: N", "read_u32", ...). */
+typedef struct cllm_hip_gguf cllm_hip_gguf;
+
+/* ModelConfig (include/cllm/core/gguf.hpp:13-34), head_dim resolved, plus the file's layout. */
+typedef struct {
+    char arch[64];
+    uint32_t n_layers, n_embd, n_head, n_head_kv, n_ctx, n_ff, vocab_size, head_dim;
+    float rope_theta, norm_eps;
+    uint32_t version;
+    uint64_t data_offset, data_bytes;
+} cllm_hip_model_config;
+
+/* Opens and parses path. With upload != 0 the data section is copied to the current device
+ * once (pinned, double-buffered) and registered like cllm_hip_register_weights, so host
+ * tensor pointers of this file resolve to the device copy in every matmul call. Replaces
+ * the engine's zero-copy mmap use (engine.cpp:182-199) for the GPU. */
+int cllm_hip_gguf_open(const char* path, int upload, cllm_hip_gguf** out);
+/* Unregisters and frees the device copy, unmaps the file. */
+int cllm_hip_gguf_close(cllm_hip_gguf* g);
+int cllm_hip_gguf_tensor_count(const cllm_hip_gguf* g);
+/* Index of the tensor called name, -1 if none. */
+int cllm_hip_gguf_find(const cllm_hip_gguf* g, const char* name);
+/* Tensor i: name, GgmlType id, dims rows-first (up to 4, the file's order reversed like
+ * Tensor::shape, gguf.cpp:163-165), offset in the data section, host address in the
+ * mapping, device address (null without upload). Any output may be null. */
+int cllm_hip_gguf_tensor(const cllm_hip_gguf* g, int i, const char** name, uint32_t* type,
+                         int* n_dims, uint64_t* dims, uint64_t* offset, const void** host,
+                         const void** dev);
+int cllm_hip_gguf_config(const cllm_hip_gguf* g, cllm_hip_model_config* cfg);
+
 /* Name of the kernel family cllm_hip_matmul_quant_dev would run for this shape: "gemv" or
  * "mfma" (vec_dot types), "fdot" (the float-dot kernels of the other types), "none" (no
  * GGML type); for tests and benchmarks. */

@@ -136,10 +136,34 @@ class Oracle(_Lib):
 
 
 class Reference(_Lib):
-    """The reference's quant.cpp + thread_pool.cpp, compiled unmodified (oracle/Makefile)."""
+    """The reference's quant.cpp + thread_pool.cpp + gguf.cpp, compiled unmodified
+    (oracle/Makefile)."""
 
     def __init__(self, path: str = REF_SO):
         super().__init__(path, "ref_")
+
+    def gguf_dump(self, path: str):
+        """GgufLoader::load(path) as (config fields, [(name, type, shape, offset, data_delta)])."""
+        f = self.lib.ref_gguf_dump
+        f.restype, f.argtypes = ctypes.c_long, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_size_t]
+        buf = ctypes.create_string_buffer(1 << 22)
+        n = f(str(path).encode(), buf, len(buf))
+        if n < 0:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+        lines = buf.raw[:n].decode().splitlines()
+        head = lines[0].split()
+        cfg = dict(arch="" if head[0] == "-" else head[0],
+                   **{k: int(v) for k, v in zip(("n_layers", "n_embd", "n_head", "n_head_kv",
+                                                 "n_ctx", "n_ff", "vocab_size", "head_dim"),
+                                                head[1:9])},
+                   rope_theta=float.fromhex(head[9]), norm_eps=float.fromhex(head[10]))
+        tensors = []
+        for ln in lines[1:]:
+            p = ln.split()
+            nd = int(p[2])
+            tensors.append((p[0], int(p[1]), tuple(int(v) for v in p[3:3 + nd]), int(p[3 + nd]),
+                            int(p[4 + nd])))
+        return cfg, tensors
 
 
 def oracle() -> Oracle:

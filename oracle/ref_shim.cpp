@@ -3,7 +3,9 @@
 // compiled from its unmodified sources (src/core/quant.cpp, src/core/thread_pool.cpp).
 //
 // TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile into oracle/_ref/, never shipped.
-// Interfaces wrapped: include/cllm/core/quant.hpp:90-151, include/cllm/core/thread_pool.hpp:12-24.
+// Interfaces wrapped: include/cllm/core/quant.hpp:90-151, include/cllm/core/thread_pool.hpp:12-24,
+// include/cllm/core/gguf.hpp:79-82 (GgufLoader::load, for the GGUF reader's parity).
+#include "cllm/core/gguf.hpp"
 #include "cllm/core/quant.hpp"
 #include "cllm/core/thread_pool.hpp"
 
@@ -90,3 +92,48 @@ int ref_matmul_quant_batch(const float* x, const void* w, uint32_t t, const floa
 }
 
 }  // extern "C"
+
+// GgufLoader::load of path, written as text into buf (cap bytes): one line
+//   arch n_layers n_embd n_head n_head_kv n_ctx n_ff vocab_size head_dim rope_theta norm_eps
+// (floats as %a), then one line per tensor in file order:
+//   name type n_dims dim... offset data_delta
+// where data_delta is the tensor's data pointer minus the mapping's base. Returns the length
+// written (truncated at cap), or -1 with ref_last_error() set.
+extern "C" long ref_gguf_dump(const char* path, char* buf, size_t cap) {
+    try {
+        cllm::GgufModel m = cllm::GgufLoader::load(path);
+        std::string out;
+        char line[512];
+        const cllm::ModelConfig& c = m.config;
+        std::snprintf(line, sizeof line, "%s %u %u %u %u %u %u %u %u %a %a\n",
+                      c.arch.empty() ? "-" : c.arch.c_str(), c.n_layers, c.n_embd, c.n_head,
+                      c.n_head_kv, c.n_ctx, c.n_ff, c.vocab_size,
+                      c.n_head ? c.head_dim() : c.head_dim_explicit, (double)c.rope_theta,
+                      (double)c.norm_eps);
+        out += line;
+        std::vector<std::pair<std::string, const cllm::Tensor*>> named;
+        for (const auto& kv : m.tensors) named.emplace_back(kv.first, &kv.second);
+        for (const cllm::Tensor& t : m.tensor_list) {
+            const std::string* name = nullptr;
+            for (const auto& nt : named)
+                if (nt.second->data == t.data && nt.second->offset == t.offset) name = &nt.first;
+            std::snprintf(line, sizeof line, "%s %u %zu", name ? name->c_str() : "?",
+                          (unsigned)t.type, t.shape.size());
+            out += line;
+            for (uint32_t d : t.shape) {
+                std::snprintf(line, sizeof line, " %u", d);
+                out += line;
+            }
+            std::snprintf(line, sizeof line, " %llu %lld\n", (unsigned long long)t.offset,
+                          (long long)((const char*)t.data - (const char*)m.mmap_base));
+            out += line;
+        }
+        const size_t n = out.size() < cap ? out.size() : cap;
+        std::memcpy(buf, out.data(), n);
+        return (long)n;
+    } catch (const std::exception& e) {
+        set_err(e);
+        return -1;
+    }
+}
+
