@@ -19,8 +19,8 @@
 //
 // Activations. The MR activation rows of a workgroup's token group are staged in LDS as fp32
 // with 16 bytes of padding after every 32 values, so the 16-byte reads of the lanes (units at
-// a stride of 144 bytes) spread over all 64 banks. Rows too long for the LDS budget are read
-// from global memory instead (they stay in L2).
+// a stride of 144 bytes) spread over all 64 banks. Rows too long for the LDS budget (80 KB,
+// two workgroups per CU) are read from global memory instead (they stay in L2).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -34,7 +34,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr size_t kLdsBudget = 64 * 1024;
+constexpr size_t kLdsBudget = 80 * 1024;  // two workgroups per CU
 
 // byte b (0..3) of dword v as a float: v_cvt_f32_ubyte{0..3}
 __device__ __forceinline__ float ubyte_f(uint32_t v, int b) {

@@ -152,11 +152,11 @@ def batch_fixtures(ref: oracle.Reference) -> None:
 def fdot_fixtures(ref: oracle.Reference) -> None:
     """The types without a vec_dot kernel (the reference's dequantize-and-float-dot fallback,
     src/core/quant.cpp:1404-1430): short and long rows, batches of 1-5 rows, rows too long
-    for one LDS-resident activation row, and F16 / F32 rows whose length is not a multiple
-    of 32."""
+    for an LDS-resident activation row (18432), and F16 / F32 rows whose length is not a
+    multiple of 32."""
     data = {}
     shapes = [(300, 256, 1), (64, 4096, 1), (257, 4096, 3), (100, 1024, 5), (16, 16640, 1),
-              (16, 16640, 3), (50, 33, 2), (40, 100, 1)]
+              (16, 16640, 3), (16, 18432, 1), (16, 18432, 3), (50, 33, 2), (40, 100, 1)]
     for qt in S.FLOAT_DOT_TYPES:
         for (n, k, m) in shapes:
             if k % S.BLOCK[qt]:

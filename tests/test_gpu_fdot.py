@@ -49,8 +49,8 @@ def test_fdot_vs_reference_golden(gpu, orc):
 
 @pytest.mark.parametrize("qt", FD_TYPES)
 def test_fdot_batch_rows_equal_single_rows(gpu, qt):
-    # k = 4096 stages the activation rows in LDS, k = 16640 reads them from global memory
-    for k, m in ((4096, 6), (16640, 3)):
+    # k = 4096 stages the activation rows in LDS, k = 18432 reads them from global memory
+    for k, m in ((4096, 6), (18432, 3)):
         n = 75
         w = S.make_weight(qt, n, k, 31 + k)
         x = S.make_activation(m, k, 32 + k, outliers=True)
