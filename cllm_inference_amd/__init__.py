@@ -76,6 +76,8 @@ SIGNATURES = {
                                   ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(_P),
                                   ctypes.POINTER(_P)]),
     "cllm_hip_gguf_config": (_I, [_P, _P]),
+    "cllm_hip_rope_neox_dev": (_I, [_P, _I, _I, _I, _I, ctypes.c_float, _P]),
+    "cllm_hip_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
 }
 
 
@@ -381,3 +383,30 @@ class GgufFile:
         c = ModelConfig()
         _check(load_library().cllm_hip_gguf_config(self._h, ctypes.byref(c)))
         return c
+
+
+# ---- float ops between the linear layers ------------------------------------------------
+
+def rope_neox_dev(x, n_heads: int, head_dim: int, pos0: int, theta_base: float):
+    """NEOX RoPE in place on x (float32 CUDA tensor of n_rows x n_heads x head_dim), row t at
+    position pos0 + t -- engine.cpp:41-56."""
+    n_rows = x.numel() // (n_heads * head_dim)
+    _check(load_library().cllm_hip_rope_neox_dev(_tp(x), int(n_rows), int(n_heads),
+                                                 int(head_dim), int(pos0), float(theta_base),
+                                                 _stream()))
+    return x
+
+
+def attention_dev(q, k_cache, v_cache, pos0: int, n_head: int, n_head_kv: int, head_dim: int,
+                  out=None):
+    """Grouped-query attention of the query rows q (n_rows x n_head x head_dim) over the
+    caches (positions x n_head_kv x head_dim); row t sees positions [0, pos0 + t] --
+    engine.cpp:114-146."""
+    import torch
+    n_rows = q.numel() // (n_head * head_dim)
+    if out is None:
+        out = torch.empty((n_rows, n_head * head_dim), dtype=torch.float32, device=q.device)
+    _check(load_library().cllm_hip_attention_dev(_tp(q), _tp(k_cache), _tp(v_cache), int(n_rows),
+                                                 int(pos0), int(n_head), int(n_head_kv),
+                                                 int(head_dim), _tp(out), _stream()))
+    return out

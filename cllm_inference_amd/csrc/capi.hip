@@ -77,6 +77,7 @@ struct DevBuf {
 struct Workspace {
     DevBuf buf;
     DevBuf part;  // split-K partial sums of the weight-row GEMM
+    DevBuf att;   // sequence-split partials of the attention kernel
     int8_t* qs = nullptr;
     float* sc = nullptr;
     int32_t* bs = nullptr;
@@ -650,6 +651,49 @@ int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream) {
     int rc = acquire(&st);
     if (rc) return rc;
     HIP_TRY(launch_add(x, d, n, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_rope_neox_dev(float* x, int n_rows, int n_heads, int head_dim, int pos0,
+                           float theta_base, void* stream) {
+    if (n_rows < 0 || n_heads < 0 || head_dim <= 0 || head_dim % 2 != 0 || head_dim > 512 ||
+        pos0 < 0)
+        return set_err(CLLM_HIP_E_ARG, "rope: bad shape");
+    if (n_rows == 0 || n_heads == 0) return CLLM_HIP_OK;
+    if (!x) return set_err(CLLM_HIP_E_ARG, "rope: null pointer");
+    if ((uintptr_t)x & 3u) return set_err(CLLM_HIP_E_ARG, "rope: misaligned device pointer");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    HIP_TRY(launch_rope_neox(x, n_rows, n_heads, head_dim, pos0, theta_base, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_cache,
+                           int n_rows, int pos0, int n_head, int n_head_kv, int head_dim,
+                           float* out, void* stream) {
+    if (n_rows < 0 || pos0 < 0) return set_err(CLLM_HIP_E_ARG, "attention: bad shape");
+    if (!attention_supported(head_dim, n_head, n_head_kv))
+        return set_err(CLLM_HIP_E_ARG,
+                       "attention: head_dim must be 64, 128 or 256 and n_head a multiple of "
+                       "n_head_kv, at most 8 query heads per KV head");
+    if (n_rows == 0) return CLLM_HIP_OK;
+    if (!q || !k_cache || !v_cache || !out) return set_err(CLLM_HIP_E_ARG, "attention: null pointer");
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || ((uintptr_t)out & 3u))
+        return set_err(CLLM_HIP_E_ARG, "attention: misaligned device pointer");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    Workspace* ws;
+    if ((rc = stream_workspace(st, s, 32, 1, &ws))) return rc;
+    const size_t floats = attention_partial_floats(n_rows, n_head, head_dim);
+    {
+        std::lock_guard<std::mutex> lk(st->mtx);
+        HIP_TRY(ws->att.ensure(floats * sizeof(float), s));
+    }
+    HIP_TRY(launch_attention(q, k_cache, v_cache, n_rows, pos0, n_head, n_head_kv, head_dim, out,
+                             (float*)ws->att.p, ws->att.cap / sizeof(float), s));
     return CLLM_HIP_OK;
 }
 

@@ -1,0 +1,268 @@
+// k_attention.hip -- the float ops between the linear layers on the device: NEOX RoPE and
+// grouped-query attention over a KV cache (decode and prefill).
+//
+// Reference (src/core/engine.cpp):
+//   apply_rope (41-56): per head, pairs (i, i + half), theta = pos / base^(i / half),
+//     x_i' = x_i cos - x_{i+half} sin, x_{i+half}' = x_i sin + x_{i+half} cos;
+//   attention (114-146): per query head h (KV head h / n_rep), s_t = dot(q_h, k_t) / sqrt(d)
+//     over the t < seq cached positions, softmax (max subtracted, exp, sum), then
+//     out_h = sum_t (e_t / sum) v_t; decode (495) and prefill (581-583, query t of the
+//     batch sees pos0 + t + 1 positions).
+//
+// Attention layout. One workgroup per (KV head, query row, sequence split); it serves the
+// n_rep query heads of that KV head, so every K and V row is loaded once for all of them.
+// Positions go in chunks of 64: sixteen lanes per position read the K row (16-byte pieces,
+// coalesced), each lane dots its slice with every query head held in registers, a 16-lane
+// reduction gives the scores; the softmax is online (running max and sum per head, the
+// partial output rescaled when the max grows); then the threads owning output elements
+// (head, d) add p_t v_t[d] for the chunk's positions, reading V rows coalesced along d.
+// Long sequences are split over several workgroups whose (max, sum, unnormalised output)
+// partials a second kernel combines, so a decode step (one query row) still spreads over
+// the device. The summation order differs from the reference's (per-chunk and per-split
+// partial sums, output divided by the sum once); the arithmetic is otherwise the same
+// fp32 operations with the device's expf, sinf, cosf and powf.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+
+#include "device_utils.h"
+#include "launch.h"
+
+namespace cllm_hip {
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------------- RoPE
+
+// grid (rows, heads), half = head_dim / 2 threads (up to 256): row t has position pos0 + t.
+__global__ __launch_bounds__(256) void k_rope_neox(float* __restrict__ x, int n_heads,
+                                                   int head_dim, int pos0, float base) {
+    const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+    const int half = head_dim / 2;
+    if (i >= half) return;
+    float* xh = x + ((size_t)t * n_heads + h) * head_dim;
+    const float theta = __fdiv_rn((float)(pos0 + t), powf(base, __fdiv_rn((float)i, (float)half)));
+    const float c = cosf(theta), s = sinf(theta);
+    const float x0 = xh[i], x1 = xh[i + half];
+    xh[i] = __builtin_fmaf(x0, c, -__fmul_rn(x1, s));
+    xh[i + half] = __builtin_fmaf(x0, s, __fmul_rn(x1, c));
+}
+
+// ----------------------------------------------------------------------------- attention
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 64;       // positions per online-softmax step
+constexpr int kLanesPerPos = 16; // lanes sharing one K row
+constexpr int kMaxRep = 8;       // query heads per KV head
+
+// HD = head_dim (multiple of 64, at most 256). Partials of split z for query head hq of row
+// t: part[((t * n_head + hq) * S + z) * (HD + 2) + ...] = unnormalised output [HD], max, sum.
+// With one split, the normalised output goes straight to out.
+template <int HD>
+__global__ __launch_bounds__(kThreads) void k_attention(
+    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    int n_head, int n_kv, int pos0, int split_len, float scale, float* __restrict__ part,
+    float* __restrict__ out) {
+    constexpr int PER = HD / kLanesPerPos;  // K elements per lane (4 .. 16)
+    constexpr int NOUT = kMaxRep * HD / kThreads > 0 ? (kMaxRep * HD + kThreads - 1) / kThreads : 1;
+    __shared__ float sc[kMaxRep][kChunk];
+    __shared__ float m_run[kMaxRep], l_run[kMaxRep], corr[kMaxRep];
+
+    const int kvh = blockIdx.x, t = blockIdx.y, z = blockIdx.z, S = gridDim.z;
+    const int n_rep = n_head / n_kv;
+    const int kv_dim = n_kv * HD;
+    const int L = pos0 + t + 1;
+    const int begin = z * split_len;
+    const int end = min(L, begin + split_len);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int seg = lane % kLanesPerPos, sub = lane / kLanesPerPos;  // sub: position in wave
+
+    // this lane's slice of every query head of the group
+    float qv[kMaxRep][PER];
+#pragma unroll
+    for (int r = 0; r < kMaxRep; ++r) {
+        const float* qh = q + ((size_t)t * n_head + kvh * n_rep + min(r, n_rep - 1)) * HD + seg * PER;
+#pragma unroll
+        for (int e = 0; e < PER; e += 4) {
+            const f32x4 v = *(const f32x4*)(qh + e);
+            qv[r][e] = v.x; qv[r][e + 1] = v.y; qv[r][e + 2] = v.z; qv[r][e + 3] = v.w;
+        }
+    }
+    // output elements (head r, dim d) owned by this thread: index o = threadIdx.x + kThreads i
+    float acc[NOUT];
+#pragma unroll
+    for (int i = 0; i < NOUT; ++i) acc[i] = 0.0f;
+    if (threadIdx.x < kMaxRep) {
+        m_run[threadIdx.x] = -INFINITY;
+        l_run[threadIdx.x] = 0.0f;
+    }
+    __syncthreads();
+
+    for (int c0 = begin; c0 < end; c0 += kChunk) {
+        // scores of the chunk: each wave takes 4 positions per round, 4 rounds
+#pragma unroll
+        for (int round = 0; round < kChunk / 16; ++round) {
+            const int slot = round * 16 + wave * 4 + sub;
+            const int p = c0 + slot;
+            const int pc = min(p, end - 1);
+            const float* kr = kc + (size_t)pc * kv_dim + kvh * HD + seg * PER;
+            float kv[PER];
+#pragma unroll
+            for (int e = 0; e < PER; e += 4) {
+                const f32x4 v = *(const f32x4*)(kr + e);
+                kv[e] = v.x; kv[e + 1] = v.y; kv[e + 2] = v.z; kv[e + 3] = v.w;
+            }
+#pragma unroll
+            for (int r = 0; r < kMaxRep; ++r) {
+                if (r >= n_rep) break;
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < PER; ++e) d = __builtin_fmaf(qv[r][e], kv[e], d);
+                d += __shfl_xor(d, 8, 16);
+                d += __shfl_xor(d, 4, 16);
+                d += __shfl_xor(d, 2, 16);
+                d += __shfl_xor(d, 1, 16);
+                if (seg == 0) sc[r][slot] = p < end ? __fmul_rn(d, scale) : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // running max per head; the factor that rescales what is already summed
+        if (threadIdx.x < n_rep) {
+            const int r = threadIdx.x;
+            float cm = -INFINITY;
+            for (int i = 0; i < kChunk; ++i) cm = fmaxf(cm, sc[r][i]);
+            const float mo = m_run[r], mn = fmaxf(mo, cm);
+            corr[r] = mo == -INFINITY ? 0.0f : expf(mo - mn);
+            m_run[r] = mn;
+        }
+        __syncthreads();
+        // probabilities (relative to the running max) in place of the scores
+        for (int i = threadIdx.x; i < n_rep * kChunk; i += kThreads) {
+            const int r = i / kChunk, j = i - r * kChunk;
+            const float s = sc[r][j];
+            sc[r][j] = s == -INFINITY ? 0.0f : expf(s - m_run[r]);
+        }
+        __syncthreads();
+        if (threadIdx.x < n_rep) {
+            const int r = threadIdx.x;
+            float l = l_run[r] * corr[r];
+            for (int i = 0; i < kChunk; ++i) l += sc[r][i];
+            l_run[r] = l;
+        }
+        const int nv = min(kChunk, end - c0);
+#pragma unroll
+        for (int i = 0; i < NOUT; ++i) {
+            const int o = threadIdx.x + kThreads * i;
+            const int r = o / HD, d = o - r * HD;
+            if (r < n_rep) {
+                float a = acc[i] * corr[r];
+                const float* vr = vc + (size_t)c0 * kv_dim + kvh * HD + d;
+                for (int j = 0; j < nv; ++j) a = __builtin_fmaf(sc[r][j], vr[(size_t)j * kv_dim], a);
+                acc[i] = a;
+            }
+        }
+        __syncthreads();
+    }
+
+    // write the split's partial, or the normalised output
+#pragma unroll
+    for (int i = 0; i < NOUT; ++i) {
+        const int o = threadIdx.x + kThreads * i;
+        const int r = o / HD, d = o - r * HD;
+        if (r >= n_rep) continue;
+        const int hq = kvh * n_rep + r;
+        if (S == 1) {
+            out[((size_t)t * n_head + hq) * HD + d] = __fdiv_rn(acc[i], l_run[r]);
+        } else {
+            float* pp = part + (((size_t)t * n_head + hq) * S + z) * (HD + 2);
+            pp[d] = acc[i];
+            if (d == 0) {
+                pp[HD] = m_run[r];
+                pp[HD + 1] = l_run[r];
+            }
+        }
+    }
+}
+
+// grid (n_head, rows), HD threads: out = sum_z e^(m_z - M) o_z / sum_z e^(m_z - M) l_z.
+__global__ __launch_bounds__(256) void k_attention_combine(const float* __restrict__ part,
+                                                           int n_head, int hd, int S,
+                                                           float* __restrict__ out) {
+    const int hq = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+    if (d >= hd) return;
+    const float* pp = part + ((size_t)t * n_head + hq) * S * (hd + 2);
+    float M = -INFINITY;
+    for (int z = 0; z < S; ++z) M = fmaxf(M, pp[(size_t)z * (hd + 2) + hd]);
+    float num = 0.0f, den = 0.0f;
+    for (int z = 0; z < S; ++z) {
+        const float* p = pp + (size_t)z * (hd + 2);
+        const float m = p[hd];
+        if (m == -INFINITY) continue;
+        const float w = expf(m - M);
+        num = __builtin_fmaf(w, p[d], num);
+        den = __builtin_fmaf(w, p[hd + 1], den);
+    }
+    out[((size_t)t * n_head + hq) * hd + d] = __fdiv_rn(num, den);
+}
+
+template <int HD>
+hipError_t launch_attention_hd(const float* q, const float* kc, const float* vc, int rows,
+                               int pos0, int n_head, int n_kv, float* out, float* part,
+                               size_t part_floats, hipStream_t stream) {
+    const int L_max = pos0 + rows;
+    // splits: enough workgroups for the device, at least one chunk per split
+    const int64_t base = (int64_t)n_kv * rows;
+    int S = (int)std::min<int64_t>(std::max<int64_t>(1, (1024 + base - 1) / base),
+                                   (L_max + kChunk - 1) / kChunk);
+    if ((size_t)rows * n_head * S * (HD + 2) > part_floats) S = 1;
+    const int split_len = ((L_max + S - 1) / S + kChunk - 1) / kChunk * kChunk;
+    S = (L_max + split_len - 1) / split_len;
+    const float scale = 1.0f / std::sqrt((float)HD);  // engine.cpp:121, IEEE on the host
+    hipLaunchKernelGGL((k_attention<HD>), dim3((unsigned)n_kv, (unsigned)rows, (unsigned)S),
+                       dim3(kThreads), 0, stream, q, kc, vc, n_head, n_kv, pos0, split_len, scale,
+                       part, out);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || S == 1) return e;
+    hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)n_head, (unsigned)rows), dim3(HD), 0,
+                       stream, part, n_head, HD, S, out);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_rope_neox(float* x, int rows, int n_heads, int head_dim, int pos0, float base,
+                            hipStream_t stream) {
+    if (rows <= 0 || n_heads <= 0) return hipSuccess;
+    if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 512) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rope_neox, dim3((unsigned)rows, (unsigned)n_heads), dim3(256), 0, stream,
+                       x, n_heads, head_dim, pos0, base);
+    return hipGetLastError();
+}
+
+size_t attention_partial_floats(int rows, int n_head, int head_dim) {
+    // at most 1024 / (n_kv * rows) + 1 splits, n_kv >= 1
+    const size_t splits = (size_t)(1024 / std::max(rows, 1) + 1);
+    return (size_t)rows * n_head * splits * (head_dim + 2);
+}
+
+bool attention_supported(int head_dim, int n_head, int n_kv) {
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && n_kv > 0 &&
+           n_head % n_kv == 0 && n_head / n_kv <= kMaxRep;
+}
+
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int pos0,
+                            int n_head, int n_kv, int head_dim, float* out, float* part,
+                            size_t part_floats, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (!attention_supported(head_dim, n_head, n_kv)) return hipErrorInvalidValue;
+    switch (head_dim) {
+        case 64: return launch_attention_hd<64>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, stream);
+        case 128: return launch_attention_hd<128>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, stream);
+        default: return launch_attention_hd<256>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, stream);
+    }
+}
+
+}  // namespace cllm_hip

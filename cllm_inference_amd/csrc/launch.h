@@ -90,6 +90,19 @@ hipError_t launch_swiglu_q8_0(const float* gate, const float* up, int64_t total,
                               int8_t* qs, float* scales, int32_t* bsums, hipStream_t stream);
 hipError_t launch_add(float* x, const float* d, int64_t n, hipStream_t stream);
 
+// Float ops between the linear layers (k_attention.hip): NEOX RoPE in place on `rows` rows
+// of n_heads x head_dim (row t at position pos0 + t), and grouped-query attention of `rows`
+// query rows (n_head x head_dim each) over KV caches of n_kv x head_dim per position, query
+// row t seeing positions [0, pos0 + t]. `part` (at least attention_partial_floats floats, or
+// null for no sequence split) holds the split partials.
+hipError_t launch_rope_neox(float* x, int rows, int n_heads, int head_dim, int pos0, float base,
+                            hipStream_t stream);
+bool attention_supported(int head_dim, int n_head, int n_kv);
+size_t attention_partial_floats(int rows, int n_head, int head_dim);
+hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int pos0,
+                            int n_head, int n_kv, int head_dim, float* out, float* part,
+                            size_t part_floats, hipStream_t stream);
+
 // Float-dot GEMV (k_gemv_f.hip) for the types without a vec_dot kernel (F32, F16, Q4_1,
 // Q5_1, Q8_1, Q2_K, Q3_K): y[t, j] = bias[j] + sum_i x[t, i] * deq(W[j, i]) on fp32
 // activation rows x[m][k], as the reference's dequantize fallback computes it.

@@ -150,6 +150,23 @@ int cllm_hip_swiglu_q8_0_dev(const float* gate, const float* up, int n, int n_ro
 /* x[i] += d[i], i < n: the residual adds (src/core/engine.cpp:506, 513, 587, 598). */
 int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream);
 
+/* ---- float ops between the linear layers (stream-ordered) ----------------------------- */
+
+/* NEOX RoPE in place (apply_rope, src/core/engine.cpp:41-56): x holds n_rows rows of
+ * n_heads x head_dim; row t sits at position pos0 + t; pair (i, i + head_dim / 2) of each
+ * head turns by (pos0 + t) / theta_base^(i / (head_dim / 2)). */
+int cllm_hip_rope_neox_dev(float* x, int n_rows, int n_heads, int head_dim, int pos0,
+                           float theta_base, void* stream);
+
+/* Grouped-query attention (attention, src/core/engine.cpp:114-146): q holds n_rows rows of
+ * n_head x head_dim; the caches hold n_head_kv x head_dim per position, positions
+ * [0, pos0 + n_rows) filled; query row t sees positions [0, pos0 + t] (decode: n_rows = 1,
+ * pos0 = the new token's position; prefill: engine.cpp:581-583). out: n_rows rows of
+ * n_head x head_dim. head_dim 64, 128 or 256; n_head / n_head_kv at most 8. */
+int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_cache,
+                           int n_rows, int pos0, int n_head, int n_head_kv, int head_dim,
+                           float* out, void* stream);
+
 /* ---- GGUF files ------------------------------------------------------------------------ */
 
 /* A GGUF file mapped read-only, parsed like GgufLoader::load (src/core/gguf.cpp:122-275):
