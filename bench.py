@@ -209,6 +209,44 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
     return per
 
 
+def decode_model(C, S, steps, warmup, n_layers=4, pos=1024):
+    """A whole decode step on the device (embedding lookup, n_layers Llama-3-8B layers in the
+    Q4_K_M mix with attention over `pos` cached positions, final norm, Q6_K head of 128256
+    rows), from a GGUF file uploaded once; the per-layer figure gives a 32-layer projection.
+    Random weights, synthetic cache contents."""
+    import tempfile
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import device_model as DM
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "llama3_8b_slice.gguf")
+        DM.write_model(path, arch="llama", n_layers=n_layers, n_embd=4096, n_head=32, n_kv=8,
+                       n_ff=14336, vocab=128256, n_ctx=pos + 8, wtype=S.Q4_K,
+                       wtype_down=S.Q6_K, emb_type=S.Q4_K, out_type=S.Q6_K, seed=11)
+        m = DM.DeviceModel(path)
+    for kc, vc in zip(m.k_cache, m.v_cache):
+        kc.normal_()
+        vc.normal_()
+    ids = torch.tensor([1234], dtype=torch.int32, device="cuda")
+    ms = time_loop(lambda i: m.step_ids(ids, pos), steps, warmup)
+    head_w = m.t["output.weight"]
+    head_bytes = S.row_bytes(head_w.type, 4096) * 128256
+    layer_bytes = sum(S.row_bytes(qt, k) * n for _, qt, n, k in S.CONFIGS["c3_q4_k_m_layer"]["mats"])
+    kv_bytes = 2 * (pos + 1) * 8 * 128 * 4
+    m.close()
+    # per layer: the step minus the head GEMV's share (its bytes at the step's mean rate)
+    total = n_layers * (layer_bytes + kv_bytes) + head_bytes
+    layer_ms = ms * (layer_bytes + kv_bytes) / total
+    proj = 32 * layer_ms + ms * head_bytes / total
+    out = {"n_layers": n_layers, "kv_positions": pos, "step_us": round(ms * 1e3, 1),
+           "gbs": round(total / ms / 1e6, 1), "frac_hbm": round(total / ms / 1e6 / HBM_PEAK_GBS, 4),
+           "projected_llama3_8b_32_layer_tokens_per_s": round(1e3 / proj, 1)}
+    print(f"[bench] device decode step, {n_layers} layers at position {pos}: {ms * 1e3:.1f} us "
+          f"({total / ms / 1e6:.1f} GB/s); 32-layer projection {1e3 / proj:.1f} tokens/s",
+          file=sys.stderr, flush=True)
+    return out
+
+
 def gguf_upload(C, S, gib=1.0):
     """f2: the GGUF data section's one-time upload (parse, map, pinned double-buffered H2D,
     registration) for a synthetic file of `gib` GiB written to local temporary storage."""
@@ -311,6 +349,8 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the M=512 Q4_K_M layer (for counter profiles of the GEMM) and "
                          "print its figures as one JSON line")
+    ap.add_argument("--model-only", action="store_true",
+                    help="run only the whole-model decode step and print it as one JSON line")
     ap.add_argument("--upload-only", action="store_true",
                     help="run only the GGUF upload measurement and print it as one JSON line")
     ap.add_argument("--layer-only", action="store_true",
@@ -342,6 +382,11 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.model_only:
+        print(json.dumps({"f4_device_decode_step": decode_model(C, S, max(10, args.steps // 10),
+                                                                 max(2, args.warmup // 10))}))
+        return
 
     if args.upload_only:
         print(json.dumps({"f2_gguf_upload": gguf_upload(C, S)}))
@@ -399,6 +444,8 @@ def main():
         extra["f1_decode_layer_device"] = decode_layer_device(C, S, max(20, args.steps // 4),
                                                               max(3, args.warmup // 4))
         extra["f2_gguf_upload"] = gguf_upload(C, S)
+        extra["f4_device_decode_step"] = decode_model(C, S, max(10, args.steps // 10),
+                                                      max(2, args.warmup // 10))
 
     cpu = None
     if not args.no_cpu_baseline:

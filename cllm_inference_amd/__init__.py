@@ -77,6 +77,7 @@ SIGNATURES = {
                                   ctypes.POINTER(_P)]),
     "cllm_hip_gguf_config": (_I, [_P, _P]),
     "cllm_hip_rope_neox_dev": (_I, [_P, _I, _I, _I, _I, ctypes.c_float, _P]),
+    "cllm_hip_dequantize_rows_dev": (_I, [_P, _U, _I, _P, _I, _P, _P]),
     "cllm_hip_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
 }
 
@@ -409,4 +410,16 @@ def attention_dev(q, k_cache, v_cache, pos0: int, n_head: int, n_head_kv: int, h
     _check(load_library().cllm_hip_attention_dev(_tp(q), _tp(k_cache), _tp(v_cache), int(n_rows),
                                                  int(pos0), int(n_head), int(n_head_kv),
                                                  int(head_dim), _tp(out), _stream()))
+    return out
+
+
+def dequantize_rows_dev(w, t: int, in_dim: int, ids, out=None):
+    """Rows ids (int32 CUDA tensor) of the weight matrix w (uint8 CUDA tensor) as fp32 --
+    the embedding lookup, bit for bit like dequantize_block."""
+    import torch
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, in_dim), dtype=torch.float32, device=ids.device)
+    _check(load_library().cllm_hip_dequantize_rows_dev(_tp(w), int(t), int(in_dim), _tp(ids),
+                                                       int(n), _tp(out), _stream()))
     return out

@@ -654,6 +654,26 @@ int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream) {
     return CLLM_HIP_OK;
 }
 
+int cllm_hip_dequantize_rows_dev(const void* w, uint32_t type, int in_dim, const int32_t* ids,
+                                 int n_ids, float* out, void* stream) {
+    const int bs = block_elems(type);
+    if (!has_kernel(type) && !gemv_f_supported(type))
+        return set_err(CLLM_HIP_E_TYPE, "unsupported ggml type for dequantize");
+    if (in_dim <= 0 || in_dim % bs != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "dequantize: in_dim not divisible by block size");
+    if (n_ids < 0) return set_err(CLLM_HIP_E_ARG, "dequantize: negative row count");
+    if (n_ids == 0) return CLLM_HIP_OK;
+    if (!w || !ids || !out) return set_err(CLLM_HIP_E_ARG, "dequantize: null pointer");
+    if (!aligned16(w) || ((uintptr_t)ids & 3u) || ((uintptr_t)out & 15u))
+        return set_err(CLLM_HIP_E_ARG, "dequantize: misaligned device pointer");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    HIP_TRY(launch_dequantize_rows(type, (const uint8_t*)w, in_dim, ids, n_ids, out,
+                                   (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
 int cllm_hip_rope_neox_dev(float* x, int n_rows, int n_heads, int head_dim, int pos0,
                            float theta_base, void* stream) {
     if (n_rows < 0 || n_heads < 0 || head_dim <= 0 || head_dim % 2 != 0 || head_dim > 512 ||

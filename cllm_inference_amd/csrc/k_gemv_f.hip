@@ -32,6 +32,8 @@
 namespace cllm_hip {
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr size_t kLdsBudget = 80 * 1024;  // two workgroups per CU
@@ -254,6 +256,157 @@ template <> struct FUnit<T_Q3_K> {
     }
 };
 
+// The six vec_dot types, for the row dequantization below (the GEMV keeps their integer
+// kernels). Values as the reference's deq_* produce them (quant.cpp:39-161, 302-336).
+
+// Q8_0: [d][qs i8 x32], 34 bytes (2-byte aligned blocks): d * q
+template <> struct FUnit<T_Q8_0> {
+    struct Raw { uint32_t d; uint32_t q[8]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 34;
+        Raw r;
+        r.d = ld_u16(blk);
+        ld_a2<8>(blk + 2, r.q);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+        const float d = f16_to_f32(r.d);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) w[4 * i + b] = d * (float)(int8_t)((r.q[i] >> (8 * b)) & 0xFFu);
+    }
+};
+
+// Q4_0: [d][qs 16 B], 18 bytes: d * (q - 8), low nibble element j, high nibble j + 16
+template <> struct FUnit<T_Q4_0> {
+    struct Raw { uint32_t d; uint32_t q[4]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 18;
+        Raw r;
+        r.d = ld_u16(blk);
+        ld_a2<4>(blk + 2, r.q);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+        const float d = f16_to_f32(r.d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = r.q[i] & 0x0F0F0F0Fu, hi = (r.q[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                w[4 * i + b] = d * (ubyte_f(lo, b) - 8.0f);
+                w[16 + 4 * i + b] = d * (ubyte_f(hi, b) - 8.0f);
+            }
+        }
+    }
+};
+
+// Q5_0: [d][qh u32][qs 16 B], 22 bytes: d * (q - 16), bit j of qh = bit 4 of element j
+template <> struct FUnit<T_Q5_0> {
+    struct Raw { uint32_t d; uint32_t qh[1]; uint32_t q[4]; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 22;
+        Raw r;
+        r.d = ld_u16(blk);
+        ld_a2<1>(blk + 2, r.qh);
+        ld_a2<4>(blk + 6, r.q);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int, float (&w)[32]) {
+        const float d = f16_to_f32(r.d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int j = 4 * i + b;
+                const uint32_t byte = (r.q[i] >> (8 * b)) & 0xFFu;
+                const uint32_t q0 = (byte & 0xFu) | (((r.qh[0] >> j) & 1u) << 4);
+                const uint32_t q1 = (byte >> 4) | (((r.qh[0] >> (j + 16)) & 1u) << 4);
+                w[j] = d * ((float)q0 - 16.0f);
+                w[j + 16] = d * ((float)q1 - 16.0f);
+            }
+        }
+    }
+};
+
+// Q4_K / Q5_K: unit u = sub-block u of the super-block: low (u even) or high (u odd)
+// nibbles of the 32-byte chunk u / 2, Q5_K adding bit u of qh[l] as bit 4; value
+// d * sc_u * q - dmin * m_u (quant.cpp:82-108, 302-336).
+template <bool Q5>
+struct FUnitK45 {
+    struct Raw { uint32_t dd; uint32_t s[3]; u32x4 q0, q1, h0, h1; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 3) * (Q5 ? 176 : 144);
+        const int c = (u & 7) >> 1;
+        Raw r;
+        r.dd = *(const uint32_t*)blk;
+        r.s[0] = *(const uint32_t*)(blk + 4);
+        r.s[1] = *(const uint32_t*)(blk + 8);
+        r.s[2] = *(const uint32_t*)(blk + 12);
+        const u32x4* qs = (const u32x4*)(blk + (Q5 ? 48 : 16) + 32 * c);
+        r.q0 = qs[0];
+        r.q1 = qs[1];
+        if constexpr (Q5) {
+            r.h0 = *(const u32x4*)(blk + 16);
+            r.h1 = *(const u32x4*)(blk + 32);
+        }
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int u, float (&w)[32]) {
+        const int k = u & 7;
+        int sc, m;
+        k4_scale_min(r.s[0], r.s[1], r.s[2], k, sc, m);
+        const float d1 = f16_to_f32(r.dd & 0xFFFFu) * (float)sc;
+        const float m1 = f16_to_f32(r.dd >> 16) * (float)m;
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t h[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t v = (k & 1) ? (q[i] >> 4) & 0x0F0F0F0Fu : q[i] & 0x0F0F0F0Fu;
+            if constexpr (Q5) v |= ((h[i] >> k) & 0x01010101u) << 4;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) w[4 * i + b] = __builtin_fmaf(d1, ubyte_f(v, b), -m1);
+        }
+    }
+};
+template <> struct FUnit<T_Q4_K> : FUnitK45<false> {};
+template <> struct FUnit<T_Q5_K> : FUnitK45<true> {};
+
+// Q6_K: [ql 128][qh 64][sc i8 x16][d], 210 bytes (2-byte aligned). Unit u = 4 g + i (half g,
+// quarter i): element l takes the low (i < 2) or high nibble of ql[64 g + 32 (i & 1) + l],
+// bits 2i..2i+1 of qh[32 g + l] as bits 4-5, scale sc[8 g + 2 i + l / 16]; value
+// d * sc * (q - 32) (quant.cpp:135-161).
+template <> struct FUnit<T_Q6_K> {
+    struct Raw { uint32_t ql[8], qh[8], sc, d; };
+    __device__ __forceinline__ static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 3) * 210;
+        const int g = (u & 7) >> 2, i = u & 3;
+        Raw r;
+        ld_a2<8>(blk + 64 * g + 32 * (i & 1), r.ql);
+        ld_a2<8>(blk + 128 + 32 * g, r.qh);
+        r.sc = ld_u16(blk + 192 + 8 * g + 2 * i);
+        r.d = ld_u16(blk + 208);
+        return r;
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, int u, float (&w)[32]) {
+        const int i = u & 3;
+        const float d = f16_to_f32(r.d);
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+            const float ds = d * (float)(int8_t)((r.sc >> (8 * hb)) & 0xFFu);  // exact
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t lo = (i < 2 ? r.ql[4 * hb + j] : r.ql[4 * hb + j] >> 4) & 0x0F0F0F0Fu;
+                const uint32_t hi = ((r.qh[4 * hb + j] >> (2 * i)) & 0x03030303u) << 4;
+                const uint32_t v = lo | hi;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w[16 * hb + 4 * j + b] = ds * (ubyte_f(v, b) - 32.0f);
+            }
+        }
+    }
+};
+
 // ------------------------------------------------------------------------------ kernel
 
 __host__ __device__ constexpr int xpad_row(int k) { return k + k / 8; }  // floats per LDS row
@@ -421,7 +574,76 @@ hipError_t launch_type(const uint8_t* w, int k, int n, int m, const float* x, co
     return launch_mr<T, 1, true>(w, row_bytes, k, n, m, x, bias, y, stream);
 }
 
+// Rows ids[i] of a weight matrix dequantized to fp32 (get_embedding's dequantize_block,
+// engine.cpp:310-317, quant.cpp:371-389): one thread per 32-element unit.
+template <uint32_t T>
+__global__ __launch_bounds__(kThreads) void k_dequant_rows(const uint8_t* __restrict__ w,
+                                                           size_t row_bytes, int k,
+                                                           const int32_t* __restrict__ ids,
+                                                           int n_ids, float* __restrict__ out) {
+    const int units = k / 32;
+    const int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (g >= (int64_t)n_ids * units) return;
+    const int r = (int)(g / units), u = (int)(g - (int64_t)r * units);
+    float v[32];
+    FUnit<T>::decode(FUnit<T>::load(w + (size_t)ids[r] * row_bytes, u), u, v);
+    f32x4* o = (f32x4*)(out + (size_t)r * k + 32 * u);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+}
+
+// F32 / F16 rows of any length, one element per thread.
+template <uint32_t T>
+__global__ __launch_bounds__(kThreads) void k_dequant_rows_any(const uint8_t* __restrict__ w,
+                                                               size_t row_bytes, int k,
+                                                               const int32_t* __restrict__ ids,
+                                                               int n_ids, float* __restrict__ out) {
+    const int64_t g = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (g >= (int64_t)n_ids * k) return;
+    const int r = (int)(g / k), e = (int)(g - (int64_t)r * k);
+    const uint8_t* row = w + (size_t)ids[r] * row_bytes;
+    out[(size_t)r * k + e] = T == T_F32 ? ((const float*)row)[e] : f16_to_f32(((const uint16_t*)row)[e]);
+}
+
+template <uint32_t T>
+hipError_t launch_dequant_t(const uint8_t* w, int k, const int32_t* ids, int n, float* out,
+                            hipStream_t stream) {
+    const size_t row_bytes = (size_t)(k / block_elems(T)) * block_bytes(T);
+    if ((T == T_F32 || T == T_F16) && k % 32 != 0) {
+        const int64_t threads = (int64_t)n * k;
+        hipLaunchKernelGGL((k_dequant_rows_any<T>), dim3((unsigned)((threads + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, stream, w, row_bytes, k, ids, n, out);
+    } else {
+        const int64_t threads = (int64_t)n * (k / 32);
+        hipLaunchKernelGGL((k_dequant_rows<T>), dim3((unsigned)((threads + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, stream, w, row_bytes, k, ids, n, out);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_dequantize_rows(uint32_t type, const uint8_t* w, int k, const int32_t* ids,
+                                  int n, float* out, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    if (k <= 0 || k % block_elems(type) != 0) return hipErrorInvalidValue;
+    switch (type) {
+        case T_F32: return launch_dequant_t<T_F32>(w, k, ids, n, out, stream);
+        case T_F16: return launch_dequant_t<T_F16>(w, k, ids, n, out, stream);
+        case T_Q4_0: return launch_dequant_t<T_Q4_0>(w, k, ids, n, out, stream);
+        case T_Q4_1: return launch_dequant_t<T_Q4_1>(w, k, ids, n, out, stream);
+        case T_Q5_0: return launch_dequant_t<T_Q5_0>(w, k, ids, n, out, stream);
+        case T_Q5_1: return launch_dequant_t<T_Q5_1>(w, k, ids, n, out, stream);
+        case T_Q8_0: return launch_dequant_t<T_Q8_0>(w, k, ids, n, out, stream);
+        case T_Q8_1: return launch_dequant_t<T_Q8_1>(w, k, ids, n, out, stream);
+        case T_Q2_K: return launch_dequant_t<T_Q2_K>(w, k, ids, n, out, stream);
+        case T_Q3_K: return launch_dequant_t<T_Q3_K>(w, k, ids, n, out, stream);
+        case T_Q4_K: return launch_dequant_t<T_Q4_K>(w, k, ids, n, out, stream);
+        case T_Q5_K: return launch_dequant_t<T_Q5_K>(w, k, ids, n, out, stream);
+        case T_Q6_K: return launch_dequant_t<T_Q6_K>(w, k, ids, n, out, stream);
+        default: return hipErrorNotSupported;
+    }
+}
 
 bool gemv_f_supported(uint32_t type) {
     return type == T_F32 || type == T_F16 || type == T_Q4_1 || type == T_Q5_1 ||

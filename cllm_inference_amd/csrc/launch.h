@@ -103,6 +103,11 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, in
                             int n_head, int n_kv, int head_dim, float* out, float* part,
                             size_t part_floats, hipStream_t stream);
 
+// Rows ids[0..n) of a weight matrix of any GGML type, dequantized to fp32 out[n][k] exactly
+// as the reference's dequantize_block (the embedding lookup). k_gemv_f.hip.
+hipError_t launch_dequantize_rows(uint32_t type, const uint8_t* w, int k, const int32_t* ids,
+                                  int n, float* out, hipStream_t stream);
+
 // Float-dot GEMV (k_gemv_f.hip) for the types without a vec_dot kernel (F32, F16, Q4_1,
 // Q5_1, Q8_1, Q2_K, Q3_K): y[t, j] = bias[j] + sum_i x[t, i] * deq(W[j, i]) on fp32
 // activation rows x[m][k], as the reference's dequantize fallback computes it.

@@ -152,6 +152,12 @@ int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream);
 
 /* ---- float ops between the linear layers (stream-ordered) ----------------------------- */
 
+/* Rows ids[0..n_ids) of a weight matrix of any GGML type (device pointers), dequantized
+ * to fp32 out[n_ids][in_dim] bit for bit like dequantize_block (src/core/quant.cpp:
+ * 371-389): the embedding lookup of get_embedding (src/core/engine.cpp:306-322). */
+int cllm_hip_dequantize_rows_dev(const void* w, uint32_t type, int in_dim, const int32_t* ids,
+                                 int n_ids, float* out, void* stream);
+
 /* NEOX RoPE in place (apply_rope, src/core/engine.cpp:41-56): x holds n_rows rows of
  * n_heads x head_dim; row t sits at position pos0 + t; pair (i, i + head_dim / 2) of each
  * head turns by (pos0 + t) / theta_base^(i / (head_dim / 2)). */

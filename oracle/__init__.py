@@ -142,6 +142,21 @@ class Reference(_Lib):
     def __init__(self, path: str = REF_SO):
         super().__init__(path, "ref_")
 
+    def engine_logits(self, path: str, tokens, prefill: bool = False, threads: int = 4):
+        """The reference engine's logits on the model file: prefill(tokens) -> (1, vocab), or
+        forward(t) for each token in turn -> (len(tokens), vocab)."""
+        f = self.lib.ref_engine_logits
+        f.restype = ctypes.c_long
+        f.argtypes = [ctypes.c_char_p, _P, _I, _I, _I, _P, ctypes.c_size_t]
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros(1 << 22, np.float32)
+        n = f(str(path).encode(), _ptr(toks), len(toks), 1 if prefill else 0, threads, _ptr(out),
+              out.size)
+        if n < 0:
+            raise RuntimeError(self.lib.ref_last_error().decode())
+        rows = 1 if prefill else len(toks)
+        return out[:n].reshape(rows, n // rows).copy()
+
     def gguf_dump(self, path: str):
         """GgufLoader::load(path) as (config fields, [(name, type, shape, offset, data_delta)])."""
         f = self.lib.ref_gguf_dump

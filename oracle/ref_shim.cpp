@@ -4,7 +4,9 @@
 //
 // TEST INFRASTRUCTURE ONLY. Built by oracle/Makefile into oracle/_ref/, never shipped.
 // Interfaces wrapped: include/cllm/core/quant.hpp:90-151, include/cllm/core/thread_pool.hpp:12-24,
-// include/cllm/core/gguf.hpp:79-82 (GgufLoader::load, for the GGUF reader's parity).
+// include/cllm/core/gguf.hpp:79-82 (GgufLoader::load, for the GGUF reader's parity),
+// include/cllm/core/engine.hpp:24-49 (TransformerEngine, for the device forward's parity).
+#include "cllm/core/engine.hpp"
 #include "cllm/core/gguf.hpp"
 #include "cllm/core/quant.hpp"
 #include "cllm/core/thread_pool.hpp"
@@ -137,3 +139,31 @@ extern "C" long ref_gguf_dump(const char* path, char* buf, size_t cap) {
     }
 }
 
+
+// Logits of the reference engine (Quant weight mode, a pool of `threads` workers) on the model
+// file path: with use_prefill, prefill(tokens) (the last token's logits, vocab floats);
+// otherwise forward(tokens[t]) for each t in turn (n * vocab floats). Returns the number of
+// floats written, or -1 with ref_last_error() set.
+extern "C" long ref_engine_logits(const char* path, const int* tokens, int n, int use_prefill,
+                                  int threads, float* out, size_t cap) {
+    try {
+        cllm::GgufModel m = cllm::GgufLoader::load(path);
+        cllm::ThreadPool pool((size_t)(threads > 0 ? threads : 1));
+        cllm::TransformerEngine eng(m, pool);
+        size_t at = 0;
+        auto put = [&](const std::vector<float>& v) {
+            if (at + v.size() > cap) throw std::runtime_error("ref_engine_logits: output too small");
+            std::memcpy(out + at, v.data(), v.size() * sizeof(float));
+            at += v.size();
+        };
+        if (use_prefill) {
+            put(eng.prefill(std::vector<int>(tokens, tokens + n)));
+        } else {
+            for (int t = 0; t < n; ++t) put(eng.forward(tokens[t], true));
+        }
+        return (long)at;
+    } catch (const std::exception& e) {
+        set_err(e);
+        return -1;
+    }
+}

@@ -176,6 +176,43 @@ def fdot_fixtures(ref: oracle.Reference) -> None:
     np.savez_compressed(os.path.join(OUT, "fdot.npz"), **data)
 
 
+MODELS = {
+    # Llama layout, Q4_K projections, Q6_K down and head, Q8_0 embedding
+    "llama_q4k": dict(arch="llama"),
+    # Qwen2: q/k/v biases, Q8_0 projections, F16 embedding tied to the head (float-dot)
+    "qwen2_q80_tied": dict(arch="qwen2", wtype=S.Q8_0, wtype_down=S.Q8_0, emb_type=S.F16,
+                           out_type=None),
+    # Qwen3: per-head q/k norms, head_dim 128 != n_embd / n_head, Q5_K, a Q3_K head
+    "qwen3_q5k": dict(arch="qwen3", head_dim=128, wtype=S.Q5_K, wtype_v=S.Q6_K,
+                      out_type=S.Q3_K, emb_type=S.Q4_K),
+}
+MODEL_TOKENS = [5, 17, 3, 99, 42, 7, 250, 1, 64, 128, 300, 12, 13, 14, 15, 16, 17, 18, 19, 20]
+
+
+def model_fixtures(ref: oracle.Reference) -> None:
+    """The reference engine (TransformerEngine, engine.cpp) on small random models written by
+    tests/device_model.py: logits of forward() for each of the first 6 tokens in turn, and of
+    prefill() on 6 and on 20 tokens (the batch takes the MFMA route from 16 rows)."""
+    import json
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import device_model as DM
+    data = {}
+    with tempfile.TemporaryDirectory() as d:
+        for name, kw in MODELS.items():
+            path = os.path.join(d, name + ".gguf")
+            DM.write_model(path, **kw)
+            with open(path, "rb") as f:
+                data[f"{name}__file_sha"] = np.array(hashlib.sha256(f.read()).hexdigest())
+            data[f"{name}__kwargs"] = np.array(json.dumps(kw))
+            data[f"{name}__tokens"] = np.array(MODEL_TOKENS, np.int32)
+            data[f"{name}__decode6"] = ref.engine_logits(path, MODEL_TOKENS[:6])
+            data[f"{name}__prefill6"] = ref.engine_logits(path, MODEL_TOKENS[:6], prefill=True)
+            data[f"{name}__prefill20"] = ref.engine_logits(path, MODEL_TOKENS, prefill=True)
+            print(name, flush=True)
+    np.savez_compressed(os.path.join(OUT, "model.npz"), **data)
+
+
 def refkat_fixtures(ref: oracle.Reference) -> None:
     """Outputs of the reference on the inputs its own tests build (tests/quant_test.cpp:237-361):
     weight bytes (k + blk + j) % 7 after a leading fp16 1.0, x = ((i % 5) - 2) * 0.5."""
@@ -204,7 +241,8 @@ def refkat_fixtures(ref: oracle.Reference) -> None:
 
 
 FIXTURES = {"quant": quant_fixtures, "refkat": refkat_fixtures, "types": extra_type_fixtures,
-            "gemv": gemv_fixtures, "batch": batch_fixtures, "fdot": fdot_fixtures}
+            "gemv": gemv_fixtures, "batch": batch_fixtures, "fdot": fdot_fixtures,
+            "model": model_fixtures}
 
 
 def main() -> None:

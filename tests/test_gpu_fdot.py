@@ -115,3 +115,22 @@ def test_fdot_routes_and_errors(gpu):
         gpu.matmul_quant_dev(x, wd[2:], S.F16, None, 256, 4)
     with pytest.raises(RuntimeError, match="in_dim not divisible by block size"):
         gpu.matmul_quant_dev(x[:, :100].contiguous(), wd, S.Q3_K, None, 100, 4)
+
+
+@pytest.mark.parametrize("qt", sorted(S.TYPE_NAMES))
+def test_dequantize_rows_bit_exact(gpu, orc, qt):
+    """The embedding lookup: rows dequantized on the device equal the reference's
+    dequantize_block (through the oracle, bit-exact with it) bit for bit."""
+    import torch
+    bs = S.BLOCK[qt]
+    for n, k in ((40, 4096 if bs > 1 else 896), (7, 256 if bs > 1 else 33)):
+        if k % bs:
+            continue
+        w = S.make_weight(qt, n, k, 60 + qt)
+        ids = np.array([n - 1, 0, 3, 3, n // 2], np.int32)
+        got = gpu.dequantize_rows_dev(_dev(w), qt, k, _dev(ids)).cpu().numpy()
+        rb = S.row_bytes(qt, k)
+        for i, j in enumerate(ids):
+            want = orc.dequantize(w[j * rb:(j + 1) * rb], qt, k)
+            assert np.array_equal(bits(got[i]), bits(want)), (S.TYPE_NAMES[qt], n, k, j)
+    torch.cuda.synchronize()
