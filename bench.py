@@ -146,10 +146,11 @@ def float_dot_points(C, S, steps, warmup):
 
 def decode_layer_device(C, S, steps, warmup, copies=4):
     """The linear path of one Llama-3-8B decode layer in the Q4_K_M mix, device-resident:
-    RMSNorm+Q8_0 -> one GEMV launch for q/k/v; Q8_0 of the attention output (a fixed
-    synthetic vector: attention itself is not part of this path) -> wo GEMV + residual add;
+    RMSNorm+Q8_0 -> one GEMV launch for q/k/v; the wo GEMV quantizing the attention output
+    (a fixed synthetic vector: attention itself is measured with the whole model) and adding
+    the residual;
     RMSNorm+Q8_0 -> one launch for gate/up -> SwiGLU+Q8_0 -> down GEMV + residual add
-    (engine.cpp:475-513). Eight launches per layer (the residual adds ride in the wo and
+    (engine.cpp:475-513). Seven launches per layer (the residual adds ride in the wo and
     down GEMVs). `copies` distinct
     copies of the layer's weights rotate so that each step streams its weights from HBM, as
     the 32 different layers of a model would."""
@@ -184,9 +185,8 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
         qt, _, k = mats["wq"]
         C.gemv_q8_multi_dev([L[l] for l in qkv], qt, k, [mats[l][1] for l in qkv], qs, sc, bs,
                             ys=[outs[l] for l in qkv])
-        qa, sa, ba = C.quantize_q8_0_dev(attn)
         qt, n, k = mats["wo"]
-        C.gemv_q8_residual_dev(L["wo"], qt, k, n, qa, sa, ba, x)
+        C.matmul_quant_residual_dev(attn, L["wo"], qt, None, k, n, x)
         _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn2, 1e-5, h=False)
         qt, _, k = mats["gate"]
         C.gemv_q8_multi_dev([L[l] for l in gu], qt, k, [mats[l][1] for l in gu], qs, sc, bs,
@@ -197,7 +197,7 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
 
     ms = time_loop(step, steps, warmup)
     x.copy_(x0)
-    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 8,
+    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 7,
            "gbs": round(wbytes / ms / 1e6, 1),
            "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
            "projected_tokens_per_s_32_layers_linear_only": round(1e3 / (32 * ms), 1),

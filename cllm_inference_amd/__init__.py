@@ -77,6 +77,8 @@ SIGNATURES = {
                                   ctypes.POINTER(_P)]),
     "cllm_hip_gguf_config": (_I, [_P, _P]),
     "cllm_hip_rope_neox_dev": (_I, [_P, _I, _I, _I, _I, ctypes.c_float, _P]),
+    "cllm_hip_rope_neox2_dev": (_I, [_P, _I, _P, _I, _I, _I, _I, ctypes.c_float, _P]),
+    "cllm_hip_matmul_quant_residual_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
     "cllm_hip_dequantize_rows_dev": (_I, [_P, _U, _I, _P, _I, _P, _P]),
     "cllm_hip_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
 }
@@ -277,6 +279,16 @@ def matmul_quant_dev(x, w, t: int, bias, in_dim: int, out_dim: int, y=None):
     return y
 
 
+def matmul_quant_residual_dev(x, w, t: int, bias, in_dim: int, out_dim: int, y):
+    """y += matmul_quant_batch(x, w) (+ bias) on device tensors: a matmul and the residual
+    add after it (engine.cpp:505-506, 512-513)."""
+    m = x.shape[0]
+    _check(load_library().cllm_hip_matmul_quant_residual_dev(_tp(x), _tp(w), int(t), _tp(bias),
+                                                             int(in_dim), int(out_dim), int(m),
+                                                             _tp(y), _stream()))
+    return y
+
+
 def matmul_route(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:
     return load_library().cllm_hip_matmul_route(int(t), int(in_dim), int(out_dim),
                                                 int(n_rows)).decode()
@@ -396,6 +408,15 @@ def rope_neox_dev(x, n_heads: int, head_dim: int, pos0: int, theta_base: float):
                                                  int(head_dim), int(pos0), float(theta_base),
                                                  _stream()))
     return x
+
+
+def rope_neox2_dev(q, n_head: int, k, n_head_kv: int, head_dim: int, pos0: int,
+                   theta_base: float):
+    """NEOX RoPE on the queries and the keys in one launch (engine.cpp:481-482)."""
+    n_rows = q.numel() // (n_head * head_dim)
+    _check(load_library().cllm_hip_rope_neox2_dev(_tp(q), int(n_head), _tp(k), int(n_head_kv),
+                                                  int(n_rows), int(head_dim), int(pos0),
+                                                  float(theta_base), _stream()))
 
 
 def attention_dev(q, k_cache, v_cache, pos0: int, n_head: int, n_head_kv: int, head_dim: int,

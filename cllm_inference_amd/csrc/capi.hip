@@ -78,6 +78,7 @@ struct Workspace {
     DevBuf buf;
     DevBuf part;  // split-K partial sums of the weight-row GEMM
     DevBuf att;   // sequence-split partials of the attention kernel
+    DevBuf tmp;   // matmul result before a residual add the kernel cannot fuse
     int8_t* qs = nullptr;
     float* sc = nullptr;
     int32_t* bs = nullptr;
@@ -305,11 +306,13 @@ bool needs_workspace(uint32_t type, int k, int m) {
 
 // GEMV route on fp32 activation rows.
 hipError_t run_gemv_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
-                        const float* bias, float* y, Workspace* ws, hipStream_t stream) {
-    if (m <= kFusedMaxRows) return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream);
+                        const float* bias, float* y, Workspace* ws, hipStream_t stream,
+                        bool accumulate = false) {
+    if (m <= kFusedMaxRows)
+        return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream, accumulate);
     hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws->qs, ws->sc, ws->bs, stream);
     if (e != hipSuccess) return e;
-    return launch_gemv(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, stream);
+    return launch_gemv(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, stream, accumulate);
 }
 
 // The per-stream activation workspace of the device entry points, grown to m x k.
@@ -604,6 +607,40 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
     return CLLM_HIP_OK;
 }
 
+int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t type,
+                                       const float* bias, int in_dim, int out_dim, int n_rows,
+                                       float* y, void* stream) {
+    int rc = check_matmul(n_rows > 1 ? "matmul_quant_batch" : "matmul_quant", type, in_dim, out_dim);
+    if (rc) return rc;
+    if (n_rows <= 0 || out_dim == 0) return CLLM_HIP_OK;
+    if (!x || !w || !y) return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(x) || !aligned16(w) || !aligned16(y) || ((uintptr_t)bias & 3u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    Workspace* ws = nullptr;
+    if ((rc = stream_workspace(st, s, in_dim, n_rows, &ws))) return rc;
+    if (has_kernel(type) && !use_mfma(type, in_dim, n_rows)) {
+        // the GEMV adds into y in its epilogue
+        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws, s,
+                             true));
+        return CLLM_HIP_OK;
+    }
+    const size_t bytes = (size_t)n_rows * out_dim * sizeof(float);
+    {
+        std::lock_guard<std::mutex> lk(st->mtx);
+        HIP_TRY(ws->tmp.ensure(bytes, s));
+    }
+    float* t = (float*)ws->tmp.p;
+    if (!has_kernel(type))
+        HIP_TRY(launch_gemv_f(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, t, s));
+    else
+        HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, t, ws, s));
+    HIP_TRY(launch_add(y, t, (int64_t)n_rows * out_dim, s));
+    return CLLM_HIP_OK;
+}
+
 int cllm_hip_rmsnorm_q8_0_dev(const float* x, const float* w, float eps, int n, int n_rows,
                               float* h, int8_t* qs, float* scales, int32_t* bsums,
                               void* stream) {
@@ -676,16 +713,25 @@ int cllm_hip_dequantize_rows_dev(const void* w, uint32_t type, int in_dim, const
 
 int cllm_hip_rope_neox_dev(float* x, int n_rows, int n_heads, int head_dim, int pos0,
                            float theta_base, void* stream) {
-    if (n_rows < 0 || n_heads < 0 || head_dim <= 0 || head_dim % 2 != 0 || head_dim > 512 ||
-        pos0 < 0)
+    return cllm_hip_rope_neox2_dev(x, n_heads, nullptr, 0, n_rows, head_dim, pos0, theta_base,
+                                   stream);
+}
+
+int cllm_hip_rope_neox2_dev(float* q, int n_head, float* k, int n_head_kv, int n_rows,
+                            int head_dim, int pos0, float theta_base, void* stream) {
+    if (!k) n_head_kv = 0;
+    if (n_rows < 0 || n_head < 0 || n_head_kv < 0 || head_dim <= 0 || head_dim % 2 != 0 ||
+        head_dim > 512 || pos0 < 0)
         return set_err(CLLM_HIP_E_ARG, "rope: bad shape");
-    if (n_rows == 0 || n_heads == 0) return CLLM_HIP_OK;
-    if (!x) return set_err(CLLM_HIP_E_ARG, "rope: null pointer");
-    if ((uintptr_t)x & 3u) return set_err(CLLM_HIP_E_ARG, "rope: misaligned device pointer");
+    if (n_rows == 0 || n_head + n_head_kv == 0) return CLLM_HIP_OK;
+    if (!q && n_head > 0) return set_err(CLLM_HIP_E_ARG, "rope: null pointer");
+    if (((uintptr_t)q & 3u) || ((uintptr_t)k & 3u))
+        return set_err(CLLM_HIP_E_ARG, "rope: misaligned device pointer");
     DeviceState* st;
     int rc = acquire(&st);
     if (rc) return rc;
-    HIP_TRY(launch_rope_neox(x, n_rows, n_heads, head_dim, pos0, theta_base, (hipStream_t)stream));
+    HIP_TRY(launch_rope_neox(q, n_rows, n_head, k, n_head_kv, head_dim, pos0, theta_base,
+                             (hipStream_t)stream));
     return CLLM_HIP_OK;
 }
 

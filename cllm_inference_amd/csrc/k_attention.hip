@@ -37,13 +37,19 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------------- RoPE
 
-// grid (rows, heads), half = head_dim / 2 threads (up to 256): row t has position pos0 + t.
+// grid (rows, n_heads + n_heads2), half = head_dim / 2 threads (up to 256): row t has
+// position pos0 + t; heads past n_heads belong to the second tensor x2 (the keys), so the
+// queries and keys of a layer turn in one launch.
 __global__ __launch_bounds__(256) void k_rope_neox(float* __restrict__ x, int n_heads,
+                                                   float* __restrict__ x2, int n_heads2,
                                                    int head_dim, int pos0, float base) {
-    const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+    const int t = blockIdx.x, i = threadIdx.x;
     const int half = head_dim / 2;
     if (i >= half) return;
-    float* xh = x + ((size_t)t * n_heads + h) * head_dim;
+    const bool second = (int)blockIdx.y >= n_heads;
+    const int h = second ? blockIdx.y - n_heads : blockIdx.y;
+    float* xh = (second ? x2 + (size_t)t * n_heads2 * head_dim : x + (size_t)t * n_heads * head_dim) +
+                (size_t)h * head_dim;
     const float theta = __fdiv_rn((float)(pos0 + t), powf(base, __fdiv_rn((float)i, (float)half)));
     const float c = cosf(theta), s = sinf(theta);
     const float x0 = xh[i], x1 = xh[i + half];
@@ -160,7 +166,16 @@ __global__ __launch_bounds__(kThreads) void k_attention(
             if (r < n_rep) {
                 float a = acc[i] * corr[r];
                 const float* vr = vc + (size_t)c0 * kv_dim + kvh * HD + d;
-                for (int j = 0; j < nv; ++j) a = __builtin_fmaf(sc[r][j], vr[(size_t)j * kv_dim], a);
+                int j = 0;
+                // eight V loads in flight before their fmas (the loop is latency-bound)
+                for (; j + 8 <= nv; j += 8) {
+                    float vv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) vv[u] = vr[(size_t)(j + u) * kv_dim];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) a = __builtin_fmaf(sc[r][j + u], vv[u], a);
+                }
+                for (; j < nv; ++j) a = __builtin_fmaf(sc[r][j], vr[(size_t)j * kv_dim], a);
                 acc[i] = a;
             }
         }
@@ -187,25 +202,47 @@ __global__ __launch_bounds__(kThreads) void k_attention(
     }
 }
 
-// grid (n_head, rows), HD threads: out = sum_z e^(m_z - M) o_z / sum_z e^(m_z - M) l_z.
+// grid (n_head, rows), 256 threads, S <= kMaxSplits: out = sum_z e^(m_z - M) o_z /
+// sum_z e^(m_z - M) l_z. The split maxima and sums are read once, in parallel, into LDS.
+constexpr int kMaxSplits = 256;
+
 __global__ __launch_bounds__(256) void k_attention_combine(const float* __restrict__ part,
                                                            int n_head, int hd, int S,
                                                            float* __restrict__ out) {
-    const int hq = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
-    if (d >= hd) return;
+    __shared__ float wz[kMaxSplits], lz[kMaxSplits];
+    __shared__ float red[4];
+    const int hq = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
     const float* pp = part + ((size_t)t * n_head + hq) * S * (hd + 2);
-    float M = -INFINITY;
-    for (int z = 0; z < S; ++z) M = fmaxf(M, pp[(size_t)z * (hd + 2) + hd]);
-    float num = 0.0f, den = 0.0f;
-    for (int z = 0; z < S; ++z) {
-        const float* p = pp + (size_t)z * (hd + 2);
-        const float m = p[hd];
-        if (m == -INFINITY) continue;
-        const float w = expf(m - M);
-        num = __builtin_fmaf(w, p[d], num);
-        den = __builtin_fmaf(w, p[hd + 1], den);
+    float m = -INFINITY;
+    if (tid < S) {
+        m = pp[(size_t)tid * (hd + 2) + hd];
+        lz[tid] = pp[(size_t)tid * (hd + 2) + hd + 1];
     }
-    out[((size_t)t * n_head + hq) * hd + d] = __fdiv_rn(num, den);
+    float M = m;
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (tid < S) wz[tid] = m == -INFINITY ? 0.0f : expf(m - M);
+    __syncthreads();
+    if (tid >= hd) return;
+    float num = 0.0f, den = 0.0f;
+    int z = 0;
+    for (; z + 4 <= S; z += 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = pp[(size_t)(z + u) * (hd + 2) + tid];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            num = __builtin_fmaf(wz[z + u], v[u], num);
+            den = __builtin_fmaf(wz[z + u], lz[z + u], den);
+        }
+    }
+    for (; z < S; ++z) {
+        num = __builtin_fmaf(wz[z], pp[(size_t)z * (hd + 2) + tid], num);
+        den = __builtin_fmaf(wz[z], lz[z], den);
+    }
+    out[((size_t)t * n_head + hq) * hd + tid] = __fdiv_rn(num, den);
 }
 
 template <int HD>
@@ -217,6 +254,7 @@ hipError_t launch_attention_hd(const float* q, const float* kc, const float* vc,
     const int64_t base = (int64_t)n_kv * rows;
     int S = (int)std::min<int64_t>(std::max<int64_t>(1, (1024 + base - 1) / base),
                                    (L_max + kChunk - 1) / kChunk);
+    S = std::min(S, kMaxSplits);
     if ((size_t)rows * n_head * S * (HD + 2) > part_floats) S = 1;
     const int split_len = ((L_max + S - 1) / S + kChunk - 1) / kChunk * kChunk;
     S = (L_max + split_len - 1) / split_len;
@@ -226,19 +264,20 @@ hipError_t launch_attention_hd(const float* q, const float* kc, const float* vc,
                        part, out);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || S == 1) return e;
-    hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)n_head, (unsigned)rows), dim3(HD), 0,
+    hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)n_head, (unsigned)rows), dim3(256), 0,
                        stream, part, n_head, HD, S, out);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_rope_neox(float* x, int rows, int n_heads, int head_dim, int pos0, float base,
-                            hipStream_t stream) {
-    if (rows <= 0 || n_heads <= 0) return hipSuccess;
+hipError_t launch_rope_neox(float* x, int rows, int n_heads, float* x2, int n_heads2,
+                            int head_dim, int pos0, float base, hipStream_t stream) {
+    if (!x2) n_heads2 = 0;
+    if (rows <= 0 || n_heads + n_heads2 <= 0) return hipSuccess;
     if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > 512) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rope_neox, dim3((unsigned)rows, (unsigned)n_heads), dim3(256), 0, stream,
-                       x, n_heads, head_dim, pos0, base);
+    hipLaunchKernelGGL(k_rope_neox, dim3((unsigned)rows, (unsigned)(n_heads + n_heads2)), dim3(256),
+                       0, stream, x, n_heads, x2, n_heads2, head_dim, pos0, base);
     return hipGetLastError();
 }
 

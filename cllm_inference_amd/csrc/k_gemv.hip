@@ -936,9 +936,10 @@ hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* co
 }
 
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
-                             const float* x, const float* bias, float* y, hipStream_t stream) {
-    return gemv_dispatch(type, one_segment(w, n, bias, y), k, n, m, nullptr, nullptr, nullptr, x, 0,
-                         stream);
+                             const float* x, const float* bias, float* y, hipStream_t stream,
+                             bool accumulate) {
+    return gemv_dispatch(type, one_segment(w, n, bias, y), k, n, m, nullptr, nullptr, nullptr, x,
+                         accumulate ? 1 : 0, stream);
 }
 
 }  // namespace cllm_hip

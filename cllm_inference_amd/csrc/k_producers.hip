@@ -123,11 +123,13 @@ __global__ __launch_bounds__(kRegThreads) void k_rmsnorm_q8_0_reg(const float* _
     const int row = blockIdx.x;
     const float* xr = x + (size_t)row * n;
     const int chunks = n / 4;
-    f32x4 v[CPT];
+    f32x4 v[CPT], wv[CPT];
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
         const int c = threadIdx.x + kRegThreads * i;
+        // the weight row is loaded with x, so its latency hides behind the reduction
+        wv[i] = c < chunks ? *(const f32x4*)(w + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
         v[i] = c < chunks ? *(const f32x4*)(xr + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
         ss = __builtin_fmaf(v[i].x, v[i].x, ss);
         ss = __builtin_fmaf(v[i].y, v[i].y, ss);
@@ -146,12 +148,11 @@ __global__ __launch_bounds__(kRegThreads) void k_rmsnorm_q8_0_reg(const float* _
     for (int i = 0; i < CPT; ++i) {
         const int c = threadIdx.x + kRegThreads * i;
         if (c >= chunks) break;  // whole 8-lane groups (chunks % 8 == 0)
-        const f32x4 wv = *(const f32x4*)(w + 4 * c);
         f32x4 hv;
-        hv.x = __fmul_rn(__fmul_rn(v[i].x, rms), wv.x);
-        hv.y = __fmul_rn(__fmul_rn(v[i].y, rms), wv.y);
-        hv.z = __fmul_rn(__fmul_rn(v[i].z, rms), wv.z);
-        hv.w = __fmul_rn(__fmul_rn(v[i].w, rms), wv.w);
+        hv.x = __fmul_rn(__fmul_rn(v[i].x, rms), wv[i].x);
+        hv.y = __fmul_rn(__fmul_rn(v[i].y, rms), wv[i].y);
+        hv.z = __fmul_rn(__fmul_rn(v[i].z, rms), wv[i].z);
+        hv.w = __fmul_rn(__fmul_rn(v[i].w, rms), wv[i].w);
         if (h) *(f32x4*)(h + (size_t)row * n + 4 * c) = hv;
         if (qs) quantize_block8(hv, part, (int64_t)row * (n / 32) + c / 8, qs, scales, bsums);
     }

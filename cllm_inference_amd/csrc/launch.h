@@ -52,7 +52,8 @@ hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* co
 // Q8_0 in LDS (bit-identical to launch_quantize_q8_0) instead of reading a quantized batch,
 // so a decode step is a single kernel.
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
-                             const float* x, const float* bias, float* y, hipStream_t stream);
+                             const float* x, const float* bias, float* y, hipStream_t stream,
+                             bool accumulate = false);
 
 // Same contract as launch_gemv, on the int8 MFMA path (m >= 1, any n; k % 256 == 0 for the
 // K-quants, k % 32 == 0 otherwise). Returns hipErrorNotSupported for types without an MFMA
@@ -91,12 +92,13 @@ hipError_t launch_swiglu_q8_0(const float* gate, const float* up, int64_t total,
 hipError_t launch_add(float* x, const float* d, int64_t n, hipStream_t stream);
 
 // Float ops between the linear layers (k_attention.hip): NEOX RoPE in place on `rows` rows
-// of n_heads x head_dim (row t at position pos0 + t), and grouped-query attention of `rows`
+// of n_heads x head_dim (row t at position pos0 + t), optionally on a second tensor x2 of
+// n_heads2 heads per row in the same launch (queries and keys), and grouped-query attention of `rows`
 // query rows (n_head x head_dim each) over KV caches of n_kv x head_dim per position, query
 // row t seeing positions [0, pos0 + t]. `part` (at least attention_partial_floats floats, or
 // null for no sequence split) holds the split partials.
-hipError_t launch_rope_neox(float* x, int rows, int n_heads, int head_dim, int pos0, float base,
-                            hipStream_t stream);
+hipError_t launch_rope_neox(float* x, int rows, int n_heads, float* x2, int n_heads2,
+                            int head_dim, int pos0, float base, hipStream_t stream);
 bool attention_supported(int head_dim, int n_head, int n_kv);
 size_t attention_partial_floats(int rows, int n_head, int head_dim);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int pos0,

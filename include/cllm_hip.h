@@ -123,6 +123,14 @@ int cllm_hip_gemv_q8_residual_dev(const void* w, uint32_t type, int in_dim, int 
                                   const int32_t* bsums, const float* bias, float* y,
                                   void* stream);
 
+/* cllm_hip_matmul_quant_dev followed by the residual add (x += mm(...),
+ * src/core/engine.cpp:505-506, 512-513): y[t, j] += (row t of x . W row j) (+ bias[j]).
+ * Small batches of the vec_dot types quantize their rows in the GEMV and add in its
+ * epilogue (one launch); other shapes and types add a separate pass. */
+int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t type,
+                                       const float* bias, int in_dim, int out_dim, int n_rows,
+                                       float* y, void* stream);
+
 /* matmul_quant_batch on device buffers. vec_dot types, small n_rows: one GEMV launch that
  * quantizes its activation rows itself; large n_rows: quantizes x into a library-owned
  * per-stream workspace, then runs the MFMA GEMM. Other types: the float-dot GEMV on x. */
@@ -163,6 +171,11 @@ int cllm_hip_dequantize_rows_dev(const void* w, uint32_t type, int in_dim, const
  * head turns by (pos0 + t) / theta_base^(i / (head_dim / 2)). */
 int cllm_hip_rope_neox_dev(float* x, int n_rows, int n_heads, int head_dim, int pos0,
                            float theta_base, void* stream);
+
+/* The same on the queries q (n_rows x n_head heads) and the keys k (n_rows x n_head_kv
+ * heads, e.g. the cache rows just written) in one launch (engine.cpp:481-482). */
+int cllm_hip_rope_neox2_dev(float* q, int n_head, float* k, int n_head_kv, int n_rows,
+                            int head_dim, int pos0, float theta_base, void* stream);
 
 /* Grouped-query attention (attention, src/core/engine.cpp:114-146): q holds n_rows rows of
  * n_head x head_dim; the caches hold n_head_kv x head_dim per position, positions

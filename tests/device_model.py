@@ -177,12 +177,13 @@ class DeviceModel:
                 qv = q.view(T * self.n_head, self.hd)
                 self._norm_inplace(qv, self.w[p + "attn_q_norm.weight"])
                 self._norm_inplace(kc.view(T * self.n_kv, self.hd), self.w[p + "attn_k_norm.weight"])
-            C.rope_neox_dev(q, self.n_head, self.hd, pos0, self.theta)
-            C.rope_neox_dev(kc, self.n_kv, self.hd, pos0, self.theta)
+            C.rope_neox2_dev(q, self.n_head, kc, self.n_kv, self.hd, pos0, self.theta)
             C.attention_dev(q, self.k_cache[l], self.v_cache[l], pos0, self.n_head, self.n_kv,
                             self.hd, out=attn)
-            qa = C.quantize_q8_0_dev(attn)
-            self._linear([p + "attn_output.weight"], [x], attn, qa, residual=True)
+            # the GEMV quantizes the attention output itself and adds into x
+            wo = p + "attn_output.weight"
+            C.matmul_quant_residual_dev(attn, self.w[wo], self._type(wo), None, self.q_dim,
+                                        self.n_embd, x)
             h, qs, sc, bs = C.rmsnorm_q8_0_dev(x, self.w[p + "ffn_norm.weight"], self.eps)
             self._linear([p + "ffn_gate.weight", p + "ffn_up.weight"], [gate, up], h, (qs, sc, bs))
             hs, qs, sc, bs = C.swiglu_q8_0_dev(gate, up)

@@ -157,3 +157,20 @@ def test_gemv_multi_equals_separate_launches(gpu, qt):
         for i in range(n_mats):
             one = gpu.gemv_q8_dev(ws[i], qt, k, dims[i], qs, sc, bs, bias=biases[i])
             assert np.array_equal(bits(ys[i].cpu().numpy()), bits(one.cpu().numpy())), (n_mats, i)
+
+
+@pytest.mark.parametrize("qt,m", [(S.Q4_K, 1), (S.Q6_K, 2), (S.Q8_0, 5), (S.Q4_K, 20), (S.F16, 1),
+                                  (S.Q3_K, 3)])
+def test_matmul_residual_equals_matmul_then_add(gpu, qt, m):
+    """y += matmul(x) in the fused GEMV (small batches of vec_dot types) or with a separate
+    add (float-dot types, MFMA batches) gives the bits of the matmul and the add."""
+    n_out, k = 1024, 4096
+    rng = np.random.default_rng(qt + 300 + m)
+    w = _dev(S.make_weight(qt, n_out, k, 14))
+    x = _dev(S.make_activation(m, k, 15))
+    bias = _dev(rng.standard_normal(n_out).astype(np.float32))
+    resid = rng.standard_normal((m, n_out)).astype(np.float32)
+    mm = gpu.matmul_quant_dev(x, w, qt, bias, k, n_out).cpu().numpy()
+    y = _dev(resid)
+    gpu.matmul_quant_residual_dev(x, w, qt, bias, k, n_out, y)
+    assert np.array_equal(bits(y.cpu().numpy()), bits((resid + mm).astype(np.float32)))
