@@ -14,8 +14,10 @@
 // Positions go in chunks of 64: sixteen lanes per position read the K row (16-byte pieces,
 // coalesced), each lane dots its slice with every query head held in registers, a 16-lane
 // reduction gives the scores; the softmax is online (running max and sum per head, the
-// partial output rescaled when the max grows); then the threads owning output elements
-// (head, d) add p_t v_t[d] for the chunk's positions, reading V rows coalesced along d.
+// partial output rescaled when the max grows); each wave adds p_t v_t for its 16 positions
+// of the chunk into per-lane partial outputs (lane l owns dims l + 64 e of every head), with
+// every K and V load of a chunk issued before the arithmetic that needs it; the four waves'
+// partials are added at the end.
 // Long sequences are split over several workgroups whose (max, sum, unnormalised output)
 // partials a second kernel combines, so a decode step (one query row) still spreads over
 // the device. The summation order differs from the reference's (per-chunk and per-split
@@ -73,7 +75,6 @@ __global__ __launch_bounds__(kThreads) void k_attention(
     int n_head, int n_kv, int pos0, int split_len, float scale, float* __restrict__ part,
     float* __restrict__ out) {
     constexpr int PER = HD / kLanesPerPos;  // K elements per lane (4 .. 16)
-    constexpr int NOUT = kMaxRep * HD / kThreads > 0 ? (kMaxRep * HD + kThreads - 1) / kThreads : 1;
     __shared__ float sc[kMaxRep][kChunk];
     __shared__ float m_run[kMaxRep], l_run[kMaxRep], corr[kMaxRep];
 
@@ -97,10 +98,15 @@ __global__ __launch_bounds__(kThreads) void k_attention(
             qv[r][e] = v.x; qv[r][e + 1] = v.y; qv[r][e + 2] = v.z; qv[r][e + 3] = v.w;
         }
     }
-    // output elements (head r, dim d) owned by this thread: index o = threadIdx.x + kThreads i
-    float acc[NOUT];
+    // Each wave accumulates the output of its own 16 positions of every chunk: lane l owns
+    // dims l + 64 e (e < HD / 64) of every query head of the group; the four waves' partials
+    // are added at the end.
+    constexpr int DE = HD / 64;
+    float acc[kMaxRep][DE];
 #pragma unroll
-    for (int i = 0; i < NOUT; ++i) acc[i] = 0.0f;
+    for (int r = 0; r < kMaxRep; ++r)
+#pragma unroll
+        for (int e = 0; e < DE; ++e) acc[r][e] = 0.0f;
     if (threadIdx.x < kMaxRep) {
         m_run[threadIdx.x] = -INFINITY;
         l_run[threadIdx.x] = 0.0f;
@@ -108,31 +114,46 @@ __global__ __launch_bounds__(kThreads) void k_attention(
     __syncthreads();
 
     for (int c0 = begin; c0 < end; c0 += kChunk) {
-        // scores of the chunk: each wave takes 4 positions per round, 4 rounds
+        // scores of the chunk: each wave takes 4 positions per round, 4 rounds; all the K
+        // loads of the chunk are issued before the first dot
+        float kv[kChunk / 16][PER];
+#pragma unroll
+        for (int round = 0; round < kChunk / 16; ++round) {
+            const int pc = min(c0 + round * 16 + wave * 4 + sub, end - 1);
+            const float* kr = kc + (size_t)pc * kv_dim + kvh * HD + seg * PER;
+#pragma unroll
+            for (int e = 0; e < PER; e += 4) {
+                const f32x4 v = *(const f32x4*)(kr + e);
+                kv[round][e] = v.x; kv[round][e + 1] = v.y; kv[round][e + 2] = v.z;
+                kv[round][e + 3] = v.w;
+            }
+        }
 #pragma unroll
         for (int round = 0; round < kChunk / 16; ++round) {
             const int slot = round * 16 + wave * 4 + sub;
             const int p = c0 + slot;
-            const int pc = min(p, end - 1);
-            const float* kr = kc + (size_t)pc * kv_dim + kvh * HD + seg * PER;
-            float kv[PER];
-#pragma unroll
-            for (int e = 0; e < PER; e += 4) {
-                const f32x4 v = *(const f32x4*)(kr + e);
-                kv[e] = v.x; kv[e + 1] = v.y; kv[e + 2] = v.z; kv[e + 3] = v.w;
-            }
 #pragma unroll
             for (int r = 0; r < kMaxRep; ++r) {
                 if (r >= n_rep) break;
                 float d = 0.0f;
 #pragma unroll
-                for (int e = 0; e < PER; ++e) d = __builtin_fmaf(qv[r][e], kv[e], d);
+                for (int e = 0; e < PER; ++e) d = __builtin_fmaf(qv[r][e], kv[round][e], d);
                 d += __shfl_xor(d, 8, 16);
                 d += __shfl_xor(d, 4, 16);
                 d += __shfl_xor(d, 2, 16);
                 d += __shfl_xor(d, 1, 16);
                 if (seg == 0) sc[r][slot] = p < end ? __fmul_rn(d, scale) : -INFINITY;
             }
+        }
+        // this wave's V rows, issued before the softmax bookkeeping so their latency hides
+        // behind it (rows past the end are clamped, their probability is zero)
+        float vv[16][DE];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int pc = min(c0 + wave * 16 + j, end - 1);
+            const float* vr = vc + (size_t)pc * kv_dim + kvh * HD + lane;
+#pragma unroll
+            for (int e = 0; e < DE; ++e) vv[j][e] = vr[64 * e];
         }
         __syncthreads();
         // running max per head; the factor that rescales what is already summed
@@ -158,42 +179,40 @@ __global__ __launch_bounds__(kThreads) void k_attention(
             for (int i = 0; i < kChunk; ++i) l += sc[r][i];
             l_run[r] = l;
         }
-        const int nv = min(kChunk, end - c0);
 #pragma unroll
-        for (int i = 0; i < NOUT; ++i) {
-            const int o = threadIdx.x + kThreads * i;
-            const int r = o / HD, d = o - r * HD;
-            if (r < n_rep) {
-                float a = acc[i] * corr[r];
-                const float* vr = vc + (size_t)c0 * kv_dim + kvh * HD + d;
-                int j = 0;
-                // eight V loads in flight before their fmas (the loop is latency-bound)
-                for (; j + 8 <= nv; j += 8) {
-                    float vv[8];
+        for (int r = 0; r < kMaxRep; ++r) {
+            if (r >= n_rep) break;
+            const float cr = corr[r];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) vv[u] = vr[(size_t)(j + u) * kv_dim];
+            for (int e = 0; e < DE; ++e) {
+                float a = acc[r][e] * cr;
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) a = __builtin_fmaf(sc[r][j + u], vv[u], a);
-                }
-                for (; j < nv; ++j) a = __builtin_fmaf(sc[r][j], vr[(size_t)j * kv_dim], a);
-                acc[i] = a;
+                for (int j = 0; j < 16; ++j) a = __builtin_fmaf(sc[r][wave * 16 + j], vv[j][e], a);
+                acc[r][e] = a;
             }
         }
         __syncthreads();
     }
 
-    // write the split's partial, or the normalised output
+    // the four waves' partial outputs, added through LDS (reusing nothing else: a separate
+    // buffer), then the split's partial or the normalised output
+    __shared__ float wpart[kThreads / 64][kMaxRep * HD];
 #pragma unroll
-    for (int i = 0; i < NOUT; ++i) {
-        const int o = threadIdx.x + kThreads * i;
+    for (int r = 0; r < kMaxRep; ++r) {
+        if (r >= n_rep) break;
+#pragma unroll
+        for (int e = 0; e < DE; ++e) wpart[wave][r * HD + lane + 64 * e] = acc[r][e];
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < n_rep * HD; o += kThreads) {
         const int r = o / HD, d = o - r * HD;
-        if (r >= n_rep) continue;
+        const float v = (wpart[0][o] + wpart[1][o]) + (wpart[2][o] + wpart[3][o]);
         const int hq = kvh * n_rep + r;
         if (S == 1) {
-            out[((size_t)t * n_head + hq) * HD + d] = __fdiv_rn(acc[i], l_run[r]);
+            out[((size_t)t * n_head + hq) * HD + d] = __fdiv_rn(v, l_run[r]);
         } else {
             float* pp = part + (((size_t)t * n_head + hq) * S + z) * (HD + 2);
-            pp[d] = acc[i];
+            pp[d] = v;
             if (d == 0) {
                 pp[HD] = m_run[r];
                 pp[HD + 1] = l_run[r];
