@@ -753,13 +753,16 @@ int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_
     hipStream_t s = (hipStream_t)stream;
     Workspace* ws;
     if ((rc = stream_workspace(st, s, 32, 1, &ws))) return rc;
-    const size_t floats = attention_partial_floats(n_rows, n_head, head_dim);
+    const size_t bytes = attention_workspace_bytes(n_rows, n_head, head_dim);
     {
         std::lock_guard<std::mutex> lk(st->mtx);
-        HIP_TRY(ws->att.ensure(floats * sizeof(float), s));
+        const void* before = ws->att.p;
+        HIP_TRY(ws->att.ensure(bytes, s));
+        // a new allocation starts with zero arrival counters; every launch leaves them zero
+        if (ws->att.p != before) HIP_TRY(gemmw_workspace_init(ws->att.p, ws->att.cap, s));
     }
     HIP_TRY(launch_attention(q, k_cache, v_cache, n_rows, pos0, n_head, n_head_kv, head_dim, out,
-                             (float*)ws->att.p, ws->att.cap / sizeof(float), s));
+                             ws->att.p, ws->att.cap, s));
     return CLLM_HIP_OK;
 }
 

@@ -19,8 +19,8 @@
 // every K and V load of a chunk issued before the arithmetic that needs it; the four waves'
 // partials are added at the end.
 // Long sequences are split over several workgroups whose (max, sum, unnormalised output)
-// partials a second kernel combines, so a decode step (one query row) still spreads over
-// the device. The summation order differs from the reference's (per-chunk and per-split
+// partials the last of them to finish combines (a per-(row, KV head) arrival counter), so a
+// decode step (one query row) still spreads over the device in one launch. The summation order differs from the reference's (per-chunk and per-split
 // partial sums, output divided by the sum once); the arithmetic is otherwise the same
 // fp32 operations with the device's expf, sinf, cosf and powf.
 #include <hip/hip_runtime.h>
@@ -65,6 +65,8 @@ constexpr int kThreads = 256;
 constexpr int kChunk = 64;       // positions per online-softmax step
 constexpr int kLanesPerPos = 16; // lanes sharing one K row
 constexpr int kMaxRep = 8;       // query heads per KV head
+constexpr int kAttnCounters = 1024;  // (row, KV head) pairs a split launch may have
+constexpr int kMaxSplits = 256;      // sequence splits per (row, KV head)
 
 // HD = head_dim (multiple of 64, at most 256). Partials of split z for query head hq of row
 // t: part[((t * n_head + hq) * S + z) * (HD + 2) + ...] = unnormalised output [HD], max, sum.
@@ -73,7 +75,7 @@ template <int HD>
 __global__ __launch_bounds__(kThreads) void k_attention(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
     int n_head, int n_kv, int pos0, int split_len, float scale, float* __restrict__ part,
-    float* __restrict__ out) {
+    int* __restrict__ counters, float* __restrict__ out) {
     constexpr int PER = HD / kLanesPerPos;  // K elements per lane (4 .. 16)
     __shared__ float sc[kMaxRep][kChunk];
     __shared__ float m_run[kMaxRep], l_run[kMaxRep], corr[kMaxRep];
@@ -128,6 +130,16 @@ __global__ __launch_bounds__(kThreads) void k_attention(
                 kv[round][e + 3] = v.w;
             }
         }
+        // this wave's V rows, issued with the K rows so both latencies overlap the score and softmax
+        // work (rows past the end are clamped, their probability is zero)
+        float vv[16][DE];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int pc = min(c0 + wave * 16 + j, end - 1);
+            const float* vr = vc + (size_t)pc * kv_dim + kvh * HD + lane;
+#pragma unroll
+            for (int e = 0; e < DE; ++e) vv[j][e] = vr[64 * e];
+        }
 #pragma unroll
         for (int round = 0; round < kChunk / 16; ++round) {
             const int slot = round * 16 + wave * 4 + sub;
@@ -144,16 +156,6 @@ __global__ __launch_bounds__(kThreads) void k_attention(
                 d += __shfl_xor(d, 1, 16);
                 if (seg == 0) sc[r][slot] = p < end ? __fmul_rn(d, scale) : -INFINITY;
             }
-        }
-        // this wave's V rows, issued before the softmax bookkeeping so their latency hides
-        // behind it (rows past the end are clamped, their probability is zero)
-        float vv[16][DE];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int pc = min(c0 + wave * 16 + j, end - 1);
-            const float* vr = vc + (size_t)pc * kv_dim + kvh * HD + lane;
-#pragma unroll
-            for (int e = 0; e < DE; ++e) vv[j][e] = vr[64 * e];
         }
         __syncthreads();
         // running max per head; the factor that rescales what is already summed
@@ -204,87 +206,104 @@ __global__ __launch_bounds__(kThreads) void k_attention(
         for (int e = 0; e < DE; ++e) wpart[wave][r * HD + lane + 64 * e] = acc[r][e];
     }
     __syncthreads();
+    if (S == 1) {
+        for (int o = threadIdx.x; o < n_rep * HD; o += kThreads) {
+            const int r = o / HD, d = o - r * HD;
+            const float v = (wpart[0][o] + wpart[1][o]) + (wpart[2][o] + wpart[3][o]);
+            out[((size_t)t * n_head + kvh * n_rep + r) * HD + d] = __fdiv_rn(v, l_run[r]);
+        }
+        return;
+    }
+    // Several splits: write this split's partial; the last split of (row, KV head) to
+    // arrive, found by a counter it resets, combines them all. The partials cross XCDs, whose
+    // L2s are not coherent with each other, so they are stored and loaded as relaxed
+    // agent-scope atomics (coherent device-wide by themselves; no L2-wide fence).
     for (int o = threadIdx.x; o < n_rep * HD; o += kThreads) {
         const int r = o / HD, d = o - r * HD;
         const float v = (wpart[0][o] + wpart[1][o]) + (wpart[2][o] + wpart[3][o]);
-        const int hq = kvh * n_rep + r;
-        if (S == 1) {
-            out[((size_t)t * n_head + hq) * HD + d] = __fdiv_rn(v, l_run[r]);
-        } else {
-            float* pp = part + (((size_t)t * n_head + hq) * S + z) * (HD + 2);
-            pp[d] = v;
-            if (d == 0) {
-                pp[HD] = m_run[r];
-                pp[HD + 1] = l_run[r];
-            }
+        float* pp = part + (((size_t)t * n_head + kvh * n_rep + r) * S + z) * (HD + 2);
+        __hip_atomic_store(pp + d, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+            __hip_atomic_store(pp + HD, m_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pp + HD + 1, l_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-}
-
-// grid (n_head, rows), 256 threads, S <= kMaxSplits: out = sum_z e^(m_z - M) o_z /
-// sum_z e^(m_z - M) l_z. The split maxima and sums are read once, in parallel, into LDS.
-constexpr int kMaxSplits = 256;
-
-__global__ __launch_bounds__(256) void k_attention_combine(const float* __restrict__ part,
-                                                           int n_head, int hd, int S,
-                                                           float* __restrict__ out) {
-    __shared__ float wz[kMaxSplits], lz[kMaxSplits];
-    __shared__ float red[4];
-    const int hq = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const float* pp = part + ((size_t)t * n_head + hq) * S * (hd + 2);
-    float m = -INFINITY;
-    if (tid < S) {
-        m = pp[(size_t)tid * (hd + 2) + hd];
-        lz[tid] = pp[(size_t)tid * (hd + 2) + hd + 1];
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
+    __syncthreads();
+    __shared__ int last;
+    if (threadIdx.x == 0) {
+        int* cnt = counters + (size_t)t * n_kv + kvh;
+        const int arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = arrived == S - 1;
+        if (arrived == S - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    float M = m;
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    if ((tid & 63) == 0) red[tid >> 6] = M;
     __syncthreads();
-    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    if (tid < S) wz[tid] = m == -INFINITY ? 0.0f : expf(m - M);
+    if (!last) return;
+    // out = sum_z e^(m_z - M) o_z / sum_z e^(m_z - M) l_z, per head of the group. The maxima
+    // and sums of all splits are loaded at once (one per thread) into LDS; each output then
+    // reads its S values eight loads at a time.
+    auto ld = [](const float* a) {
+        return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    __shared__ float wz[kMaxRep][kMaxSplits], lsum[kMaxRep];
+    float* mz = &wpart[0][0];  // the wave partials are consumed: reuse as [kMaxRep][S] maxima
+    for (int i = threadIdx.x; i < n_rep * S; i += kThreads) {
+        const int r = i / S, zz = i - r * S;
+        const float* pz = part + (((size_t)t * n_head + kvh * n_rep + r) * S + zz) * (HD + 2);
+        mz[r * S + zz] = ld(pz + HD);
+        wz[r][zz] = ld(pz + HD + 1);  // the sums for now
+    }
     __syncthreads();
-    if (tid >= hd) return;
-    float num = 0.0f, den = 0.0f;
-    int z = 0;
-    for (; z + 4 <= S; z += 4) {
-        float v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = pp[(size_t)(z + u) * (hd + 2) + tid];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            num = __builtin_fmaf(wz[z + u], v[u], num);
-            den = __builtin_fmaf(wz[z + u], lz[z + u], den);
+    if (threadIdx.x < n_rep) {
+        const int r = threadIdx.x;
+        float M = -INFINITY;
+        for (int zz = 0; zz < S; ++zz) M = fmaxf(M, mz[r * S + zz]);
+        float den = 0.0f;
+        for (int zz = 0; zz < S; ++zz) {
+            const float m = mz[r * S + zz];
+            const float wgt = m == -INFINITY ? 0.0f : expf(m - M);
+            den = __builtin_fmaf(wgt, wz[r][zz], den);
+            wz[r][zz] = wgt;
         }
+        lsum[r] = den;
     }
-    for (; z < S; ++z) {
-        num = __builtin_fmaf(wz[z], pp[(size_t)z * (hd + 2) + tid], num);
-        den = __builtin_fmaf(wz[z], lz[z], den);
+    __syncthreads();
+    for (int o = threadIdx.x; o < n_rep * HD; o += kThreads) {
+        const int r = o / HD, d = o - r * HD;
+        const float* pp = part + ((size_t)t * n_head + kvh * n_rep + r) * S * (HD + 2) + d;
+        float num = 0.0f;
+        int zz = 0;
+        for (; zz + 8 <= S; zz += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = ld(pp + (size_t)(zz + u) * (HD + 2));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) num = __builtin_fmaf(wz[r][zz + u], v[u], num);
+        }
+        for (; zz < S; ++zz) num = __builtin_fmaf(wz[r][zz], ld(pp + (size_t)zz * (HD + 2)), num);
+        out[((size_t)t * n_head + kvh * n_rep + r) * HD + d] = __fdiv_rn(num, lsum[r]);
     }
-    out[((size_t)t * n_head + hq) * hd + tid] = __fdiv_rn(num, den);
 }
 
 template <int HD>
 hipError_t launch_attention_hd(const float* q, const float* kc, const float* vc, int rows,
                                int pos0, int n_head, int n_kv, float* out, float* part,
-                               size_t part_floats, hipStream_t stream) {
+                               size_t part_floats, int* counters, hipStream_t stream) {
     const int L_max = pos0 + rows;
     // splits: enough workgroups for the device, at least one chunk per split
     const int64_t base = (int64_t)n_kv * rows;
     int S = (int)std::min<int64_t>(std::max<int64_t>(1, (1024 + base - 1) / base),
                                    (L_max + kChunk - 1) / kChunk);
     S = std::min(S, kMaxSplits);
-    if ((size_t)rows * n_head * S * (HD + 2) > part_floats) S = 1;
+    if ((size_t)rows * n_head * S * (HD + 2) > part_floats || !counters ||
+        (int64_t)rows * n_kv > kAttnCounters)
+        S = 1;
     const int split_len = ((L_max + S - 1) / S + kChunk - 1) / kChunk * kChunk;
     S = (L_max + split_len - 1) / split_len;
     const float scale = 1.0f / std::sqrt((float)HD);  // engine.cpp:121, IEEE on the host
     hipLaunchKernelGGL((k_attention<HD>), dim3((unsigned)n_kv, (unsigned)rows, (unsigned)S),
                        dim3(kThreads), 0, stream, q, kc, vc, n_head, n_kv, pos0, split_len, scale,
-                       part, out);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || S == 1) return e;
-    hipLaunchKernelGGL(k_attention_combine, dim3((unsigned)n_head, (unsigned)rows), dim3(256), 0,
-                       stream, part, n_head, HD, S, out);
+                       part, counters, out);
     return hipGetLastError();
 }
 
@@ -300,10 +319,10 @@ hipError_t launch_rope_neox(float* x, int rows, int n_heads, float* x2, int n_he
     return hipGetLastError();
 }
 
-size_t attention_partial_floats(int rows, int n_head, int head_dim) {
+size_t attention_workspace_bytes(int rows, int n_head, int head_dim) {
     // at most 1024 / (n_kv * rows) + 1 splits, n_kv >= 1
     const size_t splits = (size_t)(1024 / std::max(rows, 1) + 1);
-    return (size_t)rows * n_head * splits * (head_dim + 2);
+    return kAttnCounters * sizeof(int) + (size_t)rows * n_head * splits * (head_dim + 2) * sizeof(float);
 }
 
 bool attention_supported(int head_dim, int n_head, int n_kv) {
@@ -311,15 +330,21 @@ bool attention_supported(int head_dim, int n_head, int n_kv) {
            n_head % n_kv == 0 && n_head / n_kv <= kMaxRep;
 }
 
+// The workspace: kAttnCounters arrival counters (zero when allocated, left zero by every
+// launch), then the split partials.
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int pos0,
-                            int n_head, int n_kv, int head_dim, float* out, float* part,
-                            size_t part_floats, hipStream_t stream) {
+                            int n_head, int n_kv, int head_dim, float* out, void* ws,
+                            size_t ws_bytes, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     if (!attention_supported(head_dim, n_head, n_kv)) return hipErrorInvalidValue;
+    constexpr size_t kCountBytes = kAttnCounters * sizeof(int);
+    int* counters = ws && ws_bytes > kCountBytes ? (int*)ws : nullptr;
+    float* part = counters ? (float*)((char*)ws + kCountBytes) : nullptr;
+    const size_t part_floats = counters ? (ws_bytes - kCountBytes) / sizeof(float) : 0;
     switch (head_dim) {
-        case 64: return launch_attention_hd<64>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, stream);
-        case 128: return launch_attention_hd<128>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, stream);
-        default: return launch_attention_hd<256>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, stream);
+        case 64: return launch_attention_hd<64>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, stream);
+        case 128: return launch_attention_hd<128>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, stream);
+        default: return launch_attention_hd<256>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, stream);
     }
 }
 

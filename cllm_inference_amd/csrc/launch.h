@@ -95,15 +95,15 @@ hipError_t launch_add(float* x, const float* d, int64_t n, hipStream_t stream);
 // of n_heads x head_dim (row t at position pos0 + t), optionally on a second tensor x2 of
 // n_heads2 heads per row in the same launch (queries and keys), and grouped-query attention of `rows`
 // query rows (n_head x head_dim each) over KV caches of n_kv x head_dim per position, query
-// row t seeing positions [0, pos0 + t]. `part` (at least attention_partial_floats floats, or
-// null for no sequence split) holds the split partials.
+// row t seeing positions [0, pos0 + t]. `ws` (attention_workspace_bytes, zeroed when first
+// allocated; null for no sequence split) holds the splits' arrival counters and partials.
 hipError_t launch_rope_neox(float* x, int rows, int n_heads, float* x2, int n_heads2,
                             int head_dim, int pos0, float base, hipStream_t stream);
 bool attention_supported(int head_dim, int n_head, int n_kv);
-size_t attention_partial_floats(int rows, int n_head, int head_dim);
+size_t attention_workspace_bytes(int rows, int n_head, int head_dim);
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int pos0,
-                            int n_head, int n_kv, int head_dim, float* out, float* part,
-                            size_t part_floats, hipStream_t stream);
+                            int n_head, int n_kv, int head_dim, float* out, void* ws,
+                            size_t ws_bytes, hipStream_t stream);
 
 // Rows ids[0..n) of a weight matrix of any GGML type, dequantized to fp32 out[n][k] exactly
 // as the reference's dequantize_block (the embedding lookup). k_gemv_f.hip.
