@@ -96,11 +96,36 @@ __device__ __forceinline__ A2<NDW> load_a2(const uint8_t* p) {
     return r;
 }
 
+
+
 template <int NDW>
 __device__ __forceinline__ void align_a2(const A2<NDW>& r, uint32_t sh, uint32_t (&out)[NDW]) {
 #pragma unroll
     for (int i = 0; i < NDW - 1; ++i) out[i] = __builtin_amdgcn_alignbyte(r.v[i + 1], r.v[i], sh);
     out[NDW - 1] = __builtin_amdgcn_alignbyte(r.tail, r.v[NDW - 1], sh);
+}
+
+// The same field read from a weight piece staged in LDS at byte offset off of buf (any
+// alignment of 2): the aligned dwords at off & ~3 and the last two bytes.
+template <int NDW>
+__device__ __forceinline__ A2<NDW> lds_a2(const uint8_t* buf, int off) {
+    const uint32_t* q = (const uint32_t*)(buf + (off & ~3));
+    A2<NDW> r;
+    if constexpr (NDW % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < NDW; i += 4) {
+            const u32x4_a4 t = *(const u32x4_a4*)(q + i);
+            r.v[i] = t.x; r.v[i + 1] = t.y; r.v[i + 2] = t.z; r.v[i + 3] = t.w;
+        }
+    } else if constexpr (NDW == 2) {
+        const u32x2_a4 t = *(const u32x2_a4*)q;
+        r.v[0] = t.x; r.v[1] = t.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < NDW; ++i) r.v[i] = q[i];
+    }
+    r.tail = *(const uint16_t*)(buf + off + 4 * NDW - 2);
+    return r;
 }
 
 // ------------------------------------------------------------------------------ Q4_K / Q5_K
@@ -109,6 +134,8 @@ __device__ __forceinline__ void align_a2(const A2<NDW>& r, uint32_t sh, uint32_t
 template <bool Q5>
 struct TraitsK45 {
     static constexpr int UNIT = 64;
+    static constexpr int BLK_BYTES = Q5 ? Q5_K_BYTES : Q4_K_BYTES, UNITS_PER_BLK = 4;
+    static constexpr bool ALIGN16 = true;  // every field is a whole 16-byte piece
     static constexpr bool NEED_XM = true, NEED_XB = false, NEED_HS = false;
     struct Raw {
         u32x4 h, qa, qb;
@@ -125,6 +152,21 @@ struct TraitsK45 {
         if constexpr (Q5) {
             r.hha = ld_u32x4(blk + Q5_K_QH);
             r.hhb = ld_u32x4(blk + Q5_K_QH + 16);
+        }
+        return r;
+    }
+    // Unit u (its quarter c = u & 3) of the super-block staged at byte o of buf.
+    static __device__ __forceinline__ Raw load_lds(const uint8_t* buf, int o, int u) {
+        const int c = u & 3;
+        const uint8_t* blk = buf + o;
+        const uint8_t* qp = blk + (Q5 ? Q5_K_QS : Q4_K_QS) + 32 * c;
+        Raw r;
+        r.h = *(const u32x4*)blk;
+        r.qa = *(const u32x4*)qp;
+        r.qb = *(const u32x4*)(qp + 16);
+        if constexpr (Q5) {
+            r.hha = *(const u32x4*)(blk + Q5_K_QH);
+            r.hhb = *(const u32x4*)(blk + Q5_K_QH + 16);
         }
         return r;
     }
@@ -193,6 +235,8 @@ struct TraitsK45 {
 // a sub-block form the reference's integer sc_a*dot_a + sc_b*dot_b with one DPP move.
 struct TraitsQ6K {
     static constexpr int UNIT = 64;
+    static constexpr int BLK_BYTES = Q6_K_BYTES, UNITS_PER_BLK = 4;
+    static constexpr bool ALIGN16 = false;
     static constexpr bool NEED_XM = false, NEED_XB = false, NEED_HS = true;
     struct Raw {
         A2<4> qa, qb, qh;
@@ -210,6 +254,17 @@ struct TraitsQ6K {
         r.sc = load_a2<2>(blk + Q6_K_SC + 8 * g);
         r.d = ld_u16(blk + Q6_K_D);
         r.sh = (uint32_t)((uintptr_t)blk & 3u);  // every field offset is a multiple of 4
+        return r;
+    }
+    static __device__ __forceinline__ Raw load_lds(const uint8_t* buf, int o, int u) {
+        const int g = (u >> 1) & 1, h = u & 1;
+        Raw r;
+        r.qa = lds_a2<4>(buf, o + 64 * g + 16 * h);
+        r.qb = lds_a2<4>(buf, o + 64 * g + 32 + 16 * h);
+        r.qh = lds_a2<4>(buf, o + Q6_K_QH + 32 * g + 16 * h);
+        r.sc = lds_a2<2>(buf, o + Q6_K_SC + 8 * g);
+        r.d = *(const uint16_t*)(buf + o + Q6_K_D);
+        r.sh = (uint32_t)o & 3u;
         return r;
     }
     template <int MR>
@@ -267,6 +322,8 @@ struct TraitsQ6K {
 // ------------------------------------------------------------------------------------ Q8_0
 struct TraitsQ80 {
     static constexpr int UNIT = 32;
+    static constexpr int BLK_BYTES = Q8_0_BYTES, UNITS_PER_BLK = 1;
+    static constexpr bool ALIGN16 = false;
     static constexpr bool NEED_XM = false, NEED_XB = false, NEED_HS = false;
     struct Raw {
         A2<8> q;
@@ -278,6 +335,13 @@ struct TraitsQ80 {
         r.q = load_a2<8>(blk + 2);
         r.d = ld_u16(blk);
         r.sh = (uint32_t)((uintptr_t)(blk + 2) & 3u);
+        return r;
+    }
+    static __device__ __forceinline__ Raw load_lds(const uint8_t* buf, int o, int) {
+        Raw r;
+        r.q = lds_a2<8>(buf, o + 2);
+        r.d = *(const uint16_t*)(buf + o);
+        r.sh = (uint32_t)(o + 2) & 3u;
         return r;
     }
     template <int MR>
@@ -305,6 +369,8 @@ struct TraitsQ80 {
 template <bool Q5>
 struct TraitsQ450 {
     static constexpr int UNIT = 32;
+    static constexpr int BLK_BYTES = Q5 ? Q5_0_BYTES : Q4_0_BYTES, UNITS_PER_BLK = 1;
+    static constexpr bool ALIGN16 = false;
     static constexpr bool NEED_XM = false, NEED_XB = true, NEED_HS = false;
     struct Raw {
         A2<4> q;
@@ -322,6 +388,14 @@ struct TraitsQ450 {
         if constexpr (Q5) r.qh = load_a2<1>(blk + 2);
         r.d = ld_u16(blk);
         r.sh = (uint32_t)((uintptr_t)(blk + 2) & 3u);  // qh (+2) and qs (+6) share it
+        return r;
+    }
+    static __device__ __forceinline__ Raw load_lds(const uint8_t* buf, int o, int) {
+        Raw r;
+        r.q = lds_a2<4>(buf, o + (Q5 ? 6 : 2));
+        if constexpr (Q5) r.qh = lds_a2<1>(buf, o + 2);
+        r.d = *(const uint16_t*)(buf + o);
+        r.sh = (uint32_t)(o + 2) & 3u;
         return r;
     }
     template <int MR>
@@ -740,6 +814,186 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_
     }
 }
 
+// ------------------------------------------------------------ weight stream staged in LDS
+// The same GEMV with the weight bytes routed through LDS. An item (a row's slice of 64 units:
+// 16 K-quant super-blocks or 64 32-element blocks) is read as whole, aligned 16-byte pieces
+// straight into one of the wave's S LDS slots (global_load_lds: piece 64 L + l of the item
+// goes to lane l of wave-load L and lands at byte 16 (64 L + l) of the slot), so each load
+// instruction reads 1 KB of contiguous memory, where k_gemv's per-unit field loads spread each
+// instruction over 16 to 64 separate places of a row. The lanes then read their unit's fields
+// from the slot and compute exactly as k_gemv. Items are cut into pieces starting at the
+// 16-byte boundary at or below the item, and pieces past its end repeat its last piece, so
+// every read stays within 16-byte pieces that hold bytes of the matrix.
+//
+// The slots are private to their wave: no barrier orders them, only this wave's vmcnt. The
+// loads of an item are the NL wave-loads issued for it, in order, and every item issues the
+// same NL (the last items of a wave refill their slots with clamped, repeated items), so
+// waiting until at most (S - 1) NL vector-memory operations are outstanding means the oldest
+// slot has landed; stores issued in between only make that wait stricter.
+constexpr int kSlotBytes = 4096;
+
+template <class Tr>
+__host__ __device__ constexpr int item_blocks() { return 64 / Tr::UNITS_PER_BLK; }
+template <class Tr>
+__host__ __device__ constexpr int item_loads() {
+    return (item_blocks<Tr>() * Tr::BLK_BYTES + 15 + 1023) / 1024;
+}
+static_assert(item_loads<TraitsQ6K>() * 1024 <= kSlotBytes, "slot size");
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, the other counters at max).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// One wave-load of 16 bytes per lane from g into LDS at lds + 16 * lane (global_load_lds).
+// Written as inline assembly so that the compiler does not track it: it would otherwise wait
+// for every load in flight before each LDS read of the kernel, since it cannot tell which LDS
+// bytes a load writes. The caller orders the reads with wait_vmcnt.
+__device__ __forceinline__ void dma16(const void* g, const uint8_t* lds) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)lds;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(g), "s"(m0) : "memory", "m0");
+}
+
+template <uint32_t T, int MR, int S, int WV>
+__global__ __launch_bounds__(64 * WV) void k_gemv_st(GemvSegs sg, int64_t row_bytes, int k, int n,
+                                                     const int8_t* __restrict__ qs,
+                                                     const float* __restrict__ xs,
+                                                     const int32_t* __restrict__ xb,
+                                                     const float* __restrict__ x_f32,
+                                                     int accumulate) {
+    using Tr = typename TraitsOf<T>::type;
+    constexpr int NL = item_loads<Tr>();
+    constexpr int BPI = item_blocks<Tr>();
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_waves = gridDim.x * WV;
+    const int wid = blockIdx.x * WV + wave;
+    const int units = k / Tr::UNIT;
+    const int iters = (units + 63) / 64;
+    const int nblk = units / Tr::UNITS_PER_BLK;
+    const int my_rows = wid < n ? (n - 1 - wid) / n_waves + 1 : 0;
+    const int n_items = my_rows * iters;
+    // One LDS array per slot: with the slots in distinct objects the compiler can tell that a
+    // read of one slot does not touch the loads in flight to the other (it would otherwise wait
+    // for every outstanding load before each LDS read).
+    static_assert(S == 1 || S == 2, "one or two slots");
+    __shared__ __align__(16) uint8_t slot_a[WV * kSlotBytes];
+    __shared__ __align__(16) uint8_t slot_b[S == 2 ? WV * kSlotBytes : 16];
+    auto slot_ptr = [&](int p) { return (p == 0 ? slot_a : slot_b) + wave * kSlotBytes; };
+
+    // First byte of item `item` (clamped to the wave's items; a wave with none reads row n-1).
+    auto item_first = [&](int item, int& it) {
+        const int c = max(0, min(item, n_items - 1));
+        const int t = c / iters;
+        it = c - t * iters;
+        const int jr = min(wid + t * n_waves, n - 1);
+        const int s = seg_of(sg, jr);
+        const uint8_t* row = seg_pick(s, sg.w[0], sg.w[1], sg.w[2]) +
+                             (int64_t)(jr - seg_pick(s, sg.start[0], sg.start[1], sg.start[2])) * row_bytes;
+        return row + (size_t)(it * BPI) * Tr::BLK_BYTES;
+    };
+    auto issue = [&](int item, int slot) {
+        int it;
+        const uint8_t* first = item_first(item, it);
+        const int mis = (int)((uintptr_t)first & 15u);
+        const int last = (mis + min(BPI, nblk - it * BPI) * Tr::BLK_BYTES - 1) >> 4;
+        const uint8_t* base = first - mis;
+#pragma unroll
+        for (int L = 0; L < NL; ++L)
+            dma16(base + 16 * min(64 * L + lane, last), slot_ptr(slot) + L * 1024);
+    };
+
+    const ActLds a = act_layout<T, MR>(lds, k);
+    StageCopy<T, MR> sc{qs, xs, xb, k, {}, {}, {}};
+    StageQuant<T, MR> sq{x_f32, k, {}};
+    const bool fused = x_f32 != nullptr;
+    if (fused)
+        sq.issue();
+    else
+        sc.issue();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int p = 0; p < S; ++p) issue(p, p);
+    __builtin_amdgcn_sched_barrier(0);
+    if (fused) {
+        sq.commit(a);
+        sq.rest(a);
+    } else {
+        sc.commit(a);
+        sc.rest(a);
+    }
+    // The activation rows are complete in LDS once every wave's LDS writes have: a fenced
+    // barrier would also wait for the ring loads (LDS writes of this wave too).
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    if (n_items == 0) {
+        wait_vmcnt<0>();
+        return;
+    }
+
+    float acc[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
+
+    const int n_pad = ((n_items + S - 1) / S) * S;
+    for (int base = 0; base < n_pad; base += S) {
+#pragma unroll
+        for (int p = 0; p < S; ++p) {
+            const int item = base + p;
+            const int t = item / iters, it = item - t * iters;
+            const int u = lane + 64 * it;
+            const bool row_end = item < n_items && it == iters - 1;
+            wait_vmcnt<(S - 1) * NL>();
+            __builtin_amdgcn_sched_barrier(0);
+            {
+                int itc;
+                const int mis = (int)((uintptr_t)item_first(item, itc) & 15u);
+                const int uc = min(u, units - 1) - 64 * itc;  // unit within the item
+                const typename Tr::Raw raw = Tr::load_lds(
+                    slot_ptr(p), mis + (uc / Tr::UNITS_PER_BLK) * Tr::BLK_BYTES, uc);
+                float nacc[MR];
+#pragma unroll
+                for (int r = 0; r < MR; ++r) nacc[r] = acc[r];
+                Tr::template compute<MR>(raw, min(u, units - 1), a, nacc);
+                const bool keep = item < n_items && u < units;
+#pragma unroll
+                for (int r = 0; r < MR; ++r) acc[r] = keep ? nacc[r] : acc[r];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            issue(item + S, p);
+            // No vector-memory load in the loop but the ring's: one would have to be waited for
+            // behind the refill just issued. The bias is read by a scalar load (the constant
+            // address space; it is never written here) and the residual add is an atomic add
+            // of the result (one wave owns the row, so it is the plain sum y + v).
+            if (row_end) {
+                const int jv = __builtin_amdgcn_readfirstlane(wid + t * n_waves);
+                const int s = seg_of(sg, jv);
+                const int j = jv - seg_pick(s, sg.start[0], sg.start[1], sg.start[2]);
+                const float* bias = seg_pick(s, sg.bias[0], sg.bias[1], sg.bias[2]);
+                float* y = seg_pick(s, sg.y[0], sg.y[1], sg.y[2]);
+                const int ny = seg_pick(s, sg.rows[0], sg.rows[1], sg.rows[2]);
+                const float bj = bias ? ((const __attribute__((address_space(4))) float*)bias)[j] : 0.0f;
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    const float v = wave_sum(acc[r]) + bj;
+                    if (lane == r) {
+                        float* yp = y + (size_t)r * ny + j;
+                        if (accumulate)
+                            __hip_atomic_fetch_add(yp, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        else
+                            *yp = v;
+                    }
+                    acc[r] = 0.0f;
+                }
+            }
+        }
+    }
+    wait_vmcnt<0>();  // the refills past the wave's last item land before its LDS is released
+}
+
 static int g_cu_count = 0;
 
 static int cu_count() {
@@ -804,6 +1058,48 @@ static int64_t resident_waves(size_t shmem) {
     return (int64_t)blocks * (gemv_threads<MR>() / 64) * cu_count();
 }
 
+// The LDS-staged stream, one slot per wave, 16 waves per workgroup (from sweeps on MI355X,
+// cold HBM, fused quantization: the Q6_K 128256x4096 head 72 us against 73-78 us for 8-wave
+// workgroups at 3-4 per CU and 78-81 us with two slots; the register-ring k_gemv 81-88 us on
+// the same boxes). Grid: the workgroups resident at once, or fewer if the rows run out.
+constexpr int kStWaves = 16;
+
+template <uint32_t T>
+static int64_t resident_st_wgs(size_t shmem) {
+    static std::atomic<uint64_t> cache{0};
+    uint64_t c = cache.load(std::memory_order_relaxed);
+    int blocks;
+    if (c != 0 && (c >> 16) == shmem) {
+        blocks = (int)(c & 0xFFFFu);
+    } else {
+        blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv_st<T, 1, 1, kStWaves>),
+                                                         64 * kStWaves, shmem) != hipSuccess ||
+            blocks < 1)
+            blocks = 1;
+        cache.store(((uint64_t)shmem << 16) | (uint64_t)(blocks & 0xFFFF), std::memory_order_relaxed);
+    }
+    return (int64_t)blocks * cu_count();
+}
+
+template <uint32_t T>
+static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
+                            const int32_t* xb, const float* x_f32, int accumulate, int64_t items,
+                            hipStream_t stream) {
+    const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
+    const size_t shmem = act_lds_bytes<T>(1, k);
+    const int64_t grid = std::min((items + kStWaves - 1) / kStWaves, resident_st_wgs<T>(shmem));
+    hipLaunchKernelGGL((k_gemv_st<T, 1, 1, kStWaves>), dim3((unsigned)grid), dim3(64 * kStWaves), shmem,
+                       stream, sg, row_bytes, k, n, qs, xs, xb, x_f32, accumulate);
+    return hipGetLastError();
+}
+
+// Q6_K decode streams of at least this many weight bytes take the LDS-staged kernel: its
+// contiguous nontemporal loads win on long streams (the 128256x4096 head, 431 MB: 72 against
+// 81-88 us; the 4096x14336 FFN down matrix, 48 MB: 15.5 against 18.2 us) and lose on short ones,
+// where its extra startup shows (4096x4096, 14 MB: 6.5 against 6.1 us).
+constexpr int64_t kStagedMinBytes = 32ll << 20;
+
 template <uint32_t T, int MR, int P>
 static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
                            const int32_t* xb, const float* x_f32, int accumulate, int waves,
@@ -837,6 +1133,11 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
     const int64_t simds = (int64_t)cu_count() * 4;
     const GemvTuning& tu = gemv_tuning();
     const size_t shmem = act_lds_bytes<T>(MR, k);
+    if constexpr (T == T_Q6_K && MR == 1) {
+        const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
+        if (bytes >= kStagedMinBytes && act_lds_bytes<T>(1, k) <= 64 * 1024)
+            return launch_st<T>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
+    }
     if (MR > 2 && items > simds * 32) {
         const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2>(shmem));
         return launch_t<T, MR, 2>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);

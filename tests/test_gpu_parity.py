@@ -115,6 +115,51 @@ def test_q6_k_output_head_full_size(gpu, orc):
     check_close(y1[:, others], yo, exact, abs_sum, "c2-oracle")
 
 
+@pytest.mark.parametrize("k", [4096, 14336])
+def test_q6_k_staged_stream_equals_register_ring(gpu, orc, k):
+    """Q6_K decode streams of at least 32 MB take the LDS-staged kernel and shorter ones the
+    register-ring kernel; both compute the same per-unit terms in the same order, so rows of a
+    40 MB matrix (ragged row count; k = 14336 ends every row with a half item) must equal bit
+    for bit the same rows run as a small matrix -- with a bias, with the residual add, and in
+    the three-matrix launch -- and match the oracle."""
+    import torch
+    qt = S.Q6_K
+    rb = S.row_bytes(qt, k)
+    n = (40 << 20) // rb + 3
+    print("staged Q6_K", n, k, flush=True)
+    w = S.make_weight(qt, n, k, 9100 + k)
+    x = S.make_activation(1, k, 9200 + k, outliers=True)
+    bias = np.random.default_rng(k).standard_normal(n).astype(np.float32)
+    rows = np.r_[0:96, n // 2:n // 2 + 64, n - 96:n]
+    sub = w.reshape(n, rb)[rows].reshape(-1)
+    wd, xd, bd = _dev(w), _dev(x), _dev(bias)
+    sd, sbd = _dev(sub), _dev(bias[rows])
+
+    y = gpu.matmul_quant_dev(xd, wd, qt, bd, k, n).cpu().numpy()
+    y_small = gpu.matmul_quant_dev(xd, sd, qt, sbd, k, len(rows)).cpu().numpy()
+    assert np.array_equal(bits(y[:, rows]), bits(y_small))
+    exact, abs_sum = orc.matmul_f64(x, sub, qt, bias[rows], k, len(rows), 1)
+    yo = orc.matmul(x, sub, qt, bias[rows], k, len(rows), 1)
+    check_close(y[:, rows], yo, exact, abs_sum, "staged")
+
+    base = np.random.default_rng(k + 1).standard_normal((1, n)).astype(np.float32)
+    r = _dev(base)
+    gpu.matmul_quant_residual_dev(xd, wd, qt, bd, k, n, r)
+    r_small = _dev(base[:, rows])
+    gpu.matmul_quant_residual_dev(xd, sd, qt, sbd, k, len(rows), r_small)
+    assert np.array_equal(bits(r.cpu().numpy()[:, rows]), bits(r_small.cpu().numpy()))
+
+    # three matrices in one launch (40 MB in all): the segment of every row resolves as in
+    # separate launches
+    qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+    cuts = [0, n // 3, n // 3 + 1000, n]
+    mats = [_dev(w.reshape(n, rb)[a:b].reshape(-1)) for a, b in zip(cuts, cuts[1:])]
+    outs = gpu.gemv_q8_multi_dev(mats, qt, k, [b - a for a, b in zip(cuts, cuts[1:])], qs, sc, bs)
+    y_nb = gpu.matmul_quant_dev(xd, wd, qt, None, k, n).cpu().numpy()
+    assert np.array_equal(bits(np.concatenate([o.cpu().numpy() for o in outs], axis=1)), bits(y_nb))
+    torch.cuda.synchronize()
+
+
 def test_all_types_shapes_bias_vs_reference_golden(gpu, orc):
     cases = split_cases(load_golden("types.npz"))
     for tag, c in cases.items():
