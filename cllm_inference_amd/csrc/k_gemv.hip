@@ -822,23 +822,29 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_
 // instruction reads 1 KB of contiguous memory, where k_gemv's per-unit field loads spread each
 // instruction over 16 to 64 separate places of a row. The lanes then read their unit's fields
 // from the slot and compute exactly as k_gemv. Items are cut into pieces starting at the
-// 16-byte boundary at or below the item, and pieces past its end repeat its last piece, so
-// every read stays within 16-byte pieces that hold bytes of the matrix.
+// 16-byte boundary at or below the item, so every read stays within 16-byte pieces that hold
+// bytes of the matrix; lanes past an item's last piece stay idle, except lane 0, which reads
+// the last piece again (into its own place, past the item) so that every item issues the
+// same NL load instructions.
 //
 // The slots are private to their wave: no barrier orders them, only this wave's vmcnt. The
-// loads of an item are the NL wave-loads issued for it, in order, and every item issues the
-// same NL (the last items of a wave refill their slots with clamped, repeated items), so
-// waiting until at most (S - 1) NL vector-memory operations are outstanding means the oldest
-// slot has landed; stores issued in between only make that wait stricter.
-constexpr int kSlotBytes = 4096;
-
+// loads of an item are its NL wave-loads, in order, and every item issues NL (the last items
+// of a wave refill their slots with clamped, repeated items), so waiting until at most
+// (S - 1) NL vector-memory operations are outstanding means the oldest slot has landed;
+// stores issued in between only make that wait stricter.
 template <class Tr>
 __host__ __device__ constexpr int item_blocks() { return 64 / Tr::UNITS_PER_BLK; }
 template <class Tr>
-__host__ __device__ constexpr int item_loads() {
-    return (item_blocks<Tr>() * Tr::BLK_BYTES + 15 + 1023) / 1024;
+__host__ __device__ constexpr int item_pieces() {  // 16-byte pieces, a misaligned start included
+    return (15 + item_blocks<Tr>() * Tr::BLK_BYTES - 1) / 16 + 1;
 }
-static_assert(item_loads<TraitsQ6K>() * 1024 <= kSlotBytes, "slot size");
+template <class Tr>
+__host__ __device__ constexpr int item_loads() { return (item_pieces<Tr>() + 63) / 64; }
+template <class Tr>
+__host__ __device__ constexpr int slot_bytes() {
+    return 16 * (item_pieces<Tr>() > 64 * (item_loads<Tr>() - 1) + 1 ? item_pieces<Tr>()
+                                                                     : 64 * (item_loads<Tr>() - 1) + 1);
+}
 
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits 3:0 and 15:14, the other counters at max).
 template <int N>
@@ -876,13 +882,9 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_st(GemvSegs sg, int64_t row_by
     const int nblk = units / Tr::UNITS_PER_BLK;
     const int my_rows = wid < n ? (n - 1 - wid) / n_waves + 1 : 0;
     const int n_items = my_rows * iters;
-    // One LDS array per slot: with the slots in distinct objects the compiler can tell that a
-    // read of one slot does not touch the loads in flight to the other (it would otherwise wait
-    // for every outstanding load before each LDS read).
-    static_assert(S == 1 || S == 2, "one or two slots");
-    __shared__ __align__(16) uint8_t slot_a[WV * kSlotBytes];
-    __shared__ __align__(16) uint8_t slot_b[S == 2 ? WV * kSlotBytes : 16];
-    auto slot_ptr = [&](int p) { return (p == 0 ? slot_a : slot_b) + wave * kSlotBytes; };
+    constexpr int SLOT = slot_bytes<Tr>();
+    __shared__ __align__(16) uint8_t slots[S * WV * SLOT];
+    auto slot_ptr = [&](int p) { return slots + (p * WV + wave) * SLOT; };
 
     // First byte of item `item` (clamped to the wave's items; a wave with none reads row n-1).
     auto item_first = [&](int item, int& it) {
@@ -902,8 +904,10 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_st(GemvSegs sg, int64_t row_by
         const int last = (mis + min(BPI, nblk - it * BPI) * Tr::BLK_BYTES - 1) >> 4;
         const uint8_t* base = first - mis;
 #pragma unroll
-        for (int L = 0; L < NL; ++L)
-            dma16(base + 16 * min(64 * L + lane, last), slot_ptr(slot) + L * 1024);
+        for (int L = 0; L < NL; ++L) {
+            const int c = 64 * L + lane;
+            if (c <= last || lane == 0) dma16(base + 16 * min(c, last), slot_ptr(slot) + L * 1024);
+        }
     };
 
     const ActLds a = act_layout<T, MR>(lds, k);
@@ -1062,9 +1066,7 @@ static int64_t resident_waves(size_t shmem) {
 // cold HBM, fused quantization: the Q6_K 128256x4096 head 72 us against 73-78 us for 8-wave
 // workgroups at 3-4 per CU and 78-81 us with two slots; the register-ring k_gemv 81-88 us on
 // the same boxes). Grid: the workgroups resident at once, or fewer if the rows run out.
-constexpr int kStWaves = 16;
-
-template <uint32_t T>
+template <uint32_t T, int S, int WV>
 static int64_t resident_st_wgs(size_t shmem) {
     static std::atomic<uint64_t> cache{0};
     uint64_t c = cache.load(std::memory_order_relaxed);
@@ -1073,8 +1075,8 @@ static int64_t resident_st_wgs(size_t shmem) {
         blocks = (int)(c & 0xFFFFu);
     } else {
         blocks = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv_st<T, 1, 1, kStWaves>),
-                                                         64 * kStWaves, shmem) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv_st<T, 1, S, WV>),
+                                                         64 * WV, shmem) != hipSuccess ||
             blocks < 1)
             blocks = 1;
         cache.store(((uint64_t)shmem << 16) | (uint64_t)(blocks & 0xFFFF), std::memory_order_relaxed);
@@ -1082,23 +1084,27 @@ static int64_t resident_st_wgs(size_t shmem) {
     return (int64_t)blocks * cu_count();
 }
 
-template <uint32_t T>
+template <uint32_t T, int S, int WV>
 static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
                             const int32_t* xb, const float* x_f32, int accumulate, int64_t items,
                             hipStream_t stream) {
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
     const size_t shmem = act_lds_bytes<T>(1, k);
-    const int64_t grid = std::min((items + kStWaves - 1) / kStWaves, resident_st_wgs<T>(shmem));
-    hipLaunchKernelGGL((k_gemv_st<T, 1, 1, kStWaves>), dim3((unsigned)grid), dim3(64 * kStWaves), shmem,
+    const int64_t grid = std::min((items + WV - 1) / WV, resident_st_wgs<T, S, WV>(shmem));
+    hipLaunchKernelGGL((k_gemv_st<T, 1, S, WV>), dim3((unsigned)grid), dim3(64 * WV), shmem,
                        stream, sg, row_bytes, k, n, qs, xs, xb, x_f32, accumulate);
     return hipGetLastError();
 }
 
-// Q6_K decode streams of at least this many weight bytes take the LDS-staged kernel: its
-// contiguous nontemporal loads win on long streams (the 128256x4096 head, 431 MB: 72 against
-// 81-88 us; the 4096x14336 FFN down matrix, 48 MB: 15.5 against 18.2 us) and lose on short ones,
-// where its extra startup shows (4096x4096, 14 MB: 6.5 against 6.1 us).
-constexpr int64_t kStagedMinBytes = 32ll << 20;
+// Decode streams of at least this many weight bytes take the LDS-staged kernel: its contiguous
+// nontemporal loads win on long streams and lose on short ones, where its extra startup shows.
+// Q6_K: the 128256x4096 head (431 MB) 72-80 against 81-88 us, the 4096x14336 FFN down matrix
+// (48 MB) 15.5 against 18.2 us, 4096x4096 (14 MB) 6.5 against 6.1 us. Q4_K: 128256x4096
+// (295 MB) 52 against 57 us, 14336x4096 (33 MB) 10.1 against 9.1 us. More slots per wave
+// (all of a short stream's items in flight from the start) lost everywhere: Q4_K 14336x4096
+// took 12.8 / 15.4 / 13.7 us with 2 / 3 / 4 slots.
+template <uint32_t T>
+constexpr int64_t staged_min_bytes() { return T == T_Q6_K ? 32ll << 20 : T == T_Q4_K ? 96ll << 20 : INT64_MAX; }
 
 template <uint32_t T, int MR, int P>
 static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
@@ -1133,10 +1139,14 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
     const int64_t simds = (int64_t)cu_count() * 4;
     const GemvTuning& tu = gemv_tuning();
     const size_t shmem = act_lds_bytes<T>(MR, k);
-    if constexpr (T == T_Q6_K && MR == 1) {
+    if constexpr ((T == T_Q6_K || T == T_Q4_K) && MR == 1) {
+        // (Q4_K's LDS field reads are whole 16-byte pieces: its rows must start 16-byte aligned)
         const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
-        if (bytes >= kStagedMinBytes && act_lds_bytes<T>(1, k) <= 64 * 1024)
-            return launch_st<T>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
+        bool aligned = true;
+        if constexpr (T == T_Q4_K)
+            for (int i = 0; i < 3; ++i) aligned = aligned && ((uintptr_t)sg.w[i] & 15u) == 0;
+        if (bytes >= staged_min_bytes<T>() && aligned && act_lds_bytes<T>(1, k) <= 64 * 1024)
+            return launch_st<T, 1, 16>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
     }
     if (MR > 2 && items > simds * 32) {
         const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2>(shmem));

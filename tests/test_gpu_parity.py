@@ -115,18 +115,17 @@ def test_q6_k_output_head_full_size(gpu, orc):
     check_close(y1[:, others], yo, exact, abs_sum, "c2-oracle")
 
 
-@pytest.mark.parametrize("k", [4096, 14336])
-def test_q6_k_staged_stream_equals_register_ring(gpu, orc, k):
-    """Q6_K decode streams of at least 32 MB take the LDS-staged kernel and shorter ones the
-    register-ring kernel; both compute the same per-unit terms in the same order, so rows of a
-    40 MB matrix (ragged row count; k = 14336 ends every row with a half item) must equal bit
-    for bit the same rows run as a small matrix -- with a bias, with the residual add, and in
-    the three-matrix launch -- and match the oracle."""
+@pytest.mark.parametrize("qt,k,mb", [(S.Q6_K, 4096, 40), (S.Q6_K, 14336, 40), (S.Q4_K, 4096, 100)])
+def test_staged_stream_equals_register_ring(gpu, orc, qt, k, mb):
+    """Long decode streams (Q6_K from 32 MB, Q4_K from 96 MB) take the LDS-staged kernel and
+    shorter ones the register-ring kernel; both compute the same per-unit terms in the same
+    order, so rows of a long matrix (ragged row count; k = 14336 ends every Q6_K row with a half
+    item) must equal bit for bit the same rows run as a small matrix -- with a bias, with the
+    residual add, and in the three-matrix launch -- and match the oracle."""
     import torch
-    qt = S.Q6_K
     rb = S.row_bytes(qt, k)
-    n = (40 << 20) // rb + 3
-    print("staged Q6_K", n, k, flush=True)
+    n = (mb << 20) // rb + 3
+    print("staged", S.TYPE_NAMES[qt], n, k, flush=True)
     w = S.make_weight(qt, n, k, 9100 + k)
     x = S.make_activation(1, k, 9200 + k, outliers=True)
     bias = np.random.default_rng(k).standard_normal(n).astype(np.float32)
