@@ -359,6 +359,9 @@ def main():
     ap.add_argument("--float-dot-only", action="store_true",
                     help="run only the float-dot types' decode GEMVs and print them as one "
                          "JSON line")
+    ap.add_argument("--head-only", action="store_true",
+                    help="run only the Q6_K 128256x4096 output-head GEMV and print it as one JSON "
+                         "line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 10 device copies of 64 MiB (a kernel of known traffic, for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -400,6 +403,14 @@ def main():
     if args.float_dot_only:
         print(json.dumps({"f3_float_dot_types": float_dot_points(C, S, max(20, args.steps // 4),
                                                                  max(3, args.warmup // 4))}))
+        return
+
+    if args.head_only:
+        c2 = decode_point(C, S, "c2_q6_k_head", "output", 1, max(20, args.steps // 4),
+                          max(3, args.warmup // 4), cold=True)
+        print(json.dumps({"c2_q6_k_head": {"gemv_gbs": round(c2["gbs_gemv"], 1),
+                                           "gemv_frac_hbm": round(c2["gbs_gemv"] / HBM_PEAK_GBS, 4),
+                                           "gemv_us": round(c2["ms_gemv"] * 1e3, 2)}}))
         return
 
     if args.prefill_only:
