@@ -1095,10 +1095,14 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
         // From sweeps on MI355X at m = 512 (us for n = 14336 / 4096 / 1024): 256 x 128 tiles
         // when they fill the CUs (163), else 256 x 64 tiles split to one workgroup per CU
         // (4096: 63 against 70 for 128 x 32), else 128 x 32 tiles split to two per CU (1024: 30).
+        // The 8-wave workgroups hold one CU's LDS each, so their split target is one per CU:
+        // with the split-K sums completed in the GEMM, 14336 x 4096 runs its 224 tiles unsplit
+        // in 123 us against 134 us split in two (448 workgroups, a second round on 192 CUs).
         const int t84 = ((n + 255) / 256) * ((m + 127) / 128);
         const int t82 = ((n + 255) / 256) * ((m + 63) / 64);
         if (t84 >= cus * 3 / 4) {
             p.wv = 8, p.nt = 1, p.mt = 4;
+            target = cus;
         } else if (t82 >= cus / 4) {
             p.wv = 8, p.nt = 1, p.mt = 2;
             target = cus;
