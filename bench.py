@@ -149,9 +149,9 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
     RMSNorm+Q8_0 -> one GEMV launch for q/k/v; the wo GEMV quantizing the attention output
     (a fixed synthetic vector: attention itself is measured with the whole model) and adding
     the residual;
-    RMSNorm+Q8_0 -> one launch for gate/up -> SwiGLU+Q8_0 -> down GEMV + residual add
-    (engine.cpp:475-513). Seven launches per layer (the residual adds ride in the wo and
-    down GEMVs). `copies` distinct
+    RMSNorm+Q8_0 -> one launch for gate, up and silu(gate) * up -> the down GEMV quantizing h
+    and adding the residual (engine.cpp:475-513). Six launches per layer (the residual adds
+    ride in the wo and down GEMVs, the SwiGLU in the gate/up GEMV). `copies` distinct
     copies of the layer's weights rotate so that each step streams its weights from HBM, as
     the 32 different layers of a model would."""
     import torch
@@ -176,6 +176,7 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
     outs = {l: torch.empty((1, n), dtype=torch.float32, device="cuda")
             for l, (_, n, _) in mats.items()}
 
+    hbuf = torch.empty((1, n_ff), dtype=torch.float32, device="cuda")
     qkv, gu = ("wq", "wk", "wv"), ("gate", "up")
     assert len({mats[l][0] for l in qkv}) == 1 and len({mats[l][0] for l in gu}) == 1
 
@@ -188,16 +189,14 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
         qt, n, k = mats["wo"]
         C.matmul_quant_residual_dev(attn, L["wo"], qt, None, k, n, x)
         _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn2, 1e-5, h=False)
-        qt, _, k = mats["gate"]
-        C.gemv_q8_multi_dev([L[l] for l in gu], qt, k, [mats[l][1] for l in gu], qs, sc, bs,
-                            ys=[outs[l] for l in gu])
-        _, qs, sc, bs = C.swiglu_q8_0_dev(outs["gate"], outs["up"], h=False)
+        qt, n_g, k = mats["gate"]
+        C.gemv_q8_swiglu_dev(L["gate"], L["up"], qt, k, n_g, qs, sc, bs, h=hbuf)
         qt, n, k = mats["down"]
-        C.gemv_q8_residual_dev(L["down"], qt, k, n, qs, sc, bs, x)
+        C.matmul_quant_residual_dev(hbuf, L["down"], qt, None, k, n, x)
 
     ms = time_loop(step, steps, warmup)
     x.copy_(x0)
-    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 7,
+    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 6,
            "gbs": round(wbytes / ms / 1e6, 1),
            "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
            "projected_tokens_per_s_32_layers_linear_only": round(1e3 / (32 * ms), 1),

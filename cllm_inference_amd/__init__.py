@@ -67,6 +67,7 @@ SIGNATURES = {
     "cllm_hip_add_dev": (_I, [_P, _P, _I64, _P]),
     "cllm_hip_gemv_q8_residual_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_multi_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
+    "cllm_hip_gemv_q8_swiglu_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_gguf_open": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_P)]),
     "cllm_hip_gguf_close": (_I, [_P]),
     "cllm_hip_gguf_tensor_count": (_I, [_P]),
@@ -255,6 +256,20 @@ def gemv_q8_multi_dev(ws, t: int, in_dim: int, out_dims, qs, scales, bsums, ys=N
         int(t), int(in_dim), n_mats, wa, na, ba, ya, int(m), _tp(qs), _tp(scales), _tp(bsums),
         _stream()))
     return ys
+
+
+def gemv_q8_swiglu_dev(w_gate, w_up, t: int, in_dim: int, n_ff: int, qs, scales, bsums,
+                       h=None, bias_gate=None, bias_up=None):
+    """h = silu(gate . a) * (up . a) for the n_ff rows of the gate and up matrices against the
+    quantized rows, in one launch (engine.cpp:509-512). Returns h [n_rows, n_ff]."""
+    import torch
+    m = qs.shape[0]
+    if h is None:
+        h = torch.empty((m, int(n_ff)), dtype=torch.float32, device=qs.device)
+    _check(load_library().cllm_hip_gemv_q8_swiglu_dev(
+        int(t), int(in_dim), int(n_ff), _tp(w_gate), _tp(w_up), _tp(bias_gate), _tp(bias_up),
+        int(m), _tp(qs), _tp(scales), _tp(bsums), _tp(h), _stream()))
+    return h
 
 
 def gemv_q8_residual_dev(w, t: int, in_dim: int, out_dim: int, qs, scales, bsums, y, bias=None):

@@ -560,6 +560,27 @@ int cllm_hip_gemv_q8_multi_dev(uint32_t type, int in_dim, int n_mats, const void
     return CLLM_HIP_OK;
 }
 
+int cllm_hip_gemv_q8_swiglu_dev(uint32_t type, int in_dim, int n_ff, const void* w_gate,
+                                const void* w_up, const float* bias_gate, const float* bias_up,
+                                int n_rows, const int8_t* qs, const float* scales,
+                                const int32_t* bsums, float* h, void* stream) {
+    int rc = check_matmul("matmul_quant", type, in_dim, n_ff);
+    if (rc) return rc;
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if (n_rows <= 0 || n_ff == 0) return CLLM_HIP_OK;
+    if (!w_gate || !w_up || !h || !qs || !scales || !bsums)
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(w_gate) || !aligned16(w_up) || !aligned16(qs) || ((uintptr_t)scales & 7u) ||
+        ((uintptr_t)bsums & 7u) || ((uintptr_t)h & 3u) || ((uintptr_t)bias_gate & 3u) ||
+        ((uintptr_t)bias_up & 3u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    HIP_TRY(launch_gemv_swiglu(type, in_dim, n_ff, (const uint8_t*)w_gate, (const uint8_t*)w_up,
+                               bias_gate, bias_up, h, n_rows, qs, scales, bsums, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
 int cllm_hip_gemv_q8_residual_dev(const void* w, uint32_t type, int in_dim, int out_dim,
                                   int n_rows, const int8_t* qs, const float* scales,
                                   const int32_t* bsums, const float* bias, float* y,

@@ -143,6 +143,12 @@ constexpr int DPP_ROW_HALF_MIRROR = 0x141;
 constexpr int DPP_ROW_MIRROR = 0x140;
 
 // Sum over all 64 lanes; the result is valid in every lane.
+// silu(g) * u, silu(v) = v / (1 + exp(-v)) (the reference engine's SwiGLU, engine.cpp:38),
+// with IEEE division and product and the device expf.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, 1.0f + expf(-g)), u);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f32<DPP_QUAD_SWAP1>(v);
     v += dpp_f32<DPP_QUAD_SWAP2>(v);

@@ -696,7 +696,11 @@ __device__ __forceinline__ V seg_pick(int s, V a, V b, V c) {
 template <int MR>
 constexpr int gemv_threads() { return MR <= 2 ? 512 : 256; }
 
-template <uint32_t T, int MR, int P>
+// With SW (the gate and up projections of a SwiGLU feed-forward, engine.cpp:509-512): segment 0
+// is the gate matrix, segment 1 the up matrix, both of n rows; a wave takes row p of both in
+// turn (row p of gate, then row p of up) and writes h[p] = silu(gate_p) * up_p to y[0] instead
+// of the two projections, so the SwiGLU needs no launch of its own.
+template <uint32_t T, int MR, int P, bool SW = false>
 __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_t row_bytes,
                                               int k, int n, const int8_t* __restrict__ qs,
                                               const float* __restrict__ xs,
@@ -711,20 +715,26 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_
     const int wid = blockIdx.x * kWaves + wave;
     const int units = k / Tr::UNIT;
     const int iters = (units + 63) / 64;
-    const int my_rows = wid < n ? (n - 1 - wid) / n_waves + 1 : 0;
+    const int my_rows = (wid < n ? (n - 1 - wid) / n_waves + 1 : 0) * (SW ? 2 : 1);
     const int n_items = my_rows * iters;
 
-    // Item i of this wave is row wid + (i / iters) * n_waves, unit slice i % iters. Refills are
+    // Item i of this wave is row wid + (i / iters) * n_waves, unit slice i % iters (with SW,
+    // row slot t = i / iters is row wid + (t / 2) n_waves of gate (t even) or up). Refills are
     // issued for every slot, with the item, row and unit clamped to valid memory (a wave with
     // no rows reads row n - 1), so the number of loads in flight is the same on every path
     // and the compiler's vmcnt waits only ever wait for the oldest slot.
     auto slot_addr = [&](int item, const uint8_t*& row, int& u) {
         const int c = max(0, min(item, n_items - 1));
         const int t = c / iters, it = c - t * iters;
-        const int jr = min(wid + t * n_waves, n - 1);
-        const int s = seg_of(sg, jr);
-        row = seg_pick(s, sg.w[0], sg.w[1], sg.w[2]) +
-              (int64_t)(jr - seg_pick(s, sg.start[0], sg.start[1], sg.start[2])) * row_bytes;
+        if constexpr (SW) {
+            const int p = min(wid + (t >> 1) * n_waves, n - 1);
+            row = ((t & 1) ? sg.w[1] : sg.w[0]) + (int64_t)p * row_bytes;
+        } else {
+            const int jr = min(wid + t * n_waves, n - 1);
+            const int s = seg_of(sg, jr);
+            row = seg_pick(s, sg.w[0], sg.w[1], sg.w[2]) +
+                  (int64_t)(jr - seg_pick(s, sg.start[0], sg.start[1], sg.start[2])) * row_bytes;
+        }
         u = min(lane + 64 * it, units - 1);
     };
 
@@ -760,9 +770,9 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_
     lds_barrier();
     if (n_items == 0) return;
 
-    float acc[MR];
+    float acc[MR], gate_v[MR];
 #pragma unroll
-    for (int r = 0; r < MR; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < MR; ++r) acc[r] = gate_v[r] = 0.0f;
 
     const int n_pad = ((n_items + P - 1) / P) * P;
     for (int base = 0; base < n_pad; base += P) {
@@ -791,7 +801,23 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_
                 slot_addr(item + P, row, u2);
                 ring[p] = Tr::load(row, u2);
             }
-            if (item < n_items && it == iters - 1) {
+            if (SW && item < n_items && it == iters - 1) {
+                const int j = __builtin_amdgcn_readfirstlane(wid + (t >> 1) * n_waves);
+                const bool up = t & 1;
+                const float* bias = up ? sg.bias[1] : sg.bias[0];
+                const float bj = bias ? bias[j] : 0.0f;
+#pragma unroll
+                for (int r = 0; r < MR; ++r) {
+                    float v = wave_sum(acc[r]);
+                    if (bias) v += bj;
+                    if (!up) {
+                        gate_v[r] = v;
+                    } else if (lane == r) {
+                        sg.y[0][(size_t)r * sg.rows[0] + j] = silu_mul(gate_v[r], v);
+                    }
+                    acc[r] = 0.0f;
+                }
+            } else if (item < n_items && it == iters - 1) {
                 const int jv = __builtin_amdgcn_readfirstlane(wid + t * n_waves);
                 const int s = seg_of(sg, jv);
                 const int j = jv - seg_pick(s, sg.start[0], sg.start[1], sg.start[2]);
@@ -1044,7 +1070,7 @@ static const GemvTuning& gemv_tuning() {
 
 // Waves of k_gemv<T, MR, P> resident on the whole device with `shmem` bytes of LDS per
 // workgroup (cached per instantiation for the last LDS size asked).
-template <uint32_t T, int MR, int P>
+template <uint32_t T, int MR, int P, bool SW = false>
 static int64_t resident_waves(size_t shmem) {
     static std::atomic<uint64_t> cache{0};  // (shmem << 16) | workgroups per CU, 0 = empty
     uint64_t c = cache.load(std::memory_order_relaxed);
@@ -1053,7 +1079,7 @@ static int64_t resident_waves(size_t shmem) {
         blocks = (int)(c & 0xFFFFu);
     } else {
         blocks = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv<T, MR, P>),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv<T, MR, P, SW>),
                                                          gemv_threads<MR>(), shmem) != hipSuccess ||
             blocks < 1)
             blocks = 1;
@@ -1106,7 +1132,7 @@ static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, 
 template <uint32_t T>
 constexpr int64_t staged_min_bytes() { return T == T_Q6_K ? 32ll << 20 : T == T_Q4_K ? 96ll << 20 : INT64_MAX; }
 
-template <uint32_t T, int MR, int P>
+template <uint32_t T, int MR, int P, bool SW>
 static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
                            const int32_t* xb, const float* x_f32, int accumulate, int waves,
                            hipStream_t stream) {
@@ -1115,7 +1141,7 @@ static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, c
     constexpr int kWaves = gemv_threads<MR>() / 64;
     const int grid = (waves + kWaves - 1) / kWaves;
     const size_t shmem = act_lds_bytes<T>(MR, k);
-    hipLaunchKernelGGL((k_gemv<T, MR, P>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, sg,
+    hipLaunchKernelGGL((k_gemv<T, MR, P, SW>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, sg,
                        row_bytes, k, n, qs, xs, xb, x_f32, accumulate);
     return hipGetLastError();
 }
@@ -1129,17 +1155,18 @@ static int max_rows_per_launch(int k) {
     return mr;
 }
 
-template <uint32_t T, int MR>
+// SW: n is the row count of each of the two matrices (gate and up), whose rows pair up.
+template <uint32_t T, int MR, bool SW>
 static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
                             const int32_t* xb, const float* x_f32, int accumulate,
                             hipStream_t stream) {
     using Tr = typename TraitsOf<T>::type;
     const int iters = (k / Tr::UNIT + 63) / 64;
-    const int64_t items = (int64_t)n * iters;
+    const int64_t items = (int64_t)n * iters * (SW ? 2 : 1);
     const int64_t simds = (int64_t)cu_count() * 4;
     const GemvTuning& tu = gemv_tuning();
     const size_t shmem = act_lds_bytes<T>(MR, k);
-    if constexpr ((T == T_Q6_K || T == T_Q4_K) && MR == 1) {
+    if constexpr ((T == T_Q6_K || T == T_Q4_K) && MR == 1 && !SW) {
         // (Q4_K's LDS field reads are whole 16-byte pieces: its rows must start 16-byte aligned)
         const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
         bool aligned = true;
@@ -1149,28 +1176,28 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
             return launch_st<T, 1, 16>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
     }
     if (MR > 2 && items > simds * 32) {
-        const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2>(shmem));
-        return launch_t<T, MR, 2>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);
+        const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2, SW>(shmem));
+        return launch_t<T, MR, 2, SW>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);
     }
-    const int64_t waves = std::min({items, simds * tu.short_wps, resident_waves<T, MR, 1>(shmem)});
-    return launch_t<T, MR, 1>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);
+    const int64_t waves = std::min({items, simds * tu.short_wps, resident_waves<T, MR, 1, SW>(shmem)});
+    return launch_t<T, MR, 1, SW>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);
 }
 
-template <uint32_t T>
+template <uint32_t T, bool SW>
 static hipError_t launch_rows(const GemvSegs& sg, int k, int n, int mr, const int8_t* qs,
                               const float* xs, const int32_t* xb, const float* x_f32, int acc,
                               hipStream_t stream) {
     switch (mr) {
-        case 1: return launch_mr<T, 1>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
-        case 2: return launch_mr<T, 2>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
-        case 4: return launch_mr<T, 4>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
-        default: return launch_mr<T, 8>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 1: return launch_mr<T, 1, SW>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 2: return launch_mr<T, 2, SW>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 4: return launch_mr<T, 4, SW>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        default: return launch_mr<T, 8, SW>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
     }
 }
 
 // Runs every activation row through the GEMV, MR rows per launch. With x_f32 set, the rows
 // are fp32 and each launch quantizes its rows itself (qs / scales / bsums unused).
-template <uint32_t T>
+template <uint32_t T, bool SW = false>
 static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const int8_t* qs,
                                 const float* scales, const int32_t* bsums, const float* x_f32,
                                 int acc, hipStream_t stream) {
@@ -1183,7 +1210,7 @@ static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const 
         while (mr > cap) mr /= 2;
         GemvSegs sg = sg0;
         for (int i = 0; i < 3; ++i) sg.y[i] = sg0.y[i] + (size_t)t * sg0.rows[i];
-        const hipError_t e = launch_rows<T>(
+        const hipError_t e = launch_rows<T, SW>(
             sg, k, n, mr, qs ? qs + (size_t)t * k : nullptr, scales ? scales + (size_t)t * nb : nullptr,
             bsums ? bsums + (size_t)t * nb : nullptr, x_f32 ? x_f32 + (size_t)t * k : nullptr, acc,
             stream);
@@ -1244,6 +1271,25 @@ hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* co
     }
     if (total == 0) return hipSuccess;
     return gemv_dispatch(type, sg, k, total, m, qs, scales, bsums, nullptr, 0, stream);
+}
+
+hipError_t launch_gemv_swiglu(uint32_t type, int k, int n, const uint8_t* w_gate,
+                              const uint8_t* w_up, const float* bias_gate, const float* bias_up,
+                              float* h, int m, const int8_t* qs, const float* scales,
+                              const int32_t* bsums, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    GemvSegs sg = one_segment(w_gate, n, bias_gate, h);
+    sg.w[1] = w_up;
+    sg.bias[1] = bias_up;
+    switch (type) {
+        case T_Q4_K: return gemv_all_rows<T_Q4_K, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
+        case T_Q5_K: return gemv_all_rows<T_Q5_K, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
+        case T_Q6_K: return gemv_all_rows<T_Q6_K, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
+        case T_Q8_0: return gemv_all_rows<T_Q8_0, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
+        case T_Q4_0: return gemv_all_rows<T_Q4_0, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
+        case T_Q5_0: return gemv_all_rows<T_Q5_0, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,

@@ -173,9 +173,6 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_q8_0(const float* __restric
     const int64_t at = blk * 32 + part * 4;
     const f32x4 g = *(const f32x4*)(gate + at);
     const f32x4 u = *(const f32x4*)(up + at);
-    auto silu_mul = [](float gv, float uv) {
-        return __fmul_rn(__fdiv_rn(gv, 1.0f + expf(-gv)), uv);
-    };
     f32x4 hv;
     hv.x = silu_mul(g.x, u.x);
     hv.y = silu_mul(g.y, u.y);
@@ -190,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_f32(const float* __restrict
                                                          const float* __restrict__ up,
                                                          int64_t total, float* __restrict__ h) {
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i < total) h[i] = __fmul_rn(__fdiv_rn(gate[i], 1.0f + expf(-gate[i])), up[i]);
+    if (i < total) h[i] = silu_mul(gate[i], up[i]);
 }
 
 // x += d (the residual adds), four elements per thread where aligned

@@ -51,6 +51,12 @@ hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* co
 // Same as launch_gemv with fp32 activation rows x[m][k]: each launch quantizes its rows to
 // Q8_0 in LDS (bit-identical to launch_quantize_q8_0) instead of reading a quantized batch,
 // so a decode step is a single kernel.
+// SwiGLU feed-forward input: h[t, j] = silu(gate_j . a_t + bg_j) * (up_j . a_t + bu_j) for the
+// n rows of the gate and up matrices (biases may be null), one launch, on Q8_0 activation rows.
+hipError_t launch_gemv_swiglu(uint32_t type, int k, int n, const uint8_t* w_gate,
+                              const uint8_t* w_up, const float* bias_gate, const float* bias_up,
+                              float* h, int m, const int8_t* qs, const float* scales,
+                              const int32_t* bsums, hipStream_t stream);
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
                              const float* x, const float* bias, float* y, hipStream_t stream,
                              bool accumulate = false);

@@ -114,6 +114,17 @@ int cllm_hip_gemv_q8_multi_dev(uint32_t type, int in_dim, int n_mats, const void
                                int n_rows, const int8_t* qs, const float* scales,
                                const int32_t* bsums, void* stream);
 
+/* The gate and up projections of a SwiGLU feed-forward and the product after them in one
+ * launch (src/core/engine.cpp:509-512, 38-39): h[t, j] = silu(g) * u with
+ * g = vec_dot_row(w_gate row j, qx row t) (+ bias_gate[j]), u likewise for w_up, silu(v) =
+ * v / (1 + exp(-v)); both matrices have n_ff rows of in_dim, h is [n_rows][n_ff]. The same
+ * values as cllm_hip_gemv_q8_multi_dev on the two matrices followed by cllm_hip_swiglu_q8_0_dev,
+ * bit for bit. Biases may be null. */
+int cllm_hip_gemv_q8_swiglu_dev(uint32_t type, int in_dim, int n_ff, const void* w_gate,
+                                const void* w_up, const float* bias_gate, const float* bias_up,
+                                int n_rows, const int8_t* qs, const float* scales,
+                                const int32_t* bsums, float* h, void* stream);
+
 /* cllm_hip_gemv_q8_dev fused with the residual add that follows the matmul in the engine
  * (x += mm(...), src/core/engine.cpp:505-506, 512-513): y[t, j] += vec_dot_row(...)
  * (+ bias[j]), so y holds the residual stream on entry. Always the GEMV kernels (meant for

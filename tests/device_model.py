@@ -185,9 +185,19 @@ class DeviceModel:
             C.matmul_quant_residual_dev(attn, self.w[wo], self._type(wo), None, self.q_dim,
                                         self.n_embd, x)
             h, qs, sc, bs = C.rmsnorm_q8_0_dev(x, self.w[p + "ffn_norm.weight"], self.eps)
-            self._linear([p + "ffn_gate.weight", p + "ffn_up.weight"], [gate, up], h, (qs, sc, bs))
-            hs, qs, sc, bs = C.swiglu_q8_0_dev(gate, up)
-            self._linear([p + "ffn_down.weight"], [x], hs, (qs, sc, bs), residual=True)
+            wg, wu, wd = p + "ffn_gate.weight", p + "ffn_up.weight", p + "ffn_down.weight"
+            tg = self._type(wg)
+            if T < 16 and tg == self._type(wu) and C.has_vec_dot(tg) and C.has_vec_dot(self._type(wd)):
+                # gate, up and the SwiGLU in one launch; the down GEMV quantizes h itself and
+                # adds the residual
+                C.gemv_q8_swiglu_dev(self.w[wg], self.w[wu], tg, self.n_embd, self.n_ff, qs, sc, bs,
+                                     h=gate)
+                C.matmul_quant_residual_dev(gate, self.w[wd], self._type(wd), None, self.n_ff,
+                                            self.n_embd, x)
+            else:
+                self._linear([wg, wu], [gate, up], h, (qs, sc, bs))
+                hs, qs, sc, bs = C.swiglu_q8_0_dev(gate, up)
+                self._linear([wd], [x], hs, (qs, sc, bs), residual=True)
         if not logits:
             return None
         h, qs, sc, bs = C.rmsnorm_q8_0_dev(x[T - 1:T].contiguous(), self.w["output_norm.weight"], self.eps)

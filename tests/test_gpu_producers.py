@@ -159,6 +159,28 @@ def test_gemv_multi_equals_separate_launches(gpu, qt):
             assert np.array_equal(bits(ys[i].cpu().numpy()), bits(one.cpu().numpy())), (n_mats, i)
 
 
+@pytest.mark.parametrize("qt,m,n_ff", [(S.Q4_K, 1, 14336), (S.Q4_K, 2, 1000), (S.Q6_K, 1, 4096),
+                                       (S.Q8_0, 5, 2048), (S.Q5_K, 8, 777)])
+def test_gemv_swiglu_equals_projections_then_swiglu(gpu, qt, m, n_ff):
+    """gate, up and silu(gate) * up in one launch give the bits of the two projections in one
+    launch followed by the SwiGLU producer (ragged row counts and several activation rows
+    included), with and without biases."""
+    k = 4096
+    rng = np.random.default_rng(qt + 400 + m)
+    wg = _dev(S.make_weight(qt, n_ff, k, 40))
+    wu = _dev(S.make_weight(qt, n_ff, k, 41))
+    qs, sc, bs = gpu.quantize_q8_0_dev(_dev(S.make_activation(m, k, 42)))
+    for with_bias in (False, True):
+        bg = _dev(rng.standard_normal(n_ff).astype(np.float32)) if with_bias else None
+        bu = _dev(rng.standard_normal(n_ff).astype(np.float32)) if with_bias else None
+        print("swiglu gemv", S.TYPE_NAMES[qt], m, n_ff, with_bias, flush=True)
+        g, u = gpu.gemv_q8_multi_dev([wg, wu], qt, k, [n_ff, n_ff], qs, sc, bs,
+                                     biases=[bg, bu] if with_bias else None)
+        h_ref = gpu.swiglu_q8_0_dev(g, u, quantize=False)[0]
+        h = gpu.gemv_q8_swiglu_dev(wg, wu, qt, k, n_ff, qs, sc, bs, bias_gate=bg, bias_up=bu)
+        assert np.array_equal(bits(h.cpu().numpy()), bits(h_ref.cpu().numpy())), with_bias
+
+
 @pytest.mark.parametrize("qt,m", [(S.Q4_K, 1), (S.Q6_K, 2), (S.Q8_0, 5), (S.Q4_K, 20), (S.F16, 1),
                                   (S.Q3_K, 3)])
 def test_matmul_residual_equals_matmul_then_add(gpu, qt, m):
