@@ -158,29 +158,29 @@ __global__ __launch_bounds__(kThreads) void k_attention(
             }
         }
         __syncthreads();
-        // running max per head; the factor that rescales what is already summed
-        if (threadIdx.x < n_rep) {
-            const int r = threadIdx.x;
-            float cm = -INFINITY;
-            for (int i = 0; i < kChunk; ++i) cm = fmaxf(cm, sc[r][i]);
+        // one wave per query head (lane i = position i of the chunk): the running max, the
+        // probabilities relative to it in place of the scores, their sum, and the factor that
+        // rescales what is already summed
+        static_assert(kChunk == 64, "a chunk is one wave's lanes");
+        for (int r = wave; r < n_rep; r += kThreads / 64) {
+            const float s = sc[r][lane];
+            float cm = s;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 64));
             const float mo = m_run[r], mn = fmaxf(mo, cm);
-            corr[r] = mo == -INFINITY ? 0.0f : expf(mo - mn);
-            m_run[r] = mn;
+            const float pr = s == -INFINITY ? 0.0f : expf(s - mn);
+            float ps = pr;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ps += __shfl_xor(ps, o, 64);
+            sc[r][lane] = pr;
+            if (lane == 0) {
+                const float cr = mo == -INFINITY ? 0.0f : expf(mo - mn);
+                corr[r] = cr;
+                m_run[r] = mn;
+                l_run[r] = __builtin_fmaf(l_run[r], cr, ps);
+            }
         }
         __syncthreads();
-        // probabilities (relative to the running max) in place of the scores
-        for (int i = threadIdx.x; i < n_rep * kChunk; i += kThreads) {
-            const int r = i / kChunk, j = i - r * kChunk;
-            const float s = sc[r][j];
-            sc[r][j] = s == -INFINITY ? 0.0f : expf(s - m_run[r]);
-        }
-        __syncthreads();
-        if (threadIdx.x < n_rep) {
-            const int r = threadIdx.x;
-            float l = l_run[r] * corr[r];
-            for (int i = 0; i < kChunk; ++i) l += sc[r][i];
-            l_run[r] = l;
-        }
 #pragma unroll
         for (int r = 0; r < kMaxRep; ++r) {
             if (r >= n_rep) break;
