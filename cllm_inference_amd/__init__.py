@@ -82,6 +82,7 @@ SIGNATURES = {
     "cllm_hip_matmul_quant_residual_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
     "cllm_hip_dequantize_rows_dev": (_I, [_P, _U, _I, _P, _I, _P, _P]),
     "cllm_hip_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
+    "cllm_hip_attention_rope_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, ctypes.c_float, _P, _P]),
 }
 
 
@@ -446,6 +447,20 @@ def attention_dev(q, k_cache, v_cache, pos0: int, n_head: int, n_head_kv: int, h
     _check(load_library().cllm_hip_attention_dev(_tp(q), _tp(k_cache), _tp(v_cache), int(n_rows),
                                                  int(pos0), int(n_head), int(n_head_kv),
                                                  int(head_dim), _tp(out), _stream()))
+    return out
+
+
+def attention_rope_dev(q, k_cache, v_cache, pos0: int, n_head: int, n_head_kv: int,
+                       head_dim: int, theta_base: float, out=None):
+    """A decode step's RoPE and attention in one launch (engine.cpp:486-495): q (one row,
+    unrotated, left as it is) and the unrotated key row pos0 of k_cache (rotated in place) get
+    the NEOX rotation at position pos0, then the attention over positions [0, pos0]."""
+    import torch
+    if out is None:
+        out = torch.empty((1, n_head * head_dim), dtype=torch.float32, device=q.device)
+    _check(load_library().cllm_hip_attention_rope_dev(
+        _tp(q), _tp(k_cache), _tp(v_cache), int(pos0), int(n_head), int(n_head_kv),
+        int(head_dim), float(theta_base), _tp(out), _stream()))
     return out
 
 

@@ -756,9 +756,9 @@ int cllm_hip_rope_neox2_dev(float* q, int n_head, float* k, int n_head_kv, int n
     return CLLM_HIP_OK;
 }
 
-int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_cache,
-                           int n_rows, int pos0, int n_head, int n_head_kv, int head_dim,
-                           float* out, void* stream) {
+static int attention_impl(const float* q, const float* k_cache, const float* v_cache,
+                          int n_rows, int pos0, int n_head, int n_head_kv, int head_dim,
+                          float* out, void* stream, float rope_base) {
     if (n_rows < 0 || pos0 < 0) return set_err(CLLM_HIP_E_ARG, "attention: bad shape");
     if (!attention_supported(head_dim, n_head, n_head_kv))
         return set_err(CLLM_HIP_E_ARG,
@@ -783,8 +783,23 @@ int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_
         if (ws->att.p != before) HIP_TRY(gemmw_workspace_init(ws->att.p, ws->att.cap, s));
     }
     HIP_TRY(launch_attention(q, k_cache, v_cache, n_rows, pos0, n_head, n_head_kv, head_dim, out,
-                             ws->att.p, ws->att.cap, s));
+                             ws->att.p, ws->att.cap, s, rope_base));
     return CLLM_HIP_OK;
+}
+
+int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_cache,
+                           int n_rows, int pos0, int n_head, int n_head_kv, int head_dim,
+                           float* out, void* stream) {
+    return attention_impl(q, k_cache, v_cache, n_rows, pos0, n_head, n_head_kv, head_dim, out,
+                          stream, 0.0f);
+}
+
+int cllm_hip_attention_rope_dev(const float* q, float* k_cache, const float* v_cache, int pos0,
+                                int n_head, int n_head_kv, int head_dim, float theta_base,
+                                float* out, void* stream) {
+    if (!(theta_base > 0.0f)) return set_err(CLLM_HIP_E_ARG, "attention: theta_base must be positive");
+    return attention_impl(q, k_cache, v_cache, 1, pos0, n_head, n_head_kv, head_dim, out, stream,
+                          theta_base);
 }
 
 // ---- GGUF files (gguf.cpp:122-275 of the reference) ---------------------------------------

@@ -71,11 +71,16 @@ constexpr int kMaxSplits = 256;      // sequence splits per (row, KV head)
 // HD = head_dim (multiple of 64, at most 256). Partials of split z for query head hq of row
 // t: part[((t * n_head + hq) * S + z) * (HD + 2) + ...] = unnormalised output [HD], max, sum.
 // With one split, the normalised output goes straight to out.
+//
+// rope_base > 0 (one query row, a decode step): the queries and the key row at pos0 arrive
+// unrotated and the kernel applies the NEOX rotation of k_rope_neox itself, to the queries in
+// registers and to the key row as it loads it, writing the rotated key row back to k_new (the
+// cache row pos0, read by no other workgroup: only the split holding pos0 covers it).
 template <int HD>
 __global__ __launch_bounds__(kThreads) void k_attention(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
     int n_head, int n_kv, int pos0, int split_len, float scale, float* __restrict__ part,
-    int* __restrict__ counters, float* __restrict__ out) {
+    int* __restrict__ counters, float* __restrict__ out, float rope_base, float* k_new) {
     constexpr int PER = HD / kLanesPerPos;  // K elements per lane (4 .. 16)
     __shared__ float sc[kMaxRep][kChunk];
     __shared__ float m_run[kMaxRep], l_run[kMaxRep], corr[kMaxRep];
@@ -100,6 +105,28 @@ __global__ __launch_bounds__(kThreads) void k_attention(
             qv[r][e] = v.x; qv[r][e + 1] = v.y; qv[r][e + 2] = v.z; qv[r][e + 3] = v.w;
         }
     }
+    // NEOX rotation at position pos0: dims seg * PER + e pair with the partner lane seg ^ 8
+    // (the other half of the head); lanes seg < 8 hold x0 (dims i < HD / 2), the others x1.
+    const bool rope = rope_base > 0.0f;
+    const bool lo_half = seg < 8;
+    float rc[PER], rs[PER];
+    auto rotate = [&](float (&x)[PER]) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const float other = __shfl_xor(x[e], 8, 16);
+            const float x0 = lo_half ? x[e] : other, x1 = lo_half ? other : x[e];
+            x[e] = lo_half ? __builtin_fmaf(x0, rc[e], -__fmul_rn(x1, rs[e]))
+                           : __builtin_fmaf(x0, rs[e], __fmul_rn(x1, rc[e]));
+        }
+    };
+    // the angles of the HD / 2 pairs, one per thread, shared through LDS
+    __shared__ float rope_cs[2][HD / 2];
+    if (rope && threadIdx.x < HD / 2) {
+        const int i = threadIdx.x;
+        const float theta = __fdiv_rn((float)pos0, powf(rope_base, __fdiv_rn((float)i, (float)(HD / 2))));
+        rope_cs[0][i] = cosf(theta);
+        rope_cs[1][i] = sinf(theta);
+    }
     // Each wave accumulates the output of its own 16 positions of every chunk: lane l owns
     // dims l + 64 e (e < HD / 64) of every query head of the group; the four waves' partials
     // are added at the end.
@@ -114,6 +141,15 @@ __global__ __launch_bounds__(kThreads) void k_attention(
         l_run[threadIdx.x] = 0.0f;
     }
     __syncthreads();
+    if (rope) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            rc[e] = rope_cs[0][(seg & 7) * PER + e];
+            rs[e] = rope_cs[1][(seg & 7) * PER + e];
+        }
+#pragma unroll
+        for (int r = 0; r < kMaxRep; ++r) rotate(qv[r]);
+    }
 
     for (int c0 = begin; c0 < end; c0 += kChunk) {
         // scores of the chunk: each wave takes 4 positions per round, 4 rounds; all the K
@@ -128,6 +164,22 @@ __global__ __launch_bounds__(kThreads) void k_attention(
                 const f32x4 v = *(const f32x4*)(kr + e);
                 kv[round][e] = v.x; kv[round][e + 1] = v.y; kv[round][e + 2] = v.z;
                 kv[round][e + 3] = v.w;
+            }
+        }
+        // the new key row (clamped positions past the end repeat it, and rotate it alike)
+        bool knew[kChunk / 16];
+        if (rope) {
+#pragma unroll
+            for (int round = 0; round < kChunk / 16; ++round) {
+                knew[round] = min(c0 + round * 16 + wave * 4 + sub, end - 1) == pos0;
+                float rot[PER];
+#pragma unroll
+                for (int e = 0; e < PER; ++e) rot[e] = kv[round][e];
+                rotate(rot);
+                if (knew[round]) {
+#pragma unroll
+                    for (int e = 0; e < PER; ++e) kv[round][e] = rot[e];
+                }
             }
         }
         // this wave's V rows, issued with the K rows so both latencies overlap the score and softmax
@@ -158,6 +210,18 @@ __global__ __launch_bounds__(kThreads) void k_attention(
             }
         }
         __syncthreads();
+        // every K load of the workgroup has been consumed: the rotated row can go back
+        if (rope) {
+#pragma unroll
+            for (int round = 0; round < kChunk / 16; ++round) {
+                if (knew[round]) {
+                    float* kw = k_new + kvh * HD + seg * PER;
+#pragma unroll
+                    for (int e = 0; e < PER; e += 4)
+                        *(f32x4*)(kw + e) = f32x4{kv[round][e], kv[round][e + 1], kv[round][e + 2], kv[round][e + 3]};
+                }
+            }
+        }
         // one wave per query head (lane i = position i of the chunk): the running max, the
         // probabilities relative to it in place of the scores, their sum, and the factor that
         // rescales what is already summed
@@ -288,7 +352,8 @@ __global__ __launch_bounds__(kThreads) void k_attention(
 template <int HD>
 hipError_t launch_attention_hd(const float* q, const float* kc, const float* vc, int rows,
                                int pos0, int n_head, int n_kv, float* out, float* part,
-                               size_t part_floats, int* counters, hipStream_t stream) {
+                               size_t part_floats, int* counters, float rope_base, float* k_new,
+                               hipStream_t stream) {
     const int L_max = pos0 + rows;
     // splits: enough workgroups for the device, at least one chunk per split
     const int64_t base = (int64_t)n_kv * rows;
@@ -303,7 +368,7 @@ hipError_t launch_attention_hd(const float* q, const float* kc, const float* vc,
     const float scale = 1.0f / std::sqrt((float)HD);  // engine.cpp:121, IEEE on the host
     hipLaunchKernelGGL((k_attention<HD>), dim3((unsigned)n_kv, (unsigned)rows, (unsigned)S),
                        dim3(kThreads), 0, stream, q, kc, vc, n_head, n_kv, pos0, split_len, scale,
-                       part, counters, out);
+                       part, counters, out, rope_base, k_new);
     return hipGetLastError();
 }
 
@@ -334,17 +399,19 @@ bool attention_supported(int head_dim, int n_head, int n_kv) {
 // launch), then the split partials.
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int pos0,
                             int n_head, int n_kv, int head_dim, float* out, void* ws,
-                            size_t ws_bytes, hipStream_t stream) {
+                            size_t ws_bytes, hipStream_t stream, float rope_base) {
     if (rows <= 0) return hipSuccess;
     if (!attention_supported(head_dim, n_head, n_kv)) return hipErrorInvalidValue;
+    if (rope_base > 0.0f && rows != 1) return hipErrorInvalidValue;
+    float* k_new = rope_base > 0.0f ? const_cast<float*>(kc) + (size_t)pos0 * n_kv * head_dim : nullptr;
     constexpr size_t kCountBytes = kAttnCounters * sizeof(int);
     int* counters = ws && ws_bytes > kCountBytes ? (int*)ws : nullptr;
     float* part = counters ? (float*)((char*)ws + kCountBytes) : nullptr;
     const size_t part_floats = counters ? (ws_bytes - kCountBytes) / sizeof(float) : 0;
     switch (head_dim) {
-        case 64: return launch_attention_hd<64>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, stream);
-        case 128: return launch_attention_hd<128>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, stream);
-        default: return launch_attention_hd<256>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, stream);
+        case 64: return launch_attention_hd<64>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, rope_base, k_new, stream);
+        case 128: return launch_attention_hd<128>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, rope_base, k_new, stream);
+        default: return launch_attention_hd<256>(q, kc, vc, rows, pos0, n_head, n_kv, out, part, part_floats, counters, rope_base, k_new, stream);
     }
 }
 

@@ -107,9 +107,11 @@ hipError_t launch_rope_neox(float* x, int rows, int n_heads, float* x2, int n_he
                             int head_dim, int pos0, float base, hipStream_t stream);
 bool attention_supported(int head_dim, int n_head, int n_kv);
 size_t attention_workspace_bytes(int rows, int n_head, int head_dim);
+// With rope_base > 0 (rows == 1 only), q and the key row at pos0 are unrotated: the kernel
+// applies launch_rope_neox's rotation to both (the key row in place in kc).
 hipError_t launch_attention(const float* q, const float* kc, const float* vc, int rows, int pos0,
                             int n_head, int n_kv, int head_dim, float* out, void* ws,
-                            size_t ws_bytes, hipStream_t stream);
+                            size_t ws_bytes, hipStream_t stream, float rope_base = 0.0f);
 
 // Rows ids[0..n) of a weight matrix of any GGML type, dequantized to fp32 out[n][k] exactly
 // as the reference's dequantize_block (the embedding lookup). k_gemv_f.hip.

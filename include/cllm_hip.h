@@ -197,6 +197,15 @@ int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_
                            int n_rows, int pos0, int n_head, int n_head_kv, int head_dim,
                            float* out, void* stream);
 
+/* One decode step's RoPE and attention in one launch (engine.cpp:486-495): q holds one row of
+ * n_head unrotated query heads, k_cache row pos0 the unrotated new key; both get the NEOX
+ * rotation of cllm_hip_rope_neox2_dev at position pos0 (the queries in registers, q is not
+ * written; the key row in place in k_cache), then the attention of cllm_hip_attention_dev over
+ * the pos0 + 1 cached positions. The same output and key row as those two calls, bit for bit. */
+int cllm_hip_attention_rope_dev(const float* q, float* k_cache, const float* v_cache, int pos0,
+                                int n_head, int n_head_kv, int head_dim, float theta_base,
+                                float* out, void* stream);
+
 /* ---- GGUF files ------------------------------------------------------------------------ */
 
 /* A GGUF file mapped read-only, parsed like GgufLoader::load (src/core/gguf.cpp:122-275):

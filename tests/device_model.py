@@ -177,9 +177,13 @@ class DeviceModel:
                 qv = q.view(T * self.n_head, self.hd)
                 self._norm_inplace(qv, self.w[p + "attn_q_norm.weight"])
                 self._norm_inplace(kc.view(T * self.n_kv, self.hd), self.w[p + "attn_k_norm.weight"])
-            C.rope_neox2_dev(q, self.n_head, kc, self.n_kv, self.hd, pos0, self.theta)
-            C.attention_dev(q, self.k_cache[l], self.v_cache[l], pos0, self.n_head, self.n_kv,
-                            self.hd, out=attn)
+            if T == 1:  # decode: the rotation rides in the attention launch
+                C.attention_rope_dev(q, self.k_cache[l], self.v_cache[l], pos0, self.n_head,
+                                     self.n_kv, self.hd, self.theta, out=attn)
+            else:
+                C.rope_neox2_dev(q, self.n_head, kc, self.n_kv, self.hd, pos0, self.theta)
+                C.attention_dev(q, self.k_cache[l], self.v_cache[l], pos0, self.n_head, self.n_kv,
+                                self.hd, out=attn)
             # the GEMV quantizes the attention output itself and adds into x
             wo = p + "attn_output.weight"
             C.matmul_quant_residual_dev(attn, self.w[wo], self._type(wo), None, self.q_dim,

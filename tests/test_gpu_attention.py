@@ -82,6 +82,32 @@ def test_attention(gpu, hd, n_head, n_kv, rows, pos0):
     assert (err <= 2e-6 * np.maximum(scale, 1e-3)).all(), err.max()
 
 
+@pytest.mark.parametrize("hd,n_head,n_kv,pos0,base", [(128, 32, 8, 1024, 500000.0),
+                                                      (128, 32, 8, 0, 500000.0),
+                                                      (64, 14, 2, 63, 1000000.0),
+                                                      (256, 8, 1, 200, 10000.0),
+                                                      (128, 40, 8, 4095, 1000000.0)])
+def test_attention_rope_equals_rope_then_attention(gpu, hd, n_head, n_kv, pos0, base):
+    """RoPE fused into the decode attention: the output and the rotated key row equal, bit for
+    bit, the rotation of the queries and the key row followed by the attention; q stays as it
+    was and no other cache row changes."""
+    rng = np.random.default_rng(hd + n_head + pos0)
+    L = pos0 + 1
+    q = rng.standard_normal((1, n_head * hd)).astype(np.float32)
+    kc = rng.standard_normal((L + 3, n_kv * hd)).astype(np.float32)
+    vc = rng.standard_normal((L + 3, n_kv * hd)).astype(np.float32)
+    print("attention+rope", hd, n_head, n_kv, pos0, flush=True)
+    qa, ka = _dev(q), _dev(kc)
+    gpu.rope_neox2_dev(qa, n_head, ka[pos0:pos0 + 1], n_kv, hd, pos0, base)
+    want = gpu.attention_dev(qa, ka, _dev(vc), pos0, n_head, n_kv, hd).cpu().numpy()
+    qb, kb = _dev(q), _dev(kc)
+    got = gpu.attention_rope_dev(qb, kb, _dev(vc), pos0, n_head, n_kv, hd, base).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    kb_h, ka_h = kb.cpu().numpy(), ka.cpu().numpy()
+    assert np.array_equal(kb_h.view(np.uint32), ka_h.view(np.uint32))
+    assert np.array_equal(qb.cpu().numpy().view(np.uint32), q.view(np.uint32))
+
+
 def test_attention_closed_forms(gpu):
     rng = np.random.default_rng(1)
     hd, n_head, n_kv = 128, 8, 2
