@@ -136,3 +136,10 @@ def test_attention_argument_errors(gpu):
     q = torch.zeros((1, 32 * 128), device="cuda")
     with pytest.raises(RuntimeError, match="at most 8 query heads"):
         gpu.attention_dev(q, q, q, 0, 32, 2, 128)
+    q = torch.zeros((1, 32 * 128), device="cuda")
+    kv = torch.zeros((4, 8 * 128), device="cuda")
+    for bad in (0.0, -10000.0, float("nan")):
+        with pytest.raises(RuntimeError, match="theta_base must be positive"):
+            gpu.attention_rope_dev(q, kv, kv, 3, 32, 8, 128, bad)
+    with pytest.raises(RuntimeError, match="head_dim must be 64, 128 or 256"):
+        gpu.attention_rope_dev(q, kv, kv, 3, 32, 8, 96, 10000.0)
