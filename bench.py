@@ -366,8 +366,8 @@ def main():
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this path is not sharded across GPUs in this build "
-              "(see the sharding design notes); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the path is not sharded across GPUs; run with "
+              "--gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch

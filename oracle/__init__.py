@@ -1,8 +1,9 @@
-"""ctypes access to the checkers: the C restatement (liboracle.so) and, where it was built,
+"""ctypes access to the test oracles: the C restatement (liboracle.so) and, where it was built,
 the reference compiled from its own sources (_ref/libcllm_ref.so).
 
 TEST INFRASTRUCTURE ONLY. Imported by tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg, always as the checker or the timed CPU baseline, never as the product.
+cpu_baseline leg, always as the reference the results are compared with or the timed CPU
+baseline, never as the product.
 """
 from __future__ import annotations
 

@@ -1,7 +1,7 @@
 /*
  * cllm_oracle.c -- CPU restatement of cllm_inference's quantized linear-layer path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP path, never the product. See
+ * TEST INFRASTRUCTURE ONLY: the oracle the HIP path is tested against, never the product. See
  * cllm_oracle.h for the reference line each function follows.
  *
  * Arithmetic contract. The reference is built with clang -O3 and default FP contraction, so

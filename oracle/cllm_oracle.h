@@ -2,7 +2,7 @@
  * cllm_oracle.h -- CPU restatement of cllm_inference's quantized linear-layer path.
  *
  * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the cpu_baseline
- * leg of bench.py may load this library, and only as the checker. The product path
+ * leg of bench.py may load this library, and only as the oracle. The product path
  * (libcllm_hip.so) never links, loads or calls it.
  *
  * Every function restates one piece of the reference (citations are path:line into the

@@ -2,7 +2,7 @@
 // exercised the way the reference's tests/quant_test.cpp exercises its own: fixed weight
 // patterns with d = 1, matmul_quant against a dequantize-and-dot reference, the bias
 // difference, batch against row-by-row. The expected values come from the C oracle
-// (oracle/cllm_oracle.h), linked here as the checker only.
+// (oracle/cllm_oracle.h), linked here as the oracle only.
 //
 //   quant_api_test --cpu   checks that need no GPU: size tables, has_vec_dot, the fp16
 //                          conversions, and every argument error the API raises before it
