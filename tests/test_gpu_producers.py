@@ -159,13 +159,14 @@ def test_gemv_multi_equals_separate_launches(gpu, qt):
             assert np.array_equal(bits(ys[i].cpu().numpy()), bits(one.cpu().numpy())), (n_mats, i)
 
 
-@pytest.mark.parametrize("qt,m,n_ff", [(S.Q4_K, 1, 14336), (S.Q4_K, 2, 1000), (S.Q6_K, 1, 4096),
-                                       (S.Q8_0, 5, 2048), (S.Q5_K, 8, 777)])
-def test_gemv_swiglu_equals_projections_then_swiglu(gpu, qt, m, n_ff):
+@pytest.mark.parametrize("qt,m,n_ff,k", [(S.Q4_K, 1, 14336, 4096), (S.Q4_K, 2, 1000, 4096),
+                                         (S.Q6_K, 1, 4096, 4096), (S.Q8_0, 5, 2048, 4096),
+                                         (S.Q5_K, 8, 777, 4096), (S.Q4_K, 8, 4200, 14336)])
+def test_gemv_swiglu_equals_projections_then_swiglu(gpu, qt, m, n_ff, k):
     """gate, up and silu(gate) * up in one launch give the bits of the two projections in one
-    launch followed by the SwiGLU producer (ragged row counts and several activation rows
-    included), with and without biases."""
-    k = 4096
+    launch followed by the SwiGLU producer (ragged row counts, several activation rows, and
+    rows of several 64-unit items streamed through the two-deep ring included), with and
+    without biases."""
     rng = np.random.default_rng(qt + 400 + m)
     wg = _dev(S.make_weight(qt, n_ff, k, 40))
     wu = _dev(S.make_weight(qt, n_ff, k, 41))
