@@ -13,7 +13,10 @@
 #include <cstring>
 #include <map>
 #include <memory>
+#include <barrier>
 #include <mutex>
+#include <thread>
+#include <vector>
 #include <string>
 
 #include "../../include/cllm_hip.h"
@@ -825,7 +828,9 @@ int cllm_hip_gguf_open(const char* path, int upload, cllm_hip_gguf** out) {
         const size_t bytes = f.map_bytes > f.data_offset ? f.map_bytes - f.data_offset : 0;
         if (bytes > 0) {
             // One pass over the data section through two pinned staging buffers: the host
-            // copy into one buffer overlaps the DMA out of the other.
+            // copy into one buffer overlaps the DMA out of the other. The host copy (from the
+            // mapped file) is split over a few threads, one slice of each chunk apiece: a
+            // single thread copying out of the page cache cannot keep up with the DMA.
             constexpr size_t kChunk = 32u << 20;
             void* stage[2] = {nullptr, nullptr};
             hipEvent_t done[2] = {nullptr, nullptr};
@@ -836,16 +841,43 @@ int cllm_hip_gguf_open(const char* path, int upload, cllm_hip_gguf** out) {
                 if (e == hipSuccess) e = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
             }
             const uint8_t* src = (const uint8_t*)f.map + f.data_offset;
+            const int n_thr = (int)std::min<unsigned>(8u, std::max(1u, std::thread::hardware_concurrency()));
+            struct CopyJob {
+                void* dst = nullptr;
+                const uint8_t* src = nullptr;
+                size_t len = 0;
+                bool quit = false;
+            } job;
+            std::barrier<> sync(n_thr + 1);  // two phases per chunk: job published, job done
+            std::vector<std::thread> pool;
+            for (int t = 0; t < n_thr; ++t)
+                pool.emplace_back([&job, &sync, n_thr, t] {
+                    for (;;) {
+                        sync.arrive_and_wait();
+                        if (job.quit) return;
+                        const size_t per = (job.len + n_thr - 1) / n_thr;
+                        const size_t a = std::min(job.len, (size_t)t * per), b = std::min(job.len, a + per);
+                        if (b > a) std::memcpy((uint8_t*)job.dst + a, job.src + a, b - a);
+                        sync.arrive_and_wait();
+                    }
+                });
             for (size_t off = 0, i = 0; e == hipSuccess && off < bytes; off += kChunk, ++i) {
                 const size_t len = std::min(kChunk, bytes - off);
                 const int b = (int)(i & 1);
                 if (i >= 2) e = hipEventSynchronize(done[b]);
                 if (e != hipSuccess) break;
-                std::memcpy(stage[b], src + off, len);
+                job.dst = stage[b];
+                job.src = src + off;
+                job.len = len;
+                sync.arrive_and_wait();  // the workers copy the chunk
+                sync.arrive_and_wait();
                 e = hipMemcpyAsync((char*)g->dev + off, stage[b], len, hipMemcpyHostToDevice,
                                    st->stream);
                 if (e == hipSuccess) e = hipEventRecord(done[b], st->stream);
             }
+            job.quit = true;
+            sync.arrive_and_wait();
+            for (auto& th : pool) th.join();
             if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
             for (int i = 0; i < 2; ++i) {
                 if (done[i]) (void)hipEventDestroy(done[i]);
