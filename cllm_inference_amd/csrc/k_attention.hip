@@ -305,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void k_attention(
     if (!last) return;
     // out = sum_z e^(m_z - M) o_z / sum_z e^(m_z - M) l_z, per head of the group. The maxima
     // and sums of all splits are loaded at once (one per thread) into LDS; each output then
-    // reads its S values eight loads at a time.
+    // reads its S values sixteen loads at a time.
     auto ld = [](const float* a) {
         return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
@@ -337,12 +337,12 @@ __global__ __launch_bounds__(kThreads) void k_attention(
         const float* pp = part + ((size_t)t * n_head + kvh * n_rep + r) * S * (HD + 2) + d;
         float num = 0.0f;
         int zz = 0;
-        for (; zz + 8 <= S; zz += 8) {
-            float v[8];
+        for (; zz + 16 <= S; zz += 16) {
+            float v[16];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = ld(pp + (size_t)(zz + u) * (HD + 2));
+            for (int u = 0; u < 16; ++u) v[u] = ld(pp + (size_t)(zz + u) * (HD + 2));
 #pragma unroll
-            for (int u = 0; u < 8; ++u) num = __builtin_fmaf(wz[r][zz + u], v[u], num);
+            for (int u = 0; u < 16; ++u) num = __builtin_fmaf(wz[r][zz + u], v[u], num);
         }
         for (; zz < S; ++zz) num = __builtin_fmaf(wz[r][zz], ld(pp + (size_t)zz * (HD + 2)), num);
         out[((size_t)t * n_head + kvh * n_rep + r) * HD + d] = __fdiv_rn(num, lsum[r]);
