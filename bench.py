@@ -182,21 +182,19 @@ def decode_layer_device(C, S, steps, warmup, copies=4):
 
     def step(i):
         L = layers[i % copies]
-        _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn1, 1e-5, h=False)
         qt, _, k = mats["wq"]
-        C.gemv_q8_multi_dev([L[l] for l in qkv], qt, k, [mats[l][1] for l in qkv], qs, sc, bs,
-                            ys=[outs[l] for l in qkv])
+        C.rmsnorm_gemv_multi_dev(x, wn1, 1e-5, [L[l] for l in qkv], qt, k,
+                                 [mats[l][1] for l in qkv], ys=[outs[l] for l in qkv])
         qt, n, k = mats["wo"]
         C.matmul_quant_residual_dev(attn, L["wo"], qt, None, k, n, x)
-        _, qs, sc, bs = C.rmsnorm_q8_0_dev(x, wn2, 1e-5, h=False)
         qt, n_g, k = mats["gate"]
-        C.gemv_q8_swiglu_dev(L["gate"], L["up"], qt, k, n_g, qs, sc, bs, h=hbuf)
+        C.rmsnorm_gemv_swiglu_dev(x, wn2, 1e-5, L["gate"], L["up"], qt, k, n_g, h=hbuf)
         qt, n, k = mats["down"]
         C.matmul_quant_residual_dev(hbuf, L["down"], qt, None, k, n, x)
 
     ms = time_loop(step, steps, warmup)
     x.copy_(x0)
-    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 6,
+    per = {"layer_us": round(ms * 1e3, 2), "weight_bytes": int(wbytes), "launches": 4,
            "gbs": round(wbytes / ms / 1e6, 1),
            "frac_hbm": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
            "projected_tokens_per_s_32_layers_linear_only": round(1e3 / (32 * ms), 1),

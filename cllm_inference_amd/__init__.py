@@ -68,6 +68,10 @@ SIGNATURES = {
     "cllm_hip_gemv_q8_residual_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_multi_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_swiglu_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P]),
+    "cllm_hip_rmsnorm_gemv_multi_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.c_float,
+                                             _P]),
+    "cllm_hip_rmsnorm_gemv_swiglu_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _P, _P, ctypes.c_float,
+                                              _P, _P]),
     "cllm_hip_gguf_open": (_I, [ctypes.c_char_p, _I, ctypes.POINTER(_P)]),
     "cllm_hip_gguf_close": (_I, [_P]),
     "cllm_hip_gguf_tensor_count": (_I, [_P]),
@@ -270,6 +274,40 @@ def gemv_q8_swiglu_dev(w_gate, w_up, t: int, in_dim: int, n_ff: int, qs, scales,
     _check(load_library().cllm_hip_gemv_q8_swiglu_dev(
         int(t), int(in_dim), int(n_ff), _tp(w_gate), _tp(w_up), _tp(bias_gate), _tp(bias_up),
         int(m), _tp(qs), _tp(scales), _tp(bsums), _tp(h), _stream()))
+    return h
+
+
+def rmsnorm_gemv_multi_dev(x, norm_w, eps: float, ws, t: int, in_dim: int, out_dims, ys=None,
+                           biases=None):
+    """RMSNorm of the one row x (float32 (1, in_dim), in_dim <= 4096) with weight norm_w, then
+    gemv_q8_multi_dev on it, in one launch (engine.cpp:475-478); the bits of rmsnorm_q8_0_dev
+    followed by gemv_q8_multi_dev. Returns the list of outputs [1, out_dims[i]]."""
+    import torch
+    n_mats = len(ws)
+    if ys is None:
+        ys = [torch.empty((1, int(n)), dtype=torch.float32, device=x.device) for n in out_dims]
+    wa = (ctypes.c_void_p * n_mats)(*[w.data_ptr() for w in ws])
+    ya = (ctypes.c_void_p * n_mats)(*[y.data_ptr() for y in ys])
+    na = (ctypes.c_int * n_mats)(*[int(n) for n in out_dims])
+    ba = None
+    if biases is not None:
+        ba = (ctypes.c_void_p * n_mats)(*[0 if b is None else b.data_ptr() for b in biases])
+    _check(load_library().cllm_hip_rmsnorm_gemv_multi_dev(
+        int(t), int(in_dim), n_mats, wa, na, ba, ya, _tp(x), _tp(norm_w), float(eps), _stream()))
+    return ys
+
+
+def rmsnorm_gemv_swiglu_dev(x, norm_w, eps: float, w_gate, w_up, t: int, in_dim: int, n_ff: int,
+                            h=None, bias_gate=None, bias_up=None):
+    """RMSNorm of the one row x, then gemv_q8_swiglu_dev on it, in one launch
+    (engine.cpp:508-512); the bits of rmsnorm_q8_0_dev followed by gemv_q8_swiglu_dev.
+    Returns h [1, n_ff]."""
+    import torch
+    if h is None:
+        h = torch.empty((1, int(n_ff)), dtype=torch.float32, device=x.device)
+    _check(load_library().cllm_hip_rmsnorm_gemv_swiglu_dev(
+        int(t), int(in_dim), int(n_ff), _tp(w_gate), _tp(w_up), _tp(bias_gate), _tp(bias_up),
+        _tp(x), _tp(norm_w), float(eps), _tp(h), _stream()))
     return h
 
 

@@ -584,6 +584,60 @@ int cllm_hip_gemv_q8_swiglu_dev(uint32_t type, int in_dim, int n_ff, const void*
     return CLLM_HIP_OK;
 }
 
+// The one fp32 row a fused RMSNorm staging takes.
+static int check_norm_row(int in_dim, const float* x, const float* norm_w) {
+    if (in_dim <= 0 || in_dim > 4096 || in_dim % 32 != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "rms_norm: a fused row is a multiple of 32 up to 4096");
+    if (!x || !norm_w) return set_err(CLLM_HIP_E_ARG, "rms_norm: null pointer");
+    if (!aligned16(x) || !aligned16(norm_w))
+        return set_err(CLLM_HIP_E_ARG, "rms_norm: misaligned device pointer");
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_rmsnorm_gemv_multi_dev(uint32_t type, int in_dim, int n_mats, const void* const* w,
+                                    const int* out_dims, const float* const* bias,
+                                    float* const* y, const float* x, const float* norm_w,
+                                    float eps, void* stream) {
+    if (n_mats < 1 || n_mats > 3 || !w || !out_dims || !y)
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: 1 to 3 matrices expected");
+    int rc;
+    for (int i = 0; i < n_mats; ++i)
+        if ((rc = check_matmul("matmul_quant", type, in_dim, out_dims[i]))) return rc;
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if ((rc = check_norm_row(in_dim, x, norm_w))) return rc;
+    for (int i = 0; i < n_mats; ++i) {
+        if (!w[i] || !y[i]) return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+        if (!aligned16(w[i]) || ((uintptr_t)y[i] & 3u) || (bias && ((uintptr_t)bias[i] & 3u)))
+            return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    }
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    HIP_TRY(launch_rmsnorm_gemv_multi(type, in_dim, n_mats, (const uint8_t* const*)w, out_dims,
+                                      bias, y, x, norm_w, eps, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_rmsnorm_gemv_swiglu_dev(uint32_t type, int in_dim, int n_ff, const void* w_gate,
+                                     const void* w_up, const float* bias_gate,
+                                     const float* bias_up, const float* x, const float* norm_w,
+                                     float eps, float* h, void* stream) {
+    int rc = check_matmul("matmul_quant", type, in_dim, n_ff);
+    if (rc) return rc;
+    if (!has_kernel(type)) return set_err(CLLM_HIP_E_TYPE, "vec_dot_row: no kernel for this type");
+    if ((rc = check_norm_row(in_dim, x, norm_w))) return rc;
+    if (n_ff == 0) return CLLM_HIP_OK;
+    if (!w_gate || !w_up || !h) return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(w_gate) || !aligned16(w_up) || ((uintptr_t)h & 3u) ||
+        ((uintptr_t)bias_gate & 3u) || ((uintptr_t)bias_up & 3u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    HIP_TRY(launch_rmsnorm_gemv_swiglu(type, in_dim, n_ff, (const uint8_t*)w_gate,
+                                       (const uint8_t*)w_up, bias_gate, bias_up, x, norm_w, eps, h,
+                                       (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
 int cllm_hip_gemv_q8_residual_dev(const void* w, uint32_t type, int in_dim, int out_dim,
                                   int n_rows, const int8_t* qs, const float* scales,
                                   const int32_t* bsums, const float* bias, float* y,

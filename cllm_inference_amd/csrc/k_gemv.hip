@@ -486,6 +486,13 @@ __device__ __forceinline__ ActLds act_layout(uint8_t* lds, int k) {
 // indices (so the compiler counts them exactly); only valid slots are stored.
 constexpr int kPre = 2;
 
+// Workgroup barrier that orders LDS only: the weight loads still in flight are not waited for.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Copy of an already-quantized Q8_0 batch: slot i < MR*k/16 is 16 qs bytes (plus its
 // 16-element sum for Q6_K); slot j < MR*nb is one block's dx and bsum.
 template <uint32_t T, int MR>
@@ -559,13 +566,25 @@ struct StageCopy {
 // round-to-nearest-even rounds exactly as rint; the clamp cannot act). The four lanes of a
 // block take the same path. Other blocks run q8_quant4, which reproduces the reference's NaN
 // handling of amax and the x86 INT_MIN conversion of out-of-range values.
-template <uint32_t T, int MR>
+//
+// With NORM (one row of at most 4096 elements, 512 threads) the row first goes through the
+// RMSNorm h = (x * rms) * nw (engine.cpp:23-28) and h is quantized. The sum of squares is
+// reduced in the order of k_rmsnorm_q8_0_reg<1> (1024 threads of one 4-element chunk each, a
+// wave sum, then the 16 wave sums in order), so h and its blocks are bit-identical to that
+// kernel's: thread t holds chunks 2t and 2t + 1, and their sum followed by butterflies over
+// 2, 4, .., 32 lanes adds the same pairs of values as that kernel's wave sum (float addition
+// is commutative), leaving its wave sums 2w and 2w + 1 in lanes 0 and 32 of wave w.
+template <uint32_t T, int MR, bool NORM = false>
 struct StageQuant {
     using Tr = typename TraitsOf<T>::type;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     const float* __restrict__ x;
     int k;
     f32x4 v[2];
+    const float* __restrict__ nw = nullptr;  // NORM: the norm weight
+    float eps = 0.0f;
+    float* part = nullptr;                   // NORM: 16 floats of LDS
+    f32x4 wv[2] = {};
 
     __device__ __forceinline__ int slots() const { return MR * (k / 8); }
     __device__ __forceinline__ void load_slot(int i, f32x4 (&r)[2]) const {
@@ -641,9 +660,50 @@ struct StageQuant {
         return (int)(threadIdx.x & ~63u) < slots();
     }
     __device__ __forceinline__ void issue() {
-        if (wave_live()) load_slot(threadIdx.x, v);
+        if (wave_live()) {
+            load_slot(threadIdx.x, v);
+            if constexpr (NORM) {
+                const f32x4* p = (const f32x4*)(nw + (size_t)min((int)threadIdx.x, slots() - 1) * 8);
+                wv[0] = p[0];
+                wv[1] = p[1];
+            }
+        }
     }
-    __device__ __forceinline__ void commit(const ActLds& a) const {
+    // NORM: every thread of the workgroup takes part (one LDS barrier).
+    __device__ __forceinline__ void normalize() {
+        float sa = 0.0f, sb = 0.0f;
+        if ((int)threadIdx.x < slots()) {
+            sa = __builtin_fmaf(v[0].x, v[0].x, sa);
+            sa = __builtin_fmaf(v[0].y, v[0].y, sa);
+            sa = __builtin_fmaf(v[0].z, v[0].z, sa);
+            sa = __builtin_fmaf(v[0].w, v[0].w, sa);
+            sb = __builtin_fmaf(v[1].x, v[1].x, sb);
+            sb = __builtin_fmaf(v[1].y, v[1].y, sb);
+            sb = __builtin_fmaf(v[1].z, v[1].z, sb);
+            sb = __builtin_fmaf(v[1].w, v[1].w, sb);
+        }
+        float s = sa + sb;
+        s += dpp_f32<DPP_QUAD_SWAP1>(s);
+        s += dpp_f32<DPP_QUAD_SWAP2>(s);
+        s += dpp_f32<DPP_ROW_HALF_MIRROR>(s);
+        s += dpp_f32<DPP_ROW_MIRROR>(s);
+        s += __shfl_xor(s, 16, 64);
+        if ((threadIdx.x & 31) == 0) part[threadIdx.x >> 5] = s;
+        lds_barrier();
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sum += part[i];
+        const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sum, (float)k) + eps));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            v[j].x = __fmul_rn(__fmul_rn(v[j].x, rms), wv[j].x);
+            v[j].y = __fmul_rn(__fmul_rn(v[j].y, rms), wv[j].y);
+            v[j].z = __fmul_rn(__fmul_rn(v[j].z, rms), wv[j].z);
+            v[j].w = __fmul_rn(__fmul_rn(v[j].w, rms), wv[j].w);
+        }
+    }
+    __device__ __forceinline__ void commit(const ActLds& a) {
+        if constexpr (NORM) normalize();
         if (wave_live() && (int)threadIdx.x < slots()) quant_slot(a, threadIdx.x, v);
     }
     __device__ __forceinline__ void rest(const ActLds& a) const {
@@ -658,13 +718,6 @@ struct StageQuant {
     }
 };
 
-// Workgroup barrier that orders LDS only: the weight loads still in flight are not waited for.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Up to three weight matrices of one type and row length that read the same activation rows
 // (q, k and v; gate and up) run as one launch: virtual row j belongs to segment s with
 // start[s] <= j < start[s + 1] and is row j - start[s] of w[s], its results going to y[s]
@@ -677,6 +730,8 @@ struct GemvSegs {
     const float* bias[3];
     int start[3];
     int rows[3];
+    const float* norm_w;  // the RMSNorm weight of the NORM kernels, else null
+    float eps;
 };
 
 __device__ __forceinline__ int seg_of(const GemvSegs& sg, int j) {
@@ -700,7 +755,10 @@ constexpr int gemv_threads() { return MR <= 2 ? 512 : 256; }
 // is the gate matrix, segment 1 the up matrix, both of n rows; a wave takes row p of both in
 // turn (row p of gate, then row p of up) and writes h[p] = silu(gate_p) * up_p to y[0] instead
 // of the two projections, so the SwiGLU needs no launch of its own.
-template <uint32_t T, int MR, int P, bool SW = false>
+//
+// With NORM (MR = 1, k <= 4096): the fp32 row x_f32 goes through the RMSNorm with weight
+// sg.norm_w in the staging (StageQuant) before it is quantized.
+template <uint32_t T, int MR, int P, bool SW = false, bool NORM = false>
 __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_t row_bytes,
                                               int k, int n, const int8_t* __restrict__ qs,
                                               const float* __restrict__ xs,
@@ -743,8 +801,15 @@ __global__ __launch_bounds__(gemv_threads<MR>()) void k_gemv(GemvSegs sg, int64_
     // so no wave waits for weight bytes before the first item's compute.
     const ActLds a = act_layout<T, MR>(lds, k);
     StageCopy<T, MR> sc{qs, xs, xb, k, {}, {}, {}};
-    StageQuant<T, MR> sq{x_f32, k, {}};
-    const bool fused = x_f32 != nullptr;
+    StageQuant<T, MR, NORM> sq{x_f32, k, {}};
+    static_assert(!NORM || MR == 1, "the RMSNorm staging takes one row");
+    __shared__ float norm_part[16];
+    if constexpr (NORM) {
+        sq.nw = sg.norm_w;
+        sq.eps = sg.eps;
+        sq.part = norm_part;
+    }
+    const bool fused = NORM || x_f32 != nullptr;
     if (fused)
         sq.issue();
     else
@@ -1070,7 +1135,7 @@ static const GemvTuning& gemv_tuning() {
 
 // Waves of k_gemv<T, MR, P> resident on the whole device with `shmem` bytes of LDS per
 // workgroup (cached per instantiation for the last LDS size asked).
-template <uint32_t T, int MR, int P, bool SW = false>
+template <uint32_t T, int MR, int P, bool SW = false, bool NORM = false>
 static int64_t resident_waves(size_t shmem) {
     static std::atomic<uint64_t> cache{0};  // (shmem << 16) | workgroups per CU, 0 = empty
     uint64_t c = cache.load(std::memory_order_relaxed);
@@ -1079,7 +1144,7 @@ static int64_t resident_waves(size_t shmem) {
         blocks = (int)(c & 0xFFFFu);
     } else {
         blocks = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv<T, MR, P, SW>),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv<T, MR, P, SW, NORM>),
                                                          gemv_threads<MR>(), shmem) != hipSuccess ||
             blocks < 1)
             blocks = 1;
@@ -1132,7 +1197,7 @@ static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, 
 template <uint32_t T>
 constexpr int64_t staged_min_bytes() { return T == T_Q6_K ? 32ll << 20 : T == T_Q4_K ? 96ll << 20 : INT64_MAX; }
 
-template <uint32_t T, int MR, int P, bool SW>
+template <uint32_t T, int MR, int P, bool SW, bool NORM = false>
 static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
                            const int32_t* xb, const float* x_f32, int accumulate, int waves,
                            hipStream_t stream) {
@@ -1141,7 +1206,7 @@ static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, c
     constexpr int kWaves = gemv_threads<MR>() / 64;
     const int grid = (waves + kWaves - 1) / kWaves;
     const size_t shmem = act_lds_bytes<T>(MR, k);
-    hipLaunchKernelGGL((k_gemv<T, MR, P, SW>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, sg,
+    hipLaunchKernelGGL((k_gemv<T, MR, P, SW, NORM>), dim3(grid), dim3(gemv_threads<MR>()), shmem, stream, sg,
                        row_bytes, k, n, qs, xs, xb, x_f32, accumulate);
     return hipGetLastError();
 }
@@ -1166,6 +1231,14 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
     const int64_t simds = (int64_t)cu_count() * 4;
     const GemvTuning& tu = gemv_tuning();
     const size_t shmem = act_lds_bytes<T>(MR, k);
+    if constexpr (MR == 1) {
+        if (sg.norm_w) {  // the RMSNorm rides in the staging (one row, a ring of one)
+            const int64_t waves =
+                std::min({items, simds * tu.short_wps, resident_waves<T, 1, 1, SW, true>(shmem)});
+            return launch_t<T, 1, 1, SW, true>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves,
+                                               stream);
+        }
+    }
     if constexpr ((T == T_Q6_K || T == T_Q4_K) && MR == 1 && !SW) {
         // (Q4_K's LDS field reads are whole 16-byte pieces: its rows must start 16-byte aligned)
         const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
@@ -1243,6 +1316,8 @@ static GemvSegs one_segment(const uint8_t* w, int n, const float* bias, float* y
         sg.start[i] = i == 0 ? 0 : INT_MAX;
         sg.rows[i] = n;
     }
+    sg.norm_w = nullptr;
+    sg.eps = 0.0f;
     return sg;
 }
 
@@ -1253,13 +1328,12 @@ hipError_t launch_gemv(uint32_t type, const uint8_t* w, int k, int n, int m, con
                          accumulate ? 1 : 0, stream);
 }
 
-hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* const* w,
-                             const int* n, const float* const* bias, float* const* y, int m,
-                             const int8_t* qs, const float* scales, const int32_t* bsums,
-                             hipStream_t stream) {
+// q/k/v (or any 1 to 3 matrices) as segments of one launch.
+static hipError_t multi_segs(int n_mats, const uint8_t* const* w, const int* n,
+                             const float* const* bias, float* const* y, GemvSegs& sg, int& total) {
     if (n_mats < 1 || n_mats > 3) return hipErrorInvalidValue;
-    GemvSegs sg = one_segment(w[0], n[0], bias ? bias[0] : nullptr, y[0]);
-    int total = 0;
+    sg = one_segment(w[0], n[0], bias ? bias[0] : nullptr, y[0]);
+    total = 0;
     for (int i = 0; i < n_mats; ++i) {
         sg.w[i] = w[i];
         sg.y[i] = y[i];
@@ -1269,8 +1343,48 @@ hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* co
         if (n[i] < 0 || (int64_t)total + n[i] > INT_MAX / 2) return hipErrorInvalidValue;
         total += n[i];
     }
+    return hipSuccess;
+}
+
+hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* const* w,
+                             const int* n, const float* const* bias, float* const* y, int m,
+                             const int8_t* qs, const float* scales, const int32_t* bsums,
+                             hipStream_t stream) {
+    GemvSegs sg;
+    int total;
+    const hipError_t e = multi_segs(n_mats, w, n, bias, y, sg, total);
+    if (e != hipSuccess) return e;
     if (total == 0) return hipSuccess;
     return gemv_dispatch(type, sg, k, total, m, qs, scales, bsums, nullptr, 0, stream);
+}
+
+hipError_t launch_rmsnorm_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* const* w,
+                                     const int* n, const float* const* bias, float* const* y,
+                                     const float* x, const float* norm_w, float eps,
+                                     hipStream_t stream) {
+    if (k <= 0 || k > 4096 || k % 32 != 0 || norm_w == nullptr) return hipErrorInvalidValue;
+    GemvSegs sg;
+    int total;
+    const hipError_t e = multi_segs(n_mats, w, n, bias, y, sg, total);
+    if (e != hipSuccess) return e;
+    if (total == 0) return hipSuccess;
+    sg.norm_w = norm_w;
+    sg.eps = eps;
+    return gemv_dispatch(type, sg, k, total, 1, nullptr, nullptr, nullptr, x, 0, stream);
+}
+
+static hipError_t swiglu_dispatch(uint32_t type, const GemvSegs& sg, int k, int n, int m,
+                                  const int8_t* qs, const float* scales, const int32_t* bsums,
+                                  const float* x_f32, hipStream_t stream) {
+    switch (type) {
+        case T_Q4_K: return gemv_all_rows<T_Q4_K, true>(sg, k, n, m, qs, scales, bsums, x_f32, 0, stream);
+        case T_Q5_K: return gemv_all_rows<T_Q5_K, true>(sg, k, n, m, qs, scales, bsums, x_f32, 0, stream);
+        case T_Q6_K: return gemv_all_rows<T_Q6_K, true>(sg, k, n, m, qs, scales, bsums, x_f32, 0, stream);
+        case T_Q8_0: return gemv_all_rows<T_Q8_0, true>(sg, k, n, m, qs, scales, bsums, x_f32, 0, stream);
+        case T_Q4_0: return gemv_all_rows<T_Q4_0, true>(sg, k, n, m, qs, scales, bsums, x_f32, 0, stream);
+        case T_Q5_0: return gemv_all_rows<T_Q5_0, true>(sg, k, n, m, qs, scales, bsums, x_f32, 0, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemv_swiglu(uint32_t type, int k, int n, const uint8_t* w_gate,
@@ -1281,15 +1395,21 @@ hipError_t launch_gemv_swiglu(uint32_t type, int k, int n, const uint8_t* w_gate
     GemvSegs sg = one_segment(w_gate, n, bias_gate, h);
     sg.w[1] = w_up;
     sg.bias[1] = bias_up;
-    switch (type) {
-        case T_Q4_K: return gemv_all_rows<T_Q4_K, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
-        case T_Q5_K: return gemv_all_rows<T_Q5_K, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
-        case T_Q6_K: return gemv_all_rows<T_Q6_K, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
-        case T_Q8_0: return gemv_all_rows<T_Q8_0, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
-        case T_Q4_0: return gemv_all_rows<T_Q4_0, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
-        case T_Q5_0: return gemv_all_rows<T_Q5_0, true>(sg, k, n, m, qs, scales, bsums, nullptr, 0, stream);
-        default: return hipErrorInvalidValue;
-    }
+    return swiglu_dispatch(type, sg, k, n, m, qs, scales, bsums, nullptr, stream);
+}
+
+hipError_t launch_rmsnorm_gemv_swiglu(uint32_t type, int k, int n, const uint8_t* w_gate,
+                                      const uint8_t* w_up, const float* bias_gate,
+                                      const float* bias_up, const float* x, const float* norm_w,
+                                      float eps, float* h, hipStream_t stream) {
+    if (k <= 0 || k > 4096 || k % 32 != 0 || norm_w == nullptr) return hipErrorInvalidValue;
+    if (n <= 0) return hipSuccess;
+    GemvSegs sg = one_segment(w_gate, n, bias_gate, h);
+    sg.w[1] = w_up;
+    sg.bias[1] = bias_up;
+    sg.norm_w = norm_w;
+    sg.eps = eps;
+    return swiglu_dispatch(type, sg, k, n, 1, nullptr, nullptr, nullptr, x, stream);
 }
 
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,

@@ -48,15 +48,31 @@ hipError_t launch_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* co
                              const int8_t* qs, const float* scales, const int32_t* bsums,
                              hipStream_t stream);
 
-// Same as launch_gemv with fp32 activation rows x[m][k]: each launch quantizes its rows to
-// Q8_0 in LDS (bit-identical to launch_quantize_q8_0) instead of reading a quantized batch,
-// so a decode step is a single kernel.
+// launch_gemv_multi on one fp32 row x[k] (k <= 4096, k % 32 == 0) put through the RMSNorm
+// with weight norm_w first, inside the launch: bit-identical to launch_rmsnorm_q8_0 followed
+// by launch_gemv_multi.
+hipError_t launch_rmsnorm_gemv_multi(uint32_t type, int k, int n_mats, const uint8_t* const* w,
+                                     const int* n, const float* const* bias, float* const* y,
+                                     const float* x, const float* norm_w, float eps,
+                                     hipStream_t stream);
+
 // SwiGLU feed-forward input: h[t, j] = silu(gate_j . a_t + bg_j) * (up_j . a_t + bu_j) for the
 // n rows of the gate and up matrices (biases may be null), one launch, on Q8_0 activation rows.
 hipError_t launch_gemv_swiglu(uint32_t type, int k, int n, const uint8_t* w_gate,
                               const uint8_t* w_up, const float* bias_gate, const float* bias_up,
                               float* h, int m, const int8_t* qs, const float* scales,
                               const int32_t* bsums, hipStream_t stream);
+
+// launch_gemv_swiglu on one fp32 row x[k] put through the RMSNorm first, inside the launch
+// (same limits and result as launch_rmsnorm_gemv_multi).
+hipError_t launch_rmsnorm_gemv_swiglu(uint32_t type, int k, int n, const uint8_t* w_gate,
+                                      const uint8_t* w_up, const float* bias_gate,
+                                      const float* bias_up, const float* x, const float* norm_w,
+                                      float eps, float* h, hipStream_t stream);
+
+// Same as launch_gemv with fp32 activation rows x[m][k]: each launch quantizes its rows to
+// Q8_0 in LDS (bit-identical to launch_quantize_q8_0) instead of reading a quantized batch,
+// so a decode step is a single kernel.
 hipError_t launch_gemv_fused(uint32_t type, const uint8_t* w, int k, int n, int m,
                              const float* x, const float* bias, float* y, hipStream_t stream,
                              bool accumulate = false);

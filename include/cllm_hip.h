@@ -125,6 +125,25 @@ int cllm_hip_gemv_q8_swiglu_dev(uint32_t type, int in_dim, int n_ff, const void*
                                 int n_rows, const int8_t* qs, const float* scales,
                                 const int32_t* bsums, float* h, void* stream);
 
+/* The RMSNorm before the q, k and v projections and the projections in one launch, for one
+ * activation row (decode): rms_norm_ptr(x, norm_w, eps) (src/core/engine.cpp:23-28, 475),
+ * its Q8_0 quantization and cllm_hip_gemv_q8_multi_dev on it (476-478). x and norm_w are
+ * in_dim fp32 values on the device, in_dim a multiple of 32 up to 4096. The outputs are
+ * bit-identical to cllm_hip_rmsnorm_q8_0_dev followed by cllm_hip_gemv_q8_multi_dev. */
+int cllm_hip_rmsnorm_gemv_multi_dev(uint32_t type, int in_dim, int n_mats, const void* const* w,
+                                    const int* out_dims, const float* const* bias,
+                                    float* const* y, const float* x, const float* norm_w,
+                                    float eps, void* stream);
+
+/* The RMSNorm before the feed-forward and cllm_hip_gemv_q8_swiglu_dev on its output in one
+ * launch, for one activation row (src/core/engine.cpp:23-28, 508-512); same limits as
+ * cllm_hip_rmsnorm_gemv_multi_dev, bit-identical to cllm_hip_rmsnorm_q8_0_dev followed by
+ * cllm_hip_gemv_q8_swiglu_dev. */
+int cllm_hip_rmsnorm_gemv_swiglu_dev(uint32_t type, int in_dim, int n_ff, const void* w_gate,
+                                     const void* w_up, const float* bias_gate,
+                                     const float* bias_up, const float* x, const float* norm_w,
+                                     float eps, float* h, void* stream);
+
 /* cllm_hip_gemv_q8_dev fused with the residual add that follows the matmul in the engine
  * (x += mm(...), src/core/engine.cpp:505-506, 512-513): y[t, j] += vec_dot_row(...)
  * (+ bias[j]), so y holds the residual stream on entry. Always the GEMV kernels (meant for

@@ -165,14 +165,20 @@ class DeviceModel:
         up = torch.empty((T, self.n_ff), device="cuda")
         for l in range(self.n_layers):
             p = f"blk.{l}."
-            h, qs, sc, bs = C.rmsnorm_q8_0_dev(x, self.w[p + "attn_norm.weight"], self.eps)
             kc = self.k_cache[l][pos0:pos0 + T]
             vc = self.v_cache[l][pos0:pos0 + T]
             biases = None
             if p + "attn_q.bias" in self.w:
                 biases = [self.w[p + "attn_q.bias"], self.w[p + "attn_k.bias"], self.w[p + "attn_v.bias"]]
-            self._linear([p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"],
-                         [q, kc, vc], h, (qs, sc, bs), biases)
+            qkv = [p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"]
+            if self._norm_fusable(T, qkv):  # attn_norm rides in the q/k/v launch
+                C.rmsnorm_gemv_multi_dev(x, self.w[p + "attn_norm.weight"], self.eps,
+                                         [self.w[n] for n in qkv], self._type(qkv[0]), self.n_embd,
+                                         [self.q_dim, self.kv_dim, self.kv_dim], ys=[q, kc, vc],
+                                         biases=biases)
+            else:
+                h, qs, sc, bs = C.rmsnorm_q8_0_dev(x, self.w[p + "attn_norm.weight"], self.eps)
+                self._linear(qkv, [q, kc, vc], h, (qs, sc, bs), biases)
             if p + "attn_q_norm.weight" in self.w:  # Qwen3 per-head norms, in place
                 qv = q.view(T * self.n_head, self.hd)
                 self._norm_inplace(qv, self.w[p + "attn_q_norm.weight"])
@@ -188,9 +194,16 @@ class DeviceModel:
             wo = p + "attn_output.weight"
             C.matmul_quant_residual_dev(attn, self.w[wo], self._type(wo), None, self.q_dim,
                                         self.n_embd, x)
-            h, qs, sc, bs = C.rmsnorm_q8_0_dev(x, self.w[p + "ffn_norm.weight"], self.eps)
             wg, wu, wd = p + "ffn_gate.weight", p + "ffn_up.weight", p + "ffn_down.weight"
             tg = self._type(wg)
+            if self._norm_fusable(T, [wg, wu]) and C.has_vec_dot(self._type(wd)):
+                # ffn_norm, gate, up and the SwiGLU in one launch
+                C.rmsnorm_gemv_swiglu_dev(x, self.w[p + "ffn_norm.weight"], self.eps, self.w[wg],
+                                          self.w[wu], tg, self.n_embd, self.n_ff, h=gate)
+                C.matmul_quant_residual_dev(gate, self.w[wd], self._type(wd), None, self.n_ff,
+                                            self.n_embd, x)
+                continue
+            h, qs, sc, bs = C.rmsnorm_q8_0_dev(x, self.w[p + "ffn_norm.weight"], self.eps)
             if T < 16 and tg == self._type(wu) and C.has_vec_dot(tg) and C.has_vec_dot(self._type(wd)):
                 # gate, up and the SwiGLU in one launch; the down GEMV quantizes h itself and
                 # adds the residual
@@ -208,6 +221,13 @@ class DeviceModel:
         out = torch.empty((1, self.vocab), device="cuda")
         self._linear(["output.weight"], [out], h, (qs, sc, bs))
         return out
+
+    def _norm_fusable(self, T, names):
+        """One decode row, matrices of one vec_dot type, and a row the fused RMSNorm staging
+        takes (a multiple of 32 up to 4096 elements)."""
+        types = {self._type(n) for n in names}
+        return (T == 1 and len(types) == 1 and self.C.has_vec_dot(next(iter(types)))
+                and self.n_embd <= 4096 and self.n_embd % 32 == 0)
 
     def _norm_inplace(self, rows, w):
         lib = self.C.load_library()

@@ -182,6 +182,57 @@ def test_gemv_swiglu_equals_projections_then_swiglu(gpu, qt, m, n_ff, k):
         assert np.array_equal(bits(h.cpu().numpy()), bits(h_ref.cpu().numpy())), with_bias
 
 
+@pytest.mark.parametrize("qt,k,dims,with_bias", [
+    (S.Q4_K, 4096, (4096, 1024, 1024), False), (S.Q6_K, 2048, (512, 256), False),
+    (S.Q8_0, 896, (896, 128, 128), True), (S.Q5_0, 4096, (300,), True),
+    (S.Q4_0, 1024, (1000, 24), False), (S.Q5_K, 3072, (3072, 1024, 1024), True)])
+def test_rmsnorm_gemv_equals_rmsnorm_then_gemv(gpu, qt, k, dims, with_bias):
+    """The RMSNorm inside the GEMV's staging (q/k/v after attn_norm) gives the bits of the
+    RMSNorm producer followed by the GEMV on its Q8_0 rows: the staging reduces the sum of
+    squares in the producer's order. Row lengths below 4096 and not a multiple of 256 (the
+    producer's idle threads) included."""
+    rng = np.random.default_rng(qt + 500 + k)
+    ws = [_dev(S.make_weight(qt, n, k, 50 + i)) for i, n in enumerate(dims)]
+    x = _dev((3.0 * rng.standard_normal((1, k))).astype(np.float32))
+    nw = _dev((1 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    biases = [_dev(rng.standard_normal(n).astype(np.float32)) for n in dims] if with_bias else None
+    print("rmsnorm gemv", S.TYPE_NAMES[qt], k, dims, with_bias, flush=True)
+    _, qs, sc, bs = gpu.rmsnorm_q8_0_dev(x, nw, 1e-5, h=False)
+    ref = gpu.gemv_q8_multi_dev(ws, qt, k, dims, qs, sc, bs, biases=biases)
+    got = gpu.rmsnorm_gemv_multi_dev(x, nw, 1e-5, ws, qt, k, dims, biases=biases)
+    for g, r in zip(got, ref):
+        assert np.array_equal(bits(g.cpu().numpy()), bits(r.cpu().numpy()))
+
+
+@pytest.mark.parametrize("qt,k,n_ff", [(S.Q4_K, 4096, 14336), (S.Q8_0, 896, 4864),
+                                       (S.Q6_K, 1024, 3000)])
+def test_rmsnorm_gemv_swiglu_equals_rmsnorm_then_swiglu_gemv(gpu, qt, k, n_ff):
+    """ffn_norm, gate, up and their SwiGLU in one launch give the bits of the RMSNorm producer
+    followed by the SwiGLU GEMV."""
+    rng = np.random.default_rng(qt + 600 + k)
+    wg = _dev(S.make_weight(qt, n_ff, k, 60))
+    wu = _dev(S.make_weight(qt, n_ff, k, 61))
+    x = _dev((0.02 * rng.standard_normal((1, k))).astype(np.float32))
+    nw = _dev((1 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    print("rmsnorm swiglu gemv", S.TYPE_NAMES[qt], k, n_ff, flush=True)
+    _, qs, sc, bs = gpu.rmsnorm_q8_0_dev(x, nw, 1e-6, h=False)
+    ref = gpu.gemv_q8_swiglu_dev(wg, wu, qt, k, n_ff, qs, sc, bs)
+    got = gpu.rmsnorm_gemv_swiglu_dev(x, nw, 1e-6, wg, wu, qt, k, n_ff)
+    assert np.array_equal(bits(got.cpu().numpy()), bits(ref.cpu().numpy()))
+
+
+def test_rmsnorm_gemv_argument_errors(gpu):
+    """Rows longer than 4096, or not a multiple of 32, are refused before any launch."""
+    k = 8192
+    w = _dev(S.make_weight(S.Q8_0, 64, k, 62))
+    x = _dev(np.ones((1, k), np.float32))
+    nw = _dev(np.ones(k, np.float32))
+    with pytest.raises(Exception, match="rms_norm"):
+        gpu.rmsnorm_gemv_multi_dev(x, nw, 1e-5, [w], S.Q8_0, k, [64])
+    with pytest.raises(Exception, match="rms_norm"):
+        gpu.rmsnorm_gemv_swiglu_dev(x, nw, 1e-5, w, w, S.Q8_0, k, 64)
+
+
 @pytest.mark.parametrize("qt,m", [(S.Q4_K, 1), (S.Q6_K, 2), (S.Q8_0, 5), (S.Q4_K, 20), (S.F16, 1),
                                   (S.Q3_K, 3)])
 def test_matmul_residual_equals_matmul_then_add(gpu, qt, m):
