@@ -344,7 +344,14 @@ __global__ __launch_bounds__(kThreads) void k_attention(
 #pragma unroll
             for (int u = 0; u < 16; ++u) num = __builtin_fmaf(wz[r][zz + u], v[u], num);
         }
-        for (; zz < S; ++zz) num = __builtin_fmaf(wz[r][zz], ld(pp + (size_t)zz * (HD + 2)), num);
+        if (zz < S) {  // the last S % 16, also loaded together (one round trip, same order)
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) v[u] = zz + u < S ? ld(pp + (size_t)(zz + u) * (HD + 2)) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (zz + u < S) num = __builtin_fmaf(wz[r][zz + u], v[u], num);
+        }
         out[((size_t)t * n_head + kvh * n_rep + r) * HD + d] = __fdiv_rn(num, lsum[r]);
     }
 }
