@@ -65,6 +65,7 @@ def _attn_ref(q, kc, vc, pos0, n_head, n_kv, hd):
 
 
 @pytest.mark.parametrize("hd,n_head,n_kv,rows,pos0", [(128, 32, 8, 1, 0), (128, 32, 8, 1, 4095),
+                                                      (128, 32, 8, 1, 1500),
                                                       (128, 32, 8, 7, 300), (64, 14, 2, 1, 1000),
                                                       (64, 16, 16, 33, 0), (256, 8, 1, 2, 129),
                                                       (128, 40, 8, 64, 64)])
