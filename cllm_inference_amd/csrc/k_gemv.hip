@@ -573,8 +573,10 @@ struct StageCopy {
 // wave sum, then the 16 wave sums in order), so h and its blocks are bit-identical to that
 // kernel's: thread t holds chunks 2t and 2t + 1, and their sum followed by butterflies over
 // 2, 4, .., 32 lanes adds the same pairs of values as that kernel's wave sum (float addition
-// is commutative), leaving its wave sums 2w and 2w + 1 in lanes 0 and 32 of wave w.
-template <uint32_t T, int MR, bool NORM = false>
+// is commutative), leaving its wave sums 2w and 2w + 1 in lanes 0 and 32 of wave w; waves
+// past the eighth hold no elements. RAWBAR: the workgroup barrier waits for LDS writes only
+// (k_gemv_st, whose LDS-DMA weight loads a fenced barrier would wait for too).
+template <uint32_t T, int MR, bool NORM = false, bool RAWBAR = false>
 struct StageQuant {
     using Tr = typename TraitsOf<T>::type;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -688,8 +690,13 @@ struct StageQuant {
         s += dpp_f32<DPP_ROW_HALF_MIRROR>(s);
         s += dpp_f32<DPP_ROW_MIRROR>(s);
         s += __shfl_xor(s, 16, 64);
-        if ((threadIdx.x & 31) == 0) part[threadIdx.x >> 5] = s;
-        lds_barrier();
+        if ((threadIdx.x & 31) == 0 && (threadIdx.x >> 5) < 16) part[threadIdx.x >> 5] = s;
+        if constexpr (RAWBAR) {
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            asm volatile("s_barrier" ::: "memory");
+        } else {
+            lds_barrier();
+        }
         float sum = 0.0f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) sum += part[i];
@@ -953,7 +960,7 @@ __device__ __forceinline__ void dma16(const void* g, const uint8_t* lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(g), "s"(m0) : "memory", "m0");
 }
 
-template <uint32_t T, int MR, int S, int WV>
+template <uint32_t T, int MR, int S, int WV, bool NORM = false>
 __global__ __launch_bounds__(64 * WV) void k_gemv_st(GemvSegs sg, int64_t row_bytes, int k, int n,
                                                      const int8_t* __restrict__ qs,
                                                      const float* __restrict__ xs,
@@ -1003,8 +1010,15 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_st(GemvSegs sg, int64_t row_by
 
     const ActLds a = act_layout<T, MR>(lds, k);
     StageCopy<T, MR> sc{qs, xs, xb, k, {}, {}, {}};
-    StageQuant<T, MR> sq{x_f32, k, {}};
-    const bool fused = x_f32 != nullptr;
+    StageQuant<T, MR, NORM, true> sq{x_f32, k, {}};
+    static_assert(!NORM || MR == 1, "the RMSNorm staging takes one row");
+    __shared__ float norm_part[16];
+    if constexpr (NORM) {
+        sq.nw = sg.norm_w;
+        sq.eps = sg.eps;
+        sq.part = norm_part;
+    }
+    const bool fused = NORM || x_f32 != nullptr;
     if (fused)
         sq.issue();
     else
@@ -1157,7 +1171,7 @@ static int64_t resident_waves(size_t shmem) {
 // cold HBM, fused quantization: the Q6_K 128256x4096 head 72 us against 73-78 us for 8-wave
 // workgroups at 3-4 per CU and 78-81 us with two slots; the register-ring k_gemv 81-88 us on
 // the same boxes). Grid: the workgroups resident at once, or fewer if the rows run out.
-template <uint32_t T, int S, int WV>
+template <uint32_t T, int S, int WV, bool NORM = false>
 static int64_t resident_st_wgs(size_t shmem) {
     static std::atomic<uint64_t> cache{0};
     uint64_t c = cache.load(std::memory_order_relaxed);
@@ -1166,7 +1180,7 @@ static int64_t resident_st_wgs(size_t shmem) {
         blocks = (int)(c & 0xFFFFu);
     } else {
         blocks = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv_st<T, 1, S, WV>),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(&k_gemv_st<T, 1, S, WV, NORM>),
                                                          64 * WV, shmem) != hipSuccess ||
             blocks < 1)
             blocks = 1;
@@ -1175,14 +1189,14 @@ static int64_t resident_st_wgs(size_t shmem) {
     return (int64_t)blocks * cu_count();
 }
 
-template <uint32_t T, int S, int WV>
+template <uint32_t T, int S, int WV, bool NORM = false>
 static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
                             const int32_t* xb, const float* x_f32, int accumulate, int64_t items,
                             hipStream_t stream) {
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
     const size_t shmem = act_lds_bytes<T>(1, k);
-    const int64_t grid = std::min((items + WV - 1) / WV, resident_st_wgs<T, S, WV>(shmem));
-    hipLaunchKernelGGL((k_gemv_st<T, 1, S, WV>), dim3((unsigned)grid), dim3(64 * WV), shmem,
+    const int64_t grid = std::min((items + WV - 1) / WV, resident_st_wgs<T, S, WV, NORM>(shmem));
+    hipLaunchKernelGGL((k_gemv_st<T, 1, S, WV, NORM>), dim3((unsigned)grid), dim3(64 * WV), shmem,
                        stream, sg, row_bytes, k, n, qs, xs, xb, x_f32, accumulate);
     return hipGetLastError();
 }
@@ -1196,6 +1210,18 @@ static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, 
 // took 12.8 / 15.4 / 13.7 us with 2 / 3 / 4 slots.
 template <uint32_t T>
 constexpr int64_t staged_min_bytes() { return T == T_Q6_K ? 32ll << 20 : T == T_Q4_K ? 96ll << 20 : INT64_MAX; }
+
+// One activation row over a long Q6_K / Q4_K stream takes the staged kernel (Q4_K's LDS field
+// reads are whole 16-byte pieces: its rows must start 16-byte aligned).
+template <uint32_t T>
+static bool use_staged(const GemvSegs& sg, int k, int n) {
+    if constexpr (T != T_Q6_K && T != T_Q4_K) return false;
+    const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
+    bool aligned = true;
+    if constexpr (T == T_Q4_K)
+        for (int i = 0; i < 3; ++i) aligned = aligned && ((uintptr_t)sg.w[i] & 15u) == 0;
+    return bytes >= staged_min_bytes<T>() && aligned && act_lds_bytes<T>(1, k) <= 64 * 1024;
+}
 
 template <uint32_t T, int MR, int P, bool SW, bool NORM = false>
 static hipError_t launch_t(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
@@ -1232,22 +1258,20 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
     const GemvTuning& tu = gemv_tuning();
     const size_t shmem = act_lds_bytes<T>(MR, k);
     if constexpr (MR == 1) {
-        if (sg.norm_w) {  // the RMSNorm rides in the staging (one row, a ring of one)
+        if (sg.norm_w) {  // the RMSNorm rides in the staging (one row)
+            if constexpr ((T == T_Q6_K || T == T_Q4_K) && !SW)
+                if (use_staged<T>(sg, k, n))
+                    return launch_st<T, 1, 16, true>(sg, k, n, qs, xs, xb, x_f32, accumulate, items,
+                                                     stream);
             const int64_t waves =
                 std::min({items, simds * tu.short_wps, resident_waves<T, 1, 1, SW, true>(shmem)});
             return launch_t<T, 1, 1, SW, true>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves,
                                                stream);
         }
     }
-    if constexpr ((T == T_Q6_K || T == T_Q4_K) && MR == 1 && !SW) {
-        // (Q4_K's LDS field reads are whole 16-byte pieces: its rows must start 16-byte aligned)
-        const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
-        bool aligned = true;
-        if constexpr (T == T_Q4_K)
-            for (int i = 0; i < 3; ++i) aligned = aligned && ((uintptr_t)sg.w[i] & 15u) == 0;
-        if (bytes >= staged_min_bytes<T>() && aligned && act_lds_bytes<T>(1, k) <= 64 * 1024)
+    if constexpr ((T == T_Q6_K || T == T_Q4_K) && MR == 1 && !SW)
+        if (use_staged<T>(sg, k, n))
             return launch_st<T, 1, 16>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
-    }
     if (MR > 2 && items > simds * 32) {
         const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2, SW>(shmem));
         return launch_t<T, MR, 2, SW>(sg, k, n, qs, xs, xb, x_f32, accumulate, (int)waves, stream);

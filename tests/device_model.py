@@ -217,8 +217,14 @@ class DeviceModel:
                 self._linear([wd], [x], hs, (qs, sc, bs), residual=True)
         if not logits:
             return None
-        h, qs, sc, bs = C.rmsnorm_q8_0_dev(x[T - 1:T].contiguous(), self.w["output_norm.weight"], self.eps)
+        xl = x[T - 1:T].contiguous()
         out = torch.empty((1, self.vocab), device="cuda")
+        if self._norm_fusable(1, ["output.weight"]):  # output_norm rides in the head GEMV
+            C.rmsnorm_gemv_multi_dev(xl, self.w["output_norm.weight"], self.eps,
+                                     [self.w["output.weight"]], self._type("output.weight"),
+                                     self.n_embd, [self.vocab], ys=[out])
+            return out
+        h, qs, sc, bs = C.rmsnorm_q8_0_dev(xl, self.w["output_norm.weight"], self.eps)
         self._linear(["output.weight"], [out], h, (qs, sc, bs))
         return out
 

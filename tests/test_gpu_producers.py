@@ -185,12 +185,14 @@ def test_gemv_swiglu_equals_projections_then_swiglu(gpu, qt, m, n_ff, k):
 @pytest.mark.parametrize("qt,k,dims,with_bias", [
     (S.Q4_K, 4096, (4096, 1024, 1024), False), (S.Q6_K, 2048, (512, 256), False),
     (S.Q8_0, 896, (896, 128, 128), True), (S.Q5_0, 4096, (300,), True),
-    (S.Q4_0, 1024, (1000, 24), False), (S.Q5_K, 3072, (3072, 1024, 1024), True)])
+    (S.Q4_0, 1024, (1000, 24), False), (S.Q5_K, 3072, (3072, 1024, 1024), True),
+    # streams long enough for the LDS-staged kernel (40 MB of Q6_K, 99 MB of Q4_K)
+    (S.Q6_K, 4096, (12000,), False), (S.Q4_K, 4096, (43000,), True)])
 def test_rmsnorm_gemv_equals_rmsnorm_then_gemv(gpu, qt, k, dims, with_bias):
     """The RMSNorm inside the GEMV's staging (q/k/v after attn_norm) gives the bits of the
     RMSNorm producer followed by the GEMV on its Q8_0 rows: the staging reduces the sum of
     squares in the producer's order. Row lengths below 4096 and not a multiple of 256 (the
-    producer's idle threads) included."""
+    producer's idle threads) included, and streams that take the LDS-staged kernel."""
     rng = np.random.default_rng(qt + 500 + k)
     ws = [_dev(S.make_weight(qt, n, k, 50 + i)) for i, n in enumerate(dims)]
     x = _dev((3.0 * rng.standard_normal((1, k))).astype(np.float32))
