@@ -56,12 +56,16 @@ SIGNATURES = {
     "cllm_hip_vec_dot_rows": (_I, [_P, _U, _I64, _I, _P, _P, _P, _P]),
     "cllm_hip_matmul_quant": (_I, [_P, _P, _U, _P, _I, _I, _P]),
     "cllm_hip_matmul_quant_batch": (_I, [_P, _P, _U, _P, _I, _I, _I, _P]),
+    "cllm_hip_dequantize_block": (_I, [_P, _P, _U, _I64]),
+    "cllm_hip_dequantize_block_f16": (_I, [_P, _P, _U, _I64]),
     "cllm_hip_register_weights": (_I, [_P, _SZ]),
     "cllm_hip_unregister_weights": (_I, [_P]),
     "cllm_hip_quantize_q8_0_dev": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_matmul_quant_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
     "cllm_hip_matmul_route": (ctypes.c_char_p, [_U, _I, _I, _I]),
+    "cllm_hip_matmul_plan": (ctypes.c_char_p, [_U, _I, _I, _I]),
+    "cllm_hip_tune": (_I, [ctypes.c_char_p, _P, _I]),
     "cllm_hip_rmsnorm_q8_0_dev": (_I, [_P, _P, ctypes.c_float, _I, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_swiglu_q8_0_dev": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_add_dev": (_I, [_P, _P, _I64, _P]),
@@ -206,6 +210,30 @@ def matmul_quant_batch(x: np.ndarray, w: np.ndarray, t: int, bias: np.ndarray | 
     return y
 
 
+def _src_ptr(src):
+    """A host array's address, a torch tensor's device address, or an int address as it is."""
+    if isinstance(src, np.ndarray):
+        return _ptr(src)
+    if hasattr(src, "data_ptr"):
+        return ctypes.c_void_p(src.data_ptr())
+    return ctypes.c_void_p(int(src))
+
+
+def dequantize_block(src, t: int, n: int) -> np.ndarray:
+    """The first n elements of the blocks at src as float32 -- reference quant.hpp:99. src is a
+    uint8 host array, a device tensor, or a raw address (host or device)."""
+    out = np.empty(max(int(n), 0), np.float32)
+    _check(load_library().cllm_hip_dequantize_block(_src_ptr(src), _ptr(out), int(t), int(n)))
+    return out
+
+
+def dequantize_block_f16(src, t: int, n: int) -> np.ndarray:
+    """The same values as binary16 bits (uint16) -- reference quant.hpp:105."""
+    out = np.empty(max(int(n), 0), np.uint16)
+    _check(load_library().cllm_hip_dequantize_block_f16(_src_ptr(src), _ptr(out), int(t), int(n)))
+    return out
+
+
 # ---- device (torch) entry points --------------------------------------------------------
 
 def _tp(t):
@@ -346,6 +374,19 @@ def matmul_quant_residual_dev(x, w, t: int, bias, in_dim: int, out_dim: int, y):
 def matmul_route(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:
     return load_library().cllm_hip_matmul_route(int(t), int(in_dim), int(out_dim),
                                                 int(n_rows)).decode()
+
+
+def matmul_plan(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:
+    """The kernel instantiation and split count the batch would run (or the route name)."""
+    return load_library().cllm_hip_matmul_plan(int(t), int(in_dim), int(out_dim),
+                                               int(n_rows)).decode()
+
+
+def tune(knob: str, *values: int) -> None:
+    """Sets a process-wide kernel-choice override (cllm_hip_tune); no values resets it."""
+    arr = (ctypes.c_int * max(len(values), 1))(*[int(v) for v in values])
+    _check(load_library().cllm_hip_tune(knob.encode(), ctypes.cast(arr, ctypes.c_void_p),
+                                        len(values)))
 
 
 # ---- producers of a device-resident layer ------------------------------------------------

@@ -15,6 +15,7 @@
 #include <memory>
 #include <barrier>
 #include <mutex>
+#include <set>
 #include <thread>
 #include <vector>
 #include <string>
@@ -75,51 +76,119 @@ struct DevBuf {
     }
 };
 
-// Activation workspace: the Q8_0 batch qs[m*k] | scales[m*k/32] | bsums[m*k/32], and the
-// MFMA paths' qh[m*k] (fp16) | px[m*k/32] (dx * bsum) | xq[m*k/8] (dx * bsum as bf16 parts).
-struct Workspace {
-    DevBuf buf;
-    DevBuf part;  // split-K partial sums of the weight-row GEMM
-    DevBuf att;   // sequence-split partials of the attention kernel
-    DevBuf tmp;   // matmul result before a residual add the kernel cannot fuse
+// The scratch one matmul call uses, as plain device pointers: the Q8_0 batch qs[m*k] |
+// scales[m*k/32] | bsums[m*k/32], the MFMA paths' qh[m*k] (fp16) | px[m*k/32] (dx * bsum) |
+// xq[m*k/8] (dx * bsum as bf16 parts), and the weight-row GEMM's split-K region (tile
+// counters that must be zero when a launch starts, then the partial sums).
+struct WsView {
     int8_t* qs = nullptr;
     float* sc = nullptr;
     int32_t* bs = nullptr;
     _Float16* qh = nullptr;
     float* px = nullptr;
     uint16_t* xq = nullptr;
+    float* part = nullptr;
+    size_t part_cap = 0;
+};
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Bytes of the activation arrays of a k x m batch, and their places from base p.
+size_t act_bytes(int k, int m) {
+    const size_t n = (size_t)k * (size_t)m;
+    return round256(n) + 3 * round256((n / 32) * 4) + round256(2 * n) + round256(n / 4);
+}
+void carve_act(char* p, int k, int m, WsView& v) {
+    const size_t n = (size_t)k * (size_t)m;
+    const size_t qs_bytes = round256(n), sc_bytes = round256((n / 32) * 4), qh_bytes = round256(2 * n);
+    v.qs = (int8_t*)p;
+    v.sc = (float*)(p + qs_bytes);
+    v.bs = (int32_t*)(p + qs_bytes + sc_bytes);
+    v.px = (float*)(p + qs_bytes + 2 * sc_bytes);
+    v.qh = (_Float16*)(p + qs_bytes + 3 * sc_bytes);
+    v.xq = (uint16_t*)(p + qs_bytes + 3 * sc_bytes + qh_bytes);
+}
+
+// A growable workspace of the library's own (per device stream, or per device for the host
+// entry points).
+struct Workspace {
+    DevBuf buf;
+    DevBuf part;  // split-K partial sums of the weight-row GEMM
+    DevBuf att;   // sequence-split partials of the attention kernel
+    DevBuf tmp;   // matmul result before a residual add the kernel cannot fuse
+    WsView v;
     hipError_t ensure(int k, int m, hipStream_t stream) {
-        const size_t n = (size_t)k * (size_t)m;
-        const size_t qs_bytes = (n + 255) & ~(size_t)255;
-        const size_t sc_bytes = ((n / 32) * 4 + 255) & ~(size_t)255;
-        const size_t qh_bytes = (2 * n + 255) & ~(size_t)255;
-        const size_t xq_bytes = (n / 4 + 255) & ~(size_t)255;
-        hipError_t e = buf.ensure(qs_bytes + 3 * sc_bytes + qh_bytes + xq_bytes, stream);
+        hipError_t e = buf.ensure(act_bytes(k, m), stream);
         if (e != hipSuccess) return e;
-        char* p = (char*)buf.p;
-        qs = (int8_t*)p;
-        sc = (float*)(p + qs_bytes);
-        bs = (int32_t*)(p + qs_bytes + sc_bytes);
-        px = (float*)(p + qs_bytes + 2 * sc_bytes);
-        qh = (_Float16*)(p + qs_bytes + 3 * sc_bytes);
-        xq = (uint16_t*)(p + qs_bytes + 3 * sc_bytes + qh_bytes);
+        carve_act((char*)buf.p, k, m, v);
         return hipSuccess;
     }
-    // The weight-row GEMM's split-K workspace; a new allocation is zeroed (its tile counters
+    // The weight-row GEMM's split-K region; a new allocation is zeroed (its tile counters
     // must start at zero; every launch leaves them zero).
     hipError_t ensure_part(size_t bytes, hipStream_t stream) {
+        if (bytes == 0) return hipSuccess;
         const void* before = part.p;
         hipError_t e = part.ensure(bytes, stream);
-        if (e != hipSuccess || part.p == before) return e;
-        return gemmw_workspace_init(part.p, part.cap, stream);
+        if (e != hipSuccess) return e;
+        if (part.p != before) e = gemmw_workspace_init(part.p, part.cap, stream);
+        v.part = (float*)part.p;
+        v.part_cap = part.cap;
+        return e;
     }
 };
 
+// A host address range whose bytes have a device copy. Automatic regions are read-only file
+// mappings found by resolve_weights; they carry the mapping's identity, so a range that was
+// unmapped (and perhaps mapped again with other contents) is noticed and dropped.
 struct Region {
     size_t bytes;
     void* dev;    // device address of the region's first byte
     void* alloc;  // the allocation to free
+    bool automatic = false;
+    uint64_t file_off = 0, inode = 0;
+    char fdev[16] = {};
 };
+
+// One line of /proc/self/maps.
+struct Mapping {
+    uintptr_t lo = 0, hi = 0;
+    char perms[8] = {};
+    uint64_t off = 0, inode = 0;
+    char dev[16] = {};
+    bool file = false;  // has a path name
+};
+
+// The mapping of this process that holds address p.
+bool find_mapping(uintptr_t p, Mapping& m) {
+    FILE* f = std::fopen("/proc/self/maps", "r");
+    if (!f) return false;
+    char line[4096];
+    bool found = false;
+    while (!found && std::fgets(line, sizeof line, f)) {
+        unsigned long lo = 0, hi = 0, off = 0, ino = 0;
+        char perms[8] = {}, dev[16] = {};
+        int pos = 0;
+        if (std::sscanf(line, "%lx-%lx %7s %lx %15s %lu %n", &lo, &hi, perms, &off, dev, &ino, &pos) < 6)
+            continue;
+        if (p < lo || p >= hi) continue;
+        m.lo = lo;
+        m.hi = hi;
+        std::memcpy(m.perms, perms, sizeof m.perms);
+        m.off = off;
+        m.inode = ino;
+        std::memcpy(m.dev, dev, sizeof m.dev);
+        m.file = pos > 0 && line[pos] == '/';
+        found = true;
+    }
+    std::fclose(f);
+    return found;
+}
+
+// A private, read-only mapping of a file: what GgufLoader maps (gguf.cpp:178). Its bytes
+// cannot change through the mapping, so one device copy serves every later call.
+bool immutable_file_mapping(const Mapping& m) {
+    return m.file && m.perms[0] == 'r' && m.perms[1] == '-' && m.perms[3] == 'p' && m.inode != 0;
+}
 
 struct DeviceState {
     std::mutex mtx;
@@ -127,6 +196,7 @@ struct DeviceState {
     DevBuf x, y, bias, wstage, qin;
     Workspace act;
     std::map<uintptr_t, Region> regions;  // host base -> device copy
+    std::set<uintptr_t> no_auto;          // mappings too large to copy to the device
     std::map<hipStream_t, std::unique_ptr<Workspace>> dev_ws;
 };
 
@@ -134,6 +204,8 @@ std::mutex g_states_mtx;
 std::map<int, std::unique_ptr<DeviceState>> g_states;
 
 int current_device() { return g_device < 0 ? 0 : g_device; }
+
+Tuning g_tuning;
 
 // Makes the calling thread's device current and returns its state (created on first use).
 int acquire(DeviceState** out) {
@@ -190,19 +262,111 @@ bool is_device_ptr(const void* p) {
     return attr.type == hipMemoryTypeDevice;
 }
 
-// Device address of `bytes` of weights at host/device pointer w. Registered regions resolve
-// by offset; device pointers pass through; anything else is copied into a staging buffer.
-int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t** dev) {
-    const uintptr_t a = (uintptr_t)w;
+// Copies [a, a + bytes) of host memory to a new device allocation. The copy keeps the host
+// base's offset modulo 256, so host pointers that are 16-byte aligned stay 16-byte aligned on
+// the device. On failure nothing is left allocated.
+int upload_region(DeviceState* st, uintptr_t a, size_t bytes, Region* out) {
+    const size_t lead = a & 255u;
+    void* mem = nullptr;
+    hipError_t e = hipMalloc(&mem, bytes + lead);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_err(CLLM_HIP_E_RUNTIME, "cllm_hip: cannot allocate %zu bytes for weights: %s",
+                       bytes, hipGetErrorString(e));
+    }
+    e = hipMemcpyAsync((char*)mem + lead, (const void*)a, bytes, hipMemcpyHostToDevice, st->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(mem);
+        return set_err(CLLM_HIP_E_RUNTIME, "cllm_hip: weight upload failed: %s", hipGetErrorString(e));
+    }
+    *out = Region{bytes, (char*)mem + lead, mem};
+    return CLLM_HIP_OK;
+}
+
+// Every line of /proc/self/maps.
+std::vector<Mapping> all_mappings() {
+    std::vector<Mapping> out;
+    FILE* f = std::fopen("/proc/self/maps", "r");
+    if (!f) return out;
+    char line[4096];
+    while (std::fgets(line, sizeof line, f)) {
+        unsigned long lo = 0, hi = 0, off = 0, ino = 0;
+        char perms[8] = {}, dev[16] = {};
+        int pos = 0;
+        if (std::sscanf(line, "%lx-%lx %7s %lx %15s %lu %n", &lo, &hi, perms, &off, dev, &ino, &pos) < 6)
+            continue;
+        Mapping m;
+        m.lo = lo;
+        m.hi = hi;
+        std::memcpy(m.perms, perms, sizeof m.perms);
+        m.off = off;
+        m.inode = ino;
+        std::memcpy(m.dev, dev, sizeof m.dev);
+        m.file = pos > 0 && line[pos] == '/';
+        out.push_back(m);
+    }
+    std::fclose(f);
+    return out;
+}
+
+// An automatic region is still backed by the read-only file mapping it was copied from.
+bool same_mapping(uintptr_t base, const Region& r, const Mapping& m) {
+    return m.lo == base && m.hi - m.lo == r.bytes && m.inode == r.inode && m.off == r.file_off &&
+           std::strcmp(m.dev, r.fdev) == 0 && immutable_file_mapping(m);
+}
+
+// Frees the automatic regions whose file mappings are gone (the caller unmapped the file).
+int prune_auto_regions(DeviceState* st) {
+    const std::vector<Mapping> maps = all_mappings();
+    for (auto it = st->regions.begin(); it != st->regions.end();) {
+        bool live = !it->second.automatic;
+        for (const Mapping& m : maps)
+            if (!live && same_mapping(it->first, it->second, m)) live = true;
+        if (live) {
+            ++it;
+            continue;
+        }
+        HIP_TRY(hipStreamSynchronize(st->stream));
+        HIP_TRY(hipFree(it->second.alloc));
+        it = st->regions.erase(it);
+    }
+    return CLLM_HIP_OK;
+}
+
+// The device copy of [a, a + bytes) if a registered region holds it (null if none). An
+// automatic region is checked against the current mapping first, and dropped if the file it
+// was copied from is no longer mapped there.
+int lookup_region(DeviceState* st, uintptr_t a, size_t bytes, const uint8_t** dev) {
+    *dev = nullptr;
     auto it = st->regions.upper_bound(a);
-    if (it != st->regions.begin()) {
-        --it;
-        if (a >= it->first && a + bytes <= it->first + it->second.bytes) {
-            *dev = (const uint8_t*)it->second.dev + (a - it->first);
-            if (!aligned16(*dev))
-                return set_err(CLLM_HIP_E_ARG, "cllm_hip: weight pointer is not 16-byte aligned");
+    if (it == st->regions.begin()) return CLLM_HIP_OK;
+    --it;
+    if (a < it->first || a + bytes > it->first + it->second.bytes) return CLLM_HIP_OK;
+    if (it->second.automatic) {
+        Mapping m;
+        if (!find_mapping(a, m) || !same_mapping(it->first, it->second, m)) {
+            HIP_TRY(hipStreamSynchronize(st->stream));
+            HIP_TRY(hipFree(it->second.alloc));
+            st->regions.erase(it);
             return CLLM_HIP_OK;
         }
+    }
+    *dev = (const uint8_t*)it->second.dev + (a - it->first);
+    return CLLM_HIP_OK;
+}
+
+// Device address of `bytes` of weights at host/device pointer w. Registered regions resolve
+// by offset; device pointers pass through; a read-only file mapping is copied to the device
+// once; anything else is copied into a staging buffer.
+int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t** dev) {
+    const uintptr_t a = (uintptr_t)w;
+    int rc;
+    if ((rc = lookup_region(st, a, bytes, dev))) return rc;
+    if (*dev) {
+        if (!aligned16(*dev))
+            return set_err(CLLM_HIP_E_ARG, "cllm_hip: weight pointer is not 16-byte aligned");
+        return CLLM_HIP_OK;
     }
     if (is_device_ptr(w)) {
         if (!aligned16(w))
@@ -210,9 +374,86 @@ int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t*
         *dev = (const uint8_t*)w;
         return CLLM_HIP_OK;
     }
+    // Weights inside a read-only private file mapping (the engine's mmap'd GGUF file): the
+    // whole mapping goes to the device once and later calls resolve by offset, as after
+    // cllm_hip_register_weights. If the device cannot hold it, the bytes are copied per call.
+    Mapping m;
+    if (find_mapping(a, m) && immutable_file_mapping(m) && a + bytes <= m.hi &&
+        st->no_auto.count(m.lo) == 0) {
+        if ((rc = prune_auto_regions(st))) return rc;
+        Region r;
+        if (st->regions.count(m.lo) == 0 && upload_region(st, m.lo, m.hi - m.lo, &r) == CLLM_HIP_OK) {
+            r.automatic = true;
+            r.file_off = m.off;
+            r.inode = m.inode;
+            std::memcpy(r.fdev, m.dev, sizeof r.fdev);
+            st->regions[m.lo] = r;
+            *dev = (const uint8_t*)r.dev + (a - m.lo);
+            if (!aligned16(*dev))
+                return set_err(CLLM_HIP_E_ARG, "cllm_hip: weight pointer is not 16-byte aligned");
+            return CLLM_HIP_OK;
+        }
+        st->no_auto.insert(m.lo);
+    }
     HIP_TRY(st->wstage.ensure(bytes, st->stream));
     HIP_TRY(hipMemcpyAsync(st->wstage.p, w, bytes, hipMemcpyHostToDevice, st->stream));
     *dev = (const uint8_t*)st->wstage.p;
+    return CLLM_HIP_OK;
+}
+
+// Device address of `bytes` at src for a kernel that needs a 16-byte-aligned start: a
+// registered region or a device pointer is used in place when aligned, and anything else
+// (host memory, a misaligned device address) is first copied into the staging buffer.
+int resolve_span(DeviceState* st, const void* src, size_t bytes, const uint8_t** dev) {
+    const uint8_t* d = nullptr;
+    int rc;
+    if ((rc = lookup_region(st, (uintptr_t)src, bytes, &d))) return rc;
+    if (!d && is_device_ptr(src)) d = (const uint8_t*)src;
+    if (d && aligned16(d)) {
+        *dev = d;
+        return CLLM_HIP_OK;
+    }
+    HIP_TRY(st->wstage.ensure(bytes, st->stream));
+    HIP_TRY(hipMemcpyAsync(st->wstage.p, d ? (const void*)d : src, bytes,
+                           d ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st->stream));
+    *dev = (const uint8_t*)st->wstage.p;
+    return CLLM_HIP_OK;
+}
+
+// dequantize_block / dequantize_block_f16 into host memory, in passes of at most 2^26
+// elements (a multiple of every block size) so the device staging stays bounded.
+int dequantize_host(const char* who, const void* src, float* dst32, uint16_t* dst16,
+                    uint32_t type, int64_t n) {
+    if (!has_kernel(type) && !gemv_f_supported(type))
+        return set_err(CLLM_HIP_E_TYPE, "unsupported ggml type for dequantize");
+    if (n <= 0) return CLLM_HIP_OK;
+    if (!src || (!dst32 && !dst16)) return set_err(CLLM_HIP_E_ARG, "%s: null pointer", who);
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(st->mtx);
+    const int64_t bs = block_elems(type);
+    const size_t ts = block_bytes(type);
+    const size_t esz = dst16 ? sizeof(uint16_t) : sizeof(float);
+    constexpr int64_t kPass = (int64_t)1 << 26;
+    HIP_TRY(st->y.ensure((size_t)std::min(n, kPass) * esz, st->stream));
+    for (int64_t at = 0; at < n; at += kPass) {
+        const int64_t len = std::min(kPass, n - at);
+        const uint8_t* s = (const uint8_t*)src + (size_t)(at / bs) * ts;
+        const uint8_t* d = nullptr;
+        if ((rc = resolve_span(st, s, (size_t)((len + bs - 1) / bs) * ts, &d))) return rc;
+        void* out = dst16 ? (void*)(dst16 + at) : (void*)(dst32 + at);
+        if (dst16 && type == T_F16) {
+            // binary16 blocks are copied as they are (quant.cpp:400-403)
+            HIP_TRY(hipMemcpyAsync(out, d, (size_t)len * esz, hipMemcpyDeviceToHost, st->stream));
+        } else {
+            HIP_TRY(launch_dequantize_span(type, d, len, dst16 ? nullptr : (float*)st->y.p,
+                                           dst16 ? (uint16_t*)st->y.p : nullptr, st->stream));
+            HIP_TRY(hipMemcpyAsync(out, st->y.p, (size_t)len * esz, hipMemcpyDeviceToHost, st->stream));
+        }
+        // the staging buffers are reused by the next pass
+        HIP_TRY(hipStreamSynchronize(st->stream));
+    }
     return CLLM_HIP_OK;
 }
 
@@ -230,71 +471,64 @@ bool use_mfma(uint32_t type, int k, int m) {
 }
 
 // MFMA kernel choice. Default: the weight-row fp16 kernel (k_gemmw.hip) where it has the
-// type, else the int8 kernel (k_gemm.hip). CLLM_HIP_GEMM=int8 or =f16 forces the int8 kernel
-// or the activation-row fp16 kernel (k_gemm16.hip) for every type (tests run all three).
+// type, else the int8 kernel (k_gemm.hip). The tuning knob "gemm_kernel" (cllm_hip_tune)
+// forces the int8 kernel (1) or the activation-row fp16 kernel (k_gemm16.hip, 2) for every
+// type (tests run all three).
 enum class GemmKind { W16, I8, F16 };
 
-bool gemm_forced() {
-    const char* e = std::getenv("CLLM_HIP_GEMM");
-    return e && (std::strcmp(e, "f16") == 0 || std::strcmp(e, "int8") == 0);
-}
+bool gemm_forced() { return tuning().gemm_kind.load(std::memory_order_relaxed) != 0; }
 
 GemmKind gemm_kind(uint32_t type) {
-    const char* e = std::getenv("CLLM_HIP_GEMM");
-    if (e && std::strcmp(e, "f16") == 0) return GemmKind::F16;
-    if (e && std::strcmp(e, "int8") == 0) return GemmKind::I8;
+    const int k = tuning().gemm_kind.load(std::memory_order_relaxed);
+    if (k == 2) return GemmKind::F16;
+    if (k == 1) return GemmKind::I8;
     return gemmw_supported(type) ? GemmKind::W16 : GemmKind::I8;
 }
 
-// MFMA route on a Q8_0 batch already in device memory; ws supplies the fp16 staging of the
-// activation-row fp16 kernel.
+// Split-K bytes the MFMA route of this shape needs (the weight-row kernel only).
+size_t part_bytes_for(uint32_t type, int k, int n, int m) {
+    return gemm_kind(type) == GemmKind::W16 ? gemmw_partial_bytes(type, k, n, m) : 0;
+}
+
+// MFMA route on a Q8_0 batch already in device memory; ws supplies the activation formats of
+// the fp16 kernels and the split-K region.
 hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                     const float* sc, const int32_t* bs, const float* bias, float* y,
-                    Workspace* ws, hipStream_t stream) {
+                    const WsView& ws, hipStream_t stream) {
     const GemmKind kind = gemm_kind(type);
     if (kind == GemmKind::W16) {
-        const size_t pb = gemmw_partial_bytes(type, k, n, m);
-        if (pb) {
-            hipError_t e = ws->ensure_part(pb, stream);
-            if (e != hipSuccess) return e;
-        }
-        hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws->sc, ws->qh,
-                                      (type == T_Q4_K || type == T_Q5_K) ? ws->xq : nullptr, stream);
+        hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws.sc, ws.qh,
+                                      (type == T_Q4_K || type == T_Q5_K) ? ws.xq : nullptr, stream);
         if (e != hipSuccess) return e;
-        return launch_gemmw(type, w, k, n, m, ws->sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,
-                            pb ? ws->part.cap : 0, stream);
+        return launch_gemmw(type, w, k, n, m, ws.sc, ws.qh, ws.xq, bias, y, ws.part, ws.part_cap,
+                            stream);
     }
     if (kind == GemmKind::I8) return launch_gemm(type, w, k, n, m, qs, sc, bs, bias, y, stream);
-    hipError_t e = launch_q8_to_mfma(qs, sc, bs, (int64_t)m * k / 32, ws->qh, ws->px, stream);
+    hipError_t e = launch_q8_to_mfma(qs, sc, bs, (int64_t)m * k / 32, ws.qh, ws.px, stream);
     if (e != hipSuccess) return e;
-    return launch_gemm16(type, w, k, n, m, ws->qh, sc, ws->px, bias, y, stream);
+    return launch_gemm16(type, w, k, n, m, ws.qh, sc, ws.px, bias, y, stream);
 }
 
 // MFMA route from fp32 activations: quantize straight into the format the kernel reads.
 hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
-                        const float* bias, float* y, Workspace* ws, hipStream_t stream) {
+                        const float* bias, float* y, const WsView& ws, hipStream_t stream) {
     const int64_t nblk = (int64_t)m * k / 32;
     const GemmKind kind = gemm_kind(type);
     if (kind == GemmKind::F16) {
-        hipError_t e = launch_quantize_mfma(x, nblk, ws->sc, ws->qh, ws->px, stream);
+        hipError_t e = launch_quantize_mfma(x, nblk, ws.sc, ws.qh, ws.px, stream);
         if (e != hipSuccess) return e;
-        return launch_gemm16(type, w, k, n, m, ws->qh, ws->sc, ws->px, bias, y, stream);
+        return launch_gemm16(type, w, k, n, m, ws.qh, ws.sc, ws.px, bias, y, stream);
     }
     if (kind == GemmKind::W16) {
-        hipError_t e = launch_quantize_w(x, nblk, ws->sc, ws->qh, (type == T_Q4_K || type == T_Q5_K) ? ws->xq : nullptr,
-                                         stream);
+        hipError_t e = launch_quantize_w(x, nblk, ws.sc, ws.qh,
+                                         (type == T_Q4_K || type == T_Q5_K) ? ws.xq : nullptr, stream);
         if (e != hipSuccess) return e;
-        const size_t pb = gemmw_partial_bytes(type, k, n, m);
-        if (pb) {
-            e = ws->ensure_part(pb, stream);
-            if (e != hipSuccess) return e;
-        }
-        return launch_gemmw(type, w, k, n, m, ws->sc, ws->qh, ws->xq, bias, y, (float*)ws->part.p,
-                            pb ? ws->part.cap : 0, stream);
+        return launch_gemmw(type, w, k, n, m, ws.sc, ws.qh, ws.xq, bias, y, ws.part, ws.part_cap,
+                            stream);
     }
-    hipError_t e = launch_quantize_q8_0(x, nblk, ws->qs, ws->sc, ws->bs, stream);
+    hipError_t e = launch_quantize_q8_0(x, nblk, ws.qs, ws.sc, ws.bs, stream);
     if (e != hipSuccess) return e;
-    return run_gemm(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, ws, stream);
+    return run_gemm(type, w, k, n, m, ws.qs, ws.sc, ws.bs, bias, y, ws, stream);
 }
 
 // Batches of at most this many rows take the fused GEMV (quantization inside the kernel, one
@@ -309,21 +543,24 @@ bool needs_workspace(uint32_t type, int k, int m) {
 
 // GEMV route on fp32 activation rows.
 hipError_t run_gemv_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
-                        const float* bias, float* y, Workspace* ws, hipStream_t stream,
+                        const float* bias, float* y, const WsView& ws, hipStream_t stream,
                         bool accumulate = false) {
     if (m <= kFusedMaxRows)
         return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream, accumulate);
-    hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws->qs, ws->sc, ws->bs, stream);
+    hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws.qs, ws.sc, ws.bs, stream);
     if (e != hipSuccess) return e;
-    return launch_gemv(type, w, k, n, m, ws->qs, ws->sc, ws->bs, bias, y, stream, accumulate);
+    return launch_gemv(type, w, k, n, m, ws.qs, ws.sc, ws.bs, bias, y, stream, accumulate);
 }
 
-// The per-stream activation workspace of the device entry points, grown to m x k.
-int stream_workspace(DeviceState* st, hipStream_t s, int k, int m, Workspace** out) {
+// The per-stream workspace of the device entry points, grown to an m x k batch and to the
+// split-K region of an n-row MFMA call on it (n = 0: none).
+int stream_workspace(DeviceState* st, hipStream_t s, uint32_t type, int k, int n, int m,
+                     Workspace** out) {
     std::lock_guard<std::mutex> lk(st->mtx);
     auto& slot = st->dev_ws[s];
     if (!slot) slot = std::make_unique<Workspace>();
     HIP_TRY(slot->ensure(k, m, s));
+    if (n > 0 && use_mfma(type, k, m)) HIP_TRY(slot->ensure_part(part_bytes_for(type, k, n, m), s));
     *out = slot.get();
     return CLLM_HIP_OK;
 }
@@ -344,7 +581,11 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
     if ((rc = resolve_weights(st, w, row_bytes(type, in_dim) * (size_t)out_dim, &wd))) return rc;
     HIP_TRY(st->x.ensure(xb, st->stream));
     HIP_TRY(st->y.ensure(yb, st->stream));
-    if (needs_workspace(type, in_dim, n_rows)) HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
+    if (needs_workspace(type, in_dim, n_rows)) {
+        HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
+        if (use_mfma(type, in_dim, n_rows))
+            HIP_TRY(st->act.ensure_part(part_bytes_for(type, in_dim, out_dim, n_rows), st->stream));
+    }
     HIP_TRY(hipMemcpyAsync(st->x.p, x, xb, hipMemcpyHostToDevice, st->stream));
     const float* bd = nullptr;
     if (bias) {
@@ -358,10 +599,10 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
                               (float*)st->y.p, st->stream));
     } else if (use_mfma(type, in_dim, n_rows)) {
         HIP_TRY(run_gemm_f32(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
-                             (float*)st->y.p, &st->act, st->stream));
+                             (float*)st->y.p, st->act.v, st->stream));
     } else {
         HIP_TRY(run_gemv_f32(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
-                             (float*)st->y.p, &st->act, st->stream));
+                             (float*)st->y.p, st->act.v, st->stream));
     }
     HIP_TRY(hipMemcpyAsync(y, st->y.p, yb, hipMemcpyDeviceToHost, st->stream));
     HIP_TRY(hipStreamSynchronize(st->stream));
@@ -369,6 +610,10 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
 }
 
 }  // namespace
+
+namespace cllm_hip {
+Tuning& tuning() { return g_tuning; }
+}  // namespace cllm_hip
 
 extern "C" {
 
@@ -402,12 +647,12 @@ int cllm_hip_quantize_row_q8_0(const float* x, int64_t n, int n_rows, int8_t* qs
     HIP_TRY(st->x.ensure(total * sizeof(float), st->stream));
     HIP_TRY(st->act.ensure((int)n, n_rows, st->stream));
     HIP_TRY(hipMemcpyAsync(st->x.p, x, total * sizeof(float), hipMemcpyHostToDevice, st->stream));
-    HIP_TRY(launch_quantize_q8_0((const float*)st->x.p, (int64_t)(total / 32), st->act.qs,
-                                 st->act.sc, st->act.bs, st->stream));
-    HIP_TRY(hipMemcpyAsync(qs, st->act.qs, total, hipMemcpyDeviceToHost, st->stream));
-    HIP_TRY(hipMemcpyAsync(scales, st->act.sc, total / 32 * sizeof(float), hipMemcpyDeviceToHost,
+    HIP_TRY(launch_quantize_q8_0((const float*)st->x.p, (int64_t)(total / 32), st->act.v.qs,
+                                 st->act.v.sc, st->act.v.bs, st->stream));
+    HIP_TRY(hipMemcpyAsync(qs, st->act.v.qs, total, hipMemcpyDeviceToHost, st->stream));
+    HIP_TRY(hipMemcpyAsync(scales, st->act.v.sc, total / 32 * sizeof(float), hipMemcpyDeviceToHost,
                            st->stream));
-    HIP_TRY(hipMemcpyAsync(bsums, st->act.bs, total / 32 * sizeof(int32_t), hipMemcpyDeviceToHost,
+    HIP_TRY(hipMemcpyAsync(bsums, st->act.v.bs, total / 32 * sizeof(int32_t), hipMemcpyDeviceToHost,
                            st->stream));
     HIP_TRY(hipStreamSynchronize(st->stream));
     return CLLM_HIP_OK;
@@ -431,12 +676,12 @@ int cllm_hip_vec_dot_rows(const void* w, uint32_t type, int64_t n, int n_w_rows,
     if ((rc = resolve_weights(st, w, row_bytes(type, k) * (size_t)n_w_rows, &wd))) return rc;
     HIP_TRY(st->act.ensure(k, 1, st->stream));
     HIP_TRY(st->y.ensure((size_t)n_w_rows * sizeof(float), st->stream));
-    HIP_TRY(hipMemcpyAsync(st->act.qs, qs, (size_t)k, hipMemcpyHostToDevice, st->stream));
-    HIP_TRY(hipMemcpyAsync(st->act.sc, scales, (size_t)k / 32 * sizeof(float),
+    HIP_TRY(hipMemcpyAsync(st->act.v.qs, qs, (size_t)k, hipMemcpyHostToDevice, st->stream));
+    HIP_TRY(hipMemcpyAsync(st->act.v.sc, scales, (size_t)k / 32 * sizeof(float),
                            hipMemcpyHostToDevice, st->stream));
-    HIP_TRY(hipMemcpyAsync(st->act.bs, bsums, (size_t)k / 32 * sizeof(int32_t),
+    HIP_TRY(hipMemcpyAsync(st->act.v.bs, bsums, (size_t)k / 32 * sizeof(int32_t),
                            hipMemcpyHostToDevice, st->stream));
-    HIP_TRY(launch_gemv(type, wd, k, n_w_rows, 1, st->act.qs, st->act.sc, st->act.bs, nullptr,
+    HIP_TRY(launch_gemv(type, wd, k, n_w_rows, 1, st->act.v.qs, st->act.v.sc, st->act.v.bs, nullptr,
                         (float*)st->y.p, st->stream));
     HIP_TRY(hipMemcpyAsync(out, st->y.p, (size_t)n_w_rows * sizeof(float), hipMemcpyDeviceToHost,
                            st->stream));
@@ -470,13 +715,9 @@ int cllm_hip_register_weights(const void* host_base, size_t bytes) {
         HIP_TRY(hipFree(it->second.alloc));
         st->regions.erase(it);
     }
-    // Keep the device copy at the same offset modulo 256 as the host base, so host pointers
-    // that are 16-byte aligned stay 16-byte aligned on the device.
-    const size_t lead = a & 255u;
-    void* dev = nullptr;
-    HIP_TRY(hipMalloc(&dev, bytes + lead));
-    HIP_TRY(hipMemcpy((char*)dev + lead, host_base, bytes, hipMemcpyHostToDevice));
-    st->regions[a] = Region{bytes, (char*)dev + lead, dev};
+    Region r;
+    if ((rc = upload_region(st, a, bytes, &r))) return rc;
+    st->regions[a] = r;
     return CLLM_HIP_OK;
 }
 
@@ -492,6 +733,14 @@ int cllm_hip_unregister_weights(const void* host_base) {
     HIP_TRY(hipFree(it->second.alloc));
     st->regions.erase(it);
     return CLLM_HIP_OK;
+}
+
+int cllm_hip_dequantize_block(const void* src, float* dst, uint32_t type, int64_t n) {
+    return dequantize_host("dequantize_block", src, dst, nullptr, type, n);
+}
+
+int cllm_hip_dequantize_block_f16(const void* src, uint16_t* dst, uint32_t type, int64_t n) {
+    return dequantize_host("dequantize_block_f16", src, nullptr, dst, type, n);
 }
 
 int cllm_hip_quantize_q8_0_dev(const float* x, int64_t n, int n_rows, int8_t* qs, float* scales,
@@ -531,9 +780,9 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
         return CLLM_HIP_OK;
     }
     Workspace* ws;
-    if ((rc = stream_workspace(st, s, in_dim, n_rows, &ws))) return rc;
+    if ((rc = stream_workspace(st, s, type, in_dim, out_dim, n_rows, &ws))) return rc;
     HIP_TRY(run_gemm(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums, bias, y,
-                     ws, s));
+                     ws->v, s));
     return CLLM_HIP_OK;
 }
 
@@ -673,15 +922,18 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
         HIP_TRY(launch_gemv_f(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, s));
         return CLLM_HIP_OK;
     }
-    Workspace* ws = nullptr;
-    if (needs_workspace(type, in_dim, n_rows) && (rc = stream_workspace(st, s, in_dim, n_rows, &ws)))
-        return rc;
+    WsView v;
+    if (needs_workspace(type, in_dim, n_rows)) {
+        Workspace* ws;
+        if ((rc = stream_workspace(st, s, type, in_dim, out_dim, n_rows, &ws))) return rc;
+        v = ws->v;
+    }
     if (!use_mfma(type, in_dim, n_rows)) {
         // decode-sized batch: one or two rows in a single launch that quantizes them in LDS
-        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws, s));
+        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
         return CLLM_HIP_OK;
     }
-    HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws, s));
+    HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
     return CLLM_HIP_OK;
 }
 
@@ -698,10 +950,10 @@ int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t t
     if ((rc = acquire(&st))) return rc;
     hipStream_t s = (hipStream_t)stream;
     Workspace* ws = nullptr;
-    if ((rc = stream_workspace(st, s, in_dim, n_rows, &ws))) return rc;
+    if ((rc = stream_workspace(st, s, type, in_dim, out_dim, n_rows, &ws))) return rc;
     if (has_kernel(type) && !use_mfma(type, in_dim, n_rows)) {
         // the GEMV adds into y in its epilogue
-        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws, s,
+        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws->v, s,
                              true));
         return CLLM_HIP_OK;
     }
@@ -714,7 +966,7 @@ int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t t
     if (!has_kernel(type))
         HIP_TRY(launch_gemv_f(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, t, s));
     else
-        HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, t, ws, s));
+        HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, t, ws->v, s));
     HIP_TRY(launch_add(y, t, (int64_t)n_rows * out_dim, s));
     return CLLM_HIP_OK;
 }
@@ -830,7 +1082,7 @@ static int attention_impl(const float* q, const float* k_cache, const float* v_c
     if (rc) return rc;
     hipStream_t s = (hipStream_t)stream;
     Workspace* ws;
-    if ((rc = stream_workspace(st, s, 32, 1, &ws))) return rc;
+    if ((rc = stream_workspace(st, s, T_Q8_0, 32, 0, 1, &ws))) return rc;
     const size_t bytes = attention_workspace_bytes(n_rows, n_head, head_dim);
     {
         std::lock_guard<std::mutex> lk(st->mtx);
@@ -1016,6 +1268,44 @@ int cllm_hip_gguf_config(const cllm_hip_gguf* g, cllm_hip_model_config* c) {
     c->data_offset = g->file.data_offset;
     c->data_bytes = g->file.map_bytes > g->file.data_offset ? g->file.map_bytes - g->file.data_offset : 0;
     return CLLM_HIP_OK;
+}
+
+int cllm_hip_tune(const char* knob, const int* values, int n_values) {
+    if (!knob || n_values < 0 || (n_values > 0 && !values))
+        return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: bad arguments");
+    Tuning& t = tuning();
+    auto v = [&](int i) { return i < n_values ? values[i] : 0; };
+    if (std::strcmp(knob, "gemm_kernel") == 0) {
+        if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemm_kernel is 0, 1 or 2");
+        t.gemm_kind.store(v(0));
+    } else if (std::strcmp(knob, "gemm_tiles") == 0) {
+        t.gemm_waves.store(v(0));
+        t.gemm_wtiles.store(v(1));
+        t.gemm_ttiles.store(v(2));
+    } else if (std::strcmp(knob, "gemm_splits") == 0) {
+        t.gemm_splits.store(v(0));
+    } else if (std::strcmp(knob, "gemv_waves") == 0) {
+        t.gemv_short_wps.store(v(0));
+        t.gemv_deep_wps.store(v(1));
+    } else {
+        return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: unknown knob %s", knob);
+    }
+    return CLLM_HIP_OK;
+}
+
+const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_rows) {
+    static thread_local char buf[128];
+    const char* route = cllm_hip_matmul_route(type, in_dim, out_dim, n_rows);
+    if (std::strcmp(route, "mfma") != 0) {
+        snprintf(buf, sizeof buf, "%s", route);
+    } else {
+        const GemmKind kind = gemm_kind(type);
+        if (kind == GemmKind::W16)
+            gemmw_plan_name(type, in_dim, out_dim, n_rows, buf, sizeof buf);
+        else
+            snprintf(buf, sizeof buf, "%s", kind == GemmKind::I8 ? "k_gemm_i8" : "k_gemm16");
+    }
+    return buf;
 }
 
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows) {

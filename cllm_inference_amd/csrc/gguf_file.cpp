@@ -8,6 +8,8 @@
 // cursor; a read past the end fails with the message of the reference's read helper.
 #include "gguf_file.h"
 
+#include "ggml_blocks.h"
+
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -18,6 +20,8 @@
 namespace cllm_hip {
 
 namespace {
+
+constexpr uint32_t kMaxDims = 4;  // GGML_MAX_DIMS
 
 enum ValueType : uint32_t {
     V_U8 = 0, V_I8 = 1, V_U16 = 2, V_I16 = 3, V_U32 = 4, V_I32 = 5, V_F32 = 6, V_BOOL = 7,
@@ -210,6 +214,12 @@ bool gguf_open(const char* path, GgufFile& out, std::string& err) {
             err = c.err;
             return false;
         }
+        // GGML tensors have at most 4 dimensions; a larger count is a malformed file (the
+        // reference would allocate whatever the count says)
+        if (n_dims > kMaxDims) {
+            err = "tensor " + t.name + ": " + std::to_string(n_dims) + " dimensions";
+            return false;
+        }
         std::vector<uint64_t> dims(n_dims);
         for (uint32_t d = 0; d < n_dims; ++d)
             if (!c.u64(dims[d])) {
@@ -225,6 +235,23 @@ bool gguf_open(const char* path, GgufFile& out, std::string& err) {
         out.tensors.push_back(std::move(t));
     }
     out.data_offset = (c.at + 31) & ~(size_t)31;
+
+    // Every tensor of a known type must lie inside the mapped data section: the device copy
+    // is exactly that section, and a pointer past it would send the kernels out of bounds.
+    // (The reference does not check; its reads past a truncated file fault on the host.)
+    const size_t data_bytes = out.map_bytes > out.data_offset ? out.map_bytes - out.data_offset : 0;
+    for (const GgufTensor& t : out.tensors) {
+        const int bs = block_elems(t.type);
+        const size_t ts = block_bytes(t.type);
+        if (bs <= 0 || ts == 0) continue;  // an unknown type: its size cannot be known
+        unsigned __int128 elems = 1;
+        for (uint64_t d : t.shape) elems *= d;
+        const unsigned __int128 bytes = (elems + (unsigned)bs - 1) / (unsigned)bs * ts;
+        if ((unsigned __int128)t.offset + bytes > data_bytes) {
+            err = "tensor " + t.name + " extends past the end of the file";
+            return false;
+        }
+    }
 
     // hyper-parameters (gguf.cpp:197-272)
     auto str_of = [&](const std::string& k) -> std::string {

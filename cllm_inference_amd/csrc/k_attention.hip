@@ -75,10 +75,12 @@ constexpr int kMaxSplits = 256;      // sequence splits per (row, KV head)
 // rope_base > 0 (one query row, a decode step): the queries and the key row at pos0 arrive
 // unrotated and the kernel applies the NEOX rotation of k_rope_neox itself, to the queries in
 // registers and to the key row as it loads it, writing the rotated key row back to k_new (the
-// cache row pos0, read by no other workgroup: only the split holding pos0 covers it).
+// cache row pos0, read by no other workgroup: only the split holding pos0 covers it). k_new
+// points into the key cache, so kc carries no __restrict__: the compiler may not treat the
+// cache as unwritten by this kernel.
 template <int HD>
 __global__ __launch_bounds__(kThreads) void k_attention(
-    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    const float* __restrict__ q, const float* kc, const float* __restrict__ vc,
     int n_head, int n_kv, int pos0, int split_len, float scale, float* __restrict__ part,
     int* __restrict__ counters, float* __restrict__ out, float rope_base, float* k_new) {
     constexpr int PER = HD / kLanesPerPos;  // K elements per lane (4 .. 16)

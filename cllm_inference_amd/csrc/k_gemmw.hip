@@ -1073,12 +1073,12 @@ struct Plan {
 
 Plan plan_for(uint32_t type, int k, int n, int m) {
     Plan p{};
-    int wv = 0, nt = 0, mt = 0;
-    // CLLM_HIP_GEMMW_CFG="<waves>,<weight tiles per wave>,<token tiles>" and
-    // CLLM_HIP_GEMMW_SPLITS=<n> override the Q4_K tile shape and the split-K factor (sweeps).
-    if (const char* e = getenv("CLLM_HIP_GEMMW_CFG")) {
-        if (sscanf(e, "%d,%d,%d", &wv, &nt, &mt) != 3) wv = nt = mt = 0;
-    }
+    // the tuning overrides (cllm_hip_tune "gemm_tiles" / "gemm_splits"): any compiled tile
+    // shape of the K-quant kernels, and the split-K factor
+    const Tuning& tu = tuning();
+    const int wv = tu.gemm_waves.load(std::memory_order_relaxed);
+    const int nt = tu.gemm_wtiles.load(std::memory_order_relaxed);
+    const int mt = tu.gemm_ttiles.load(std::memory_order_relaxed);
     const int cus = device_cus();
     int target = 2 * cus;  // workgroups to aim for
     if (is_b32(type)) {
@@ -1089,7 +1089,9 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
     } else if (type == T_Q6_K) {
         // 128 weight rows x 64 tokens (4 waves, two workgroups per CU)
         p.wv = 4, p.nt = 1, p.mt = 2;
-    } else if (wv != 0 && type == T_Q4_K) {
+    } else if (wv != 0 && (type == T_Q4_K ||
+                           (wv == 8 && nt == 1 && (mt == 4 || mt == 2)) || (wv == 4 && nt == 1 && mt == 1))) {
+        // Q5_K has the three shapes of the default plan compiled
         p.wv = wv, p.nt = nt, p.mt = mt;
     } else {
         // From sweeps on MI355X at m = 512 (us for n = 14336 / 4096 / 1024): 256 x 128 tiles
@@ -1113,10 +1115,8 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
     const int bn = 32 * p.nt * p.wv, bm = 32 * p.mt;
     const int tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
     p.splits = choose_splits(tiles, k / kKS, target);
-    if (const char* e = getenv("CLLM_HIP_GEMMW_SPLITS")) {
-        const int sp = atoi(e);
-        if (sp >= 1 && sp <= 16 && sp <= k / kKS) p.splits = sp;
-    }
+    const int sp = tu.gemm_splits.load(std::memory_order_relaxed);
+    if (sp >= 1 && sp <= 16 && sp <= k / kKS) p.splits = sp;
     return p;
 }
 
@@ -1269,6 +1269,22 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
 #undef CLLM_GEMMW_CASE
     }
     return e;
+}
+
+void gemmw_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap) {
+    if (!gemmw_supported(type) || k % 256 != 0) {
+        snprintf(buf, cap, "none");
+        return;
+    }
+    const Plan p = plan_for(type, k, n, m);
+    if (type == T_Q6_K)
+        snprintf(buf, cap, "k_gemmw_q6k<4,2> splits=%d", p.splits);
+    else if (is_b32(type))
+        snprintf(buf, cap, "k_gemmw_b32<%s,4,%d> splits=%d",
+                 type == T_Q8_0 ? "Q8_0" : type == T_Q4_0 ? "Q4_0" : "Q5_0", p.mt, p.splits);
+    else
+        snprintf(buf, cap, "k_gemmw_q4k<%d,%d,%d,%s> splits=%d", p.wv, p.nt, p.mt,
+                 type == T_Q5_K ? "Q5_K" : "Q4_K", p.splits);
 }
 
 }  // namespace cllm_hip

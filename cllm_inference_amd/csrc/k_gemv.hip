@@ -1125,26 +1125,20 @@ static int cu_count() {
 // 128256x4096 head 81 us against 88-96 us for the 2-deep ring at 4 waves per SIMD. More
 // loads in flight per wave lost even when every extra load was useful. With 4 or 8 rows,
 // streams longer than 32 items per SIMD use the 2-deep ring at 4 waves per SIMD.
-// CLLM_HIP_GEMV_SHAPE="<one-deep>,<two-deep>" caps the waves per SIMD of the two rings (for
-// tuning sweeps; read once per process). The grid never exceeds the waves resident at once.
+// The tuning knob "gemv_waves" (cllm_hip_tune) caps the waves per SIMD of the two rings for
+// sweeps. The grid never exceeds the waves resident at once.
 struct GemvTuning {
     int short_wps = 8;
     int deep_wps = 4;
 };
 
-static const GemvTuning& gemv_tuning() {
-    static const GemvTuning t = [] {
-        GemvTuning r;
-        if (const char* e = getenv("CLLM_HIP_GEMV_SHAPE")) {
-            int a = 0, b = 0;
-            if (sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && a <= 16 && b >= 1 && b <= 16) {
-                r.short_wps = a;
-                r.deep_wps = b;
-            }
-        }
-        return r;
-    }();
-    return t;
+static GemvTuning gemv_tuning() {
+    GemvTuning r;
+    const int a = tuning().gemv_short_wps.load(std::memory_order_relaxed);
+    const int b = tuning().gemv_deep_wps.load(std::memory_order_relaxed);
+    if (a >= 1 && a <= 16) r.short_wps = a;
+    if (b >= 1 && b <= 16) r.deep_wps = b;
+    return r;
 }
 
 // Waves of k_gemv<T, MR, P> resident on the whole device with `shmem` bytes of LDS per
@@ -1255,7 +1249,7 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
     const int iters = (k / Tr::UNIT + 63) / 64;
     const int64_t items = (int64_t)n * iters * (SW ? 2 : 1);
     const int64_t simds = (int64_t)cu_count() * 4;
-    const GemvTuning& tu = gemv_tuning();
+    const GemvTuning tu = gemv_tuning();
     const size_t shmem = act_lds_bytes<T>(MR, k);
     if constexpr (MR == 1) {
         if (sg.norm_w) {  // the RMSNorm rides in the staging (one row)

@@ -605,6 +605,126 @@ __global__ __launch_bounds__(kThreads) void k_dequant_rows_any(const uint8_t* __
     out[(size_t)r * k + e] = T == T_F32 ? ((const float*)row)[e] : f16_to_f32(((const uint16_t*)row)[e]);
 }
 
+// binary16 bits -> float by integer operations only: exact for every encoding, and a NaN keeps
+// its payload and signalling bit (half_to_float, include/cllm/core/quant.hpp:31-56), which the
+// hardware conversion would quiet.
+__device__ __forceinline__ float f16_to_f32_exact(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+    if (e == 0x1Fu) return __builtin_bit_cast(float, sign | 0x7F800000u | (man << 13));
+    if (e != 0) return __builtin_bit_cast(float, sign | ((e + 112u) << 23) | (man << 13));
+    // zero or subnormal: man * 2^-24, exact in fp32
+    return __builtin_bit_cast(float, sign | __builtin_bit_cast(uint32_t, (float)man * 0x1p-24f));
+}
+
+// float -> binary16 bits by the rule of the reference header's float_to_half (its
+// include/cllm/core/quant.hpp:58-87): results in the normal range keep the top 10 mantissa
+// bits (truncation), results below it are rounded to nearest with ties to even, results
+// below 2^-25 or so become signed zero, overflow becomes infinity and NaN a quiet NaN.
+__device__ __forceinline__ uint32_t f32_to_f16_trunc(float f) {
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t biased = (x >> 23) & 0xFFu;
+    uint32_t man = x & 0x7FFFFFu;
+    if (biased == 0xFFu) return sign | (man ? 0x7E00u : 0x7C00u);
+    const int e = (int)biased - 112;  // rebias 127 -> 15
+    if (e >= 31) return sign | 0x7C00u;
+    if (e > 0) return sign | ((uint32_t)e << 10) | (man >> 13);
+    if (e < -10) return sign;
+    man |= 0x800000u;
+    const uint32_t shift = (uint32_t)(14 - e);
+    return sign | ((man + ((1u << (shift - 1)) - 1u) + ((man >> shift) & 1u)) >> shift);
+}
+
+// Elements [0, n) of a run of blocks (dequantize_block, quant.cpp:371-389, and
+// dequantize_block_f16, 398-407): thread u decodes the 32-element unit u; the elements at and
+// past n of a partial last block are not written, as the reference's loops guard them. H: the
+// values go out as binary16 bits (f32_to_f16_trunc) instead of fp32.
+template <uint32_t T, bool H>
+__global__ __launch_bounds__(kThreads) void k_dequant_span(const uint8_t* __restrict__ src,
+                                                           int64_t n, float* __restrict__ out,
+                                                           uint16_t* __restrict__ out16) {
+    const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (u >= (n + 31) / 32) return;
+    float v[32];
+    if constexpr (T == T_F16) {
+        // integer conversion, so NaN payloads pass unchanged as in half_to_float
+        const u32x4* p = (const u32x4*)(src + 64 * u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 r = p[q];
+            const uint32_t d[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[8 * q + 2 * i] = f16_to_f32_exact(d[i] & 0xFFFFu);
+                v[8 * q + 2 * i + 1] = f16_to_f32_exact(d[i] >> 16);
+            }
+        }
+    } else {
+        FUnit<T>::decode(FUnit<T>::load(src, (int)u), (int)u, v);
+    }
+    const int64_t e0 = 32 * u;
+    if (e0 + 32 <= n) {
+        if constexpr (H) {
+            u32x4* o = (u32x4*)(out16 + e0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    p[i] = f32_to_f16_trunc(v[8 * q + 2 * i]) | (f32_to_f16_trunc(v[8 * q + 2 * i + 1]) << 16);
+                o[q] = u32x4{p[0], p[1], p[2], p[3]};
+            }
+        } else {
+            f32x4* o = (f32x4*)(out + e0);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) o[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            if (e0 + i < n) {
+                if constexpr (H)
+                    out16[e0 + i] = (uint16_t)f32_to_f16_trunc(v[i]);
+                else
+                    out[e0 + i] = v[i];
+            }
+        }
+    }
+}
+
+// F32 / F16 runs of any length, one element per thread.
+template <uint32_t T, bool H>
+__global__ __launch_bounds__(kThreads) void k_dequant_span_any(const uint8_t* __restrict__ src,
+                                                               int64_t n, float* __restrict__ out,
+                                                               uint16_t* __restrict__ out16) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float v = T == T_F32 ? ((const float*)src)[i] : f16_to_f32_exact(((const uint16_t*)src)[i]);
+    if constexpr (H)
+        out16[i] = (uint16_t)f32_to_f16_trunc(v);
+    else
+        out[i] = v;
+}
+
+template <uint32_t T>
+hipError_t launch_span_t(const uint8_t* src, int64_t n, float* out, uint16_t* out16,
+                         hipStream_t stream) {
+    if ((T == T_F32 || T == T_F16) && n % 32 != 0) {
+        const unsigned grid = (unsigned)((n + kThreads - 1) / kThreads);
+        if (out16)
+            hipLaunchKernelGGL((k_dequant_span_any<T, true>), dim3(grid), dim3(kThreads), 0, stream, src, n, out, out16);
+        else
+            hipLaunchKernelGGL((k_dequant_span_any<T, false>), dim3(grid), dim3(kThreads), 0, stream, src, n, out, out16);
+    } else {
+        const unsigned grid = (unsigned)(((n + 31) / 32 + kThreads - 1) / kThreads);
+        if (out16)
+            hipLaunchKernelGGL((k_dequant_span<T, true>), dim3(grid), dim3(kThreads), 0, stream, src, n, out, out16);
+        else
+            hipLaunchKernelGGL((k_dequant_span<T, false>), dim3(grid), dim3(kThreads), 0, stream, src, n, out, out16);
+    }
+    return hipGetLastError();
+}
+
 template <uint32_t T>
 hipError_t launch_dequant_t(const uint8_t* w, int k, const int32_t* ids, int n, float* out,
                             hipStream_t stream) {
@@ -641,6 +761,28 @@ hipError_t launch_dequantize_rows(uint32_t type, const uint8_t* w, int k, const 
         case T_Q4_K: return launch_dequant_t<T_Q4_K>(w, k, ids, n, out, stream);
         case T_Q5_K: return launch_dequant_t<T_Q5_K>(w, k, ids, n, out, stream);
         case T_Q6_K: return launch_dequant_t<T_Q6_K>(w, k, ids, n, out, stream);
+        default: return hipErrorNotSupported;
+    }
+}
+
+hipError_t launch_dequantize_span(uint32_t type, const uint8_t* src, int64_t n, float* out,
+                                  uint16_t* out16, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    if ((out == nullptr) == (out16 == nullptr) || n > ((int64_t)1 << 36)) return hipErrorInvalidValue;
+    switch (type) {
+        case T_F32: return launch_span_t<T_F32>(src, n, out, out16, stream);
+        case T_F16: return launch_span_t<T_F16>(src, n, out, out16, stream);
+        case T_Q4_0: return launch_span_t<T_Q4_0>(src, n, out, out16, stream);
+        case T_Q4_1: return launch_span_t<T_Q4_1>(src, n, out, out16, stream);
+        case T_Q5_0: return launch_span_t<T_Q5_0>(src, n, out, out16, stream);
+        case T_Q5_1: return launch_span_t<T_Q5_1>(src, n, out, out16, stream);
+        case T_Q8_0: return launch_span_t<T_Q8_0>(src, n, out, out16, stream);
+        case T_Q8_1: return launch_span_t<T_Q8_1>(src, n, out, out16, stream);
+        case T_Q2_K: return launch_span_t<T_Q2_K>(src, n, out, out16, stream);
+        case T_Q3_K: return launch_span_t<T_Q3_K>(src, n, out, out16, stream);
+        case T_Q4_K: return launch_span_t<T_Q4_K>(src, n, out, out16, stream);
+        case T_Q5_K: return launch_span_t<T_Q5_K>(src, n, out, out16, stream);
+        case T_Q6_K: return launch_span_t<T_Q6_K>(src, n, out, out16, stream);
         default: return hipErrorNotSupported;
     }
 }

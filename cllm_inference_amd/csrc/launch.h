@@ -7,7 +7,19 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace cllm_hip {
+
+// Process-wide kernel-choice overrides for tests and tuning sweeps (cllm_hip_tune). Zero
+// everywhere means the planners' own choices; the product never sets them itself.
+struct Tuning {
+    std::atomic<int> gemm_kind{0};  // 0 planner, 1 int8 MFMA (k_gemm), 2 activation-row fp16 (k_gemm16)
+    std::atomic<int> gemm_waves{0}, gemm_wtiles{0}, gemm_ttiles{0};  // weight-row GEMM tile
+    std::atomic<int> gemm_splits{0};                                   // weight-row GEMM K splits
+    std::atomic<int> gemv_short_wps{0}, gemv_deep_wps{0};              // GEMV waves per SIMD
+};
+Tuning& tuning();
 
 // n_blocks consecutive 32-element fp32 blocks -> Q8_0 (qs, fp32 scales, int32 block sums).
 hipError_t launch_quantize_q8_0(const float* x, int64_t n_blocks, int8_t* qs, float* scales,
@@ -102,6 +114,9 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream);
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
+// Name of the weight-row kernel instantiation and its split count for this shape, e.g.
+// "k_gemmw_q4k<8,1,2,Q5_K> splits=1" (written into buf).
+void gemmw_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap);
 
 // Producers of the linear layers' activations (k_producers.hip): RMSNorm of `rows` rows of n
 // and SwiGLU (silu(gate) * up) over `total` elements, each writing h (fp32, may be null)
@@ -133,6 +148,12 @@ hipError_t launch_attention(const float* q, const float* kc, const float* vc, in
 // as the reference's dequantize_block (the embedding lookup). k_gemv_f.hip.
 hipError_t launch_dequantize_rows(uint32_t type, const uint8_t* w, int k, const int32_t* ids,
                                   int n, float* out, hipStream_t stream);
+
+// Elements [0, n) of the run of blocks at src (16-byte aligned), dequantized bit for bit as
+// dequantize_block (to fp32 out) or dequantize_block_f16 (to binary16 bits out16; exactly one
+// of the two outputs is given). A partial last block is read whole, written up to n.
+hipError_t launch_dequantize_span(uint32_t type, const uint8_t* src, int64_t n, float* out,
+                                  uint16_t* out16, hipStream_t stream);
 
 // Float-dot GEMV (k_gemv_f.hip) for the types without a vec_dot kernel (F32, F16, Q4_1,
 // Q5_1, Q8_1, Q2_K, Q3_K): y[t, j] = bias[j] + sum_i x[t, i] * deq(W[j, i]) on fp32

@@ -3,8 +3,9 @@
 //
 // Errors: each C-ABI failure becomes std::runtime_error carrying the library's message, which
 // reproduces the reference's exception text where the reference has one
-// (src/core/quant.cpp:423, 1370, 1379, 1443).
+// (src/core/quant.cpp:387, 423, 1370, 1379, 1443).
 #include "cllm/core/quant.hpp"
+#include "cllm/core/tensor.hpp"
 
 #include <stdexcept>
 #include <string>
@@ -24,6 +25,27 @@ int block_size(GgmlType type) { return cllm_hip_block_size((uint32_t)type); }
 size_t type_size(GgmlType type) { return cllm_hip_type_size((uint32_t)type); }
 
 bool has_vec_dot(GgmlType type) { return cllm_hip_has_vec_dot((uint32_t)type) != 0; }
+
+void dequantize_block(const void* src, float* dst, GgmlType type, int64_t n) {
+    check(cllm_hip_dequantize_block(src, dst, (uint32_t)type, n));
+}
+
+void dequantize_block_f16(const void* src, uint16_t* dst, GgmlType type, int64_t n) {
+    check(cllm_hip_dequantize_block_f16(src, dst, (uint32_t)type, n));
+}
+
+// quant.cpp:391-395 and 409-412 of the reference
+std::vector<float> Tensor::dequantize() const {
+    std::vector<float> out(numel());
+    dequantize_block(data, out.data(), type, (int64_t)numel());
+    return out;
+}
+
+std::vector<uint16_t> Tensor::dequantize_f16() const {
+    std::vector<uint16_t> out(numel());
+    dequantize_block_f16(data, out.data(), type, (int64_t)numel());
+    return out;
+}
 
 void quantize_row_q8_0(const float* x, QuantizedQ8_0& out, int64_t n) {
     if (n % 32 != 0) throw std::runtime_error("quantize_row_q8_0: n not divisible by 32");

@@ -1,17 +1,20 @@
 // quant.hpp -- the cllm Quant API, served by the MI355X (gfx950) kernels of libcllm_hip.so.
 //
-// Source-compatible with the hot-path part of cllm_inference's include/cllm/core/quant.hpp
-// (lines 13-27 and 90-151 there): same namespace, names, signatures, GgmlType ids and
-// QuantizedQ8_0 layout, so TransformerEngine::mm / mm_batch (src/core/engine.cpp:237-238,
-// 284) compile and link against this header unchanged. Implemented in
-// cllm_inference_amd/csrc/quant_api.cpp (libcllm_quant.so) over the C ABI in cllm_hip.h.
+// Source-compatible with cllm_inference's include/cllm/core/quant.hpp (lines 13-151 there):
+// same namespace, names, signatures, GgmlType ids and QuantizedQ8_0 layout. With
+// include/cllm/core/tensor.hpp beside it, the reference's src/core/engine.cpp compiles
+// against these headers unchanged and links against libcllm_quant.so: every Quant symbol the
+// engine calls (matmul_quant, matmul_quant_batch at engine.cpp:237-238, 284; dequantize_block
+// at 316; Tensor::dequantize / dequantize_f16 at 191-224) is defined there. Implemented in
+// cllm_inference_amd/csrc/quant_api.cpp over the C ABI in cllm_hip.h.
 //
 // Differences a caller can observe:
 //   - The ThreadPool* argument is accepted and ignored; the GPU grid replaces the pool.
 //   - All thirteen types are computed on the GPU: the six with a vec_dot kernel (Q4_0, Q5_0,
 //     Q8_0, Q4_K, Q5_K, Q6_K) on Q8_0 activations, the others (F32, F16, Q4_1, Q5_1, Q8_1,
 //     Q2_K, Q3_K) as the reference's dequantize-and-float-dot fallback, on fp32 activations.
-//     dequantize_block / dequantize_block_f16 are not part of this library.
+//   - dequantize_block / dequantize_block_f16 decode on the GPU (bit for bit the reference's
+//     values) and copy the result back; they are meant for load time and single rows.
 //   - Failures of the GPU runtime also surface as std::runtime_error.
 #pragma once
 
@@ -91,6 +94,14 @@ inline uint16_t float_to_half(float f) {
 // Elements per block, and bytes per block.
 int block_size(GgmlType type);
 size_t type_size(GgmlType type);
+
+// The first n elements of the blocks at src, dequantized to float dst[n]. A partial last
+// block is read whole and written up to n. Throws "unsupported ggml type for dequantize" for
+// an id that is no GGML type.
+void dequantize_block(const void* src, float* dst, GgmlType type, int64_t n);
+
+// The same values as binary16 bits (float_to_half of each; F16 blocks are copied as they are).
+void dequantize_block_f16(const void* src, uint16_t* dst, GgmlType type, int64_t n);
 
 // A Q8_0-quantized activation row: 32-element blocks, one fp32 scale and one int32 sum of
 // the quantized values per block.

@@ -91,6 +91,20 @@ int cllm_hip_matmul_quant_batch(const float* x, const void* w, uint32_t type,
 int cllm_hip_register_weights(const void* host_base, size_t bytes);
 int cllm_hip_unregister_weights(const void* host_base);
 
+/* dequantize_block: the first n elements of the run of blocks at src (ceil(n / block_size)
+ * blocks of any of the thirteen types) to fp32 dst[n], bit for bit. A partial last block is
+ * read whole and written up to n, as the reference's loops do. src is a host pointer (it may
+ * lie in a registered region) or a device pointer, of any alignment; dst is host memory.
+ * Decoded on the GPU. Replaces include/cllm/core/quant.hpp:99 / src/core/quant.cpp:371-389
+ * (the engine's embedding lookup, engine.cpp:316, and Tensor::dequantize, quant.cpp:391-395). */
+int cllm_hip_dequantize_block(const void* src, float* dst, uint32_t type, int64_t n);
+
+/* dequantize_block_f16: the same values as binary16 bits, converted with the reference
+ * header's float_to_half rule (normal results truncated); F16 blocks are copied as they are.
+ * Replaces include/cllm/core/quant.hpp:105 / src/core/quant.cpp:398-407 (and
+ * Tensor::dequantize_f16, 409-412). */
+int cllm_hip_dequantize_block_f16(const void* src, uint16_t* dst, uint32_t type, int64_t n);
+
 /* ---- device-pointer entry points (stream-ordered) ------------------------------------ */
 
 /* quantize_row_q8_0 on device buffers (same layout as cllm_hip_quantize_row_q8_0). */
@@ -265,6 +279,22 @@ int cllm_hip_gguf_config(const cllm_hip_gguf* g, cllm_hip_model_config* cfg);
  * "mfma" (vec_dot types), "fdot" (the float-dot kernels of the other types), "none" (no
  * GGML type); for tests and benchmarks. */
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows);
+
+/* The kernel instantiation and launch plan cllm_hip_matmul_quant_dev would run for this shape,
+ * e.g. "k_gemmw_q4k<8,1,2,Q5_K> splits=1", or the route name for the GEMV and float-dot
+ * routes; for tests and benchmarks. No reference counterpart. */
+const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_rows);
+
+/* Process-wide kernel-choice overrides for tests and tuning sweeps; no reference counterpart.
+ * The library itself never sets them, and nothing reads the environment. Knobs:
+ *   "gemm_kernel"  values[0]: 0 the planner's MFMA kernel, 1 the int8 MFMA kernel, 2 the
+ *                  activation-row fp16 MFMA kernel (from 16 rows, every vec_dot type)
+ *   "gemm_tiles"   waves, weight tiles per wave, token tiles of the weight-row GEMM (a shape
+ *                  it has compiled; 0, 0, 0 = the planner's)
+ *   "gemm_splits"  K splits of the weight-row GEMM (0 = the planner's)
+ *   "gemv_waves"   waves per SIMD of the one-deep and two-deep GEMV rings (0 = defaults)
+ * Missing values count as 0, so n_values = 0 resets a knob. Takes effect on the next call. */
+int cllm_hip_tune(const char* knob, const int* values, int n_values);
 
 #ifdef __cplusplus
 }

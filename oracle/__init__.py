@@ -16,6 +16,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libcllm_ref.so")
+DROPIN_SO = os.path.join(HERE, "_ref", "libengine_dropin.so")
 REF_ROOT = "/root/reference"
 
 _P = ctypes.c_void_p
@@ -24,11 +25,14 @@ _U = ctypes.c_uint32
 _I64 = ctypes.c_int64
 
 
-def build(with_ref: bool = True) -> None:
-    """Compiles liboracle.so, and _ref/libcllm_ref.so when the reference tree is present."""
+def build(with_ref: bool = True, dropin: bool = False) -> None:
+    """Compiles liboracle.so, and _ref/libcllm_ref.so when the reference tree is present; with
+    dropin (after cllm_inference_amd's libraries are built) also _ref/libengine_dropin.so."""
     targets = ["all"]
     if with_ref and os.path.isdir(REF_ROOT):
         targets.append("ref")
+        if dropin:
+            targets.append("dropin")
     subprocess.run(["make", "-s", "-C", HERE, *targets], check=True)
 
 
@@ -51,9 +55,19 @@ class _Lib:
             "dequantize": (_I, [_P, _P, _U, _I64]),
             "last_error": (ctypes.c_char_p, []),
         }
+        optional = {  # present in rebuilt libraries only
+            "dequantize_block": (_I, [_P, _P, _U, _I64]),
+            "dequantize_block_f16": (_I, [_P, _P, _U, _I64]),
+            "dequantize_f16": (_I, [_P, _P, _U, _I64]),
+            "float_to_half": (ctypes.c_uint16, [ctypes.c_float]),
+        }
         for name, (res, args) in sig.items():
             fn = getattr(self.lib, prefix + name)
             fn.restype, fn.argtypes = res, args
+        for name, (res, args) in optional.items():
+            fn = getattr(self.lib, prefix + name, None)
+            if fn is not None:
+                fn.restype, fn.argtypes = res, args
 
     def _fn(self, name):
         return getattr(self.lib, self.prefix + name)
@@ -94,6 +108,25 @@ class _Lib:
         self._check(self._fn("dequantize")(_ptr(np.ascontiguousarray(src, dtype=np.uint8)),
                                            _ptr(out), int(qtype), int(n)))
         return out
+
+    def dequantize_block(self, src, qtype, n):
+        """dequantize_block: any n (the reference library's own entry takes any n too)."""
+        out = np.empty(n, np.float32)
+        name = "dequantize_block" if self.prefix == "oracle_" else "dequantize"
+        self._check(self._fn(name)(_ptr(np.ascontiguousarray(src, dtype=np.uint8)), _ptr(out),
+                                   int(qtype), int(n)))
+        return out
+
+    def dequantize_block_f16(self, src, qtype, n):
+        out = np.empty(n, np.uint16)
+        name = "dequantize_block_f16" if self.prefix == "oracle_" else "dequantize_f16"
+        self._check(self._fn(name)(_ptr(np.ascontiguousarray(src, dtype=np.uint8)), _ptr(out),
+                                   int(qtype), int(n)))
+        return out
+
+    def float_to_half(self, x):
+        f = self._fn("float_to_half")
+        return np.array([f(float(v)) for v in np.asarray(x, np.float32)], np.uint16)
 
 
 class Oracle(_Lib):
@@ -180,6 +213,16 @@ class Reference(_Lib):
             tensors.append((p[0], int(p[1]), tuple(int(v) for v in p[3:3 + nd]), int(p[3 + nd]),
                             int(p[4 + nd])))
         return cfg, tensors
+
+
+class DropIn(Reference):
+    """The reference's engine.cpp, gguf.cpp and thread_pool.cpp compiled against this
+    repository's headers and linked to libcllm_quant.so (oracle/Makefile, `dropin`): the
+    reference engine with every Quant call served by the MI355X kernels. A test harness for
+    the drop-in boundary; the code under test is libcllm_quant.so / libcllm_hip.so."""
+
+    def __init__(self, path: str = DROPIN_SO):
+        super().__init__(path)
 
 
 def oracle() -> Oracle:

@@ -309,6 +309,61 @@ int oracle_dequantize(const void* src, float* dst, uint32_t t, int64_t n) {
     return ORACLE_OK;
 }
 
+/* ---- dequantize_block (src/core/quant.cpp:371-389) ----------------------------------------
+ * ceil(n / bs) whole blocks are decoded and the first n elements kept: the reference's deq_*
+ * loops read a partial last block whole and guard every store with "< n". */
+int oracle_dequantize_block(const void* src, float* dst, uint32_t t, int64_t n) {
+    if (!known_type(t)) return fail(ORACLE_ERR_TYPE, "unsupported ggml type for dequantize");
+    if (n <= 0) return ORACLE_OK;
+    const int64_t bs = oracle_block_size(t), nfull = (n + bs - 1) / bs * bs;
+    if (nfull == n) return oracle_dequantize(src, dst, t, n);
+    float* tmp = (float*)malloc((size_t)nfull * sizeof(float));
+    if (!tmp) return fail(ORACLE_ERR_SYS, "out of memory");
+    const int rc = oracle_dequantize(src, tmp, t, nfull);
+    if (rc == ORACLE_OK) memcpy(dst, tmp, (size_t)n * sizeof(float));
+    free(tmp);
+    return rc;
+}
+
+/* ---- float_to_half (include/cllm/core/quant.hpp:58-87) ------------------------------------
+ * Normal results keep the top ten mantissa bits (no rounding); results below the normal range
+ * are rounded to nearest, ties to even; |f| below 2^-25 gives a signed zero, overflow an
+ * infinity, NaN the quiet NaN 0x7E00 (with the sign). */
+uint16_t oracle_float_to_half(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t be = (x >> 23) & 0xFFu;
+    uint32_t m = x & 0x7FFFFFu;
+    const int32_t e = (int32_t)be - 127 + 15;
+    if (be == 0xFFu) return (uint16_t)(sign | (m ? 0x7E00u : 0x7C00u));
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (e >= 1) return (uint16_t)(sign | ((uint32_t)e << 10) | (m >> 13));
+    if (e < -10) return (uint16_t)sign;
+    m |= 0x800000u;
+    const uint32_t sh = (uint32_t)(14 - e);
+    const uint32_t bias = (1u << (sh - 1)) - 1u, odd = (m >> sh) & 1u;
+    return (uint16_t)(sign | ((m + bias + odd) >> sh));
+}
+
+/* ---- dequantize_block_f16 (src/core/quant.cpp:398-407) --------------------------------------
+ * F16 blocks are copied as they are; every other type is dequantized to float, then each value
+ * goes through float_to_half. */
+int oracle_dequantize_block_f16(const void* src, uint16_t* dst, uint32_t t, int64_t n) {
+    if (n <= 0) return known_type(t) ? ORACLE_OK : fail(ORACLE_ERR_TYPE, "unsupported ggml type for dequantize");
+    if (t == ORACLE_F16) {
+        memcpy(dst, src, (size_t)n * 2);
+        return ORACLE_OK;
+    }
+    float* tmp = (float*)malloc((size_t)n * sizeof(float));
+    if (!tmp) return fail(ORACLE_ERR_SYS, "out of memory");
+    const int rc = oracle_dequantize_block(src, tmp, t, n);
+    if (rc == ORACLE_OK)
+        for (int64_t i = 0; i < n; ++i) dst[i] = oracle_float_to_half(tmp[i]);
+    free(tmp);
+    return rc;
+}
+
 /* ---- fp32 -> Q8_0 (src/core/quant.cpp:420-452) ------------------------------------------ */
 int oracle_quantize_row_q8_0(const float* x, int64_t n, int8_t* qs, float* scales,
                              int32_t* bsums) {

@@ -9,8 +9,12 @@
  * reference tree):
  *   oracle_half_to_float        include/cllm/core/quant.hpp:31-56
  *   oracle_block_size/type_size src/core/quant.cpp:340-369
- *   oracle_dequantize           src/core/quant.cpp:39-336 (Q8_0 40-51, Q4_0 55-68,
- *                               Q4_K 82-108, Q5_0 113-132, Q6_K 135-161, Q5_K 302-336)
+ *   oracle_dequantize           src/core/quant.cpp:28-336 (Q8_0 40-51, Q4_0 55-68,
+ *                               Q4_K 82-108, Q5_0 113-132, Q6_K 135-161, Q5_K 302-336 and
+ *                               the seven fallback types)
+ *   oracle_dequantize_block     src/core/quant.cpp:371-389
+ *   oracle_float_to_half        include/cllm/core/quant.hpp:58-87
+ *   oracle_dequantize_block_f16 src/core/quant.cpp:398-407
  *   oracle_quantize_row_q8_0    src/core/quant.cpp:420-452
  *   oracle_vec_dot_row          src/core/quant.cpp:1359-1372 dispatching to the AVX2 forms
  *                               Q8_0 534-547, Q4_K 549-590, Q5_K 592-628, Q6_K 630-687,
@@ -46,8 +50,17 @@ float oracle_half_to_float(uint16_t h);
 int oracle_block_size(uint32_t type);
 size_t oracle_type_size(uint32_t type);
 
-/* Scalar dequantization of the six vec_dot weight types (the layout oracle). */
+/* Scalar dequantization of the thirteen types (the layout oracle); n % block_size == 0. */
 int oracle_dequantize(const void* src, float* dst, uint32_t type, int64_t n);
+
+/* dequantize_block (src/core/quant.cpp:371-389): any n, a partial last block read whole. */
+int oracle_dequantize_block(const void* src, float* dst, uint32_t type, int64_t n);
+
+/* float_to_half of the reference header (include/cllm/core/quant.hpp:58-87). */
+uint16_t oracle_float_to_half(float f);
+
+/* dequantize_block_f16 (src/core/quant.cpp:398-407). */
+int oracle_dequantize_block_f16(const void* src, uint16_t* dst, uint32_t type, int64_t n);
 
 /* fp32 -> Q8_0: qs[n], scales[n/32], bsums[n/32]. Bit-exact restatement. */
 int oracle_quantize_row_q8_0(const float* x, int64_t n, int8_t* qs, float* scales,

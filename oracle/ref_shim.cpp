@@ -72,6 +72,17 @@ int ref_dequantize(const void* src, float* dst, uint32_t t, int64_t n) {
     }
 }
 
+int ref_dequantize_f16(const void* src, uint16_t* dst, uint32_t t, int64_t n) {
+    try {
+        cllm::dequantize_block_f16(src, dst, (cllm::GgmlType)t, n);
+        return 0;
+    } catch (const std::exception& e) {
+        return set_err(e);
+    }
+}
+
+uint16_t ref_float_to_half(float f) { return cllm::float_to_half(f); }
+
 int ref_matmul_quant(const float* x, const void* w, uint32_t t, const float* bias, int in_dim,
                      int out_dim, float* y, int n_threads) {
     try {

@@ -240,7 +240,67 @@ def refkat_fixtures(ref: oracle.Reference) -> None:
     np.savez_compressed(os.path.join(OUT, "refkat.npz"), **data)
 
 
-FIXTURES = {"quant": quant_fixtures, "refkat": refkat_fixtures, "types": extra_type_fixtures,
+def special_floats() -> np.ndarray:
+    """fp32 values around every case of float_to_half: signed zeros, the smallest and largest
+    binary16 subnormals and normals, ties of the subnormal rounding, values just below the
+    overflow threshold, infinities and NaNs with payloads."""
+    bits = [0x00000000, 0x80000000, 0x33000000, 0x33000001, 0x32FFFFFF, 0x33800000, 0x337FFFFF,
+            0x33C00000, 0x34200000, 0x387FC000, 0x387FE000, 0x38800000, 0x38801FFF, 0x3F800000,
+            0x3F801FFF, 0x3F802000, 0x477FE000, 0x477FEFFF, 0x477FF000, 0x47800000, 0x7F7FFFFF,
+            0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001, 0xFFC12345, 0x7FBFFFFF, 0x00000001,
+            0x807FFFFF, 0xB3400000, 0x38000000, 0x38400001]
+    rng = np.random.default_rng(11)
+    rnd = (rng.standard_normal(224) * np.exp2(rng.integers(-28, 18, 224))).astype(np.float32)
+    return np.concatenate([np.array(bits, np.uint32).view(np.float32), rnd])
+
+
+def deq_fixtures(ref: oracle.Reference) -> None:
+    """dequantize_block and dequantize_block_f16 (src/core/quant.cpp:371-412) of the thirteen
+    types: a run of random blocks read in full and with n ending inside the last block; F16
+    over all 65536 encodings; F32 over the special values of float_to_half."""
+    data = {}
+    for qt in sorted(S.TYPE_NAMES):
+        bs = S.BLOCK[qt]
+        nb = {1: 320, 32: 9, 256: 3}[bs]
+        seed = 7100 + qt
+        w = S.make_weight(qt, 1, nb * bs, seed)
+        name = S.TYPE_NAMES[qt]
+        for tag, n in (("full", nb * bs), ("part", nb * bs - (bs // 2 + 3 if bs > 1 else 7))):
+            data[f"{name}_{tag}__meta"] = np.array([qt, n, nb, seed], np.int64)
+            data[f"{name}_{tag}__w_sha"] = np.array(sha(w))
+            data[f"{name}_{tag}__y"] = ref.dequantize_block(w, qt, n)
+            data[f"{name}_{tag}__y16"] = ref.dequantize_block_f16(w, qt, n)
+        print(name, flush=True)
+    allh = np.arange(65536, dtype=np.uint16)
+    data["f16_all__src"] = allh
+    data["f16_all__y"] = ref.dequantize_block(allh.view(np.uint8), S.F16, 65536)
+    data["f16_all__y16"] = ref.dequantize_block_f16(allh.view(np.uint8), S.F16, 65536)
+    sf = special_floats()
+    data["f32_special__src"] = sf
+    data["f32_special__y"] = ref.dequantize_block(sf.view(np.uint8), S.F32, sf.size)
+    data["f32_special__y16"] = ref.dequantize_block_f16(sf.view(np.uint8), S.F32, sf.size)
+    np.savez_compressed(os.path.join(OUT, "deq.npz"), **data)
+
+
+def m_sweep_large_fixtures(ref: oracle.Reference) -> None:
+    """The M-sweep's Q5_K 14336x4096 matrix at M = 256 and a 512-row batch of the same
+    distribution: every output of a few activation rows (the reference's batch rows equal its
+    single-row results, so a row subset is exact), for the MFMA plans those batches take."""
+    data = {}
+    qt, n, k, w = S.config_weight("c4_m_sweep", "q5_k")
+    for m, rows in ((256, [0, 77, 255]), (512, [3, 300, 511])):
+        x = S.config_activation("c4_m_sweep", m, k)
+        xs = x[rows]
+        y = ref.matmul(xs, w, qt, None, k, n, len(rows), threads=THREADS)
+        data[f"q5_k_m{m}__rows"] = np.array(rows, np.int64)
+        data[f"q5_k_m{m}__y"] = y
+        data[f"q5_k_m{m}__x_sha"] = np.array(sha(x))
+        print("m sweep", m, flush=True)
+    data["q5_k__w_sha"] = np.array(sha(w))
+    np.savez_compressed(os.path.join(OUT, "batch_large.npz"), **data)
+
+
+FIXTURES = {"quant": quant_fixtures, "deq": deq_fixtures, "batch_large": m_sweep_large_fixtures, "refkat": refkat_fixtures, "types": extra_type_fixtures,
             "gemv": gemv_fixtures, "batch": batch_fixtures, "fdot": fdot_fixtures,
             "model": model_fixtures}
 

@@ -155,3 +155,27 @@ def test_matches_compiled_reference_loader(tmp_path):
         for (name, gtype, shape, off, delta), t in zip(rtensors, got):
             assert (name, gtype, shape, off) == (t.name, t.type, t.shape, t.offset)
             assert delta == cfg.data_offset + t.offset
+
+
+def test_truncated_file_is_rejected(tmp_path):
+    """A tensor whose bytes run past the end of the file fails at open (the device copy is the
+    data section, so such a pointer would send kernels out of bounds)."""
+    path = tmp_path / "m.gguf"
+    _llama_file(path)
+    raw = path.read_bytes()
+    cut = tmp_path / "cut.gguf"
+    cut.write_bytes(raw[:-100])  # odd.weight (280 bytes, the last tensor) loses its tail
+    with pytest.raises(RuntimeError, match="odd.weight extends past the end of the file"):
+        C.GgufFile(cut)
+    cut.write_bytes(raw)  # the whole file opens
+    with C.GgufFile(cut) as g:
+        assert len(g) == 6
+
+
+def test_too_many_dimensions_is_rejected(tmp_path):
+    path = tmp_path / "m.gguf"
+    data = np.zeros(32, np.float32).tobytes()
+    G.write_gguf(path, [("general.architecture", G.STR, "llama")],
+                 [("t5.weight", (1, 1, 2, 2, 8), S.F32, data)])
+    with pytest.raises(RuntimeError, match="t5.weight: 5 dimensions"):
+        C.GgufFile(path)

@@ -17,16 +17,17 @@ from test_gpu_parity import check_close, _dev, TYPES
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=["default", "int8", "f16"], autouse=True)
-def gemm_kernel(request, monkeypatch):
+KERNELS = {"default": 0, "int8": 1, "f16": 2}
+
+
+@pytest.fixture(params=list(KERNELS), autouse=True)
+def gemm_kernel(request, gpu):
     """Every test runs on each MFMA kernel choice: the default (weight-row fp16 kernel
     k_gemmw.hip where it has the type, else int8), int8 (k_gemm.hip) and activation-row fp16
-    (k_gemm16.hip)."""
-    if request.param == "default":
-        monkeypatch.delenv("CLLM_HIP_GEMM", raising=False)
-    else:
-        monkeypatch.setenv("CLLM_HIP_GEMM", request.param)
-    return request.param
+    (k_gemm16.hip), chosen through the library's tuning knob."""
+    gpu.tune("gemm_kernel", KERNELS[request.param])
+    yield request.param
+    gpu.tune("gemm_kernel")
 
 
 def test_prefill_layer_slices_vs_reference_golden(gpu, orc):
@@ -119,21 +120,49 @@ def test_full_prefill_layer_sampled_rows(gpu, orc):
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("splits", [None, "4"])
+@pytest.mark.parametrize("splits", [None, 4])
 @pytest.mark.parametrize("qt", TYPES)
-def test_mfma_tails_and_split_k(gpu, orc, qt, splits, gemm_kernel, monkeypatch):
+def test_mfma_tails_and_split_k(gpu, orc, qt, splits, gemm_kernel):
     """Output rows and activation rows that end inside a tile (n = 520, m = 80), K = 2048, with
     the planned K split and with K forced into 4 splits (partial sums plus the reduction)."""
-    if splits:
-        monkeypatch.setenv("CLLM_HIP_GEMMW_SPLITS", splits)
-    else:
-        monkeypatch.delenv("CLLM_HIP_GEMMW_SPLITS", raising=False)
+    gpu.tune("gemm_splits", splits or 0)
     k, n, m = 2048, 520, 80
     w = S.make_weight(qt, n, k, 90 + qt)
     x = S.make_activation(m, k, 91 + qt, outliers=True)
     bias = np.linspace(-1.0, 1.0, n).astype(np.float32)
     print("tails", S.TYPE_NAMES[qt], "splits", splits, flush=True)
     y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, _dev(bias), k, n).cpu().numpy()
+    gpu.tune("gemm_splits")
     exact, abs_sum = orc.matmul_f64(x, w, qt, bias, k, n, m)
     yo = orc.matmul(x, w, qt, bias, k, n, m)
     check_close(y, yo, exact, abs_sum, f"tails {S.TYPE_NAMES[qt]} splits={splits}")
+
+
+@pytest.mark.parametrize("m", [256, 512])
+def test_m_sweep_q5_k_large_batches_vs_reference_golden(gpu, orc, m, gemm_kernel):
+    """The M-sweep's Q5_K 14336x4096 matrix at full size with M = 256 (the plan the bench
+    times there) and M = 512 (the largest weight-row tile): every output of three activation
+    rows against the reference's (tests/golden/batch_large.npz), eight rows against the oracle,
+    and the plan the batch ran named."""
+    import hashlib
+    import torch
+    if gemm_kernel != "default":
+        pytest.skip("the default plan's large tiles are the point here")
+    c = split_cases(load_golden("batch_large.npz"))
+    qt, n, k, w = S.config_weight("c4_m_sweep", "q5_k")
+    assert hashlib.sha256(w.tobytes()).hexdigest() == str(c["q5_k"]["w_sha"])
+    x = S.config_activation("c4_m_sweep", m, k)
+    plan = gpu.matmul_plan(qt, k, n, m)
+    print("q5_k 14336x4096 m", m, "plan", plan, flush=True)
+    assert plan.startswith("k_gemmw_q4k<8,1,%d,Q5_K>" % (2 if m == 256 else 4)), plan
+    y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, None, k, n)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    g = c[f"q5_k_m{m}"]
+    rows = g["rows"]
+    exact, abs_sum = orc.matmul_f64(x[rows], w, qt, None, k, n, len(rows))
+    check_close(y[rows], g["y"], exact, abs_sum, f"q5_k m{m} golden rows")
+    sample = np.sort(np.random.default_rng(m).choice(m, size=8, replace=False))
+    yo = orc.matmul(x[sample], w, qt, None, k, n, 8, threads=8)
+    exact, abs_sum = orc.matmul_f64(x[sample], w, qt, None, k, n, 8)
+    check_close(y[sample], yo, exact, abs_sum, f"q5_k m{m} oracle rows")

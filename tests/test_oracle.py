@@ -415,3 +415,63 @@ def test_swiglu_closed_forms_and_f64(orc):
     g64 = g.astype(np.float64)
     want = g64 / (1 + np.exp(-g64)) * u
     np.testing.assert_allclose(orc.swiglu(g, u), want, rtol=1e-6, atol=1e-30)
+
+
+# ------------------------------------------------ dequantize_block / dequantize_block_f16
+
+def _deq_cases():
+    return split_cases(load_golden("deq.npz"))
+
+
+def test_dequantize_block_oracle_matches_reference_golden(orc):
+    """oracle_dequantize_block / _f16 against the compiled reference's dequantize_block and
+    dequantize_block_f16 (src/core/quant.cpp:371-412), bit for bit: thirteen types, n at a
+    block boundary and inside the last block, all 65536 binary16 encodings, and fp32 values
+    at every case of float_to_half."""
+    import hashlib
+    for tag, c in _deq_cases().items():
+        if "meta" in c:
+            qt, n, nb, seed = (int(v) for v in c["meta"])
+            w = S.make_weight(qt, 1, nb * S.BLOCK[qt], seed)
+            assert hashlib.sha256(w.tobytes()).hexdigest() == str(c["w_sha"]), tag
+            src, t = w, qt
+        else:
+            src = c["src"].view(np.uint8)
+            t = S.F16 if tag.startswith("f16") else S.F32
+            n = c["src"].size
+        y = orc.dequantize_block(src, t, n)
+        assert np.array_equal(y.view(np.uint32), c["y"].view(np.uint32)), tag
+        assert np.array_equal(orc.dequantize_block_f16(src, t, n), c["y16"]), tag
+
+
+def test_float_to_half_closed_forms(orc):
+    """Pins oracle_float_to_half by what the rule fixes: every binary16 value converts back
+    to itself; normal results truncate (the next float below 2^k(1 + 2^-10) keeps 2^k);
+    subnormal results round to nearest with ties to even; overflow and NaN; and, for
+    the quantized blocks, the f16 output is float_to_half of the fp32 output."""
+    h = np.arange(65536, dtype=np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    finite = np.isfinite(f)
+    assert np.array_equal(orc.float_to_half(f[finite]), h[finite])
+    one_minus = np.nextafter(np.float32(1.0 + 2 ** -10), np.float32(0))
+    assert orc.float_to_half(np.array([one_minus], np.float32))[0] == 0x3C00  # truncated
+    tiny = np.float32(2.0 ** -24)  # binary16's smallest subnormal
+    got = orc.float_to_half(np.array([tiny * 0.5, tiny * 1.5, tiny * 2.5, tiny * 0.75], np.float32))
+    assert list(got) == [0x0000, 0x0002, 0x0002, 0x0001]  # ties to even, 0.75 rounds up
+    big = orc.float_to_half(np.array([65520.0, 1e30, -np.inf, np.nan], np.float32))
+    assert list(big) == [0x7BFF, 0x7C00, 0xFC00, 0x7E00]
+    for tag, c in _deq_cases().items():
+        if "meta" in c:
+            assert np.array_equal(orc.float_to_half(c["y"]), c["y16"]), tag
+
+
+def test_dequantize_block_partial_equals_prefix(orc):
+    """A partial last block yields the prefix of the whole block's values (the reference
+    guards its stores with < n and reads the block whole)."""
+    for qt in ALL_TYPES:
+        bs = S.BLOCK[qt]
+        w = S.make_weight(qt, 1, 2 * max(bs, 32), 31 + qt)
+        full = orc.dequantize_block(w, qt, 2 * max(bs, 32))
+        for n in (1, max(bs, 32) + 5, 2 * max(bs, 32) - 1):
+            assert np.array_equal(orc.dequantize_block(w, qt, n).view(np.uint32),
+                                  full[:n].view(np.uint32)), (qt, n)
