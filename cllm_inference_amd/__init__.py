@@ -63,6 +63,8 @@ SIGNATURES = {
     "cllm_hip_quantize_q8_0_dev": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_matmul_quant_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
+    "cllm_hip_matmul_quant_static_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
+    "cllm_hip_static_scratch_bytes": (_SZ, []),
     "cllm_hip_matmul_route": (ctypes.c_char_p, [_U, _I, _I, _I]),
     "cllm_hip_matmul_plan": (ctypes.c_char_p, [_U, _I, _I, _I]),
     "cllm_hip_tune": (_I, [ctypes.c_char_p, _P, _I]),

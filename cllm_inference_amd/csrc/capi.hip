@@ -190,9 +190,16 @@ bool immutable_file_mapping(const Mapping& m) {
     return m.file && m.perms[0] == 'r' && m.perms[1] == '-' && m.perms[3] == 'p' && m.inode != 0;
 }
 
+// Fixed scratch of cllm_hip_matmul_quant_static_dev, one copy per GPU for the life of the
+// process. Host code never uses this name as an address: each device's copy is found with
+// hipGetSymbolAddress when its state is built (DeviceState::scratch).
+constexpr size_t kStaticScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
 struct DeviceState {
     std::mutex mtx;
     hipStream_t stream = nullptr;
+    uint8_t* scratch = nullptr;  // this device's copy of the static scratch array
     DevBuf x, y, bias, wstage, qin;
     Workspace act;
     std::map<uintptr_t, Region> regions;  // host base -> device copy
@@ -228,6 +235,10 @@ int acquire(DeviceState** out) {
                            prop.gcnArchName);
         auto st = std::make_unique<DeviceState>();
         HIP_TRY(hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking));
+        // the device is current: its copy of the static scratch array
+        HIP_TRY(hipGetSymbolAddress((void**)&st->scratch, HIP_SYMBOL(scratch)));
+        if (st->scratch == nullptr || ((uintptr_t)st->scratch & 255u))
+            return set_err(CLLM_HIP_E_RUNTIME, "cllm_hip: static scratch of device %d not found", dev);
         it = g_states.emplace(dev, std::move(st)).first;
     }
     *out = it->second.get();
@@ -936,6 +947,54 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
     HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
     return CLLM_HIP_OK;
 }
+
+int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t type,
+                                     const float* bias, int in_dim, int out_dim, int n_rows,
+                                     float* y, void* stream) {
+    int rc = check_matmul(n_rows > 1 ? "matmul_quant_batch" : "matmul_quant", type, in_dim, out_dim);
+    if (rc) return rc;
+    if (n_rows <= 0 || out_dim == 0) return CLLM_HIP_OK;
+    if (!x || !w || !y) return set_err(CLLM_HIP_E_ARG, "matmul_quant: null pointer");
+    if (!aligned16(x) || !aligned16(w) || ((uintptr_t)y & 3u) || ((uintptr_t)bias & 3u))
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant: misaligned device pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (!has_kernel(type)) {
+        HIP_TRY(launch_gemv_f(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, s));
+        return CLLM_HIP_OK;
+    }
+    // The same routes as cllm_hip_matmul_quant_dev, their scratch carved from this device's
+    // static array: the activation arrays first, then the split-K region (at a multiple of
+    // 256 bytes). Nothing is allocated.
+    WsView v;
+    size_t act = 0, pb = 0;
+    if (needs_workspace(type, in_dim, n_rows)) {
+        act = act_bytes(in_dim, n_rows);
+        if (use_mfma(type, in_dim, n_rows)) pb = part_bytes_for(type, in_dim, out_dim, n_rows);
+    }
+    if (act + pb > kStaticScratchBytes)
+        return set_err(CLLM_HIP_E_ARG,
+                       "matmul_quant: %d rows of %d need %zu bytes of scratch, more than the %zu "
+                       "of the fixed buffer; pass fewer rows per call",
+                       n_rows, in_dim, act + pb, kStaticScratchBytes);
+    if (act) carve_act((char*)st->scratch, in_dim, n_rows, v);
+    if (pb) {
+        v.part = (float*)(st->scratch + act);
+        v.part_cap = pb;
+        // the tile counters must start at zero; the last call on this GPU may have left
+        // activations in these bytes (a fill kernel, so the call can be captured in a graph)
+        HIP_TRY(gemmw_workspace_init(v.part, gemmw_counter_bytes(), s));
+    }
+    if (!use_mfma(type, in_dim, n_rows)) {
+        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
+        return CLLM_HIP_OK;
+    }
+    HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
+    return CLLM_HIP_OK;
+}
+
+size_t cllm_hip_static_scratch_bytes(void) { return kStaticScratchBytes; }
 
 int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t type,
                                        const float* bias, int in_dim, int out_dim, int n_rows,

@@ -1199,6 +1199,8 @@ size_t slices_bytes(const Plan& p, int n, int m) {
 }
 constexpr size_t kCounterBytes = 64 * 1024;  // 16384 tiles
 
+size_t gemmw_counter_bytes() { return kCounterBytes; }
+
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m) {
     if (!gemmw_supported(type) || k % 256 != 0) return 0;
     const Plan p = plan_for(type, k, n, m);

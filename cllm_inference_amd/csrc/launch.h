@@ -114,6 +114,8 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream);
 size_t gemmw_partial_bytes(uint32_t type, int k, int n, int m);
+// The tile-counter block at the start of that region (the bytes that must be zero).
+size_t gemmw_counter_bytes();
 // Name of the weight-row kernel instantiation and its split count for this shape, e.g.
 // "k_gemmw_q4k<8,1,2,Q5_K> splits=1" (written into buf).
 void gemmw_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap);

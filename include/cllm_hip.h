@@ -181,6 +181,21 @@ int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t t
 int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,
                               int in_dim, int out_dim, int n_rows, float* y, void* stream);
 
+/* cllm_hip_matmul_quant_dev for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. Same routes, kernels and results (bit for bit); the scratch the routes need
+ * (quantized activations, the MFMA formats, split-K partial sums) is carved from a fixed
+ * array of cllm_hip_static_scratch_bytes() (64 MiB) per GPU, held from library load to process
+ * end, and nothing is allocated or freed (call cllm_hip_init first: it builds the per-device
+ * state once). A batch whose scratch exceeds the array fails with CLLM_HIP_E_ARG (M = 512
+ * rows of 14336 need ~27 MB; split larger batches). Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, or host threads) race and must be
+ * ordered by the caller. */
+int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t type,
+                                     const float* bias, int in_dim, int out_dim, int n_rows,
+                                     float* y, void* stream);
+size_t cllm_hip_static_scratch_bytes(void);
+
 /* ---- producers of a device-resident layer's activations (stream-ordered) -------------- */
 
 /* RMSNorm of n_rows rows of n floats fused with the Q8_0 quantization matmul_quant applies

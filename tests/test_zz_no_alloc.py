@@ -1,0 +1,69 @@
+"""cllm_hip_matmul_quant_static_dev, the matmul entry point that allocates nothing: called
+through the C ABI, its output must equal cllm_hip_matmul_quant_dev's bit for bit (the same
+kernels on the same plan; only the scratch comes from the fixed per-GPU array), on two calls
+in a row of each route, the second with a smaller input, so the second call runs on scratch
+the first one left behind. A batch whose scratch exceeds the array is refused with an error.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import cllm_inference_amd as C
+from cllm_inference_amd import synth as S
+
+pytestmark = pytest.mark.gpu
+
+
+def _static(lib, x, w, qt, bias, k, n, y):
+    import torch
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return lib.cllm_hip_matmul_quant_static_dev(p(x), p(w), int(qt), p(bias), int(k), int(n),
+                                                int(x.shape[0]), p(y), stream)
+
+
+# (type, n, k, [m of the first call, m of the second]): the MFMA route with split K (the
+# 4096 x 4096 Q4_K matrix at 512 rows plans two splits) and then without, Q6_K's kernel, a
+# 32-element block type, the GEMV route with a quantized batch (3..15 rows) and the fused
+# decode GEMV (1 row)
+CASES = [
+    (S.Q4_K, 4096, 4096, [512, 64]),
+    (S.Q6_K, 1024, 4096, [256, 16]),
+    (S.Q8_0, 768, 2048, [96, 32]),
+    (S.Q5_K, 600, 1024, [12, 5]),
+    (S.Q4_0, 512, 1024, [2, 1]),
+]
+
+
+@pytest.mark.parametrize("qt,n,k,ms", CASES, ids=[S.TYPE_NAMES[c[0]] for c in CASES])
+def test_static_scratch_matches_matmul_quant_dev(gpu, qt, n, k, ms):
+    import torch
+    lib = C.load_library()
+    assert lib.cllm_hip_init(0) == 0
+    w = torch.from_numpy(S.make_weight(qt, n, k, 300 + qt)).cuda()
+    bias = torch.linspace(-1, 1, n, dtype=torch.float32, device="cuda")
+    for call, m in enumerate(ms):
+        x = torch.from_numpy(S.make_activation(m, k, 40 + 7 * call + qt, outliers=True)).cuda()
+        print("static scratch", S.TYPE_NAMES[qt], n, k, "m", m, "plan", gpu.matmul_plan(qt, k, n, m),
+              flush=True)
+        want = gpu.matmul_quant_dev(x, w, qt, bias, k, n)
+        y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        rc = _static(lib, x, w, qt, bias, k, n, y)
+        assert rc == 0, lib.cllm_hip_last_error().decode()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32)), (S.TYPE_NAMES[qt], m)
+
+
+def test_static_scratch_refuses_oversized_batches(gpu):
+    import torch
+    lib = C.load_library()
+    cap = lib.cllm_hip_static_scratch_bytes()
+    assert cap == 64 << 20
+    k, n, m = 14336, 256, 2048  # ~106 MB of activation scratch
+    w = torch.zeros(S.row_bytes(S.Q6_K, k) * n, dtype=torch.uint8, device="cuda")
+    x = torch.zeros((m, k), dtype=torch.float32, device="cuda")
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    rc = _static(lib, x, w, S.Q6_K, None, k, n, y)
+    assert rc != 0
+    assert "fixed buffer" in lib.cllm_hip_last_error().decode()
