@@ -50,8 +50,11 @@ def time_loop(fn, steps, warmup):
 
     The `steps` calls are captured once into a HIP graph on a dedicated stream (after
     `warmup` eager calls on that stream, so every per-stream workspace already exists and
-    nothing allocates during capture); one untimed replay warms it, then three replays are
-    timed with HIP events, each bracketed by device synchronisation, and the median is kept.
+    nothing allocates during capture); untimed replays run for at least 30 ms of GPU time,
+    then three replays are timed with HIP events, each bracketed by device synchronisation,
+    and the median is kept. The 30 ms: after the host-side setup of a workload the first
+    ~10 ms of replays ran slower on MI355X (the Q6_K 128256x4096 head: 74.6 us per call in
+    the first 50-call replay after one warm replay, 66.6 us after 30 ms, for either kernel).
     """
     import torch
     s = torch.cuda.Stream()
@@ -64,7 +67,13 @@ def time_loop(fn, steps, warmup):
     with torch.cuda.graph(g, stream=s):
         for i in range(steps):
             fn(i)
+    a, b = _events()
+    a.record()
     g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    for _ in range(min(200, int(30.0 / max(a.elapsed_time(b), 1e-3)))):
+        g.replay()
     torch.cuda.synchronize()
     times = []
     for _ in range(3):
@@ -110,7 +119,7 @@ def decode_point(C, S, cfg, label, m, steps, warmup, cold=True):
     return dict(type=S.TYPE_NAMES[qt], n=n, k=k, m=m, copies=copies, bytes=nbytes,
                 ms_step=ms_step, ms_gemv=ms_gemv,
                 gbs_step=nbytes / ms_step / 1e6, gbs_gemv=nbytes / ms_gemv / 1e6,
-                route=C.matmul_route(qt, k, n, m))
+                route=C.matmul_route(qt, k, n, m), plan=C.matmul_plan(qt, k, n, m))
 
 
 def float_dot_points(C, S, steps, warmup):
@@ -484,12 +493,12 @@ def main():
                    "algorithmic_bytes_per_step": head["bytes"]},
         "frac_of_hbm_peak": round(head["gbs_step"] / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(1e3 / head["ms_step"], 1),
-        # A decode step is one kernel launch (k_gemv<Q4_K, MR=1> quantizing its activation in
-        # LDS), so the step's HIP-event time is that kernel's average duration.
+        # A decode step is one kernel launch (the GEMV quantizing its activation in LDS), so
+        # the step's HIP-event time is that kernel's average duration.
         "roofline": {"bound": "hbm", "achieved": round(head["gbs_step"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs_step"] / HBM_PEAK_GBS, 4),
-                     "kernel": "k_gemv<Q4_K, 1 row> (fused Q8_0 activation quantization)",
+                     "kernel": head["plan"] + " (fused Q8_0 activation quantization)",
                      "kernel_us": round(head["ms_step"] * 1e3, 3),
                      "traffic": traffic},
         "gemv_prequantized": {"kernel_us": round(head["ms_gemv"] * 1e3, 3),

@@ -1343,6 +1343,12 @@ int cllm_hip_tune(const char* knob, const int* values, int n_values) {
         t.gemm_ttiles.store(v(2));
     } else if (std::strcmp(knob, "gemm_splits") == 0) {
         t.gemm_splits.store(v(0));
+    } else if (std::strcmp(knob, "gemv_kernel") == 0) {
+        if (v(0) < 0 || v(0) > 3) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemv_kernel is 0 to 3");
+        t.gemv_kind.store(v(0));
+    } else if (std::strcmp(knob, "gemv_str_grid") == 0) {
+        if (v(0) < 0 || v(0) > 65535) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemv_str_grid out of range");
+        t.gemv_str_grid.store(v(0));
     } else if (std::strcmp(knob, "gemv_waves") == 0) {
         t.gemv_short_wps.store(v(0));
         t.gemv_deep_wps.store(v(1));
@@ -1355,7 +1361,9 @@ int cllm_hip_tune(const char* knob, const int* values, int n_values) {
 const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_rows) {
     static thread_local char buf[128];
     const char* route = cllm_hip_matmul_route(type, in_dim, out_dim, n_rows);
-    if (std::strcmp(route, "mfma") != 0) {
+    if (std::strcmp(route, "gemv") == 0) {
+        gemv_plan_name(type, in_dim, out_dim, n_rows, buf, sizeof buf);
+    } else if (std::strcmp(route, "mfma") != 0) {
         snprintf(buf, sizeof buf, "%s", route);
     } else {
         const GemmKind kind = gemm_kind(type);

@@ -149,6 +149,31 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, 1.0f + expf(-g)), u);
 }
 
+// A zero the compiler cannot see through, and a fence for it: the asm statement has side
+// effects, clobbers memory and takes the base pointers of the loads issued before it (a, b, c:
+// wave-uniform, or null), so for the compiler it may write their memory and no load of theirs
+// moves below it, not even with __restrict__ pointers or into a later branch; adding the zero
+// to a later address keeps that load below it. Every load stays one the compiler counts in its
+// own vmcnt waits.
+__device__ __forceinline__ uint32_t opaque_zero(const void* a = nullptr, const void* b = nullptr,
+                                                const void* c = nullptr) {
+    uint32_t z;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z) : "s"(a), "s"(b), "s"(c) : "memory");
+    return z;
+}
+
+// Sum over all 64 lanes, valid in lane 63 only: row sums by quad and mirror moves, then
+// row_bcast:15 and row_bcast:31 carry them up (DPP only, no LDS-path permutes).
+__device__ __forceinline__ float wave_sum63(float v) {
+    v += dpp_f32<DPP_QUAD_SWAP1>(v);
+    v += dpp_f32<DPP_QUAD_SWAP2>(v);
+    v += dpp_f32<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_f32<DPP_ROW_MIRROR>(v);
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f32<DPP_QUAD_SWAP1>(v);
     v += dpp_f32<DPP_QUAD_SWAP2>(v);

@@ -170,25 +170,34 @@ struct TraitsK45 {
         }
         return r;
     }
-    template <int MR>
-    static __device__ __forceinline__ void compute(const Raw& r, int u, const ActLds& a,
-                                                   float (&acc)[MR]) {
-        const int c = u & 3;
-        const int b0 = 8 * (u >> 2) + 2 * c;
-        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+    // The weight side of unit u: nibbles (plus the Q5_K bit) and the two sub-blocks' scale and
+    // minimum products.
+    struct W {
         uint32_t lo[8], hi[8];
+        float ws0, ws1, wm0, wm1;
+    };
+    // The activation side of unit u for row t: the 64 quantized values, dx and dx * bsum of its
+    // two blocks.
+    struct X {
+        uint32_t x0[8], x1[8];
+        float2 xd, xm;
+    };
+    static __device__ __forceinline__ W wdec(const Raw& r, int u) {
+        const int c = u & 3;
+        W w;
+        const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            lo[i] = q[i] & 0x0F0F0F0Fu;
-            hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+            w.lo[i] = q[i] & 0x0F0F0F0Fu;
+            w.hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
         }
         if constexpr (Q5) {
             const uint32_t qh[8] = {r.hha.x, r.hha.y, r.hha.z, r.hha.w,
                                     r.hhb.x, r.hhb.y, r.hhb.z, r.hhb.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                lo[i] |= ((qh[i] >> (2 * c)) & 0x01010101u) << 4;
-                hi[i] |= ((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4;
+                w.lo[i] |= ((qh[i] >> (2 * c)) & 0x01010101u) << 4;
+                w.hi[i] |= ((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4;
             }
         }
         // 6-bit scales / mins of sub-blocks 2c and 2c+1 (get_scale_min_k4, quant.cpp:72-80).
@@ -200,28 +209,40 @@ struct TraitsK45 {
         const uint32_t sc2 = c < 2 ? (w0 & 0x3F3Fu) : ((w2 & 0x0F0Fu) | ((w0 >> 2) & 0x3030u));
         const uint32_t mn2 = c < 2 ? (w1 & 0x3F3Fu) : (((w2 >> 4) & 0x0F0Fu) | ((w1 >> 2) & 0x3030u));
         const float d = f16_to_f32(r.h.x & 0xFFFFu), dmin = f16_to_f32(r.h.x >> 16);
-        const float ws0 = d * (float)(sc2 & 0xFFu), ws1 = d * (float)(sc2 >> 8);
-        const float wm0 = dmin * (float)(mn2 & 0xFFu), wm1 = dmin * (float)(mn2 >> 8);
+        w.ws0 = d * (float)(sc2 & 0xFFu);
+        w.ws1 = d * (float)(sc2 >> 8);
+        w.wm0 = dmin * (float)(mn2 & 0xFFu);
+        w.wm1 = dmin * (float)(mn2 >> 8);
+        return w;
+    }
+    static __device__ __forceinline__ X x_of(const ActLds& a, int t, int u) {
+        const int b0 = 8 * (u >> 2) + 2 * (u & 3);
+        X x;
+        lds_x32(a, t, b0, x.x0);
+        lds_x32(a, t, b0 + 1, x.x1);
+        x.xd = *(const float2*)(a.xd + (size_t)t * a.nb + b0);
+        x.xm = *(const float2*)(a.xm + (size_t)t * a.nb + b0);
+        return x;
+    }
+    static __device__ __forceinline__ float fin(const W& w, const X& x, float v, int) {
+        int d0 = 0, d1 = 0;
 #pragma unroll
-        for (int t = 0; t < MR; ++t) {
-            uint32_t x0[8], x1[8];
-            lds_x32(a, t, b0, x0);
-            lds_x32(a, t, b0 + 1, x1);
-            int d0 = 0, d1 = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                d0 = sdot4(lo[i], x0[i], d0);
-                d1 = sdot4(hi[i], x1[i], d1);
-            }
-            const float2 xd = *(const float2*)(a.xd + (size_t)t * a.nb + b0);
-            const float2 xm = *(const float2*)(a.xm + (size_t)t * a.nb + b0);
-            float v = acc[t];
-            v = fmaf(ws0 * xd.x, (float)d0, v);
-            v = fmaf(-wm0, xm.x, v);
-            v = fmaf(ws1 * xd.y, (float)d1, v);
-            v = fmaf(-wm1, xm.y, v);
-            acc[t] = v;
+        for (int i = 0; i < 8; ++i) {
+            d0 = sdot4(w.lo[i], x.x0[i], d0);
+            d1 = sdot4(w.hi[i], x.x1[i], d1);
         }
+        v = fmaf(w.ws0 * x.xd.x, (float)d0, v);
+        v = fmaf(-w.wm0, x.xm.x, v);
+        v = fmaf(w.ws1 * x.xd.y, (float)d1, v);
+        v = fmaf(-w.wm1, x.xm.y, v);
+        return v;
+    }
+    template <int MR>
+    static __device__ __forceinline__ void compute(const Raw& r, int u, const ActLds& a,
+                                                   float (&acc)[MR]) {
+        const W w = wdec(r, u);
+#pragma unroll
+        for (int t = 0; t < MR; ++t) acc[t] = fin(w, x_of(a, t, u), acc[t], u);
     }
 };
 
@@ -267,55 +288,79 @@ struct TraitsQ6K {
         r.sh = (uint32_t)o & 3u;
         return r;
     }
-    template <int MR>
-    static __device__ __forceinline__ void compute(const Raw& r, int u, const ActLds& a,
-                                                   float (&acc)[MR]) {
-        const int g = (u >> 1) & 1, h = u & 1;
-        const int bb = 8 * (u >> 2) + 4 * g;
+    struct W {
+        uint32_t v[4][4];  // [sub-block i][dword]: unsigned 6-bit values
+        int scv[4];
+        float d;
+    };
+    struct X {
+        u32x4 x[4];   // the 16 quantized values of sub-block i the unit covers
+        int hs[4];    // their sums
+        float2 xd;    // dx of blocks bb + 2h, bb + 2h + 1
+    };
+    static __device__ __forceinline__ W wdec(const Raw& r, int u) {
+        const int h = u & 1;
         uint32_t la[4], lb[4], qh[4], sc[2];
         align_a2<4>(r.qa, r.sh, la);
         align_a2<4>(r.qb, r.sh, lb);
         align_a2<4>(r.qh, r.sh, qh);
         align_a2<2>(r.sc, r.sh, sc);
-        uint32_t v[4][4];  // [sub-block i][dword]: unsigned 6-bit values
+        W w;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            v[0][t] = (la[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x03030303u) << 4);
-            v[1][t] = (lb[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x0C0C0C0Cu) << 2);
-            v[2][t] = ((la[t] >> 4) & 0x0F0F0F0Fu) | (qh[t] & 0x30303030u);
-            v[3][t] = ((lb[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> 2) & 0x30303030u);
+            w.v[0][t] = (la[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x03030303u) << 4);
+            w.v[1][t] = (lb[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x0C0C0C0Cu) << 2);
+            w.v[2][t] = ((la[t] >> 4) & 0x0F0F0F0Fu) | (qh[t] & 0x30303030u);
+            w.v[3][t] = ((lb[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> 2) & 0x30303030u);
         }
         // sc[8g + 2i + h]: byte h (i = 0), 2 + h (i = 1) of dword 0, same of dword 1 (i = 2, 3)
-        int scv[4];
-        scv[0] = __builtin_amdgcn_sbfe((int)sc[0], 8 * h, 8);
-        scv[1] = __builtin_amdgcn_sbfe((int)sc[0], 16 + 8 * h, 8);
-        scv[2] = __builtin_amdgcn_sbfe((int)sc[1], 8 * h, 8);
-        scv[3] = __builtin_amdgcn_sbfe((int)sc[1], 16 + 8 * h, 8);
-        const float d = f16_to_f32(r.d);
+        w.scv[0] = __builtin_amdgcn_sbfe((int)sc[0], 8 * h, 8);
+        w.scv[1] = __builtin_amdgcn_sbfe((int)sc[0], 16 + 8 * h, 8);
+        w.scv[2] = __builtin_amdgcn_sbfe((int)sc[1], 8 * h, 8);
+        w.scv[3] = __builtin_amdgcn_sbfe((int)sc[1], 16 + 8 * h, 8);
+        w.d = f16_to_f32(r.d);
+        return w;
+    }
+    static __device__ __forceinline__ X x_of(const ActLds& a, int t, int u) {
+        const int g = (u >> 1) & 1, h = u & 1;
+        const int bb = 8 * (u >> 2) + 4 * g;
+        X x;
+        const u32x4 hs = *(const u32x4*)(a.hs + (size_t)t * 2 * a.nb + (size_t)h * a.nb + bb);
+        x.hs[0] = (int)hs.x;
+        x.hs[1] = (int)hs.y;
+        x.hs[2] = (int)hs.z;
+        x.hs[3] = (int)hs.w;
 #pragma unroll
-        for (int t = 0; t < MR; ++t) {
-            const u32x4 hs = *(const u32x4*)(a.hs + (size_t)t * 2 * a.nb + (size_t)h * a.nb + bb);
-            const int hsv[4] = {(int)hs.x, (int)hs.y, (int)hs.z, (int)hs.w};
-            int tot[4];
+        for (int i = 0; i < 4; ++i) x.x[i] = lds_x16(a, t, (bb + i) * 32 + 16 * h);
+        x.xd = *(const float2*)(a.xd + (size_t)t * a.nb + bb + 2 * h);
+        return x;
+    }
+    // The two lanes h = 0, 1 of a sub-block form the reference's integer
+    // sc_a * dot_a + sc_b * dot_b with one DPP move; lane h finishes sub-blocks 2h and 2h + 1.
+    static __device__ __forceinline__ float fin(const W& w, const X& x, float vacc, int u) {
+        const int h = u & 1;
+        int tot[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const u32x4 x = lds_x16(a, t, (bb + i) * 32 + 16 * h);
-                int dot = sdot4(v[i][0], x.x, 0);
-                dot = sdot4(v[i][1], x.y, dot);
-                dot = sdot4(v[i][2], x.z, dot);
-                dot = sdot4(v[i][3], x.w, dot);
-                const int part = scv[i] * (dot - 32 * hsv[i]);
-                tot[i] = part + dpp_i32<DPP_QUAD_SWAP1>(part);  // + partner lane h ^ 1
-            }
-            // lane h finishes sub-blocks 2h and 2h + 1
-            const int ia = h ? tot[2] : tot[0];
-            const int ib = h ? tot[3] : tot[1];
-            const float2 xd = *(const float2*)(a.xd + (size_t)t * a.nb + bb + 2 * h);
-            float vacc = acc[t];
-            vacc = fmaf(d * xd.x, (float)ia, vacc);
-            vacc = fmaf(d * xd.y, (float)ib, vacc);
-            acc[t] = vacc;
+        for (int i = 0; i < 4; ++i) {
+            int dot = sdot4(w.v[i][0], x.x[i].x, 0);
+            dot = sdot4(w.v[i][1], x.x[i].y, dot);
+            dot = sdot4(w.v[i][2], x.x[i].z, dot);
+            dot = sdot4(w.v[i][3], x.x[i].w, dot);
+            const int part = w.scv[i] * (dot - 32 * x.hs[i]);
+            tot[i] = part + dpp_i32<DPP_QUAD_SWAP1>(part);  // + partner lane h ^ 1
         }
+        const int ia = h ? tot[2] : tot[0];
+        const int ib = h ? tot[3] : tot[1];
+        vacc = fmaf(w.d * x.xd.x, (float)ia, vacc);
+        vacc = fmaf(w.d * x.xd.y, (float)ib, vacc);
+        return vacc;
+    }
+    template <int MR>
+    static __device__ __forceinline__ void compute(const Raw& r, int u, const ActLds& a,
+                                                   float (&acc)[MR]) {
+        const W w = wdec(r, u);
+#pragma unroll
+        for (int t = 0; t < MR; ++t) acc[t] = fin(w, x_of(a, t, u), acc[t], u);
     }
 };
 
@@ -344,21 +389,38 @@ struct TraitsQ80 {
         r.sh = (uint32_t)(o + 2) & 3u;
         return r;
     }
+    struct W {
+        uint32_t q[8];
+        float d;
+    };
+    struct X {
+        uint32_t x[8];
+        float xd;
+    };
+    static __device__ __forceinline__ W wdec(const Raw& r, int) {
+        W w;
+        align_a2<8>(r.q, r.sh, w.q);
+        w.d = f16_to_f32(r.d);
+        return w;
+    }
+    static __device__ __forceinline__ X x_of(const ActLds& a, int t, int b) {
+        X x;
+        lds_x32(a, t, b, x.x);
+        x.xd = a.xd[(size_t)t * a.nb + b];
+        return x;
+    }
+    static __device__ __forceinline__ float fin(const W& w, const X& x, float acc, int) {
+        int dot = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dot = sdot4(w.q[i], x.x[i], dot);
+        return fmaf(w.d * x.xd, (float)dot, acc);
+    }
     template <int MR>
     static __device__ __forceinline__ void compute(const Raw& r, int b, const ActLds& a,
                                                    float (&acc)[MR]) {
-        uint32_t q[8];
-        align_a2<8>(r.q, r.sh, q);
-        const float d = f16_to_f32(r.d);
+        const W w = wdec(r, b);
 #pragma unroll
-        for (int t = 0; t < MR; ++t) {
-            uint32_t x[8];
-            lds_x32(a, t, b, x);
-            int dot = 0;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) dot = sdot4(q[i], x[i], dot);
-            acc[t] = fmaf(d * a.xd[(size_t)t * a.nb + b], (float)dot, acc[t]);
-        }
+        for (int t = 0; t < MR; ++t) acc[t] = fin(w, x_of(a, t, b), acc[t], b);
     }
 };
 
@@ -398,42 +460,61 @@ struct TraitsQ450 {
         r.sh = (uint32_t)(o + 2) & 3u;
         return r;
     }
-    template <int MR>
-    static __device__ __forceinline__ void compute(const Raw& r, int b, const ActLds& a,
-                                                   float (&acc)[MR]) {
+    struct W {
+        uint32_t lo[4], hi[4];
+        float d;
+    };
+    struct X {
+        uint32_t x[8];
+        float xd;
+        int xb;
+    };
+    static __device__ __forceinline__ W wdec(const Raw& r, int) {
         uint32_t q[4];
         align_a2<4>(r.q, r.sh, q);
-        uint32_t lo[4], hi[4];
         uint32_t qh = 0;
         if constexpr (Q5) {
             uint32_t t1[1];
             align_a2<1>(r.qh, r.sh, t1);
             qh = t1[0];
         }
+        W w;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            lo[t] = q[t] & 0x0F0F0F0Fu;
-            hi[t] = (q[t] >> 4) & 0x0F0F0F0Fu;
+            w.lo[t] = q[t] & 0x0F0F0F0Fu;
+            w.hi[t] = (q[t] >> 4) & 0x0F0F0F0Fu;
             if constexpr (Q5) {
-                lo[t] |= spread4((qh >> (4 * t)) & 0xFu);
-                hi[t] |= spread4((qh >> (16 + 4 * t)) & 0xFu);
+                w.lo[t] |= spread4((qh >> (4 * t)) & 0xFu);
+                w.hi[t] |= spread4((qh >> (16 + 4 * t)) & 0xFu);
             }
         }
-        const float d = f16_to_f32(r.d);
+        w.d = f16_to_f32(r.d);
+        return w;
+    }
+    static __device__ __forceinline__ X x_of(const ActLds& a, int t, int b) {
+        X x;
+        lds_x32(a, t, b, x.x);
+        const size_t ix = (size_t)t * a.nb + b;
+        x.xd = a.xd[ix];
+        x.xb = a.xb[ix];
+        return x;
+    }
+    static __device__ __forceinline__ float fin(const W& w, const X& x, float acc, int) {
+        int dot = 0;
 #pragma unroll
-        for (int t = 0; t < MR; ++t) {
-            uint32_t x[8];
-            lds_x32(a, t, b, x);
-            int dot = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                dot = sdot4(lo[i], x[i], dot);
-                dot = sdot4(hi[i], x[4 + i], dot);
-            }
-            const size_t ix = (size_t)t * a.nb + b;
-            const int inner = dot - (Q5 ? 16 : 8) * a.xb[ix];
-            acc[t] = fmaf(d * a.xd[ix], (float)inner, acc[t]);
+        for (int i = 0; i < 4; ++i) {
+            dot = sdot4(w.lo[i], x.x[i], dot);
+            dot = sdot4(w.hi[i], x.x[4 + i], dot);
         }
+        const int inner = dot - (Q5 ? 16 : 8) * x.xb;
+        return fmaf(w.d * x.xd, (float)inner, acc);
+    }
+    template <int MR>
+    static __device__ __forceinline__ void compute(const Raw& r, int b, const ActLds& a,
+                                                   float (&acc)[MR]) {
+        const W w = wdec(r, b);
+#pragma unroll
+        for (int t = 0; t < MR; ++t) acc[t] = fin(w, x_of(a, t, b), acc[t], b);
     }
 };
 
@@ -669,6 +750,17 @@ struct StageQuant {
                 wv[0] = p[0];
                 wv[1] = p[1];
             }
+        }
+    }
+    // issue() in every wave, with no branch (waves past the slots load the last slot again):
+    // loads issued after these on one straight path leave the compiler's wait before their
+    // first use at vmcnt(loads issued since), so those loads stay in flight meanwhile.
+    __device__ __forceinline__ void issue_all() {
+        load_slot(threadIdx.x, v);
+        if constexpr (NORM) {
+            const f32x4* p = (const f32x4*)(nw + (size_t)min((int)threadIdx.x, slots() - 1) * 8);
+            wv[0] = p[0];
+            wv[1] = p[1];
         }
     }
     // NORM: every thread of the workgroup takes part (one LDS barrier).
@@ -1103,6 +1195,182 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_st(GemvSegs sg, int64_t row_by
     wait_vmcnt<0>();  // the refills past the wave's last item land before its LDS is released
 }
 
+// ---------------------------------------------- decode stream, one item in flight per wave
+// One activation row against a long weight stream, shaped for the HBM queues rather than for
+// occupancy. A cold one-launch read of a matrix is bound by how many bytes are in flight:
+// with F bytes requested the loads return after about max(L0, F / BW), so a whole matrix
+// requested at once comes back all at the end (nothing for the arithmetic to overlap), and an
+// activation row requested beside it waits its turn in the same queues. Here each wave keeps
+// exactly one item in flight (one 16-wave workgroup per CU, the LDS request keeps a second one
+// off: ~8 MB in flight over the device, about the bandwidth-latency product), the activation
+// row goes out with the first item, and each step issues the next item's loads before it
+// computes the current one.
+//
+// An item's bytes are read as whole, contiguous 16-byte pieces (nontemporal: each line is used
+// once, by this load) into registers, then written to the wave's LDS slot, from which each lane
+// reads its unit's fields as k_gemv does. The activation slices of the lane's units (one per
+// item of a row, XR of them) are read from LDS once and kept in registers; XR = 0 reads them per
+// unit. Measured on the Q4_K 14336 x 4096 decode step against the same kernel with
+// direct-to-LDS item loads and per-unit activation reads: 7.8 against 9.9 us.
+// FUSED: fp32 activation rows quantized here (x_f32), else a Q8_0 batch (qs, xs, xb). With
+// XR > 0 the row is at most 8192 elements and the 1024 threads stage it in one pass; only
+// XR = 0 has the staging's second pass (rest()), whose loads would otherwise make the compiler
+// wait for every load in flight, the first item's included, after the staging.
+//
+// Rows are handed out inside the workgroup: workgroup b owns rows [b rpw, (b + 1) rpw), wave w
+// starts with row b rpw + w and takes each further row from an LDS counter, one row ahead. A
+// fixed share per wave would leave the workgroup waiting on its slowest waves: the CU does not
+// serve its SIMDs' memory requests evenly (per-wave timestamps on the Q4_K 14336 x 4096 step:
+// the last four waves of a workgroup ended 2.5 us after the first four).
+template <uint32_t T, int WV, int XR, bool NORM, bool FUSED>
+__global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_bytes, int k, int n,
+                                                      int rpw, const int8_t* __restrict__ qs,
+                                                      const float* __restrict__ xs,
+                                                      const int32_t* __restrict__ xb,
+                                                      const float* __restrict__ x_f32,
+                                                      int accumulate) {
+    using Tr = typename TraitsOf<T>::type;
+    constexpr int NL = item_loads<Tr>();
+    constexpr int BPI = item_blocks<Tr>();
+    constexpr int SLOT = slot_bytes<Tr>();
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int next_row;  // rows of this workgroup handed out so far
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int units = k / Tr::UNIT;
+    const int iters = (units + 63) / 64;
+    const int nblk = units / Tr::UNITS_PER_BLK;
+    const int r0 = blockIdx.x * rpw;
+    const int r_end = min(n, r0 + rpw);
+    uint8_t* slot = lds + align16(act_lds_bytes<T>(1, k)) + (size_t)wave * SLOT;
+
+    // First byte of item `it` of row jr.
+    auto item_first = [&](int jr, int it) {
+        const int s = seg_of(sg, jr);
+        const uint8_t* row = seg_pick(s, sg.w[0], sg.w[1], sg.w[2]) +
+                             (int64_t)(jr - seg_pick(s, sg.start[0], sg.start[1], sg.start[2])) * row_bytes;
+        return row + (size_t)(it * BPI) * Tr::BLK_BYTES;
+    };
+    // The item's 16-byte pieces from the one at or below its first byte: piece 64 L + lane to
+    // pc[L] (lanes past the last piece load the last one again: straight-line loads, so the
+    // compiler counts exactly NL per item in its waits). dep is an opaque zero.
+    u32x4 pc[NL];
+    auto load_item = [&](int jr, int it, uint32_t dep) {
+        const uint8_t* first = item_first(jr, it);
+        const int mis = (int)((uintptr_t)first & 15u);
+        const int last = (mis + min(BPI, nblk - it * BPI) * Tr::BLK_BYTES - 1) >> 4;
+        const u32x4* base = (const u32x4*)(first - mis + dep);
+#pragma unroll
+        for (int L = 0; L < NL; ++L)
+            pc[L] = __builtin_nontemporal_load(base + min(64 * L + lane, last));
+    };
+    auto to_slot = [&](int jr, int it) {
+        const uint8_t* first = item_first(jr, it);
+        const int mis = (int)((uintptr_t)first & 15u);
+        const int last = (mis + min(BPI, nblk - it * BPI) * Tr::BLK_BYTES - 1) >> 4;
+#pragma unroll
+        for (int L = 0; L < NL; ++L)
+            if (64 * L + lane <= last) *(u32x4*)(slot + 16 * (64 * L + lane)) = pc[L];
+        return mis;
+    };
+    // The next row of this workgroup, -1 when they are all handed out.
+    auto grab = [&]() {
+        int c = 0;
+        if (lane == 0) c = __hip_atomic_fetch_add(&next_row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        c = __builtin_amdgcn_readfirstlane(c);
+        return r0 + c < r_end ? r0 + c : -1;
+    };
+
+    const ActLds a = act_layout<T, 1>(lds, k);
+    StageQuant<T, 1, NORM> sq{x_f32, k, {}};
+    StageCopy<T, 1> sc{qs, xs, xb, k, {}, {}, {}};
+    __shared__ float norm_part[16];
+    if constexpr (NORM) {
+        sq.nw = sg.norm_w;
+        sq.eps = sg.eps;
+        sq.part = norm_part;
+    }
+    if (threadIdx.x == 0) next_row = WV;
+    int row = r0 + wave < r_end ? r0 + wave : -1;
+    // The activation loads and item 0 fly together; the activation is waited for alone. Every
+    // wave loads an item 0 (a wave with no row that of row r0, which every workgroup owns),
+    // so the path to the staging has no branch: behind the fence the item loads are the last
+    // NL issued, and the compiler's wait before the staging reads the activation is vmcnt(NL).
+    static_assert(!NORM || FUSED, "the RMSNorm staging quantizes an fp32 row");
+    if constexpr (FUSED)
+        sq.issue_all();
+    else
+        sc.issue();
+    load_item(row >= 0 ? row : r0, 0, FUSED ? opaque_zero(x_f32, sg.norm_w) : opaque_zero(qs, xs, xb));
+    if constexpr (FUSED) {
+        sq.commit(a);
+        if constexpr (XR == 0) sq.rest(a);
+    } else {
+        sc.commit(a);
+        if constexpr (XR == 0) sc.rest(a);
+    }
+    lds_barrier();  // also publishes next_row
+    if (row < 0) return;
+
+    // the activation slices of this lane's units, one per item of a row
+    typename Tr::X xr[XR > 0 ? XR : 1];
+#pragma unroll
+    for (int i = 0; i < XR; ++i) xr[i] = Tr::x_of(a, 0, min(lane + 64 * i, units - 1));
+
+    int it = 0;
+    int nrow = grab();  // the row after the current one
+    float acc = 0.0f;
+    while (row >= 0) {
+        const int u = min(lane + 64 * it, units - 1);
+        const int mis = to_slot(row, it);
+        // issue the next item: the current row's next one, or the first of the next row
+        const bool last_item = it == iters - 1;
+        const int frow = last_item ? nrow : row, fit = last_item ? 0 : it + 1;
+        if (frow >= 0) load_item(frow, fit, 0u);
+        int nnrow = nrow;
+        if (last_item && nrow >= 0) nnrow = grab();
+        {
+            const int uc = u - 64 * it;  // unit within the item
+            const typename Tr::Raw raw =
+                Tr::load_lds(slot, mis + (uc / Tr::UNITS_PER_BLK) * Tr::BLK_BYTES, uc);
+            const typename Tr::W w = Tr::wdec(raw, u);
+            float v;
+            if constexpr (XR > 0) {
+                typename Tr::X x = xr[0];
+#pragma unroll
+                for (int i = 1; i < XR; ++i)
+                    if (it == i) x = xr[i];
+                v = Tr::fin(w, x, acc, u);
+            } else {
+                v = Tr::fin(w, Tr::x_of(a, 0, u), acc, u);
+            }
+            acc = lane + 64 * it < units ? v : acc;
+        }
+        if (last_item) {
+            const int s = seg_of(sg, row);
+            const int j = row - seg_pick(s, sg.start[0], sg.start[1], sg.start[2]);
+            const float* bias = seg_pick(s, sg.bias[0], sg.bias[1], sg.bias[2]);
+            float* y = seg_pick(s, sg.y[0], sg.y[1], sg.y[2]);
+            float v = wave_sum63(acc);  // the same additions as wave_sum's, in lane 63
+            if (bias) v += ((const __attribute__((address_space(4))) float*)bias)[j];
+            // the residual add as an atomic (one wave owns the row, so it is the plain sum
+            // y + v): a load of y here would wait behind the next item's loads
+            if (lane == 63) {
+                if (accumulate)
+                    __hip_atomic_fetch_add(y + j, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    y[j] = v;
+            }
+            acc = 0.0f;
+            row = nrow;
+            nrow = nnrow;
+            it = 0;
+        } else {
+            ++it;
+        }
+    }
+}
+
 static int g_cu_count = 0;
 
 static int cu_count() {
@@ -1195,6 +1463,80 @@ static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, 
     return hipGetLastError();
 }
 
+// The streaming kernel: 16-wave workgroups, at most one per CU (the LDS request is at least
+// kStrMinLds, more than half a CU's 160 KB), the rows split evenly over them.
+constexpr int kStrWaves = 16;
+constexpr size_t kStrMinLds = 96 * 1024;
+
+template <uint32_t T>
+__host__ constexpr size_t str_lds_bytes(int k) {
+    using Tr = typename TraitsOf<T>::type;
+    return align16(act_lds_bytes<T>(1, k)) + (size_t)kStrWaves * slot_bytes<Tr>();
+}
+
+template <uint32_t T, int XR, bool NORM, bool FUSED>
+static hipError_t launch_str_k(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
+                               const int32_t* xb, const float* x_f32, int accumulate,
+                               hipStream_t stream) {
+    const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
+    const size_t shmem = std::max(str_lds_bytes<T>(k), kStrMinLds);
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)k_gemv_str<T, kStrWaves, XR, NORM, FUSED>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    // one workgroup per CU (fewer for a short matrix: at least one row per wave), rows split
+    // evenly (the tuning knob "gemv_str_grid" overrides the count)
+    int64_t grid = std::min<int64_t>(cu_count(), (n + kStrWaves - 1) / kStrWaves);
+    const int force = tuning().gemv_str_grid.load(std::memory_order_relaxed);
+    if (force > 0) grid = force;
+    const int rpw = (int)((n + grid - 1) / grid);
+    grid = (n + rpw - 1) / rpw;
+    hipLaunchKernelGGL((k_gemv_str<T, kStrWaves, XR, NORM, FUSED>), dim3((unsigned)grid),
+                       dim3(64 * kStrWaves), shmem, stream, sg, row_bytes, k, n, rpw, qs, xs, xb,
+                       x_f32, accumulate);
+    return hipGetLastError();
+}
+
+template <uint32_t T, int XR, bool NORM>
+static hipError_t launch_str_x(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
+                               const int32_t* xb, const float* x_f32, int accumulate,
+                               hipStream_t stream) {
+    if (NORM || x_f32 != nullptr)
+        return launch_str_k<T, XR, NORM, true>(sg, k, n, qs, xs, xb, x_f32, accumulate, stream);
+    if constexpr (!NORM)
+        return launch_str_k<T, XR, false, false>(sg, k, n, qs, xs, xb, x_f32, accumulate, stream);
+    return hipErrorInvalidValue;
+}
+
+// Rows of one or two items keep the activation slices in registers; longer rows read them per
+// unit (their slices would not fit beside the item pieces).
+template <uint32_t T, bool NORM = false>
+static hipError_t launch_str(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
+                             const int32_t* xb, const float* x_f32, int accumulate, int64_t,
+                             hipStream_t stream) {
+    using Tr = typename TraitsOf<T>::type;
+    const int iters = (k / Tr::UNIT + 63) / 64;
+    if (iters == 1) return launch_str_x<T, 1, NORM>(sg, k, n, qs, xs, xb, x_f32, accumulate, stream);
+    if (iters == 2) return launch_str_x<T, 2, NORM>(sg, k, n, qs, xs, xb, x_f32, accumulate, stream);
+    return launch_str_x<T, 0, NORM>(sg, k, n, qs, xs, xb, x_f32, accumulate, stream);
+}
+
+template <uint32_t T>
+static bool str_fits(int k) { return str_lds_bytes<T>(k) <= 150 * 1024; }
+
+// The streaming kernel takes one activation row over a stream of at least 4 MiB; shorter
+// streams fill too few workgroups of 16 rows each and keep the register ring (MI355X, cold
+// HBM: Q4_K 1024x4096, 2.4 MB, 3.85 against 3.24 us; Q8_0 4864x896, 4.7 MB, 3.90 against
+// 4.37 us).
+template <uint32_t T>
+static bool use_str(int k, int n) {
+    const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
+    return bytes >= (4ll << 20) && str_fits<T>(k);
+}
+
 // Decode streams of at least this many weight bytes take the LDS-staged kernel: its contiguous
 // nontemporal loads win on long streams and lose on short ones, where its extra startup shows.
 // Q6_K: the 128256x4096 head (431 MB) 72-80 against 81-88 us, the 4096x14336 FFN down matrix
@@ -1251,10 +1593,19 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
     const int64_t simds = (int64_t)cu_count() * 4;
     const GemvTuning tu = gemv_tuning();
     const size_t shmem = act_lds_bytes<T>(MR, k);
+    // one activation row: the streaming kernel (tuning knob "gemv_kernel": 0 the default,
+    // 1 the register ring k_gemv, 2 the staged k_gemv_st, 3 k_gemv_str)
+    const int kind = tuning().gemv_kind.load(std::memory_order_relaxed);
+    if constexpr (MR == 1 && !SW) {
+        if ((kind == 0 && use_str<T>(k, n)) || (kind == 3 && str_fits<T>(k))) {
+            if (sg.norm_w) return launch_str<T, true>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
+            return launch_str<T, false>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
+        }
+    }
     if constexpr (MR == 1) {
         if (sg.norm_w) {  // the RMSNorm rides in the staging (one row)
             if constexpr ((T == T_Q6_K || T == T_Q4_K) && !SW)
-                if (use_staged<T>(sg, k, n))
+                if (kind == 2 || (kind == 0 && use_staged<T>(sg, k, n)))
                     return launch_st<T, 1, 16, true>(sg, k, n, qs, xs, xb, x_f32, accumulate, items,
                                                      stream);
             const int64_t waves =
@@ -1264,7 +1615,7 @@ static hipError_t launch_mr(const GemvSegs& sg, int k, int n, const int8_t* qs, 
         }
     }
     if constexpr ((T == T_Q6_K || T == T_Q4_K) && MR == 1 && !SW)
-        if (use_staged<T>(sg, k, n))
+        if (kind == 2 || (kind == 0 && use_staged<T>(sg, k, n)))
             return launch_st<T, 1, 16>(sg, k, n, qs, xs, xb, x_f32, accumulate, items, stream);
     if (MR > 2 && items > simds * 32) {
         const int64_t waves = std::min(simds * tu.deep_wps, resident_waves<T, MR, 2, SW>(shmem));
@@ -1309,6 +1660,43 @@ static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const 
         t += mr;
     }
     return hipSuccess;
+}
+
+// The kernel gemv_all_rows runs first for m activation rows, and its launch count; weights
+// taken as 16-byte aligned.
+template <uint32_t T>
+static void plan_rows(const char* tname, int k, int n, int m, char* buf, size_t cap) {
+    const int lim = max_rows_per_launch<T>(k);
+    int mr0 = 0, launches = 0;
+    for (int t = 0; t < m; ++launches) {
+        const int left = m - t;
+        int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        while (mr > lim) mr /= 2;
+        if (mr0 == 0) mr0 = mr;
+        t += mr;
+    }
+    const int kind = tuning().gemv_kind.load(std::memory_order_relaxed);
+    const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
+    const char* name = "k_gemv";
+    if (mr0 == 1 && ((kind == 0 && use_str<T>(k, n)) || (kind == 3 && str_fits<T>(k))))
+        name = "k_gemv_str";
+    else if (mr0 == 1 && (T == T_Q6_K || T == T_Q4_K) &&
+             (kind == 2 || (kind == 0 && bytes >= staged_min_bytes<T>() &&
+                            act_lds_bytes<T>(1, k) <= 64 * 1024)))
+        name = "k_gemv_st";
+    snprintf(buf, cap, "%s<%s,%d> launches=%d", name, tname, mr0, launches);
+}
+
+void gemv_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap) {
+    switch (type) {
+        case T_Q4_K: return plan_rows<T_Q4_K>("Q4_K", k, n, m, buf, cap);
+        case T_Q5_K: return plan_rows<T_Q5_K>("Q5_K", k, n, m, buf, cap);
+        case T_Q6_K: return plan_rows<T_Q6_K>("Q6_K", k, n, m, buf, cap);
+        case T_Q8_0: return plan_rows<T_Q8_0>("Q8_0", k, n, m, buf, cap);
+        case T_Q4_0: return plan_rows<T_Q4_0>("Q4_0", k, n, m, buf, cap);
+        case T_Q5_0: return plan_rows<T_Q5_0>("Q5_0", k, n, m, buf, cap);
+        default: snprintf(buf, cap, "none");
+    }
 }
 
 static hipError_t gemv_dispatch(uint32_t type, const GemvSegs& sg, int k, int n, int m,

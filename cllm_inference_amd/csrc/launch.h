@@ -18,6 +18,8 @@ struct Tuning {
     std::atomic<int> gemm_waves{0}, gemm_wtiles{0}, gemm_ttiles{0};  // weight-row GEMM tile
     std::atomic<int> gemm_splits{0};                                   // weight-row GEMM K splits
     std::atomic<int> gemv_short_wps{0}, gemv_deep_wps{0};              // GEMV waves per SIMD
+    std::atomic<int> gemv_kind{0};  // one-row GEMV: 0 planner, 1 k_gemv, 2 k_gemv_st, 3 k_gemv_str
+    std::atomic<int> gemv_str_grid{0};  // workgroups of k_gemv_str (0 = one per CU)
 };
 Tuning& tuning();
 
@@ -43,6 +45,10 @@ hipError_t launch_quantize_w(const float* x, int64_t n_blocks, float* scales, _F
 hipError_t launch_q8_to_w(const int8_t* qs, const float* scales, const int32_t* bsums,
                           int64_t n_blocks, float* scales_out, _Float16* qh, uint16_t* xq,
                           hipStream_t stream);
+
+// The decode kernel launch_gemv runs first for m activation rows of a k x n matrix ("none"
+// for a type with no vec_dot kernel): name<type,rows per launch> launches=count.
+void gemv_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap);
 
 // y[t, j] = vec_dot(W row j, activation row t) (+ bias[j]) for t < m, j < n.
 // Activation rows are Q8_0: qs[t * k], scales / bsums[t * k / 32]. Any m >= 1.

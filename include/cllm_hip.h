@@ -296,8 +296,9 @@ int cllm_hip_gguf_config(const cllm_hip_gguf* g, cllm_hip_model_config* cfg);
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows);
 
 /* The kernel instantiation and launch plan cllm_hip_matmul_quant_dev would run for this shape,
- * e.g. "k_gemmw_q4k<8,1,2,Q5_K> splits=1", or the route name for the GEMV and float-dot
- * routes; for tests and benchmarks. No reference counterpart. */
+ * e.g. "k_gemmw_q4k<8,1,2,Q5_K> splits=1" (MFMA route), "k_gemv_str<Q4_K,1> launches=1" (GEMV
+ * route: kernel, activation rows per launch, launches), or the route name for the float-dot
+ * route; for tests and benchmarks. No reference counterpart. */
 const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_rows);
 
 /* Process-wide kernel-choice overrides for tests and tuning sweeps; no reference counterpart.
@@ -308,6 +309,9 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
  *                  it has compiled; 0, 0, 0 = the planner's)
  *   "gemm_splits"  K splits of the weight-row GEMM (0 = the planner's)
  *   "gemv_waves"   waves per SIMD of the one-deep and two-deep GEMV rings (0 = defaults)
+ *   "gemv_kernel"  kernel of one-activation-row GEMVs: 0 the default, 1 the register ring,
+ *                  2 the LDS-staged stream, 3 the one-item-in-flight stream
+ *   "gemv_str_grid" workgroups of the one-item-in-flight stream (0 = one per CU)
  * Missing values count as 0, so n_values = 0 resets a knob. Takes effect on the next call. */
 int cllm_hip_tune(const char* knob, const int* values, int n_values);
 

@@ -80,3 +80,24 @@ def test_no_device_is_reported_not_faked():
     lib = C.load_library()
     assert lib.cllm_hip_init(0) == 5  # CLLM_HIP_E_NODEV
     assert b"device" in lib.cllm_hip_last_error()
+
+
+def test_decode_plans():
+    """One activation row over a weight stream of at least 4 MiB runs the streaming kernel
+    (k_gemv_str, one workgroup per CU), shorter streams the register-ring k_gemv; several rows
+    run in launches of up to 8. The tuning knob forces either kernel."""
+    assert C.matmul_plan(S.Q4_K, 4096, 14336, 1) == "k_gemv_str<Q4_K,1> launches=1"
+    assert C.matmul_plan(S.Q6_K, 4096, 128256, 1) == "k_gemv_str<Q6_K,1> launches=1"
+    assert C.matmul_plan(S.Q6_K, 14336, 4096, 1) == "k_gemv_str<Q6_K,1> launches=1"
+    assert C.matmul_plan(S.Q8_0, 896, 4864, 1) == "k_gemv_str<Q8_0,1> launches=1"
+    assert C.matmul_plan(S.Q4_K, 4096, 1024, 1) == "k_gemv<Q4_K,1> launches=1"
+    assert C.matmul_plan(S.Q4_K, 4096, 14336, 13) == "k_gemv<Q4_K,8> launches=3"
+    try:
+        C.tune("gemv_kernel", 1)
+        assert C.matmul_plan(S.Q6_K, 4096, 128256, 1) == "k_gemv<Q6_K,1> launches=1"
+        C.tune("gemv_kernel", 2)
+        assert C.matmul_plan(S.Q6_K, 4096, 128256, 1) == "k_gemv_st<Q6_K,1> launches=1"
+        C.tune("gemv_kernel", 3)
+        assert C.matmul_plan(S.Q4_K, 4096, 1024, 1) == "k_gemv_str<Q4_K,1> launches=1"
+    finally:
+        C.tune("gemv_kernel")

@@ -159,6 +159,47 @@ def test_staged_stream_equals_register_ring(gpu, orc, qt, k, mb):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("qt,n,k", [(S.Q8_0, 4096, 4096), (S.Q4_K, 1024, 4096),
+                                    (S.Q6_K, 1000, 14336), (S.Q5_K, 333, 4096)])
+def test_streaming_decode_row_handout(gpu, orc, qt, n, k):
+    """The one-workgroup-per-CU decode kernel hands a workgroup's rows to its 16 waves from an
+    LDS counter. Grids that leave workgroups with fewer rows than waves (a wave with no row
+    still stages its share of the activation), and grids whose workgroups hand out several rows
+    per wave, must give bit for bit the register-ring kernel's result -- fused quantization,
+    a prequantized batch, and the RMSNorm staging -- and match the oracle."""
+    import torch
+    w = S.make_weight(qt, n, k, 31 + n)
+    x = S.make_activation(1, k, 32 + n, outliers=True)
+    nw = (1.0 + 0.1 * np.random.default_rng(n).standard_normal(k)).astype(np.float32)
+    wd, xd, nwd = _dev(w), _dev(x), _dev(nw)
+    qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+    norm = k <= 4096
+
+    def run():
+        y = gpu.matmul_quant_dev(xd, wd, qt, None, k, n).cpu().numpy()
+        yq = gpu.gemv_q8_dev(wd, qt, k, n, qs, sc, bs).cpu().numpy()
+        yn = gpu.rmsnorm_gemv_multi_dev(xd, nwd, 1e-5, [wd], qt, k, [n])[0].cpu().numpy() if norm else None
+        torch.cuda.synchronize()
+        return y, yq, yn
+
+    try:
+        gpu.tune("gemv_kernel", 1)
+        ring = run()
+        for grid in (0, 7, 61, 192, 224, 300):
+            print("row handout", S.TYPE_NAMES[qt], n, k, "grid", grid, flush=True)
+            gpu.tune("gemv_kernel", 3)
+            gpu.tune("gemv_str_grid", grid)
+            got = run()
+            for a, b, what in zip(got, ring, ("fused", "prequantized", "rmsnorm")):
+                if a is not None:
+                    assert np.array_equal(bits(a), bits(b)), (what, grid, np.flatnonzero(bits(a) != bits(b))[:8])
+    finally:
+        gpu.tune("gemv_kernel")
+        gpu.tune("gemv_str_grid")
+    exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, 1)
+    check_close(ring[0], orc.matmul(x, w, qt, None, k, n, 1), exact, abs_sum, "row handout")
+
+
 def test_all_types_shapes_bias_vs_reference_golden(gpu, orc):
     cases = split_cases(load_golden("types.npz"))
     for tag, c in cases.items():
