@@ -45,6 +45,9 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
+WARM_MS = 30.0  # untimed graph replays before timing (--warm-ms)
+
+
 def time_loop(fn, steps, warmup):
     """Average ms per call of fn(i), i < steps, with launch overhead taken out.
 
@@ -72,7 +75,7 @@ def time_loop(fn, steps, warmup):
     g.replay()
     b.record()
     torch.cuda.synchronize()
-    for _ in range(min(200, int(30.0 / max(a.elapsed_time(b), 1e-3)))):
+    for _ in range(min(200, int(WARM_MS / max(a.elapsed_time(b), 1e-3)))):
         g.replay()
     torch.cuda.synchronize()
     times = []
@@ -93,8 +96,10 @@ def rotated_weights(w_np, copies):
     return [base] + [base.clone() for _ in range(copies - 1)]
 
 
-def decode_point(C, S, cfg, label, m, steps, warmup, cold=True):
-    """One decode workload: returns dict with step and GEMV-kernel timings."""
+def decode_point(C, S, cfg, label, m, steps, warmup, cold=True, ceiling=False):
+    """One decode workload: returns dict with step and GEMV-kernel timings. With ceiling, also
+    the one-launch read ceiling of the same weight copies (cllm_hip_read_stream_dev: the
+    stream read once, nothing computed)."""
     import torch
     qt, n, k, w = S.config_weight(cfg, label)
     x = torch.from_numpy(S.config_activation(cfg, m, k)).cuda()
@@ -111,15 +116,61 @@ def decode_point(C, S, cfg, label, m, steps, warmup, cold=True):
 
     ms_step = time_loop(step, steps, warmup)
     ms_gemv = time_loop(gemv, steps, warmup)
+    ms_read = time_loop(lambda i: C.read_stream_dev(ws[i % copies]), steps, warmup) if ceiling else None
     nbytes = algo_bytes(qt, n, k, m)
     del ws
     torch.cuda.empty_cache()
     print(f"[bench] {S.TYPE_NAMES[qt]} {n}x{k} m={m} copies={copies}: step {ms_step * 1e3:.2f} us, "
           f"gemv {ms_gemv * 1e3:.2f} us, {nbytes / ms_gemv / 1e6:.1f} GB/s", file=sys.stderr, flush=True)
+    if ceiling:
+        print(f"[bench] one-launch read of the same {w.size} weight bytes: {ms_read * 1e3:.2f} us, "
+              f"{w.size / ms_read / 1e6:.1f} GB/s", file=sys.stderr, flush=True)
     return dict(type=S.TYPE_NAMES[qt], n=n, k=k, m=m, copies=copies, bytes=nbytes,
-                ms_step=ms_step, ms_gemv=ms_gemv,
+                weight_bytes=int(w.size), ms_step=ms_step, ms_gemv=ms_gemv, ms_read=ms_read,
                 gbs_step=nbytes / ms_step / 1e6, gbs_gemv=nbytes / ms_gemv / 1e6,
                 route=C.matmul_route(qt, k, n, m), plan=C.matmul_plan(qt, k, n, m))
+
+
+def host_api_point(C, S, calls=50):
+    """c1 through the host-pointer matmul_quant the engine calls (engine.cpp:237-238): x and y in
+    host memory, so each call copies x in and y out over PCIe and synchronizes. With the
+    weights registered once (cllm_hip_register_weights) they stay in HBM; unregistered host
+    weights are copied in on every call. Wall-clock medians."""
+    import ctypes
+    qt, n, k, w = S.config_weight("c1_q4_k_gemv", "ffn")
+    x = S.config_activation("c1_q4_k_gemv", 1, k)[0]
+    lib = C.load_library()
+
+    def med():
+        C.matmul_quant(x, w, qt, None, k, n)
+        ts = []
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            C.matmul_quant(x, w, qt, None, k, n)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    unreg = med()
+    assert lib.cllm_hip_register_weights(ctypes.c_void_p(w.ctypes.data), w.size) == 0
+    try:
+        reg = med()
+    finally:
+        lib.cllm_hip_unregister_weights(ctypes.c_void_p(w.ctypes.data))
+    nbytes = algo_bytes(qt, n, k, 1)
+    print(f"[bench] host-pointer matmul_quant c1: registered {reg * 1e6:.1f} us, unregistered "
+          f"{unreg * 1e6:.1f} us", file=sys.stderr, flush=True)
+    return {"registered_us": round(reg * 1e6, 1), "registered_gbs": round(nbytes / reg / 1e9, 1),
+            "unregistered_us": round(unreg * 1e6, 1),
+            "unregistered_gbs": round(nbytes / unreg / 1e9, 1), "calls": calls}
+
+
+def read_ceiling(p):
+    """The one-launch read of a decode point's weight copies, and the fused step against it."""
+    wb = p["weight_bytes"]
+    return {"us": round(p["ms_read"] * 1e3, 3), "gbs": round(wb / p["ms_read"] / 1e6, 1),
+            "frac_hbm": round(wb / p["ms_read"] / 1e6 / HBM_PEAK_GBS, 4),
+            "step_over_read": round(p["ms_step"] / p["ms_read"], 3),
+            "kernel": "k_read_stream (16-byte nontemporal grid-stride loop, 4 x 512 threads per CU)"}
 
 
 def float_dot_points(C, S, steps, warmup):
@@ -302,7 +353,7 @@ def prefill_layer(C, S, steps, warmup):
         per[label] = {"type": S.TYPE_NAMES[qt], "n": n, "k": k, "us": round(ms * 1e3, 1),
                       "tops": round(ops / ms / 1e9, 1),
                       "frac_int8": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4),
-                      "route": C.matmul_route(qt, k, n, 512)}
+                      "route": C.matmul_route(qt, k, n, 512), "plan": C.matmul_plan(qt, k, n, 512)}
         print(f"[bench] prefill {label} {S.TYPE_NAMES[qt]} {n}x{k} m=512: {ms * 1e3:.1f} us, "
               f"{ops / ms / 1e9:.1f} TOPS", file=sys.stderr, flush=True)
         total_ms += ms
@@ -317,41 +368,120 @@ def prefill_layer(C, S, steps, warmup):
             "matrices": per}
 
 
-def cpu_baseline(S, cfg, label, seconds=10.0):
-    """The reference's matmul_quant (AVX2 + ThreadPool) on this host, bounded sample."""
+def cpu_share():
+    """CPUs this process may run on: its affinity set, capped by a cgroup v2 CPU quota."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()
+        if quota != "max":
+            n = min(n, max(1, int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_call(fn, cap_s, least=3):
+    """Median seconds of fn(): 3 warm-up calls (1 if a call is long), then timed calls until 10
+    have run or cap_s has passed (at least `least`)."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    for _ in range(2 if first * 4 < cap_s else 0):
+        fn()
+    times = []
+    t_end = time.perf_counter() + cap_s
+    while len(times) < least or (len(times) < 10 and time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(S, seconds=30.0):
+    """The reference's matmul_quant / matmul_quant_batch (AVX2 + its ThreadPool, compiled from
+    its sources into oracle/_ref; the oracle's C restatement if that is absent) on this host,
+    on the same seeded workloads as the GPU figures, activation quantization included. Threads
+    = the CPUs this job may use (the reference's ThreadPool(0) takes hardware_concurrency();
+    on a host whose job share is smaller, more threads than the share only time-slice). Each
+    point is bounded to a share of `seconds`; c1 also runs on one thread."""
     import oracle
-    ref = oracle.reference_or_none()
-    kind = "reference"
-    lib = ref
+    lib, kind = oracle.reference_or_none(), "reference"
     if lib is None:
         lib, kind = oracle.Oracle(), "port"
-    qt, n, k, w = S.config_weight(cfg, label)
-    x = S.config_activation(cfg, 1, k)
-    threads = min(16, os.cpu_count() or 1)
-    lib.matmul(x, w, qt, None, k, n, 1, threads=threads)  # warm-up
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        lib.matmul(x, w, qt, None, k, n, 1, threads=threads)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    nbytes = algo_bytes(qt, n, k, 1)
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": kind,
-            "sample": f"{len(times)} matmul_quant calls on the same {S.TYPE_NAMES[qt]} {n}x{k} "
-                      f"M=1 workload (activation quantization included), median "
-                      f"{med * 1e3:.2f} ms, {threads} ThreadPool workers"}
+    threads = cpu_share()
+    points = [("c1_q4_k_gemv", "ffn", 1), ("c0_q8_0_gemv", "w", 1), ("c2_q6_k_head", "output", 1)]
+    points += [("c4_m_sweep", lab, m) for lab in ("q5_k", "q8_0") for m in (1, 4, 16, 64, 256)]
+    cap = seconds / (len(points) + 4)
+    out, head, samples = {}, None, 0
+    for cfg, label, m in points:
+        qt, n, k, w = S.config_weight(cfg, label)
+        x = S.config_activation(cfg, m, k)
+        sec, calls = _median_call(lambda: lib.matmul(x, w, qt, None, k, n, m, threads=threads), cap)
+        samples += calls
+        nbytes = algo_bytes(qt, n, k, m)
+        tag = f"{cfg}_{label}_m{m}" if cfg == "c4_m_sweep" else cfg
+        rec = {"type": S.TYPE_NAMES[qt], "n": n, "k": k, "m": m, "ms": round(sec * 1e3, 3),
+               "calls": calls}
+        if m <= 64:
+            rec["gbs"] = round(nbytes / sec / 1e9, 3)
+        if m >= 64:
+            rec["gops"] = round(2.0 * m * n * k / sec / 1e9, 2)
+        out[tag] = rec
+        if cfg == "c1_q4_k_gemv":
+            head = (nbytes, sec, calls)
+            sec1, calls1 = _median_call(lambda: lib.matmul(x, w, qt, None, k, n, m, threads=1), cap)
+            samples += calls1
+            out["c1_q4_k_gemv_1_thread"] = {"ms": round(sec1 * 1e3, 3), "calls": calls1,
+                                            "gbs": round(nbytes / sec1 / 1e9, 3)}
+        del w
+    # c3: the Q4_K_M layer at M = 512, each matrix once per call
+    cfg = "c3_q4_k_m_layer"
+    mats = [(S.config_weight(cfg, label), label) for label, _, _, _ in S.CONFIGS[cfg]["mats"]]
+    xs = {k: S.config_activation(cfg, 512, k) for k in {mk for (_, _, mk, _), _ in mats}}
+
+    def layer():
+        for (qt, n, k, w), _ in mats:
+            lib.matmul(xs[k], w, qt, None, k, n, 512, threads=threads)
+
+    sec, calls = _median_call(layer, 2 * cap, least=2)
+    samples += calls
+    ops = sum(2.0 * 512 * n * k for (_, n, k, _), _ in mats)
+    out["c3_q4_k_m_layer_m512"] = {"ms": round(sec * 1e3, 1), "calls": calls,
+                                   "gops": round(ops / sec / 1e9, 2)}
+    nbytes, sec, calls = head
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": kind, "nproc": os.cpu_count(), "cpu_share": threads, "cpu_model": cpu_model(),
+            "sample": f"median of {calls} matmul_quant calls on the same Q4_K 14336x4096 M=1 "
+                      f"workload (activation quantization included) after warm-up, {threads} "
+                      f"ThreadPool workers; {samples} timed calls over all points, each point "
+                      f"bounded to ~{cap:.1f} s",
+            "configs": out}
 
 
 def main():
+    global WARM_MS
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=30.0)
+    ap.add_argument("--warm-ms", type=float, default=WARM_MS,
+                    help="GPU time of untimed graph replays before each timed loop (0 for "
+                         "counter runs, which profile every dispatch)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the M=512 Q4_K_M layer (for counter profiles of the GEMM) and "
                          "print its figures as one JSON line")
@@ -372,6 +502,7 @@ def main():
                     help="also run 10 device copies of 64 MiB (a kernel of known traffic, for "
                          "scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    WARM_MS = args.warm_ms
     if args.gpus != 1:
         print("bench.py measures one GPU: the path is not sharded across GPUs; run with "
               "--gpus 1", file=sys.stderr)
@@ -413,10 +544,12 @@ def main():
 
     if args.head_only:
         c2 = decode_point(C, S, "c2_q6_k_head", "output", 1, max(20, args.steps // 4),
-                          max(3, args.warmup // 4), cold=True)
-        print(json.dumps({"c2_q6_k_head": {"gemv_gbs": round(c2["gbs_gemv"], 1),
+                          max(3, args.warmup // 4), cold=True, ceiling=True)
+        print(json.dumps({"c2_q6_k_head": {"step_us": round(c2["ms_step"] * 1e3, 2),
+                                           "gemv_gbs": round(c2["gbs_gemv"], 1),
                                            "gemv_frac_hbm": round(c2["gbs_gemv"] / HBM_PEAK_GBS, 4),
-                                           "gemv_us": round(c2["ms_gemv"] * 1e3, 2)}}))
+                                           "gemv_us": round(c2["ms_gemv"] * 1e3, 2),
+                                           "read_ceiling": read_ceiling(c2)}}))
         return
 
     if args.prefill_only:
@@ -424,17 +557,22 @@ def main():
         print(json.dumps({"c3_prefill_layer_m512": layer}))
         return
 
-    head = decode_point(C, S, "c1_q4_k_gemv", "ffn", 1, args.steps, args.warmup, cold=True)
+    head = decode_point(C, S, "c1_q4_k_gemv", "ffn", 1, args.steps, args.warmup, cold=True,
+                        ceiling=True)
     extra = {}
     if not args.no_extra:
         warm = decode_point(C, S, "c1_q4_k_gemv", "ffn", 1, args.steps, args.warmup, cold=False)
         extra["c1_q4_k_warm_mall_gbs"] = round(warm["gbs_gemv"], 1)
         c2 = decode_point(C, S, "c2_q6_k_head", "output", 1, max(20, args.steps // 4),
-                          max(3, args.warmup // 4), cold=True)
-        extra["c2_q6_k_head"] = {"gemv_gbs": round(c2["gbs_gemv"], 1),
-                                 "gemv_frac_hbm": round(c2["gbs_gemv"] / HBM_PEAK_GBS, 4),
+                          max(3, args.warmup // 4), cold=True, ceiling=True)
+        extra["c2_q6_k_head"] = {"kernel": c2["plan"],
+                                 "step_us": round(c2["ms_step"] * 1e3, 2),
                                  "step_gbs": round(c2["gbs_step"], 1),
+                                 "step_frac_hbm": round(c2["gbs_step"] / HBM_PEAK_GBS, 4),
                                  "gemv_us": round(c2["ms_gemv"] * 1e3, 2),
+                                 "gemv_gbs": round(c2["gbs_gemv"], 1),
+                                 "gemv_frac_hbm": round(c2["gbs_gemv"] / HBM_PEAK_GBS, 4),
+                                 "read_ceiling": read_ceiling(c2),
                                  "tokens_per_s": round(1e3 / c2["ms_step"], 1)}
         c0 = decode_point(C, S, "c0_q8_0_gemv", "w", 1, args.steps, args.warmup, cold=False)
         extra["c0_q8_0_l2_resident"] = {"gemv_gbs": round(c0["gbs_gemv"], 1),
@@ -448,7 +586,7 @@ def main():
                 qt = S.NAME_TO_TYPE[p["type"]]
                 ops = 2.0 * m * p["n"] * p["k"]
                 sweep[f"{label}_m{m}"] = {
-                    "route": p["route"], "us": round(p["ms_step"] * 1e3, 2),
+                    "route": p["route"], "plan": p["plan"], "us": round(p["ms_step"] * 1e3, 2),
                     "gbs": round(p["gbs_step"], 1),
                     "frac_hbm": round(p["gbs_step"] / HBM_PEAK_GBS, 4),
                     "tops": round(ops / p["ms_step"] / 1e9, 2),
@@ -456,6 +594,15 @@ def main():
         extra["c4_m_sweep"] = sweep
         extra["c3_prefill_layer_m512"] = prefill_layer(C, S, max(5, args.steps // 20),
                                                         max(2, args.warmup // 10))
+        C.tune("gemm_kernel", 1)  # the int8 MFMA kernel on the same layer
+        try:
+            l8 = prefill_layer(C, S, max(5, args.steps // 20), max(2, args.warmup // 10))
+        finally:
+            C.tune("gemm_kernel")
+        extra["c3_prefill_layer_m512_int8_kernel"] = {
+            "layer_us": l8["layer_us"], "tops": l8["tops"], "frac_int8": l8["frac_int8"],
+            "matrices_us": {lab: r["us"] for lab, r in l8["matrices"].items()}}
+        extra["c1_host_pointer_api"] = host_api_point(C, S)
         extra["f3_float_dot_types"] = float_dot_points(C, S, max(20, args.steps // 4),
                                                        max(3, args.warmup // 4))
         extra["f1_decode_layer_device"] = decode_layer_device(C, S, max(20, args.steps // 4),
@@ -466,7 +613,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(S, "c1_q4_k_gemv", "ffn", seconds=args.cpu_seconds)
+        cpu = cpu_baseline(S, seconds=args.cpu_seconds)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_c1_q4_k_gemv.json")
@@ -500,7 +647,8 @@ def main():
                      "frac": round(head["gbs_step"] / HBM_PEAK_GBS, 4),
                      "kernel": head["plan"] + " (fused Q8_0 activation quantization)",
                      "kernel_us": round(head["ms_step"] * 1e3, 3),
-                     "traffic": traffic},
+                     "traffic": traffic,
+                     "one_launch_read_ceiling": read_ceiling(head)},
         "gemv_prequantized": {"kernel_us": round(head["ms_gemv"] * 1e3, 3),
                               "gbs": round(head["gbs_gemv"], 1)},
         "cpu_baseline": cpu,

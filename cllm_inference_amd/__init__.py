@@ -65,6 +65,7 @@ SIGNATURES = {
     "cllm_hip_matmul_quant_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
     "cllm_hip_matmul_quant_static_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
     "cllm_hip_static_scratch_bytes": (_SZ, []),
+    "cllm_hip_read_stream_dev": (_I, [_P, ctypes.c_uint64, _P]),
     "cllm_hip_matmul_route": (ctypes.c_char_p, [_U, _I, _I, _I]),
     "cllm_hip_matmul_plan": (ctypes.c_char_p, [_U, _I, _I, _I]),
     "cllm_hip_tune": (_I, [ctypes.c_char_p, _P, _I]),
@@ -376,6 +377,13 @@ def matmul_quant_residual_dev(x, w, t: int, bias, in_dim: int, out_dim: int, y):
 def matmul_route(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:
     return load_library().cllm_hip_matmul_route(int(t), int(in_dim), int(out_dim),
                                                 int(n_rows)).decode()
+
+
+def read_stream_dev(t) -> None:
+    """Reads the CUDA tensor t's bytes once and computes nothing (cllm_hip_read_stream_dev): the
+    one-launch HBM read ceiling a GEMV over the same bytes is measured against."""
+    _check(load_library().cllm_hip_read_stream_dev(_tp(t), t.numel() * t.element_size(),
+                                                   _stream()))
 
 
 def matmul_plan(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:

@@ -474,7 +474,7 @@ bool gemm_forced();
 // weights once per 8 activation rows) measured on MI355X: 16 rows for the types the
 // weight-row kernel has; 64 for the others, whose int8 kernel only overtakes the GEMV there
 // (Q5_K 14336 x 4096: 155 us at 16 rows against ~50 us on the GEMV). A forced kernel choice
-// (CLLM_HIP_GEMM) takes the MFMA route from 16 rows for every type.
+// (the tuning knob gemm_kernel) takes the MFMA route from 16 rows for every type.
 bool use_mfma(uint32_t type, int k, int m) {
     if (k % 256 != 0 || !gemm_supported(type)) return false;
     const int min_rows = (gemmw_supported(type) || gemm_forced()) ? kMfmaMinRows : 4 * kMfmaMinRows;
@@ -767,6 +767,20 @@ int cllm_hip_quantize_q8_0_dev(const float* x, int64_t n, int n_rows, int8_t* qs
     int rc = acquire(&st);
     if (rc) return rc;
     HIP_TRY(launch_quantize_q8_0(x, n * n_rows / 32, qs, scales, bsums, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_read_stream_dev(const void* p, uint64_t bytes, void* stream) {
+    if (bytes == 0) return CLLM_HIP_OK;
+    if (!p) return set_err(CLLM_HIP_E_ARG, "read_stream: null pointer");
+    if (!aligned16(p) || bytes % 16 != 0)
+        return set_err(CLLM_HIP_E_ARG, "read_stream: address or size not a multiple of 16 bytes");
+    DeviceState* st;
+    int rc = acquire(&st);
+    if (rc) return rc;
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, current_device()));
+    HIP_TRY(launch_read_stream(p, (int64_t)bytes, cus, (hipStream_t)stream));
     return CLLM_HIP_OK;
 }
 

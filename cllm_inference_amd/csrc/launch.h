@@ -172,4 +172,8 @@ hipError_t launch_gemv_f(uint32_t type, const uint8_t* w, int k, int n, int m, c
 hipError_t gemmw_workspace_init(void* part, size_t bytes, hipStream_t stream);
 bool gemmw_supported(uint32_t type);
 
+// Reads `bytes` (a multiple of 16) at the 16-byte-aligned device address p once and computes
+// nothing: the one-launch read ceiling of that stream (k_read.hip). cus = the device's CUs.
+hipError_t launch_read_stream(const void* p, int64_t bytes, int cus, hipStream_t stream);
+
 }  // namespace cllm_hip

@@ -196,6 +196,12 @@ int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t typ
                                      float* y, void* stream);
 size_t cllm_hip_static_scratch_bytes(void);
 
+/* Reads `bytes` bytes at the device address p (16-byte aligned, bytes a multiple of 16) once,
+ * by 16-byte nontemporal loads in a grid-stride loop over four 512-thread workgroups per CU,
+ * and computes nothing from them: the one-launch HBM read ceiling of that stream, which a
+ * GEMV over the same bytes is measured against. For benchmarks; no reference counterpart. */
+int cllm_hip_read_stream_dev(const void* p, uint64_t bytes, void* stream);
+
 /* ---- producers of a device-resident layer's activations (stream-ordered) -------------- */
 
 /* RMSNorm of n_rows rows of n floats fused with the Q8_0 quantization matmul_quant applies
