@@ -173,6 +173,22 @@ def read_ceiling(p):
             "kernel": "k_read_stream (16-byte nontemporal grid-stride loop, 4 x 512 threads per CU)"}
 
 
+def m_sweep(C, S, steps, warmup):
+    """c4: Q5_K 14336x4096 and Q8_0 4096x4096 at M = 1, 4, 16, 64, 256, cold weights."""
+    sweep = {}
+    for label in ("q5_k", "q8_0"):
+        for m in (1, 4, 16, 64, 256):
+            p = decode_point(C, S, "c4_m_sweep", label, m, steps, warmup, cold=True)
+            ops = 2.0 * m * p["n"] * p["k"]
+            sweep[f"{label}_m{m}"] = {
+                "route": p["route"], "plan": p["plan"], "us": round(p["ms_step"] * 1e3, 2),
+                "gbs": round(p["gbs_step"], 1),
+                "frac_hbm": round(p["gbs_step"] / HBM_PEAK_GBS, 4),
+                "tops": round(ops / p["ms_step"] / 1e9, 2),
+                "frac_int8": round(ops / p["ms_step"] / 1e9 / INT8_PEAK_TOPS, 4)}
+    return sweep
+
+
 def float_dot_points(C, S, steps, warmup):
     """The types without vec_dot (float-dot kernels): decode GEMV at the Llama-3-8B FFN shape
     14336 x 4096 for each type, M = 1 and 4, plus an F16 output head of Qwen2.5-0.5B's shape
@@ -495,6 +511,8 @@ def main():
     ap.add_argument("--float-dot-only", action="store_true",
                     help="run only the float-dot types' decode GEMVs and print them as one "
                          "JSON line")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="run only the c4 M-sweep and print it as one JSON line")
     ap.add_argument("--head-only", action="store_true",
                     help="run only the Q6_K 128256x4096 output-head GEMV and print it as one JSON "
                          "line")
@@ -542,6 +560,11 @@ def main():
                                                                  max(3, args.warmup // 4))}))
         return
 
+    if args.sweep_only:
+        print(json.dumps({"c4_m_sweep": m_sweep(C, S, max(20, args.steps // 4),
+                                                max(3, args.warmup // 4))}))
+        return
+
     if args.head_only:
         c2 = decode_point(C, S, "c2_q6_k_head", "output", 1, max(20, args.steps // 4),
                           max(3, args.warmup // 4), cold=True, ceiling=True)
@@ -578,20 +601,7 @@ def main():
         extra["c0_q8_0_l2_resident"] = {"gemv_gbs": round(c0["gbs_gemv"], 1),
                                         "gemv_us": round(c0["ms_gemv"] * 1e3, 2),
                                         "step_us": round(c0["ms_step"] * 1e3, 2)}
-        sweep = {}
-        for label in ("q5_k", "q8_0"):
-            for m in (1, 4, 16, 64, 256):
-                p = decode_point(C, S, "c4_m_sweep", label, m, max(20, args.steps // 4),
-                                 max(3, args.warmup // 4), cold=True)
-                qt = S.NAME_TO_TYPE[p["type"]]
-                ops = 2.0 * m * p["n"] * p["k"]
-                sweep[f"{label}_m{m}"] = {
-                    "route": p["route"], "plan": p["plan"], "us": round(p["ms_step"] * 1e3, 2),
-                    "gbs": round(p["gbs_step"], 1),
-                    "frac_hbm": round(p["gbs_step"] / HBM_PEAK_GBS, 4),
-                    "tops": round(ops / p["ms_step"] / 1e9, 2),
-                    "frac_int8": round(ops / p["ms_step"] / 1e9 / INT8_PEAK_TOPS, 4)}
-        extra["c4_m_sweep"] = sweep
+        extra["c4_m_sweep"] = m_sweep(C, S, max(20, args.steps // 4), max(3, args.warmup // 4))
         extra["c3_prefill_layer_m512"] = prefill_layer(C, S, max(5, args.steps // 20),
                                                         max(2, args.warmup // 10))
         C.tune("gemm_kernel", 1)  # the int8 MFMA kernel on the same layer

@@ -23,7 +23,7 @@ CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-HIP_SOURCES = ["k_quantize.hip", "k_gemv.hip", "k_gemm.hip", "k_gemm16.hip", "k_gemmw.hip", "k_gemv_f.hip", "k_producers.hip", "k_attention.hip", "k_read.hip", "gguf_file.cpp", "capi.hip"]
+HIP_SOURCES = ["k_quantize.hip", "k_gemv.hip", "k_gemm.hip", "k_gemm16.hip", "k_gemmw.hip", "k_gemm_sm.hip", "k_gemv_f.hip", "k_producers.hip", "k_attention.hip", "k_read.hip", "gguf_file.cpp", "capi.hip"]
 HIP_FLAGS = [
     "-O3", "-std=c++20", "--offload-arch=gfx950", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -470,13 +470,30 @@ int dequantize_host(const char* who, const void* src, float* dst32, uint16_t* ds
 
 bool gemm_forced();
 
+// Small batches of the types k_gemm_sm.hip has take it (the weights streamed once for the whole
+// batch, int8 MFMA), unless a kernel choice is forced: from 8 rows, up to 32 rows of the
+// K-quants and 64 of Q8_0. Measured on MI355X (fused step, cold weights, us): Q5_K 14336x4096
+// at 4 / 8 / 16 / 32 / 64 rows 21.3 / 19.5 / 20.7 / 29.0 / 49 against 17.4 (GEMV) / 28.7 /
+// 27.7 / 28.9 / 43.5 (MFMA); Q8_0 4096x4096 at 4 / 8 / 16 / 64 rows 13.6 / 13.5 / 12.4 / 20.9
+// against 10.2 / 12.8 / 22.0 / 30.6.
+constexpr int kSmallMinRows = 8;
+
+bool use_small(uint32_t type, int k, int m) {
+    const int knob = tuning().gemm_small.load(std::memory_order_relaxed);
+    if (knob == 2 || tuning().gemm_kind.load(std::memory_order_relaxed) != 0 ||
+        !gemm_sm_supported(type, k, m))
+        return false;
+    if (knob == 1) return m >= 3;
+    return m >= kSmallMinRows && m <= (type == T_Q8_0 ? 64 : 32);
+}
+
 // The MFMA kernels walk K in 256-element steps. Crossover from the GEMV (which streams the
 // weights once per 8 activation rows) measured on MI355X: 16 rows for the types the
 // weight-row kernel has; 64 for the others, whose int8 kernel only overtakes the GEMV there
 // (Q5_K 14336 x 4096: 155 us at 16 rows against ~50 us on the GEMV). A forced kernel choice
 // (the tuning knob gemm_kernel) takes the MFMA route from 16 rows for every type.
 bool use_mfma(uint32_t type, int k, int m) {
-    if (k % 256 != 0 || !gemm_supported(type)) return false;
+    if (k % 256 != 0 || !gemm_supported(type) || use_small(type, k, m)) return false;
     const int min_rows = (gemmw_supported(type) || gemm_forced()) ? kMfmaMinRows : 4 * kMfmaMinRows;
     return m >= min_rows;
 }
@@ -498,6 +515,7 @@ GemmKind gemm_kind(uint32_t type) {
 
 // Split-K bytes the MFMA route of this shape needs (the weight-row kernel only).
 size_t part_bytes_for(uint32_t type, int k, int n, int m) {
+    if (use_small(type, k, m)) return gemm_sm_partial_bytes(type, k, n, m);
     return gemm_kind(type) == GemmKind::W16 ? gemmw_partial_bytes(type, k, n, m) : 0;
 }
 
@@ -506,6 +524,8 @@ size_t part_bytes_for(uint32_t type, int k, int n, int m) {
 hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                     const float* sc, const int32_t* bs, const float* bias, float* y,
                     const WsView& ws, hipStream_t stream) {
+    if (use_small(type, k, m))
+        return launch_gemm_sm_q8(type, w, k, n, m, qs, sc, bs, bias, y, ws.part, ws.part_cap, stream);
     const GemmKind kind = gemm_kind(type);
     if (kind == GemmKind::W16) {
         hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws.sc, ws.qh,
@@ -523,6 +543,8 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
 // MFMA route from fp32 activations: quantize straight into the format the kernel reads.
 hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                         const float* bias, float* y, const WsView& ws, hipStream_t stream) {
+    if (use_small(type, k, m))
+        return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
     const int64_t nblk = (int64_t)m * k / 32;
     const GemmKind kind = gemm_kind(type);
     if (kind == GemmKind::F16) {
@@ -549,13 +571,15 @@ constexpr int kFusedMaxRows = 2;
 
 bool needs_workspace(uint32_t type, int k, int m) {
     if (!has_kernel(type)) return false;  // the float-dot kernels read fp32 rows directly
-    return use_mfma(type, k, m) || m > kFusedMaxRows;
+    return use_mfma(type, k, m) || use_small(type, k, m) || m > kFusedMaxRows;
 }
 
 // GEMV route on fp32 activation rows.
 hipError_t run_gemv_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                         const float* bias, float* y, const WsView& ws, hipStream_t stream,
                         bool accumulate = false) {
+    if (!accumulate && use_small(type, k, m))
+        return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
     if (m <= kFusedMaxRows)
         return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream, accumulate);
     hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws.qs, ws.sc, ws.bs, stream);
@@ -571,7 +595,8 @@ int stream_workspace(DeviceState* st, hipStream_t s, uint32_t type, int k, int n
     auto& slot = st->dev_ws[s];
     if (!slot) slot = std::make_unique<Workspace>();
     HIP_TRY(slot->ensure(k, m, s));
-    if (n > 0 && use_mfma(type, k, m)) HIP_TRY(slot->ensure_part(part_bytes_for(type, k, n, m), s));
+    if (n > 0 && (use_mfma(type, k, m) || use_small(type, k, m)))
+        HIP_TRY(slot->ensure_part(part_bytes_for(type, k, n, m), s));
     *out = slot.get();
     return CLLM_HIP_OK;
 }
@@ -594,7 +619,7 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
     HIP_TRY(st->y.ensure(yb, st->stream));
     if (needs_workspace(type, in_dim, n_rows)) {
         HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
-        if (use_mfma(type, in_dim, n_rows))
+        if (use_mfma(type, in_dim, n_rows) || use_small(type, in_dim, n_rows))
             HIP_TRY(st->act.ensure_part(part_bytes_for(type, in_dim, out_dim, n_rows), st->stream));
     }
     HIP_TRY(hipMemcpyAsync(st->x.p, x, xb, hipMemcpyHostToDevice, st->stream));
@@ -799,7 +824,7 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
     DeviceState* st;
     if ((rc = acquire(&st))) return rc;
     hipStream_t s = (hipStream_t)stream;
-    if (!use_mfma(type, in_dim, n_rows)) {
+    if (!use_mfma(type, in_dim, n_rows) && !use_small(type, in_dim, n_rows)) {
         HIP_TRY(launch_gemv(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums,
                             bias, y, s));
         return CLLM_HIP_OK;
@@ -985,7 +1010,8 @@ int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t typ
     size_t act = 0, pb = 0;
     if (needs_workspace(type, in_dim, n_rows)) {
         act = act_bytes(in_dim, n_rows);
-        if (use_mfma(type, in_dim, n_rows)) pb = part_bytes_for(type, in_dim, out_dim, n_rows);
+        if (use_mfma(type, in_dim, n_rows) || use_small(type, in_dim, n_rows))
+            pb = part_bytes_for(type, in_dim, out_dim, n_rows);
     }
     if (act + pb > kStaticScratchBytes)
         return set_err(CLLM_HIP_E_ARG,
@@ -1024,7 +1050,7 @@ int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t t
     hipStream_t s = (hipStream_t)stream;
     Workspace* ws = nullptr;
     if ((rc = stream_workspace(st, s, type, in_dim, out_dim, n_rows, &ws))) return rc;
-    if (has_kernel(type) && !use_mfma(type, in_dim, n_rows)) {
+    if (has_kernel(type) && !use_mfma(type, in_dim, n_rows) && !use_small(type, in_dim, n_rows)) {
         // the GEMV adds into y in its epilogue
         HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws->v, s,
                              true));
@@ -1363,6 +1389,12 @@ int cllm_hip_tune(const char* knob, const int* values, int n_values) {
     } else if (std::strcmp(knob, "gemv_str_grid") == 0) {
         if (v(0) < 0 || v(0) > 65535) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemv_str_grid out of range");
         t.gemv_str_grid.store(v(0));
+    } else if (std::strcmp(knob, "gemm_small") == 0) {
+        if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemm_small is 0, 1 or 2");
+        t.gemm_small.store(v(0));
+    } else if (std::strcmp(knob, "gemm_small_plan") == 0) {
+        t.gemm_small_splits.store(v(0));
+        t.gemm_small_kp.store(v(1));
     } else if (std::strcmp(knob, "gemv_waves") == 0) {
         t.gemv_short_wps.store(v(0));
         t.gemv_deep_wps.store(v(1));
@@ -1377,6 +1409,8 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
     const char* route = cllm_hip_matmul_route(type, in_dim, out_dim, n_rows);
     if (std::strcmp(route, "gemv") == 0) {
         gemv_plan_name(type, in_dim, out_dim, n_rows, buf, sizeof buf);
+    } else if (std::strcmp(route, "small") == 0) {
+        gemm_sm_plan_name(type, in_dim, out_dim, n_rows, buf, sizeof buf);
     } else if (std::strcmp(route, "mfma") != 0) {
         snprintf(buf, sizeof buf, "%s", route);
     } else {
@@ -1393,6 +1427,7 @@ const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_
     (void)out_dim;
     if (gemv_f_supported(type)) return "fdot";
     if (!has_kernel(type)) return "none";
+    if (use_small(type, in_dim, n_rows)) return "small";
     return use_mfma(type, in_dim, n_rows) ? "mfma" : "gemv";
 }
 

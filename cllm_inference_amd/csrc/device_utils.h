@@ -149,6 +149,71 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, 1.0f + expf(-g)), u);
 }
 
+// Q8_0 quantization of one 32-element block held by a DPP quad of lanes, 8 consecutive
+// elements e[] per lane (lane 4g + p holds elements 8p .. 8p+7), bit for bit as
+// quantize_row_q8_0 (src/core/quant.cpp:431-450): q receives the lane's 8 int8 values packed
+// little-endian, d the block's scale (the same in the four lanes), s8 the sum of the lane's 8
+// values. All four lanes of the quad must be active.
+//
+// Fast path, for blocks with no inf / NaN and a finite 1/d (every real activation): amax is
+// the largest (bits << 1), which orders finite floats by |x|, so it is the reference's amax;
+// since fl(amax * id) < 127.5 bounds every |fl(x * id)|, rint(v) lies in [-127, 127] and is
+// the low byte of fl(v + 1.5 * 2^23) (the sum lands in [2^23, 2^24), where the ulp is 1 and
+// round-to-nearest-even rounds exactly as rint; the clamp cannot act). The four lanes of a
+// block take the same path. Other blocks run q8_quant4, which reproduces the reference's NaN
+// handling of amax and the x86 INT_MIN conversion of out-of-range values.
+// fl(x * id) must be rounded before the 1.5 * 2^23 is added, so the function is compiled with
+// contraction off (with it, the compiler fuses the two into one FMA, which rounds the exact
+// product instead and moves a quant by one for about one value in 10^5). The product and the
+// sum are written as plain * and + in this scope: HIP's __fmul_rn and __fadd_rn are plain
+// operations compiled in the header's own scope, where contraction stays on.
+__device__ __forceinline__ void q8_quant_quad(const float (&e)[8], uint32_t (&q)[2], float& d,
+                                              int& s8) {
+#pragma clang fp contract(off)
+    uint32_t mb = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) mb = max(mb, __builtin_bit_cast(uint32_t, e[j]) << 1);
+    mb = max(mb, (uint32_t)dpp_i32<DPP_QUAD_SWAP1>((int)mb));
+    mb = max(mb, (uint32_t)dpp_i32<DPP_QUAD_SWAP2>((int)mb));
+    float id = 0.0f;
+    d = 0.0f;
+    bool fast = mb < 0xFF000000u;  // no inf or NaN in the block
+    if (fast) {
+        const float amax = __builtin_bit_cast(float, mb >> 1);
+        d = q8_scale(amax);
+        id = q8_inv_scale(d);
+        fast = __fmul_rn(amax, id) < 127.5f;  // false when 1/d overflowed to inf
+    }
+    s8 = 0;
+    if (fast) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t rb[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                rb[t] = __builtin_bit_cast(uint32_t, e[4 * j + t] * id + 12582912.0f);
+            const uint32_t lo = __builtin_amdgcn_perm(rb[1], rb[0], 0x0C0C0400u);
+            const uint32_t hi = __builtin_amdgcn_perm(rb[3], rb[2], 0x0C0C0400u);
+            q[j] = lo | (hi << 16);
+            s8 = sdot4(q[j], 0x01010101u, s8);
+        }
+    } else {
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(e[j]));
+        amax = fmaxf(amax, dpp_f32<DPP_QUAD_SWAP1>(amax));
+        amax = fmaxf(amax, dpp_f32<DPP_QUAD_SWAP2>(amax));
+        d = q8_scale(amax);
+        id = q8_inv_scale(d);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            int sm;
+            q[j] = q8_quant4(e[4 * j], e[4 * j + 1], e[4 * j + 2], e[4 * j + 3], id, sm);
+            s8 += sm;
+        }
+    }
+}
+
 // A zero the compiler cannot see through, and a fence for it: the asm statement has side
 // effects, clobbers memory and takes the base pointers of the loads issued before it (a, b, c:
 // wave-uniform, or null), so for the compiler it may write their memory and no load of theirs

@@ -637,16 +637,8 @@ struct StageCopy {
 };
 
 // Fused decode: quantize MR fp32 activation rows straight into the LDS layout, bit for bit as
-// k_quantize_q8_0. Slot i = lanes 4g + p of the workgroup: elements 8p .. 8p+7 of activation
-// block g (row-major over the rows); the four lanes of a block are one DPP quad.
-//
-// Fast path, for blocks with no inf / NaN and a finite 1/d (every real activation): amax is
-// the largest (bits << 1), which orders finite floats by |x|, so it is the reference's amax;
-// since fl(amax * id) < 127.5 bounds every |fl(x * id)|, rint(v) lies in [-127, 127] and is
-// the low byte of fl(v + 1.5 * 2^23) (the sum lands in [2^23, 2^24), where the ulp is 1 and
-// round-to-nearest-even rounds exactly as rint; the clamp cannot act). The four lanes of a
-// block take the same path. Other blocks run q8_quant4, which reproduces the reference's NaN
-// handling of amax and the x86 INT_MIN conversion of out-of-range values.
+// k_quantize_q8_0 (q8_quant_quad). Slot i = lanes 4g + p of the workgroup: elements 8p .. 8p+7
+// of activation block g (row-major over the rows); the four lanes of a block are one DPP quad.
 //
 // With NORM (one row of at most 4096 elements, 512 threads) the row first goes through the
 // RMSNorm h = (x * rms) * nw (engine.cpp:23-28) and h is quantized. The sum of squares is
@@ -682,48 +674,10 @@ struct StageQuant {
         const int g = i >> 2, part = i & 3;
         const int row = MR == 1 ? 0 : g / nb, b = g - row * nb;
         const float e[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[1].x, r[1].y, r[1].z, r[1].w};
-        uint32_t mb = 0;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) mb = max(mb, __builtin_bit_cast(uint32_t, e[j]) << 1);
-        mb = max(mb, (uint32_t)dpp_i32<DPP_QUAD_SWAP1>((int)mb));
-        mb = max(mb, (uint32_t)dpp_i32<DPP_QUAD_SWAP2>((int)mb));
-        float d = 0.0f, id = 0.0f;
-        bool fast = mb < 0xFF000000u;  // no inf or NaN in the block
-        if (fast) {
-            const float amax = __builtin_bit_cast(float, mb >> 1);
-            d = q8_scale(amax);
-            id = q8_inv_scale(d);
-            fast = __fmul_rn(amax, id) < 127.5f;  // false when 1/d overflowed to inf
-        }
         uint32_t q[2];
-        int s8 = 0;
-        if (fast) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                uint32_t rb[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    rb[t] = __builtin_bit_cast(uint32_t, __fadd_rn(__fmul_rn(e[4 * j + t], id), 12582912.0f));
-                const uint32_t lo = __builtin_amdgcn_perm(rb[1], rb[0], 0x0C0C0400u);
-                const uint32_t hi = __builtin_amdgcn_perm(rb[3], rb[2], 0x0C0C0400u);
-                q[j] = lo | (hi << 16);
-                s8 = sdot4(q[j], 0x01010101u, s8);
-            }
-        } else {
-            float amax = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(e[j]));
-            amax = fmaxf(amax, dpp_f32<DPP_QUAD_SWAP1>(amax));
-            amax = fmaxf(amax, dpp_f32<DPP_QUAD_SWAP2>(amax));
-            d = q8_scale(amax);
-            id = q8_inv_scale(d);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                int sm;
-                q[j] = q8_quant4(e[4 * j], e[4 * j + 1], e[4 * j + 2], e[4 * j + 3], id, sm);
-                s8 += sm;
-            }
-        }
+        float d;
+        int s8;
+        q8_quant_quad(e, q, d, s8);
         *(u32x2*)(const_cast<int8_t*>(a.qs) + row * lds_qs_row(a.k) + lds_qs_off(b * 32 + part * 8)) =
             u32x2{q[0], q[1]};
         const int s16 = s8 + dpp_i32<DPP_QUAD_SWAP1>(s8);  // this half block's sum

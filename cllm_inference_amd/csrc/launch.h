@@ -20,6 +20,8 @@ struct Tuning {
     std::atomic<int> gemv_short_wps{0}, gemv_deep_wps{0};              // GEMV waves per SIMD
     std::atomic<int> gemv_kind{0};  // one-row GEMV: 0 planner, 1 k_gemv, 2 k_gemv_st, 3 k_gemv_str
     std::atomic<int> gemv_str_grid{0};  // workgroups of k_gemv_str (0 = one per CU)
+    std::atomic<int> gemm_small{0};  // small-batch GEMM: 0 planner, 1 from 3 rows, 2 never
+    std::atomic<int> gemm_small_splits{0}, gemm_small_kp{0};  // its plan (0 = planner's)
 };
 Tuning& tuning();
 
@@ -175,5 +177,21 @@ bool gemmw_supported(uint32_t type);
 // Reads `bytes` (a multiple of 16) at the 16-byte-aligned device address p once and computes
 // nothing: the one-launch read ceiling of that stream (k_read.hip). cus = the device's CUs.
 hipError_t launch_read_stream(const void* p, int64_t bytes, int cus, hipStream_t stream);
+
+// Small-batch GEMM (k_gemm_sm.hip): the same contract as launch_gemv for 1 <= m <= 64 rows of
+// Q4_K / Q5_K / Q8_0 weights with k % 256 == 0, on int8 MFMA, the weights streamed once for the
+// whole batch. From fp32 rows x[m][k] (quantized in the kernel) or from a Q8_0 batch. part /
+// part_bytes: the split-K region (gemm_sm_partial_bytes; its first 64 KB are tile counters that
+// must be zero, and every launch leaves them zero).
+bool gemm_sm_supported(uint32_t type, int k, int m);
+size_t gemm_sm_partial_bytes(uint32_t type, int k, int n, int m);
+void gemm_sm_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap);
+hipError_t launch_gemm_sm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
+                              const float* bias, float* y, float* part, size_t part_bytes,
+                              hipStream_t stream);
+hipError_t launch_gemm_sm_q8(uint32_t type, const uint8_t* w, int k, int n, int m,
+                             const int8_t* qs, const float* xs, const int32_t* xb,
+                             const float* bias, float* y, float* part, size_t part_bytes,
+                             hipStream_t stream);
 
 }  // namespace cllm_hip

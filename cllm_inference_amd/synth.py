@@ -138,3 +138,36 @@ def config_weight(cfg: str, label: str) -> tuple[int, int, int, np.ndarray]:
 def config_activation(cfg: str, m: int, k: int) -> np.ndarray:
     c = CONFIGS[cfg]
     return make_activation(m, k, c["seed"] * 16 + 15 + k, outliers=c["outliers"])
+
+
+def rounding_boundary_activation(m: int, k: int, seed: int) -> np.ndarray:
+    """fp32 activations m x k in which every 32-element block holds one value x whose Q8_0
+    product x * id rounds to the tie fl(x * id) = k + 0.5, while the exact product lies on the
+    side of k + 0.5 away from the even neighbour -- so rint(fl(x * id)), the reference's quant,
+    and the rounding of the exact product (what a fused multiply-add would give) differ by one.
+    The block's other elements are uniform in (-a, a), a its largest magnitude."""
+    rng = np.random.default_rng([seed, 0xB0D])
+    x = rng.uniform(-1.0, 1.0, size=(m, k)).astype(np.float32)
+    for t in range(m):
+        for b in range(k // 32):
+            blk = x[t, 32 * b: 32 * b + 32]
+            a = np.float32(rng.uniform(0.5, 4.0))
+            blk *= a * np.float32(0.98)
+            blk[0] = a  # the block's amax
+            d = np.float32(a / np.float32(127.0))
+            inv = np.float32(np.float32(1.0) / d)
+            for _ in range(10000):
+                kk = int(rng.integers(1, 126))
+                cand = np.float32((kk + 0.5) / float(inv))
+                for c in (cand, np.nextafter(cand, np.float32(0)), np.nextafter(cand, np.float32(1e9))):
+                    exact = float(c) * float(inv)  # exact in double: 24 x 24 bits
+                    if (abs(c) < a and float(np.float32(exact)) == kk + 0.5 and
+                            np.rint(exact) != np.rint(kk + 0.5)):
+                        blk[1 + int(rng.integers(0, 31))] = -c if rng.integers(0, 2) else c
+                        break
+                else:
+                    continue
+                break
+            else:
+                raise RuntimeError("no boundary value found")
+    return x

@@ -296,9 +296,9 @@ int cllm_hip_gguf_tensor(const cllm_hip_gguf* g, int i, const char** name, uint3
                          const void** dev);
 int cllm_hip_gguf_config(const cllm_hip_gguf* g, cllm_hip_model_config* cfg);
 
-/* Name of the kernel family cllm_hip_matmul_quant_dev would run for this shape: "gemv" or
- * "mfma" (vec_dot types), "fdot" (the float-dot kernels of the other types), "none" (no
- * GGML type); for tests and benchmarks. */
+/* Name of the kernel family cllm_hip_matmul_quant_dev would run for this shape: "gemv",
+ * "small" (the small-batch int8 MFMA kernel) or "mfma" (vec_dot types), "fdot" (the float-dot
+ * kernels of the other types), "none" (no GGML type); for tests and benchmarks. */
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows);
 
 /* The kernel instantiation and launch plan cllm_hip_matmul_quant_dev would run for this shape,
@@ -318,6 +318,11 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
  *   "gemv_kernel"  kernel of one-activation-row GEMVs: 0 the default, 1 the register ring,
  *                  2 the LDS-staged stream, 3 the one-item-in-flight stream
  *   "gemv_str_grid" workgroups of the one-item-in-flight stream (0 = one per CU)
+ *   "gemm_small"   the small-batch kernel (Q4_K / Q5_K / Q8_0, up to 64 rows): 0 the default
+ *                  rows, 1 every batch of 3 to 64 rows, 2 never (it is also off while
+ *                  "gemm_kernel" forces a kernel)
+ *   "gemm_small_plan" K splits (more than the planner's) and K parts per workgroup (1, 2, 4,
+ *                  8 or 16) of the small-batch kernel (0, 0 = the planner's)
  * Missing values count as 0, so n_values = 0 resets a knob. Takes effect on the next call. */
 int cllm_hip_tune(const char* knob, const int* values, int n_values);
 

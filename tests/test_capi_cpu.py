@@ -85,13 +85,16 @@ def test_no_device_is_reported_not_faked():
 def test_decode_plans():
     """One activation row over a weight stream of at least 4 MiB runs the streaming kernel
     (k_gemv_str, one workgroup per CU), shorter streams the register-ring k_gemv; several rows
-    run in launches of up to 8. The tuning knob forces either kernel."""
+    run in launches of up to 8 (below the small-batch route's 4 rows, or for types it does not
+    have). The tuning knob forces either kernel."""
     assert C.matmul_plan(S.Q4_K, 4096, 14336, 1) == "k_gemv_str<Q4_K,1> launches=1"
     assert C.matmul_plan(S.Q6_K, 4096, 128256, 1) == "k_gemv_str<Q6_K,1> launches=1"
     assert C.matmul_plan(S.Q6_K, 14336, 4096, 1) == "k_gemv_str<Q6_K,1> launches=1"
     assert C.matmul_plan(S.Q8_0, 896, 4864, 1) == "k_gemv_str<Q8_0,1> launches=1"
     assert C.matmul_plan(S.Q4_K, 4096, 1024, 1) == "k_gemv<Q4_K,1> launches=1"
-    assert C.matmul_plan(S.Q4_K, 4096, 14336, 13) == "k_gemv<Q4_K,8> launches=3"
+    assert C.matmul_plan(S.Q6_K, 4096, 14336, 13) == "k_gemv<Q6_K,8> launches=3"
+    assert C.matmul_plan(S.Q4_K, 4096, 14336, 3) == "k_gemv<Q4_K,2> launches=2"
+    assert C.matmul_plan(S.Q4_K, 4096, 14336, 5) == "k_gemv<Q4_K,4> launches=2"
     try:
         C.tune("gemv_kernel", 1)
         assert C.matmul_plan(S.Q6_K, 4096, 128256, 1) == "k_gemv<Q6_K,1> launches=1"
@@ -101,3 +104,30 @@ def test_decode_plans():
         assert C.matmul_plan(S.Q4_K, 4096, 1024, 1) == "k_gemv_str<Q4_K,1> launches=1"
     finally:
         C.tune("gemv_kernel")
+
+
+def test_small_batch_plans():
+    """8 to 32 rows of Q4_K / Q5_K weights and 8 to 64 of Q8_0 take the small-batch kernel:
+    token tiles of 16, K split over workgroups in ranges of at most 1024 elements, K parts per
+    workgroup chosen for one workgroup per CU (256 CUs when no device is present)."""
+    assert C.matmul_plan(S.Q5_K, 4096, 14336, 16) == "k_gemm_sm<Q5_K,1> splits=4 kp=1"
+    assert C.matmul_plan(S.Q5_K, 4096, 14336, 32) == "k_gemm_sm<Q5_K,2> splits=4 kp=1"
+    assert C.matmul_plan(S.Q8_0, 4096, 4096, 16) == "k_gemm_sm<Q8_0,1> splits=4 kp=4"
+    assert C.matmul_plan(S.Q8_0, 4096, 4096, 64) == "k_gemm_sm<Q8_0,4> splits=4 kp=4"
+    assert C.matmul_plan(S.Q4_K, 14336, 4096, 16) == "k_gemm_sm<Q4_K,1> splits=14 kp=1"
+    assert C.matmul_route(S.Q4_K, 4096, 14336, 4) == "gemv"
+    assert C.matmul_route(S.Q4_K, 4096, 14336, 8) == "small"
+    assert C.matmul_route(S.Q4_K, 4096, 14336, 64) == "mfma"
+    assert C.matmul_route(S.Q8_0, 4096, 4096, 64) == "small"
+    assert C.matmul_route(S.Q6_K, 4096, 14336, 16) == "mfma"
+    try:
+        C.tune("gemm_small", 1)
+        assert C.matmul_route(S.Q4_K, 4096, 14336, 3) == "small"
+        C.tune("gemm_small", 2)
+        assert C.matmul_route(S.Q4_K, 4096, 14336, 16) == "mfma"
+        C.tune("gemm_small")
+        C.tune("gemm_kernel", 1)
+        assert C.matmul_route(S.Q4_K, 4096, 14336, 16) == "mfma"
+    finally:
+        C.tune("gemm_small")
+        C.tune("gemm_kernel")

@@ -200,6 +200,35 @@ def test_streaming_decode_row_handout(gpu, orc, qt, n, k):
     check_close(ring[0], orc.matmul(x, w, qt, None, k, n, 1), exact, abs_sum, "row handout")
 
 
+@pytest.mark.parametrize("m", [1, 2, 16])
+def test_fused_quantization_at_rounding_boundaries(gpu, orc, m):
+    """Every quantized block of the input holds a value whose rounding a contracted
+    x * id + 1.5 * 2^23 would move by one (synth.rounding_boundary_activation): the kernels that
+    quantize inside (the one-row streaming GEMV, the two-row register ring, the small-batch
+    kernel) must give the pre-quantized path's results bit for bit, and the quantizer the
+    oracle's bytes."""
+    import torch
+    k = 4096
+    x = S.rounding_boundary_activation(m, k, 17 + m)
+    xd = _dev(x)
+    qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+    oq, osc, obs = orc.quantize(x)
+    assert np.array_equal(qs.cpu().numpy(), oq)
+    assert np.array_equal(bits(sc.cpu().numpy()), bits(osc))
+    for qt in (S.Q4_K, S.Q8_0):
+        n = 2048
+        w = S.make_weight(qt, n, k, 600 + qt)
+        wd = _dev(w)
+        print("boundary", S.TYPE_NAMES[qt], "m", m, gpu.matmul_plan(qt, k, n, m), flush=True)
+        y_fused = gpu.matmul_quant_dev(xd, wd, qt, None, k, n).cpu().numpy()
+        y_q8 = gpu.gemv_q8_dev(wd, qt, k, n, qs, sc, bs).cpu().numpy()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(y_fused), bits(y_q8)), (S.TYPE_NAMES[qt], m)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+        yo = orc.matmul(x, w, qt, None, k, n, m)
+        check_close(y_fused.reshape(m, n), yo.reshape(m, n), exact, abs_sum, f"boundary m{m}")
+
+
 def test_all_types_shapes_bias_vs_reference_golden(gpu, orc):
     cases = split_cases(load_golden("types.npz"))
     for tag, c in cases.items():
@@ -231,11 +260,17 @@ def test_reference_test_inputs(gpu, orc):
 
 @pytest.mark.parametrize("qt", TYPES)
 def test_batch_rows_equal_single_rows(gpu, qt):
+    """A 13-row batch on the GEMV (the small-batch kernel turned off) equals its rows run one
+    at a time, bit for bit."""
     k = 1024
     n = 333
     w = S.make_weight(qt, n, k, 55)
     x = S.make_activation(13, k, 56, outliers=True)
-    yb = gpu.matmul_quant_batch(x, w, qt, None, k, n, 13)
+    try:
+        gpu.tune("gemm_small", 2)
+        yb = gpu.matmul_quant_batch(x, w, qt, None, k, n, 13)
+    finally:
+        gpu.tune("gemm_small")
     for t in (0, 5, 12):
         y1 = gpu.matmul_quant(x[t], w, qt, None, k, n)
         assert np.array_equal(bits(y1), bits(yb[t])), (S.TYPE_NAMES[qt], t)

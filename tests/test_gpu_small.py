@@ -1,0 +1,137 @@
+"""The small-batch route (k_gemm_sm.hip: by default 8 to 32 activation rows of Q4_K / Q5_K
+weights and 8 to 64 of Q8_0, on int8 MFMA, the weights streamed once for the batch; the kernel
+takes 1 to 64) on an MI355X, through the C ABI.
+
+Bars: the check_close bars of test_gpu_parity.py against the oracle (the reference's own
+quant.cpp restated) and the fp64 evaluation of the same quantized terms; bit-identical results
+between the fused-quantization and pre-quantized entry points (the fused staging quantizes
+bit for bit as quantize_row_q8_0) and between repeated runs (every sum has a fixed order,
+split-K included).
+"""
+import numpy as np
+import pytest
+
+from conftest import load_golden, split_cases
+from cllm_inference_amd import synth as S
+from test_gpu_parity import bits, check_close, _dev
+
+pytestmark = pytest.mark.gpu
+
+SMALL_TYPES = [S.Q4_K, S.Q5_K, S.Q8_0]
+
+
+def _run(gpu, w, x, qt, bias, k, n, m):
+    """Fused and pre-quantized results of one batch (device entry points)."""
+    import torch
+    wd, xd = _dev(w), _dev(x)
+    bd = None if bias is None else _dev(bias)
+    y_fused = gpu.matmul_quant_dev(xd, wd, qt, bd, k, n).cpu().numpy()
+    qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+    y_q8 = gpu.gemv_q8_dev(wd, qt, k, n, qs, sc, bs, bd).cpu().numpy()
+    torch.cuda.synchronize()
+    return y_fused, y_q8
+
+
+@pytest.fixture
+def small_everywhere(gpu):
+    """The small-batch kernel for every batch of 3 to 64 rows (its default range is narrower)."""
+    gpu.tune("gemm_small", 1)
+    yield
+    gpu.tune("gemm_small")
+
+
+@pytest.mark.parametrize("qt", SMALL_TYPES)
+def test_small_batches_ragged_shapes_vs_oracle(gpu, orc, qt, small_everywhere):
+    """Batch sizes that leave token tiles part-empty (5, 17, 33, 63), row counts that leave a
+    row group part-empty, K that splits over workgroups (K = 4096 takes four splits; K = 2816
+    is 11 super-blocks, an uneven split), with and without a bias."""
+    for (n, k, m) in [(100, 256, 5), (130, 1024, 17), (333, 2816, 33), (77, 4096, 63),
+                      (512, 4096, 64), (16, 512, 4)]:
+        w = S.make_weight(qt, n, k, 900 + n + m)
+        x = S.make_activation(m, k, 901 + m, outliers=True)
+        bias = np.random.default_rng(n + m).standard_normal(n).astype(np.float32)
+        print("small", S.TYPE_NAMES[qt], n, k, m, gpu.matmul_plan(qt, k, n, m), flush=True)
+        assert gpu.matmul_route(qt, k, n, m) == "small"
+        for b in (None, bias):
+            y_fused, y_q8 = _run(gpu, w, x, qt, b, k, n, m)
+            assert np.array_equal(bits(y_fused), bits(y_q8)), (S.TYPE_NAMES[qt], n, k, m)
+            exact, abs_sum = orc.matmul_f64(x, w, qt, b, k, n, m)
+            yo = orc.matmul(x, w, qt, b, k, n, m)
+            check_close(y_fused.reshape(m, n), yo.reshape(m, n), exact, abs_sum,
+                        f"small {S.TYPE_NAMES[qt]} {n}x{k} m{m}")
+
+
+@pytest.mark.parametrize("label,m", [("q5_k", 16), ("q5_k", 64), ("q8_0", 16), ("q8_0", 64)])
+def test_m_sweep_full_size_vs_reference_golden(gpu, orc, label, m):
+    """The c4 workloads at full size (Q5_K 14336x4096, Q8_0 4096x4096) on the small-batch
+    kernel (Q5_K at 64 rows forced onto it, past its default range): the golden rows from the
+    compiled reference, sampled rows against the oracle, and two runs bit for bit."""
+    qt, n, k, w = S.config_weight("c4_m_sweep", label)
+    x = S.config_activation("c4_m_sweep", m, k)
+    try:
+        gpu.tune("gemm_small", 1)
+        plan = gpu.matmul_plan(qt, k, n, m)
+        print("c4 full", label, m, plan, flush=True)
+        assert plan.startswith("k_gemm_sm<")
+        _check_full_size(gpu, orc, label, m, qt, n, k, w, x)
+    finally:
+        gpu.tune("gemm_small")
+
+
+def _check_full_size(gpu, orc, label, m, qt, n, k, w, x):
+    y1, y_q8 = _run(gpu, w, x, qt, None, k, n, m)
+    y2, _ = _run(gpu, w, x, qt, None, k, n, m)
+    assert np.array_equal(bits(y1), bits(y2))
+    assert np.array_equal(bits(y1), bits(y_q8))
+    y1 = y1.reshape(m, n)
+    c = split_cases(load_golden("batch.npz"))[f"c4_{label}_m{m}"]
+    rb = S.row_bytes(qt, k)
+    wsub = w[: 512 * rb]
+    exact, abs_sum = orc.matmul_f64(x, wsub, qt, None, k, 512, m)
+    check_close(y1[:, :512], c["y"], exact, abs_sum, f"c4 {label} m{m} golden")
+    rows = np.arange(3, n, 517)
+    sub = w.reshape(n, rb)[rows].reshape(-1)
+    exact, abs_sum = orc.matmul_f64(x, sub, qt, None, k, len(rows), m)
+    yo = orc.matmul(x, sub, qt, None, k, len(rows), m).reshape(m, len(rows))
+    check_close(y1[:, rows], yo, exact, abs_sum, f"c4 {label} m{m} oracle rows")
+
+
+def test_long_k_splits_and_knobs(gpu, orc):
+    """K = 14336 (56 super-blocks: fourteen splits), the knob that takes 3-row batches
+    onto the small route and the one that turns it off (the GEMV then computes the same
+    terms: within the bars of each other)."""
+    qt, n, k = S.Q4_K, 272, 14336
+    w = S.make_weight(qt, n, k, 4242)
+    for m in (3, 32):
+        x = S.make_activation(m, k, 4243 + m, outliers=True)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+        yo = orc.matmul(x, w, qt, None, k, n, m).reshape(m, n)
+        try:
+            gpu.tune("gemm_small", 1)
+            assert gpu.matmul_route(qt, k, n, m) == "small"
+            print("long k", m, gpu.matmul_plan(qt, k, n, m), flush=True)
+            y_small = gpu.matmul_quant_batch(x, w, qt, None, k, n, m).reshape(m, n)
+            gpu.tune("gemm_small", 2)
+            assert gpu.matmul_route(qt, k, n, m) != "small"
+            y_other = gpu.matmul_quant_batch(x, w, qt, None, k, n, m).reshape(m, n)
+        finally:
+            gpu.tune("gemm_small")
+        check_close(y_small, yo, exact, abs_sum, f"small m{m}")
+        check_close(y_other, yo, exact, abs_sum, f"other m{m}")
+
+
+def test_residual_add_on_small_route(gpu, orc):
+    """matmul_quant_residual_dev on a small batch: y += x W^T (+ bias), as matmul then add."""
+    import torch
+    qt, n, k, m = S.Q5_K, 200, 1024, 8
+    w = S.make_weight(qt, n, k, 77)
+    x = S.make_activation(m, k, 78)
+    bias = np.random.default_rng(79).standard_normal(n).astype(np.float32)
+    base = np.random.default_rng(80).standard_normal((m, n)).astype(np.float32)
+    assert gpu.matmul_route(qt, k, n, m) == "small"
+    wd, xd, bd = _dev(w), _dev(x), _dev(bias)
+    y = _dev(base)
+    gpu.matmul_quant_residual_dev(xd, wd, qt, bd, k, n, y)
+    ref = gpu.matmul_quant_dev(xd, wd, qt, bd, k, n).cpu().numpy()
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(y.cpu().numpy()), bits((base + ref).astype(np.float32)))

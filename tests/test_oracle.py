@@ -475,3 +475,22 @@ def test_dequantize_block_partial_equals_prefix(orc):
         for n in (1, max(bs, 32) + 5, 2 * max(bs, 32) - 1):
             assert np.array_equal(orc.dequantize_block(w, qt, n).view(np.uint32),
                                   full[:n].view(np.uint32)), (qt, n)
+
+
+def test_quantization_rounds_the_product_before_the_magic_add():
+    """Inputs whose every 32-element block holds a value with fl(x * id) on a tie that the
+    exact product x * id does not sit on: the oracle's quants are rint(fl(x * id)) (the
+    reference's (int)nearbyint(x[i] * id), quant.cpp:444) and differ from the rounding of the
+    exact product -- what a fused multiply-add computes -- in every block, so the device tests
+    on this input catch a contracted rounding."""
+    x = S.rounding_boundary_activation(4, 1024, 3)
+    qs, sc, _ = O.oracle().quantize(x)
+    f32 = np.float32
+    for t in range(4):
+        for b in range(1024 // 32):
+            e = x[t, 32 * b: 32 * b + 32]
+            inv = f32(f32(1.0) / sc[t, b])
+            sep = np.rint((e * inv).astype(np.float32).astype(np.float64)).astype(np.int64)
+            fused = np.rint(e.astype(np.float64) * np.float64(inv)).astype(np.int64)
+            assert np.array_equal(qs[t, 32 * b: 32 * b + 32], sep)
+            assert (sep != fused).sum() == 1, (t, b)

@@ -24,14 +24,15 @@ def _static(lib, x, w, qt, bias, k, n, y):
 
 
 # (type, n, k, [m of the first call, m of the second]): the MFMA route with split K (the
-# 4096 x 4096 Q4_K matrix at 512 rows plans two splits) and then without, Q6_K's kernel, a
-# 32-element block type, the GEMV route with a quantized batch (3..15 rows) and the fused
-# decode GEMV (1 row)
+# 4096 x 4096 Q4_K matrix at 512 rows plans two splits), then the small-batch route with split
+# K (32 rows: four splits), Q6_K's kernel, a 32-element block type on the MFMA then the
+# small-batch route, the small-batch route then the GEMV route with a quantized batch (3
+# rows), and the fused decode GEMV (1 row)
 CASES = [
-    (S.Q4_K, 4096, 4096, [512, 64]),
+    (S.Q4_K, 4096, 4096, [512, 32]),
     (S.Q6_K, 1024, 4096, [256, 16]),
     (S.Q8_0, 768, 2048, [96, 32]),
-    (S.Q5_K, 600, 1024, [12, 5]),
+    (S.Q5_K, 600, 1024, [12, 3]),
     (S.Q4_0, 512, 1024, [2, 1]),
 ]
 
