@@ -511,6 +511,9 @@ def main():
     ap.add_argument("--float-dot-only", action="store_true",
                     help="run only the float-dot types' decode GEMVs and print them as one "
                          "JSON line")
+    ap.add_argument("--c0-only", action="store_true",
+                    help="run only the L2-resident Q8_0 4864x896 GEMV (c0) and print it as one "
+                         "JSON line")
     ap.add_argument("--sweep-only", action="store_true",
                     help="run only the c4 M-sweep and print it as one JSON line")
     ap.add_argument("--head-only", action="store_true",
@@ -560,6 +563,13 @@ def main():
                                                                  max(3, args.warmup // 4))}))
         return
 
+    if args.c0_only:
+        c0 = decode_point(C, S, "c0_q8_0_gemv", "w", 1, args.steps, args.warmup, cold=False)
+        print(json.dumps({"c0_q8_0_l2_resident": {"kernel": c0["plan"],
+                                                  "step_us": round(c0["ms_step"] * 1e3, 2),
+                                                  "gemv_us": round(c0["ms_gemv"] * 1e3, 2)}}))
+        return
+
     if args.sweep_only:
         print(json.dumps({"c4_m_sweep": m_sweep(C, S, max(20, args.steps // 4),
                                                 max(3, args.warmup // 4))}))
@@ -598,7 +608,7 @@ def main():
                                  "read_ceiling": read_ceiling(c2),
                                  "tokens_per_s": round(1e3 / c2["ms_step"], 1)}
         c0 = decode_point(C, S, "c0_q8_0_gemv", "w", 1, args.steps, args.warmup, cold=False)
-        extra["c0_q8_0_l2_resident"] = {"gemv_gbs": round(c0["gbs_gemv"], 1),
+        extra["c0_q8_0_l2_resident"] = {"kernel": c0["plan"], "gemv_gbs": round(c0["gbs_gemv"], 1),
                                         "gemv_us": round(c0["ms_gemv"] * 1e3, 2),
                                         "step_us": round(c0["ms_step"] * 1e3, 2)}
         extra["c4_m_sweep"] = m_sweep(C, S, max(20, args.steps // 4), max(3, args.warmup // 4))

@@ -1087,8 +1087,10 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
         // would spill); split K to about two workgroups per CU
         p.wv = 4, p.nt = 1, p.mt = m <= 32 ? 1 : 2;
     } else if (type == T_Q6_K) {
-        // 128 weight rows x 64 tokens (4 waves, two workgroups per CU)
+        // 128 weight rows x 64 tokens (4 waves, two workgroups per CU); the tuning override
+        // takes the other compiled shapes (8 waves and / or 128 tokens)
         p.wv = 4, p.nt = 1, p.mt = 2;
+        if ((wv == 8 || wv == 4) && nt == 1 && (mt == 2 || mt == 4)) p.wv = wv, p.mt = mt;
     } else if (wv != 0 && (type == T_Q4_K ||
                            (wv == 8 && nt == 1 && (mt == 4 || mt == 2)) || (wv == 4 && nt == 1 && mt == 1))) {
         // Q5_K has the three shapes of the default plan compiled
@@ -1236,7 +1238,14 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     part = p.splits > 1 ? (float*)((char*)part + kCounterBytes) : nullptr;
     hipError_t e = hipErrorNotSupported;
     if (type == T_Q6_K) {
-        e = launch_q6<4, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
+        if (p.wv == 8 && p.mt == 4)
+            e = launch_q6<8, 4>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
+        else if (p.wv == 8)
+            e = launch_q6<8, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
+        else if (p.mt == 4)
+            e = launch_q6<4, 4>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
+        else
+            e = launch_q6<4, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
     } else if (is_b32(type)) {
 #define CLLM_GEMMW_B32(TT)                                                                    \
         if (type == TT) {                                                                      \
@@ -1280,7 +1289,7 @@ void gemmw_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap) 
     }
     const Plan p = plan_for(type, k, n, m);
     if (type == T_Q6_K)
-        snprintf(buf, cap, "k_gemmw_q6k<4,2> splits=%d", p.splits);
+        snprintf(buf, cap, "k_gemmw_q6k<%d,%d> splits=%d", p.wv, p.mt, p.splits);
     else if (is_b32(type))
         snprintf(buf, cap, "k_gemmw_b32<%s,4,%d> splits=%d",
                  type == T_Q8_0 ? "Q8_0" : type == T_Q4_0 ? "Q4_0" : "Q5_0", p.mt, p.splits);
