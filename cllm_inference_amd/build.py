@@ -27,6 +27,9 @@ HIP_SOURCES = ["k_quantize.hip", "k_gemv.hip", "k_gemm.hip", "k_gemm16.hip", "k_
 HIP_FLAGS = [
     "-O3", "-std=c++20", "--offload-arch=gfx950", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the kernels consume them with VALU instructions, which cannot
+    # read the accumulation registers (each use would cost a v_accvgpr_read)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-I" + CSRC, "-I" + os.path.join(ROOT, "include"),
 ]
 LIB_HIP = os.path.join(PKG, "libcllm_hip.so")

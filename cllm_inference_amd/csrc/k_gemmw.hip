@@ -365,23 +365,24 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 
     float* scratch = (float*)(lds + 2 * C::STAGE) + wave * NT * 64;
 
-    // One stage: half HALF = s & 1 of a super-block. The host keeps every split's stage range
-    // even and super-block aligned, so stage s sits in LDS buffer HALF; the scaled sums are
-    // folded into the output sums (times d) and cleared at the end of each super-block.
-    auto run_stage = [&](int s) {
-        const int HALF = s & 1;
+    // this lane's weight row r32 of the wave's first tile, as an offset into a stage buffer
+    const uint32_t woff = (uint32_t)C::OFF_W + (uint32_t)((wave * NT * 32 + r32) * C::WROW);
+
+    // One stage: half HALF of a super-block. The host keeps every split's stage range even and
+    // super-block aligned, so stage s sits in LDS buffer HALF = s & 1; the first block of each
+    // super-block starts the scaled sums (sacc = dx * F), its last stage folds them into the
+    // output sums (times d, minus the minimum term).
+    auto run_stage = [&]<int HALF>(int s) {
         uint8_t* cur = lds + HALF * C::STAGE;
         uint8_t* nxt = lds + (1 - HALF) * C::STAGE;
 
         // this lane's weight rows: row r32 of each of the wave's NT tiles. The rows' d and dmin
         // go to this wave's scratch before the next stage's direct-to-LDS loads are issued: an
         // LDS store while those are in flight would make the compiler wait for all of them.
-        const uint8_t* wr[NT];
         wu4 hdr[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            wr[t] = cur + C::OFF_W + ((wave * NT + t) * 32 + r32) * C::WROW;
-            hdr[t] = *(const wu4*)wr[t];
+            hdr[t] = *(const wu4*)(cur + woff + t * 32 * C::WROW);
             if (h == 0 && HALF == 1) {
                 float* sc_t = scratch + t * 64;
                 sc_t[r32] = f16_to_f32(hdr[t].x & 0xFFFFu);
@@ -390,17 +391,15 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
         }
         const bool more = s + 1 < s_end;
 
-        const uint8_t* act = cur;
-        const float* dxl = (const float*)(cur + C::OFF_DX);
-
-        // blocks 2 pc and 2 pc + 1 of the stage (sub-blocks 2c and 2c + 1, c = 2 HALF + pc)
-        auto blocks = [&](int pc) {
-            const int c = 2 * HALF + pc;
+        // blocks 2 PC and 2 PC + 1 of the stage (sub-blocks 2c and 2c + 1, c = 2 HALF + PC)
+        auto blocks = [&](int PC) {
+            const int c = 2 * HALF + PC;
             // A fragments: sub-block 2c (low nibbles) and 2c+1 (high nibbles), K steps j = 0, 1
             wh8 afr[NT][2][2];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                const wu4 q = *(const wu4*)(wr[t] + QS_AT + 32 * pc + 16 * h);
+                const uint8_t* wr = cur + woff + t * 32 * C::WROW;
+                const wu4 q = *(const wu4*)(wr + QS_AT + 32 * PC + 16 * h);
                 int sa, ma, sb, mb;
                 k4_sm(2 * c, hdr[t].y, hdr[t].z, hdr[t].w, sa, ma);
                 k4_sm(2 * c + 1, hdr[t].y, hdr[t].z, hdr[t].w, sb, mb);
@@ -409,7 +408,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                 if constexpr (Q5) {
                     // 5-bit values: bit 2c (sub-block 2c) or 2c+1 of qh[l] above the nibble;
                     // sc * q <= 63 * 31 stays exact in fp16
-                    const wu4 hb = *(const wu4*)(wr[t] + 16 + 16 * h);
+                    const wu4 hb = *(const wu4*)(wr + 16 + 16 * h);
                     const uint32_t q4[4] = {q.x, q.y, q.z, q.w}, h4[4] = {hb.x, hb.y, hb.z, hb.w};
                     uint32_t lo[4], hi[4];
 #pragma unroll
@@ -436,28 +435,34 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                     afr[t][1][1] = scaled8(q.z & 0xF0F0F0F0u, q.w & 0xF0F0F0F0u, s_hi, c_hi);
                 }
             }
-#pragma unroll
-            for (int blk = 0; blk < 2; ++blk) {
-                const int b = 2 * pc + blk;  // block within the stage
+            auto block = [&]<int BLK, bool FRESH>() {
+                const int b = 2 * PC + BLK;  // block within the stage
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    const int tok = mt * 32 + r32;
-                    const uint8_t* arow = act + tok * 256;
-                    const int sw = tok & 15;
+                    const uint8_t* arow = cur + (mt * 32 + r32) * 256;
+                    const int sw = r32 & 15;
                     const wh8 b0 = *(const wh8*)(arow + (((4 * b + 2 * h) ^ sw) << 4));
                     const wh8 b1 = *(const wh8*)(arow + (((4 * b + 2 * h + 1) ^ sw) << 4));
-                    const float dxv = dxl[tok * 4 + b];
+                    const float dxv = *(const float*)(cur + C::OFF_DX + (mt * 32 + r32) * 16 + 4 * b);
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
                         wf16 f = {};
-                        f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][blk][0], b0, f, 0, 0, 0);
-                        f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][blk][1], b1, f, 0, 0, 0);
+                        f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][BLK][0], b0, f, 0, 0, 0);
+                        f = __builtin_amdgcn_mfma_f32_32x32x16_f16(afr[t][BLK][1], b1, f, 0, 0, 0);
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) sacc[t][mt][r] = fmaf(dxv, f[r], sacc[t][mt][r]);
+                        for (int r = 0; r < 16; ++r)
+                            sacc[t][mt][r] = FRESH ? dxv * f[r] : fmaf(dxv, f[r], sacc[t][mt][r]);
                     }
                 }
-            }
+            };
+            // the super-block's first block starts the scaled sums (PC is wave-uniform)
+            if (HALF == 0 && PC == 0)
+                block.template operator()<0, true>();
+            else
+                block.template operator()<0, false>();
+            block.template operator()<1, false>();
         };
+        // (a rolled loop: unrolled, the compiler interleaves the two block pairs and spills)
 #pragma unroll 1
         for (int pc = 0; pc < 2; ++pc) {
             if (more) issue_part(s + 1, nxt, pc);
@@ -471,7 +476,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
         // End of the super-block: the minimum term of its 8 sub-blocks, then d.
         //   fm = sum_b mn_b * (hi_b + mid_b + lo_b) as two bf16 MFMAs: the weight operand holds
         //   the 8 minima in both K halves, the token operand hi | mid, then lo | 0.
-        if (HALF == 1) {
+        if constexpr (HALF == 1) {
             const uint8_t* xql = cur + C::OFF_XQ;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -501,10 +506,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
                     fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, *(const wbf8*)q, fm, 0, 0, 0);
                     fm = __builtin_amdgcn_mfma_f32_32x32x16_bf16(amq, *(const wbf8*)(q + 32), fm, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
+                    for (int r = 0; r < 16; ++r)
                         yacc[t][mt][r] = fmaf(-dmr[r], fm[r], fmaf(dr[r], sacc[t][mt][r], yacc[t][mt][r]));
-                        sacc[t][mt][r] = 0.0f;
-                    }
                 }
             }
         }
@@ -512,13 +515,17 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     };
 
     // An empty split range (the host rounds the stages per split up to whole super-blocks)
-    // loads nothing and contributes zeros.
+    // loads nothing and contributes zeros. Stage ranges are even: stage pairs are the halves
+    // of one super-block.
     if (s_begin < s_end) {
         issue_part(s_begin, lds, 0);
         issue_part(s_begin, lds, 1);
         wait_vm();
         __syncthreads();
-        for (int s = s_begin; s < s_end; ++s) run_stage(s);
+        for (int s = s_begin; s < s_end; s += 2) {
+            run_stage.template operator()<0>(s);
+            run_stage.template operator()<1>(s + 1);
+        }
     }
 
     // ---- output: lane holds rows 8q + 4h + (0..3) of each tile, token column r32 ----------
@@ -620,6 +627,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     };
     // activations and dx go straight to LDS; the 2-byte-aligned weight pieces come through
     // registers and are realigned by commit_stage
+    const uint32_t w_lo = (uint32_t)(uintptr_t)w & 3u;
     auto issue_stage = [&](int s, uint8_t* st, Pending& pd) {
         const int sb = s >> 1, gh = s & 1;
 #pragma unroll
@@ -638,27 +646,31 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         for (int j = 0; j < C::R_SLOTS; ++j) {
             const int i = tid + j * C::THREADS;
             const int piece = __builtin_amdgcn_readfirstlane(min(i, C::R_CHUNKS - 1) / C::BN);
-            const uint8_t* base = w + r_row[j] + (uint32_t)sb * Q6_K_BYTES;
+            // 32-bit byte offsets from w (the whole matrix is below 4 GB: r_row is 32-bit), so
+            // the loads take w as a scalar base and no 64-bit address arithmetic is needed;
+            // w_lo is w's own misalignment, for the realignment shift
+            const uint32_t base = r_row[j] + (uint32_t)sb * Q6_K_BYTES;
             if (piece < 6) {
                 // 16 bytes at p (2-byte aligned): dwords at p - (p & 2) .. + 20, all inside the
                 // super-block (p + 18 <= base + 194)
-                const uint8_t* p = piece < 4 ? base + 64 * gh + 16 * piece
+                const uint32_t p = piece < 4 ? base + 64 * gh + 16 * piece
                                              : base + Q6_K_QH + 32 * gh + 16 * (piece - 4);
-                const uint8_t* pa = p - ((uintptr_t)p & 3u);
-                const u32x4_a4 v = *(const u32x4_a4*)pa;
+                const uint32_t sh = (p + w_lo) & 3u;
+                const uint32_t pa = p - sh;
+                const u32x4_a4 v = *(const u32x4_a4*)(w + pa);
                 pd.r[j][0] = v.x; pd.r[j][1] = v.y; pd.r[j][2] = v.z; pd.r[j][3] = v.w;
-                pd.r[j][4] = *(const uint32_t*)(pa + 16);
-                pd.r[j][5] = (uint32_t)((uintptr_t)p & 3u);
+                pd.r[j][4] = *(const uint32_t*)(w + pa + 16);
+                pd.r[j][5] = sh;
             } else {
                 // the 16 scales (bytes 192..207) and d (208..209): dwords from 192 - (p & 2),
                 // the fifth only when the region starts 2 bytes into a dword, d by a u16 load
-                const uint8_t* p = base + Q6_K_SC;
-                const uint32_t sh = (uint32_t)((uintptr_t)p & 3u);
-                const uint8_t* pa = p - sh;
-                const u32x4_a4 v = *(const u32x4_a4*)pa;
+                const uint32_t p = base + Q6_K_SC;
+                const uint32_t sh = (p + w_lo) & 3u;
+                const uint32_t pa = p - sh;
+                const u32x4_a4 v = *(const u32x4_a4*)(w + pa);
                 pd.r[j][0] = v.x; pd.r[j][1] = v.y; pd.r[j][2] = v.z; pd.r[j][3] = v.w;
-                pd.r[j][4] = *(const uint32_t*)(sh ? pa + 16 : pa);
-                pd.r[j][5] = sh | ((uint32_t)*(const uint16_t*)(base + Q6_K_D) << 16);
+                pd.r[j][4] = *(const uint32_t*)(w + (sh ? pa + 16 : pa));
+                pd.r[j][5] = sh | ((uint32_t)*(const uint16_t*)(w + base + Q6_K_D) << 16);
             }
         }
     };
