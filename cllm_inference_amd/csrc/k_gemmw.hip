@@ -731,12 +731,16 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
 
         auto block = [&]<bool FRESH>(int i) {
             const wu4 ql = *(const wu4*)(wr + 32 * (i & 1) + 16 * h);
-            const uint32_t lsh = i >= 2 ? 4u : 0u, hsh = 2u * (uint32_t)i;
+            const uint32_t lsh = i >= 2 ? 4u : 0u;
+            // bits 2i, 2i+1 of every qh byte to bits 4, 5 of the same byte: a rotation right by
+            // 2i - 4 (mod 32); the bits it carries across bytes are masked off
+            const uint32_t rot = (uint32_t)(2 * i - 4) & 31u;
+            const uint32_t qhv[4] = {qhb.x, qhb.y, qhb.z, qhb.w}, qlv[4] = {ql.x, ql.y, ql.z, ql.w};
             uint32_t q6[4];
-            q6[0] = ((ql.x >> lsh) & 0x0F0F0F0Fu) | (((qhb.x >> hsh) & 0x03030303u) << 4);
-            q6[1] = ((ql.y >> lsh) & 0x0F0F0F0Fu) | (((qhb.y >> hsh) & 0x03030303u) << 4);
-            q6[2] = ((ql.z >> lsh) & 0x0F0F0F0Fu) | (((qhb.z >> hsh) & 0x03030303u) << 4);
-            q6[3] = ((ql.w >> lsh) & 0x0F0F0F0Fu) | (((qhb.w >> hsh) & 0x03030303u) << 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                q6[e] = ((qlv[e] >> lsh) & 0x0F0F0F0Fu) |
+                        (__builtin_amdgcn_alignbit(qhv[e], qhv[e], rot) & 0x30303030u);
             // scale of this lane's 16 values: sc[8 g + 2 i + h], local index 2 i + h
             const int si = 2 * i + h;
             const uint32_t scw = si < 4 ? scv.x : scv.y;
