@@ -276,8 +276,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     const int nblk = lin / mb_count, mblk = lin - nblk * mb_count;
     const int n0 = nblk * C::BN, m0 = mblk * BM;
     const int nb = k / 32;
-    // split-K: blockIdx.y owns stages [s_begin, s_end) and writes a partial sum (no bias) to
-    // slice blockIdx.y of y; a reduction adds the slices and the bias
+    // split-K: blockIdx.y owns stages [s_begin, s_end) (an even count: whole super-blocks);
+    // store_tile completes the tile (the last split to arrive adds the partials and the bias)
     const int s_begin = blockIdx.y * split_stages;
     const int s_end = min(s_begin + split_stages, k / kKS);
 
