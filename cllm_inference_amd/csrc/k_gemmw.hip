@@ -267,12 +267,13 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     const int h = lane >> 5;
     const int r32 = lane & 31;
 
-    // Workgroup -> (weight block, token block). Hardware hands consecutive workgroups to the
-    // 8 XCDs in turn; renumber so the token blocks of one weight block share an XCD's L2.
+    // Workgroup -> (weight block, token block), token blocks fastest. Hardware hands
+    // consecutive workgroups to the 8 XCDs in turn, so an XCD holds few token blocks of many
+    // weight blocks. (Renumbering so that the token blocks of one weight block share an XCD,
+    // as the Q6_K kernel does, measured slower here at M = 512: gate 127.3 against 125.2 us,
+    // wq 52.9 against 51.9, wk 26.2 against 24.9.)
     const int mb_count = (m + BM - 1) / BM;
-    const int g = gridDim.x;
-    const int bid = blockIdx.x;
-    const int lin = (g % 8 == 0) ? (bid % 8) * (g / 8) + bid / 8 : bid;
+    const int lin = blockIdx.x;
     const int nblk = lin / mb_count, mblk = lin - nblk * mb_count;
     const int n0 = nblk * C::BN, m0 = mblk * BM;
     const int nb = k / 32;
@@ -589,6 +590,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     const int h = lane >> 5;
     const int r32 = lane & 31;
 
+    // Workgroup -> (weight block, token block), renumbered so that the token blocks of one
+    // weight block share an XCD (hardware hands consecutive workgroups to the 8 XCDs in
+    // turn), whose L2 then serves the weight tile's rereads (Q6_K down, M = 512: 198 us,
+    // 212 without the renumbering).
     const int mb_count = (m + BM - 1) / BM;
     const int g = gridDim.x;
     const int bid = blockIdx.x;
@@ -901,6 +906,10 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_b32(const uint8_t* __restrict_
     const int h = lane >> 5;
     const int r32 = lane & 31;
 
+    // Workgroup -> (weight block, token block), renumbered so that the token blocks of one
+    // weight block share an XCD (hardware hands consecutive workgroups to the 8 XCDs in
+    // turn), whose L2 then serves the weight tile's rereads (Q6_K down, M = 512: 198 us,
+    // 212 without the renumbering).
     const int mb_count = (m + BM - 1) / BM;
     const int g = gridDim.x;
     const int bid = blockIdx.x;
