@@ -348,7 +348,14 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
         }
     }
     const bool owner = kpart == 0 && rg < n_rg;
+    // the lane's 4 rows are the same for every token tile: their bias values are loaded
+    // together first (rows past n clamped), not one dependent load per output
     auto write_out = [&](const f32x4 (&v)[MT]) {
+        float bv[4];
+        if (bias) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bv[i] = bias[min(rg * 16 + 4 * g + i, n - 1)];
+        }
 #pragma unroll
         for (int j = 0; j < MT; ++j) {
             const int tok = 16 * j + r;
@@ -356,11 +363,7 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = rg * 16 + 4 * g + i;
-                if (row < n) {
-                    float o = v[j][i];
-                    if (bias) o += bias[row];
-                    y[(size_t)tok * n + row] = o;
-                }
+                if (row < n) y[(size_t)tok * n + row] = bias ? v[j][i] + bv[i] : v[j][i];
             }
         }
     };

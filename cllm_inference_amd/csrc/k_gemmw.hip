@@ -168,21 +168,27 @@ __device__ __forceinline__ void store_tile(int n, int m, const float* __restrict
                                            int* __restrict__ counters, uint8_t* lds, int wave,
                                            Val val, Tok tok, Row row) {
     const int splits = (int)gridDim.y;
-    if (splits == 1) {
+    // y (plus the bias): a token tile's 16 bias values are loaded together (rows past n
+    // clamped), not one dependent load per output
+    auto write_out = [&](auto get) {
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const int t = tok(i);
             if (t >= m) continue;
+            float bv[16];
+            if (bias) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) bv[r] = bias[min(row(i, r), n - 1)];
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int j = row(i, r);
-                if (j < n) {
-                    float v = val(i, r);
-                    if (bias) v += bias[j];
-                    y[(size_t)t * n + j] = v;
-                }
+                if (j < n) y[(size_t)t * n + j] = bias ? get(i, r) + bv[r] : get(i, r);
             }
         }
+    };
+    if (splits == 1) {
+        write_out(val);
         return;
     }
     constexpr int SLOT = NI * 8 * 64;  // 8-byte pairs per wave slot
@@ -233,16 +239,7 @@ __device__ __forceinline__ void store_tile(int n, int m, const float* __restrict
                 acc[i][2 * r2 + 1] = sp == 0 ? x1 : acc[i][2 * r2 + 1] + x1;
             }
     }
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int t = tok(i);
-        if (t >= m) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int j = row(i, r);
-            if (j < n) y[(size_t)t * n + j] = bias ? acc[i][r] + bias[j] : acc[i][r];
-        }
-    }
+    write_out([&](int i, int r) { return acc[i][r]; });
 }
 
 }  // namespace
