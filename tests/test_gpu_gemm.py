@@ -168,3 +168,22 @@ def test_m_sweep_q5_k_large_batches_vs_reference_golden(gpu, orc, m, gemm_kernel
     yo = orc.matmul(x[sample], w, qt, None, k, n, 8, threads=8)
     exact, abs_sum = orc.matmul_f64(x[sample], w, qt, None, k, n, 8)
     check_close(y[sample], yo, exact, abs_sum, f"q5_k m{m} oracle rows")
+
+
+@pytest.mark.parametrize("k, n", [(768, 77), (1280, 130), (3328, 33)])
+def test_q6_k_prefill_super_block_alignments(gpu, orc, k, n, gemm_kernel):
+    """Q6_K rows of an odd number of 210-byte super-blocks: the super-blocks sit at byte offsets
+    0 and 2 mod 4 by row and by position, so the weight-row kernel realigns its dword loads
+    both ways, and (n odd) the matrix ends 2 bytes past a dword boundary, where the last
+    super-block's loads must stop. Planned split and 4 splits."""
+    m = 40
+    w = S.make_weight(S.Q6_K, n, k, k + n)
+    x = S.make_activation(m, k, k - n, outliers=True)
+    exact, abs_sum = orc.matmul_f64(x, w, S.Q6_K, None, k, n, m)
+    yo = orc.matmul(x, w, S.Q6_K, None, k, n, m)
+    for splits in (0, 4):
+        gpu.tune("gemm_splits", splits)
+        print("q6_k alignments", k, n, "splits", splits, flush=True)
+        y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
+        gpu.tune("gemm_splits")
+        check_close(y, yo, exact, abs_sum, f"q6_k {n}x{k} splits={splits}")
