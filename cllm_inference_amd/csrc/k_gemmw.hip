@@ -541,11 +541,18 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
 // four MFMAs per token tile and F = sc * I (exact while the partial sums stay below 2^24, else
 // within one fp32 rounding). No minimum term; d is applied once per super-block.
 //
-// A stage is half a super-block (g = stage parity). Q6_K blocks are 2-byte aligned, so the raw
-// bytes come through registers (aligned dword loads, realigned with v_alignbyte) into an LDS
-// row of 112 bytes: ql[64 g .. +64] | qh[32 g .. +32] | the half's 8 scales | d.
-constexpr int kQ6Row = 112;
-constexpr int kQ6Pieces = 7;  // 4 ql chunks, 2 qh chunks, 1 scale / d chunk
+// A stage is half a super-block (g = stage parity). Q6_K super-blocks (210 bytes) sit at
+// 2-byte alignment, so a row's bytes of the half come by 4-byte direct-to-LDS loads of
+// dword-aligned windows around them, each inside the super-block at byte offset base of the
+// matrix (sh = base & 3, 0 or 2: the weights are 16-byte aligned):
+//   ql: 80 bytes from base + 64 g - sh, qh: 48 bytes from base + 128 + 32 g - sh,
+//   scales: 16 bytes from base + 192 - sh (g = 0) or base + 192 + sh (g = 1).
+// LDS holds them as nine 16-byte chunks per row, chunk-major ([chunk][row][16 bytes]), so
+// that one wave-load fills one chunk of 16 rows (256 contiguous bytes) and the lanes' 16-byte
+// reads of consecutive rows fall on distinct banks; each lane realigns its row's bytes with
+// v_alignbyte. d comes by a 2-byte register load in the stage of half 0.
+constexpr int kQ6Ch = 9;                  // 16-byte chunks per row and stage
+constexpr int kQ6QhCh = 5, kQ6ScCh = 8;   // first chunk of the qh window, the scale chunk
 
 template <int W, int MT>
 struct Cfg6 {
@@ -554,20 +561,21 @@ struct Cfg6 {
     static constexpr int BM = 32 * MT;
     static constexpr int ACT = BM * 256;          // swizzled fp16 activations, as for Q4_K
     static constexpr int DX = 4 * BM * 4;
-    static constexpr int WB = BN * kQ6Row;
+    static constexpr int WB = kQ6Ch * BN * 16;  // [chunk][row][16 bytes]
     static constexpr int OFF_DX = ACT;
     static constexpr int OFF_W = OFF_DX + DX;
     static constexpr int STAGE = OFF_W + WB;
     static constexpr int SCRATCH = W * 32 * 4;  // per wave: d[32]
     static constexpr int LDS = 2 * STAGE + SCRATCH;
     static_assert(LDS <= 160 * 1024, "LDS budget");
-    static_assert(BN % 64 == 0, "a wave loads one raw piece type per slot");
     static constexpr int A_LOADS = ACT / 1024;    // direct-to-LDS wave-loads
     static constexpr int A_SLOTS = (A_LOADS + W - 1) / W;
     static constexpr int DX_LOADS = DX / 256;
     static constexpr int DX_SLOTS = (DX_LOADS + W - 1) / W;
-    static constexpr int R_CHUNKS = BN * kQ6Pieces;  // raw weight pieces through registers
-    static constexpr int R_SLOTS = (R_CHUNKS + THREADS - 1) / THREADS;
+    // weight wave-loads: chunk c of 16 rows; BN / 16 = 2 W of them per chunk, so wave w's
+    // slot j loads chunk j / 2 of rows 16 (w + W (j & 1)) ..
+    static_assert(BN / 16 == 2 * W, "two row groups of 16 per wave and chunk");
+    static constexpr int W_SLOTS = 2 * kQ6Ch;
 };
 
 template <int W, int MT>
@@ -610,12 +618,14 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         const int c = (lane & 15) ^ (t & 15);
         a_off[j] = ((uint32_t)min(m0 + t, m - 1) * (uint32_t)k + 8u * (uint32_t)c) * 2u;
     }
-    uint32_t r_row[C::R_SLOTS];  // byte offset of the row's first super-block
-#pragma unroll
-    for (int j = 0; j < C::R_SLOTS; ++j) {
-        const int i = min(tid + j * C::THREADS, C::R_CHUNKS - 1);
-        r_row[j] = (uint32_t)min(n0 + i % C::BN, n - 1) * row_bytes;
-    }
+    // weight windows: this lane loads dword lane & 3 of a chunk of row 16 q + (lane >> 2);
+    // rows past the matrix are clamped to the last one (their results are dropped). A tile
+    // with all its rows inside the matrix takes each row's offset from rowoff0.
+    const int lrow = lane >> 2;
+    const uint32_t rowoff0 = (uint32_t)(n0 + lrow) * row_bytes;
+    const bool full_tile = n0 + C::BN <= n;
+    const int wrow = wave * 32 + r32;
+    const uint32_t ro_own = (uint32_t)min(n0 + wrow, n - 1) * row_bytes;
     uint32_t dx_off[C::DX_SLOTS];  // elements into xs: [block][token] in LDS
 #pragma unroll
     for (int j = 0; j < C::DX_SLOTS; ++j) {
@@ -624,14 +634,9 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         dx_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)nb + b;
     }
 
-    struct Pending {
-        uint32_t r[C::R_SLOTS][6];
-    };
-    // activations and dx go straight to LDS; the 2-byte-aligned weight pieces come through
-    // registers and are realigned by commit_stage
-    const uint32_t w_lo = (uint32_t)(uintptr_t)w & 3u;
-    auto issue_stage = [&](int s, uint8_t* st, Pending& pd) {
-        const int sb = s >> 1, gh = s & 1;
+    // every operand goes straight to LDS (direct-to-LDS loads); GH = s & 1
+    auto issue_stage = [&]<int GH>(int s, uint8_t* st) {
+        const int sb = s >> 1;
 #pragma unroll
         for (int j = 0; j < C::A_SLOTS; ++j) {
             const int L = wave + j * W;
@@ -644,62 +649,28 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
             if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
                 lds_load4(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + L * 256);
         }
+        const uint32_t sbo = (uint32_t)sb * Q6_K_BYTES;
+        // a full tile: rows 16 q + lrow at rowoff0 + 16 q row_bytes, all with the shift of
+        // the lane's own row (16 q row_bytes is a multiple of 4)
+        const uint32_t sh0 = (rowoff0 + sbo) & 3u;
+        const uint32_t lb = rowoff0 + sbo + 4u * (uint32_t)(lane & 3) - sh0;  // ql, qh, scales of half 0
+        const uint32_t lbs = lb + 2u * sh0;                                   // scales of half 1
 #pragma unroll
-        for (int j = 0; j < C::R_SLOTS; ++j) {
-            const int i = tid + j * C::THREADS;
-            const int piece = __builtin_amdgcn_readfirstlane(min(i, C::R_CHUNKS - 1) / C::BN);
-            // 32-bit byte offsets from w (the whole matrix is below 4 GB: r_row is 32-bit), so
-            // the loads take w as a scalar base and no 64-bit address arithmetic is needed;
-            // w_lo is w's own misalignment, for the realignment shift
-            const uint32_t base = r_row[j] + (uint32_t)sb * Q6_K_BYTES;
-            if (piece < 6) {
-                // 16 bytes at p (2-byte aligned): dwords at p - (p & 2) .. + 20, all inside the
-                // super-block (p + 18 <= base + 194)
-                const uint32_t p = piece < 4 ? base + 64 * gh + 16 * piece
-                                             : base + Q6_K_QH + 32 * gh + 16 * (piece - 4);
-                const uint32_t sh = (p + w_lo) & 3u;
-                const uint32_t pa = p - sh;
-                const u32x4_a4 v = *(const u32x4_a4*)(w + pa);
-                pd.r[j][0] = v.x; pd.r[j][1] = v.y; pd.r[j][2] = v.z; pd.r[j][3] = v.w;
-                pd.r[j][4] = *(const uint32_t*)(w + pa + 16);
-                pd.r[j][5] = sh;
+        for (int j = 0; j < C::W_SLOTS; ++j) {
+            const int c = j >> 1;
+            const int q = wave + W * (j & 1);
+            const uint32_t win = c < kQ6QhCh ? 64u * GH + 16u * c
+                               : c < kQ6ScCh ? 128u + 32u * GH + 16u * (c - kQ6QhCh) : 192u;
+            uint32_t src;
+            if (full_tile) {
+                src = (c == kQ6ScCh && GH == 1 ? lbs : lb) + (uint32_t)(16 * q) * row_bytes + win;
             } else {
-                // the 16 scales (bytes 192..207) and d (208..209): dwords from 192 - (p & 2),
-                // the fifth only when the region starts 2 bytes into a dword, d by a u16 load
-                const uint32_t p = base + Q6_K_SC;
-                const uint32_t sh = (p + w_lo) & 3u;
-                const uint32_t pa = p - sh;
-                const u32x4_a4 v = *(const u32x4_a4*)(w + pa);
-                pd.r[j][0] = v.x; pd.r[j][1] = v.y; pd.r[j][2] = v.z; pd.r[j][3] = v.w;
-                pd.r[j][4] = *(const uint32_t*)(w + (sh ? pa + 16 : pa));
-                pd.r[j][5] = sh | ((uint32_t)*(const uint16_t*)(w + base + Q6_K_D) << 16);
+                const uint32_t base = (uint32_t)min(n0 + 16 * q + lrow, n - 1) * row_bytes + sbo;
+                const uint32_t sh = base & 3u;
+                src = base + 4u * (uint32_t)(lane & 3) + win +
+                      ((c == kQ6ScCh && GH == 1) ? sh : 0u - sh);
             }
-        }
-    };
-    auto commit_stage = [&](uint8_t* st, int gh, const Pending& pd) {
-#pragma unroll
-        for (int j = 0; j < C::R_SLOTS; ++j) {
-            const int i = tid + j * C::THREADS;
-            uint32_t r[6];
-#pragma unroll
-            for (int e = 0; e < 6; ++e) r[e] = pinned(pd.r[j][e]);
-            if (i < C::R_CHUNKS) {
-                const int piece = i / C::BN, row = i - piece * C::BN;
-                const uint32_t sh = r[5] & 3u;
-                uint8_t* dst = st + C::OFF_W + row * kQ6Row;
-                wu4 o;
-                o.x = __builtin_amdgcn_alignbyte(r[1], r[0], sh);
-                o.y = __builtin_amdgcn_alignbyte(r[2], r[1], sh);
-                o.z = __builtin_amdgcn_alignbyte(r[3], r[2], sh);
-                o.w = __builtin_amdgcn_alignbyte(r[4], r[3], sh);
-                if (piece < 6) {
-                    *(wu4*)(dst + 16 * piece) = o;
-                } else {
-                    // the 8 scales of this half, then d
-                    *(u32x2*)(dst + 96) = gh ? u32x2{o.z, o.w} : u32x2{o.x, o.y};
-                    *(uint32_t*)(dst + 104) = r[5] >> 16;
-                }
-            }
+            lds_load4(w + src, st + C::OFF_W + (c * C::BN + 16 * q) * 16);
         }
     };
 
@@ -710,29 +681,49 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         for (int r = 0; r < 16; ++r) sacc[a][r] = yacc[a][r] = 0.0f;
 
     float* scratch = (float*)(lds + 2 * C::STAGE) + wave * 32;
-    const int wrow = wave * 32 + r32;
+    uint32_t dbits = 0;  // d of the wave row's super-block, loaded in the stage of its half 0
 
     // One stage: half GH of a super-block (stage ranges are even and super-block aligned, so
     // stage s sits in LDS buffer GH and the first block of GH = 0 starts the scaled sums).
     auto run_stage = [&]<int GH>(int s) {
         uint8_t* cur = lds + GH * C::STAGE;
         uint8_t* nxt = lds + (1 - GH) * C::STAGE;
-        const uint8_t* wr = cur + C::OFF_W + wrow * kQ6Row;
-        // d of the super-block for the lane's output rows goes to the wave's scratch before the
-        // next stage's direct-to-LDS loads are issued (an LDS store while they are in flight
-        // would make the compiler wait for all of them)
-        if (GH == 1 && h == 0) scratch[r32] = f16_to_f32(*(const uint16_t*)(wr + 104));
-        Pending pd;
+        // chunk c of the lane's weight row: wr + c * BN * 16
+        const uint8_t* wr = cur + C::OFF_W + wrow * 16;
+        const uint32_t own = ro_own + (uint32_t)(s >> 1) * Q6_K_BYTES;
+        const uint32_t sh = own & 3u;  // the windows' lead before the row's bytes
+        // 16 bytes at byte sh of the window from chunk c: the chunk, the next one's first
+        // dword, realigned
+        auto window16 = [&](int c) {
+            const wu4 a = *(const wu4*)(wr + c * (C::BN * 16));
+            const uint32_t e = *(const uint32_t*)(wr + (c + 1) * (C::BN * 16));
+            return wu4{__builtin_amdgcn_alignbyte(a.y, a.x, sh), __builtin_amdgcn_alignbyte(a.z, a.y, sh),
+                       __builtin_amdgcn_alignbyte(a.w, a.z, sh), __builtin_amdgcn_alignbyte(e, a.w, sh)};
+        };
+        // d for the lane's output rows goes to the wave's scratch; half 0 loads the next one
+        if (GH == 1 && h == 0) scratch[r32] = f16_to_f32(dbits);
+        if (GH == 0) dbits = *(const uint16_t*)(w + own + Q6_K_D);
         const bool more = s + 1 < s_end;
-        if (more) issue_stage(s + 1, nxt, pd);
+        if (more) issue_stage.template operator()<1 - GH>(s + 1, nxt);
 
-        const wu4 qhb = *(const wu4*)(wr + 64 + 16 * h);
-        const u32x2 scv = *(const u32x2*)(wr + 96);  // the 8 scales of this half
+        const wu4 qhb = window16(kQ6QhCh + h);
+        // the half's 8 scales: at byte sh (half 0) or 8 - sh (half 1) of the scale chunk
+        uint32_t scx, scy;
+        {
+            const wu4 c = *(const wu4*)(wr + kQ6ScCh * (C::BN * 16));
+            if (GH == 0) {
+                scx = __builtin_amdgcn_alignbyte(c.y, c.x, sh);
+                scy = __builtin_amdgcn_alignbyte(c.z, c.y, sh);
+            } else {
+                scx = sh ? __builtin_amdgcn_alignbyte(c.z, c.y, 2u) : c.z;
+                scy = sh ? __builtin_amdgcn_alignbyte(c.w, c.z, 2u) : c.w;
+            }
+        }
         const uint8_t* act = cur;
         const float* dxl = (const float*)(cur + C::OFF_DX);
 
         auto block = [&]<bool FRESH>(int i) {
-            const wu4 ql = *(const wu4*)(wr + 32 * (i & 1) + 16 * h);
+            const wu4 ql = window16(2 * (i & 1) + h);
             const uint32_t lsh = i >= 2 ? 4u : 0u;
             // bits 2i, 2i+1 of every qh byte to bits 4, 5 of the same byte: a rotation right by
             // 2i - 4 (mod 32); the bits it carries across bytes are masked off
@@ -745,7 +736,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
                         (__builtin_amdgcn_alignbit(qhv[e], qhv[e], rot) & 0x30303030u);
             // scale of this lane's 16 values: sc[8 g + 2 i + h], local index 2 i + h
             const int si = 2 * i + h;
-            const uint32_t scw = si < 4 ? scv.x : scv.y;
+            const uint32_t scw = si < 4 ? scx : scy;
             const int sc = (int)(int8_t)((scw >> (8 * (si & 3))) & 0xFFu);
             const int s_hi = sc >> 4, s_lo = sc & 15;
             const wh2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
@@ -804,19 +795,14 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
 #pragma unroll
                 for (int r = 0; r < 16; ++r) yacc[mt][r] = fmaf(dr[r], sacc[mt][r], yacc[mt][r]);
         }
-        if (more) commit_stage(nxt, (s + 1) & 1, pd);
         __syncthreads();
     };
 
     // An empty split range (stages per split are rounded up to whole super-blocks) loads
     // nothing and contributes zeros.
     if (s_begin < s_end) {
-        {
-            Pending pd;
-            issue_stage(s_begin, lds, pd);
-            wait_vm();
-            commit_stage(lds, s_begin & 1, pd);
-        }
+        issue_stage.template operator()<0>(s_begin, lds);
+        wait_vm();
         __syncthreads();
         for (int s = s_begin; s < s_end; s += 2) {
             run_stage.template operator()<0>(s);
