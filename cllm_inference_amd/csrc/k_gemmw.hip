@@ -18,11 +18,10 @@
 // 32w .. 32w+31 (one MFMA tile) against all MT token tiles, so each wave unpacks only its own
 // rows, straight from the raw bytes in LDS into MFMA fragments, and the token fragments in LDS
 // are shared by all waves. K advances half a super-block (128 elements) per stage through two
-// LDS buffers, filled one stage ahead: the raw Q4_K bytes of the half (header + 64 quant
-// bytes per row) and dx by direct-to-LDS loads (global_load_lds); the int8 activations
-// through registers, widened to fp16 on the way in (token rows padded by 16 bytes, so the
-// 16-byte fragment reads of 16 consecutive tokens fall on distinct banks);
-// dx * bsum likewise, split into bf16 parts.
+// LDS buffers, filled one stage ahead, every operand by direct-to-LDS loads (global_load_lds):
+// the raw Q4_K bytes of the half (header + 64 quant bytes per row), dx, the activations as
+// fp16 integers (16-byte chunks swizzled by token, so the fragment reads of 16 consecutive
+// tokens fall on distinct banks) and dx * bsum split into bf16 parts.
 #include <cstdio>
 #include <cstdlib>
 
