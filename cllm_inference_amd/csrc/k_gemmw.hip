@@ -633,20 +633,24 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         dx_off[j] = (uint32_t)min(m0 + tok, m - 1) * (uint32_t)nb + b;
     }
 
-    // every operand goes straight to LDS (direct-to-LDS loads); GH = s & 1
-    auto issue_stage = [&]<int GH>(int s, uint8_t* st) {
+    // every operand goes straight to LDS (direct-to-LDS loads); GH = s & 1. A stage's loads
+    // go out in two parts (PART < 0: both), each before half of the stage's MFMA work, as
+    // for Q4_K: part 0 the activations, dx and the first half of the weight wave-loads.
+    auto issue_stage = [&]<int GH, int PART>(int s, uint8_t* st) {
         const int sb = s >> 1;
+        if (PART <= 0) {
 #pragma unroll
-        for (int j = 0; j < C::A_SLOTS; ++j) {
-            const int L = wave + j * W;
-            if (C::A_LOADS % W == 0 || L < C::A_LOADS)
-                lds_load16((const uint8_t*)qh + a_off[j] + (uint32_t)s * (2u * kKS), st + L * 1024);
-        }
+            for (int j = 0; j < C::A_SLOTS; ++j) {
+                const int L = wave + j * W;
+                if (C::A_LOADS % W == 0 || L < C::A_LOADS)
+                    lds_load16((const uint8_t*)qh + a_off[j] + (uint32_t)s * (2u * kKS), st + L * 1024);
+            }
 #pragma unroll
-        for (int j = 0; j < C::DX_SLOTS; ++j) {
-            const int L = wave + j * W;
-            if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
-                lds_load4(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + L * 256);
+            for (int j = 0; j < C::DX_SLOTS; ++j) {
+                const int L = wave + j * W;
+                if (C::DX_LOADS % W == 0 || L < C::DX_LOADS)
+                    lds_load4(xs + dx_off[j] + (uint32_t)s * 4, st + C::OFF_DX + L * 256);
+            }
         }
         const uint32_t sbo = (uint32_t)sb * Q6_K_BYTES;
         // a full tile: rows 16 q + lrow at rowoff0 + 16 q row_bytes, all with the shift of
@@ -656,6 +660,8 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         const uint32_t lbs = lb + 2u * sh0;                                   // scales of half 1
 #pragma unroll
         for (int j = 0; j < C::W_SLOTS; ++j) {
+            if (PART == 0 && j >= C::W_SLOTS / 2) continue;
+            if (PART == 1 && j < C::W_SLOTS / 2) continue;
             const int c = j >> 1;
             const int q = wave + W * (j & 1);
             const uint32_t win = c < kQ6QhCh ? 64u * GH + 16u * c
@@ -703,7 +709,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
         if (GH == 1 && h == 0) scratch[r32] = f16_to_f32(dbits);
         if (GH == 0) dbits = *(const uint16_t*)(w + own + Q6_K_D);
         const bool more = s + 1 < s_end;
-        if (more) issue_stage.template operator()<1 - GH>(s + 1, nxt);
+        if (more) issue_stage.template operator()<1 - GH, 0>(s + 1, nxt);
 
         const wu4 qhb = window16(kQ6QhCh + h);
         // the half's 8 scales: at byte sh (half 0) or 8 - sh (half 1) of the scale chunk
@@ -773,14 +779,14 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
                 }
             }
         };
-        if constexpr (GH == 0) {
+        if constexpr (GH == 0)
             block.template operator()<true>(0);
+        else
+            block.template operator()<false>(0);
+        block.template operator()<false>(1);
+        if (more) issue_stage.template operator()<1 - GH, 1>(s + 1, nxt);
 #pragma unroll 1
-            for (int i = 1; i < 4; ++i) block.template operator()<false>(i);
-        } else {
-#pragma unroll 1
-            for (int i = 0; i < 4; ++i) block.template operator()<false>(i);
-        }
+        for (int i = 2; i < 4; ++i) block.template operator()<false>(i);
         if (more) wait_vm();
         if constexpr (GH == 1) {
             float dr[16];
@@ -800,7 +806,7 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q6k(const uint8_t* __restrict_
     // An empty split range (stages per split are rounded up to whole super-blocks) loads
     // nothing and contributes zeros.
     if (s_begin < s_end) {
-        issue_stage.template operator()<0>(s_begin, lds);
+        issue_stage.template operator()<0, -1>(s_begin, lds);
         wait_vm();
         __syncthreads();
         for (int s = s_begin; s < s_end; s += 2) {
