@@ -1073,10 +1073,10 @@ int device_cus() {
     return cached;
 }
 
-// Split-K factor: workgroups up to `target`, at least 8 stages per split.
-int choose_splits(int tiles, int stages, int target) {
+// Split-K factor: workgroups up to `target`, at least min_stages stages per split.
+int choose_splits(int tiles, int stages, int target, int min_stages = 8) {
     int sp = 1;
-    while (sp < 8 && tiles * sp * 2 <= target && stages / (sp * 2) >= 8) sp *= 2;
+    while (sp < 8 && tiles * sp * 2 <= target && stages / (sp * 2) >= min_stages) sp *= 2;
     return sp;
 }
 
@@ -1094,6 +1094,7 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
     const int mt = tu.gemm_ttiles.load(std::memory_order_relaxed);
     const int cus = device_cus();
     int target = 2 * cus;  // workgroups to aim for
+    int min_stages = 8;    // stages per split at least
     if (is_b32(type)) {
         // 32-element block types: 128 x 32 tiles up to 32 rows, else 128 x 64 (the per-block
         // d of the 16 output rows a lane holds stays in registers, which larger token tiles
@@ -1105,31 +1106,35 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
         p.wv = 4, p.nt = 1, p.mt = 2;
         if ((wv == 8 || wv == 4) && nt == 1 && (mt == 2 || mt == 4)) p.wv = wv, p.mt = mt;
     } else if (wv != 0 && (type == T_Q4_K ||
-                           (wv == 8 && nt == 1 && (mt == 4 || mt == 2)) || (wv == 4 && nt == 1 && mt == 1))) {
-        // Q5_K has the three shapes of the default plan compiled
+                           (wv == 8 && nt == 1 && (mt == 4 || mt == 2)) ||
+                           (wv == 4 && nt == 1 && (mt == 2 || mt == 1)))) {
+        // Q5_K has the four shapes of the default plan compiled
         p.wv = wv, p.nt = nt, p.mt = mt;
     } else {
-        // From sweeps on MI355X at m = 512 (us for n = 14336 / 4096 / 1024): 256 x 128 tiles
-        // when they fill the CUs (163), else 256 x 64 tiles split to one workgroup per CU
-        // (4096: 63 against 70 for 128 x 32), else 128 x 32 tiles split to two per CU (1024: 30).
-        // The 8-wave workgroups hold one CU's LDS each, so their split target is one per CU:
-        // with the split-K sums completed in the GEMM, 14336 x 4096 runs its 224 tiles unsplit
-        // in 123 us against 134 us split in two (448 workgroups, a second round on 192 CUs).
+        // From sweeps on MI355X over n = 14336 / 4096 / 1024 and m = 64 .. 512 (k = 4096):
+        // - 256 x 128 tiles (8 waves, one workgroup per CU) when they fill the CUs: 14336 x
+        //   4096 at m = 512 runs its 224 tiles unsplit in 129 us (152 for the best 128 x 64);
+        // - else 128 x 64 tiles (4 waves, two workgroups per CU) above 32 rows when there are
+        //   at least 3/8 as many as CUs, split to about two workgroups per CU (4096 at m = 512:
+        //   50 us against 53 for 256 x 64; 14336 at m = 64: 33 against 39 for 128 x 32);
+        // - else 128 x 32 tiles split to about two workgroups per CU, down to 4 stages per
+        //   split (4096 at m = 64: 21 us for 8 splits against 22 for 4; 1024 at m = 128: 20
+        //   against 22).
         const int t84 = ((n + 255) / 256) * ((m + 127) / 128);
-        const int t82 = ((n + 255) / 256) * ((m + 63) / 64);
+        const int t42 = ((n + 127) / 128) * ((m + 63) / 64);
         if (t84 >= cus * 3 / 4) {
             p.wv = 8, p.nt = 1, p.mt = 4;
             target = cus;
-        } else if (t82 >= cus / 4) {
-            p.wv = 8, p.nt = 1, p.mt = 2;
-            target = cus;
+        } else if (m > 32 && t42 >= cus * 3 / 8) {
+            p.wv = 4, p.nt = 1, p.mt = 2;
         } else {
             p.wv = 4, p.nt = 1, p.mt = 1;
+            min_stages = 4;
         }
     }
     const int bn = 32 * p.nt * p.wv, bm = 32 * p.mt;
     const int tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
-    p.splits = choose_splits(tiles, k / kKS, target);
+    p.splits = choose_splits(tiles, k / kKS, target, min_stages);
     const int sp = tu.gemm_splits.load(std::memory_order_relaxed);
     if (sp >= 1 && sp <= 16 && sp <= k / kKS) p.splits = sp;
     return p;
@@ -1272,11 +1277,13 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
         CLLM_GEMMW_B32(T_Q5_0)
 #undef CLLM_GEMMW_B32
     } else if (type == T_Q5_K) {
-        // the three shapes of the default plan (tuning overrides apply to Q4_K only)
+        // the four shapes of the default plan (the only ones the tuning override takes)
         if (p.wv == 8 && p.nt == 1 && p.mt == 4)
             e = launch_q4<8, 1, 4, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
         else if (p.wv == 8 && p.nt == 1 && p.mt == 2)
             e = launch_q4<8, 1, 2, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
+        else if (p.wv == 4 && p.nt == 1 && p.mt == 2)
+            e = launch_q4<4, 1, 2, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
         else
             e = launch_q4<4, 1, 1, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
     } else {

@@ -156,7 +156,7 @@ def test_m_sweep_q5_k_large_batches_vs_reference_golden(gpu, orc, m, gemm_kernel
     x = S.config_activation("c4_m_sweep", m, k)
     plan = gpu.matmul_plan(qt, k, n, m)
     print("q5_k 14336x4096 m", m, "plan", plan, flush=True)
-    assert plan.startswith("k_gemmw_q4k<8,1,%d,Q5_K>" % (2 if m == 256 else 4)), plan
+    assert plan.startswith("k_gemmw_q4k<4,1,2,Q5_K>" if m == 256 else "k_gemmw_q4k<8,1,4,Q5_K>"), plan
     y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, None, k, n)
     torch.cuda.synchronize()
     y = y.cpu().numpy()
