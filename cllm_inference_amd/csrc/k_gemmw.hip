@@ -1101,10 +1101,12 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
         // would spill); split K to about two workgroups per CU
         p.wv = 4, p.nt = 1, p.mt = m <= 32 ? 1 : 2;
     } else if (type == T_Q6_K) {
-        // 128 weight rows x 64 tokens (4 waves, two workgroups per CU); the tuning override
-        // takes the other compiled shapes (8 waves and / or 128 tokens)
-        p.wv = 4, p.nt = 1, p.mt = 2;
-        if ((wv == 8 || wv == 4) && nt == 1 && (mt == 2 || mt == 4)) p.wv = wv, p.mt = mt;
+        // 128 weight rows x 64 tokens (4 waves, two workgroups per CU), x 32 tokens up to 32
+        // rows; the tuning override takes the other compiled shapes (8 waves and / or 128
+        // tokens)
+        p.wv = 4, p.nt = 1, p.mt = m <= 32 ? 1 : 2;
+        if ((wv == 8 && nt == 1 && (mt == 2 || mt == 4)) || (wv == 4 && nt == 1 && mt >= 1 && mt <= 4 && mt != 3))
+            p.wv = wv, p.mt = mt;
     } else if (wv != 0 && (type == T_Q4_K ||
                            (wv == 8 && nt == 1 && (mt == 4 || mt == 2)) ||
                            (wv == 4 && nt == 1 && (mt == 2 || mt == 1)))) {
@@ -1262,6 +1264,8 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
             e = launch_q6<8, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
         else if (p.mt == 4)
             e = launch_q6<4, 4>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
+        else if (p.mt == 1)
+            e = launch_q6<4, 1>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
         else
             e = launch_q6<4, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
     } else if (is_b32(type)) {

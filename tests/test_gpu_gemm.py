@@ -187,3 +187,22 @@ def test_q6_k_prefill_super_block_alignments(gpu, orc, k, n, gemm_kernel):
         y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
         gpu.tune("gemm_splits")
         check_close(y, yo, exact, abs_sum, f"q6_k {n}x{k} splits={splits}")
+
+
+@pytest.mark.parametrize("shape", [(4, 1, 1), (4, 1, 2), (4, 1, 4), (8, 1, 2), (8, 1, 4)])
+def test_q6_k_tile_shapes(gpu, orc, shape, gemm_kernel):
+    """Every compiled Q6_K weight-row tile shape (the plan's 128 x 32 and 128 x 64, and the
+    tuning override's others) on ragged batches, against the oracle."""
+    if gemm_kernel != "default":
+        pytest.skip("tile shapes of the default kernel")
+    k, n = 1024, 300
+    for m in (16, 40, 100):
+        w = S.make_weight(S.Q6_K, n, k, 5 + m)
+        x = S.make_activation(m, k, 6 + m, outliers=True)
+        exact, abs_sum = orc.matmul_f64(x, w, S.Q6_K, None, k, n, m)
+        yo = orc.matmul(x, w, S.Q6_K, None, k, n, m)
+        gpu.tune("gemm_tiles", *shape)
+        print("q6_k shape", shape, "m", m, gpu.matmul_plan(S.Q6_K, k, n, m), flush=True)
+        y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
+        gpu.tune("gemm_tiles")
+        check_close(y, yo, exact, abs_sum, f"q6_k {shape} m{m}")
