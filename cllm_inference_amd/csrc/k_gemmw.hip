@@ -1102,10 +1102,10 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
         p.wv = 4, p.nt = 1, p.mt = m <= 32 ? 1 : 2;
     } else if (type == T_Q6_K) {
         // 128 weight rows x 64 tokens (4 waves, two workgroups per CU), x 32 tokens up to 32
-        // rows; the tuning override takes the other compiled shapes (8 waves and / or 128
-        // tokens)
+        // rows; the tuning override takes the other compiled shapes (256 x 64 on 8 waves,
+        // 128 x 128)
         p.wv = 4, p.nt = 1, p.mt = m <= 32 ? 1 : 2;
-        if ((wv == 8 && nt == 1 && (mt == 2 || mt == 4)) || (wv == 4 && nt == 1 && mt >= 1 && mt <= 4 && mt != 3))
+        if ((wv == 8 && nt == 1 && mt == 2) || (wv == 4 && nt == 1 && (mt == 1 || mt == 2 || mt == 4)))
             p.wv = wv, p.mt = mt;
     } else if (wv != 0 && (type == T_Q4_K ||
                            (wv == 8 && nt == 1 && (mt == 4 || mt == 2)) ||
@@ -1258,9 +1258,7 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     part = p.splits > 1 ? (float*)((char*)part + kCounterBytes) : nullptr;
     hipError_t e = hipErrorNotSupported;
     if (type == T_Q6_K) {
-        if (p.wv == 8 && p.mt == 4)
-            e = launch_q6<8, 4>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
-        else if (p.wv == 8)
+        if (p.wv == 8)
             e = launch_q6<8, 2>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);
         else if (p.mt == 4)
             e = launch_q6<4, 4>(w, k, n, m, qh, xs, bias, y, part, counters, p.splits, stream);

@@ -189,7 +189,7 @@ def test_q6_k_prefill_super_block_alignments(gpu, orc, k, n, gemm_kernel):
         check_close(y, yo, exact, abs_sum, f"q6_k {n}x{k} splits={splits}")
 
 
-@pytest.mark.parametrize("shape", [(4, 1, 1), (4, 1, 2), (4, 1, 4), (8, 1, 2), (8, 1, 4)])
+@pytest.mark.parametrize("shape", [(4, 1, 1), (4, 1, 2), (4, 1, 4), (8, 1, 2)])
 def test_q6_k_tile_shapes(gpu, orc, shape, gemm_kernel):
     """Every compiled Q6_K weight-row tile shape (the plan's 128 x 32 and 128 x 64, and the
     tuning override's others) on ragged batches, against the oracle."""
