@@ -476,14 +476,20 @@ bool gemm_forced();
 // at 4 / 8 / 16 / 32 / 64 rows 21.3 / 19.5 / 20.7 / 29.0 / 49 against 17.4 (GEMV) / 28.7 /
 // 27.7 / 28.9 / 43.5 (MFMA); Q8_0 4096x4096 at 4 / 8 / 16 / 64 rows 13.6 / 13.5 / 12.4 / 20.9
 // against 10.2 / 12.8 / 22.0 / 30.6.
+// Above 16 rows the K-quants of at least kSmallMaxN output rows take the weight-row MFMA
+// kernel instead: Q5_K 14336x4096 at 20 / 24 / 28 / 32 rows 25.9 / 26.5 / 26.5 / 27.0 us
+// against 28.2 / 28.6 / 28.8 / 29.6 (Q4_K 4096x4096 and 1024x4096 stay faster here: 15.3
+// against 18.9 us at 32 rows).
 constexpr int kSmallMinRows = 8;
+constexpr int kSmallMaxN = 8192;
 
-bool use_small(uint32_t type, int k, int m) {
+bool use_small(uint32_t type, int k, int n, int m) {
     const int knob = tuning().gemm_small.load(std::memory_order_relaxed);
     if (knob == 2 || tuning().gemm_kind.load(std::memory_order_relaxed) != 0 ||
         !gemm_sm_supported(type, k, m))
         return false;
     if (knob == 1) return m >= 3;
+    if (type != T_Q8_0 && m > 16 && n >= kSmallMaxN) return false;
     return m >= kSmallMinRows && m <= (type == T_Q8_0 ? 64 : 32);
 }
 
@@ -492,8 +498,8 @@ bool use_small(uint32_t type, int k, int m) {
 // weight-row kernel has; 64 for the others, whose int8 kernel only overtakes the GEMV there
 // (Q5_K 14336 x 4096: 155 us at 16 rows against ~50 us on the GEMV). A forced kernel choice
 // (the tuning knob gemm_kernel) takes the MFMA route from 16 rows for every type.
-bool use_mfma(uint32_t type, int k, int m) {
-    if (k % 256 != 0 || !gemm_supported(type) || use_small(type, k, m)) return false;
+bool use_mfma(uint32_t type, int k, int n, int m) {
+    if (k % 256 != 0 || !gemm_supported(type) || use_small(type, k, n, m)) return false;
     const int min_rows = (gemmw_supported(type) || gemm_forced()) ? kMfmaMinRows : 4 * kMfmaMinRows;
     return m >= min_rows;
 }
@@ -515,7 +521,7 @@ GemmKind gemm_kind(uint32_t type) {
 
 // Split-K bytes the MFMA route of this shape needs (the weight-row kernel only).
 size_t part_bytes_for(uint32_t type, int k, int n, int m) {
-    if (use_small(type, k, m)) return gemm_sm_partial_bytes(type, k, n, m);
+    if (use_small(type, k, n, m)) return gemm_sm_partial_bytes(type, k, n, m);
     return gemm_kind(type) == GemmKind::W16 ? gemmw_partial_bytes(type, k, n, m) : 0;
 }
 
@@ -524,7 +530,7 @@ size_t part_bytes_for(uint32_t type, int k, int n, int m) {
 hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const int8_t* qs,
                     const float* sc, const int32_t* bs, const float* bias, float* y,
                     const WsView& ws, hipStream_t stream) {
-    if (use_small(type, k, m))
+    if (use_small(type, k, n, m))
         return launch_gemm_sm_q8(type, w, k, n, m, qs, sc, bs, bias, y, ws.part, ws.part_cap, stream);
     const GemmKind kind = gemm_kind(type);
     if (kind == GemmKind::W16) {
@@ -543,7 +549,7 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
 // MFMA route from fp32 activations: quantize straight into the format the kernel reads.
 hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                         const float* bias, float* y, const WsView& ws, hipStream_t stream) {
-    if (use_small(type, k, m))
+    if (use_small(type, k, n, m))
         return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
     const int64_t nblk = (int64_t)m * k / 32;
     const GemmKind kind = gemm_kind(type);
@@ -569,16 +575,16 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
 // workgroup re-quantizes all of its rows and that redundant work grows with the row count.
 constexpr int kFusedMaxRows = 2;
 
-bool needs_workspace(uint32_t type, int k, int m) {
+bool needs_workspace(uint32_t type, int k, int n, int m) {
     if (!has_kernel(type)) return false;  // the float-dot kernels read fp32 rows directly
-    return use_mfma(type, k, m) || use_small(type, k, m) || m > kFusedMaxRows;
+    return use_mfma(type, k, n, m) || use_small(type, k, n, m) || m > kFusedMaxRows;
 }
 
 // GEMV route on fp32 activation rows.
 hipError_t run_gemv_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                         const float* bias, float* y, const WsView& ws, hipStream_t stream,
                         bool accumulate = false) {
-    if (!accumulate && use_small(type, k, m))
+    if (!accumulate && use_small(type, k, n, m))
         return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
     if (m <= kFusedMaxRows)
         return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream, accumulate);
@@ -595,7 +601,7 @@ int stream_workspace(DeviceState* st, hipStream_t s, uint32_t type, int k, int n
     auto& slot = st->dev_ws[s];
     if (!slot) slot = std::make_unique<Workspace>();
     HIP_TRY(slot->ensure(k, m, s));
-    if (n > 0 && (use_mfma(type, k, m) || use_small(type, k, m)))
+    if (n > 0 && (use_mfma(type, k, n, m) || use_small(type, k, n, m)))
         HIP_TRY(slot->ensure_part(part_bytes_for(type, k, n, m), s));
     *out = slot.get();
     return CLLM_HIP_OK;
@@ -617,9 +623,9 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
     if ((rc = resolve_weights(st, w, row_bytes(type, in_dim) * (size_t)out_dim, &wd))) return rc;
     HIP_TRY(st->x.ensure(xb, st->stream));
     HIP_TRY(st->y.ensure(yb, st->stream));
-    if (needs_workspace(type, in_dim, n_rows)) {
+    if (needs_workspace(type, in_dim, out_dim, n_rows)) {
         HIP_TRY(st->act.ensure(in_dim, n_rows, st->stream));
-        if (use_mfma(type, in_dim, n_rows) || use_small(type, in_dim, n_rows))
+        if (use_mfma(type, in_dim, out_dim, n_rows) || use_small(type, in_dim, out_dim, n_rows))
             HIP_TRY(st->act.ensure_part(part_bytes_for(type, in_dim, out_dim, n_rows), st->stream));
     }
     HIP_TRY(hipMemcpyAsync(st->x.p, x, xb, hipMemcpyHostToDevice, st->stream));
@@ -633,7 +639,7 @@ int host_matmul(const char* who, const float* x, const void* w, uint32_t type, c
     if (!has_kernel(type)) {
         HIP_TRY(launch_gemv_f(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
                               (float*)st->y.p, st->stream));
-    } else if (use_mfma(type, in_dim, n_rows)) {
+    } else if (use_mfma(type, in_dim, out_dim, n_rows)) {
         HIP_TRY(run_gemm_f32(type, wd, in_dim, out_dim, n_rows, (const float*)st->x.p, bd,
                              (float*)st->y.p, st->act.v, st->stream));
     } else {
@@ -824,7 +830,7 @@ int cllm_hip_gemv_q8_dev(const void* w, uint32_t type, int in_dim, int out_dim, 
     DeviceState* st;
     if ((rc = acquire(&st))) return rc;
     hipStream_t s = (hipStream_t)stream;
-    if (!use_mfma(type, in_dim, n_rows) && !use_small(type, in_dim, n_rows)) {
+    if (!use_mfma(type, in_dim, out_dim, n_rows) && !use_small(type, in_dim, out_dim, n_rows)) {
         HIP_TRY(launch_gemv(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums,
                             bias, y, s));
         return CLLM_HIP_OK;
@@ -973,12 +979,12 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
         return CLLM_HIP_OK;
     }
     WsView v;
-    if (needs_workspace(type, in_dim, n_rows)) {
+    if (needs_workspace(type, in_dim, out_dim, n_rows)) {
         Workspace* ws;
         if ((rc = stream_workspace(st, s, type, in_dim, out_dim, n_rows, &ws))) return rc;
         v = ws->v;
     }
-    if (!use_mfma(type, in_dim, n_rows)) {
+    if (!use_mfma(type, in_dim, out_dim, n_rows)) {
         // decode-sized batch: one or two rows in a single launch that quantizes them in LDS
         HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
         return CLLM_HIP_OK;
@@ -1008,9 +1014,9 @@ int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t typ
     // 256 bytes). Nothing is allocated.
     WsView v;
     size_t act = 0, pb = 0;
-    if (needs_workspace(type, in_dim, n_rows)) {
+    if (needs_workspace(type, in_dim, out_dim, n_rows)) {
         act = act_bytes(in_dim, n_rows);
-        if (use_mfma(type, in_dim, n_rows) || use_small(type, in_dim, n_rows))
+        if (use_mfma(type, in_dim, out_dim, n_rows) || use_small(type, in_dim, out_dim, n_rows))
             pb = part_bytes_for(type, in_dim, out_dim, n_rows);
     }
     if (act + pb > kStaticScratchBytes)
@@ -1026,7 +1032,7 @@ int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t typ
         // activations in these bytes (a fill kernel, so the call can be captured in a graph)
         HIP_TRY(gemmw_workspace_init(v.part, gemmw_counter_bytes(), s));
     }
-    if (!use_mfma(type, in_dim, n_rows)) {
+    if (!use_mfma(type, in_dim, out_dim, n_rows)) {
         HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
         return CLLM_HIP_OK;
     }
@@ -1050,7 +1056,7 @@ int cllm_hip_matmul_quant_residual_dev(const float* x, const void* w, uint32_t t
     hipStream_t s = (hipStream_t)stream;
     Workspace* ws = nullptr;
     if ((rc = stream_workspace(st, s, type, in_dim, out_dim, n_rows, &ws))) return rc;
-    if (has_kernel(type) && !use_mfma(type, in_dim, n_rows) && !use_small(type, in_dim, n_rows)) {
+    if (has_kernel(type) && !use_mfma(type, in_dim, out_dim, n_rows) && !use_small(type, in_dim, out_dim, n_rows)) {
         // the GEMV adds into y in its epilogue
         HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, ws->v, s,
                              true));
@@ -1424,11 +1430,10 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
 }
 
 const char* cllm_hip_matmul_route(uint32_t type, int in_dim, int out_dim, int n_rows) {
-    (void)out_dim;
     if (gemv_f_supported(type)) return "fdot";
     if (!has_kernel(type)) return "none";
-    if (use_small(type, in_dim, n_rows)) return "small";
-    return use_mfma(type, in_dim, n_rows) ? "mfma" : "gemv";
+    if (use_small(type, in_dim, out_dim, n_rows)) return "small";
+    return use_mfma(type, in_dim, out_dim, n_rows) ? "mfma" : "gemv";
 }
 
 }  // extern "C"

@@ -111,7 +111,11 @@ def test_small_batch_plans():
     token tiles of 16, K split over workgroups in ranges of at most 1024 elements, K parts per
     workgroup chosen for one workgroup per CU (256 CUs when no device is present)."""
     assert C.matmul_plan(S.Q5_K, 4096, 14336, 16) == "k_gemm_sm<Q5_K,1> splits=4 kp=1"
-    assert C.matmul_plan(S.Q5_K, 4096, 14336, 32) == "k_gemm_sm<Q5_K,2> splits=4 kp=1"
+    # above 16 rows, matrices of 8192 output rows or more take the weight-row kernel
+    assert C.matmul_plan(S.Q5_K, 4096, 14336, 32) == "k_gemmw_q4k<4,1,1,Q5_K> splits=4"
+    assert C.matmul_plan(S.Q5_K, 4096, 14336, 17) == "k_gemmw_q4k<4,1,1,Q5_K> splits=4"
+    assert C.matmul_plan(S.Q5_K, 4096, 4096, 32) == "k_gemm_sm<Q5_K,2> splits=4 kp=4"
+    assert C.matmul_plan(S.Q8_0, 4096, 14336, 32) == "k_gemm_sm<Q8_0,2> splits=4 kp=1"
     assert C.matmul_plan(S.Q8_0, 4096, 4096, 16) == "k_gemm_sm<Q8_0,1> splits=4 kp=4"
     assert C.matmul_plan(S.Q8_0, 4096, 4096, 64) == "k_gemm_sm<Q8_0,4> splits=4 kp=4"
     assert C.matmul_plan(S.Q4_K, 14336, 4096, 16) == "k_gemm_sm<Q4_K,1> splits=14 kp=1"
