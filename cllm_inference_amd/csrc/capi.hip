@@ -500,8 +500,26 @@ bool use_small(uint32_t type, int k, int n, int m) {
 // (the tuning knob gemm_kernel) takes the MFMA route from 16 rows for every type.
 bool use_mfma(uint32_t type, int k, int n, int m) {
     if (k % 256 != 0 || !gemm_supported(type) || use_small(type, k, n, m)) return false;
-    const int min_rows = (gemmw_supported(type) || gemm_forced()) ? kMfmaMinRows : 4 * kMfmaMinRows;
-    return m >= min_rows;
+    if (gemm_forced()) return m >= kMfmaMinRows;
+    if (!gemmw_supported(type)) return m >= 4 * kMfmaMinRows;
+    if (m >= kMfmaMinRows) return true;
+    if (type != T_Q6_K && type != T_Q4_0 && type != T_Q5_0) return false;
+    // Q6_K, Q4_0 and Q5_0 have no small-batch kernel. Below 16 rows their GEMV reads the
+    // weights once per launch (8, 4 or 2 rows each, as LDS allows), and the weight-row kernel,
+    // which pads the batch to one 16-row tile, takes about the time of its 16-row call. On
+    // matrices of 32 M weights or more it wins from three GEMV launches or 8 rows (Q6_K: 8 rows
+    // in two launches); on smaller ones from four launches. MI355X, cold weights, us, GEMV
+    // against weight-row kernel:
+    //   Q6_K 4096x14336, 5 / 8 / 15 rows:   41.7 / 58.5 / 107.3 against 34.9 - 35.5
+    //   Q6_K 14336x4096, 7 / 8 / 12 rows:   41.2 / 30.2 / 45.9 against 33.8 - 34.4
+    //   Q4_0 14336x4096, 7 / 8 / 15 rows:   34.7 / 27.0 / 57.3 against 24.0 - 24.5
+    //   Q5_0 4096x4096,  7 / 8 / 15 rows:   20.6 / 12.9 / 30.4 against 19.7 - 19.9
+    //   Q6_K 1024x4096,  7 / 8 / 15 rows:   15.5 / 10.5 / 23.2 against 19.9 - 20.4
+    const int launches = gemv_launch_count(type, k, m);
+    const bool large = (int64_t)n * k >= (int64_t(32) << 20);
+    if (launches >= (large ? 3 : 4)) return true;
+    if (m < 8 || !large) return false;
+    return type != T_Q6_K || launches >= 2;
 }
 
 // MFMA kernel choice. Default: the weight-row fp16 kernel (k_gemmw.hip) where it has the

@@ -1641,6 +1641,32 @@ static void plan_rows(const char* tname, int k, int n, int m, char* buf, size_t 
     snprintf(buf, cap, "%s<%s,%d> launches=%d", name, tname, mr0, launches);
 }
 
+// Launches gemv_all_rows makes for m activation rows (each streams the whole matrix).
+template <uint32_t T>
+static int launches_for(int k, int m) {
+    const int lim = max_rows_per_launch<T>(k);
+    int launches = 0;
+    for (int t = 0; t < m; ++launches) {
+        const int left = m - t;
+        int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        while (mr > lim) mr /= 2;
+        t += mr;
+    }
+    return launches;
+}
+
+int gemv_launch_count(uint32_t type, int k, int m) {
+    switch (type) {
+        case T_Q4_K: return launches_for<T_Q4_K>(k, m);
+        case T_Q5_K: return launches_for<T_Q5_K>(k, m);
+        case T_Q6_K: return launches_for<T_Q6_K>(k, m);
+        case T_Q8_0: return launches_for<T_Q8_0>(k, m);
+        case T_Q4_0: return launches_for<T_Q4_0>(k, m);
+        case T_Q5_0: return launches_for<T_Q5_0>(k, m);
+        default: return 1;
+    }
+}
+
 void gemv_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap) {
     switch (type) {
         case T_Q4_K: return plan_rows<T_Q4_K>("Q4_K", k, n, m, buf, cap);

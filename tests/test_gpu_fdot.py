@@ -6,8 +6,9 @@ by row in matmul_quant_batch, 1471-1474).
 Bars (the same as for the vec_dot types):
   - |gpu - ref| <= 1e-4 * max(|ref|, 2^-8 * A) against the reference's own fp32 output
     (golden vectors from the compiled reference), A = the row's sum of |x_i * w_i|, and
-    |gpu - exact| <= max(1e-4 * max(|exact|, 2^-10 * A), 2 * |ref - exact|) against the
-    fp64 sum of the same products;
+    |gpu - exact| <= max(1e-4 * max(|exact|, 2^-10 * A), 2 * |ref - exact|, R * A) against
+    the fp64 sum of the same products, R = the reference's largest |ref - exact| / A over the
+    same output;
   - host and device entry points, and a batch row and the same row alone, agree bit for bit.
 """
 import numpy as np

@@ -5,7 +5,8 @@ engine.
 Same bars as the GEMV tests (check_close in test_gpu_parity.py): |gpu - ref| <=
 1e-4 * max(|ref|, 2^-8 * A) against the reference's fp32 output, and no further from the fp64
 evaluation of the same quantized terms than max(1e-4 * max(|exact|, 2^-10 * A),
-2 * |ref - exact|) (A = sum of absolute per-block terms).
+2 * |ref - exact|, R * A) (A = sum of absolute per-block terms, R = the reference's largest
+|ref - exact| / A over the same output).
 """
 import numpy as np
 import pytest
@@ -93,6 +94,24 @@ def test_mfma_partial_tiles_and_bias(gpu, orc, qt):
         exact, abs_sum = orc.matmul_f64(x, w, qt, bias, k, n, m)
         yo = orc.matmul(x, w, qt, bias, k, n, m)
         check_close(y, yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")
+
+
+@pytest.mark.parametrize("qt, k, n, m", [(S.Q6_K, 4096, 14336, 7), (S.Q6_K, 4096, 14336, 13),
+                                         (S.Q6_K, 14336, 4096, 5), (S.Q4_0, 4096, 14336, 8),
+                                         (S.Q5_0, 4096, 4096, 15), (S.Q6_K, 4096, 1024, 15)])
+def test_mid_batches_on_weight_row_kernel(gpu, orc, qt, k, n, m, gemm_kernel):
+    """Batches below 16 rows that the default route sends to the weight-row kernel (one
+    partly filled 16-row tile) on full-size matrices, every output against the oracle."""
+    if gemm_kernel != "default":
+        pytest.skip("the default route only")
+    assert gpu.matmul_route(qt, k, n, m) == "mfma"
+    w = S.make_weight(qt, n, k, 11 + m)
+    x = S.make_activation(m, k, 12 + m, outliers=True)
+    print("mid batch", S.TYPE_NAMES[qt], n, k, m, gpu.matmul_plan(qt, k, n, m), flush=True)
+    y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, None, k, n).cpu().numpy()
+    yo = orc.matmul(x, w, qt, None, k, n, m, threads=8)
+    exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+    check_close(y, yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")
 
 
 def test_full_prefill_layer_sampled_rows(gpu, orc):

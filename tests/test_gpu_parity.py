@@ -5,10 +5,17 @@ Bars (written into each test):
   - Outputs: |gpu - ref| <= 1e-4 * max(|ref|, 2^-8 * A) against the reference's own fp32
     output, where A is the row's sum of absolute per-block terms; and, against the fp64
     evaluation of the same quantized terms,
-    |gpu - exact| <= max(1e-4 * max(|exact|, 2^-10 * A), 2 * |ref - exact|):
-    never further from the exact value than twice the reference's own rounding error. The
-    reference's sequential fp32 sum is itself up to 1.5e-4 away from exact under the 2^-10
-    floor on outlier inputs, which is why neither gate can use that floor alone.
+    |gpu - exact| <= max(1e-4 * max(|exact|, 2^-10 * A), 2 * |ref - exact|, R * A), where
+    R = max over the same output of |ref - exact| / A: never further from the exact value
+    than twice the reference's own rounding error there, or than the reference's worst
+    rounding anywhere in the output relative to A. The reference's sequential fp32 sum is
+    itself up to 1.5e-4 away from exact under the 2^-10 floor on outlier inputs, which is
+    why neither gate can use that floor alone. The R * A term is there because a different
+    fp32 order than the reference's (split-K partials, fma per block) can miss the first two
+    at an element where the reference happens to land near the exact value: on Q4_0
+    14336 x 4096 at 8 rows (128 blocks a row), a CPU emulation of the weight-row kernel's
+    order lands 5.1e-6 from exact at one element against an allowance of 4.5e-6, while its
+    worst |gpu - exact| / A over the output is 1.4e-7 against the reference's 2.9e-7.
   - Anything the GEMV computes twice the same way (host vs device entry point, batch row vs
     single row) must agree bit for bit.
 """
@@ -35,8 +42,9 @@ def check_close(got, ref, exact, abs_sum, what):
     exact = np.asarray(exact, np.float64)
     d_ref = np.abs(got - ref) / np.maximum(np.maximum(np.abs(ref), abs_sum * 2.0 ** -8), 1e-30)
     assert d_ref.max() <= TOL, f"{what}: vs reference {d_ref.max():.3g} at {np.argmax(d_ref)}"
-    allowed = np.maximum(TOL * np.maximum(np.abs(exact), abs_sum * 2.0 ** -10),
-                         2.0 * np.abs(ref - exact))
+    ref_worst = (np.abs(ref - exact) / np.maximum(abs_sum, 1e-30)).max()
+    allowed = np.maximum(np.maximum(TOL * np.maximum(np.abs(exact), abs_sum * 2.0 ** -10),
+                                    2.0 * np.abs(ref - exact)), ref_worst * abs_sum)
     excess = np.abs(got - exact) - allowed
     assert excess.max() <= 0, f"{what}: vs exact exceeds the bound at {np.argmax(excess)}"
 
