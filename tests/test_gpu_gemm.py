@@ -225,3 +225,39 @@ def test_q6_k_tile_shapes(gpu, orc, shape, gemm_kernel):
         y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
         gpu.tune("gemm_tiles")
         check_close(y, yo, exact, abs_sum, f"q6_k {shape} m{m}")
+
+
+K_QUANT_SHAPES = [(S.Q4_K, sh) for sh in [(8, 1, 4), (8, 1, 2), (8, 2, 2), (4, 2, 4), (4, 2, 2),
+                                          (4, 1, 2), (4, 1, 1)]] + \
+                 [(S.Q5_K, sh) for sh in [(8, 1, 4), (8, 1, 2), (4, 1, 2), (4, 1, 1)]]
+
+
+@pytest.mark.parametrize("qt, shape", K_QUANT_SHAPES)
+def test_k_quant_tile_shapes(gpu, orc, qt, shape, gemm_kernel):
+    """Every compiled Q4_K / Q5_K weight-row tile shape (the plan's, and the tuning override's
+    others), forced through the knob with the small-batch route off, on ragged batches and
+    partial row tiles, against the oracle."""
+    if gemm_kernel != "default":
+        pytest.skip("tile shapes of the default kernel")
+    k, n = 1024, 300
+    name = S.TYPE_NAMES[qt]
+    for m in (16, 40, 100):
+        w = S.make_weight(qt, n, k, 31 + m)
+        x = S.make_activation(m, k, 32 + m, outliers=True)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+        yo = orc.matmul(x, w, qt, None, k, n, m)
+        splits = 2 if m == 100 else 1  # the 100-row batch also through split-K completion
+        gpu.tune("gemm_small", 2)
+        gpu.tune("gemm_tiles", *shape)
+        gpu.tune("gemm_splits", splits)
+        try:
+            plan = gpu.matmul_plan(qt, k, n, m)
+            print(name, "shape", shape, "m", m, plan, flush=True)
+            assert gpu.matmul_route(qt, k, n, m) == "mfma"
+            assert plan == "k_gemmw_q4k<%d,%d,%d,%s> splits=%d" % (*shape, name, splits), plan
+            y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, None, k, n).cpu().numpy()
+        finally:
+            gpu.tune("gemm_splits")
+            gpu.tune("gemm_tiles")
+            gpu.tune("gemm_small")
+        check_close(y, yo, exact, abs_sum, f"{name} {shape} m{m}")
