@@ -1591,6 +1591,14 @@ static hipError_t launch_rows(const GemvSegs& sg, int k, int n, int mr, const in
     }
 }
 
+// Rows of the next launch with `left` activation rows to go: 8, 4, 2 or 1, halved down to
+// what one launch's LDS holds (`lim`, max_rows_per_launch).
+static int next_launch_rows(int left, int lim) {
+    int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+    while (mr > lim) mr /= 2;
+    return mr;
+}
+
 // Runs every activation row through the GEMV, MR rows per launch. With x_f32 set, the rows
 // are fp32 and each launch quantizes its rows itself (qs / scales / bsums unused).
 template <uint32_t T, bool SW = false>
@@ -1601,9 +1609,7 @@ static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const 
     const int cap = max_rows_per_launch<T>(k);
     int t = 0;
     while (t < m) {
-        const int left = m - t;
-        int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
-        while (mr > cap) mr /= 2;
+        const int mr = next_launch_rows(m - t, cap);
         GemvSegs sg = sg0;
         for (int i = 0; i < 3; ++i) sg.y[i] = sg0.y[i] + (size_t)t * sg0.rows[i];
         const hipError_t e = launch_rows<T, SW>(
@@ -1616,19 +1622,21 @@ static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const 
     return hipSuccess;
 }
 
+// Launches gemv_all_rows makes for m activation rows (each streams the whole matrix).
+template <uint32_t T>
+static int launches_for(int k, int m) {
+    const int lim = max_rows_per_launch<T>(k);
+    int launches = 0;
+    for (int t = 0; t < m; ++launches) t += next_launch_rows(m - t, lim);
+    return launches;
+}
+
 // The kernel gemv_all_rows runs first for m activation rows, and its launch count; weights
 // taken as 16-byte aligned.
 template <uint32_t T>
 static void plan_rows(const char* tname, int k, int n, int m, char* buf, size_t cap) {
-    const int lim = max_rows_per_launch<T>(k);
-    int mr0 = 0, launches = 0;
-    for (int t = 0; t < m; ++launches) {
-        const int left = m - t;
-        int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
-        while (mr > lim) mr /= 2;
-        if (mr0 == 0) mr0 = mr;
-        t += mr;
-    }
+    const int mr0 = m > 0 ? next_launch_rows(m, max_rows_per_launch<T>(k)) : 0;
+    const int launches = launches_for<T>(k, m);
     const int kind = tuning().gemv_kind.load(std::memory_order_relaxed);
     const int64_t bytes = (int64_t)n * (k / block_elems(T)) * block_bytes(T);
     const char* name = "k_gemv";
@@ -1639,20 +1647,6 @@ static void plan_rows(const char* tname, int k, int n, int m, char* buf, size_t 
                             act_lds_bytes<T>(1, k) <= 64 * 1024)))
         name = "k_gemv_st";
     snprintf(buf, cap, "%s<%s,%d> launches=%d", name, tname, mr0, launches);
-}
-
-// Launches gemv_all_rows makes for m activation rows (each streams the whole matrix).
-template <uint32_t T>
-static int launches_for(int k, int m) {
-    const int lim = max_rows_per_launch<T>(k);
-    int launches = 0;
-    for (int t = 0; t < m; ++launches) {
-        const int left = m - t;
-        int mr = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
-        while (mr > lim) mr /= 2;
-        t += mr;
-    }
-    return launches;
 }
 
 int gemv_launch_count(uint32_t type, int k, int m) {
