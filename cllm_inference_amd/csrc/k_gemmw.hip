@@ -1122,11 +1122,22 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
         // - else 128 x 32 tiles split to about two workgroups per CU, down to 4 stages per
         //   split (4096 at m = 64: 21 us for 8 splits against 22 for 4; 1024 at m = 128: 20
         //   against 22).
+        // - long K (at least 24 stages per split): 256 x 128 tiles on 2 or 4 splits when that
+        //   fills 3/4 of the CUs. Q4_K 4096 x 14336 at m = 384 / 512 / 768 / 1024: 122 / 128 /
+        //   210 / 224 us against 134 / 137 / 249 / 256 on 128 x 64 tiles (Q5_K and K = 11008
+        //   alike; 3 splits were slower than 2 and 4 throughout, and K = 4096 has too few
+        //   stages: wq 4096 x 4096 at m = 512 took 58.5 us on 4 splits against 48.3).
         const int t84 = ((n + 255) / 256) * ((m + 127) / 128);
         const int t42 = ((n + 127) / 128) * ((m + 63) / 64);
+        constexpr int kLongKStages = 24;
+        const int s84 = choose_splits(t84, k / kKS, cus, kLongKStages);
         if (t84 >= cus * 3 / 4) {
             p.wv = 8, p.nt = 1, p.mt = 4;
             target = cus;
+        } else if (s84 >= 2 && t84 * s84 >= cus * 3 / 4) {
+            p.wv = 8, p.nt = 1, p.mt = 4;
+            target = cus;
+            min_stages = kLongKStages;
         } else if (m > 32 && t42 >= cus * 3 / 8) {
             p.wv = 4, p.nt = 1, p.mt = 2;
         } else {

@@ -129,6 +129,25 @@ def test_mid_batch_routes_without_small_kernel():
         assert C.matmul_route(S.Q8_0, 4096, 4096, m) == "gemv"
 
 
+def test_prefill_plans():
+    """Weight-row plans at large batches (256 CUs when no device is present): 256 x 128 tiles
+    unsplit when they fill 3/4 of the CUs; on long K (24 stages of 128 elements per split or
+    more) also on 2 or 4 splits that do; else 128 x 64 or 128 x 32 tiles, split to about two
+    workgroups per CU. The Q4_K_M layer's shapes at 512 rows keep their plans."""
+    assert C.matmul_plan(S.Q4_K, 4096, 14336, 512) == "k_gemmw_q4k<8,1,4,Q4_K> splits=1"
+    assert C.matmul_plan(S.Q4_K, 4096, 4096, 512) == "k_gemmw_q4k<4,1,2,Q4_K> splits=2"
+    assert C.matmul_plan(S.Q4_K, 4096, 1024, 512) == "k_gemmw_q4k<4,1,1,Q4_K> splits=4"
+    assert C.matmul_plan(S.Q6_K, 14336, 4096, 512) == "k_gemmw_q6k<4,2> splits=2"
+    # long K
+    assert C.matmul_plan(S.Q4_K, 14336, 4096, 384) == "k_gemmw_q4k<8,1,4,Q4_K> splits=4"
+    assert C.matmul_plan(S.Q4_K, 14336, 4096, 1024) == "k_gemmw_q4k<8,1,4,Q4_K> splits=2"
+    assert C.matmul_plan(S.Q5_K, 11008, 4096, 768) == "k_gemmw_q4k<8,1,4,Q5_K> splits=2"
+    assert C.matmul_plan(S.Q4_K, 14336, 2048, 768) == "k_gemmw_q4k<8,1,4,Q4_K> splits=4"
+    # too few stages per split (K = 11008 on 4 splits), too few tiles (2048 rows at 512)
+    assert C.matmul_plan(S.Q4_K, 11008, 4096, 512) == "k_gemmw_q4k<4,1,2,Q4_K> splits=2"
+    assert C.matmul_plan(S.Q4_K, 14336, 2048, 512) == "k_gemmw_q4k<4,1,2,Q4_K> splits=4"
+
+
 def test_small_batch_plans():
     """8 to 32 rows of Q4_K / Q5_K weights and 8 to 64 of Q8_0 take the small-batch kernel:
     token tiles of 16, K split over workgroups in ranges of at most 1024 elements, K parts per

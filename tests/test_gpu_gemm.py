@@ -261,3 +261,31 @@ def test_k_quant_tile_shapes(gpu, orc, qt, shape, gemm_kernel):
             gpu.tune("gemm_tiles")
             gpu.tune("gemm_small")
         check_close(y, yo, exact, abs_sum, f"{name} {shape} m{m}")
+
+
+@pytest.mark.parametrize("qt, n, k, m, plan", [
+    (S.Q4_K, 4096, 14336, 384, "k_gemmw_q4k<8,1,4,Q4_K> splits=4"),
+    (S.Q5_K, 4096, 11008, 768, "k_gemmw_q4k<8,1,4,Q5_K> splits=2")])
+def test_long_k_large_batches(gpu, orc, qt, n, k, m, plan, gemm_kernel):
+    """Long-K matrices at large batches take 256 x 128 tiles on 2 or 4 splits: 8 sampled
+    activation rows (all outputs) against the oracle, every row against row-wise GEMV."""
+    import torch
+    if gemm_kernel != "default":
+        pytest.skip("the default plan only")
+    assert gpu.matmul_plan(qt, k, n, m) == plan
+    w = S.make_weight(qt, n, k, 41)
+    x = S.make_activation(m, k, 42, outliers=True)
+    print("long K", S.TYPE_NAMES[qt], n, k, m, plan, flush=True)
+    wd, xd = _dev(w), _dev(x)
+    y = gpu.matmul_quant_dev(xd, wd, qt, None, k, n)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(m).choice(m, size=8, replace=False))
+    yo = orc.matmul(x[rows], w, qt, None, k, n, 8, threads=8)
+    exact, abs_sum = orc.matmul_f64(x[rows], w, qt, None, k, n, 8)
+    check_close(y.cpu().numpy()[rows], yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")
+    qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+    yg = torch.cat([gpu.gemv_q8_dev(wd, qt, k, n, qs[i:i + 8], sc[i:i + 8], bs[i:i + 8])
+                    for i in range(0, m, 8)])
+    d = (y - yg).abs().cpu().numpy().astype(np.float64)
+    scale = np.maximum(np.abs(yg.cpu().numpy()), 1e-3 * np.abs(yg.cpu().numpy()).max(axis=1, keepdims=True))
+    assert (d / scale).max() < 1e-3, (d / scale).max()
