@@ -146,6 +146,16 @@ def test_prefill_plans():
     # too few stages per split (K = 11008 on 4 splits), too few tiles (2048 rows at 512)
     assert C.matmul_plan(S.Q4_K, 11008, 4096, 512) == "k_gemmw_q4k<4,1,2,Q4_K> splits=2"
     assert C.matmul_plan(S.Q4_K, 14336, 2048, 512) == "k_gemmw_q4k<4,1,2,Q4_K> splits=4"
+    # 32-element block types and Q6_K above 256 rows: splits by stage-rounds while the tiles
+    # make fewer than two rounds (1 resident workgroup per CU for b32, 2 for Q6_K)
+    assert C.matmul_plan(S.Q8_0, 14336, 4096, 384) == "k_gemmw_b32<Q8_0,4,2> splits=4"
+    assert C.matmul_plan(S.Q8_0, 14336, 4096, 512) == "k_gemmw_b32<Q8_0,4,2> splits=1"
+    assert C.matmul_plan(S.Q8_0, 14336, 4096, 768) == "k_gemmw_b32<Q8_0,4,2> splits=2"
+    assert C.matmul_plan(S.Q8_0, 4096, 14336, 768) == "k_gemmw_b32<Q8_0,4,2> splits=1"
+    assert C.matmul_plan(S.Q8_0, 4096, 4096, 256) == "k_gemmw_b32<Q8_0,4,2> splits=4"
+    assert C.matmul_plan(S.Q6_K, 4096, 4096, 384) == "k_gemmw_q6k<4,2> splits=4"
+    assert C.matmul_plan(S.Q6_K, 4096, 4096, 768) == "k_gemmw_q6k<4,2> splits=4"
+    assert C.matmul_plan(S.Q6_K, 4096, 14336, 1024) == "k_gemmw_q6k<4,2> splits=1"
 
 
 def test_small_batch_plans():
