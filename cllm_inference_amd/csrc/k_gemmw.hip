@@ -1148,23 +1148,26 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
     const int bn = 32 * p.nt * p.wv, bm = 32 * p.mt;
     const int tiles = ((n + bn - 1) / bn) * ((m + bm - 1) / bm);
     p.splits = choose_splits(tiles, k / kKS, target, min_stages);
-    // Above 256 rows, while the tiles make fewer than two rounds of the CUs' resident
-    // workgroups (1 per CU for the 32-element block types' 128 x 64 tile at 306 VGPRs, 2 for
-    // Q6_K's): the split count (1, 2 or 4) whose workgroups run in the fewest stage-rounds,
-    // ceil(workgroups / slots) x stages per split; on a tie, more splits only while the CUs
+    // Above 256 rows on 128 x 64 tiles, while the tiles make fewer than two rounds of the
+    // CUs' resident workgroups (1 per CU for the 32-element block types' tile at 306 VGPRs, 2
+    // for the K-quants'): the split count (1, 2 or 4) whose workgroups run in the fewest
+    // stage-rounds,
+    // ceil(workgroups / slots) x ceil(stages / splits); on a tie, more splits only while the CUs
     // are not yet filled. Measured at m = 384 .. 1024: on 4096 x 14336 and 4096 x 4096 this
     // picks the fastest of 1 / 2 / 4 splits (within 1 %), e.g. Q8_0 4096 x 14336 at m = 384 /
     // 768 took 175 / 329 us against 218 / 425 for the at-most-two-per-CU rule above, Q6_K
     // 4096 x 14336 147 / 275 against 169 / 334. With more tiles the extra splits cost more
     // than the rounds save (Q8_0 14336 x 4096 at m = 768: 405 us on 4 splits, 386 unsplit).
-    const int slots = cus * (type == T_Q6_K ? 2 : 1);
-    if ((is_b32(type) || type == T_Q6_K) && m > 256 && p.wv == 4 && p.mt == 2 && tiles < 2 * slots) {
+    // Q4_K alike: 4096 x 4096 at m = 768 73 us on 4 splits against 81 unsplit, 11008 x 4096
+    // at m = 384 109 against 130.
+    const int slots = cus * (is_b32(type) ? 1 : 2);
+    if (m > 256 && p.wv == 4 && p.nt == 1 && p.mt == 2 && tiles < 2 * slots) {
         const int stages = k / kKS;
         int best = 1;
         long best_cost = -1;
         for (int s = 1; s <= 4 && stages / s >= min_stages; s *= 2) {
             const long wgs = (long)tiles * s;
-            const long cost = (wgs + slots - 1) / slots * (stages / s);
+            const long cost = (wgs + slots - 1) / slots * ((stages + s - 1) / s);
             if (best_cost < 0 || cost < best_cost || (cost == best_cost && (long)tiles * best < slots)) {
                 best = s;
                 best_cost = cost;

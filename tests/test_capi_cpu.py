@@ -156,6 +156,10 @@ def test_prefill_plans():
     assert C.matmul_plan(S.Q6_K, 4096, 4096, 384) == "k_gemmw_q6k<4,2> splits=4"
     assert C.matmul_plan(S.Q6_K, 4096, 4096, 768) == "k_gemmw_q6k<4,2> splits=4"
     assert C.matmul_plan(S.Q6_K, 4096, 14336, 1024) == "k_gemmw_q6k<4,2> splits=1"
+    assert C.matmul_plan(S.Q4_K, 4096, 4096, 768) == "k_gemmw_q4k<4,1,2,Q4_K> splits=4"
+    assert C.matmul_plan(S.Q4_K, 4096, 11008, 384) == "k_gemmw_q4k<4,1,2,Q4_K> splits=4"
+    assert C.matmul_plan(S.Q5_K, 4096, 14336, 384) == "k_gemmw_q4k<4,1,2,Q5_K> splits=2"
+    assert C.matmul_plan(S.Q4_K, 4096, 4096, 1024) == "k_gemmw_q4k<4,1,2,Q4_K> splits=1"
 
 
 def test_small_batch_plans():

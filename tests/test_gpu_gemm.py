@@ -267,7 +267,8 @@ def test_k_quant_tile_shapes(gpu, orc, qt, shape, gemm_kernel):
     (S.Q4_K, 4096, 14336, 384, "k_gemmw_q4k<8,1,4,Q4_K> splits=4"),
     (S.Q5_K, 4096, 11008, 768, "k_gemmw_q4k<8,1,4,Q5_K> splits=2"),
     (S.Q8_0, 4096, 14336, 384, "k_gemmw_b32<Q8_0,4,2> splits=4"),
-    (S.Q6_K, 4096, 4096, 768, "k_gemmw_q6k<4,2> splits=4")])
+    (S.Q6_K, 4096, 4096, 768, "k_gemmw_q6k<4,2> splits=4"),
+    (S.Q4_K, 11008, 4096, 384, "k_gemmw_q4k<4,1,2,Q4_K> splits=4")])
 def test_long_k_large_batches(gpu, orc, qt, n, k, m, plan, gemm_kernel):
     """Large batches on the plans that split K to fill the CUs (Q4_K / Q5_K long K on 256 x
     128 tiles, the 32-element block types and Q6_K by stage-rounds): 8 sampled activation rows
