@@ -495,13 +495,14 @@ bool use_small(uint32_t type, int k, int n, int m) {
 
 // The MFMA kernels walk K in 256-element steps. Crossover from the GEMV (which streams the
 // weights once per 8 activation rows) measured on MI355X: 16 rows for the types the
-// weight-row kernel has; 64 for the others, whose int8 kernel only overtakes the GEMV there
+// weight-row kernel has; 64 for the others (and for shapes past the weight-row kernel's 32-bit
+// offsets), whose int8 kernel only overtakes the GEMV there
 // (Q5_K 14336 x 4096: 155 us at 16 rows against ~50 us on the GEMV). A forced kernel choice
 // (the tuning knob gemm_kernel) takes the MFMA route from 16 rows for every type.
 bool use_mfma(uint32_t type, int k, int n, int m) {
     if (k % 256 != 0 || !gemm_supported(type) || use_small(type, k, n, m)) return false;
     if (gemm_forced()) return m >= kMfmaMinRows;
-    if (!gemmw_supported(type)) return m >= 4 * kMfmaMinRows;
+    if (!gemmw_supported(type) || !gemmw_fits(type, k, n, m)) return m >= 4 * kMfmaMinRows;
     if (m >= kMfmaMinRows) return true;
     if (type != T_Q6_K && type != T_Q4_0 && type != T_Q5_0) return false;
     // Q6_K, Q4_0 and Q5_0 have no small-batch kernel. Below 16 rows their GEMV reads the
@@ -525,22 +526,24 @@ bool use_mfma(uint32_t type, int k, int n, int m) {
 // MFMA kernel choice. Default: the weight-row fp16 kernel (k_gemmw.hip) where it has the
 // type, else the int8 kernel (k_gemm.hip). The tuning knob "gemm_kernel" (cllm_hip_tune)
 // forces the int8 kernel (1) or the activation-row fp16 kernel (k_gemm16.hip, 2) for every
-// type (tests run all three).
+// type (tests run all three). Shapes past the weight-row kernels' 32-bit offsets (weights of
+// 4 GiB and up, such as a Q8_0 262144 x 16384 output head) take the int8 kernel, which
+// indexes with 64-bit offsets.
 enum class GemmKind { W16, I8, F16 };
 
 bool gemm_forced() { return tuning().gemm_kind.load(std::memory_order_relaxed) != 0; }
 
-GemmKind gemm_kind(uint32_t type) {
-    const int k = tuning().gemm_kind.load(std::memory_order_relaxed);
-    if (k == 2) return GemmKind::F16;
-    if (k == 1) return GemmKind::I8;
-    return gemmw_supported(type) ? GemmKind::W16 : GemmKind::I8;
+GemmKind gemm_kind(uint32_t type, int k, int n, int m) {
+    const int knob = tuning().gemm_kind.load(std::memory_order_relaxed);
+    if (knob == 2) return GemmKind::F16;
+    if (knob == 1) return GemmKind::I8;
+    return gemmw_supported(type) && gemmw_fits(type, k, n, m) ? GemmKind::W16 : GemmKind::I8;
 }
 
 // Split-K bytes the MFMA route of this shape needs (the weight-row kernel only).
 size_t part_bytes_for(uint32_t type, int k, int n, int m) {
     if (use_small(type, k, n, m)) return gemm_sm_partial_bytes(type, k, n, m);
-    return gemm_kind(type) == GemmKind::W16 ? gemmw_partial_bytes(type, k, n, m) : 0;
+    return gemm_kind(type, k, n, m) == GemmKind::W16 ? gemmw_partial_bytes(type, k, n, m) : 0;
 }
 
 // MFMA route on a Q8_0 batch already in device memory; ws supplies the activation formats of
@@ -550,7 +553,7 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
                     const WsView& ws, hipStream_t stream) {
     if (use_small(type, k, n, m))
         return launch_gemm_sm_q8(type, w, k, n, m, qs, sc, bs, bias, y, ws.part, ws.part_cap, stream);
-    const GemmKind kind = gemm_kind(type);
+    const GemmKind kind = gemm_kind(type, k, n, m);
     if (kind == GemmKind::W16) {
         hipError_t e = launch_q8_to_w(qs, sc, bs, (int64_t)m * k / 32, ws.sc, ws.qh,
                                       (type == T_Q4_K || type == T_Q5_K) ? ws.xq : nullptr, stream);
@@ -570,7 +573,7 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
     if (use_small(type, k, n, m))
         return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
     const int64_t nblk = (int64_t)m * k / 32;
-    const GemmKind kind = gemm_kind(type);
+    const GemmKind kind = gemm_kind(type, k, n, m);
     if (kind == GemmKind::F16) {
         hipError_t e = launch_quantize_mfma(x, nblk, ws.sc, ws.qh, ws.px, stream);
         if (e != hipSuccess) return e;
@@ -1438,7 +1441,7 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
     } else if (std::strcmp(route, "mfma") != 0) {
         snprintf(buf, sizeof buf, "%s", route);
     } else {
-        const GemmKind kind = gemm_kind(type);
+        const GemmKind kind = gemm_kind(type, in_dim, out_dim, n_rows);
         if (kind == GemmKind::W16)
             gemmw_plan_name(type, in_dim, out_dim, n_rows, buf, sizeof buf);
         else

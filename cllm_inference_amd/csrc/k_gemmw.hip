@@ -1057,6 +1057,12 @@ bool gemmw_supported(uint32_t type) {
            type == T_Q5_0;
 }
 
+// The kernels index the weights and the fp16 activations with 32-bit byte offsets.
+bool gemmw_fits(uint32_t type, int k, int n, int m) {
+    const uint64_t wbytes = (uint64_t)n * (uint64_t)(k / block_elems(type)) * (uint64_t)block_bytes(type);
+    return wbytes < (1ull << 32) && 2ull * (uint64_t)m * (uint64_t)k < (1ull << 32);
+}
+
 bool is_b32(uint32_t type) { return type == T_Q8_0 || type == T_Q4_0 || type == T_Q5_0; }
 
 namespace {
@@ -1284,10 +1290,8 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         const _Float16* qh, const uint16_t* xq,
                         const float* bias, float* y, float* part, size_t part_bytes,
                         hipStream_t stream) {
-    if (!gemmw_supported(type) || k % 256 != 0) return hipErrorNotSupported;
-    const uint64_t wbytes = (uint64_t)n * (uint64_t)(k / block_elems(type)) * (uint64_t)block_bytes(type);
-    if (wbytes >= (1ull << 32) || 2ull * (uint64_t)m * (uint64_t)k >= (1ull << 32))
-        return hipErrorNotSupported;  // the kernels index with 32-bit byte offsets
+    if (!gemmw_supported(type) || k % 256 != 0 || !gemmw_fits(type, k, n, m))
+        return hipErrorNotSupported;
     Plan p = plan_for(type, k, n, m);
     if (p.splits > 1 && (part == nullptr || part_bytes < slices_bytes(p, n, m) + kCounterBytes ||
                          plan_tiles(p, n, m) * 4 > (int64_t)kCounterBytes))

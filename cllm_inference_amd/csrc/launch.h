@@ -175,6 +175,9 @@ hipError_t launch_gemv_f(uint32_t type, const uint8_t* w, int k, int n, int m, c
                          const float* bias, float* y, hipStream_t stream);
 hipError_t gemmw_workspace_init(void* part, size_t bytes, hipStream_t stream);
 bool gemmw_supported(uint32_t type);
+// false when the shape's weights (4 GiB and up) or fp16 activations (2 m k bytes, 4 GiB and
+// up) are past the weight-row kernels' 32-bit offsets; such shapes take the int8 kernel
+bool gemmw_fits(uint32_t type, int k, int n, int m);
 
 // Reads `bytes` (a multiple of 16) at the 16-byte-aligned device address p once and computes
 // nothing: the one-launch read ceiling of that stream (k_read.hip). cus = the device's CUs.

@@ -37,6 +37,22 @@ def orc():
     return oracle.Oracle()
 
 
+# every process-wide kernel-choice override of cllm_hip_tune
+TUNING_KNOBS = ("gemm_kernel", "gemm_tiles", "gemm_splits", "gemv_kernel", "gemv_str_grid",
+                "gemm_small", "gemm_small_plan", "gemv_waves")
+
+
+@pytest.fixture(autouse=True)
+def _reset_tuning_knobs():
+    """A test that forces a kernel plan and then fails leaves no override behind for the tests
+    after it: every knob is reset after each test that loaded the library."""
+    yield
+    import cllm_inference_amd as C
+    if C._lib_handle is not None:
+        for knob in TUNING_KNOBS:
+            C.tune(knob)
+
+
 @pytest.fixture(scope="session")
 def gpu():
     """The HIP library on device 0; the test fails (never falls back) if it cannot run."""

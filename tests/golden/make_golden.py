@@ -297,6 +297,21 @@ def m_sweep_large_fixtures(ref: oracle.Reference) -> None:
         data[f"q5_k_m{m}__x_sha"] = np.array(sha(x))
         print("m sweep", m, flush=True)
     data["q5_k__w_sha"] = np.array(sha(w))
+    # every other point of the sweep at full size: all outputs of up to three activation rows
+    # (the first, one inside, the last)
+    for label in ("q5_k", "q8_0"):
+        qt, n, k, w = S.config_weight("c4_m_sweep", label)
+        data[f"{label}__w_sha"] = np.array(sha(w))
+        for m in S.CONFIGS["c4_m_sweep"]["m"]:
+            if label == "q5_k" and m == 256:
+                continue
+            rows = sorted({0, (m * 3) // 10, m - 1})
+            x = S.config_activation("c4_m_sweep", m, k)
+            y = ref.matmul(x[rows], w, qt, None, k, n, len(rows), threads=THREADS)
+            data[f"{label}_m{m}__rows"] = np.array(rows, np.int64)
+            data[f"{label}_m{m}__y"] = y
+            data[f"{label}_m{m}__x_sha"] = np.array(sha(x))
+            print("m sweep", label, m, flush=True)
     np.savez_compressed(os.path.join(OUT, "batch_large.npz"), **data)
 
 

@@ -162,6 +162,24 @@ def test_prefill_plans():
     assert C.matmul_plan(S.Q4_K, 4096, 4096, 1024) == "k_gemmw_q4k<4,1,2,Q4_K> splits=1"
 
 
+def test_shapes_past_32_bit_offsets_take_the_int8_kernel():
+    """The weight-row kernels index with 32-bit byte offsets: a Q8_0 262144 x 16384 output head
+    (4.5 GB of weights) and a batch whose fp16 activations reach 4 GiB go to the int8 kernel
+    (64-bit offsets); just below the limit the weight-row kernel keeps them."""
+    assert C.matmul_route(S.Q8_0, 16384, 262144, 512) == "mfma"
+    assert C.matmul_plan(S.Q8_0, 16384, 262144, 512) == "k_gemm_i8"
+    # the small-batch kernel (64-bit offsets) keeps its batches; above it, the int8 kernel
+    assert C.matmul_route(S.Q8_0, 16384, 262144, 16) == "small"
+    assert C.matmul_plan(S.Q8_0, 16384, 262144, 100) == "k_gemm_i8"
+    # weights just under 4 GiB: 4 GiB / 34 bytes per block, 512 blocks per row
+    n = ((1 << 32) - 1) // (512 * 34)
+    assert C.matmul_plan(S.Q8_0, 16384, n, 512).startswith("k_gemmw_b32<Q8_0")
+    assert C.matmul_plan(S.Q8_0, 16384, n + 1, 512) == "k_gemm_i8"
+    # activations: 2 m k bytes of fp16 reach 4 GiB at m k = 2^31
+    assert C.matmul_plan(S.Q4_K, 8192, 4096, (1 << 31) // 8192 - 1).startswith("k_gemmw_q4k")
+    assert C.matmul_plan(S.Q4_K, 8192, 4096, (1 << 31) // 8192) == "k_gemm_i8"
+
+
 def test_small_batch_plans():
     """8 to 32 rows of Q4_K / Q5_K weights and 8 to 64 of Q8_0 take the small-batch kernel:
     token tiles of 16, K split over workgroups in ranges of at most 1024 elements, K parts per

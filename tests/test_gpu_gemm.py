@@ -146,14 +146,16 @@ def test_full_prefill_layer_sampled_rows(gpu, orc):
 def test_mfma_tails_and_split_k(gpu, orc, qt, splits, gemm_kernel):
     """Output rows and activation rows that end inside a tile (n = 520, m = 80), K = 2048, with
     the planned K split and with K forced into 4 splits (partial sums plus the reduction)."""
-    gpu.tune("gemm_splits", splits or 0)
     k, n, m = 2048, 520, 80
     w = S.make_weight(qt, n, k, 90 + qt)
     x = S.make_activation(m, k, 91 + qt, outliers=True)
     bias = np.linspace(-1.0, 1.0, n).astype(np.float32)
     print("tails", S.TYPE_NAMES[qt], "splits", splits, flush=True)
-    y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, _dev(bias), k, n).cpu().numpy()
-    gpu.tune("gemm_splits")
+    try:
+        gpu.tune("gemm_splits", splits or 0)
+        y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, _dev(bias), k, n).cpu().numpy()
+    finally:
+        gpu.tune("gemm_splits")
     exact, abs_sum = orc.matmul_f64(x, w, qt, bias, k, n, m)
     yo = orc.matmul(x, w, qt, bias, k, n, m)
     check_close(y, yo, exact, abs_sum, f"tails {S.TYPE_NAMES[qt]} splits={splits}")
@@ -201,10 +203,12 @@ def test_q6_k_prefill_super_block_alignments(gpu, orc, k, n, gemm_kernel):
     exact, abs_sum = orc.matmul_f64(x, w, S.Q6_K, None, k, n, m)
     yo = orc.matmul(x, w, S.Q6_K, None, k, n, m)
     for splits in (0, 4):
-        gpu.tune("gemm_splits", splits)
         print("q6_k alignments", k, n, "splits", splits, flush=True)
-        y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
-        gpu.tune("gemm_splits")
+        try:
+            gpu.tune("gemm_splits", splits)
+            y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
+        finally:
+            gpu.tune("gemm_splits")
         check_close(y, yo, exact, abs_sum, f"q6_k {n}x{k} splits={splits}")
 
 
@@ -220,10 +224,12 @@ def test_q6_k_tile_shapes(gpu, orc, shape, gemm_kernel):
         x = S.make_activation(m, k, 6 + m, outliers=True)
         exact, abs_sum = orc.matmul_f64(x, w, S.Q6_K, None, k, n, m)
         yo = orc.matmul(x, w, S.Q6_K, None, k, n, m)
-        gpu.tune("gemm_tiles", *shape)
-        print("q6_k shape", shape, "m", m, gpu.matmul_plan(S.Q6_K, k, n, m), flush=True)
-        y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
-        gpu.tune("gemm_tiles")
+        try:
+            gpu.tune("gemm_tiles", *shape)
+            print("q6_k shape", shape, "m", m, gpu.matmul_plan(S.Q6_K, k, n, m), flush=True)
+            y = gpu.matmul_quant_dev(_dev(x), _dev(w), S.Q6_K, None, k, n).cpu().numpy()
+        finally:
+            gpu.tune("gemm_tiles")
         check_close(y, yo, exact, abs_sum, f"q6_k {shape} m{m}")
 
 

@@ -6,9 +6,9 @@ Bars (written into each test):
     output, where A is the row's sum of absolute per-block terms; and, against the fp64
     evaluation of the same quantized terms,
     |gpu - exact| <= max(1e-4 * max(|exact|, 2^-10 * A), 2 * |ref - exact|, R * A), where
-    R = max over the same output of |ref - exact| / A: never further from the exact value
+    R = max over the same activation row of |ref - exact| / A: never further from the exact value
     than twice the reference's own rounding error there, or than the reference's worst
-    rounding anywhere in the output relative to A. The reference's sequential fp32 sum is
+    rounding anywhere in that row of outputs relative to A. The reference's sequential fp32 sum is
     itself up to 1.5e-4 away from exact under the 2^-10 floor on outlier inputs, which is
     why neither gate can use that floor alone. The R * A term is there because a different
     fp32 order than the reference's (split-K partials, fma per block) can miss the first two
@@ -37,12 +37,15 @@ def bits(a):
 
 
 def check_close(got, ref, exact, abs_sum, what):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
+    """The two bars above. exact has the outputs' (m, n) shape; R is taken per activation
+    row (the last axis), so one row's rounding does not loosen another's."""
     exact = np.asarray(exact, np.float64)
+    got = np.asarray(got, np.float64).reshape(exact.shape)
+    ref = np.asarray(ref, np.float64).reshape(exact.shape)
+    abs_sum = np.asarray(abs_sum, np.float64).reshape(exact.shape)
     d_ref = np.abs(got - ref) / np.maximum(np.maximum(np.abs(ref), abs_sum * 2.0 ** -8), 1e-30)
     assert d_ref.max() <= TOL, f"{what}: vs reference {d_ref.max():.3g} at {np.argmax(d_ref)}"
-    ref_worst = (np.abs(ref - exact) / np.maximum(abs_sum, 1e-30)).max()
+    ref_worst = (np.abs(ref - exact) / np.maximum(abs_sum, 1e-30)).max(axis=-1, keepdims=True)
     allowed = np.maximum(np.maximum(TOL * np.maximum(np.abs(exact), abs_sum * 2.0 ** -10),
                                     2.0 * np.abs(ref - exact)), ref_worst * abs_sum)
     excess = np.abs(got - exact) - allowed

@@ -256,6 +256,25 @@ def test_oracle_matches_reference_golden_workloads(orc, tag):
     assert np.array_equal(bits(y), bits(c["y"]))
 
 
+def test_oracle_matches_reference_golden_m_sweep_full_size(orc):
+    """Every point of the M-sweep at full size (Q5_K 14336x4096, Q8_0 4096x4096): the oracle's
+    rows bit-identical to the compiled reference's (tests/golden/batch_large.npz)."""
+    c = split_cases(load_golden("batch_large.npz"))
+    seen = 0
+    for label in ("q5_k", "q8_0"):
+        qt, n, k, w = S.config_weight("c4_m_sweep", label)
+        assert O_sha(w) == str(c[label]["w_sha"]), f"generator drift for {label}"
+        for m in S.CONFIGS["c4_m_sweep"]["m"] + ([512] if label == "q5_k" else []):
+            g = c[f"{label}_m{m}"]
+            x = S.config_activation("c4_m_sweep", m, k)
+            assert O_sha(x) == str(g["x_sha"]), f"generator drift for {label} m{m}"
+            rows = g["rows"]
+            y = orc.matmul(x[rows], w, qt, None, k, n, len(rows), threads=8)
+            assert np.array_equal(bits(y), bits(g["y"])), f"{label} m{m}"
+            seen += 1
+    assert seen == 11
+
+
 def test_oracle_matches_reference_golden_refkat(orc):
     cases = split_cases(load_golden("refkat.npz"))
     assert len(cases) == 13
