@@ -60,6 +60,7 @@ SIGNATURES = {
     "cllm_hip_dequantize_block_f16": (_I, [_P, _P, _U, _I64]),
     "cllm_hip_register_weights": (_I, [_P, _SZ]),
     "cllm_hip_unregister_weights": (_I, [_P]),
+    "cllm_hip_file_mapping_identity": (_I, [_P, _P]),
     "cllm_hip_quantize_q8_0_dev": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_matmul_quant_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),
@@ -133,6 +134,15 @@ def _check(rc: int) -> None:
 
 def _ptr(a: np.ndarray | None):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def file_mapping_identity(addr: int) -> tuple:
+    """What the library compares before reusing the device copy of the read-only private file
+    mapping that holds host address addr (cllm_hip_file_mapping_identity): (start, end, file
+    offset, inode, device, file size, mtime ns, ctime ns, file reachable by its path)."""
+    info = (ctypes.c_uint64 * 9)()
+    _check(load_library().cllm_hip_file_mapping_identity(ctypes.c_void_p(addr), info))
+    return tuple(int(v) for v in info)
 
 
 def block_size(t: int) -> int:

@@ -20,6 +20,13 @@
 #include <vector>
 #include <string>
 
+#include <fcntl.h>
+#include <sys/ioctl.h>
+#include <sys/stat.h>
+#include <sys/sysmacros.h>
+#include <unistd.h>
+#include <cerrno>
+
 #include "../../include/cllm_hip.h"
 #include "ggml_blocks.h"
 #include "gguf_file.h"
@@ -138,56 +145,132 @@ struct Workspace {
 };
 
 // A host address range whose bytes have a device copy. Automatic regions are read-only file
-// mappings found by resolve_weights; they carry the mapping's identity, so a range that was
-// unmapped (and perhaps mapped again with other contents) is noticed and dropped.
+// mappings found by resolve_weights; they carry the mapping's identity and the mapped file's
+// size and times, so a range that was unmapped (and perhaps mapped again with other contents),
+// or whose file was rewritten in place, is noticed and dropped.
 struct Region {
     size_t bytes;
     void* dev;    // device address of the region's first byte
     void* alloc;  // the allocation to free
     bool automatic = false;
     uint64_t file_off = 0, inode = 0;
-    char fdev[16] = {};
+    uint32_t dev_major = 0, dev_minor = 0;
+    int fd = -1;  // the mapped file, opened at the copy (-1: no longer reachable by its path)
+    struct stat at_copy = {};
 };
 
-// One line of /proc/self/maps.
+// One mapping (VMA) of this process.
 struct Mapping {
     uintptr_t lo = 0, hi = 0;
-    char perms[8] = {};
+    bool readable = false, writable = false, shared = false;
     uint64_t off = 0, inode = 0;
-    char dev[16] = {};
-    bool file = false;  // has a path name
+    uint32_t dev_major = 0, dev_minor = 0;
+    bool file = false;  // backed by a file with a path name
+    std::string path;   // filled when asked for
 };
 
-// The mapping of this process that holds address p.
-bool find_mapping(uintptr_t p, Mapping& m) {
+// The mapping of this process that holds address p, parsed from /proc/self/maps.
+bool parse_mapping(uintptr_t p, Mapping& m, bool want_path) {
     FILE* f = std::fopen("/proc/self/maps", "r");
     if (!f) return false;
     char line[4096];
     bool found = false;
     while (!found && std::fgets(line, sizeof line, f)) {
         unsigned long lo = 0, hi = 0, off = 0, ino = 0;
-        char perms[8] = {}, dev[16] = {};
+        unsigned maj = 0, mnr = 0;
+        char perms[8] = {};
         int pos = 0;
-        if (std::sscanf(line, "%lx-%lx %7s %lx %15s %lu %n", &lo, &hi, perms, &off, dev, &ino, &pos) < 6)
+        if (std::sscanf(line, "%lx-%lx %7s %lx %x:%x %lu %n", &lo, &hi, perms, &off, &maj, &mnr, &ino, &pos) < 7)
             continue;
         if (p < lo || p >= hi) continue;
+        m = Mapping{};
         m.lo = lo;
         m.hi = hi;
-        std::memcpy(m.perms, perms, sizeof m.perms);
+        m.readable = perms[0] == 'r';
+        m.writable = perms[1] == 'w';
+        m.shared = perms[3] == 's';
         m.off = off;
         m.inode = ino;
-        std::memcpy(m.dev, dev, sizeof m.dev);
+        m.dev_major = maj;
+        m.dev_minor = mnr;
         m.file = pos > 0 && line[pos] == '/';
+        if (m.file && want_path) {
+            m.path.assign(line + pos);
+            while (!m.path.empty() && (m.path.back() == '\n' || m.path.back() == '\r')) m.path.pop_back();
+        }
         found = true;
     }
     std::fclose(f);
     return found;
 }
 
+// The kernel's one-address query of a process's mappings (PROCMAP_QUERY, an ioctl on an open
+// /proc/<pid>/maps, Linux 6.11 and later; uapi linux/fs.h). The layout is the kernel's ABI;
+// the system headers of this build predate it.
+struct ProcmapQuery {
+    uint64_t size, query_flags, query_addr;
+    uint64_t vma_start, vma_end, vma_flags, vma_page_size, vma_offset, inode;
+    uint32_t dev_major, dev_minor, vma_name_size, build_id_size;
+    uint64_t vma_name_addr, build_id_addr;
+};
+static_assert(sizeof(ProcmapQuery) == 104, "struct procmap_query is 104 bytes");
+constexpr unsigned long kProcmapQuery = _IOWR('f', 17, ProcmapQuery);
+constexpr uint64_t kVmaReadable = 1, kVmaWritable = 2, kVmaShared = 8;
+
+std::mutex g_maps_mtx;
+int g_maps_fd = -1;       // /proc/self/maps of process g_maps_pid
+pid_t g_maps_pid = -1;
+bool g_maps_query = true;  // false once the kernel has refused the query
+
+// The mapping of this process that holds address p: one PROCMAP_QUERY (about 0.3 us) where
+// the kernel has it, else a parse of /proc/self/maps (hundreds of us with HIP loaded).
+bool find_mapping(uintptr_t p, Mapping& m, bool want_path = false) {
+    {
+        std::lock_guard<std::mutex> lk(g_maps_mtx);
+        if (g_maps_query) {
+            const pid_t pid = getpid();  // a forked child must not query its parent's mappings
+            if (g_maps_fd >= 0 && g_maps_pid != pid) {
+                ::close(g_maps_fd);
+                g_maps_fd = -1;
+            }
+            if (g_maps_fd < 0) {
+                g_maps_fd = ::open("/proc/self/maps", O_RDONLY | O_CLOEXEC);
+                g_maps_pid = pid;
+            }
+            char name[4096];
+            ProcmapQuery q = {};
+            q.size = sizeof q;
+            q.query_addr = p;
+            if (want_path) {
+                q.vma_name_size = sizeof name;
+                q.vma_name_addr = (uint64_t)(uintptr_t)name;
+            }
+            if (g_maps_fd >= 0 && ::ioctl(g_maps_fd, kProcmapQuery, &q) == 0) {
+                m = Mapping{};
+                m.lo = q.vma_start;
+                m.hi = q.vma_end;
+                m.readable = q.vma_flags & kVmaReadable;
+                m.writable = q.vma_flags & kVmaWritable;
+                m.shared = q.vma_flags & kVmaShared;
+                m.off = q.vma_offset;
+                m.inode = q.inode;
+                m.dev_major = q.dev_major;
+                m.dev_minor = q.dev_minor;
+                m.file = q.inode != 0;
+                if (want_path && q.vma_name_size > 0) m.path.assign(name);
+                return p >= m.lo && p < m.hi;
+            }
+            if (errno == ENOENT) return false;  // no mapping holds p
+            if (errno == ENOTTY || errno == EINVAL || errno == EOPNOTSUPP) g_maps_query = false;
+        }
+    }
+    return parse_mapping(p, m, want_path);
+}
+
 // A private, read-only mapping of a file: what GgufLoader maps (gguf.cpp:178). Its bytes
 // cannot change through the mapping, so one device copy serves every later call.
 bool immutable_file_mapping(const Mapping& m) {
-    return m.file && m.perms[0] == 'r' && m.perms[1] == '-' && m.perms[3] == 'p' && m.inode != 0;
+    return m.file && m.readable && !m.writable && !m.shared && m.inode != 0;
 }
 
 // Fixed scratch of cllm_hip_matmul_quant_static_dev, one copy per GPU for the life of the
@@ -295,76 +378,81 @@ int upload_region(DeviceState* st, uintptr_t a, size_t bytes, Region* out) {
     return CLLM_HIP_OK;
 }
 
-// Every line of /proc/self/maps.
-std::vector<Mapping> all_mappings() {
-    std::vector<Mapping> out;
-    FILE* f = std::fopen("/proc/self/maps", "r");
-    if (!f) return out;
-    char line[4096];
-    while (std::fgets(line, sizeof line, f)) {
-        unsigned long lo = 0, hi = 0, off = 0, ino = 0;
-        char perms[8] = {}, dev[16] = {};
-        int pos = 0;
-        if (std::sscanf(line, "%lx-%lx %7s %lx %15s %lu %n", &lo, &hi, perms, &off, dev, &ino, &pos) < 6)
-            continue;
-        Mapping m;
-        m.lo = lo;
-        m.hi = hi;
-        std::memcpy(m.perms, perms, sizeof m.perms);
-        m.off = off;
-        m.inode = ino;
-        std::memcpy(m.dev, dev, sizeof m.dev);
-        m.file = pos > 0 && line[pos] == '/';
-        out.push_back(m);
-    }
-    std::fclose(f);
-    return out;
-}
-
-// An automatic region is still backed by the read-only file mapping it was copied from.
+// An automatic region is still backed by the read-only file mapping it was copied from, and
+// that file still has the size and times it had at the copy. A rewrite in place (same inode)
+// changes the times; one of the same size within one timestamp tick of the copy is not seen.
 bool same_mapping(uintptr_t base, const Region& r, const Mapping& m) {
-    return m.lo == base && m.hi - m.lo == r.bytes && m.inode == r.inode && m.off == r.file_off &&
-           std::strcmp(m.dev, r.fdev) == 0 && immutable_file_mapping(m);
+    if (!(m.lo == base && m.hi - m.lo == r.bytes && m.inode == r.inode && m.off == r.file_off &&
+          m.dev_major == r.dev_major && m.dev_minor == r.dev_minor && immutable_file_mapping(m)))
+        return false;
+    if (r.fd < 0) return true;
+    struct stat now;
+    if (::fstat(r.fd, &now) != 0) return false;
+    return now.st_ino == r.at_copy.st_ino && now.st_size == r.at_copy.st_size &&
+           now.st_mtim.tv_sec == r.at_copy.st_mtim.tv_sec &&
+           now.st_mtim.tv_nsec == r.at_copy.st_mtim.tv_nsec &&
+           now.st_ctim.tv_sec == r.at_copy.st_ctim.tv_sec &&
+           now.st_ctim.tv_nsec == r.at_copy.st_ctim.tv_nsec;
 }
 
-// Frees the automatic regions whose file mappings are gone (the caller unmapped the file).
+// Frees a region's device copy (after the stream's work that may read it) and its file.
+int drop_region(DeviceState* st, std::map<uintptr_t, Region>::iterator it) {
+    HIP_TRY(hipStreamSynchronize(st->stream));
+    HIP_TRY(hipFree(it->second.alloc));
+    if (it->second.fd >= 0) ::close(it->second.fd);
+    st->regions.erase(it);
+    return CLLM_HIP_OK;
+}
+
+// An automatic region is live while its mapping and file are unchanged.
+bool auto_region_live(uintptr_t base, const Region& r) {
+    Mapping m;
+    return find_mapping(base, m) && same_mapping(base, r, m);
+}
+
+// Frees the automatic regions whose file mappings are gone or changed.
 int prune_auto_regions(DeviceState* st) {
-    const std::vector<Mapping> maps = all_mappings();
     for (auto it = st->regions.begin(); it != st->regions.end();) {
-        bool live = !it->second.automatic;
-        for (const Mapping& m : maps)
-            if (!live && same_mapping(it->first, it->second, m)) live = true;
-        if (live) {
+        if (!it->second.automatic || auto_region_live(it->first, it->second)) {
             ++it;
             continue;
         }
-        HIP_TRY(hipStreamSynchronize(st->stream));
-        HIP_TRY(hipFree(it->second.alloc));
-        it = st->regions.erase(it);
+        auto dead = it++;
+        int rc = drop_region(st, dead);
+        if (rc) return rc;
     }
     return CLLM_HIP_OK;
 }
 
 // The device copy of [a, a + bytes) if a registered region holds it (null if none). An
-// automatic region is checked against the current mapping first, and dropped if the file it
-// was copied from is no longer mapped there.
+// automatic region is checked against the current mapping and file first (one mapping query
+// and one fstat), and dropped if either changed since the copy.
 int lookup_region(DeviceState* st, uintptr_t a, size_t bytes, const uint8_t** dev) {
     *dev = nullptr;
     auto it = st->regions.upper_bound(a);
     if (it == st->regions.begin()) return CLLM_HIP_OK;
     --it;
     if (a < it->first || a + bytes > it->first + it->second.bytes) return CLLM_HIP_OK;
-    if (it->second.automatic) {
-        Mapping m;
-        if (!find_mapping(a, m) || !same_mapping(it->first, it->second, m)) {
-            HIP_TRY(hipStreamSynchronize(st->stream));
-            HIP_TRY(hipFree(it->second.alloc));
-            st->regions.erase(it);
-            return CLLM_HIP_OK;
-        }
-    }
+    if (it->second.automatic && !auto_region_live(it->first, it->second)) return drop_region(st, it);
     *dev = (const uint8_t*)it->second.dev + (a - it->first);
     return CLLM_HIP_OK;
+}
+
+// Opens the file behind an automatic region and records its identity and times. The path
+// must still name the mapped inode; otherwise (unlinked or replaced) fd stays -1 and the
+// region is checked by its mapping alone, since no path reaches the mapped file any more.
+void watch_file(const Mapping& m, Region& r) {
+    if (m.path.empty() || m.path[0] != '/') return;
+    const int fd = ::open(m.path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return;
+    struct stat sb;
+    if (::fstat(fd, &sb) == 0 && sb.st_ino == m.inode && major(sb.st_dev) == m.dev_major &&
+        minor(sb.st_dev) == m.dev_minor) {
+        r.fd = fd;
+        r.at_copy = sb;
+        return;
+    }
+    ::close(fd);
 }
 
 // Device address of `bytes` of weights at host/device pointer w. Registered regions resolve
@@ -389,7 +477,7 @@ int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t*
     // whole mapping goes to the device once and later calls resolve by offset, as after
     // cllm_hip_register_weights. If the device cannot hold it, the bytes are copied per call.
     Mapping m;
-    if (find_mapping(a, m) && immutable_file_mapping(m) && a + bytes <= m.hi &&
+    if (find_mapping(a, m, true) && immutable_file_mapping(m) && a + bytes <= m.hi &&
         st->no_auto.count(m.lo) == 0) {
         if ((rc = prune_auto_regions(st))) return rc;
         Region r;
@@ -397,7 +485,9 @@ int resolve_weights(DeviceState* st, const void* w, size_t bytes, const uint8_t*
             r.automatic = true;
             r.file_off = m.off;
             r.inode = m.inode;
-            std::memcpy(r.fdev, m.dev, sizeof r.fdev);
+            r.dev_major = m.dev_major;
+            r.dev_minor = m.dev_minor;
+            watch_file(m, r);
             st->regions[m.lo] = r;
             *dev = (const uint8_t*)r.dev + (a - m.lo);
             if (!aligned16(*dev))
@@ -773,14 +863,30 @@ int cllm_hip_register_weights(const void* host_base, size_t bytes) {
     std::lock_guard<std::mutex> lk(st->mtx);
     const uintptr_t a = (uintptr_t)host_base;
     auto it = st->regions.find(a);
-    if (it != st->regions.end()) {
-        HIP_TRY(hipStreamSynchronize(st->stream));
-        HIP_TRY(hipFree(it->second.alloc));
-        st->regions.erase(it);
-    }
+    if (it != st->regions.end() && (rc = drop_region(st, it))) return rc;
     Region r;
     if ((rc = upload_region(st, a, bytes, &r))) return rc;
     st->regions[a] = r;
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_file_mapping_identity(const void* p, uint64_t info[9]) {
+    if (!info) return set_err(CLLM_HIP_E_ARG, "cllm_hip_file_mapping_identity: null info");
+    Mapping m;
+    if (!find_mapping((uintptr_t)p, m, true) || !immutable_file_mapping(m))
+        return set_err(CLLM_HIP_E_ARG, "cllm_hip_file_mapping_identity: not in a read-only private file mapping");
+    Region r;
+    watch_file(m, r);
+    info[0] = m.lo;
+    info[1] = m.hi;
+    info[2] = m.off;
+    info[3] = m.inode;
+    info[4] = ((uint64_t)m.dev_major << 32) | m.dev_minor;
+    info[5] = (uint64_t)r.at_copy.st_size;
+    info[6] = (uint64_t)r.at_copy.st_mtim.tv_sec * 1000000000ull + (uint64_t)r.at_copy.st_mtim.tv_nsec;
+    info[7] = (uint64_t)r.at_copy.st_ctim.tv_sec * 1000000000ull + (uint64_t)r.at_copy.st_ctim.tv_nsec;
+    info[8] = r.fd >= 0;
+    if (r.fd >= 0) ::close(r.fd);
     return CLLM_HIP_OK;
 }
 
@@ -792,10 +898,7 @@ int cllm_hip_unregister_weights(const void* host_base) {
     auto it = st->regions.find((uintptr_t)host_base);
     if (it == st->regions.end())
         return set_err(CLLM_HIP_E_ARG, "cllm_hip_unregister_weights: region not registered");
-    HIP_TRY(hipStreamSynchronize(st->stream));
-    HIP_TRY(hipFree(it->second.alloc));
-    st->regions.erase(it);
-    return CLLM_HIP_OK;
+    return drop_region(st, it);
 }
 
 int cllm_hip_dequantize_block(const void* src, float* dst, uint32_t type, int64_t n) {

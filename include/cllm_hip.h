@@ -91,6 +91,16 @@ int cllm_hip_matmul_quant_batch(const float* x, const void* w, uint32_t type,
 int cllm_hip_register_weights(const void* host_base, size_t bytes);
 int cllm_hip_unregister_weights(const void* host_base);
 
+/* Weights inside a read-only private file mapping (the engine's mmap'd GGUF, gguf.cpp:178)
+ * are copied to the device once per mapping, and each later call first checks that the
+ * mapping and its file are unchanged: one kernel mapping query and one fstat. This returns
+ * what that check compares, for the mapping holding p: info[0..8] = mapping start, end,
+ * file offset, inode, device (major << 32 | minor), then the file's size, mtime and ctime
+ * (ns) and 1 if the file is reachable by its path (else the mapping alone is checked).
+ * CLLM_HIP_E_ARG if p lies in no read-only private file mapping. Needs no GPU. No reference
+ * counterpart: a diagnostic of the device copy's validation. */
+int cllm_hip_file_mapping_identity(const void* p, uint64_t info[9]);
+
 /* dequantize_block: the first n elements of the run of blocks at src (ceil(n / block_size)
  * blocks of any of the thirteen types) to fp32 dst[n], bit for bit. A partial last block is
  * read whole and written up to n, as the reference's loops do. src is a host pointer (it may

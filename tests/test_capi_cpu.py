@@ -209,3 +209,78 @@ def test_small_batch_plans():
     finally:
         C.tune("gemm_small")
         C.tune("gemm_kernel")
+
+
+def _libc():
+    libc = ctypes.CDLL(None, use_errno=True)
+    libc.mmap.restype = ctypes.c_void_p
+    libc.mmap.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                          ctypes.c_int, ctypes.c_long]
+    libc.munmap.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    return libc
+
+
+PROT_READ, PROT_WRITE, MAP_SHARED, MAP_PRIVATE, MAP_FIXED = 1, 2, 1, 2, 0x10
+
+
+def test_file_mapping_identity_sees_remaps_and_rewrites(tmp_path):
+    """The check made before the device copy of a read-only private file mapping (the engine's
+    mmap'd GGUF) is reused: a file unmapped and another mapped at the same address, a rewrite
+    in place (same inode, O_TRUNC too), and an unlinked file all change what it compares, and
+    memory that is not a read-only private file mapping is refused."""
+    import time
+    libc = _libc()
+    size = 4 * 4096
+    rng = np.random.default_rng(3)
+    paths = []
+    for name in ("a.bin", "b.bin"):
+        p = tmp_path / name
+        p.write_bytes(rng.integers(0, 256, size, dtype=np.uint8).tobytes())
+        paths.append(str(p))
+    fa = os.open(paths[0], os.O_RDONLY)
+    fb = os.open(paths[1], os.O_RDONLY)
+    addr = libc.mmap(None, size, PROT_READ, MAP_PRIVATE, fa, 0)
+    assert addr not in (None, ctypes.c_void_p(-1).value)
+    try:
+        id_a = C.file_mapping_identity(addr + 100)
+        st = os.stat(paths[0])
+        assert id_a[:4] == (addr, addr + size, 0, st.st_ino)
+        assert id_a[4] == (os.major(st.st_dev) << 32 | os.minor(st.st_dev))
+        assert id_a[5] == size and id_a[6] == st.st_mtime_ns and id_a[7] == st.st_ctime_ns
+        assert id_a[8] == 1
+        # unmap, then map the other file at the same address
+        assert libc.munmap(addr, size) == 0
+        assert libc.mmap(addr, size, PROT_READ, MAP_PRIVATE | MAP_FIXED, fb, 0) == addr
+        id_b = C.file_mapping_identity(addr)
+        assert id_b[:2] == id_a[:2] and id_b[3] == os.stat(paths[1]).st_ino != id_a[3]
+        # the same file rewritten in place, same size: same inode, new times
+        time.sleep(0.05)
+        with open(paths[1], "r+b") as f:
+            f.write(rng.integers(0, 256, size, dtype=np.uint8).tobytes())
+        id_b2 = C.file_mapping_identity(addr)
+        assert id_b2[3] == id_b[3] and id_b2[5] == size
+        assert (id_b2[6], id_b2[7]) != (id_b[6], id_b[7])
+        time.sleep(0.05)
+        with open(paths[1], "wb") as f:  # O_TRUNC, then the same size again
+            f.write(rng.integers(0, 256, size, dtype=np.uint8).tobytes())
+        id_b3 = C.file_mapping_identity(addr)
+        assert id_b3[3] == id_b[3] and (id_b3[6], id_b3[7]) != (id_b2[6], id_b2[7])
+        # unlinked: no longer reachable by its path, the mapping alone identifies it
+        os.unlink(paths[1])
+        id_b4 = C.file_mapping_identity(addr)
+        assert id_b4[:5] == id_b[:5] and id_b4[8] == 0
+    finally:
+        libc.munmap(addr, size)
+        os.close(fa)
+        os.close(fb)
+    # anonymous memory and a shared writable mapping are not read-only private file mappings
+    with pytest.raises(RuntimeError, match="read-only private file mapping"):
+        C.file_mapping_identity(np.zeros(4096, np.uint8).ctypes.data)
+    fa = os.open(paths[0], os.O_RDWR)
+    addr = libc.mmap(None, size, PROT_READ | PROT_WRITE, MAP_SHARED, fa, 0)
+    try:
+        with pytest.raises(RuntimeError, match="read-only private file mapping"):
+            C.file_mapping_identity(addr)
+    finally:
+        libc.munmap(addr, size)
+        os.close(fa)
