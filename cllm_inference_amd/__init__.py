@@ -61,6 +61,7 @@ SIGNATURES = {
     "cllm_hip_register_weights": (_I, [_P, _SZ]),
     "cllm_hip_unregister_weights": (_I, [_P]),
     "cllm_hip_file_mapping_identity": (_I, [_P, _P]),
+    "cllm_hip_allocation_count": (ctypes.c_uint64, []),
     "cllm_hip_quantize_q8_0_dev": (_I, [_P, _I64, _I, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_matmul_quant_dev": (_I, [_P, _P, _U, _P, _I, _I, _I, _P, _P]),

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -58,6 +59,15 @@ int set_err(int code, const char* fmt, ...) {
             return set_err(CLLM_HIP_E_RUNTIME, "%s failed: %s", #expr, hipGetErrorString(e_)); \
     } while (0)
 
+// Every device (and pinned host) allocation the library makes goes through here, counted, so
+// a caller can check that an entry point allocated nothing (cllm_hip_allocation_count).
+std::atomic<uint64_t> g_allocations{0};
+
+hipError_t dev_alloc(void** p, size_t bytes) {
+    g_allocations.fetch_add(1, std::memory_order_relaxed);
+    return hipMalloc(p, bytes);
+}
+
 // A device allocation that only grows.
 struct DevBuf {
     void* p = nullptr;
@@ -76,7 +86,7 @@ struct DevBuf {
             p = nullptr;
             cap = 0;
         }
-        hipError_t e = hipMalloc(&p, want);
+        hipError_t e = dev_alloc(&p, want);
         if (e != hipSuccess) return e;
         cap = want;
         return hipSuccess;
@@ -283,6 +293,11 @@ struct DeviceState {
     std::mutex mtx;
     hipStream_t stream = nullptr;
     uint8_t* scratch = nullptr;  // this device's copy of the static scratch array
+    // the last eager call on the static scratch: its stream and an event after its work
+    std::mutex static_mtx;
+    hipEvent_t static_done = nullptr;
+    hipStream_t static_last = nullptr;
+    bool static_pending = false;
     DevBuf x, y, bias, wstage, qin;
     Workspace act;
     std::map<uintptr_t, Region> regions;  // host base -> device copy
@@ -322,6 +337,7 @@ int acquire(DeviceState** out) {
         HIP_TRY(hipGetSymbolAddress((void**)&st->scratch, HIP_SYMBOL(scratch)));
         if (st->scratch == nullptr || ((uintptr_t)st->scratch & 255u))
             return set_err(CLLM_HIP_E_RUNTIME, "cllm_hip: static scratch of device %d not found", dev);
+        HIP_TRY(hipEventCreateWithFlags(&st->static_done, hipEventDisableTiming));
         it = g_states.emplace(dev, std::move(st)).first;
     }
     *out = it->second.get();
@@ -362,7 +378,7 @@ bool is_device_ptr(const void* p) {
 int upload_region(DeviceState* st, uintptr_t a, size_t bytes, Region* out) {
     const size_t lead = a & 255u;
     void* mem = nullptr;
-    hipError_t e = hipMalloc(&mem, bytes + lead);
+    hipError_t e = dev_alloc(&mem, bytes + lead);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return set_err(CLLM_HIP_E_RUNTIME, "cllm_hip: cannot allocate %zu bytes for weights: %s",
@@ -1117,6 +1133,21 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
     return CLLM_HIP_OK;
 }
 
+namespace {
+// The routes of cllm_hip_matmul_quant_dev on scratch v.
+int static_routes(uint32_t type, const void* w, int in_dim, int out_dim, int n_rows, const float* x,
+                  const float* bias, float* y, const WsView& v, hipStream_t s) {
+    if (!use_mfma(type, in_dim, out_dim, n_rows)) {
+        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
+        return CLLM_HIP_OK;
+    }
+    HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
+    return CLLM_HIP_OK;
+}
+}  // namespace
+
+uint64_t cllm_hip_allocation_count(void) { return g_allocations.load(std::memory_order_relaxed); }
+
 int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t type,
                                      const float* bias, int in_dim, int out_dim, int n_rows,
                                      float* y, void* stream) {
@@ -1148,6 +1179,27 @@ int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t typ
                        "matmul_quant: %d rows of %d need %zu bytes of scratch, more than the %zu "
                        "of the fixed buffer; pass fewer rows per call",
                        n_rows, in_dim, act + pb, kStaticScratchBytes);
+    if (act + pb == 0) return static_routes(type, w, in_dim, out_dim, n_rows, x, bias, y, v, s);
+    // One GPU's array serves every call on it. A call on another stream while an earlier
+    // eager call's work may still run would overwrite that call's scratch: it is refused.
+    // Calls on one stream are ordered by the stream. Under graph capture nothing runs now, so
+    // nothing is checked or recorded (replays of graphs on different streams must be ordered
+    // by the caller).
+    std::lock_guard<std::mutex> lk(st->static_mtx);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cap));
+    const bool eager = cap == hipStreamCaptureStatusNone;
+    if (eager && st->static_pending && st->static_last != s) {
+        const hipError_t q = hipEventQuery(st->static_done);
+        if (q == hipErrorNotReady) {
+            (void)hipGetLastError();
+            return set_err(CLLM_HIP_E_BUSY,
+                           "matmul_quant: the fixed scratch of device %d is in use by a call on "
+                           "another stream; order the calls (same stream, or wait for it)",
+                           current_device());
+        }
+        HIP_TRY(q);
+    }
     if (act) carve_act((char*)st->scratch, in_dim, n_rows, v);
     if (pb) {
         v.part = (float*)(st->scratch + act);
@@ -1156,11 +1208,12 @@ int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t typ
         // activations in these bytes (a fill kernel, so the call can be captured in a graph)
         HIP_TRY(gemmw_workspace_init(v.part, gemmw_counter_bytes(), s));
     }
-    if (!use_mfma(type, in_dim, out_dim, n_rows)) {
-        HIP_TRY(run_gemv_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
-        return CLLM_HIP_OK;
+    if ((rc = static_routes(type, w, in_dim, out_dim, n_rows, x, bias, y, v, s))) return rc;
+    if (eager) {
+        HIP_TRY(hipEventRecord(st->static_done, s));
+        st->static_last = s;
+        st->static_pending = true;
     }
-    HIP_TRY(run_gemm_f32(type, (const uint8_t*)w, in_dim, out_dim, n_rows, x, bias, y, v, s));
     return CLLM_HIP_OK;
 }
 
@@ -1370,8 +1423,9 @@ int cllm_hip_gguf_open(const char* path, int upload, cllm_hip_gguf** out) {
             void* stage[2] = {nullptr, nullptr};
             hipEvent_t done[2] = {nullptr, nullptr};
             std::lock_guard<std::mutex> lk(st->mtx);
-            hipError_t e = hipMalloc(&g->dev, bytes);
+            hipError_t e = dev_alloc(&g->dev, bytes);
             for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+                g_allocations.fetch_add(1, std::memory_order_relaxed);
                 e = hipHostMalloc(&stage[i], kChunk, hipHostMallocDefault);
                 if (e == hipSuccess) e = hipEventCreateWithFlags(&done[i], hipEventDisableTiming);
             }

@@ -42,6 +42,7 @@ extern "C" {
 #define CLLM_HIP_E_ARG 3     /* null or misaligned pointer, negative size */
 #define CLLM_HIP_E_RUNTIME 4 /* HIP runtime failure (allocation, copy, launch) */
 #define CLLM_HIP_E_NODEV 5   /* no usable gfx950 device */
+#define CLLM_HIP_E_BUSY 6    /* the fixed scratch of the GPU is in use by a call on another stream */
 
 /* Selects the device used by this thread's later calls and builds its per-device state.
  * Calling it is optional: the first call on a thread uses device 0. No reference
@@ -199,12 +200,18 @@ int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, cons
  * end, and nothing is allocated or freed (call cllm_hip_init first: it builds the per-device
  * state once). A batch whose scratch exceeds the array fails with CLLM_HIP_E_ARG (M = 512
  * rows of 14336 need ~27 MB; split larger batches). Every call on one GPU shares that GPU's
- * array: calls that overlap on one GPU (different streams, or host threads) race and must be
- * ordered by the caller. */
+ * array, which keeps the last call's contents. Calls on one stream are ordered by it; a call
+ * on another stream while the last eager call's work may still be running fails with
+ * CLLM_HIP_E_BUSY instead of overwriting its scratch. Under graph capture nothing is checked:
+ * replays of captured calls on different streams must be ordered by the caller. */
 int cllm_hip_matmul_quant_static_dev(const float* x, const void* w, uint32_t type,
                                      const float* bias, int in_dim, int out_dim, int n_rows,
                                      float* y, void* stream);
 size_t cllm_hip_static_scratch_bytes(void);
+/* Device (and pinned host) allocations the library has made since it was loaded. No
+ * reference counterpart: lets a caller check that cllm_hip_matmul_quant_static_dev
+ * allocated nothing. */
+uint64_t cllm_hip_allocation_count(void);
 
 /* Reads `bytes` bytes at the device address p (16-byte aligned, bytes a multiple of 16) once,
  * by 16-byte nontemporal loads in a grid-stride loop over four 512-thread workgroups per CU,

@@ -1,8 +1,10 @@
 """cllm_hip_matmul_quant_static_dev, the matmul entry point that allocates nothing: called
-through the C ABI, its output must equal cllm_hip_matmul_quant_dev's bit for bit (the same
-kernels on the same plan; only the scratch comes from the fixed per-GPU array), on two calls
-in a row of each route, the second with a smaller input, so the second call runs on scratch
-the first one left behind. A batch whose scratch exceeds the array is refused with an error.
+through the C ABI right after cllm_hip_init, it must leave the library's allocation count
+unchanged, and its output must equal cllm_hip_matmul_quant_dev's bit for bit (the same kernels
+on the same plan; only the scratch comes from the fixed per-GPU array), on two calls in a row
+of each route, the second with a smaller input, so the second call runs on scratch the first
+one left behind. A batch whose scratch exceeds the array is refused with an error, and so is a
+call on a second stream while the first stream's call may still be running.
 """
 import ctypes
 
@@ -44,16 +46,55 @@ def test_static_scratch_matches_matmul_quant_dev(gpu, qt, n, k, ms):
     assert lib.cllm_hip_init(0) == 0
     w = torch.from_numpy(S.make_weight(qt, n, k, 300 + qt)).cuda()
     bias = torch.linspace(-1, 1, n, dtype=torch.float32, device="cuda")
-    for call, m in enumerate(ms):
-        x = torch.from_numpy(S.make_activation(m, k, 40 + 7 * call + qt, outliers=True)).cuda()
+    xs = [torch.from_numpy(S.make_activation(m, k, 40 + 7 * call + qt, outliers=True)).cuda()
+          for call, m in enumerate(ms)]
+    ys = [torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda") for m in ms]
+    torch.cuda.synchronize()
+    # the static calls first: nothing else has run on this stream in this test
+    allocs = lib.cllm_hip_allocation_count()
+    for x, y, m in zip(xs, ys, ms):
         print("static scratch", S.TYPE_NAMES[qt], n, k, "m", m, "plan", gpu.matmul_plan(qt, k, n, m),
               flush=True)
-        want = gpu.matmul_quant_dev(x, w, qt, bias, k, n)
-        y = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
         rc = _static(lib, x, w, qt, bias, k, n, y)
         assert rc == 0, lib.cllm_hip_last_error().decode()
+    torch.cuda.synchronize()
+    assert lib.cllm_hip_allocation_count() == allocs
+    for x, y, m in zip(xs, ys, ms):
+        want = gpu.matmul_quant_dev(x, w, qt, bias, k, n)
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int32), want.view(torch.int32)), (S.TYPE_NAMES[qt], m)
+
+
+def test_static_scratch_refuses_a_second_stream_while_in_use(gpu):
+    """A call on stream B while stream A's call is still queued (behind a bounded spin kernel)
+    fails with CLLM_HIP_E_BUSY and leaves A's result intact; once A is done, B's call runs."""
+    import torch
+    lib = C.load_library()
+    assert lib.cllm_hip_init(0) == 0
+    qt, n, k, m = S.Q4_K, 1024, 4096, 64
+    w = torch.from_numpy(S.make_weight(qt, n, k, 77)).cuda()
+    x = torch.from_numpy(S.make_activation(m, k, 78, outliers=True)).cuda()
+    want = gpu.matmul_quant_dev(x, w, qt, None, k, n)
+    ya = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    yb = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(50_000_000)  # a bounded spin: A's call waits behind it
+        assert _static(lib, x, w, qt, None, k, n, ya) == 0, lib.cllm_hip_last_error().decode()
+    with torch.cuda.stream(sb):
+        rc = _static(lib, x, w, qt, None, k, n, yb)
+    assert rc == 6, (rc, lib.cllm_hip_last_error().decode())  # CLLM_HIP_E_BUSY
+    assert "another stream" in lib.cllm_hip_last_error().decode()
+    # the same stream is ordered by the stream itself
+    with torch.cuda.stream(sa):
+        assert _static(lib, x, w, qt, None, k, n, ya) == 0, lib.cllm_hip_last_error().decode()
+    sa.synchronize()
+    with torch.cuda.stream(sb):
+        assert _static(lib, x, w, qt, None, k, n, yb) == 0, lib.cllm_hip_last_error().decode()
+    sb.synchronize()
+    assert torch.equal(ya.view(torch.int32), want.view(torch.int32))
+    assert torch.equal(yb.view(torch.int32), want.view(torch.int32))
 
 
 def test_static_scratch_refuses_oversized_batches(gpu):
