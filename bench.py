@@ -419,6 +419,77 @@ def prefill_layer(C, S, steps, warmup):
             "matrices": per}
 
 
+def prefill_layer_device(C, S, steps, warmup, c3=None):
+    """The linear path of the same layer at M = 512 on the device, as one step: RMSNorm into
+    the weight-row activation format -> q/k/v in one launch; the attention output (a fixed
+    synthetic input: attention is not on the linear path) quantized into the format -> wo ->
+    residual add; RMSNorm into the format -> gate/up in one launch -> SwiGLU into the format
+    -> down -> residual add (engine.cpp:556-597): 10 launches, 4 quantizations, against the
+    14 launches and 7 quantizations of the matrices one by one (c3). Graph-timed."""
+    import torch
+    cfg = "c3_q4_k_m_layer"
+    m = 512
+    mats = {label: (qt, n, k) for label, qt, n, k in S.CONFIGS[cfg]["mats"]}
+    wd = {label: torch.from_numpy(S.config_weight(cfg, label)[3]).cuda() for label in mats}
+    n_embd, n_ff = 4096, 14336
+    rng = np.random.default_rng(20266)
+    x = torch.from_numpy(S.config_activation(cfg, m, n_embd)).cuda()
+    attn = torch.from_numpy(rng.standard_normal((m, n_embd)).astype(np.float32)).cuda()
+    wn1 = torch.from_numpy((1 + 0.1 * rng.standard_normal(n_embd)).astype(np.float32)).cuda()
+    wn2 = torch.from_numpy((1 + 0.1 * rng.standard_normal(n_embd)).astype(np.float32)).cuda()
+    out = {l: torch.empty((m, n), dtype=torch.float32, device="cuda") for l, (_, n, _) in mats.items()}
+    act1, act2 = C.mfma_act_new(n_embd, m), C.mfma_act_new(n_embd, m)
+    act3, act4 = C.mfma_act_new(n_embd, m), C.mfma_act_new(n_ff, m)
+    qkv, gu = ("wq", "wk", "wv"), ("gate", "up")
+    qt = mats["wq"][0]
+    assert {mats[l][0] for l in qkv + gu + ("wo",)} == {qt}
+
+    def run_qkv():
+        C.matmul_mfma_dev([wd[l] for l in qkv], qt, n_embd, [mats[l][1] for l in qkv], act1, m,
+                          ys=[out[l] for l in qkv])
+
+    def run_gu():
+        C.matmul_mfma_dev([wd[l] for l in gu], qt, n_embd, [n_ff, n_ff], act3, m,
+                          ys=[out[l] for l in gu])
+
+    def step(i):
+        C.rmsnorm_mfma_dev(x, wn1, 1e-5, act=act1)
+        run_qkv()
+        C.quantize_mfma_dev(attn, act=act2)
+        C.matmul_mfma_dev([wd["wo"]], qt, n_embd, [n_embd], act2, m, ys=[out["wo"]])
+        C.add_dev(x, out["wo"])
+        C.rmsnorm_mfma_dev(x, wn2, 1e-5, act=act3)
+        run_gu()
+        C.swiglu_mfma_dev(out["gate"], out["up"], act=act4)
+        C.matmul_mfma_dev([wd["down"]], mats["down"][0], n_ff, [n_embd], act4, m, ys=[out["down"]])
+        C.add_dev(x, out["down"])
+
+    ms = time_loop(step, steps, warmup)
+    ms_qkv = time_loop(lambda i: run_qkv(), steps, warmup)
+    ms_gu = time_loop(lambda i: run_gu(), steps, warmup)
+    ops = sum(2.0 * m * n * k for (_, n, k) in mats.values())
+    res = {"layer_us": round(ms * 1e3, 1), "tops": round(ops / ms / 1e9, 1),
+           "frac_int8": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4),
+           "frac_fp16_mfma": round(ops / ms / 1e9 / FP16_PEAK_TFLOPS, 4),
+           "launches": 10, "activation_quantizations": 4,
+           "qkv_one_launch_us": round(ms_qkv * 1e3, 1),
+           "qkv_plan": C.matmul_mfma_plan(qt, n_embd, [mats[l][1] for l in qkv], m),
+           "gate_up_one_launch_us": round(ms_gu * 1e3, 1),
+           "gate_up_plan": C.matmul_mfma_plan(qt, n_embd, [n_ff, n_ff], m),
+           "tokens_per_s_per_layer": round(m / (ms * 1e-3), 0)}
+    if c3 is not None:
+        mt = c3["matrices"]
+        res["c3_layer_us"] = c3["layer_us"]
+        res["c3_qkv_us"] = round(sum(mt[l]["us"] for l in qkv), 1)
+        res["c3_gate_up_us"] = round(sum(mt[l]["us"] for l in gu), 1)
+    print(f"[bench] device prefill layer m=512: {ms * 1e3:.1f} us ({ops / ms / 1e9:.1f} TOPS); "
+          f"q/k/v in one launch {ms_qkv * 1e3:.1f} us, gate/up {ms_gu * 1e3:.1f} us",
+          file=sys.stderr, flush=True)
+    del wd, x, attn, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_share():
     """CPUs this process may run on: its affinity set, capped by a cgroup v2 CPU quota."""
     n = len(os.sched_getaffinity(0))
@@ -622,7 +693,9 @@ def main():
 
     if args.prefill_only:
         layer = prefill_layer(C, S, max(5, args.steps // 20), max(2, args.warmup // 10))
-        print(json.dumps({"c3_prefill_layer_m512": layer}))
+        dev = prefill_layer_device(C, S, max(5, args.steps // 20), max(2, args.warmup // 10),
+                                   c3=layer)
+        print(json.dumps({"c3_prefill_layer_m512": layer, "f1_prefill_layer_device": dev}))
         return
 
     head = decode_point(C, S, "c1_q4_k_gemv", "ffn", 1, args.steps, args.warmup, cold=True,
@@ -662,6 +735,9 @@ def main():
                                                        max(3, args.warmup // 4))
         extra["f1_decode_layer_device"] = decode_layer_device(C, S, max(20, args.steps // 4),
                                                               max(3, args.warmup // 4))
+        extra["f1_prefill_layer_device"] = prefill_layer_device(
+            C, S, max(5, args.steps // 20), max(2, args.warmup // 10),
+            c3=extra["c3_prefill_layer_m512"])
         extra["f2_gguf_upload"] = gguf_upload(C, S)
         extra["f4_device_decode_step"] = decode_model(C, S, max(10, args.steps // 10),
                                                       max(2, args.warmup // 10))

@@ -74,6 +74,12 @@ SIGNATURES = {
     "cllm_hip_rmsnorm_q8_0_dev": (_I, [_P, _P, ctypes.c_float, _I, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_swiglu_q8_0_dev": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P]),
     "cllm_hip_add_dev": (_I, [_P, _P, _I64, _P]),
+    "cllm_hip_mfma_act_bytes": (_SZ, [_I, _I]),
+    "cllm_hip_quantize_mfma_dev": (_I, [_P, _I, _I, _P, _P]),
+    "cllm_hip_rmsnorm_mfma_dev": (_I, [_P, _P, ctypes.c_float, _I, _I, _P, _P, _P]),
+    "cllm_hip_swiglu_mfma_dev": (_I, [_P, _P, _I, _I, _P, _P, _P]),
+    "cllm_hip_matmul_mfma_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P]),
+    "cllm_hip_matmul_mfma_plan": (ctypes.c_char_p, [_U, _I, _I, _P, _I]),
     "cllm_hip_gemv_q8_residual_dev": (_I, [_P, _U, _I, _I, _I, _P, _P, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_multi_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
     "cllm_hip_gemv_q8_swiglu_dev": (_I, [_U, _I, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P]),
@@ -451,6 +457,71 @@ def add_dev(x, d):
     """x += d in place (the residual adds, engine.cpp:506, 513)."""
     _check(load_library().cllm_hip_add_dev(_tp(x), _tp(d), int(x.numel()), _stream()))
     return x
+
+
+# ---- prefill linear layer on the weight-row format ----------------------------------------
+
+def mfma_act_new(in_dim: int, n_rows: int, device="cuda"):
+    """A device buffer for n_rows rows of the weight-row kernels' activation format."""
+    import torch
+    nbytes = load_library().cllm_hip_mfma_act_bytes(int(in_dim), int(n_rows))
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def quantize_mfma_dev(x, act=None):
+    """Q8_0 of the rows of x [n_rows, in_dim] into the weight-row format (a new buffer if act
+    is None); returns act."""
+    m, k = x.shape
+    if act is None:
+        act = mfma_act_new(k, m, x.device)
+    _check(load_library().cllm_hip_quantize_mfma_dev(_tp(x), int(k), int(m), _tp(act), _stream()))
+    return act
+
+
+def rmsnorm_mfma_dev(x, norm_w, eps: float, h=None, act=None):
+    """RMSNorm of the rows of x into h (fp32, when given) and the weight-row format; returns
+    act."""
+    m, k = x.shape
+    if act is None:
+        act = mfma_act_new(k, m, x.device)
+    _check(load_library().cllm_hip_rmsnorm_mfma_dev(_tp(x), _tp(norm_w), float(eps), int(k),
+                                                    int(m), _tp(h), _tp(act), _stream()))
+    return act
+
+
+def swiglu_mfma_dev(gate, up, h=None, act=None):
+    """silu(gate) * up into h (fp32, when given) and the weight-row format; returns act."""
+    m, n = gate.shape
+    if act is None:
+        act = mfma_act_new(n, m, gate.device)
+    _check(load_library().cllm_hip_swiglu_mfma_dev(_tp(gate), _tp(up), int(n), int(m), _tp(h),
+                                                   _tp(act), _stream()))
+    return act
+
+
+def matmul_mfma_dev(ws, t: int, in_dim: int, out_dims, act, n_rows: int, ys=None, biases=None):
+    """matmul_quant_batch of the matrices ws (device weights, one type and in_dim) over the
+    activation rows in act; returns the outputs [n_rows, out_dims[i]]."""
+    import torch
+    n_mats = len(ws)
+    if ys is None:
+        ys = [torch.empty((n_rows, int(n)), dtype=torch.float32, device=act.device)
+              for n in out_dims]
+    wa = (ctypes.c_void_p * n_mats)(*[w.data_ptr() for w in ws])
+    ya = (ctypes.c_void_p * n_mats)(*[y.data_ptr() for y in ys])
+    na = (ctypes.c_int * n_mats)(*[int(n) for n in out_dims])
+    ba = None
+    if biases is not None:
+        ba = (ctypes.c_void_p * n_mats)(*[0 if b is None else b.data_ptr() for b in biases])
+    _check(load_library().cllm_hip_matmul_mfma_dev(int(t), int(in_dim), n_mats, wa, na, ba, ya,
+                                                   int(n_rows), _tp(act), _stream()))
+    return ys
+
+
+def matmul_mfma_plan(t: int, in_dim: int, out_dims, n_rows: int) -> str:
+    na = (ctypes.c_int * len(out_dims))(*[int(n) for n in out_dims])
+    return load_library().cllm_hip_matmul_mfma_plan(int(t), int(in_dim), len(out_dims), na,
+                                                    int(n_rows)).decode()
 
 
 # ---- GGUF files ---------------------------------------------------------------------------

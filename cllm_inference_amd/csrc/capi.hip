@@ -126,6 +126,21 @@ void carve_act(char* p, int k, int m, WsView& v) {
     v.xq = (uint16_t*)(p + qs_bytes + 3 * sc_bytes + qh_bytes);
 }
 
+// The weight-row kernels' activation format in a caller's buffer (cllm_hip_mfma_act_bytes):
+// the Q8_0 scales xs[m * k / 32], the codes as fp16 qh[m * k], and the minimum-term operand
+// xq[m * k / 8], each at a multiple of 256 bytes.
+size_t mfma_act_bytes(int k, int m) {
+    const size_t n = (size_t)k * (size_t)m;
+    return round256((n / 32) * 4) + round256(2 * n) + round256(n / 4);
+}
+void carve_mfma(const void* act, int k, int m, float** xs, _Float16** qh, uint16_t** xq) {
+    const size_t n = (size_t)k * (size_t)m;
+    char* p = (char*)act;
+    *xs = (float*)p;
+    *qh = (_Float16*)(p + round256((n / 32) * 4));
+    *xq = (uint16_t*)(p + round256((n / 32) * 4) + round256(2 * n));
+}
+
 // A growable workspace of the library's own (per device stream, or per device for the host
 // entry points).
 struct Workspace {
@@ -1101,6 +1116,137 @@ int cllm_hip_gemv_q8_residual_dev(const void* w, uint32_t type, int in_dim, int 
     HIP_TRY(launch_gemv(type, (const uint8_t*)w, in_dim, out_dim, n_rows, qs, scales, bsums, bias,
                         y, (hipStream_t)stream, true));
     return CLLM_HIP_OK;
+}
+
+size_t cllm_hip_mfma_act_bytes(int in_dim, int n_rows) {
+    return in_dim > 0 && n_rows > 0 ? mfma_act_bytes(in_dim, n_rows) : 0;
+}
+
+namespace {
+// The checks shared by the producers of the activation format.
+int check_mfma_act(const char* who, int in_dim, int n_rows, const void* act) {
+    if (in_dim <= 0 || in_dim % 256 != 0)
+        return set_err(CLLM_HIP_E_SHAPE, "%s: in_dim must be a multiple of 256", who);
+    if (n_rows < 0) return set_err(CLLM_HIP_E_ARG, "%s: negative n_rows", who);
+    if (!act || !aligned16(act)) return set_err(CLLM_HIP_E_ARG, "%s: null or misaligned act", who);
+    return CLLM_HIP_OK;
+}
+}  // namespace
+
+int cllm_hip_quantize_mfma_dev(const float* x, int in_dim, int n_rows, void* act, void* stream) {
+    int rc = check_mfma_act("quantize_mfma", in_dim, n_rows, act);
+    if (rc) return rc;
+    if (n_rows == 0) return CLLM_HIP_OK;
+    if (!x || !aligned16(x)) return set_err(CLLM_HIP_E_ARG, "quantize_mfma: null or misaligned x");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    float* xs;
+    _Float16* qh;
+    uint16_t* xq;
+    carve_mfma(act, in_dim, n_rows, &xs, &qh, &xq);
+    HIP_TRY(launch_quantize_w(x, (int64_t)n_rows * in_dim / 32, xs, qh, xq, (hipStream_t)stream));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_rmsnorm_mfma_dev(const float* x, const float* norm_w, float eps, int in_dim,
+                              int n_rows, float* h, void* act, void* stream) {
+    int rc = check_mfma_act("rmsnorm_mfma", in_dim, n_rows, act);
+    if (rc) return rc;
+    if (n_rows == 0) return CLLM_HIP_OK;
+    if (!x || !norm_w || !aligned16(x) || !aligned16(norm_w) || !aligned16(h))
+        return set_err(CLLM_HIP_E_ARG, "rmsnorm_mfma: null or misaligned pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    float* xs;
+    _Float16* qh;
+    uint16_t* xq;
+    carve_mfma(act, in_dim, n_rows, &xs, &qh, &xq);
+    HIP_TRY(launch_rmsnorm_q8_0(x, norm_w, eps, in_dim, n_rows, h, nullptr, xs, nullptr,
+                                (hipStream_t)stream, qh, xq));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_swiglu_mfma_dev(const float* gate, const float* up, int n, int n_rows, float* h,
+                             void* act, void* stream) {
+    int rc = check_mfma_act("swiglu_mfma", n, n_rows, act);
+    if (rc) return rc;
+    if (n_rows == 0) return CLLM_HIP_OK;
+    if (!gate || !up || !aligned16(gate) || !aligned16(up) || !aligned16(h))
+        return set_err(CLLM_HIP_E_ARG, "swiglu_mfma: null or misaligned pointer");
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    float* xs;
+    _Float16* qh;
+    uint16_t* xq;
+    carve_mfma(act, n, n_rows, &xs, &qh, &xq);
+    HIP_TRY(launch_swiglu_q8_0(gate, up, (int64_t)n * n_rows, h, nullptr, xs, nullptr,
+                               (hipStream_t)stream, qh, xq));
+    return CLLM_HIP_OK;
+}
+
+int cllm_hip_matmul_mfma_dev(uint32_t type, int in_dim, int n_mats, const void* const* w,
+                             const int* out_dims, const float* const* bias, float* const* y,
+                             int n_rows, const void* act, void* stream) {
+    if (n_mats < 1 || !w || !out_dims || !y)
+        return set_err(CLLM_HIP_E_ARG, "matmul_quant_batch: no matrices");
+    int rc;
+    for (int i = 0; i < n_mats; ++i)
+        if ((rc = check_matmul("matmul_quant_batch", type, in_dim, out_dims[i]))) return rc;
+    if ((rc = check_mfma_act("matmul_quant_batch", in_dim, n_rows, act))) return rc;
+    if (!gemmw_supported(type))
+        return set_err(CLLM_HIP_E_TYPE, "matmul_quant_batch: no weight-row kernel for this type");
+    for (int i = 0; i < n_mats; ++i) {
+        if (!w[i] || !y[i]) return set_err(CLLM_HIP_E_ARG, "matmul_quant_batch: null pointer");
+        if (!aligned16(w[i]) || ((uintptr_t)y[i] & 3u) || (bias && ((uintptr_t)bias[i] & 3u)))
+            return set_err(CLLM_HIP_E_ARG, "matmul_quant_batch: misaligned device pointer");
+        if (!gemmw_fits(type, in_dim, out_dims[i], n_rows))
+            return set_err(CLLM_HIP_E_ARG, "matmul_quant_batch: weights or activations past 4 GiB");
+    }
+    if (n_rows == 0) return CLLM_HIP_OK;
+    DeviceState* st;
+    if ((rc = acquire(&st))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    float* xs;
+    _Float16* qh;
+    uint16_t* xq;
+    carve_mfma(act, in_dim, n_rows, &xs, &qh, &xq);
+    Workspace* ws;
+    {
+        std::lock_guard<std::mutex> lk(st->mtx);
+        auto& slot = st->dev_ws[s];
+        if (!slot) slot = std::make_unique<Workspace>();
+        ws = slot.get();
+    }
+    const uint8_t* const* wb = (const uint8_t* const*)w;
+    if (gemmw_multi_supported(type, n_mats)) {
+        HIP_TRY(ws->ensure_part(gemmw_multi_partial_bytes(type, in_dim, n_mats, out_dims, n_rows), s));
+        HIP_TRY(launch_gemmw_multi(type, in_dim, n_rows, n_mats, wb, out_dims, bias, y, xs, qh, xq,
+                                   ws->v.part, ws->v.part_cap, s));
+        return CLLM_HIP_OK;
+    }
+    // one launch per matrix (types without the multi-matrix kernel), all on the one format
+    for (int i = 0; i < n_mats; ++i) {
+        HIP_TRY(ws->ensure_part(gemmw_partial_bytes(type, in_dim, out_dims[i], n_rows), s));
+        HIP_TRY(launch_gemmw(type, wb[i], in_dim, out_dims[i], n_rows, xs, qh, xq,
+                             bias ? bias[i] : nullptr, y[i], ws->v.part, ws->v.part_cap, s));
+    }
+    return CLLM_HIP_OK;
+}
+
+const char* cllm_hip_matmul_mfma_plan(uint32_t type, int in_dim, int n_mats, const int* out_dims,
+                                      int n_rows) {
+    static thread_local char buf[160];
+    if (!gemmw_supported(type) || in_dim % 256 != 0 || n_mats < 1 || !out_dims) return "none";
+    if (gemmw_multi_supported(type, n_mats)) {
+        gemmw_multi_plan_name(type, in_dim, n_mats, out_dims, n_rows, buf, sizeof buf);
+        const size_t l = std::strlen(buf);
+        snprintf(buf + l, sizeof buf - l, " matrices=%d launches=1", n_mats);
+    } else {
+        gemmw_plan_name(type, in_dim, out_dims[0], n_rows, buf, sizeof buf);
+        const size_t l = std::strlen(buf);
+        snprintf(buf + l, sizeof buf - l, " matrices=%d launches=%d", n_mats, n_mats);
+    }
+    return buf;
 }
 
 int cllm_hip_matmul_quant_dev(const float* x, const void* w, uint32_t type, const float* bias,

@@ -243,14 +243,25 @@ __device__ __forceinline__ void store_tile(int n, int m, const float* __restrict
 
 }  // namespace
 
+// Up to kMaxSegs weight matrices of one type and K over one activation batch, in one launch
+// (the q, k and v projections, or gate and up): segment i has n[i] rows, its own bias and
+// output, and owns the workgroups [tile_end[i - 1], tile_end[i]) of the grid's x dimension.
+constexpr int kMaxSegs = 3;
+struct Segs {
+    const uint8_t* w[kMaxSegs];
+    const float* bias[kMaxSegs];
+    float* y[kMaxSegs];
+    int n[kMaxSegs];
+    int tile_end[kMaxSegs];
+    int count;
+};
+
 template <int W, int NT, int MT, bool Q5>
-__global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict__ w,
-                                                      uint32_t row_bytes, int k, int n, int m,
+__global__ __launch_bounds__(64 * W) void k_gemmw_q4k(Segs segs, uint32_t row_bytes, int k, int m,
                                                       const _Float16* __restrict__ qh,
                                                       const float* __restrict__ xs,
                                                       const uint16_t* __restrict__ xq,
-                                                      const float* __restrict__ bias,
-                                                      float* __restrict__ y, float* __restrict__ part,
+                                                      float* __restrict__ part,
                                                       int* __restrict__ counters, int split_stages) {
     using C = Cfg<W, NT, MT, Q5>;
     constexpr int BM = C::BM;
@@ -269,7 +280,14 @@ __global__ __launch_bounds__(64 * W) void k_gemmw_q4k(const uint8_t* __restrict_
     // as the Q6_K kernel does, measured slower here at M = 512: gate 127.3 against 125.2 us,
     // wq 52.9 against 51.9, wk 26.2 against 24.9.)
     const int mb_count = (m + BM - 1) / BM;
-    const int lin = blockIdx.x;
+    // the workgroup's segment (wave-uniform), then its tile within the segment
+    int seg = 0;
+    while (seg + 1 < segs.count && (int)blockIdx.x >= segs.tile_end[seg]) ++seg;
+    const int lin = (int)blockIdx.x - (seg ? segs.tile_end[seg - 1] : 0);
+    const uint8_t* __restrict__ w = segs.w[seg];
+    const float* __restrict__ bias = segs.bias[seg];
+    float* __restrict__ y = segs.y[seg];
+    const int n = segs.n[seg];
     const int nblk = lin / mb_count, mblk = lin - nblk * mb_count;
     const int n0 = nblk * C::BN, m0 = mblk * BM;
     const int nb = k / 32;
@@ -1187,9 +1205,9 @@ Plan plan_for(uint32_t type, int k, int n, int m) {
 }
 
 template <int W, int NT, int MT, bool Q5>
-hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const _Float16* qh, const float* xs,
-                     const uint16_t* xq, const float* bias, float* y, float* part, int* counters,
-                     int splits, hipStream_t stream) {
+hipError_t launch_q4(Segs segs, int k, int m, const _Float16* qh, const float* xs,
+                     const uint16_t* xq, float* part, int* counters, int splits,
+                     hipStream_t stream) {
     using C = Cfg<W, NT, MT, Q5>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -1199,11 +1217,16 @@ hipError_t launch_q4(const uint8_t* w, int k, int n, int m, const _Float16* qh, 
         attr_set = true;
     }
     const uint32_t row_bytes = (uint32_t)(k / 256) * (Q5 ? Q5_K_BYTES : Q4_K_BYTES);
-    const int tiles = ((n + C::BN - 1) / C::BN) * ((m + C::BM - 1) / C::BM);
+    const int mb = (m + C::BM - 1) / C::BM;
+    int tiles = 0;
+    for (int i = 0; i < segs.count; ++i) {
+        tiles += ((segs.n[i] + C::BN - 1) / C::BN) * mb;
+        segs.tile_end[i] = tiles;
+    }
     const int stages = k / kKS, per = 2 * ((stages / 2 + splits - 1) / splits);
     hipLaunchKernelGGL((k_gemmw_q4k<W, NT, MT, Q5>), dim3((unsigned)tiles, (unsigned)splits),
-                       dim3(C::THREADS), C::LDS, stream, w, row_bytes, k, n, m, qh, xs, xq, bias,
-                       y, part, counters, per);
+                       dim3(C::THREADS), C::LDS, stream, segs, row_bytes, k, m, qh, xs, xq, part,
+                       counters, per);
     return hipGetLastError();
 }
 
@@ -1286,18 +1309,45 @@ hipError_t gemmw_workspace_init(void* part, size_t bytes, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const float* xs,
-                        const _Float16* qh, const uint16_t* xq,
-                        const float* bias, float* y, float* part, size_t part_bytes,
-                        hipStream_t stream) {
-    if (!gemmw_supported(type) || k % 256 != 0 || !gemmw_fits(type, k, n, m))
+namespace {
+
+// Tiles of a launch over the segments: whole tiles per segment.
+int64_t segs_tiles(const Plan& p, const Segs& sg, int m) {
+    const int bn = 32 * p.nt * p.wv;
+    int64_t t = 0;
+    for (int i = 0; i < sg.count; ++i) t += (sg.n[i] + bn - 1) / bn;
+    return t * ((m + 32 * p.mt - 1) / (32 * p.mt));
+}
+
+int segs_rows(const Segs& sg) {
+    int n = 0;
+    for (int i = 0; i < sg.count; ++i) n += sg.n[i];
+    return n;
+}
+
+// One launch of the weight-row kernel over the segments (several only for Q4_K / Q5_K), on
+// the plan of their rows together.
+hipError_t gemmw_dispatch(uint32_t type, const Segs& sg, int k, int m, const float* xs,
+                          const _Float16* qh, const uint16_t* xq, float* part, size_t part_bytes,
+                          hipStream_t stream) {
+    if (!gemmw_supported(type) || k % 256 != 0 || sg.count < 1 || sg.count > kMaxSegs)
         return hipErrorNotSupported;
-    Plan p = plan_for(type, k, n, m);
-    if (p.splits > 1 && (part == nullptr || part_bytes < slices_bytes(p, n, m) + kCounterBytes ||
-                         plan_tiles(p, n, m) * 4 > (int64_t)kCounterBytes))
+    if (sg.count > 1 && type != T_Q4_K && type != T_Q5_K) return hipErrorNotSupported;
+    for (int i = 0; i < sg.count; ++i)
+        if (!gemmw_fits(type, k, sg.n[i], m)) return hipErrorNotSupported;
+    Plan p = plan_for(type, k, segs_rows(sg), m);
+    const int64_t tiles = segs_tiles(p, sg, m);
+    const size_t tile_bytes = (size_t)(32 * p.nt * p.wv) * (size_t)(32 * p.mt) * sizeof(float);
+    if (p.splits > 1 && (part == nullptr ||
+                         part_bytes < (size_t)p.splits * (size_t)tiles * tile_bytes + kCounterBytes ||
+                         tiles * 4 > (int64_t)kCounterBytes))
         p.splits = 1;
     int* counters = p.splits > 1 ? (int*)part : nullptr;
     part = p.splits > 1 ? (float*)((char*)part + kCounterBytes) : nullptr;
+    const uint8_t* w = sg.w[0];
+    const int n = sg.n[0];
+    const float* bias = sg.bias[0];
+    float* y = sg.y[0];
     hipError_t e = hipErrorNotSupported;
     if (type == T_Q6_K) {
         if (p.wv == 8)
@@ -1323,17 +1373,17 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
     } else if (type == T_Q5_K) {
         // the four shapes of the default plan (the only ones the tuning override takes)
         if (p.wv == 8 && p.nt == 1 && p.mt == 4)
-            e = launch_q4<8, 1, 4, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
+            e = launch_q4<8, 1, 4, true>(sg, k, m, qh, xs, xq, part, counters, p.splits, stream);
         else if (p.wv == 8 && p.nt == 1 && p.mt == 2)
-            e = launch_q4<8, 1, 2, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
+            e = launch_q4<8, 1, 2, true>(sg, k, m, qh, xs, xq, part, counters, p.splits, stream);
         else if (p.wv == 4 && p.nt == 1 && p.mt == 2)
-            e = launch_q4<4, 1, 2, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
+            e = launch_q4<4, 1, 2, true>(sg, k, m, qh, xs, xq, part, counters, p.splits, stream);
         else
-            e = launch_q4<4, 1, 1, true>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
+            e = launch_q4<4, 1, 1, true>(sg, k, m, qh, xs, xq, part, counters, p.splits, stream);
     } else {
 #define CLLM_GEMMW_CASE(A, B, D)                                                              \
         if (p.wv == A && p.nt == B && p.mt == D)                                               \
-            e = launch_q4<A, B, D, false>(w, k, n, m, qh, xs, xq, bias, y, part, counters, p.splits, stream);
+            e = launch_q4<A, B, D, false>(sg, k, m, qh, xs, xq, part, counters, p.splits, stream);
         CLLM_GEMMW_CASE(8, 1, 4)
         CLLM_GEMMW_CASE(8, 1, 2)
         CLLM_GEMMW_CASE(8, 2, 2)
@@ -1344,6 +1394,63 @@ hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, co
 #undef CLLM_GEMMW_CASE
     }
     return e;
+}
+
+Segs one_seg(const uint8_t* w, int n, const float* bias, float* y) {
+    Segs sg{};
+    sg.w[0] = w;
+    sg.n[0] = n;
+    sg.bias[0] = bias;
+    sg.y[0] = y;
+    sg.count = 1;
+    return sg;
+}
+
+}  // namespace
+
+hipError_t launch_gemmw(uint32_t type, const uint8_t* w, int k, int n, int m, const float* xs,
+                        const _Float16* qh, const uint16_t* xq,
+                        const float* bias, float* y, float* part, size_t part_bytes,
+                        hipStream_t stream) {
+    return gemmw_dispatch(type, one_seg(w, n, bias, y), k, m, xs, qh, xq, part, part_bytes, stream);
+}
+
+bool gemmw_multi_supported(uint32_t type, int count) {
+    return (type == T_Q4_K || type == T_Q5_K) && count >= 1 && count <= kMaxSegs;
+}
+
+size_t gemmw_multi_partial_bytes(uint32_t type, int k, int count, const int* n, int m) {
+    if (!gemmw_supported(type) || k % 256 != 0 || !gemmw_multi_supported(type, count)) return 0;
+    Segs sg{};
+    sg.count = count;
+    for (int i = 0; i < count; ++i) sg.n[i] = n[i];
+    const Plan p = plan_for(type, k, segs_rows(sg), m);
+    if (p.splits <= 1) return 0;
+    const size_t tile_bytes = (size_t)(32 * p.nt * p.wv) * (size_t)(32 * p.mt) * sizeof(float);
+    return (size_t)p.splits * (size_t)segs_tiles(p, sg, m) * tile_bytes + kCounterBytes;
+}
+
+hipError_t launch_gemmw_multi(uint32_t type, int k, int m, int count, const uint8_t* const* w,
+                              const int* n, const float* const* bias, float* const* y,
+                              const float* xs, const _Float16* qh, const uint16_t* xq,
+                              float* part, size_t part_bytes, hipStream_t stream) {
+    if (!gemmw_multi_supported(type, count)) return hipErrorNotSupported;
+    Segs sg{};
+    sg.count = count;
+    for (int i = 0; i < count; ++i) {
+        sg.w[i] = w[i];
+        sg.n[i] = n[i];
+        sg.bias[i] = bias ? bias[i] : nullptr;
+        sg.y[i] = y[i];
+    }
+    return gemmw_dispatch(type, sg, k, m, xs, qh, xq, part, part_bytes, stream);
+}
+
+void gemmw_multi_plan_name(uint32_t type, int k, int count, const int* n, int m, char* buf,
+                           size_t cap) {
+    int rows = 0;
+    for (int i = 0; i < count; ++i) rows += n[i];
+    gemmw_plan_name(type, k, rows, m, buf, cap);
 }
 
 void gemmw_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap) {

@@ -23,10 +23,22 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Where a producer writes the Q8_0 blocks of its output (any pointer may be null): the Q8_0
+// row (codes qs, scales, bsums) and the weight-row MFMA kernels' format (the codes as exact
+// fp16 qh, and the minimum term's operand xq, whose record of block blk is xq + 32 (blk / 8),
+// rows of whole 256-element super-blocks).
+struct Q8Out {
+    int8_t* qs = nullptr;
+    float* scales = nullptr;
+    int32_t* bsums = nullptr;
+    _Float16* qh = nullptr;
+    uint16_t* xq = nullptr;
+    __host__ __device__ bool any() const { return qs || qh; }
+};
+
 // Q8_0 of the 32-element block held by 8 consecutive lanes (4 elements each, lane part):
 // writes the lane's 4 codes and, from part 0, the block's d and bsum.
-__device__ __forceinline__ void quantize_block8(f32x4 v, int part, int64_t blk, int8_t* qs,
-                                                float* scales, int32_t* bsums) {
+__device__ __forceinline__ void quantize_block8(f32x4 v, int part, int64_t blk, const Q8Out& o) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = fmaxf(amax, __shfl_xor(amax, 1, 8));
     amax = fmaxf(amax, __shfl_xor(amax, 2, 8));
@@ -35,13 +47,20 @@ __device__ __forceinline__ void quantize_block8(f32x4 v, int part, int64_t blk, 
     const float id = q8_inv_scale(d);
     int s;
     const uint32_t packed = q8_quant4(v.x, v.y, v.z, v.w, id, s);
-    *(uint32_t*)(qs + blk * 32 + part * 4) = packed;
+    if (o.qs) *(uint32_t*)(o.qs + blk * 32 + part * 4) = packed;
+    if (o.qh) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 hv = {(_Float16)(int8_t)(packed & 0xFF), (_Float16)(int8_t)(packed >> 8),
+                       (_Float16)(int8_t)(packed >> 16), (_Float16)(int8_t)(packed >> 24)};
+        *(h4*)(o.qh + blk * 32 + part * 4) = hv;
+    }
     s += __shfl_xor(s, 1, 8);
     s += __shfl_xor(s, 2, 8);
     s += __shfl_xor(s, 4, 8);
     if (part == 0) {
-        scales[blk] = d;
-        bsums[blk] = s;
+        if (o.scales) o.scales[blk] = d;
+        if (o.bsums) o.bsums[blk] = s;
+        if (o.xq) xq_store(o.xq + (blk >> 3) * 32, (int)(blk & 7), d * (float)s);
     }
 }
 
@@ -52,10 +71,7 @@ constexpr int kThreads = 256;
 __global__ __launch_bounds__(kThreads) void k_rmsnorm_q8_0(const float* __restrict__ x,
                                                            const float* __restrict__ w,
                                                            float eps, int n,
-                                                           float* __restrict__ h,
-                                                           int8_t* __restrict__ qs,
-                                                           float* __restrict__ scales,
-                                                           int32_t* __restrict__ bsums) {
+                                                           float* __restrict__ h, Q8Out o) {
     __shared__ float part_sums[kThreads / 64];
     const int row = blockIdx.x;
     const float* xr = x + (size_t)row * n;
@@ -81,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_q8_0(const float* __restri
     const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sum, (float)n) + eps));
 
     float* hr = h ? h + (size_t)row * n : nullptr;
-    if (qs == nullptr || n % 32 != 0) {
+    if (!o.any() || n % 32 != 0) {
         for (int i = threadIdx.x; i < n; i += kThreads)
             if (hr) hr[i] = __fmul_rn(__fmul_rn(xr[i], rms), w[i]);
         return;
@@ -100,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm_q8_0(const float* __restri
         hv.w = __fmul_rn(__fmul_rn(xv.w, rms), wv.w);
         if (b < nb) {
             if (hr) *(f32x4*)(hr + b * 32 + part * 4) = hv;
-            quantize_block8(hv, part, (int64_t)row * nb + b, qs, scales, bsums);
+            quantize_block8(hv, part, (int64_t)row * nb + b, o);
         }
     }
 }
@@ -115,10 +131,7 @@ template <int CPT>
 __global__ __launch_bounds__(kRegThreads) void k_rmsnorm_q8_0_reg(const float* __restrict__ x,
                                                                   const float* __restrict__ w,
                                                                   float eps, int n,
-                                                                  float* __restrict__ h,
-                                                                  int8_t* __restrict__ qs,
-                                                                  float* __restrict__ scales,
-                                                                  int32_t* __restrict__ bsums) {
+                                                                  float* __restrict__ h, Q8Out o) {
     __shared__ float part_sums[kRegThreads / 64];
     const int row = blockIdx.x;
     const float* xr = x + (size_t)row * n;
@@ -154,7 +167,7 @@ __global__ __launch_bounds__(kRegThreads) void k_rmsnorm_q8_0_reg(const float* _
         hv.z = __fmul_rn(__fmul_rn(v[i].z, rms), wv[i].z);
         hv.w = __fmul_rn(__fmul_rn(v[i].w, rms), wv[i].w);
         if (h) *(f32x4*)(h + (size_t)row * n + 4 * c) = hv;
-        if (qs) quantize_block8(hv, part, (int64_t)row * (n / 32) + c / 8, qs, scales, bsums);
+        if (o.any()) quantize_block8(hv, part, (int64_t)row * (n / 32) + c / 8, o);
     }
 }
 
@@ -162,10 +175,7 @@ __global__ __launch_bounds__(kRegThreads) void k_rmsnorm_q8_0_reg(const float* _
 __global__ __launch_bounds__(kThreads) void k_swiglu_q8_0(const float* __restrict__ gate,
                                                           const float* __restrict__ up,
                                                           int64_t n_blocks,
-                                                          float* __restrict__ h,
-                                                          int8_t* __restrict__ qs,
-                                                          float* __restrict__ scales,
-                                                          int32_t* __restrict__ bsums) {
+                                                          float* __restrict__ h, Q8Out o) {
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gt >> 3;
     const int part = (int)(gt & 7);
@@ -179,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void k_swiglu_q8_0(const float* __restric
     hv.z = silu_mul(g.z, u.z);
     hv.w = silu_mul(g.w, u.w);
     if (h) *(f32x4*)(h + at) = hv;
-    if (qs) quantize_block8(hv, part, blk, qs, scales, bsums);
+    if (o.any()) quantize_block8(hv, part, blk, o);
 }
 
 // silu(g) * u for lengths that are not whole blocks (fp32 output only)
@@ -208,30 +218,35 @@ __global__ __launch_bounds__(kThreads) void k_add(float* __restrict__ x, const f
 
 hipError_t launch_rmsnorm_q8_0(const float* x, const float* w, float eps, int n, int rows,
                                float* h, int8_t* qs, float* scales, int32_t* bsums,
-                               hipStream_t stream) {
+                               hipStream_t stream, _Float16* qh, uint16_t* xq) {
     if (rows <= 0 || n <= 0) return hipSuccess;
+    Q8Out o;
+    o.qs = qs, o.scales = scales, o.bsums = bsums, o.qh = qh, o.xq = xq;
     if (n % 32 == 0 && n <= 4 * 4 * kRegThreads) {
         const int cpt = (n + 4 * kRegThreads - 1) / (4 * kRegThreads);
         if (cpt == 1)
             hipLaunchKernelGGL(k_rmsnorm_q8_0_reg<1>, dim3((unsigned)rows), dim3(kRegThreads), 0,
-                               stream, x, w, eps, n, h, qs, scales, bsums);
+                               stream, x, w, eps, n, h, o);
         else if (cpt == 2)
             hipLaunchKernelGGL(k_rmsnorm_q8_0_reg<2>, dim3((unsigned)rows), dim3(kRegThreads), 0,
-                               stream, x, w, eps, n, h, qs, scales, bsums);
+                               stream, x, w, eps, n, h, o);
         else
             hipLaunchKernelGGL(k_rmsnorm_q8_0_reg<4>, dim3((unsigned)rows), dim3(kRegThreads), 0,
-                               stream, x, w, eps, n, h, qs, scales, bsums);
+                               stream, x, w, eps, n, h, o);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(k_rmsnorm_q8_0, dim3((unsigned)rows), dim3(kThreads), 0, stream, x, w, eps,
-                       n, h, qs, scales, bsums);
+                       n, h, o);
     return hipGetLastError();
 }
 
 hipError_t launch_swiglu_q8_0(const float* gate, const float* up, int64_t total, float* h,
-                              int8_t* qs, float* scales, int32_t* bsums, hipStream_t stream) {
+                              int8_t* qs, float* scales, int32_t* bsums, hipStream_t stream,
+                              _Float16* qh, uint16_t* xq) {
     if (total <= 0) return hipSuccess;
-    if (qs == nullptr || total % 32 != 0) {
+    Q8Out o;
+    o.qs = qs, o.scales = scales, o.bsums = bsums, o.qh = qh, o.xq = xq;
+    if (!o.any() || total % 32 != 0) {
         hipLaunchKernelGGL(k_swiglu_f32, dim3((unsigned)((total + kThreads - 1) / kThreads)),
                            dim3(kThreads), 0, stream, gate, up, total, h);
         return hipGetLastError();
@@ -239,7 +254,7 @@ hipError_t launch_swiglu_q8_0(const float* gate, const float* up, int64_t total,
     // one wave per workgroup: a decode row (14336 elements) then spreads over 224 CUs
     const int64_t n_blocks = total / 32;
     hipLaunchKernelGGL(k_swiglu_q8_0, dim3((unsigned)((n_blocks * 8 + 63) / 64)), dim3(64), 0,
-                       stream, gate, up, n_blocks, h, qs, scales, bsums);
+                       stream, gate, up, n_blocks, h, o);
     return hipGetLastError();
 }
 

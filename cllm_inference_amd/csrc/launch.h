@@ -133,11 +133,14 @@ void gemmw_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap);
 // Producers of the linear layers' activations (k_producers.hip): RMSNorm of `rows` rows of n
 // and SwiGLU (silu(gate) * up) over `total` elements, each writing h (fp32, may be null)
 // and, when qs is not null and n (total) is a multiple of 32, its Q8_0 blocks; x += d.
+// qh / xq (null, or both): the Q8_0 blocks also in the weight-row kernels' format (fp16
+// codes, minimum-term operand; the rows whole 256-element super-blocks).
 hipError_t launch_rmsnorm_q8_0(const float* x, const float* w, float eps, int n, int rows,
                                float* h, int8_t* qs, float* scales, int32_t* bsums,
-                               hipStream_t stream);
+                               hipStream_t stream, _Float16* qh = nullptr, uint16_t* xq = nullptr);
 hipError_t launch_swiglu_q8_0(const float* gate, const float* up, int64_t total, float* h,
-                              int8_t* qs, float* scales, int32_t* bsums, hipStream_t stream);
+                              int8_t* qs, float* scales, int32_t* bsums, hipStream_t stream,
+                              _Float16* qh = nullptr, uint16_t* xq = nullptr);
 hipError_t launch_add(float* x, const float* d, int64_t n, hipStream_t stream);
 
 // Float ops between the linear layers (k_attention.hip): NEOX RoPE in place on `rows` rows
@@ -175,6 +178,17 @@ hipError_t launch_gemv_f(uint32_t type, const uint8_t* w, int k, int n, int m, c
                          const float* bias, float* y, hipStream_t stream);
 hipError_t gemmw_workspace_init(void* part, size_t bytes, hipStream_t stream);
 bool gemmw_supported(uint32_t type);
+// Several matrices of one type and K over one activation batch in one weight-row launch
+// (Q4_K / Q5_K, up to 3): the same contract as launch_gemmw per matrix, the split-K region
+// sized by gemmw_multi_partial_bytes.
+bool gemmw_multi_supported(uint32_t type, int count);
+size_t gemmw_multi_partial_bytes(uint32_t type, int k, int count, const int* n, int m);
+hipError_t launch_gemmw_multi(uint32_t type, int k, int m, int count, const uint8_t* const* w,
+                              const int* n, const float* const* bias, float* const* y,
+                              const float* xs, const _Float16* qh, const uint16_t* xq,
+                              float* part, size_t part_bytes, hipStream_t stream);
+void gemmw_multi_plan_name(uint32_t type, int k, int count, const int* n, int m, char* buf,
+                           size_t cap);
 // false when the shape's weights (4 GiB and up) or fp16 activations (2 m k bytes, 4 GiB and
 // up) are past the weight-row kernels' 32-bit offsets; such shapes take the int8 kernel
 bool gemmw_fits(uint32_t type, int k, int n, int m);

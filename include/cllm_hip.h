@@ -240,6 +240,38 @@ int cllm_hip_swiglu_q8_0_dev(const float* gate, const float* up, int n, int n_ro
 /* x[i] += d[i], i < n: the residual adds (src/core/engine.cpp:506, 513, 587, 598). */
 int cllm_hip_add_dev(float* x, const float* d, int64_t n, void* stream);
 
+/* ---- the prefill linear layer, device-resident (stream-ordered) ------------------------
+ * The reference's prefill quantizes each projection's input inside every matmul_quant_batch
+ * call, the same rows once per matrix (q, k and v on h: src/core/engine.cpp:564-566; gate and
+ * up on h2: 594-595; mm_batch, 276-285). Here a producer writes the Q8_0 blocks of an input
+ * once, in the format the weight-row MFMA kernels read (act: the block scales, the codes as
+ * exact fp16 and the K-quant minimum term's operand; cllm_hip_mfma_act_bytes bytes of device
+ * memory, 16-byte aligned, in_dim a multiple of 256), and the matrices on that input run
+ * from it, q/k/v or gate/up in one launch. The codes and scales are quantize_row_q8_0's,
+ * bit for bit, of the producer's fp32 output. */
+size_t cllm_hip_mfma_act_bytes(int in_dim, int n_rows);
+/* Q8_0 of n_rows rows of x[n_rows][in_dim] into act. */
+int cllm_hip_quantize_mfma_dev(const float* x, int in_dim, int n_rows, void* act, void* stream);
+/* RMSNorm of each row (rms_norm_ptr, src/core/engine.cpp:23-28, 558-562, 590-592), as
+ * cllm_hip_rmsnorm_q8_0_dev, into h (fp32, may be null) and act. */
+int cllm_hip_rmsnorm_mfma_dev(const float* x, const float* norm_w, float eps, int in_dim,
+                              int n_rows, float* h, void* act, void* stream);
+/* h = silu(gate) * up (src/core/engine.cpp:596), as cllm_hip_swiglu_q8_0_dev, into h (fp32,
+ * may be null) and act; n a multiple of 256. */
+int cllm_hip_swiglu_mfma_dev(const float* gate, const float* up, int n, int n_rows, float* h,
+                             void* act, void* stream);
+/* matmul_quant_batch of n_mats matrices of one type (Q4_0/Q5_0/Q8_0/Q4_K/Q5_K/Q6_K) and
+ * in_dim over the n_rows activation rows in act: y[i][n_rows][out_dims[i]] (+ bias[i], which
+ * may be null, as may bias). Q4_K / Q5_K run up to 3 matrices in one weight-row launch; other
+ * types, or more matrices, one launch per matrix. Split-K scratch comes from the library's
+ * workspace of the stream. Replaces the mm_batch calls above (engine.cpp:276-285). */
+int cllm_hip_matmul_mfma_dev(uint32_t type, int in_dim, int n_mats, const void* const* w,
+                             const int* out_dims, const float* const* bias, float* const* y,
+                             int n_rows, const void* act, void* stream);
+/* The kernel instantiation, split and launch count cllm_hip_matmul_mfma_dev would run. */
+const char* cllm_hip_matmul_mfma_plan(uint32_t type, int in_dim, int n_mats, const int* out_dims,
+                                      int n_rows);
+
 /* ---- float ops between the linear layers (stream-ordered) ----------------------------- */
 
 /* Rows ids[0..n_ids) of a weight matrix of any GGML type (device pointers), dequantized
