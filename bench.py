@@ -209,11 +209,13 @@ def read_ceiling(p):
 
 
 def m_sweep(C, S, steps, warmup):
-    """c4: Q5_K 14336x4096 and Q8_0 4096x4096 at M = 1, 4, 16, 64, 256, cold weights."""
+    """c4: Q5_K 14336x4096 and Q8_0 4096x4096 at M = 1, 4, 16, 64, 256, cold weights; the
+    M = 1 points with the one-launch read ceiling of their weight copies."""
     sweep = {}
     for label in ("q5_k", "q8_0"):
         for m in (1, 4, 16, 64, 256):
-            p = decode_point(C, S, "c4_m_sweep", label, m, steps, warmup, cold=True)
+            p = decode_point(C, S, "c4_m_sweep", label, m, steps, warmup, cold=True,
+                             ceiling=m == 1)
             ops = 2.0 * m * p["n"] * p["k"]
             sweep[f"{label}_m{m}"] = {
                 "route": p["route"], "plan": p["plan"], "us": round(p["ms_step"] * 1e3, 2),
@@ -221,6 +223,8 @@ def m_sweep(C, S, steps, warmup):
                 "frac_hbm": round(p["gbs_step"] / HBM_PEAK_GBS, 4),
                 "tops": round(ops / p["ms_step"] / 1e9, 2),
                 "frac_int8": round(ops / p["ms_step"] / 1e9 / INT8_PEAK_TOPS, 4)}
+            if m == 1:
+                sweep[f"{label}_m{m}"]["read_ceiling"] = read_ceiling(p)
     return sweep
 
 
@@ -248,6 +252,10 @@ def float_dot_points(C, S, steps, warmup):
             out[tag] = {"us": round(ms * 1e3, 2), "gbs": round(nbytes / ms / 1e6, 1),
                         "frac_hbm": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
                         "route": C.matmul_route(qt, k, n, m)}
+            if m == 1:  # the one-launch read of the same weight copies: the step's floor
+                ms_read = time_loop(lambda i: C.read_stream_dev(ws[i % copies]), steps, warmup)
+                out[tag]["read_ceiling"] = read_ceiling(
+                    {"weight_bytes": int(w.size), "ms_read": ms_read, "ms_step": ms})
             print(f"[bench] float-dot {tag}: {ms * 1e3:.2f} us, {nbytes / ms / 1e6:.1f} GB/s",
                   file=sys.stderr, flush=True)
         del ws

@@ -610,6 +610,17 @@ bool use_small(uint32_t type, int k, int n, int m) {
         !gemm_sm_supported(type, k, m))
         return false;
     if (knob == 1) return m >= 3;
+    if (type == T_Q6_K) {
+        // up to 16 rows (one token tile; two ran 55-57 us on the large shapes against 35-36 on
+        // the weight-row kernel), where the GEMV would need two launches or more, or from 4
+        // rows on matrices of 32 M weights or more. MI355X, cold weights, us, small-batch
+        // kernel against the previous route:
+        //   Q6_K 4096x14336, 4 / 8 / 16 rows:  22.1 / 22.3 / 23.2 against 31.5 / 34.9 / 35.7
+        //   Q6_K 14336x4096, 4 / 8 / 16 rows:  21.0 / 21.3 / 22.1 against 20.9 / 29.9 / 34.2
+        //   Q6_K 1024x4096,  4 / 7 / 8 / 16:   11.3 / 11.4 / 11.5 / 11.4 against 7.4 / 15.6 / 10.3 / 20.4
+        const bool large = (int64_t)n * k >= (int64_t(32) << 20);
+        return m >= 4 && m <= 16 && (large || gemv_launch_count(type, k, m) >= 2);
+    }
     if (type != T_Q8_0 && m > 16 && n >= kSmallMaxN) return false;
     return m >= kSmallMinRows && m <= (type == T_Q8_0 ? 64 : 32);
 }
@@ -689,10 +700,22 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
 }
 
 // MFMA route from fp32 activations: quantize straight into the format the kernel reads.
+// The small-batch route from fp32 activation rows: quantized inside the kernel, except Q6_K,
+// whose small-batch kernel reads a batch quantized once into the workspace.
+hipError_t run_small_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
+                         const float* bias, float* y, const WsView& ws, hipStream_t stream) {
+    if (type == T_Q6_K) {
+        hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws.qs, ws.sc, ws.bs, stream);
+        if (e != hipSuccess) return e;
+        return launch_gemm_sm_q8(type, w, k, n, m, ws.qs, ws.sc, ws.bs, bias, y, ws.part,
+                                 ws.part_cap, stream);
+    }
+    return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
+}
+
 hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                         const float* bias, float* y, const WsView& ws, hipStream_t stream) {
-    if (use_small(type, k, n, m))
-        return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
+    if (use_small(type, k, n, m)) return run_small_f32(type, w, k, n, m, x, bias, y, ws, stream);
     const int64_t nblk = (int64_t)m * k / 32;
     const GemmKind kind = gemm_kind(type, k, n, m);
     if (kind == GemmKind::F16) {
@@ -727,7 +750,7 @@ hipError_t run_gemv_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         const float* bias, float* y, const WsView& ws, hipStream_t stream,
                         bool accumulate = false) {
     if (!accumulate && use_small(type, k, n, m))
-        return launch_gemm_sm_f32(type, w, k, n, m, x, bias, y, ws.part, ws.part_cap, stream);
+        return run_small_f32(type, w, k, n, m, x, bias, y, ws, stream);
     if (m <= kFusedMaxRows)
         return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream, accumulate);
     hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws.qs, ws.sc, ws.bs, stream);

@@ -44,17 +44,20 @@ constexpr int kSmActBytes = 64 * 1024;  // int8 activations of a split: 16 MT ro
 
 __host__ __device__ constexpr size_t sm_align16(size_t v) { return (v + 15) & ~(size_t)15; }
 
-// Bytes of 256 elements of one weight row.
+// Bytes of an item's row in its LDS slot: 256 elements of one weight row. A Q6_K super-block
+// (210 bytes, 2-byte aligned) comes as the 224-byte window from the 16-byte boundary at or
+// below it; with rows of a multiple of 16 bytes (k a multiple of 2048) the window of the
+// row's last super-block ends exactly at the row's end, and no window leaves its row.
 template <uint32_t T>
 __host__ __device__ constexpr int sm_sb_bytes() {
-    return T == T_Q8_0 ? 8 * 34 : T == T_Q5_K ? 176 : 144;
+    return T == T_Q8_0 ? 8 * 34 : T == T_Q5_K ? 176 : T == T_Q6_K ? 224 : 144;
 }
 template <uint32_t T>
 __host__ __device__ constexpr bool sm_kq() { return T == T_Q4_K || T == T_Q5_K; }
-// Per-wave exchange table: K-quants, the 6-bit scales [16 rows][8 blocks] as bytes; Q8_0, the
-// blocks' d as floats [8 blocks][16 rows].
+// Per-wave exchange table: Q4_K / Q5_K, the 6-bit scales [16 rows][8 blocks] as bytes; Q6_K,
+// the 16 int8 scales of each row [16 rows][16]; Q8_0, the blocks' d as floats [8 blocks][16 rows].
 template <uint32_t T>
-__host__ __device__ constexpr int sm_tab_bytes() { return sm_kq<T>() ? 128 : 512; }
+__host__ __device__ constexpr int sm_tab_bytes() { return sm_kq<T>() ? 128 : T == T_Q6_K ? 256 : 512; }
 
 // LDS layout of a workgroup: activations qs [16 MT][kc + 8] (the reduction area after the main
 // loop), dx [16 MT][kc / 32], for the K-quants dx * bsum [16 MT][kc / 32], the waves' weight
@@ -128,12 +131,14 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
     u32x4 pc[NL];
     auto load_item = [&](int it, uint32_t dep) {
         const int sbg = min(k0 / 256 + sb_lo + it, k / 256 - 1);
+        // the item's bytes within each row (Q6_K: the 16-byte boundary at or below the block)
+        const int64_t at = T == T_Q6_K ? ((int64_t)sbg * Q6_K_BYTES) & ~(int64_t)15 : (int64_t)sbg * SB;
 #pragma unroll
         for (int l = 0; l < NL; ++l) {
             const int p = min(64 * l + lane, NP - 1);
             const int rr = p / PPR, c = p - rr * PPR;
             const int row = min(rg * 16 + rr, n - 1);
-            const uint8_t* src = w + (int64_t)row * row_bytes + (int64_t)sbg * SB + 16 * c + dep;
+            const uint8_t* src = w + (int64_t)row * row_bytes + at + 16 * c + dep;
             pc[l] = __builtin_nontemporal_load((const u32x4*)src);
         }
     };
@@ -237,7 +242,78 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
         const int sbl = sb_lo + it;  // super-block within the split
         const uint8_t* rowp = slot + r * SB;  // this lane's A-fragment row
         u32x2 A[8];
-        if constexpr (KQ) {
+        if constexpr (T == T_Q6_K) {
+            // the super-block sits at byte sh of each slot row (even, the same for every row)
+            const int sh = ((k0 / 256 + sbl) * Q6_K_BYTES) & 15;
+            // 8 bytes at rowp + o (o even): two dword reads, or three realigned
+            auto rd8 = [&](const uint8_t* base, int o) -> u32x2 {
+                const uint8_t* q = base + o;  // 4-byte aligned when sh is, not 8
+                if ((sh & 2) == 0) return u32x2{*(const uint32_t*)q, *(const uint32_t*)(q + 4)};
+                const uint32_t d0 = *(const uint32_t*)(q - 2), d1 = *(const uint32_t*)(q + 2),
+                               d2 = *(const uint32_t*)(q + 6);
+                return u32x2{__builtin_amdgcn_alignbyte(d1, d0, 2), __builtin_amdgcn_alignbyte(d2, d1, 2)};
+            };
+            // block b = 4 half + jj holds elements 128 half + 32 jj + l (l < 32): low (jj < 2) or
+            // high nibble of ql[64 half + 32 (jj & 1) + l], bits 2 jj of qh[32 half + l]; the
+            // lane's 8 elements l = 8 g .. 8 g + 7 share the scale sc[2 b + g / 2]. As int8,
+            // 4 (q - 32) = (q << 2) ^ 0x80 per byte, exact (|4 (q - 32)| <= 128).
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const u32x2 qh8 = rd8(rowp, sh + 128 + 32 * half + 8 * g);
+#pragma unroll
+                for (int jo = 0; jo < 2; ++jo) {
+                    const u32x2 ql8 = rd8(rowp, sh + 64 * half + 32 * jo + 8 * g);
+#pragma unroll
+                    for (int hi = 0; hi < 2; ++hi) {
+                        const int jj = jo + 2 * hi;
+                        const u32x2 nib = hi ? ((ql8 >> 4) & 0x0F0F0F0Fu) : (ql8 & 0x0F0F0F0Fu);
+                        const u32x2 hb = (qh8 >> (2 * jj)) & 0x03030303u;
+                        A[4 * half + jj] = ((nib << 2) | (hb << 6)) ^ 0x80808080u;
+                    }
+                }
+            }
+            // the row's 16 scales to the table (lanes of g = 0), then the result rows' scales
+            if (g == 0) {
+                *(u32x2*)(tab + r * 16) = rd8(rowp, sh + 192);
+                *(u32x2*)(tab + r * 16 + 8) = rd8(rowp, sh + 200);
+            }
+            u32x4 scr[4];
+            float dq[4];  // the result rows' d / 4 (the weight operand holds 4 (q - 32))
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                scr[i] = *(const u32x4*)(tab + (4 * g + i) * 16);
+                dq[i] = 0.25f * f16_to_f32(*(const uint16_t*)(slot + (4 * g + i) * SB + sh + 208));
+            }
+            const u32x2 zero2 = {0u, 0u};
+#pragma unroll
+            for (int j = 0; j < MT; ++j) {
+                const int tok = 16 * j + r;
+                const f32x4 dx0 = *(const f32x4*)(axd + tok * nb + sbl * 8);
+                const f32x4 dx1 = *(const f32x4*)(axd + tok * nb + sbl * 8 + 4);
+                const float dx[8] = {dx0.x, dx0.y, dx0.z, dx0.w, dx1.x, dx1.y, dx1.z, dx1.w};
+                f32x4 sacc = fzero;
+#pragma unroll
+                for (int b = 0; b < 8; ++b) {
+                    const u32x2 bq = *(const u32x2*)(aq + tok * QSR + sbl * 256 + 32 * b + 8 * g);
+                    // the two 16-element halves of the block apart: lanes g < 2 hold the first
+                    const i32x4 d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                        as_long(g < 2 ? A[b] : zero2), as_long(bq), izero, 0, 0, 0);
+                    const i32x4 d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                        as_long(g < 2 ? zero2 : A[b]), as_long(bq), izero, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t wsc = scr[i][b >> 1];
+                        const int sc0 = __builtin_amdgcn_sbfe(wsc, 16 * (b & 1), 8);
+                        const int sc1 = __builtin_amdgcn_sbfe(wsc, 16 * (b & 1) + 8, 8);
+                        // |4 dot| <= 2^20 and |sc| <= 128: the 24-bit products are exact
+                        const int v = __mul24(sc0, d0[i]) + __mul24(sc1, d1[i]);
+                        sacc[i] = __builtin_fmaf((float)v, dx[b], sacc[i]);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_fmaf(dq[i], sacc[i], acc[j][i]);
+            }
+        } else if constexpr (KQ) {
             constexpr int QS = T == T_Q5_K ? 48 : 16;
             u32x2 h = {0, 0};
             if constexpr (T == T_Q5_K) h = *(const u32x2*)(rowp + 16 + 8 * g);
@@ -443,11 +519,14 @@ struct SmPlan {
 // MI355X (fused step, cold weights, us for splits x K parts): Q5_K 14336x4096 at 8 rows 19.5
 // (4 x 1) against 21.0 (1 x 4), at 16 rows 20.7 (4 x 1) against 21.2 (1 x 4); Q8_0 4096x4096
 // at 16 rows 12.4 (4 x 4) against 14.0 (1 x 16).
-SmPlan sm_plan(int k, int n, int m) {
+// Q6_K reads a batch quantized once (no per-workgroup quantization to bound), so its K ranges
+// may fill the activation LDS: Q6_K 4096x14336 at 8 rows runs 4 splits of 3584 elements.
+SmPlan sm_plan(uint32_t type, int k, int n, int m) {
     SmPlan p{};
     p.mt = (m + 15) / 16;
     const int nsb = k / 256;
-    const int sb_max = std::max(1, std::min(4, kSmActBytes / (16 * p.mt) / 256));
+    const int sb_act = kSmActBytes / (16 * p.mt) / 256;
+    const int sb_max = std::max(1, type == T_Q6_K ? sb_act : std::min(4, sb_act));
     p.splits = (nsb + sb_max - 1) / sb_max;
     // the tuning knob "gemm_small_plan" (splits, K parts per workgroup) overrides the plan
     const int fs = tuning().gemm_small_splits.load(std::memory_order_relaxed);
@@ -527,7 +606,7 @@ hipError_t launch_sm(uint32_t type, const uint8_t* w, int k, int n, int m, const
                      const int8_t* qs, const float* xs, const int32_t* xb, const float* bias,
                      float* y, float* part, size_t part_bytes, hipStream_t stream) {
     if (!gemm_sm_supported(type, k, m)) return hipErrorNotSupported;
-    const SmPlan p = sm_plan(k, n, m);
+    const SmPlan p = sm_plan(type, k, n, m);
     int* counters = nullptr;
     float* slices = nullptr;
     if (p.splits > 1) {
@@ -541,6 +620,10 @@ hipError_t launch_sm(uint32_t type, const uint8_t* w, int k, int n, int m, const
         case T_Q4_K: return launch_sm_mt<T_Q4_K, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
         case T_Q5_K: return launch_sm_mt<T_Q5_K, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
         case T_Q8_0: return launch_sm_mt<T_Q8_0, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
+        case T_Q6_K:  // from a quantized batch only (the fused form would spill registers)
+            if constexpr (!FUSED)
+                return launch_sm_mt<T_Q6_K, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
+            return hipErrorNotSupported;
         default: return hipErrorNotSupported;
     }
 }
@@ -548,19 +631,21 @@ hipError_t launch_sm(uint32_t type, const uint8_t* w, int k, int n, int m, const
 }  // namespace
 
 bool gemm_sm_supported(uint32_t type, int k, int m) {
-    return (type == T_Q4_K || type == T_Q5_K || type == T_Q8_0) && k % 256 == 0 && k > 0 &&
-           m >= 1 && m <= 64;
+    // Q6_K rows must be whole 16-byte pieces: k a multiple of 2048 (8 super-blocks)
+    return (type == T_Q4_K || type == T_Q5_K || type == T_Q8_0 ||
+            (type == T_Q6_K && k % 2048 == 0)) && k % 256 == 0 && k > 0 && m >= 1 && m <= 64;
 }
 
 size_t gemm_sm_partial_bytes(uint32_t type, int k, int n, int m) {
     if (!gemm_sm_supported(type, k, m)) return 0;
-    const SmPlan p = sm_plan(k, n, m);
+    const SmPlan p = sm_plan(type, k, n, m);
     return p.splits > 1 ? kSmCounterBytes + sm_slices_bytes(p, n) : 0;
 }
 
 void gemm_sm_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap) {
-    const SmPlan p = sm_plan(k, n, m);
-    snprintf(buf, cap, "k_gemm_sm<%s,%d> splits=%d kp=%d", type == T_Q8_0 ? "Q8_0" : type == T_Q5_K ? "Q5_K" : "Q4_K",
+    const SmPlan p = sm_plan(type, k, n, m);
+    snprintf(buf, cap, "k_gemm_sm<%s,%d> splits=%d kp=%d",
+             type == T_Q8_0 ? "Q8_0" : type == T_Q5_K ? "Q5_K" : type == T_Q6_K ? "Q6_K" : "Q4_K",
              p.mt, p.splits, p.kp);
 }
 

@@ -92,7 +92,7 @@ def test_decode_plans():
     assert C.matmul_plan(S.Q6_K, 14336, 4096, 1) == "k_gemv_str<Q6_K,1> launches=1"
     assert C.matmul_plan(S.Q8_0, 896, 4864, 1) == "k_gemv_str<Q8_0,1> launches=1"
     assert C.matmul_plan(S.Q4_K, 4096, 1024, 1) == "k_gemv<Q4_K,1> launches=1"
-    assert C.matmul_plan(S.Q6_K, 4096, 4096, 13) == "k_gemv<Q6_K,8> launches=3"
+    assert C.matmul_plan(S.Q4_0, 4096, 4096, 13) == "k_gemv<Q4_0,8> launches=3"
     assert C.matmul_plan(S.Q4_K, 4096, 14336, 3) == "k_gemv<Q4_K,2> launches=2"
     assert C.matmul_plan(S.Q4_K, 4096, 14336, 5) == "k_gemv<Q4_K,4> launches=2"
     try:
@@ -106,24 +106,31 @@ def test_decode_plans():
         C.tune("gemv_kernel")
 
 
-def test_mid_batch_routes_without_small_kernel():
-    """Below 16 rows, Q6_K / Q4_0 / Q5_0 (no small-batch kernel) take the weight-row kernel
-    once the GEMV would read the weights three times on matrices of 32 M weights or more, four
-    times on smaller ones, or from 8 rows on the large ones (Q6_K there: 8 rows in two
-    launches). Types with the small-batch kernel keep the GEMV up to its 8-row threshold."""
-    # (type, in_dim, out_dim, rows that go to the MFMA route among 1..16)
+def test_mid_batch_routes():
+    """Below 16 rows, Q4_0 / Q5_0 (no small-batch kernel) take the weight-row kernel once the
+    GEMV would read the weights three times on matrices of 32 M weights or more, four times on
+    smaller ones, or from 8 rows on the large ones. Q6_K takes the small-batch kernel from 4 to
+    16 rows where the GEMV would need two launches or more, or on matrices of 32 M weights or
+    more; the weight-row kernel beyond 16 rows. Q4_K / Q8_0 keep the GEMV below 8 rows."""
+    # (type, in_dim, out_dim, rows that go to the MFMA route among 1..16, to the small route)
     cases = [
-        (S.Q6_K, 4096, 14336, {7, 9, 10, 11, 12, 13, 14, 15, 16}),
-        (S.Q6_K, 14336, 4096, set(range(5, 17))),
-        (S.Q4_0, 4096, 14336, set(range(7, 17))),
-        (S.Q5_0, 4096, 4096, {15, 16}),
-        (S.Q6_K, 4096, 1024, {15, 16}),
+        (S.Q6_K, 4096, 14336, set(), set(range(4, 17))),
+        (S.Q6_K, 14336, 4096, set(), set(range(4, 17))),
+        (S.Q6_K, 4096, 1024, set(), {5, 6, 7} | set(range(9, 17))),
+        (S.Q4_0, 4096, 14336, set(range(7, 17)), set()),
+        (S.Q5_0, 4096, 4096, {15, 16}, set()),
     ]
-    for t, k, n, want in cases:
+    for t, k, n, want_mfma, want_small in cases:
         got = {m for m in range(1, 17) if C.matmul_route(t, k, n, m) == "mfma"}
-        assert got == want, (S.TYPE_NAMES[t], k, n, sorted(got))
-    assert C.matmul_plan(S.Q6_K, 4096, 14336, 13) == "k_gemmw_q6k<4,1> splits=4"
-    assert C.matmul_plan(S.Q6_K, 4096, 14336, 8) == "k_gemv<Q6_K,8> launches=1"
+        assert got == want_mfma, (S.TYPE_NAMES[t], k, n, sorted(got))
+        got = {m for m in range(1, 17) if C.matmul_route(t, k, n, m) == "small"}
+        assert got == want_small, (S.TYPE_NAMES[t], k, n, sorted(got))
+    assert C.matmul_plan(S.Q6_K, 4096, 14336, 8) == "k_gemm_sm<Q6_K,1> splits=1 kp=4"
+    assert C.matmul_plan(S.Q6_K, 14336, 4096, 8) == "k_gemm_sm<Q6_K,1> splits=4 kp=4"
+    assert C.matmul_plan(S.Q6_K, 4096, 14336, 17) == "k_gemmw_q6k<4,1> splits=4"
+    assert C.matmul_plan(S.Q6_K, 4096, 1024, 8) == "k_gemv<Q6_K,8> launches=1"
+    # Q6_K rows of a multiple of 16 bytes only (k a multiple of 2048)
+    assert C.matmul_route(S.Q6_K, 2816, 14336, 8) != "small"
     for m in range(1, 8):
         assert C.matmul_route(S.Q4_K, 4096, 14336, m) == "gemv"
         assert C.matmul_route(S.Q8_0, 4096, 4096, m) == "gemv"
@@ -197,7 +204,8 @@ def test_small_batch_plans():
     assert C.matmul_route(S.Q4_K, 4096, 14336, 8) == "small"
     assert C.matmul_route(S.Q4_K, 4096, 14336, 64) == "mfma"
     assert C.matmul_route(S.Q8_0, 4096, 4096, 64) == "small"
-    assert C.matmul_route(S.Q6_K, 4096, 14336, 16) == "mfma"
+    assert C.matmul_route(S.Q6_K, 4096, 14336, 16) == "small"
+    assert C.matmul_route(S.Q6_K, 4096, 14336, 17) == "mfma"
     try:
         C.tune("gemm_small", 1)
         assert C.matmul_route(S.Q4_K, 4096, 14336, 3) == "small"

@@ -135,3 +135,52 @@ def test_residual_add_on_small_route(gpu, orc):
     ref = gpu.matmul_quant_dev(xd, wd, qt, bd, k, n).cpu().numpy()
     torch.cuda.synchronize()
     assert np.array_equal(bits(y.cpu().numpy()), bits((base + ref).astype(np.float32)))
+
+
+@pytest.mark.parametrize("k, n, m", [(14336, 4096, 8), (14336, 4096, 4), (4096, 14336, 16),
+                                     (4096, 14336, 5), (4096, 1024, 13), (2048, 333, 9)])
+def test_q6_k_small_batches_default_route_vs_oracle(gpu, orc, k, n, m):
+    """Q6_K on the small-batch kernel (the batch quantized once, int8 MFMA, the two 16-element
+    scales of a block on two MFMAs over its halves): the default route of these shapes, every
+    output against the oracle with and without a bias, the fused and pre-quantized entry
+    points bit for bit, two runs bit for bit."""
+    qt = S.Q6_K
+    assert gpu.matmul_route(qt, k, n, m) == "small"
+    w = S.make_weight(qt, n, k, 40 + m + n)
+    x = S.make_activation(m, k, 41 + m, outliers=True)
+    bias = np.random.default_rng(n + m).standard_normal(n).astype(np.float32)
+    print("q6_k small", n, k, m, gpu.matmul_plan(qt, k, n, m), flush=True)
+    for b in (None, bias):
+        y_fused, y_q8 = _run(gpu, w, x, qt, b, k, n, m)
+        y2, _ = _run(gpu, w, x, qt, b, k, n, m)
+        assert np.array_equal(bits(y_fused), bits(y_q8))
+        assert np.array_equal(bits(y_fused), bits(y2))
+        exact, abs_sum = orc.matmul_f64(x, w, qt, b, k, n, m)
+        yo = orc.matmul(x, w, qt, b, k, n, m, threads=8)
+        check_close(y_fused.reshape(m, n), yo.reshape(m, n), exact, abs_sum,
+                    f"q6_k small {n}x{k} m{m}")
+
+
+def test_q6_k_small_kernel_tiles_and_splits(gpu, orc):
+    """The Q6_K small-batch kernel forced onto ragged batches of 1 to 4 token tiles, and onto
+    K splits and K parts the plan does not take, against the oracle."""
+    qt, k = S.Q6_K, 4096
+    for n, m, plan in [(77, 17, None), (130, 33, None), (64, 64, None), (100, 3, None),
+                       (300, 12, (4, 2)), (300, 12, (2, 8)), (300, 40, (8, 1))]:
+        w = S.make_weight(qt, n, k, 50 + n + m)
+        x = S.make_activation(m, k, 51 + m, outliers=True)
+        try:
+            gpu.tune("gemm_small", 1)
+            if plan:
+                gpu.tune("gemm_small_plan", *plan)
+            print("q6_k small forced", n, k, m, gpu.matmul_plan(qt, k, n, m), flush=True)
+            assert gpu.matmul_route(qt, k, n, m) == "small"
+            y_fused, y_q8 = _run(gpu, w, x, qt, None, k, n, m)
+        finally:
+            gpu.tune("gemm_small_plan")
+            gpu.tune("gemm_small")
+        assert np.array_equal(bits(y_fused), bits(y_q8))
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+        yo = orc.matmul(x, w, qt, None, k, n, m)
+        check_close(y_fused.reshape(m, n), yo.reshape(m, n), exact, abs_sum,
+                    f"q6_k forced {n} m{m} plan {plan}")
