@@ -699,12 +699,27 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
     return launch_gemm16(type, w, k, n, m, ws.qh, sc, ws.px, bias, y, stream);
 }
 
-// MFMA route from fp32 activations: quantize straight into the format the kernel reads.
-// The small-batch route from fp32 activation rows: quantized inside the kernel, except Q6_K,
-// whose small-batch kernel reads a batch quantized once into the workspace.
+// Whether the small-batch route quantizes fp32 activation rows once into the workspace (then
+// runs the kernel on that batch) rather than inside every workgroup of the kernel. Once: every
+// workgroup of the in-kernel form quantizes all rows of its K range, which bounds that range
+// (so longer K needs split-K and its cross-workgroup tail), while a batch quantized once lets
+// a workgroup hold K = 4096 for 16 rows. MI355X, cold weights, graph-timed us, quantized once
+// against in the kernel (the quantizing launch included):
+//   Q5_K 14336x4096, 4 / 8 / 16 rows:  17.8 / 17.9 / 18.6 against 18.8 / 19.4 / 20.4
+//   Q8_0 4096x4096, 4 / 8 / 16 / 64:   11.0 / 11.3 / 11.8 / 19.1 against 12.3 / 12.3 / 12.7 / 21.3
+// Q6_K has only this form; the tuning knob "gemm_small_q8" forces either (1 once, 2 in-kernel).
+bool small_quantize_once(uint32_t type, int k, int n, int m) {
+    (void)k;
+    (void)n;
+    (void)m;
+    if (type == T_Q6_K) return true;
+    return tuning().gemm_small_q8.load(std::memory_order_relaxed) != 2;
+}
+
+// The small-batch route from fp32 activation rows (small_quantize_once picks the form).
 hipError_t run_small_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                          const float* bias, float* y, const WsView& ws, hipStream_t stream) {
-    if (type == T_Q6_K) {
+    if (small_quantize_once(type, k, n, m)) {
         hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws.qs, ws.sc, ws.bs, stream);
         if (e != hipSuccess) return e;
         return launch_gemm_sm_q8(type, w, k, n, m, ws.qs, ws.sc, ws.bs, bias, y, ws.part,
@@ -1745,6 +1760,9 @@ int cllm_hip_tune(const char* knob, const int* values, int n_values) {
     } else if (std::strcmp(knob, "gemm_small") == 0) {
         if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemm_small is 0, 1 or 2");
         t.gemm_small.store(v(0));
+    } else if (std::strcmp(knob, "gemm_small_q8") == 0) {
+        if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemm_small_q8 is 0, 1 or 2");
+        t.gemm_small_q8.store(v(0));
     } else if (std::strcmp(knob, "gemm_small_plan") == 0) {
         t.gemm_small_splits.store(v(0));
         t.gemm_small_kp.store(v(1));
@@ -1763,7 +1781,8 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
     if (std::strcmp(route, "gemv") == 0) {
         gemv_plan_name(type, in_dim, out_dim, n_rows, buf, sizeof buf);
     } else if (std::strcmp(route, "small") == 0) {
-        gemm_sm_plan_name(type, in_dim, out_dim, n_rows, buf, sizeof buf);
+        gemm_sm_plan_name(type, in_dim, out_dim, n_rows,
+                          !small_quantize_once(type, in_dim, out_dim, n_rows), buf, sizeof buf);
     } else if (std::strcmp(route, "mfma") != 0) {
         snprintf(buf, sizeof buf, "%s", route);
     } else {

@@ -121,16 +121,16 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
     const int k0 = blockIdx.y * kc;
     const int kce = min(kc, k - k0);    // this split's elements (a multiple of 256)
     const int nsb = kce / 256;
-    const int per = (nsb + kp - 1) / kp;
-    const int sb_lo = min(kpart * per, nsb);
-    const int items = rg < n_rg ? max(0, min(nsb, sb_lo + per) - sb_lo) : 0;
+    // K part kpart takes super-blocks kpart, kpart + kp, ..: at each step the kp waves of a row
+    // group read neighbouring super-blocks of the same rows
+    const int items = rg < n_rg && kpart < nsb ? (nsb - kpart + kp - 1) / kp : 0;
     uint8_t* slot = lds + L.slots + (size_t)wave * 16 * SB;
     uint8_t* tab = lds + L.tab + (size_t)wave * sm_tab_bytes<T>();
 
     // ---- item loads: piece p = 64 L + lane is piece p % PPR of item row p / PPR ----
     u32x4 pc[NL];
     auto load_item = [&](int it, uint32_t dep) {
-        const int sbg = min(k0 / 256 + sb_lo + it, k / 256 - 1);
+        const int sbg = min(k0 / 256 + kpart + kp * it, k / 256 - 1);
         // the item's bytes within each row (Q6_K: the 16-byte boundary at or below the block)
         const int64_t at = T == T_Q6_K ? ((int64_t)sbg * Q6_K_BYTES) & ~(int64_t)15 : (int64_t)sbg * SB;
 #pragma unroll
@@ -230,16 +230,14 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
     }
     sm_barrier();
 
-    // ---- main loop: this wave's items (row group rg, super-blocks sb_lo ..) ----
+    // ---- main loop: this wave's items (row group rg, super-blocks kpart, kpart + kp, ..) ----
     f32x4 acc[MT];
 #pragma unroll
     for (int j = 0; j < MT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const i32x4 izero = {0, 0, 0, 0};
     const f32x4 fzero = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int it = 0; it < items; ++it) {
-        to_slot();
-        if (it + 1 < items) load_item(it + 1, 0u);
-        const int sbl = sb_lo + it;  // super-block within the split
+    auto compute_item = [&](int it) {
+        const int sbl = kpart + kp * it;  // super-block within the split
         const uint8_t* rowp = slot + r * SB;  // this lane's A-fragment row
         u32x2 A[8];
         if constexpr (T == T_Q6_K) {
@@ -408,60 +406,78 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
                 }
             }
         }
+    };
+    for (int it = 0; it < items; ++it) {
+        to_slot();
+        if (it + 1 < items) load_item(it + 1, 0u);
+        compute_item(it);
     }
 
     // ---- the kp parts of each row group, added in part order ----
+    // The group's tile is MT x 64 entries e = 64 j + l (token tile j, accumulator lane l: token
+    // 16 j + l % 16, rows 4 (l / 16) .. + 3 of the row group), one f32x4 each. Thread
+    // t = 64 kpart + lane of the group owns entries t, t + 64 kp, ..; it adds the kp parts of
+    // each in part order (bit for bit the order of one wave adding them one by one) and writes
+    // the result, or its split's partial.
     sm_barrier();  // every wave is past its activation reads: the qs area becomes the sums
+    f32x4* red = (f32x4*)lds;
     if (kp > 1) {
-        f32x4* red = (f32x4*)lds;
 #pragma unroll
         for (int j = 0; j < MT; ++j) red[(wave * MT + j) * 64 + lane] = acc[j];
         sm_barrier();
-        if (kpart == 0) {
-            for (int q = 1; q < kp; ++q)
+    }
+    const int t_own = 64 * kpart + lane;
+    const int gw = wave - kpart;  // the group's first wave
+    const bool live = rg < n_rg;
+    f32x4 ev[MT];
+    bool own[MT];
 #pragma unroll
-                for (int j = 0; j < MT; ++j) acc[j] += red[((wave + q) * MT + j) * 64 + lane];
+    for (int q = 0; q < MT; ++q) {
+        const int e = t_own + 64 * kp * q;
+        own[q] = live && e < 64 * MT;
+        ev[q] = fzero;
+        if (kp == 1) {
+            ev[q] = acc[q];  // t_own = lane: entry 64 q + lane is this wave's tile j = q
+        } else if (own[q]) {
+            f32x4 v = red[gw * MT * 64 + e];
+            for (int pq = 1; pq < kp; ++pq) v += red[(gw + pq) * MT * 64 + e];
+            ev[q] = v;
         }
     }
-    const bool owner = kpart == 0 && rg < n_rg;
-    // the lane's 4 rows are the same for every token tile: their bias values are loaded
-    // together first (rows past n clamped), not one dependent load per output
+    // writes entry q's values (token and rows from its entry index) plus the bias
     auto write_out = [&](const f32x4 (&v)[MT]) {
-        float bv[4];
-        if (bias) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bv[i] = bias[min(rg * 16 + 4 * g + i, n - 1)];
-        }
-#pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            const int tok = 16 * j + r;
+        for (int q = 0; q < MT; ++q) {
+            if (!own[q]) continue;
+            const int e = t_own + 64 * kp * q;
+            const int tok = 16 * (e >> 6) + (e & 15);
+            const int row0 = rg * 16 + 4 * ((e >> 4) & 3);
             if (tok >= m) continue;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int row = rg * 16 + 4 * g + i;
-                if (row < n) y[(size_t)tok * n + row] = bias ? v[j][i] + bv[i] : v[j][i];
+                const int row = row0 + i;
+                if (row < n) y[(size_t)tok * n + row] = bias ? v[q][i] + bias[row] : v[q][i];
             }
         }
     };
     const int splits = (int)gridDim.y;
     if (splits == 1) {
-        if (owner) write_out(acc);
+        write_out(ev);
         return;
     }
-    // split-K: this split's tile of sums to part[split][rg][j][lane], as relaxed agent-scope
-    // 64-bit atomic stores (coherent across XCDs by themselves); the last split of the row
-    // tile to arrive adds all splits in split order
+    // split-K: this split's tile of sums to part[split][rg][e], as relaxed agent-scope 64-bit
+    // atomic stores (coherent across XCDs by themselves); the last split of the row tile to
+    // arrive adds all splits in split order
     uint64_t* pp = (uint64_t*)part;
     const size_t stride = (size_t)n_rg * MT * 128;  // 8-byte pairs per split
-    if (owner) {
 #pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            const size_t o = (size_t)blockIdx.y * stride + ((size_t)rg * MT + j) * 128 + 2 * lane;
-            const uint64_t a = (uint64_t)__float_as_uint(acc[j][0]) | ((uint64_t)__float_as_uint(acc[j][1]) << 32);
-            const uint64_t b = (uint64_t)__float_as_uint(acc[j][2]) | ((uint64_t)__float_as_uint(acc[j][3]) << 32);
-            __hip_atomic_store(pp + o, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(pp + o + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    for (int q = 0; q < MT; ++q) {
+        if (!own[q]) continue;
+        const size_t o = (size_t)blockIdx.y * stride + (size_t)rg * MT * 128 + 2 * (t_own + 64 * kp * q);
+        const uint64_t a = (uint64_t)__float_as_uint(ev[q][0]) | ((uint64_t)__float_as_uint(ev[q][1]) << 32);
+        const uint64_t b = (uint64_t)__float_as_uint(ev[q][2]) | ((uint64_t)__float_as_uint(ev[q][3]) << 32);
+        __hip_atomic_store(pp + o, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + o + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
     __syncthreads();
@@ -473,20 +489,23 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
             __hip_atomic_store(&counters[blockIdx.x], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    if (!last_split || !owner) return;
+    if (!last_split) return;
     f32x4 sum[MT];
+#pragma unroll
+    for (int q = 0; q < MT; ++q) sum[q] = fzero;
     for (int sp = 0; sp < splits; ++sp) {
 #pragma unroll
-        for (int j = 0; j < MT; ++j) {
-            f32x4 v = acc[j];
+        for (int q = 0; q < MT; ++q) {
+            if (!own[q]) continue;
+            f32x4 v = ev[q];
             if (sp != (int)blockIdx.y) {
-                const size_t o = (size_t)sp * stride + ((size_t)rg * MT + j) * 128 + 2 * lane;
+                const size_t o = (size_t)sp * stride + (size_t)rg * MT * 128 + 2 * (t_own + 64 * kp * q);
                 const uint64_t a = __hip_atomic_load(pp + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const uint64_t b = __hip_atomic_load(pp + o + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 v = f32x4{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
                           __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32))};
             }
-            sum[j] = sp == 0 ? v : sum[j] + v;
+            sum[q] = sp == 0 ? v : sum[q] + v;
         }
     }
     write_out(sum);
@@ -511,27 +530,27 @@ struct SmPlan {
     int mt, kc, splits, kp, grid_x;
 };
 
-// Token tiles of 16; K split over workgroups in ranges of at most 1024 elements (4
-// super-blocks; fewer when 16 MT rows of them would not fit kSmActBytes); the K parts per
-// workgroup that bring the workgroup count closest to one per CU without exceeding it. The
-// 1024: each workgroup quantizes the activations of its K range, so shorter ranges cut that
-// redundant work, and the partial tiles they cost are small next to the weights. Measured on
-// MI355X (fused step, cold weights, us for splits x K parts): Q5_K 14336x4096 at 8 rows 19.5
-// (4 x 1) against 21.0 (1 x 4), at 16 rows 20.7 (4 x 1) against 21.2 (1 x 4); Q8_0 4096x4096
-// at 16 rows 12.4 (4 x 4) against 14.0 (1 x 16).
-// Q6_K reads a batch quantized once (no per-workgroup quantization to bound), so its K ranges
-// may fill the activation LDS: Q6_K 4096x14336 at 8 rows runs 4 splits of 3584 elements.
-SmPlan sm_plan(uint32_t type, int k, int n, int m) {
+// Token tiles of 16; K split over workgroups in ranges that fit kSmActBytes (16 MT rows of
+// int8 activations); the K parts per workgroup that bring the workgroup count closest to one
+// per CU without exceeding it. From a batch quantized once a range may fill the activation LDS
+// (16 rows span K = 4096 in one split: no split-K tail); the fused form (quantization inside
+// every workgroup, of its K range) caps ranges at 1024 elements, since that redundant work
+// grows with the range. Measured on MI355X (cold weights, us): from a quantized batch,
+// Q5_K 14336x4096 at 16 rows 16.0 (1 split x 4 parts) against 18.6 (4 x 1); Q8_0 4096x4096 at
+// 16 rows 9.7 (1 x 16) against 10.6 (4 x 4). Fused, at 16 rows: Q5_K 20.7 (4 x 1) against
+// 21.2 (1 x 4), Q8_0 12.4 (4 x 4) against 14.0 (1 x 16).
+SmPlan sm_plan(uint32_t type, int k, int n, int m, bool fused) {
     SmPlan p{};
     p.mt = (m + 15) / 16;
     const int nsb = k / 256;
-    const int sb_act = kSmActBytes / (16 * p.mt) / 256;
-    const int sb_max = std::max(1, type == T_Q6_K ? sb_act : std::min(4, sb_act));
+    const int sb_act = std::max(1, kSmActBytes / (16 * p.mt) / 256);
+    const int sb_max = fused ? std::min(4, sb_act) : sb_act;
     p.splits = (nsb + sb_max - 1) / sb_max;
-    // the tuning knob "gemm_small_plan" (splits, K parts per workgroup) overrides the plan
+    // the tuning knob "gemm_small_plan" (splits, K parts per workgroup) overrides the plan,
+    // within what the activation LDS holds
     const int fs = tuning().gemm_small_splits.load(std::memory_order_relaxed);
     const int fk = tuning().gemm_small_kp.load(std::memory_order_relaxed);
-    if (fs > p.splits && fs <= nsb) p.splits = fs;
+    if (fs >= (nsb + sb_act - 1) / sb_act && fs <= nsb) p.splits = fs;
     p.kc = ((nsb + p.splits - 1) / p.splits) * 256;
     p.splits = (nsb * 256 + p.kc - 1) / p.kc;
     const int n_rg = (n + 15) / 16;
@@ -570,8 +589,8 @@ size_t sm_slices_bytes(const SmPlan& p, int n) {
 
 template <uint32_t T, int MT, bool FUSED>
 hipError_t launch_sm_k(const uint8_t* w, int k, int n, int m, const SmPlan& p, const float* x,
-                       const int8_t* qs, const float* xs, const int32_t* xb, const float* bias,
-                       float* y, float* part, int* counters, hipStream_t stream) {
+                        const int8_t* qs, const float* xs, const int32_t* xb, const float* bias,
+                        float* y, float* part, int* counters, hipStream_t stream) {
     const size_t shmem = sm_layout<T, MT>(p.kc).total;
     static bool attr_set = false;
     if (!attr_set) {
@@ -587,6 +606,7 @@ hipError_t launch_sm_k(const uint8_t* w, int k, int n, int m, const SmPlan& p, c
                        xs, xb, bias, y, part, counters);
     return hipGetLastError();
 }
+
 
 template <uint32_t T, bool FUSED>
 hipError_t launch_sm_mt(const uint8_t* w, int k, int n, int m, const SmPlan& p, const float* x,
@@ -606,7 +626,7 @@ hipError_t launch_sm(uint32_t type, const uint8_t* w, int k, int n, int m, const
                      const int8_t* qs, const float* xs, const int32_t* xb, const float* bias,
                      float* y, float* part, size_t part_bytes, hipStream_t stream) {
     if (!gemm_sm_supported(type, k, m)) return hipErrorNotSupported;
-    const SmPlan p = sm_plan(type, k, n, m);
+    const SmPlan p = sm_plan(type, k, n, m, FUSED);
     int* counters = nullptr;
     float* slices = nullptr;
     if (p.splits > 1) {
@@ -636,14 +656,19 @@ bool gemm_sm_supported(uint32_t type, int k, int m) {
             (type == T_Q6_K && k % 2048 == 0)) && k % 256 == 0 && k > 0 && m >= 1 && m <= 64;
 }
 
+// The split-K region of either plan (fused or from a quantized batch).
 size_t gemm_sm_partial_bytes(uint32_t type, int k, int n, int m) {
     if (!gemm_sm_supported(type, k, m)) return 0;
-    const SmPlan p = sm_plan(type, k, n, m);
-    return p.splits > 1 ? kSmCounterBytes + sm_slices_bytes(p, n) : 0;
+    size_t bytes = 0;
+    for (const bool fused : {false, true}) {
+        const SmPlan p = sm_plan(type, k, n, m, fused);
+        if (p.splits > 1) bytes = std::max(bytes, kSmCounterBytes + sm_slices_bytes(p, n));
+    }
+    return bytes;
 }
 
-void gemm_sm_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap) {
-    const SmPlan p = sm_plan(type, k, n, m);
+void gemm_sm_plan_name(uint32_t type, int k, int n, int m, bool fused, char* buf, size_t cap) {
+    const SmPlan p = sm_plan(type, k, n, m, fused);
     snprintf(buf, cap, "k_gemm_sm<%s,%d> splits=%d kp=%d",
              type == T_Q8_0 ? "Q8_0" : type == T_Q5_K ? "Q5_K" : type == T_Q6_K ? "Q6_K" : "Q4_K",
              p.mt, p.splits, p.kp);

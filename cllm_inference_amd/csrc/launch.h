@@ -22,6 +22,7 @@ struct Tuning {
     std::atomic<int> gemv_str_grid{0};  // workgroups of k_gemv_str (0 = one per CU)
     std::atomic<int> gemm_small{0};  // small-batch GEMM: 0 planner, 1 from 3 rows, 2 never
     std::atomic<int> gemm_small_splits{0}, gemm_small_kp{0};  // its plan (0 = planner's)
+    std::atomic<int> gemm_small_q8{0};    // fp32 batches: 0 planner, 1 quantized once first, 2 in-kernel
 };
 Tuning& tuning();
 
@@ -204,7 +205,8 @@ hipError_t launch_read_stream(const void* p, int64_t bytes, int cus, hipStream_t
 // must be zero, and every launch leaves them zero).
 bool gemm_sm_supported(uint32_t type, int k, int m);
 size_t gemm_sm_partial_bytes(uint32_t type, int k, int n, int m);
-void gemm_sm_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap);
+// fused: the plan of launch_gemm_sm_f32 (quantization inside the kernel), else launch_gemm_sm_q8's
+void gemm_sm_plan_name(uint32_t type, int k, int n, int m, bool fused, char* buf, size_t cap);
 hipError_t launch_gemm_sm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, const float* x,
                               const float* bias, float* y, float* part, size_t part_bytes,
                               hipStream_t stream);

@@ -188,18 +188,19 @@ def test_shapes_past_32_bit_offsets_take_the_int8_kernel():
 
 
 def test_small_batch_plans():
-    """8 to 32 rows of Q4_K / Q5_K weights and 8 to 64 of Q8_0 take the small-batch kernel:
-    token tiles of 16, K split over workgroups in ranges of at most 1024 elements, K parts per
-    workgroup chosen for one workgroup per CU (256 CUs when no device is present)."""
-    assert C.matmul_plan(S.Q5_K, 4096, 14336, 16) == "k_gemm_sm<Q5_K,1> splits=4 kp=1"
+    """8 to 32 rows of Q4_K / Q5_K weights and 8 to 64 of Q8_0 take the small-batch kernel on
+    a batch quantized once: token tiles of 16, K split over workgroups only where 16 rows per
+    tile of it would not fit the 64 KB of activation LDS, K parts per workgroup chosen for one
+    workgroup per CU (256 CUs when no device is present)."""
+    assert C.matmul_plan(S.Q5_K, 4096, 14336, 16) == "k_gemm_sm<Q5_K,1> splits=1 kp=4"
     # above 16 rows, matrices of 8192 output rows or more take the weight-row kernel
     assert C.matmul_plan(S.Q5_K, 4096, 14336, 32) == "k_gemmw_q4k<4,1,1,Q5_K> splits=4"
     assert C.matmul_plan(S.Q5_K, 4096, 14336, 17) == "k_gemmw_q4k<4,1,1,Q5_K> splits=4"
-    assert C.matmul_plan(S.Q5_K, 4096, 4096, 32) == "k_gemm_sm<Q5_K,2> splits=4 kp=4"
-    assert C.matmul_plan(S.Q8_0, 4096, 14336, 32) == "k_gemm_sm<Q8_0,2> splits=4 kp=1"
-    assert C.matmul_plan(S.Q8_0, 4096, 4096, 16) == "k_gemm_sm<Q8_0,1> splits=4 kp=4"
+    assert C.matmul_plan(S.Q5_K, 4096, 4096, 32) == "k_gemm_sm<Q5_K,2> splits=2 kp=8"
+    assert C.matmul_plan(S.Q8_0, 4096, 14336, 32) == "k_gemm_sm<Q8_0,2> splits=2 kp=2"
+    assert C.matmul_plan(S.Q8_0, 4096, 4096, 16) == "k_gemm_sm<Q8_0,1> splits=1 kp=16"
     assert C.matmul_plan(S.Q8_0, 4096, 4096, 64) == "k_gemm_sm<Q8_0,4> splits=4 kp=4"
-    assert C.matmul_plan(S.Q4_K, 14336, 4096, 16) == "k_gemm_sm<Q4_K,1> splits=14 kp=1"
+    assert C.matmul_plan(S.Q4_K, 14336, 4096, 16) == "k_gemm_sm<Q4_K,1> splits=4 kp=4"
     assert C.matmul_route(S.Q4_K, 4096, 14336, 4) == "gemv"
     assert C.matmul_route(S.Q4_K, 4096, 14336, 8) == "small"
     assert C.matmul_route(S.Q4_K, 4096, 14336, 64) == "mfma"

@@ -1,6 +1,7 @@
 """The small-batch route (k_gemm_sm.hip: by default 8 to 32 activation rows of Q4_K / Q5_K
-weights and 8 to 64 of Q8_0, on int8 MFMA, the weights streamed once for the batch; the kernel
-takes 1 to 64) on an MI355X, through the C ABI.
+weights, 8 to 64 of Q8_0 and 4 to 16 of Q6_K, on int8 MFMA, the weights streamed once for the
+batch, the fp32 rows quantized once first; the kernel takes 1 to 64) on an MI355X, through the
+C ABI.
 
 Bars: the check_close bars of test_gpu_parity.py against the oracle (the reference's own
 quant.cpp restated) and the fp64 evaluation of the same quantized terms; bit-identical results
@@ -135,6 +136,36 @@ def test_residual_add_on_small_route(gpu, orc):
     ref = gpu.matmul_quant_dev(xd, wd, qt, bd, k, n).cpu().numpy()
     torch.cuda.synchronize()
     assert np.array_equal(bits(y.cpu().numpy()), bits((base + ref).astype(np.float32)))
+
+
+@pytest.mark.parametrize("qt", SMALL_TYPES)
+def test_in_kernel_quantization_equals_quantized_once(gpu, orc, qt):
+    """The small-batch kernel's in-kernel quantization form (every workgroup quantizes the fp32
+    rows of its K range, bit for bit as quantize_row_q8_0) against the default form (the batch
+    quantized once, then the same kernel plan): equal bit for bit, and against the oracle."""
+    for (n, k, m, splits) in [(300, 4096, 16, 4), (77, 2816, 33, 3), (130, 1024, 5, 1),
+                              (64, 2048, 64, 2)]:
+        w = S.make_weight(qt, n, k, 60 + n + m)
+        x = S.make_activation(m, k, 61 + m, outliers=True)
+        wd, xd = _dev(w), _dev(x)
+        ys, plans = [], []
+        try:
+            gpu.tune("gemm_small", 1)
+            gpu.tune("gemm_small_plan", splits, 0)
+            for form in (1, 2):
+                gpu.tune("gemm_small_q8", form)
+                plans.append(gpu.matmul_plan(qt, k, n, m))
+                ys.append(gpu.matmul_quant_dev(xd, wd, qt, None, k, n).cpu().numpy())
+        finally:
+            for knob in ("gemm_small_q8", "gemm_small_plan", "gemm_small"):
+                gpu.tune(knob)
+        print("in-kernel quantization", S.TYPE_NAMES[qt], n, k, m, plans, flush=True)
+        assert plans[0] == plans[1], plans
+        assert np.array_equal(bits(ys[0]), bits(ys[1])), (S.TYPE_NAMES[qt], n, k, m)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
+        yo = orc.matmul(x, w, qt, None, k, n, m)
+        check_close(ys[1].reshape(m, n), yo.reshape(m, n), exact, abs_sum,
+                    f"in-kernel {S.TYPE_NAMES[qt]} {n}x{k} m{m}")
 
 
 @pytest.mark.parametrize("k, n, m", [(14336, 4096, 8), (14336, 4096, 4), (4096, 14336, 16),

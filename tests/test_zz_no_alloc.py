@@ -27,7 +27,7 @@ def _static(lib, x, w, qt, bias, k, n, y):
 
 # (type, n, k, [m of the first call, m of the second]): the MFMA route with split K (the
 # 4096 x 4096 Q4_K matrix at 512 rows plans two splits), then the small-batch route with split
-# K (32 rows: four splits), Q6_K's kernel, a 32-element block type on the MFMA then the
+# K (32 rows: two splits), Q6_K's kernel, a 32-element block type on the MFMA then the
 # small-batch route, the small-batch route then the GEMV route with a quantized batch (3
 # rows), and the fused decode GEMV (1 row)
 CASES = [
@@ -79,11 +79,23 @@ def test_static_scratch_refuses_a_second_stream_while_in_use(gpu):
     yb = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
-    with torch.cuda.stream(sa):
-        torch.cuda._sleep(50_000_000)  # a bounded spin: A's call waits behind it
-        assert _static(lib, x, w, qt, None, k, n, ya) == 0, lib.cllm_hip_last_error().decode()
-    with torch.cuda.stream(sb):
-        rc = _static(lib, x, w, qt, None, k, n, yb)
+    # A's call waits behind a bounded spin; B's call must be refused if A's stream is still
+    # busy once B's call has returned (then it was busy during B's check). Should the host
+    # have been held until A finished (the spin too short), the premise does not hold: the
+    # spin is lengthened and the pair tried again.
+    for cycles in (50_000_000, 400_000_000, 2_000_000_000):
+        with torch.cuda.stream(sa):
+            torch.cuda._sleep(cycles)
+            assert _static(lib, x, w, qt, None, k, n, ya) == 0, lib.cllm_hip_last_error().decode()
+        with torch.cuda.stream(sb):
+            rc = _static(lib, x, w, qt, None, k, n, yb)
+        a_busy = not sa.query()
+        print("busy check: spin", cycles, "rc", rc, "stream A still busy", a_busy, flush=True)
+        if a_busy:
+            break
+        assert rc == 0, (rc, lib.cllm_hip_last_error().decode())
+        torch.cuda.synchronize()
+    assert a_busy, "stream A's call finished before B's call at every spin length"
     assert rc == 6, (rc, lib.cllm_hip_last_error().decode())  # CLLM_HIP_E_BUSY
     assert "another stream" in lib.cllm_hip_last_error().decode()
     # the same stream is ordered by the stream itself
