@@ -618,11 +618,23 @@ bool use_small(uint32_t type, int k, int n, int m) {
         //   Q6_K 4096x14336, 4 / 8 / 16 rows:  22.1 / 22.3 / 23.2 against 31.5 / 34.9 / 35.7
         //   Q6_K 14336x4096, 4 / 8 / 16 rows:  21.0 / 21.3 / 22.1 against 20.9 / 29.9 / 34.2
         //   Q6_K 1024x4096,  4 / 7 / 8 / 16:   11.3 / 11.4 / 11.5 / 11.4 against 7.4 / 15.6 / 10.3 / 20.4
+        // A batch of up to 6 rows the GEMV streams in one launch stays there. MI355X, cold
+        // weights, us, streaming GEMV against this kernel:
+        //   Q6_K 4096x14336, 2 / 3 / 4 rows:      15.6 / 17.5 / 19.8 against 22.1 / 22.1 / 21.7
+        //   Q6_K 14336x4096, 4 / 6 / 7 / 8 rows:  17.5 / 20.4 / 21.9 / 23.7 against 21.2 - 21.6
+        if (m <= 6 && gemv_streams_batch(type, k, n, m)) return false;
         const bool large = (int64_t)n * k >= (int64_t(32) << 20);
         return m >= 4 && m <= 16 && (large || gemv_launch_count(type, k, m) >= 2);
     }
     if (type != T_Q8_0 && m > 16 && n >= kSmallMaxN) return false;
-    return m >= kSmallMinRows && m <= (type == T_Q8_0 ? 64 : 32);
+    // Where the GEMV streams the whole batch in one launch it keeps Q8_0 up to 8 rows, Q5_K up
+    // to 5 and Q4_K up to 7. MI355X, cold weights, us, streaming GEMV against this kernel:
+    //   Q8_0 4096x4096,  4 / 6 / 8 rows:  8.7 / 9.4 / 10.2 against 11.1 / 11.2 / 11.4
+    //   Q5_K 14336x4096, 5 / 6 / 7 rows:  16.6 / 18.0 / 19.3 against 17.6 / 17.6 / 17.6
+    //   Q4_K 14336x4096, 7 / 8 rows:      17.5 / 18.6 against 17.8 / 17.6
+    int lo = kSmallMinRows;
+    if (gemv_streams_batch(type, k, n, m)) lo = type == T_Q8_0 ? 9 : type == T_Q5_K ? 6 : 8;
+    return m >= lo && m <= (type == T_Q8_0 ? 64 : 32);
 }
 
 // The MFMA kernels walk K in 256-element steps. Crossover from the GEMV (which streams the
@@ -637,6 +649,9 @@ bool use_mfma(uint32_t type, int k, int n, int m) {
     if (!gemmw_supported(type) || !gemmw_fits(type, k, n, m)) return m >= 4 * kMfmaMinRows;
     if (m >= kMfmaMinRows) return true;
     if (type != T_Q6_K && type != T_Q4_0 && type != T_Q5_0) return false;
+    // a batch the GEMV streams in one launch stays there (Q5_0 14336x4096 at 6 rows: 19.1 us
+    // against 25.7 on the weight-row kernel)
+    if (gemv_streams_batch(type, k, n, m)) return false;
     // Q6_K, Q4_0 and Q5_0 have no small-batch kernel. Below 16 rows their GEMV reads the
     // weights once per launch (8, 4 or 2 rows each, as LDS allows), and the weight-row kernel,
     // which pads the batch to one 16-row tile, takes about the time of its 16-row call. On

@@ -1176,7 +1176,10 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_st(GemvSegs sg, int64_t row_by
 // fixed share per wave would leave the workgroup waiting on its slowest waves: the CU does not
 // serve its SIMDs' memory requests evenly (per-wave timestamps on the Q4_K 14336 x 4096 step:
 // the last four waves of a workgroup ended 2.5 us after the first four).
-template <uint32_t T, int WV, int XR, bool NORM, bool FUSED>
+//
+// MR > 1: that many activation rows (a small batch) against the same stream, each lane keeping
+// MR sums and reading the rows' slices of its unit from LDS per item (XR = 0).
+template <uint32_t T, int WV, int XR, bool NORM, bool FUSED, int MR = 1>
 __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_bytes, int k, int n,
                                                       int rpw, const int8_t* __restrict__ qs,
                                                       const float* __restrict__ xs,
@@ -1194,9 +1197,10 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_b
     const int units = k / Tr::UNIT;
     const int iters = (units + 63) / 64;
     const int nblk = units / Tr::UNITS_PER_BLK;
+    static_assert(MR == 1 || (XR == 0 && !NORM), "several rows: slices read per unit, no RMSNorm");
     const int r0 = blockIdx.x * rpw;
     const int r_end = min(n, r0 + rpw);
-    uint8_t* slot = lds + align16(act_lds_bytes<T>(1, k)) + (size_t)wave * SLOT;
+    uint8_t* slot = lds + align16(act_lds_bytes<T>(MR, k)) + (size_t)wave * SLOT;
 
     // First byte of item `it` of row jr.
     auto item_first = [&](int jr, int it) {
@@ -1235,9 +1239,9 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_b
         return r0 + c < r_end ? r0 + c : -1;
     };
 
-    const ActLds a = act_layout<T, 1>(lds, k);
-    StageQuant<T, 1, NORM> sq{x_f32, k, {}};
-    StageCopy<T, 1> sc{qs, xs, xb, k, {}, {}, {}};
+    const ActLds a = act_layout<T, MR>(lds, k);
+    StageQuant<T, MR, NORM> sq{x_f32, k, {}};
+    StageCopy<T, MR> sc{qs, xs, xb, k, {}, {}, {}};
     __shared__ float norm_part[16];
     if constexpr (NORM) {
         sq.nw = sg.norm_w;
@@ -1273,7 +1277,9 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_b
 
     int it = 0;
     int nrow = grab();  // the row after the current one
-    float acc = 0.0f;
+    float acc[MR];
+#pragma unroll
+    for (int t = 0; t < MR; ++t) acc[t] = 0.0f;
     while (row >= 0) {
         const int u = min(lane + 64 * it, units - 1);
         const int mis = to_slot(row, it);
@@ -1288,34 +1294,42 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_b
             const typename Tr::Raw raw =
                 Tr::load_lds(slot, mis + (uc / Tr::UNITS_PER_BLK) * Tr::BLK_BYTES, uc);
             const typename Tr::W w = Tr::wdec(raw, u);
-            float v;
+            float v[MR];
             if constexpr (XR > 0) {
                 typename Tr::X x = xr[0];
 #pragma unroll
                 for (int i = 1; i < XR; ++i)
                     if (it == i) x = xr[i];
-                v = Tr::fin(w, x, acc, u);
+                v[0] = Tr::fin(w, x, acc[0], u);
             } else {
-                v = Tr::fin(w, Tr::x_of(a, 0, u), acc, u);
+#pragma unroll
+                for (int t = 0; t < MR; ++t) v[t] = Tr::fin(w, Tr::x_of(a, t, u), acc[t], u);
             }
-            acc = lane + 64 * it < units ? v : acc;
+#pragma unroll
+            for (int t = 0; t < MR; ++t) acc[t] = lane + 64 * it < units ? v[t] : acc[t];
         }
         if (last_item) {
             const int s = seg_of(sg, row);
             const int j = row - seg_pick(s, sg.start[0], sg.start[1], sg.start[2]);
             const float* bias = seg_pick(s, sg.bias[0], sg.bias[1], sg.bias[2]);
             float* y = seg_pick(s, sg.y[0], sg.y[1], sg.y[2]);
-            float v = wave_sum63(acc);  // the same additions as wave_sum's, in lane 63
-            if (bias) v += ((const __attribute__((address_space(4))) float*)bias)[j];
-            // the residual add as an atomic (one wave owns the row, so it is the plain sum
-            // y + v): a load of y here would wait behind the next item's loads
-            if (lane == 63) {
-                if (accumulate)
-                    __hip_atomic_fetch_add(y + j, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else
-                    y[j] = v;
+            const int ny = seg_pick(s, sg.rows[0], sg.rows[1], sg.rows[2]);
+            const float bj = bias ? ((const __attribute__((address_space(4))) float*)bias)[j] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < MR; ++t) {
+                float v = wave_sum63(acc[t]);  // the same additions as wave_sum's, in lane 63
+                if (bias) v += bj;
+                // the residual add as an atomic (one wave owns the row, so it is the plain sum
+                // y + v): a load of y here would wait behind the next item's loads
+                if (lane == 63) {
+                    float* yp = y + (size_t)t * ny + j;
+                    if (accumulate)
+                        __hip_atomic_fetch_add(yp, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else
+                        *yp = v;
+                }
+                acc[t] = 0.0f;
             }
-            acc = 0.0f;
             row = nrow;
             nrow = nnrow;
             it = 0;
@@ -1420,24 +1434,27 @@ static hipError_t launch_st(const GemvSegs& sg, int k, int n, const int8_t* qs, 
 // The streaming kernel: 16-wave workgroups, at most one per CU (the LDS request is at least
 // kStrMinLds, more than half a CU's 160 KB), the rows split evenly over them.
 constexpr int kStrWaves = 16;
+constexpr int kStrMaxRows = 8;  // activation rows of one streaming launch
 constexpr size_t kStrMinLds = 96 * 1024;
 
 template <uint32_t T>
-__host__ constexpr size_t str_lds_bytes(int k) {
+__host__ constexpr size_t str_lds_bytes(int k, int mr = 1) {
     using Tr = typename TraitsOf<T>::type;
-    return align16(act_lds_bytes<T>(1, k)) + (size_t)kStrWaves * slot_bytes<Tr>();
+    return align16(act_lds_bytes<T>(mr, k)) + (size_t)kStrWaves * slot_bytes<Tr>();
 }
 
-template <uint32_t T, int XR, bool NORM, bool FUSED>
+template <uint32_t T, int XR, bool NORM, bool FUSED, int MR = 1>
 static hipError_t launch_str_k(const GemvSegs& sg, int k, int n, const int8_t* qs, const float* xs,
                                const int32_t* xb, const float* x_f32, int accumulate,
                                hipStream_t stream) {
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * (int64_t)block_bytes(T);
-    const size_t shmem = std::max(str_lds_bytes<T>(k), kStrMinLds);
+    const size_t shmem = std::max(str_lds_bytes<T>(k, MR), kStrMinLds);
+    // the attribute covers the largest LDS request this instantiation makes (k up to what
+    // str_fits admits)
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)k_gemv_str<T, kStrWaves, XR, NORM, FUSED>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
+        const hipError_t e = hipFuncSetAttribute((const void*)k_gemv_str<T, kStrWaves, XR, NORM, FUSED, MR>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
@@ -1448,7 +1465,7 @@ static hipError_t launch_str_k(const GemvSegs& sg, int k, int n, const int8_t* q
     if (force > 0) grid = force;
     const int rpw = (int)((n + grid - 1) / grid);
     grid = (n + rpw - 1) / rpw;
-    hipLaunchKernelGGL((k_gemv_str<T, kStrWaves, XR, NORM, FUSED>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((k_gemv_str<T, kStrWaves, XR, NORM, FUSED, MR>), dim3((unsigned)grid),
                        dim3(64 * kStrWaves), shmem, stream, sg, row_bytes, k, n, rpw, qs, xs, xb,
                        x_f32, accumulate);
     return hipGetLastError();
@@ -1479,7 +1496,18 @@ static hipError_t launch_str(const GemvSegs& sg, int k, int n, const int8_t* qs,
 }
 
 template <uint32_t T>
-static bool str_fits(int k) { return str_lds_bytes<T>(k) <= 150 * 1024; }
+static bool str_fits(int k, int mr = 1) { return str_lds_bytes<T>(k, mr) <= 150 * 1024; }
+
+// A small batch (2 to kStrMaxRows rows) on the streaming kernel, from fp32 rows or a
+// quantized batch.
+template <uint32_t T, int MR>
+static hipError_t launch_str_rows(const GemvSegs& sg, int k, int n, const int8_t* qs,
+                                  const float* xs, const int32_t* xb, const float* x_f32,
+                                  int accumulate, hipStream_t stream) {
+    if (x_f32 != nullptr)
+        return launch_str_k<T, 0, false, true, MR>(sg, k, n, qs, xs, xb, x_f32, accumulate, stream);
+    return launch_str_k<T, 0, false, false, MR>(sg, k, n, qs, xs, xb, x_f32, accumulate, stream);
+}
 
 // The streaming kernel takes one activation row over a stream of at least 4 MiB; shorter
 // streams fill too few workgroups of 16 rows each and keep the register ring (MI355X, cold
@@ -1599,12 +1627,42 @@ static int next_launch_rows(int left, int lim) {
     return mr;
 }
 
-// Runs every activation row through the GEMV, MR rows per launch. With x_f32 set, the rows
-// are fp32 and each launch quantizes its rows itself (qs / scales / bsums unused).
+// 2 to 8 activation rows over a long stream run as one launch of the streaming kernel with
+// that many sums per lane (MI355X, cold HBM, us, against the register ring k_gemv: Q5_K
+// 14336x4096 at 2 / 4 rows 11.0 / 15.6 against 13.1 / 17.7, Q8_0 4096x4096 6.1 / 8.6 against
+// 7.6 / 10.1, Q6_K 4096x14336 at 2 rows 15.1 against 20.1; results bit for bit the same).
+template <uint32_t T>
+static bool str_whole_batch(int k, int n, int m) {
+    if (m < 2 || m > kStrMaxRows || !str_fits<T>(k, m)) return false;
+    const int kind = tuning().gemv_kind.load(std::memory_order_relaxed);
+    return (kind == 0 && use_str<T>(k, n)) || kind == 3;
+}
+
+template <uint32_t T>
+static hipError_t launch_str_batch(const GemvSegs& sg, int k, int n, int m, const int8_t* qs,
+                                   const float* xs, const int32_t* xb, const float* x_f32,
+                                   int acc, hipStream_t stream) {
+    switch (m) {
+        case 2: return launch_str_rows<T, 2>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 3: return launch_str_rows<T, 3>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 4: return launch_str_rows<T, 4>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 5: return launch_str_rows<T, 5>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 6: return launch_str_rows<T, 6>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 7: return launch_str_rows<T, 7>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        case 8: return launch_str_rows<T, 8>(sg, k, n, qs, xs, xb, x_f32, acc, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// Runs every activation row through the GEMV, MR rows per launch (or all of a small batch in
+// one streaming launch). With x_f32 set, the rows are fp32 and each launch quantizes its rows
+// itself (qs / scales / bsums unused).
 template <uint32_t T, bool SW = false>
 static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const int8_t* qs,
                                 const float* scales, const int32_t* bsums, const float* x_f32,
                                 int acc, hipStream_t stream) {
+    if (!SW && !sg0.norm_w && str_whole_batch<T>(k, n, m))
+        return launch_str_batch<T>(sg0, k, n, m, qs, scales, bsums, x_f32, acc, stream);
     const int nb = k / 32;
     const int cap = max_rows_per_launch<T>(k);
     int t = 0;
@@ -1622,7 +1680,8 @@ static hipError_t gemv_all_rows(const GemvSegs& sg0, int k, int n, int m, const 
     return hipSuccess;
 }
 
-// Launches gemv_all_rows makes for m activation rows (each streams the whole matrix).
+// Launches gemv_all_rows makes for m activation rows (each streams the whole matrix) when it
+// takes the register ring (k_gemv).
 template <uint32_t T>
 static int launches_for(int k, int m) {
     const int lim = max_rows_per_launch<T>(k);
@@ -1635,6 +1694,10 @@ static int launches_for(int k, int m) {
 // taken as 16-byte aligned.
 template <uint32_t T>
 static void plan_rows(const char* tname, int k, int n, int m, char* buf, size_t cap) {
+    if (str_whole_batch<T>(k, n, m)) {
+        snprintf(buf, cap, "k_gemv_str<%s,%d> launches=1", tname, m);
+        return;
+    }
     const int mr0 = m > 0 ? next_launch_rows(m, max_rows_per_launch<T>(k)) : 0;
     const int launches = launches_for<T>(k, m);
     const int kind = tuning().gemv_kind.load(std::memory_order_relaxed);
@@ -1647,6 +1710,18 @@ static void plan_rows(const char* tname, int k, int n, int m, char* buf, size_t 
                             act_lds_bytes<T>(1, k) <= 64 * 1024)))
         name = "k_gemv_st";
     snprintf(buf, cap, "%s<%s,%d> launches=%d", name, tname, mr0, launches);
+}
+
+bool gemv_streams_batch(uint32_t type, int k, int n, int m) {
+    switch (type) {
+        case T_Q4_K: return str_whole_batch<T_Q4_K>(k, n, m);
+        case T_Q5_K: return str_whole_batch<T_Q5_K>(k, n, m);
+        case T_Q6_K: return str_whole_batch<T_Q6_K>(k, n, m);
+        case T_Q8_0: return str_whole_batch<T_Q8_0>(k, n, m);
+        case T_Q4_0: return str_whole_batch<T_Q4_0>(k, n, m);
+        case T_Q5_0: return str_whole_batch<T_Q5_0>(k, n, m);
+        default: return false;
+    }
 }
 
 int gemv_launch_count(uint32_t type, int k, int m) {

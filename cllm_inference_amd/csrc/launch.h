@@ -52,8 +52,11 @@ hipError_t launch_q8_to_w(const int8_t* qs, const float* scales, const int32_t* 
 // The decode kernel launch_gemv runs first for m activation rows of a k x n matrix ("none"
 // for a type with no vec_dot kernel): name<type,rows per launch> launches=count.
 void gemv_plan_name(uint32_t type, int k, int n, int m, char* buf, size_t cap);
-// Launches the multi-row GEMV makes for m activation rows (each reads the whole matrix).
+// Launches the multi-row GEMV makes for m activation rows (each reads the whole matrix) on
+// its register-ring kernel.
 int gemv_launch_count(uint32_t type, int k, int m);
+// Whether the GEMV takes all m rows (2 to 8) in one launch of its streaming kernel.
+bool gemv_streams_batch(uint32_t type, int k, int n, int m);
 
 // y[t, j] = vec_dot(W row j, activation row t) (+ bias[j]) for t < m, j < n.
 // Activation rows are Q8_0: qs[t * k], scales / bsums[t * k / 32]. Any m >= 1.

@@ -84,17 +84,18 @@ def test_no_device_is_reported_not_faked():
 
 def test_decode_plans():
     """One activation row over a weight stream of at least 4 MiB runs the streaming kernel
-    (k_gemv_str, one workgroup per CU), shorter streams the register-ring k_gemv; several rows
-    run in launches of up to 8 (below the small-batch route's 4 rows, or for types it does not
-    have). The tuning knob forces either kernel."""
+    (k_gemv_str, one workgroup per CU), shorter streams the register-ring k_gemv; 2 to 8 rows
+    run as one streaming launch on the long streams, else in register-ring launches of up to 8.
+    The tuning knob forces either kernel."""
     assert C.matmul_plan(S.Q4_K, 4096, 14336, 1) == "k_gemv_str<Q4_K,1> launches=1"
     assert C.matmul_plan(S.Q6_K, 4096, 128256, 1) == "k_gemv_str<Q6_K,1> launches=1"
     assert C.matmul_plan(S.Q6_K, 14336, 4096, 1) == "k_gemv_str<Q6_K,1> launches=1"
     assert C.matmul_plan(S.Q8_0, 896, 4864, 1) == "k_gemv_str<Q8_0,1> launches=1"
     assert C.matmul_plan(S.Q4_K, 4096, 1024, 1) == "k_gemv<Q4_K,1> launches=1"
     assert C.matmul_plan(S.Q4_0, 4096, 4096, 13) == "k_gemv<Q4_0,8> launches=3"
-    assert C.matmul_plan(S.Q4_K, 4096, 14336, 3) == "k_gemv<Q4_K,2> launches=2"
-    assert C.matmul_plan(S.Q4_K, 4096, 14336, 5) == "k_gemv<Q4_K,4> launches=2"
+    assert C.matmul_plan(S.Q4_K, 4096, 14336, 3) == "k_gemv_str<Q4_K,3> launches=1"
+    assert C.matmul_plan(S.Q4_K, 4096, 14336, 5) == "k_gemv_str<Q4_K,5> launches=1"
+    assert C.matmul_plan(S.Q4_K, 4096, 1024, 3) == "k_gemv<Q4_K,2> launches=2"
     try:
         C.tune("gemv_kernel", 1)
         assert C.matmul_plan(S.Q6_K, 4096, 128256, 1) == "k_gemv<Q6_K,1> launches=1"
@@ -107,17 +108,19 @@ def test_decode_plans():
 
 
 def test_mid_batch_routes():
-    """Below 16 rows, Q4_0 / Q5_0 (no small-batch kernel) take the weight-row kernel once the
-    GEMV would read the weights three times on matrices of 32 M weights or more, four times on
-    smaller ones, or from 8 rows on the large ones. Q6_K takes the small-batch kernel from 4 to
-    16 rows where the GEMV would need two launches or more, or on matrices of 32 M weights or
-    more; the weight-row kernel beyond 16 rows. Q4_K / Q8_0 keep the GEMV below 8 rows."""
+    """Below 16 rows, Q4_0 / Q5_0 (no small-batch kernel) keep the GEMV while it streams the
+    batch in one launch (up to 8 rows), else take the weight-row kernel once the GEMV would read
+    the weights three times on matrices of 32 M weights or more, four times on smaller ones, or
+    from 8 rows on the large ones. Q6_K keeps a streamed batch of up to 6 rows, else takes the
+    small-batch kernel from 4 to 16 rows where the GEMV would need two launches or more, or on
+    matrices of 32 M weights or more; the weight-row kernel beyond 16 rows. Q4_K keeps the GEMV
+    below 8 rows, Q8_0 up to 8."""
     # (type, in_dim, out_dim, rows that go to the MFMA route among 1..16, to the small route)
     cases = [
-        (S.Q6_K, 4096, 14336, set(), set(range(4, 17))),
-        (S.Q6_K, 14336, 4096, set(), set(range(4, 17))),
+        (S.Q6_K, 4096, 14336, set(), set(range(7, 17))),
+        (S.Q6_K, 14336, 4096, set(), set(range(5, 17))),
         (S.Q6_K, 4096, 1024, set(), {5, 6, 7} | set(range(9, 17))),
-        (S.Q4_0, 4096, 14336, set(range(7, 17)), set()),
+        (S.Q4_0, 4096, 14336, set(range(9, 17)), set()),
         (S.Q5_0, 4096, 4096, {15, 16}, set()),
     ]
     for t, k, n, want_mfma, want_small in cases:
@@ -134,6 +137,8 @@ def test_mid_batch_routes():
     for m in range(1, 8):
         assert C.matmul_route(S.Q4_K, 4096, 14336, m) == "gemv"
         assert C.matmul_route(S.Q8_0, 4096, 4096, m) == "gemv"
+    assert C.matmul_route(S.Q8_0, 4096, 4096, 8) == "gemv"
+    assert C.matmul_route(S.Q5_K, 4096, 14336, 6) == "small"
 
 
 def test_prefill_plans():

@@ -101,13 +101,15 @@ def test_mfma_partial_tiles_and_bias(gpu, orc, qt):
                                          (S.Q5_0, 4096, 4096, 15), (S.Q6_K, 4096, 1024, 15)])
 def test_mid_batches_on_weight_row_kernel(gpu, orc, qt, k, n, m, gemm_kernel):
     """Batches below 16 rows on the weight-row kernel (one partly filled 16-row tile) on
-    full-size matrices, every output against the oracle: the default route of Q4_0 / Q5_0
-    there; Q6_K's (which takes the small-batch kernel there) with that route switched off."""
+    full-size matrices, every output against the oracle: the route Q4_0 / Q5_0 take there
+    when the GEMV runs its register ring (the streaming GEMV, which takes up to 8 rows in one
+    launch, turned off); Q6_K's with the small-batch route also switched off."""
     if gemm_kernel != "default":
         pytest.skip("the default route only")
     w = S.make_weight(qt, n, k, 11 + m)
     x = S.make_activation(m, k, 12 + m, outliers=True)
     try:
+        gpu.tune("gemv_kernel", 1)
         if qt == S.Q6_K:
             gpu.tune("gemm_small", 2)
         assert gpu.matmul_route(qt, k, n, m) == "mfma"
@@ -115,6 +117,7 @@ def test_mid_batches_on_weight_row_kernel(gpu, orc, qt, k, n, m, gemm_kernel):
         y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, None, k, n).cpu().numpy()
     finally:
         gpu.tune("gemm_small")
+        gpu.tune("gemv_kernel")
     yo = orc.matmul(x, w, qt, None, k, n, m, threads=8)
     exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
     check_close(y, yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")

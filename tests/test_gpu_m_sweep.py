@@ -21,12 +21,12 @@ pytestmark = pytest.mark.gpu
 # the default plan of each point (cllm_hip_matmul_plan), as bench.py reports it
 PLANS = {
     ("q5_k", 1): "k_gemv_str<Q5_K,1> launches=1",
-    ("q5_k", 4): "k_gemv<Q5_K,4> launches=1",
+    ("q5_k", 4): "k_gemv_str<Q5_K,4> launches=1",
     ("q5_k", 16): "k_gemm_sm<Q5_K,1> splits=1 kp=4",
     ("q5_k", 64): "k_gemmw_q4k<4,1,2,Q5_K> splits=4",
     ("q5_k", 256): "k_gemmw_q4k<4,1,2,Q5_K> splits=1",
     ("q8_0", 1): "k_gemv_str<Q8_0,1> launches=1",
-    ("q8_0", 4): "k_gemv<Q8_0,4> launches=1",
+    ("q8_0", 4): "k_gemv_str<Q8_0,4> launches=1",
     ("q8_0", 16): "k_gemm_sm<Q8_0,1> splits=1 kp=16",
     ("q8_0", 64): "k_gemm_sm<Q8_0,4> splits=4 kp=4",
     ("q8_0", 256): "k_gemmw_b32<Q8_0,4,2> splits=4",

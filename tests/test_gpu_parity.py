@@ -211,6 +211,52 @@ def test_streaming_decode_row_handout(gpu, orc, qt, n, k):
     check_close(ring[0], orc.matmul(x, w, qt, None, k, n, 1), exact, abs_sum, "row handout")
 
 
+@pytest.mark.parametrize("qt", TYPES)
+def test_streaming_batch_equals_register_ring(gpu, orc, qt):
+    """2 to 8 activation rows in one launch of the streaming kernel (each lane keeping one sum
+    per row) against the register-ring kernel's launches of 1, 2, 4 or 8 rows: bit for bit,
+    through the fp32 and quantized-batch entries, with a bias, over two matrices in one launch,
+    and on grids that leave workgroups short of rows; and against the oracle."""
+    import torch
+    k = 1024 if S.BLOCK[qt] == 32 else 2048
+    n, n2 = 333, 130
+    w, w2 = S.make_weight(qt, n, k, 71), S.make_weight(qt, n2, k, 72)
+    bias = np.random.default_rng(73).standard_normal(n).astype(np.float32)
+    wd, w2d, bd = _dev(w), _dev(w2), _dev(bias)
+    for m in (2, 3, 5, 8):
+        x = S.make_activation(m, k, 74 + m, outliers=True)
+        xd = _dev(x)
+        qs, sc, bs = gpu.quantize_q8_0_dev(xd)
+
+        def run():
+            y = gpu.matmul_quant_dev(xd, wd, qt, bd, k, n).cpu().numpy()
+            yq = gpu.gemv_q8_dev(wd, qt, k, n, qs, sc, bs, bd).cpu().numpy()
+            ym = [t.cpu().numpy() for t in gpu.gemv_q8_multi_dev([wd, w2d], qt, k, [n, n2], qs, sc, bs)]
+            torch.cuda.synchronize()
+            return [y, yq] + ym
+
+        try:
+            gpu.tune("gemm_small", 2)
+            gpu.tune("gemv_kernel", 1)
+            assert gpu.matmul_route(qt, k, n, m) == "gemv"
+            ring = run()
+            gpu.tune("gemv_kernel", 3)
+            plan = gpu.matmul_plan(qt, k, n, m)
+            assert plan == f"k_gemv_str<{S.TYPE_NAMES[qt]},{m}> launches=1", plan
+            for grid in (0, 7, 61):
+                print("streaming batch", S.TYPE_NAMES[qt], n, k, "m", m, "grid", grid, flush=True)
+                gpu.tune("gemv_str_grid", grid)
+                got = run()
+                for a, b, what in zip(got, ring, ("fused", "quantized", "multi 0", "multi 1")):
+                    assert np.array_equal(bits(a), bits(b)), (what, m, grid, np.flatnonzero(bits(a) != bits(b))[:8])
+        finally:
+            for knob in ("gemv_str_grid", "gemv_kernel", "gemm_small"):
+                gpu.tune(knob)
+        exact, abs_sum = orc.matmul_f64(x, w, qt, bias, k, n, m)
+        check_close(got[0].reshape(m, n), orc.matmul(x, w, qt, bias, k, n, m).reshape(m, n), exact,
+                    abs_sum, f"streaming batch {S.TYPE_NAMES[qt]} m{m}")
+
+
 @pytest.mark.parametrize("m", [1, 2, 16])
 def test_fused_quantization_at_rounding_boundaries(gpu, orc, m):
     """Every quantized block of the input holds a value whose rounding a contracted
