@@ -618,22 +618,23 @@ bool use_small(uint32_t type, int k, int n, int m) {
         //   Q6_K 4096x14336, 4 / 8 / 16 rows:  22.1 / 22.3 / 23.2 against 31.5 / 34.9 / 35.7
         //   Q6_K 14336x4096, 4 / 8 / 16 rows:  21.0 / 21.3 / 22.1 against 20.9 / 29.9 / 34.2
         //   Q6_K 1024x4096,  4 / 7 / 8 / 16:   11.3 / 11.4 / 11.5 / 11.4 against 7.4 / 15.6 / 10.3 / 20.4
-        // A batch of up to 6 rows the GEMV streams in one launch stays there. MI355X, cold
-        // weights, us, streaming GEMV against this kernel:
-        //   Q6_K 4096x14336, 2 / 3 / 4 rows:      15.6 / 17.5 / 19.8 against 22.1 / 22.1 / 21.7
-        //   Q6_K 14336x4096, 4 / 6 / 7 / 8 rows:  17.5 / 20.4 / 21.9 / 23.7 against 21.2 - 21.6
-        if (m <= 6 && gemv_streams_batch(type, k, n, m)) return false;
+        // A batch of up to 5 rows the GEMV streams in one launch stays there. MI355X, cold
+        // weights, us, streaming GEMV (quantizing in-kernel) against this kernel:
+        //   Q6_K 4096x14336, 2 / 3 / 4 rows:   15.6 / 15.3 / 17.3 against 22.1 / 22.1 / 21.7
+        //   Q6_K 14336x4096, 5 / 6 rows:       19.2 / 21.8 against 21.4 / 21.3
+        if (m <= 5 && gemv_streams_batch(type, k, n, m)) return false;
         const bool large = (int64_t)n * k >= (int64_t(32) << 20);
         return m >= 4 && m <= 16 && (large || gemv_launch_count(type, k, m) >= 2);
     }
     if (type != T_Q8_0 && m > 16 && n >= kSmallMaxN) return false;
     // Where the GEMV streams the whole batch in one launch it keeps Q8_0 up to 8 rows, Q5_K up
-    // to 5 and Q4_K up to 7. MI355X, cold weights, us, streaming GEMV against this kernel:
-    //   Q8_0 4096x4096,  4 / 6 / 8 rows:  8.7 / 9.4 / 10.2 against 11.1 / 11.2 / 11.4
-    //   Q5_K 14336x4096, 5 / 6 / 7 rows:  16.6 / 18.0 / 19.3 against 17.6 / 17.6 / 17.6
-    //   Q4_K 14336x4096, 7 / 8 rows:      17.5 / 18.6 against 17.8 / 17.6
+    // to 6 and Q4_K up to 7. MI355X, cold weights, us, streaming GEMV (in-kernel quantization
+    // up to 7 rows) against this kernel:
+    //   Q8_0 4096x4096,  4 / 6 / 8 rows:  7.7 / 9.1 / 10.6 against 11.1 / 11.2 / 11.4
+    //   Q5_K 14336x4096, 5 / 6 / 7 rows:  16.3 / ~16.9 / ~18.3 against 17.6 / 17.6 / 17.6
+    //   Q4_K 14336x4096, 7 / 8 rows:      17.2 / 18.6 against 17.8 / 17.6
     int lo = kSmallMinRows;
-    if (gemv_streams_batch(type, k, n, m)) lo = type == T_Q8_0 ? 9 : type == T_Q5_K ? 6 : 8;
+    if (gemv_streams_batch(type, k, n, m)) lo = type == T_Q8_0 ? 9 : type == T_Q5_K ? 7 : 8;
     return m >= lo && m <= (type == T_Q8_0 ? 64 : 32);
 }
 
@@ -770,9 +771,22 @@ hipError_t run_gemm_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
 // workgroup re-quantizes all of its rows and that redundant work grows with the row count.
 constexpr int kFusedMaxRows = 2;
 
+// Whether the GEMV route quantizes inside its kernel: up to kFusedMaxRows rows, and up to 7
+// rows of a batch the streaming kernel takes in one launch, where one workgroup per CU
+// quantizes the batch (the tuning knob "gemv_fused_rows" sets that bound; 0 = 7). MI355X,
+// cold weights, graph-timed us, in-kernel against quantized once first (bit for bit alike):
+//   Q5_K 14336x4096, 3 / 4 / 5 rows:      13.2 / 14.3 / 16.3 against 15.0 / 16.3 / 17.6
+//   Q8_0 4096x4096, 3 / 4 / 7 / 8 rows:   6.8 / 7.7 / 9.7 / 10.4 against 8.3 / 8.9 / 10.1 / 10.6
+//   Q4_0 4096x4096, 4 / 7 / 8 rows:       7.1 / 9.4 / 10.3 against 8.1 / 9.6 / 10.0
+bool gemv_fused(uint32_t type, int k, int n, int m) {
+    if (m <= kFusedMaxRows) return true;
+    const int knob = tuning().gemv_fused_rows.load(std::memory_order_relaxed);
+    return m <= (knob > 0 ? knob : 7) && gemv_streams_batch(type, k, n, m);
+}
+
 bool needs_workspace(uint32_t type, int k, int n, int m) {
     if (!has_kernel(type)) return false;  // the float-dot kernels read fp32 rows directly
-    return use_mfma(type, k, n, m) || use_small(type, k, n, m) || m > kFusedMaxRows;
+    return use_mfma(type, k, n, m) || use_small(type, k, n, m) || !gemv_fused(type, k, n, m);
 }
 
 // GEMV route on fp32 activation rows.
@@ -781,7 +795,7 @@ hipError_t run_gemv_f32(uint32_t type, const uint8_t* w, int k, int n, int m, co
                         bool accumulate = false) {
     if (!accumulate && use_small(type, k, n, m))
         return run_small_f32(type, w, k, n, m, x, bias, y, ws, stream);
-    if (m <= kFusedMaxRows)
+    if (gemv_fused(type, k, n, m))
         return launch_gemv_fused(type, w, k, n, m, x, bias, y, stream, accumulate);
     hipError_t e = launch_quantize_q8_0(x, (int64_t)m * k / 32, ws.qs, ws.sc, ws.bs, stream);
     if (e != hipSuccess) return e;
@@ -1775,6 +1789,9 @@ int cllm_hip_tune(const char* knob, const int* values, int n_values) {
     } else if (std::strcmp(knob, "gemm_small") == 0) {
         if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemm_small is 0, 1 or 2");
         t.gemm_small.store(v(0));
+    } else if (std::strcmp(knob, "gemv_fused_rows") == 0) {
+        if (v(0) < 0 || v(0) > 8) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemv_fused_rows is 0 to 8");
+        t.gemv_fused_rows.store(v(0));
     } else if (std::strcmp(knob, "gemm_small_q8") == 0) {
         if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemm_small_q8 is 0, 1 or 2");
         t.gemm_small_q8.store(v(0));

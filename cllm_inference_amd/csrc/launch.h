@@ -23,6 +23,7 @@ struct Tuning {
     std::atomic<int> gemm_small{0};  // small-batch GEMM: 0 planner, 1 from 3 rows, 2 never
     std::atomic<int> gemm_small_splits{0}, gemm_small_kp{0};  // its plan (0 = planner's)
     std::atomic<int> gemm_small_q8{0};    // fp32 batches: 0 planner, 1 quantized once first, 2 in-kernel
+    std::atomic<int> gemv_fused_rows{0};  // streamed GEMV batches quantized in-kernel up to this many rows
 };
 Tuning& tuning();
 

@@ -111,13 +111,13 @@ def test_mid_batch_routes():
     """Below 16 rows, Q4_0 / Q5_0 (no small-batch kernel) keep the GEMV while it streams the
     batch in one launch (up to 8 rows), else take the weight-row kernel once the GEMV would read
     the weights three times on matrices of 32 M weights or more, four times on smaller ones, or
-    from 8 rows on the large ones. Q6_K keeps a streamed batch of up to 6 rows, else takes the
+    from 8 rows on the large ones. Q6_K keeps a streamed batch of up to 5 rows, else takes the
     small-batch kernel from 4 to 16 rows where the GEMV would need two launches or more, or on
     matrices of 32 M weights or more; the weight-row kernel beyond 16 rows. Q4_K keeps the GEMV
-    below 8 rows, Q8_0 up to 8."""
+    below 8 rows, Q5_K up to 6, Q8_0 up to 8."""
     # (type, in_dim, out_dim, rows that go to the MFMA route among 1..16, to the small route)
     cases = [
-        (S.Q6_K, 4096, 14336, set(), set(range(7, 17))),
+        (S.Q6_K, 4096, 14336, set(), set(range(6, 17))),
         (S.Q6_K, 14336, 4096, set(), set(range(5, 17))),
         (S.Q6_K, 4096, 1024, set(), {5, 6, 7} | set(range(9, 17))),
         (S.Q4_0, 4096, 14336, set(range(9, 17)), set()),
@@ -138,7 +138,8 @@ def test_mid_batch_routes():
         assert C.matmul_route(S.Q4_K, 4096, 14336, m) == "gemv"
         assert C.matmul_route(S.Q8_0, 4096, 4096, m) == "gemv"
     assert C.matmul_route(S.Q8_0, 4096, 4096, 8) == "gemv"
-    assert C.matmul_route(S.Q5_K, 4096, 14336, 6) == "small"
+    assert C.matmul_route(S.Q5_K, 4096, 14336, 6) == "gemv"
+    assert C.matmul_route(S.Q5_K, 4096, 14336, 7) == "small"
 
 
 def test_prefill_plans():
