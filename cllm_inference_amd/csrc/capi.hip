@@ -626,6 +626,17 @@ bool use_small(uint32_t type, int k, int n, int m) {
         const bool large = (int64_t)n * k >= (int64_t(32) << 20);
         return m >= 4 && m <= 16 && (large || gemv_launch_count(type, k, m) >= 2);
     }
+    if (type == T_Q4_0 || type == T_Q5_0) {
+        // from 8 rows (9 where the GEMV streams the batch in one launch), against the weight-row
+        // kernel. MI355X, cold weights, us, this kernel against the previous route:
+        //   Q4_0 14336x4096, 9 / 16 / 32 / 64 rows:  17.5 / 17.8 / 26.6 / 42.6 against 23.8 / 24.2 / 25.5 / 44.8
+        //   Q5_0 14336x4096, 9 / 16 / 32 / 64 rows:  19.0 / 19.3 / 27.8 / 43.7 against 25.8 / 26.3 / 27.6 / 47.0
+        //   Q4_0 4096x4096,  9 / 16 / 32 / 64 rows:  10.4 / 10.6 / 14.2 / 18.6 against 17.5 / 19.8 / 20.5 / 27.5
+        //   Q4_0 4096x14336, 8 / 16 / 32 / 64 rows:  17.6 / 17.9 / 28.9 / 56.8 against 30.1 / 30.7 / 31.9 / 43.5
+        if (m < (gemv_streams_batch(type, k, n, m) ? 9 : 8)) return false;
+        if (k > 4096) return m <= 32;
+        return n < kSmallMaxN || m <= 16 || m > 32;
+    }
     if (type != T_Q8_0 && m > 16 && n >= kSmallMaxN) return false;
     // Where the GEMV streams the whole batch in one launch it keeps Q8_0 up to 8 rows, Q5_K up
     // to 6 and Q4_K up to 7. MI355X, cold weights, us, streaming GEMV (in-kernel quantization
@@ -723,12 +734,13 @@ hipError_t run_gemm(uint32_t type, const uint8_t* w, int k, int n, int m, const 
 // against in the kernel (the quantizing launch included):
 //   Q5_K 14336x4096, 4 / 8 / 16 rows:  17.8 / 17.9 / 18.6 against 18.8 / 19.4 / 20.4
 //   Q8_0 4096x4096, 4 / 8 / 16 / 64:   11.0 / 11.3 / 11.8 / 19.1 against 12.3 / 12.3 / 12.7 / 21.3
-// Q6_K has only this form; the tuning knob "gemm_small_q8" forces either (1 once, 2 in-kernel).
+// Q6_K, Q4_0 and Q5_0 have only this form; the tuning knob "gemm_small_q8" forces either for
+// the others (1 once, 2 in-kernel).
 bool small_quantize_once(uint32_t type, int k, int n, int m) {
     (void)k;
     (void)n;
     (void)m;
-    if (type == T_Q6_K) return true;
+    if (type == T_Q6_K || type == T_Q4_0 || type == T_Q5_0) return true;
     return tuning().gemm_small_q8.load(std::memory_order_relaxed) != 2;
 }
 

@@ -50,12 +50,14 @@ __host__ __device__ constexpr size_t sm_align16(size_t v) { return (v + 15) & ~(
 // row's last super-block ends exactly at the row's end, and no window leaves its row.
 template <uint32_t T>
 __host__ __device__ constexpr int sm_sb_bytes() {
-    return T == T_Q8_0 ? 8 * 34 : T == T_Q5_K ? 176 : T == T_Q6_K ? 224 : 144;
+    return T == T_Q8_0 ? 8 * Q8_0_BYTES : T == T_Q4_0 ? 8 * Q4_0_BYTES : T == T_Q5_0 ? 8 * Q5_0_BYTES
+         : T == T_Q5_K ? 176 : T == T_Q6_K ? 224 : 144;
 }
 template <uint32_t T>
 __host__ __device__ constexpr bool sm_kq() { return T == T_Q4_K || T == T_Q5_K; }
 // Per-wave exchange table: Q4_K / Q5_K, the 6-bit scales [16 rows][8 blocks] as bytes; Q6_K,
-// the 16 int8 scales of each row [16 rows][16]; Q8_0, the blocks' d as floats [8 blocks][16 rows].
+// the 16 int8 scales of each row [16 rows][16]; the 32-element block types, the blocks' d as
+// floats [8 blocks][16 rows].
 template <uint32_t T>
 __host__ __device__ constexpr int sm_tab_bytes() { return sm_kq<T>() ? 128 : T == T_Q6_K ? 256 : 512; }
 
@@ -367,25 +369,51 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
                 for (int i = 0; i < 4; ++i) acc[j][i] = __builtin_fmaf(dc[i], s[i], acc[j][i]) - mn[i];
             }
         } else {
-            // Q8_0: block b of row r at 34 b: d (fp16), then 32 quants; this lane's 8 bytes start
-            // at 34 b + 2 + 8 g, 4-byte aligned for odd b and 2 past it for even b
+            // 32-element blocks: block b of row r at BB b, d (fp16) first. This lane's 8
+            // elements are 8 g .. 8 g + 7 of each block:
+            //   Q8_0: the 8 quant bytes at 2 + 8 g;
+            //   Q4_0 / Q5_0: the low (g < 2) or high nibbles of the 8 qs bytes at QB + 8 (g & 1)
+            //   (byte j holds elements j and j + 16); Q5_0 adds bit 8 g + i of its 4 qh bytes at
+            //   2 as bit 4 of element i. As int8, q - 8 = (q + 0x78) ^ 0x80 and q - 16 =
+            //   (q + 0x70) ^ 0x80 per byte (no carry leaves a byte), exact.
+            // Every block starts 2 bytes past a 4-byte boundary when b is even (BB = 2 mod 4),
+            // so even blocks' 8 bytes are realigned from three dword reads.
+            constexpr int BB = T == T_Q8_0 ? Q8_0_BYTES : T == T_Q4_0 ? Q4_0_BYTES : Q5_0_BYTES;
+            constexpr int QB = T == T_Q5_0 ? 6 : 2;  // quant bytes within a block
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                const int a = 34 * b + 2 + 8 * g;
+                const int a = BB * b + QB + (T == T_Q8_0 ? 8 * g : 8 * (g & 1));
+                u32x2 v;
                 if ((b & 1) != 0) {
-                    A[b] = u32x2{*(const uint32_t*)(rowp + a), *(const uint32_t*)(rowp + a + 4)};
+                    v = u32x2{*(const uint32_t*)(rowp + a), *(const uint32_t*)(rowp + a + 4)};
                 } else {
                     const uint32_t d0 = *(const uint32_t*)(rowp + a - 2);
                     const uint32_t d1 = *(const uint32_t*)(rowp + a + 2);
                     const uint32_t d2 = *(const uint32_t*)(rowp + a + 6);
-                    A[b] = u32x2{__builtin_amdgcn_alignbyte(d1, d0, 2), __builtin_amdgcn_alignbyte(d2, d1, 2)};
+                    v = u32x2{__builtin_amdgcn_alignbyte(d1, d0, 2), __builtin_amdgcn_alignbyte(d2, d1, 2)};
+                }
+                if constexpr (T == T_Q8_0) {
+                    A[b] = v;
+                } else {
+                    u32x2 q = g < 2 ? (v & 0x0F0F0F0Fu) : ((v >> 4) & 0x0F0F0F0Fu);
+                    if constexpr (T == T_Q5_0) {
+                        // bits i of the qh byte to bit 4 of byte i: x * 0x00204081 puts bit i of
+                        // a 4-bit x at bit 8 i (among others off those positions)
+                        const uint32_t hb = rowp[BB * b + 2 + g];
+                        const uint32_t s0 = ((hb & 0xFu) * 0x00204081u) & 0x01010101u;
+                        const uint32_t s1 = ((hb >> 4) * 0x00204081u) & 0x01010101u;
+                        q = q | (u32x2{s0, s1} << 4);
+                        A[b] = (q + 0x70707070u) ^ 0x80808080u;
+                    } else {
+                        A[b] = (q + 0x78787878u) ^ 0x80808080u;
+                    }
                 }
             }
             // the blocks' d: this lane converts those of row r, blocks 2 g and 2 g + 1, into
             // the table [block][row]; the result rows 4 g + i read theirs back per block
             float* dt = (float*)tab;
-            dt[(2 * g) * 16 + r] = f16_to_f32(*(const uint16_t*)(rowp + 34 * (2 * g)));
-            dt[(2 * g + 1) * 16 + r] = f16_to_f32(*(const uint16_t*)(rowp + 34 * (2 * g + 1)));
+            dt[(2 * g) * 16 + r] = f16_to_f32(*(const uint16_t*)(rowp + BB * (2 * g)));
+            dt[(2 * g + 1) * 16 + r] = f16_to_f32(*(const uint16_t*)(rowp + BB * (2 * g + 1)));
             f32x4 dcb[8];
 #pragma unroll
             for (int b = 0; b < 8; ++b) dcb[b] = *(const f32x4*)(dt + b * 16 + 4 * g);
@@ -640,6 +668,14 @@ hipError_t launch_sm(uint32_t type, const uint8_t* w, int k, int n, int m, const
         case T_Q4_K: return launch_sm_mt<T_Q4_K, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
         case T_Q5_K: return launch_sm_mt<T_Q5_K, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
         case T_Q8_0: return launch_sm_mt<T_Q8_0, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
+        case T_Q4_0:  // Q4_0 / Q5_0 from a quantized batch only
+            if constexpr (!FUSED)
+                return launch_sm_mt<T_Q4_0, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
+            return hipErrorNotSupported;
+        case T_Q5_0:
+            if constexpr (!FUSED)
+                return launch_sm_mt<T_Q5_0, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
+            return hipErrorNotSupported;
         case T_Q6_K:  // from a quantized batch only (the fused form would spill registers)
             if constexpr (!FUSED)
                 return launch_sm_mt<T_Q6_K, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, slices, counters, stream);
@@ -652,7 +688,7 @@ hipError_t launch_sm(uint32_t type, const uint8_t* w, int k, int n, int m, const
 
 bool gemm_sm_supported(uint32_t type, int k, int m) {
     // Q6_K rows must be whole 16-byte pieces: k a multiple of 2048 (8 super-blocks)
-    return (type == T_Q4_K || type == T_Q5_K || type == T_Q8_0 ||
+    return (type == T_Q4_K || type == T_Q5_K || type == T_Q8_0 || type == T_Q4_0 || type == T_Q5_0 ||
             (type == T_Q6_K && k % 2048 == 0)) && k % 256 == 0 && k > 0 && m >= 1 && m <= 64;
 }
 
@@ -670,7 +706,8 @@ size_t gemm_sm_partial_bytes(uint32_t type, int k, int n, int m) {
 void gemm_sm_plan_name(uint32_t type, int k, int n, int m, bool fused, char* buf, size_t cap) {
     const SmPlan p = sm_plan(type, k, n, m, fused);
     snprintf(buf, cap, "k_gemm_sm<%s,%d> splits=%d kp=%d",
-             type == T_Q8_0 ? "Q8_0" : type == T_Q5_K ? "Q5_K" : type == T_Q6_K ? "Q6_K" : "Q4_K",
+             type == T_Q8_0 ? "Q8_0" : type == T_Q5_K ? "Q5_K" : type == T_Q6_K ? "Q6_K"
+             : type == T_Q4_0 ? "Q4_0" : type == T_Q5_0 ? "Q5_0" : "Q4_K",
              p.mt, p.splits, p.kp);
 }
 

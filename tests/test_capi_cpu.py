@@ -92,7 +92,12 @@ def test_decode_plans():
     assert C.matmul_plan(S.Q6_K, 14336, 4096, 1) == "k_gemv_str<Q6_K,1> launches=1"
     assert C.matmul_plan(S.Q8_0, 896, 4864, 1) == "k_gemv_str<Q8_0,1> launches=1"
     assert C.matmul_plan(S.Q4_K, 4096, 1024, 1) == "k_gemv<Q4_K,1> launches=1"
-    assert C.matmul_plan(S.Q4_0, 4096, 4096, 13) == "k_gemv<Q4_0,8> launches=3"
+    assert C.matmul_plan(S.Q4_0, 4096, 4096, 13) == "k_gemm_sm<Q4_0,1> splits=1 kp=16"
+    try:
+        C.tune("gemm_small", 2)
+        assert C.matmul_plan(S.Q4_0, 4096, 4096, 13) == "k_gemv<Q4_0,8> launches=3"
+    finally:
+        C.tune("gemm_small")
     assert C.matmul_plan(S.Q4_K, 4096, 14336, 3) == "k_gemv_str<Q4_K,3> launches=1"
     assert C.matmul_plan(S.Q4_K, 4096, 14336, 5) == "k_gemv_str<Q4_K,5> launches=1"
     assert C.matmul_plan(S.Q4_K, 4096, 1024, 3) == "k_gemv<Q4_K,2> launches=2"
@@ -108,10 +113,8 @@ def test_decode_plans():
 
 
 def test_mid_batch_routes():
-    """Below 16 rows, Q4_0 / Q5_0 (no small-batch kernel) keep the GEMV while it streams the
-    batch in one launch (up to 8 rows), else take the weight-row kernel once the GEMV would read
-    the weights three times on matrices of 32 M weights or more, four times on smaller ones, or
-    from 8 rows on the large ones. Q6_K keeps a streamed batch of up to 5 rows, else takes the
+    """Below 16 rows, Q4_0 / Q5_0 keep the GEMV while it streams the batch in one launch (up to
+    8 rows), else take the small-batch kernel from 8 rows. Q6_K keeps a streamed batch of up to 5 rows, else takes the
     small-batch kernel from 4 to 16 rows where the GEMV would need two launches or more, or on
     matrices of 32 M weights or more; the weight-row kernel beyond 16 rows. Q4_K keeps the GEMV
     below 8 rows, Q5_K up to 6, Q8_0 up to 8."""
@@ -120,8 +123,9 @@ def test_mid_batch_routes():
         (S.Q6_K, 4096, 14336, set(), set(range(6, 17))),
         (S.Q6_K, 14336, 4096, set(), set(range(5, 17))),
         (S.Q6_K, 4096, 1024, set(), {5, 6, 7} | set(range(9, 17))),
-        (S.Q4_0, 4096, 14336, set(range(9, 17)), set()),
-        (S.Q5_0, 4096, 4096, {15, 16}, set()),
+        (S.Q4_0, 4096, 14336, set(), set(range(9, 17))),
+        (S.Q5_0, 4096, 4096, set(), set(range(9, 17))),
+        (S.Q4_0, 14336, 4096, set(), set(range(8, 17))),
     ]
     for t, k, n, want_mfma, want_small in cases:
         got = {m for m in range(1, 17) if C.matmul_route(t, k, n, m) == "mfma"}

@@ -64,7 +64,8 @@ def test_m_sweep_batches_vs_reference_golden(gpu, orc, label, m):
 @pytest.mark.parametrize("qt", TYPES)
 def test_mfma_matches_gemv_and_oracle(gpu, orc, qt, gemm_kernel):
     """Same rows through the MFMA kernel (16 rows at once) and the GEMV kernel (8 + 8); with
-    the default kernel choice, Q4_K / Q5_K / Q8_0 take the small-batch kernel for both."""
+    the default kernel choice, every type but Q6_K (whose rows here are not a multiple of 2048
+    elements) takes the small-batch kernel for both."""
     import torch
     k, n, m = 1024, 300, 16
     w = S.make_weight(qt, n, k, 70 + qt)
@@ -74,7 +75,7 @@ def test_mfma_matches_gemv_and_oracle(gpu, orc, qt, gemm_kernel):
     y_mfma = gpu.gemv_q8_dev(wd, qt, k, n, qs, sc, bs)  # 16 rows -> MFMA route
     y_gemv = torch.cat([gpu.gemv_q8_dev(wd, qt, k, n, qs[i:i + 8], sc[i:i + 8], bs[i:i + 8])
                         for i in (0, 8)])
-    small = gemm_kernel == "default" and qt in (S.Q4_K, S.Q5_K, S.Q8_0)
+    small = gemm_kernel == "default" and qt != S.Q6_K
     assert gpu.matmul_route(qt, k, n, 8) == ("small" if small else "gemv")
     assert gpu.matmul_route(qt, k, n, 16) == ("small" if small else "mfma")
     exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, m)
@@ -101,17 +102,16 @@ def test_mfma_partial_tiles_and_bias(gpu, orc, qt):
                                          (S.Q5_0, 4096, 4096, 15), (S.Q6_K, 4096, 1024, 15)])
 def test_mid_batches_on_weight_row_kernel(gpu, orc, qt, k, n, m, gemm_kernel):
     """Batches below 16 rows on the weight-row kernel (one partly filled 16-row tile) on
-    full-size matrices, every output against the oracle: the route Q4_0 / Q5_0 take there
-    when the GEMV runs its register ring (the streaming GEMV, which takes up to 8 rows in one
-    launch, turned off); Q6_K's with the small-batch route also switched off."""
+    full-size matrices, every output against the oracle: the route Q4_0 / Q5_0 / Q6_K take
+    there with the streaming GEMV (which takes up to 8 rows in one launch) and the small-batch
+    kernel switched off."""
     if gemm_kernel != "default":
         pytest.skip("the default route only")
     w = S.make_weight(qt, n, k, 11 + m)
     x = S.make_activation(m, k, 12 + m, outliers=True)
     try:
         gpu.tune("gemv_kernel", 1)
-        if qt == S.Q6_K:
-            gpu.tune("gemm_small", 2)
+        gpu.tune("gemm_small", 2)
         assert gpu.matmul_route(qt, k, n, m) == "mfma"
         print("mid batch", S.TYPE_NAMES[qt], n, k, m, gpu.matmul_plan(qt, k, n, m), flush=True)
         y = gpu.matmul_quant_dev(_dev(x), _dev(w), qt, None, k, n).cpu().numpy()

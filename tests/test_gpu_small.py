@@ -1,7 +1,7 @@
-"""The small-batch route (k_gemm_sm.hip: by default 8 to 32 activation rows of Q4_K / Q5_K
-weights, 8 to 64 of Q8_0 and 4 to 16 of Q6_K, on int8 MFMA, the weights streamed once for the
-batch, the fp32 rows quantized once first; the kernel takes 1 to 64) on an MI355X, through the
-C ABI.
+"""The small-batch route (k_gemm_sm.hip: by default up to 32 or 64 activation rows of every
+vec_dot type, from 5 to 9 rows depending on the type and on whether the GEMV streams the batch
+in one launch; on int8 MFMA, the weights streamed once for the batch, the fp32 rows quantized
+once first; the kernel takes 1 to 64) on an MI355X, through the C ABI.
 
 Bars: the check_close bars of test_gpu_parity.py against the oracle (the reference's own
 quant.cpp restated) and the fp64 evaluation of the same quantized terms; bit-identical results
@@ -41,7 +41,7 @@ def small_everywhere(gpu):
     gpu.tune("gemm_small")
 
 
-@pytest.mark.parametrize("qt", SMALL_TYPES)
+@pytest.mark.parametrize("qt", SMALL_TYPES + [S.Q4_0, S.Q5_0])
 def test_small_batches_ragged_shapes_vs_oracle(gpu, orc, qt, small_everywhere):
     """Batch sizes that leave token tiles part-empty (5, 17, 33, 63), row counts that leave a
     row group part-empty, K that splits over workgroups (K = 4096 takes four splits; K = 2816
@@ -190,6 +190,27 @@ def test_q6_k_small_batches_default_route_vs_oracle(gpu, orc, k, n, m):
         yo = orc.matmul(x, w, qt, b, k, n, m, threads=8)
         check_close(y_fused.reshape(m, n), yo.reshape(m, n), exact, abs_sum,
                     f"q6_k small {n}x{k} m{m}")
+
+
+@pytest.mark.parametrize("qt, k, n, m", [(S.Q4_0, 4096, 14336, 12), (S.Q5_0, 4096, 14336, 16),
+                                         (S.Q4_0, 4096, 4096, 64), (S.Q5_0, 14336, 4096, 9)])
+def test_q4_0_q5_0_small_batches_default_route_vs_oracle(gpu, orc, qt, k, n, m):
+    """Q4_0 / Q5_0 on the small-batch kernel (the batch quantized once; q - 8 and q - 16 formed
+    per byte as int8, Q5_0's fifth bits spread from its qh word): the default route of these
+    full-size shapes, every output against the oracle with and without a bias, the fp32 and
+    quantized-batch entry points bit for bit."""
+    assert gpu.matmul_route(qt, k, n, m) == "small"
+    w = S.make_weight(qt, n, k, 80 + m + n)
+    x = S.make_activation(m, k, 81 + m, outliers=True)
+    bias = np.random.default_rng(n + m).standard_normal(n).astype(np.float32)
+    print("b32 small", S.TYPE_NAMES[qt], n, k, m, gpu.matmul_plan(qt, k, n, m), flush=True)
+    for b in (None, bias):
+        y_fused, y_q8 = _run(gpu, w, x, qt, b, k, n, m)
+        assert np.array_equal(bits(y_fused), bits(y_q8))
+        exact, abs_sum = orc.matmul_f64(x, w, qt, b, k, n, m)
+        yo = orc.matmul(x, w, qt, b, k, n, m, threads=8)
+        check_close(y_fused.reshape(m, n), yo.reshape(m, n), exact, abs_sum,
+                    f"{S.TYPE_NAMES[qt]} small {n}x{k} m{m}")
 
 
 def test_q6_k_small_kernel_tiles_and_splits(gpu, orc):
