@@ -29,17 +29,19 @@ def _static(lib, x, w, qt, bias, k, n, y):
 # 4096 x 4096 Q4_K matrix at 512 rows plans two splits), then the small-batch route with split
 # K (32 rows: two splits), Q6_K's kernel, a 32-element block type on the MFMA then the
 # small-batch route, the small-batch route then the GEMV route with a quantized batch (3
-# rows), and the fused decode GEMV (1 row)
+# rows), the fused decode GEMV (1 row), and the streaming GEMV's whole-batch launch on a
+# batch quantized first (8 rows) then quantized inside the launch (5 rows)
 CASES = [
     (S.Q4_K, 4096, 4096, [512, 32]),
     (S.Q6_K, 1024, 4096, [256, 16]),
     (S.Q8_0, 768, 2048, [96, 32]),
     (S.Q5_K, 600, 1024, [12, 3]),
     (S.Q4_0, 512, 1024, [2, 1]),
+    (S.Q8_0, 4096, 4096, [8, 5]),
 ]
 
 
-@pytest.mark.parametrize("qt,n,k,ms", CASES, ids=[S.TYPE_NAMES[c[0]] for c in CASES])
+@pytest.mark.parametrize("qt,n,k,ms", CASES, ids=[f"{S.TYPE_NAMES[c[0]]}-{c[1]}x{c[2]}" for c in CASES])
 def test_static_scratch_matches_matmul_quant_dev(gpu, qt, n, k, ms):
     import torch
     lib = C.load_library()
