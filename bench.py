@@ -32,6 +32,8 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5033.0  # 256 CU x 2.4 GHz x 8192 int8 ops / clk / CU (dense)
 FP16_PEAK_TFLOPS = 2516.0  # dense fp16 MFMA, the unit the prefill GEMM computes on
+FP16_MFMA_PEAK_TFLOPS = FP16_PEAK_TFLOPS
+FP32_VECTOR_PEAK_TFLOPS = 157.3  # fp32 vector (packed), the unit the attention kernel computes on
 ROTATE_BYTES = 512 << 20
 
 
@@ -363,6 +365,41 @@ def decode_model(C, S, steps, warmup, n_layers=4, pos=1024):
     return out
 
 
+def prefill_attention(C, steps, warmup, m=512, pos0=0, n_head=32, n_kv=8, head_dim=128):
+    """f4 at prefill: a prompt of m rows at positions pos0 .. pos0 + m - 1 in one Llama-3-8B
+    layer (32 query heads over 8 KV heads of 128): RoPE of q and of the new key rows, then
+    causal grouped-query attention over the cache (engine.cpp:581-586). Synthetic q/k/v.
+    Algorithmic work: 2 x 2 x head_dim multiply-adds per (query, head, visible position), for
+    q.k and for p.v."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn((m, n_head * head_dim), device="cuda", generator=g)
+    kc = torch.randn((pos0 + m, n_kv * head_dim), device="cuda", generator=g)
+    vc = torch.randn((pos0 + m, n_kv * head_dim), device="cuda", generator=g)
+    out = torch.empty_like(q)
+    q0, k0 = q.clone(), kc.clone()
+
+    def step(i):
+        q.copy_(q0)
+        kc[pos0:].copy_(k0[pos0:])
+        C.rope_neox2_dev(q, n_head, kc[pos0:], n_kv, head_dim, pos0, 500000.0)
+        C.attention_dev(q, kc, vc, pos0, n_head, n_kv, head_dim, out=out)
+
+    ms_all = time_loop(step, steps, warmup)
+    ms_att = time_loop(lambda i: C.attention_dev(q, kc, vc, pos0, n_head, n_kv, head_dim, out=out),
+                       steps, warmup)
+    visible = sum(pos0 + t + 1 for t in range(m))
+    flop = 2 * 2 * head_dim * visible * n_head
+    out_d = {"rows": m, "pos0": pos0, "n_head": n_head, "n_head_kv": n_kv, "head_dim": head_dim,
+             "attention_us": round(ms_att * 1e3, 1), "rope_and_attention_us": round(ms_all * 1e3, 1),
+             "gflops": round(flop / ms_att / 1e6, 1),
+             "frac_fp32_vector": round(flop / ms_att / 1e9 / FP32_VECTOR_PEAK_TFLOPS, 4),
+             "frac_fp16_mfma": round(flop / ms_att / 1e9 / FP16_MFMA_PEAK_TFLOPS, 4)}
+    print(f"[bench] prefill attention m={m} pos0={pos0}: {ms_att * 1e3:.1f} us ({flop / ms_att / 1e6:.1f} "
+          f"GFLOP/s), with the RoPE launch and input copies {ms_all * 1e3:.1f} us", file=sys.stderr, flush=True)
+    return out_d
+
+
 def gguf_upload(C, S, gib=1.0):
     """f2: the GGUF data section's one-time upload (parse, map, pinned double-buffered H2D,
     registration) for a synthetic file of `gib` GiB written to local temporary storage."""
@@ -630,6 +667,8 @@ def main():
                          "JSON line")
     ap.add_argument("--sweep-only", action="store_true",
                     help="run only the c4 M-sweep and print it as one JSON line")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the M=512 prefill attention (f4) and print it as one JSON line")
     ap.add_argument("--head-only", action="store_true",
                     help="run only the Q6_K 128256x4096 output-head GEMV and print it as one JSON "
                          "line")
@@ -699,6 +738,11 @@ def main():
                                            "read_ceiling": read_ceiling(c2)}}))
         return
 
+    if args.attention_only:
+        print(json.dumps({"f4_prefill_attention_m512": prefill_attention(
+            C, max(5, args.steps // 20), max(2, args.warmup // 10))}))
+        return
+
     if args.prefill_only:
         layer = prefill_layer(C, S, max(5, args.steps // 20), max(2, args.warmup // 10))
         dev = prefill_layer_device(C, S, max(5, args.steps // 20), max(2, args.warmup // 10),
@@ -749,6 +793,8 @@ def main():
         extra["f2_gguf_upload"] = gguf_upload(C, S)
         extra["f4_device_decode_step"] = decode_model(C, S, max(10, args.steps // 10),
                                                       max(2, args.warmup // 10))
+        extra["f4_prefill_attention_m512"] = prefill_attention(C, max(5, args.steps // 20),
+                                                               max(2, args.warmup // 10))
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -8,6 +8,8 @@ evaluation of the same quantized terms than max(1e-4 * max(|exact|, 2^-10 * A),
 2 * |ref - exact|, R * A) (A = sum of absolute per-block terms, R = the reference's largest
 |ref - exact| / A over the same output).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -123,31 +125,35 @@ def test_mid_batches_on_weight_row_kernel(gpu, orc, qt, k, n, m, gemm_kernel):
     check_close(y, yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")
 
 
-def test_full_prefill_layer_sampled_rows(gpu, orc):
-    """M = 512 through every matrix of the layer at full size; 8 activation rows (all
-    outputs) checked against the oracle, and every other row against row-wise GEMV."""
+def _oracle_f64_rows(orc, x, w, qt, k, n):
+    """The oracle's fp64 evaluation and absolute-term sums of every row of x, computed in row
+    chunks on a thread pool (the oracle's calls release the interpreter lock)."""
+    from concurrent.futures import ThreadPoolExecutor
+    m = x.shape[0]
+    chunks = [(i, min(i + 16, m)) for i in range(0, m, 16)]
+    workers = max(1, min(16, os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        parts = list(ex.map(lambda ab: orc.matmul_f64(x[ab[0]:ab[1]], w, qt, None, k, n, ab[1] - ab[0]),
+                            chunks))
+    return np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts])
+
+
+@pytest.mark.parametrize("label", [mat[0] for mat in S.CONFIGS["c3_q4_k_m_layer"]["mats"]])
+def test_full_prefill_layer_every_row_vs_oracle(gpu, orc, label):
+    """M = 512 through each matrix of the layer at full size on its default plan: every output
+    of all 512 activation rows against the oracle, to check_close's bars."""
     import torch
-    rng = np.random.default_rng(1)
-    for label, qt, n, k in S.CONFIGS["c3_q4_k_m_layer"]["mats"]:
-        _, _, _, w = S.config_weight("c3_q4_k_m_layer", label)
-        x = S.config_activation("c3_q4_k_m_layer", 512, k)
-        print("full layer", label, n, k, flush=True)
-        wd, xd = _dev(w), _dev(x)
-        y = gpu.matmul_quant_dev(xd, wd, qt, None, k, n)
-        torch.cuda.synchronize()
-        rows = np.sort(rng.choice(512, size=8, replace=False))
-        yo = orc.matmul(x[rows], w, qt, None, k, n, 8, threads=8)
-        exact, abs_sum = orc.matmul_f64(x[rows], w, qt, None, k, n, 8)
-        check_close(y.cpu().numpy()[rows], yo, exact, abs_sum, label)
-        # all 512 rows against the GEMV kernel (a different algorithm, same contract)
-        qs, sc, bs = gpu.quantize_q8_0_dev(xd)
-        yg = torch.cat([gpu.gemv_q8_dev(wd, qt, k, n, qs[i:i + 8], sc[i:i + 8], bs[i:i + 8])
-                        for i in range(0, 512, 8)])
-        d = (y - yg).abs().cpu().numpy().astype(np.float64)
-        scale = np.maximum(np.abs(yg.cpu().numpy()), 1e-3 * np.abs(yg.cpu().numpy()).max(axis=1, keepdims=True))
-        assert (d / scale).max() < 1e-3, (label, (d / scale).max())
-        del wd, xd, y, yg
-        torch.cuda.empty_cache()
+    qt, n, k, w = S.config_weight("c3_q4_k_m_layer", label)
+    x = S.config_activation("c3_q4_k_m_layer", 512, k)
+    print("full layer", label, n, k, gpu.matmul_plan(qt, k, n, 512), flush=True)
+    wd, xd = _dev(w), _dev(x)
+    y = gpu.matmul_quant_dev(xd, wd, qt, None, k, n).cpu().numpy()
+    torch.cuda.synchronize()
+    del wd, xd
+    torch.cuda.empty_cache()
+    yo = orc.matmul(x, w, qt, None, k, n, 512, threads=max(1, min(16, os.cpu_count() or 1)))
+    exact, abs_sum = _oracle_f64_rows(orc, x, w, qt, k, n)
+    check_close(y, yo, exact, abs_sum, f"{label} all 512 rows")
 
 
 @pytest.mark.parametrize("splits", [None, 4])
