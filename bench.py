@@ -32,8 +32,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5033.0  # 256 CU x 2.4 GHz x 8192 int8 ops / clk / CU (dense)
 FP16_PEAK_TFLOPS = 2516.0  # dense fp16 MFMA, the unit the prefill GEMM computes on
-FP16_MFMA_PEAK_TFLOPS = FP16_PEAK_TFLOPS
-FP32_VECTOR_PEAK_TFLOPS = 157.3  # fp32 vector (packed), the unit the attention kernel computes on
+FP32_MFMA_PEAK_TFLOPS = 157.3  # dense fp32 MFMA, the unit the many-row attention kernel computes on
 ROTATE_BYTES = 512 << 20
 
 
@@ -386,17 +385,24 @@ def prefill_attention(C, steps, warmup, m=512, pos0=0, n_head=32, n_kv=8, head_d
         C.attention_dev(q, kc, vc, pos0, n_head, n_kv, head_dim, out=out)
 
     ms_all = time_loop(step, steps, warmup)
-    ms_att = time_loop(lambda i: C.attention_dev(q, kc, vc, pos0, n_head, n_kv, head_dim, out=out),
-                       steps, warmup)
+    att = lambda i: C.attention_dev(q, kc, vc, pos0, n_head, n_kv, head_dim, out=out)
+    ms_att = time_loop(att, steps, warmup)
+    C.tune("attention_kernel", 1)  # the sequence-split kernel on the same rows, for comparison
+    try:
+        ms_split = time_loop(att, steps, warmup)
+    finally:
+        C.tune("attention_kernel")
     visible = sum(pos0 + t + 1 for t in range(m))
     flop = 2 * 2 * head_dim * visible * n_head
     out_d = {"rows": m, "pos0": pos0, "n_head": n_head, "n_head_kv": n_kv, "head_dim": head_dim,
+             "plan": C.attention_plan(m, pos0, n_head, n_kv, head_dim),
              "attention_us": round(ms_att * 1e3, 1), "rope_and_attention_us": round(ms_all * 1e3, 1),
+             "split_kernel_us": round(ms_split * 1e3, 1),
              "gflops": round(flop / ms_att / 1e6, 1),
-             "frac_fp32_vector": round(flop / ms_att / 1e9 / FP32_VECTOR_PEAK_TFLOPS, 4),
-             "frac_fp16_mfma": round(flop / ms_att / 1e9 / FP16_MFMA_PEAK_TFLOPS, 4)}
-    print(f"[bench] prefill attention m={m} pos0={pos0}: {ms_att * 1e3:.1f} us ({flop / ms_att / 1e6:.1f} "
-          f"GFLOP/s), with the RoPE launch and input copies {ms_all * 1e3:.1f} us", file=sys.stderr, flush=True)
+             "frac_fp32_mfma": round(flop / ms_att / 1e9 / FP32_MFMA_PEAK_TFLOPS, 4)}
+    print(f"[bench] prefill attention m={m} pos0={pos0} ({out_d['plan']}): {ms_att * 1e3:.1f} us "
+          f"({flop / ms_att / 1e6:.1f} GFLOP/s; the split kernel {ms_split * 1e3:.1f} us), with the RoPE "
+          f"launch and input copies {ms_all * 1e3:.1f} us", file=sys.stderr, flush=True)
     return out_d
 
 

@@ -102,6 +102,7 @@ SIGNATURES = {
     "cllm_hip_dequantize_rows_dev": (_I, [_P, _U, _I, _P, _I, _P, _P]),
     "cllm_hip_attention_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "cllm_hip_attention_rope_dev": (_I, [_P, _P, _P, _I, _I, _I, _I, ctypes.c_float, _P, _P]),
+    "cllm_hip_attention_plan": (ctypes.c_char_p, [_I, _I, _I, _I, _I]),
 }
 
 
@@ -407,6 +408,13 @@ def matmul_plan(t: int, in_dim: int, out_dim: int, n_rows: int) -> str:
     """The kernel instantiation and split count the batch would run (or the route name)."""
     return load_library().cllm_hip_matmul_plan(int(t), int(in_dim), int(out_dim),
                                                int(n_rows)).decode()
+
+
+def attention_plan(n_rows: int, pos0: int, n_head: int, n_head_kv: int, head_dim: int) -> str:
+    """The attention kernel attention_dev would run for this shape, with its workgroups or
+    sequence splits ("none" for an unsupported shape)."""
+    return load_library().cllm_hip_attention_plan(int(n_rows), int(pos0), int(n_head),
+                                                  int(n_head_kv), int(head_dim)).decode()
 
 
 def tune(knob: str, *values: int) -> None:

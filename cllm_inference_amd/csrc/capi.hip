@@ -1610,6 +1610,14 @@ int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_
                           stream, 0.0f);
 }
 
+const char* cllm_hip_attention_plan(int n_rows, int pos0, int n_head, int n_head_kv,
+                                    int head_dim) {
+    static thread_local char buf[96];
+    if (n_rows <= 0 || pos0 < 0 || !attention_supported(head_dim, n_head, n_head_kv)) return "none";
+    attention_plan_name(n_rows, pos0, n_head, n_head_kv, head_dim, buf, sizeof buf);
+    return buf;
+}
+
 int cllm_hip_attention_rope_dev(const float* q, float* k_cache, const float* v_cache, int pos0,
                                 int n_head, int n_head_kv, int head_dim, float theta_base,
                                 float* out, void* stream) {
@@ -1807,6 +1815,9 @@ int cllm_hip_tune(const char* knob, const int* values, int n_values) {
     } else if (std::strcmp(knob, "gemm_small_q8") == 0) {
         if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemm_small_q8 is 0, 1 or 2");
         t.gemm_small_q8.store(v(0));
+    } else if (std::strcmp(knob, "attention_kernel") == 0) {
+        if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: attention_kernel is 0, 1 or 2");
+        t.attention_kind.store(v(0));
     } else if (std::strcmp(knob, "gemm_small_plan") == 0) {
         t.gemm_small_splits.store(v(0));
         t.gemm_small_kp.store(v(1));

@@ -24,6 +24,7 @@ struct Tuning {
     std::atomic<int> gemm_small_splits{0}, gemm_small_kp{0};  // its plan (0 = planner's)
     std::atomic<int> gemm_small_q8{0};    // fp32 batches: 0 planner, 1 quantized once first, 2 in-kernel
     std::atomic<int> gemv_fused_rows{0};  // streamed GEMV batches quantized in-kernel up to this many rows
+    std::atomic<int> attention_kind{0};   // attention: 0 planner, 1 split kernel, 2 MFMA kernel
 };
 Tuning& tuning();
 
@@ -157,6 +158,11 @@ hipError_t launch_add(float* x, const float* d, int64_t n, hipStream_t stream);
 hipError_t launch_rope_neox(float* x, int rows, int n_heads, float* x2, int n_heads2,
                             int head_dim, int pos0, float base, hipStream_t stream);
 bool attention_supported(int head_dim, int n_head, int n_kv);
+// Which attention kernel launch_attention runs for these rows (true: k_attention_mfma), and
+// its name with the launch's workgroups or sequence splits.
+bool attention_uses_mfma(int rows, int pos0, int n_head, int n_kv, int head_dim);
+void attention_plan_name(int rows, int pos0, int n_head, int n_kv, int head_dim, char* buf,
+                         size_t cap);
 size_t attention_workspace_bytes(int rows, int n_head, int head_dim);
 // With rope_base > 0 (rows == 1 only), q and the key row at pos0 are unrotated: the kernel
 // applies launch_rope_neox's rotation to both (the key row in place in kc).

@@ -300,6 +300,12 @@ int cllm_hip_attention_dev(const float* q, const float* k_cache, const float* v_
                            int n_rows, int pos0, int n_head, int n_head_kv, int head_dim,
                            float* out, void* stream);
 
+/* The attention kernel cllm_hip_attention_dev would run for this shape: "k_attention_mfma<HD,
+ * CT,W> workgroups=N" (many query rows) or "k_attention<HD> splits=S"; for tests and
+ * benchmarks. No reference counterpart. */
+const char* cllm_hip_attention_plan(int n_rows, int pos0, int n_head, int n_head_kv,
+                                    int head_dim);
+
 /* One decode step's RoPE and attention in one launch (engine.cpp:486-495): q holds one row of
  * n_head unrotated query heads, k_cache row pos0 the unrotated new key; both get the NEOX
  * rotation of cllm_hip_rope_neox2_dev at position pos0 (the queries in registers, q is not
@@ -372,6 +378,12 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
  *                  "gemm_kernel" forces a kernel)
  *   "gemm_small_plan" K splits (more than the planner's) and K parts per workgroup (1, 2, 4,
  *                  8 or 16) of the small-batch kernel (0, 0 = the planner's)
+ *   "gemm_small_q8" fp32 batches on the small-batch kernel: 0 the default, 1 quantized once by
+ *                  a separate launch, 2 quantized inside the kernel
+ *   "gemv_fused_rows" batches of up to this many rows (1 to 8) on the streaming GEMV are
+ *                  quantized inside its launch (0 = the default)
+ *   "attention_kernel" 0 the default, 1 the sequence-split kernel, 2 the many-row MFMA kernel
+ *                  (decode with fused RoPE always takes the split kernel)
  * Missing values count as 0, so n_values = 0 resets a knob. Takes effect on the next call. */
 int cllm_hip_tune(const char* knob, const int* values, int n_values);
 

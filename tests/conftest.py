@@ -39,7 +39,8 @@ def orc():
 
 # every process-wide kernel-choice override of cllm_hip_tune
 TUNING_KNOBS = ("gemm_kernel", "gemm_tiles", "gemm_splits", "gemv_kernel", "gemv_str_grid",
-                "gemm_small", "gemm_small_plan", "gemm_small_q8", "gemv_fused_rows", "gemv_waves")
+                "gemm_small", "gemm_small_plan", "gemm_small_q8", "gemv_fused_rows", "gemv_waves",
+                "attention_kernel")
 
 
 @pytest.fixture(autouse=True)

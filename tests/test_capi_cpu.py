@@ -242,6 +242,32 @@ def _libc():
 PROT_READ, PROT_WRITE, MAP_SHARED, MAP_PRIVATE, MAP_FIXED = 1, 2, 1, 2, 0x10
 
 
+def test_attention_plans():
+    """Many query rows take the MFMA kernel (32 or more of its workgroups: n_kv x pairs of
+    row blocks of 32 / n_rep rows, 16 / n_rep at head_dim 256); fewer rows, and a decode row,
+    the sequence-split kernel; the attention_kernel knob forces either."""
+    p = C.attention_plan
+    assert p(512, 0, 32, 8, 128) == "k_attention_mfma<128,2,8> workgroups=256"
+    assert p(64, 0, 32, 8, 128) == "k_attention_mfma<128,2,8> workgroups=32"
+    assert p(49, 1024, 32, 8, 128) == "k_attention_mfma<128,2,8> workgroups=32"
+    assert p(48, 1024, 32, 8, 128).startswith("k_attention<128> splits=")
+    assert p(1, 4095, 32, 8, 128) == "k_attention<128> splits=64"
+    assert p(1, 0, 32, 8, 128) == "k_attention<128> splits=1"
+    assert p(2048, 0, 8, 1, 256) == "k_attention_mfma<256,1,4> workgroups=512"
+    assert p(200, 3, 32, 4, 64) == "k_attention_mfma<64,2,8> workgroups=100"
+    assert p(16, 0, 32, 2, 128) == "none"   # 16 query heads per KV head
+    assert p(16, 0, 32, 8, 96) == "none"
+    try:
+        C.tune("attention_kernel", 1)
+        assert p(512, 0, 32, 8, 128).startswith("k_attention<128> splits=")
+        C.tune("attention_kernel", 2)
+        assert p(1, 300, 32, 8, 128) == "k_attention_mfma<128,2,8> workgroups=8"
+    finally:
+        C.tune("attention_kernel")
+    with pytest.raises(RuntimeError, match="attention_kernel is 0, 1 or 2"):
+        C.tune("attention_kernel", 3)
+
+
 def test_file_mapping_identity_sees_remaps_and_rewrites(tmp_path):
     """The check made before the device copy of a read-only private file mapping (the engine's
     mmap'd GGUF) is reused: a file unmapped and another mapped at the same address, a rewrite

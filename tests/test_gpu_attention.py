@@ -4,8 +4,10 @@ attention over a KV cache (src/core/engine.cpp:41-56, 114-146).
 Bars: RoPE within 4 ulp of the reference's formula evaluated in float64 from the same
 fp32 inputs (the device's powf / cosf / sinf are within an ulp or two); attention within
 2e-6 of |out|_max per head against float64 softmax attention (the summation order differs:
-chunked online softmax, sequence splits); closed forms: one position gives v_0 exactly,
-equal keys give the mean of the values.
+chunked online softmax, sequence splits, the fp32 MFMA kernel's 16-position steps and
+position quarters); closed forms: one position gives v_0 exactly, equal keys give the mean
+of the values. Both attention kernels (the split kernel, the many-row MFMA kernel) run every
+prefill case, forced through the attention_kernel knob.
 """
 import numpy as np
 import pytest
@@ -81,6 +83,59 @@ def test_attention(gpu, hd, n_head, n_kv, rows, pos0):
     err = np.abs(got - want).reshape(rows, n_head, hd).max(axis=2)
     scale = np.abs(want).reshape(rows, n_head, hd).max(axis=2)
     assert (err <= 2e-6 * np.maximum(scale, 1e-3)).all(), err.max()
+
+
+# prefill shapes: Llama-3-8B heads at 512 rows, ragged row counts (blocks of 4 / 8 / 16 / 32
+# rows per workgroup half), a cache ahead of the batch, every GQA ratio 1..8 (3, 5, 6, 7 leave
+# columns of a block unused), one row and a few rows
+PREFILL_CASES = [(128, 32, 8, 512, 0), (128, 32, 8, 100, 37), (64, 16, 16, 33, 0),
+                 (256, 8, 1, 70, 129), (128, 40, 8, 64, 64), (64, 14, 2, 45, 1000),
+                 (128, 24, 8, 19, 5), (128, 12, 2, 130, 0), (128, 32, 8, 1, 300),
+                 (128, 32, 8, 7, 300), (128, 64, 8, 48, 2000), (256, 16, 2, 9, 0),
+                 (64, 32, 4, 200, 3)]
+
+
+@pytest.mark.parametrize("kernel", [1, 2], ids=["split", "mfma"])
+@pytest.mark.parametrize("hd,n_head,n_kv,rows,pos0", PREFILL_CASES)
+def test_attention_prefill_both_kernels(gpu, kernel, hd, n_head, n_kv, rows, pos0):
+    rng = np.random.default_rng(hd * 11 + n_head + rows + pos0)
+    L = pos0 + rows
+    q = rng.standard_normal((rows, n_head * hd)).astype(np.float32)
+    kc = rng.standard_normal((L, n_kv * hd)).astype(np.float32)
+    vc = rng.standard_normal((L, n_kv * hd)).astype(np.float32)
+    print("attention kernel", kernel, hd, n_head, n_kv, rows, pos0, flush=True)
+    gpu.tune("attention_kernel", kernel)
+    got = gpu.attention_dev(_dev(q), _dev(kc), _dev(vc), pos0, n_head, n_kv, hd).cpu().numpy()
+    want = _attn_ref(q, kc, vc, pos0, n_head, n_kv, hd)
+    err = np.abs(got - want).reshape(rows, n_head, hd).max(axis=2)
+    scale = np.abs(want).reshape(rows, n_head, hd).max(axis=2)
+    assert (err <= 2e-6 * np.maximum(scale, 1e-3)).all(), err.max()
+
+
+def test_attention_mfma_closed_forms(gpu):
+    """The MFMA kernel: one position returns v_0 bit for bit (one probability of exactly 1,
+    one sum of 1); equal keys over a long causal batch give each row the mean of the values it
+    sees."""
+    rng = np.random.default_rng(5)
+    hd, n_head, n_kv = 128, 8, 2
+    gpu.tune("attention_kernel", 2)
+    q = rng.standard_normal((1, n_head * hd)).astype(np.float32)
+    kc = rng.standard_normal((1, n_kv * hd)).astype(np.float32)
+    vc = rng.standard_normal((1, n_kv * hd)).astype(np.float32)
+    got = gpu.attention_dev(_dev(q), _dev(kc), _dev(vc), 0, n_head, n_kv, hd).cpu().numpy()
+    want = np.repeat(vc.reshape(n_kv, hd), n_head // n_kv, axis=0).reshape(1, -1)
+    assert np.array_equal(got, want)
+    rows, pos0 = 96, 300
+    L = pos0 + rows
+    q = rng.standard_normal((rows, n_head * hd)).astype(np.float32)
+    kc = np.tile(rng.standard_normal((1, n_kv * hd)).astype(np.float32), (L, 1))
+    vc = rng.standard_normal((L, n_kv * hd)).astype(np.float32)
+    got = gpu.attention_dev(_dev(q), _dev(kc), _dev(vc), pos0, n_head, n_kv, hd).cpu().numpy()
+    csum = np.cumsum(vc.astype(np.float64).reshape(L, n_kv, hd), axis=0)
+    for t in range(rows):
+        mean = csum[pos0 + t] / (pos0 + t + 1)
+        want = np.repeat(mean, n_head // n_kv, axis=0).reshape(-1)
+        assert np.abs(got[t] - want).max() <= 1e-6, t
 
 
 @pytest.mark.parametrize("hd,n_head,n_kv,pos0,base", [(128, 32, 8, 1024, 500000.0),
