@@ -1818,6 +1818,9 @@ int cllm_hip_tune(const char* knob, const int* values, int n_values) {
     } else if (std::strcmp(knob, "attention_kernel") == 0) {
         if (v(0) < 0 || v(0) > 2) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: attention_kernel is 0, 1 or 2");
         t.attention_kind.store(v(0));
+    } else if (std::strcmp(knob, "gemv_fp_wgs") == 0) {
+        if (v(0) < 0 || v(0) > 9) return set_err(CLLM_HIP_E_ARG, "cllm_hip_tune: gemv_fp_wgs is 0 to 9");
+        t.gemv_fp_wgs.store(v(0));
     } else if (std::strcmp(knob, "gemm_small_plan") == 0) {
         t.gemm_small_splits.store(v(0));
         t.gemm_small_kp.store(v(1));

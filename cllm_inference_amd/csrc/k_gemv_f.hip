@@ -6,10 +6,15 @@
 // dequantized to fp32 and dotted with the fp32 activation row, which is NOT quantized to
 // Q8_0. So here
 //     y[t, j] = bias[j] + sum_i x[t, i] * deq(W[j, i])
-// in fp32, with every dequantized value computed exactly as the reference's deq_* functions
-// compute it (quant.cpp:28-298: each is a product that fp32 holds exactly, or one rounding of
-// d * q + m), and one fma per element and activation row. Only the summation order differs:
-// lanes own 32-element units of a row and the partial sums are added across lanes.
+// in fp32. F32 and F16 take one fma per element and activation row. The quantized types
+// dequantize as w = A q + B over groups of 16 or 32 elements (q the element's small
+// non-negative or int8 code, A and B the group's scale and offset as the reference's deq_*
+// functions form them, quant.cpp:28-298), so the dot is regrouped per group:
+//     sum_i x_i w_i = A * sum_i x_i q_i + B * sum_i x_i,
+// one fma per element on the exact code, then two per group; the group sums of x are formed
+// once, with the activation rows' staging. Only the rounding order differs from the
+// reference (an exact product per element, a few roundings per group of 16 or 32): lanes own
+// 32-element units of a row and the partial sums are added across lanes.
 //
 // Work split. A unit is 32 consecutive elements of a row: 32 fp32 or fp16 values, one
 // Q4_1 / Q5_1 / Q8_1 block, or one eighth of a Q2_K / Q3_K super-block. A row's units are
@@ -19,8 +24,10 @@
 //
 // Activations. The MR activation rows of a workgroup's token group are staged in LDS as fp32
 // with 16 bytes of padding after every 32 values, so the 16-byte reads of the lanes (units at
-// a stride of 144 bytes) spread over all 64 banks. Rows too long for the LDS budget (80 KB,
-// two workgroups per CU) are read from global memory instead (they stay in L2).
+// a stride of 144 bytes) spread over all 64 banks, followed by the rows' sums of every 16
+// values (for the grouped types). Rows too long for the LDS budget (80 KB, two workgroups per
+// CU) are read from global memory instead (they stay in L2), and the quantized types then
+// take the per-element form: decode w, one fma per element.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -41,6 +48,41 @@ constexpr size_t kLdsBudget = 80 * 1024;  // two workgroups per CU
 // byte b (0..3) of dword v as a float: v_cvt_f32_ubyte{0..3}
 __device__ __forceinline__ float ubyte_f(uint32_t v, int b) {
     return (float)((v >> (8 * b)) & 0xFFu);
+}
+
+// The 16 codes held in the bytes of v[0..3] (element order; unsigned, or int8 when SIGNED) as
+// floats. The words pass through an empty asm first: the compiler knows which bits the
+// callers' masks clear and would otherwise turn each byte into a narrower bit-field extract
+// plus v_cvt_f32_ubyte0, instead of one v_cvt_f32_ubyte{0..3}.
+template <bool SIGNED>
+__device__ __forceinline__ void codes16(const uint32_t (&v)[4], float (&c)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t w = v[i];
+        asm volatile("" : "+v"(w));
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+            c[4 * i + b] = SIGNED ? (float)(int8_t)((w >> (8 * b)) & 0xFFu) : ubyte_f(w, b);
+    }
+}
+
+// sum over 16 elements of x[e] * c[e], x 16 consecutive floats (16-byte aligned), in order
+__device__ __forceinline__ float dot16(const float (&c)[16], const float* x) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 xv = *(const float4*)(x + 4 * i);
+        s = __builtin_fmaf(xv.x, c[4 * i], s);
+        s = __builtin_fmaf(xv.y, c[4 * i + 1], s);
+        s = __builtin_fmaf(xv.z, c[4 * i + 2], s);
+        s = __builtin_fmaf(xv.w, c[4 * i + 3], s);
+    }
+    return s;
+}
+
+// bits 0..3 of h (h < 16) to bit 4 of bytes 0..3: h * 0x204081 puts bit j at bit 8 j
+__device__ __forceinline__ uint32_t spread4_bit4(uint32_t h) {
+    return ((h * 0x00204081u) & 0x01010101u) << 4;
 }
 
 // ------------------------------------------------------------------------- unit decoders
@@ -114,6 +156,21 @@ template <> struct FUnit<T_Q8_1> {
             for (int b = 0; b < 4; ++b)
                 w[4 * i + b] = d * (float)(int8_t)((q[i] >> (8 * b)) & 0xFFu);
     }
+    // w = d q: A = d, no offset
+    template <int MR>
+    __device__ __forceinline__ static void gdot(const Raw& r, int, const float* xp, int xstride,
+                                                const float*, int, float (&acc)[MR]) {
+        const float d = f16_to_f32(r.a.x & 0xFFFFu);
+        const uint32_t q0[4] = {r.a.y, r.a.z, r.a.w, r.b.x}, q1[4] = {r.b.y, r.b.z, r.b.w, r.c};
+        float c0[16], c1[16];
+        codes16<true>(q0, c0);
+        codes16<true>(q1, c1);
+#pragma unroll
+        for (int t = 0; t < MR; ++t) {
+            const float* xt = xp + (size_t)t * xstride;
+            acc[t] = __builtin_fmaf(d, dot16(c0, xt) + dot16(c1, xt + 16), acc[t]);
+        }
+    }
 };
 
 // Q4_1: [d][m][qs 16 B], 20 bytes; byte j: low nibble = element j, high = element j + 16;
@@ -138,6 +195,29 @@ template <> struct FUnit<T_Q4_1> {
                 w[4 * i + b] = __builtin_fmaf(d, ubyte_f(lo, b), m);
                 w[16 + 4 * i + b] = __builtin_fmaf(d, ubyte_f(hi, b), m);
             }
+        }
+    }
+    // w = d q + m over the 32 elements: A = d, B = m
+    template <int MR>
+    __device__ __forceinline__ static void gdot(const Raw& r, int, const float* xp, int xstride,
+                                                const float* xg, int gstride, float (&acc)[MR]) {
+        const float d = f16_to_f32(r.dm & 0xFFFFu), m = f16_to_f32(r.dm >> 16);
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo[i] = q[i] & 0x0F0F0F0Fu;
+            hi[i] = (q[i] >> 4) & 0x0F0F0F0Fu;
+        }
+        float c0[16], c1[16];
+        codes16<false>(lo, c0);
+        codes16<false>(hi, c1);
+#pragma unroll
+        for (int t = 0; t < MR; ++t) {
+            const float* xt = xp + (size_t)t * xstride;
+            const float s = dot16(c0, xt) + dot16(c1, xt + 16);
+            const float xsum = xg[(size_t)t * gstride] + xg[(size_t)t * gstride + 1];
+            acc[t] = __builtin_fmaf(m, xsum, __builtin_fmaf(d, s, acc[t]));
         }
     }
 };
@@ -170,6 +250,30 @@ template <> struct FUnit<T_Q5_1> {
                 w[4 * i + b] = __builtin_fmaf(d, ubyte_f(lo, b), m);
                 w[16 + 4 * i + b] = __builtin_fmaf(d, ubyte_f(hi, b), m);
             }
+        }
+    }
+    // w = d q + m over the 32 elements (q 5 bits): A = d, B = m
+    template <int MR>
+    __device__ __forceinline__ static void gdot(const Raw& r, int, const float* xp, int xstride,
+                                                const float* xg, int gstride, float (&acc)[MR]) {
+        const float d = f16_to_f32(r.dmh.x & 0xFFFFu), m = f16_to_f32(r.dmh.x >> 16);
+        const uint32_t qh = r.dmh.y;
+        const uint32_t q[4] = {r.qs.x, r.qs.y, r.qs.z, r.qs.w};
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo[i] = (q[i] & 0x0F0F0F0Fu) | spread4_bit4((qh >> (4 * i)) & 0xFu);
+            hi[i] = ((q[i] >> 4) & 0x0F0F0F0Fu) | spread4_bit4((qh >> (16 + 4 * i)) & 0xFu);
+        }
+        float c0[16], c1[16];
+        codes16<false>(lo, c0);
+        codes16<false>(hi, c1);
+#pragma unroll
+        for (int t = 0; t < MR; ++t) {
+            const float* xt = xp + (size_t)t * xstride;
+            const float s = dot16(c0, xt) + dot16(c1, xt + 16);
+            const float xsum = xg[(size_t)t * gstride] + xg[(size_t)t * gstride + 1];
+            acc[t] = __builtin_fmaf(m, xsum, __builtin_fmaf(d, s, acc[t]));
         }
     }
 };
@@ -409,7 +513,28 @@ template <> struct FUnit<T_Q6_K> {
 
 // ------------------------------------------------------------------------------ kernel
 
+
 __host__ __device__ constexpr int xpad_row(int k) { return k + k / 8; }  // floats per LDS row
+
+// Types whose dot is regrouped per 32 elements (gdot), from the LDS-staged activations.
+// Q2_K and Q3_K keep the per-element form: regrouped per 16 elements they measured no faster
+// on one activation row at 14336 x 4096 (Q2_K 12.6 us either way; Q3_K 15.8, with whole
+// half-super-block items per lane 14.1) and, as half-super-block items, slower on four
+// (63 / 65 us against 52 / 56). A batch row and the same row alone must take one path.
+__host__ __device__ constexpr bool grouped(uint32_t T) {
+    return T == T_Q4_1 || T == T_Q5_1 || T == T_Q8_1;
+}
+// LDS floats per staged activation row: the padded row, and the sums of its 16-value groups
+__host__ __device__ constexpr int xlds_row(uint32_t T, int k) { return xpad_row(k) + (grouped(T) ? k / 16 : 0); }
+
+// Workgroups per CU of the pipelined kernel for one activation row, 0 where the per-row
+// kernel is faster (MI355X, 14336 x 4096, cold weights, us, per-row kernel against the
+// pipelined one at 3 / 4 / 8 workgroups per CU: Q4_1 12.9 against 12.4 / 11.7 / 12.3, Q5_1
+// 14.2 against 13.8 / 13.5 / 14.1; Q8_1 15.3 against 15.5 / 15.9 / 16.2)
+template <uint32_t T>
+constexpr int fp_wgs_per_cu() {
+    return T == T_Q4_1 || T == T_Q5_1 ? 4 : 0;
+}
 
 template <int MR>
 __device__ __forceinline__ void fma_unit(const float (&w)[32], const float* xp, int xstride,
@@ -428,6 +553,30 @@ __device__ __forceinline__ void fma_unit(const float (&w)[32], const float* xp, 
     }
 }
 
+// Stages the MR activation rows from t0 (zeros past m) in LDS with the 16-byte pad per 32
+// values; with GS a quad of lanes (16 consecutive values, never across rows: k / 4 is a
+// multiple of 4) also forms the group's sum, in a fixed order, into xg[t][k / 16]. Ends with
+// a workgroup barrier.
+template <int MR, bool GS>
+__device__ __forceinline__ void stage_rows(const float* __restrict__ x, int k, int m, int t0, float* xs,
+                                           float* xg) {
+    const int q4 = k / 4;
+    const int srow = xpad_row(k), gstride = k / 16;
+    for (int i = threadIdx.x; i < MR * q4; i += kThreads) {
+        const int t = i / q4, e = 4 * (i - t * q4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t0 + t < m) v = *(const float4*)(x + (size_t)(t0 + t) * k + e);
+        *(float4*)(xs + t * srow + e + (e >> 5) * 4) = v;
+        if constexpr (GS) {
+            float p = (v.x + v.y) + (v.z + v.w);
+            p += dpp_f32<DPP_QUAD_SWAP1>(p);
+            p += dpp_f32<DPP_QUAD_SWAP2>(p);
+            if ((i & 3) == 0) xg[t * gstride + (e >> 4)] = p;
+        }
+    }
+    __syncthreads();
+}
+
 // grid (row workgroups, token groups of MR), 256 threads. lpr_log2 = log2(lanes per row).
 template <uint32_t T, int MR, bool XG>
 __global__ __launch_bounds__(kThreads) void k_gemv_f(const uint8_t* __restrict__ w,
@@ -436,21 +585,14 @@ __global__ __launch_bounds__(kThreads) void k_gemv_f(const uint8_t* __restrict__
                                                      const float* __restrict__ bias,
                                                      float* __restrict__ y, int lpr_log2) {
     using U = FUnit<T>;
+    constexpr bool GDOT = grouped(T) && !XG;
     extern __shared__ __align__(16) float xs[];
     const int t0 = blockIdx.y * MR;
     const int units = k / 32;
     const int srow = xpad_row(k);
-    if constexpr (!XG) {
-        // stage the token group's rows (zeros past m) with the 16-byte pad per 32 values
-        const int q4 = k / 4;
-        for (int i = threadIdx.x; i < MR * q4; i += kThreads) {
-            const int t = i / q4, e = 4 * (i - t * q4);
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (t0 + t < m) v = *(const float4*)(x + (size_t)(t0 + t) * k + e);
-            *(float4*)(xs + t * srow + e + (e >> 5) * 4) = v;
-        }
-        __syncthreads();
-    }
+    const int gstride = k / 16;
+    float* xg = xs + MR * srow;  // GDOT: [t][k / 16] sums of 16 activations
+    if constexpr (!XG) stage_rows<MR, GDOT>(x, k, m, t0, xs, xg);
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
     const int sub = lane & (lpr - 1);
@@ -468,16 +610,41 @@ __global__ __launch_bounds__(kThreads) void k_gemv_f(const uint8_t* __restrict__
         float acc[MR];
 #pragma unroll
         for (int t = 0; t < MR; ++t) acc[t] = 0.0f;
-        for (int u = sub; u < units; u += 2 * lpr) {
-            const bool two = u + lpr < units;
-            const typename U::Raw r0 = U::load(row, u);
-            const typename U::Raw r1 = U::load(row, two ? u + lpr : u);
-            float wv[32];
-            U::decode(r0, u, wv);
-            fma_unit<MR>(wv, xptr(u), xstride, acc);
-            if (two) {
-                U::decode(r1, u + lpr, wv);
-                fma_unit<MR>(wv, xptr(u + lpr), xstride, acc);
+        if constexpr (GDOT) {
+            // each lane two units at a time. Both units' loads go out before either is used:
+            // when some lane of the wave has a second unit (u - sub is wave-uniform), every
+            // lane computes one (a lane without one takes unit u again and keeps its sums).
+            // Under a per-lane branch the second unit's loads would be issued after the first
+            // one's arithmetic, and each row would take two round trips.
+            for (int u = sub; u < units; u += 2 * lpr) {
+                const bool two = u + lpr < units;
+                if (u - sub + lpr < units) {
+                    const int u1 = two ? u + lpr : u;
+                    const typename U::Raw r0 = U::load(row, u);
+                    const typename U::Raw r1 = U::load(row, u1);
+                    U::template gdot<MR>(r0, u, xptr(u), xstride, xg + 2 * u, gstride, acc);
+                    float acc1[MR];
+#pragma unroll
+                    for (int t = 0; t < MR; ++t) acc1[t] = acc[t];
+                    U::template gdot<MR>(r1, u1, xptr(u1), xstride, xg + 2 * u1, gstride, acc1);
+#pragma unroll
+                    for (int t = 0; t < MR; ++t) acc[t] = two ? acc1[t] : acc[t];
+                } else {
+                    U::template gdot<MR>(U::load(row, u), u, xptr(u), xstride, xg + 2 * u, gstride, acc);
+                }
+            }
+        } else {
+            for (int u = sub; u < units; u += 2 * lpr) {
+                const bool two = u + lpr < units;
+                const typename U::Raw r0 = U::load(row, u);
+                const typename U::Raw r1 = U::load(row, two ? u + lpr : u);
+                float wv[32];
+                U::decode(r0, u, wv);
+                fma_unit<MR>(wv, xptr(u), xstride, acc);
+                if (two) {
+                    U::decode(r1, u + lpr, wv);
+                    fma_unit<MR>(wv, xptr(u + lpr), xstride, acc);
+                }
             }
         }
 #pragma unroll
@@ -490,6 +657,80 @@ __global__ __launch_bounds__(kThreads) void k_gemv_f(const uint8_t* __restrict__
                 if (t0 + t < m) y[(size_t)(t0 + t) * n + j] = acc[t] + b;
         }
     }
+}
+
+// The grouped types on rows of at most two units per lane, activations in LDS (staged as for
+// k_gemv_f). Each wave walks rows rb, rb + step, .. and issues the next row's loads before
+// the current row's arithmetic, unconditionally (rows past the matrix read the last row
+// again, units past a short row the last unit), so that a wave keeps a row of loads in
+// flight while it computes. (k_gemv_f gives every wave about one row at these sizes: the
+// whole matrix is requested at once and no arithmetic overlaps the transfer.) The per-row
+// arithmetic is k_gemv_f's, in the same order, so the two kernels agree bit for bit.
+// grid (row workgroups, token groups of MR), 256 threads.
+template <uint32_t T, int MR>
+__global__ __launch_bounds__(kThreads) void k_gemv_fp(const uint8_t* __restrict__ w,
+                                                      size_t row_bytes, int k, int n, int m,
+                                                      const float* __restrict__ x,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ y, int lpr_log2) {
+    using U = FUnit<T>;
+    static_assert(grouped(T), "the grouped types only");
+    extern __shared__ __align__(16) float xs[];
+    const int t0 = blockIdx.y * MR;
+    const int srow = xpad_row(k);
+    const int gstride = k / 16;
+    float* xg = xs + MR * srow;
+    stage_rows<MR, true>(x, k, m, t0, xs, xg);
+
+    const int lane = threadIdx.x & 63;
+    const int lpr = 1 << lpr_log2;
+    const int sub = lane & (lpr - 1);
+    const int rpw = 64 >> lpr_log2;
+    const int step = (int)gridDim.x * kWaves * rpw;
+    const int units = k / 32;
+    const bool has0 = sub < units, has1 = sub + lpr < units;
+    const int u0 = min(sub, units - 1), u1 = min(sub + lpr, units - 1);
+    auto row_at = [&](int rb) {
+        return w + (size_t)min(rb + (lane >> lpr_log2), n - 1) * row_bytes;
+    };
+    const int rb0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * rpw;
+    if (rb0 >= n) return;  // wave-uniform, after the last barrier
+    // NI units per lane (2 when some lane's row has a second one, else 1: uniform)
+    auto walk = [&]<int NI>() {
+        typename U::Raw a0 = U::load(row_at(rb0), u0);
+        typename U::Raw a1 = U::load(row_at(rb0), NI == 2 ? u1 : u0);
+        for (int rb = rb0; rb < n; rb += step) {
+            const typename U::Raw c0 = a0;
+            const typename U::Raw c1 = a1;
+            a0 = U::load(row_at(rb + step), u0);
+            if constexpr (NI == 2) a1 = U::load(row_at(rb + step), u1);
+            float acc[MR], acc1[MR];
+#pragma unroll
+            for (int t = 0; t < MR; ++t) acc[t] = 0.0f;
+            U::template gdot<MR>(c0, u0, xs + 36 * u0, srow, xg + 2 * u0, gstride, acc);
+            if constexpr (NI == 2) {
+#pragma unroll
+                for (int t = 0; t < MR; ++t) acc1[t] = acc[t];
+                U::template gdot<MR>(c1, u1, xs + 36 * u1, srow, xg + 2 * u1, gstride, acc1);
+            }
+#pragma unroll
+            for (int t = 0; t < MR; ++t) acc[t] = (NI == 2 && has1) ? acc1[t] : (has0 ? acc[t] : 0.0f);
+#pragma unroll
+            for (int t = 0; t < MR; ++t)
+                for (int off = lpr >> 1; off > 0; off >>= 1) acc[t] += __shfl_xor(acc[t], off, 64);
+            const int j = rb + (lane >> lpr_log2);
+            if (sub == 0 && j < n) {
+                const float b = bias ? bias[j] : 0.0f;
+#pragma unroll
+                for (int t = 0; t < MR; ++t)
+                    if (t0 + t < m) y[(size_t)(t0 + t) * n + j] = acc[t] + b;
+            }
+        }
+    };
+    if (lpr < units)
+        walk.template operator()<2>();
+    else
+        walk.template operator()<1>();
 }
 
 // F32 / F16 rows whose length is not a multiple of 32: one wave per row, lanes stride over
@@ -544,7 +785,22 @@ hipError_t launch_mr(const uint8_t* w, size_t row_bytes, int k, int n, int m, co
                                           (int64_t)device_cus_f() * 8);
     const int groups = (m + MR - 1) / MR;
     if (groups > 65535) return hipErrorInvalidConfiguration;
-    const size_t lds = XG ? 0 : (size_t)MR * xpad_row(k) * sizeof(float);
+    const size_t lds = XG ? 0 : (size_t)MR * xlds_row(T, k) * sizeof(float);
+    if constexpr (grouped(T) && !XG && MR == 1) {
+        // rows of at most two units per lane take the pipelined kernel where it is the
+        // faster one, on fp_wgs_per_cu workgroups per CU (fewer if the rows run out). The
+        // tuning knob "gemv_fp_wgs" forces it at 1 to 8 workgroups per CU, or (9) the per-row
+        // kernel.
+        const int knob = tuning().gemv_fp_wgs.load(std::memory_order_relaxed);
+        const int per_cu = knob == 0 ? fp_wgs_per_cu<T>() : knob == 9 ? 0 : knob;
+        if (units <= 2 * (1 << lpr_log2) && per_cu > 0) {
+            const int64_t fwgs = std::min<int64_t>((row_groups + kWaves - 1) / kWaves,
+                                                   (int64_t)device_cus_f() * per_cu);
+            hipLaunchKernelGGL((k_gemv_fp<T, MR>), dim3((unsigned)fwgs, (unsigned)groups),
+                               dim3(kThreads), lds, stream, w, row_bytes, k, n, m, x, bias, y, lpr_log2);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((k_gemv_f<T, MR, XG>), dim3((unsigned)wgs, (unsigned)groups),
                        dim3(kThreads), lds, stream, w, row_bytes, k, n, m, x, bias, y, lpr_log2);
     return hipGetLastError();
@@ -563,7 +819,7 @@ hipError_t launch_type(const uint8_t* w, int k, int n, int m, const float* x, co
             return hipGetLastError();
         }
     }
-    const size_t row_lds = (size_t)xpad_row(k) * sizeof(float);
+    const size_t row_lds = (size_t)xlds_row(T, k) * sizeof(float);
     if (m >= 3 && 4 * row_lds <= kLdsBudget)
         return launch_mr<T, 4, false>(w, row_bytes, k, n, m, x, bias, y, stream);
     if (m >= 2 && 2 * row_lds <= kLdsBudget)

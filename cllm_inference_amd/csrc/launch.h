@@ -25,6 +25,7 @@ struct Tuning {
     std::atomic<int> gemm_small_q8{0};    // fp32 batches: 0 planner, 1 quantized once first, 2 in-kernel
     std::atomic<int> gemv_fused_rows{0};  // streamed GEMV batches quantized in-kernel up to this many rows
     std::atomic<int> attention_kind{0};   // attention: 0 planner, 1 split kernel, 2 MFMA kernel
+    std::atomic<int> gemv_fp_wgs{0};  // one-row float-dot GEMV: 0 planner, 1-8 pipelined kernel at that many workgroups per CU, 9 per-row kernel
 };
 Tuning& tuning();
 

@@ -40,7 +40,7 @@ def orc():
 # every process-wide kernel-choice override of cllm_hip_tune
 TUNING_KNOBS = ("gemm_kernel", "gemm_tiles", "gemm_splits", "gemv_kernel", "gemv_str_grid",
                 "gemm_small", "gemm_small_plan", "gemm_small_q8", "gemv_fused_rows", "gemv_waves",
-                "attention_kernel")
+                "attention_kernel", "gemv_fp_wgs")
 
 
 @pytest.fixture(autouse=True)

@@ -81,6 +81,34 @@ def test_fdot_edge_shapes(gpu, orc, qt):
         check_close(y, yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k} m{m}")
 
 
+@pytest.mark.parametrize("qt", [S.Q4_1, S.Q5_1, S.Q8_1])
+def test_fdot_pipelined_equals_per_row_kernel(gpu, orc, qt):
+    """One activation row of the types whose dot is regrouped per block (A * sum x q + B *
+    sum x): the pipelined kernel (each wave walks rows, the next row's loads in flight; knob
+    gemv_fp_wgs 1-8 workgroups per CU) and the per-row kernel (9) make the same per-row
+    additions, so they agree bit for bit, on grids from one workgroup per CU (many rows per
+    wave) to more than the rows. The shapes cover short rows (lanes with no unit), one and
+    two units per lane, rows past the pipelined kernel's reach (K = 8192: three or more units
+    per lane, the per-row kernel whatever the knob) and rows past the grid's last wave."""
+    import cllm_inference_amd as C
+    for n, k in ((75, 256), (1000, 896), (333, 2048), (2500, 4096), (64, 8192)):
+        if k % S.BLOCK[qt]:
+            continue
+        print("fdot pipelined", S.TYPE_NAMES[qt], n, k, flush=True)
+        w = S.make_weight(qt, n, k, 5 * n + k)
+        x = S.make_activation(1, k, n + 3, outliers=True)
+        C.tune("gemv_fp_wgs", 9)
+        ref = gpu.matmul_quant(x[0], w, qt, None, k, n)
+        for knob in (1, 2, 3, 4, 8, 0):
+            C.tune("gemv_fp_wgs", knob)
+            y = gpu.matmul_quant(x[0], w, qt, None, k, n)
+            assert np.array_equal(bits(y), bits(ref)), (S.TYPE_NAMES[qt], n, k, knob)
+        C.tune("gemv_fp_wgs")
+        exact, abs_sum = orc.matmul_f64(x, w, qt, None, k, n, 1)
+        yo = orc.matmul(x, w, qt, None, k, n, 1)
+        check_close(ref[None], yo, exact, abs_sum, f"{S.TYPE_NAMES[qt]} {n}x{k}")
+
+
 def test_fdot_output_head_sample_rows(gpu, orc):
     """An F16 output head of Qwen2.5-0.5B's shape (151936 x 896) on the device path; every
     1024th row is checked against the oracle (the rows are independent)."""
