@@ -557,12 +557,12 @@ __device__ __forceinline__ void fma_unit(const float (&w)[32], const float* xp, 
 // values; with GS a quad of lanes (16 consecutive values, never across rows: k / 4 is a
 // multiple of 4) also forms the group's sum, in a fixed order, into xg[t][k / 16]. Ends with
 // a workgroup barrier.
-template <int MR, bool GS>
+template <int MR, bool GS, int NT = kThreads>
 __device__ __forceinline__ void stage_rows(const float* __restrict__ x, int k, int m, int t0, float* xs,
                                            float* xg) {
     const int q4 = k / 4;
     const int srow = xpad_row(k), gstride = k / 16;
-    for (int i = threadIdx.x; i < MR * q4; i += kThreads) {
+    for (int i = threadIdx.x; i < MR * q4; i += NT) {
         const int t = i / q4, e = 4 * (i - t * q4);
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t0 + t < m) v = *(const float4*)(x + (size_t)(t0 + t) * k + e);
@@ -577,9 +577,9 @@ __device__ __forceinline__ void stage_rows(const float* __restrict__ x, int k, i
     __syncthreads();
 }
 
-// grid (row workgroups, token groups of MR), 256 threads. lpr_log2 = log2(lanes per row).
-template <uint32_t T, int MR, bool XG>
-__global__ __launch_bounds__(kThreads) void k_gemv_f(const uint8_t* __restrict__ w,
+// grid (row workgroups, token groups of MR), NT threads. lpr_log2 = log2(lanes per row).
+template <uint32_t T, int MR, bool XG, int NT = kThreads>
+__global__ __launch_bounds__(NT) void k_gemv_f(const uint8_t* __restrict__ w,
                                                      size_t row_bytes, int k, int n, int m,
                                                      const float* __restrict__ x,
                                                      const float* __restrict__ bias,
@@ -592,13 +592,13 @@ __global__ __launch_bounds__(kThreads) void k_gemv_f(const uint8_t* __restrict__
     const int srow = xpad_row(k);
     const int gstride = k / 16;
     float* xg = xs + MR * srow;  // GDOT: [t][k / 16] sums of 16 activations
-    if constexpr (!XG) stage_rows<MR, GDOT>(x, k, m, t0, xs, xg);
+    if constexpr (!XG) stage_rows<MR, GDOT, NT>(x, k, m, t0, xs, xg);
     const int lane = threadIdx.x & 63;
     const int lpr = 1 << lpr_log2;
     const int sub = lane & (lpr - 1);
     const int rpw = 64 >> lpr_log2;  // rows per wave
-    const int gw = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    const int nw = gridDim.x * kWaves;
+    const int gw = blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int nw = gridDim.x * (NT / 64);
     // activation source: LDS rows, or global rows clamped to the last valid one
     const float* xbase = XG ? x + (size_t)min(t0, m - 1) * k : xs;
     const int xstride = XG ? k : srow;
@@ -798,6 +798,25 @@ hipError_t launch_mr(const uint8_t* w, size_t row_bytes, int k, int n, int m, co
                                                    (int64_t)device_cus_f() * per_cu);
             hipLaunchKernelGGL((k_gemv_fp<T, MR>), dim3((unsigned)fwgs, (unsigned)groups),
                                dim3(kThreads), lds, stream, w, row_bytes, k, n, m, x, bias, y, lpr_log2);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (MR >= 2 && !XG) {
+        // Several activation rows whose staging takes more than 20 KB of LDS run on 1024-thread
+        // workgroups. LDS then holds fewer than eight 256-thread workgroups per CU (four rows
+        // of 4096, ~78 KB: two), which left each wave's row loads exposed (MI355X, 14336 x
+        // 4096 at 4 rows, cold weights, us, 256 / 1024 threads: Q2_K 51.3 / 21.8, Q4_1 50.5 /
+        // 25.8, Q8_1 54.6 / 28.3, F16 56.4 / 32.9, F32 78.2 / 57.7). Shorter rows keep 256
+        // threads (the F16 151936 x 896 head at 4 rows, 16 KB: 61.9 against 78.4 us). The
+        // grid is the workgroups resident at once (two per CU; waves walk further rows): more
+        // would restage the rows in every later workgroup. Same bits either way: a row's
+        // additions do not depend on the workgroup size.
+        if (lds > 20 * 1024) {
+            constexpr int NT = 1024;
+            const int64_t wgs_nt = std::min<int64_t>((row_groups + NT / 64 - 1) / (NT / 64),
+                                                     (int64_t)device_cus_f() * 2);
+            hipLaunchKernelGGL((k_gemv_f<T, MR, XG, NT>), dim3((unsigned)wgs_nt, (unsigned)groups),
+                               dim3(NT), lds, stream, w, row_bytes, k, n, m, x, bias, y, lpr_log2);
             return hipGetLastError();
         }
     }
