@@ -384,6 +384,9 @@ const char* cllm_hip_matmul_plan(uint32_t type, int in_dim, int out_dim, int n_r
  *                  quantized inside its launch (0 = the default)
  *   "attention_kernel" 0 the default, 1 the sequence-split kernel, 2 the many-row MFMA kernel
  *                  (decode with fused RoPE always takes the split kernel)
+ *   "gemv_fp_wgs"  one activation row of Q4_1 / Q5_1 / Q8_1 (float dot), rows of up to two
+ *                  blocks per lane: 0 the default, 1 to 8 the pipelined row walk at that many
+ *                  workgroups per CU, 9 the per-row kernel
  * Missing values count as 0, so n_values = 0 resets a knob. Takes effect on the next call. */
 int cllm_hip_tune(const char* knob, const int* values, int n_values);
 
