@@ -649,13 +649,19 @@ struct StageCopy {
 // is commutative), leaving its wave sums 2w and 2w + 1 in lanes 0 and 32 of wave w; waves
 // past the eighth hold no elements. RAWBAR: the workgroup barrier waits for LDS writes only
 // (k_gemv_st, whose LDS-DMA weight loads a fenced barrier would wait for too).
-template <uint32_t T, int MR, bool NORM = false, bool RAWBAR = false>
+//
+// SP slots per thread go out with issue_all() and are quantized by commit() (SP = 2: both
+// before the caller's next loads, so a batch of up to 2 x blockDim slots is staged after
+// one round trip); rest() takes the slots past SP x blockDim.
+template <uint32_t T, int MR, bool NORM = false, bool RAWBAR = false, int SP = 1>
 struct StageQuant {
     using Tr = typename TraitsOf<T>::type;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
+    static_assert(SP == 1 || (SP == 2 && !NORM), "two slots per thread without the RMSNorm");
     const float* __restrict__ x;
     int k;
     f32x4 v[2];
+    f32x4 v2[2] = {};  // SP = 2: the thread's second slot
     const float* __restrict__ nw = nullptr;  // NORM: the norm weight
     float eps = 0.0f;
     float* part = nullptr;                   // NORM: 16 floats of LDS
@@ -711,6 +717,7 @@ struct StageQuant {
     // first use at vmcnt(loads issued since), so those loads stay in flight meanwhile.
     __device__ __forceinline__ void issue_all() {
         load_slot(threadIdx.x, v);
+        if constexpr (SP == 2) load_slot(threadIdx.x + blockDim.x, v2);
         if constexpr (NORM) {
             const f32x4* p = (const f32x4*)(nw + (size_t)min((int)threadIdx.x, slots() - 1) * 8);
             wv[0] = p[0];
@@ -758,9 +765,13 @@ struct StageQuant {
     __device__ __forceinline__ void commit(const ActLds& a) {
         if constexpr (NORM) normalize();
         if (wave_live() && (int)threadIdx.x < slots()) quant_slot(a, threadIdx.x, v);
+        if constexpr (SP == 2) {
+            const int i = (int)(threadIdx.x + blockDim.x);
+            if (i < slots()) quant_slot(a, i, v2);
+        }
     }
     __device__ __forceinline__ void rest(const ActLds& a) const {
-        for (int base = blockDim.x; base < slots(); base += blockDim.x) {
+        for (int base = SP * blockDim.x; base < slots(); base += blockDim.x) {
             const int i = base + threadIdx.x;
             if (i < slots()) {
                 f32x4 r[2];
@@ -1240,7 +1251,9 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_b
     };
 
     const ActLds a = act_layout<T, MR>(lds, k);
-    StageQuant<T, MR, NORM> sq{x_f32, k, {}};
+    // several rows stage two slots per thread up front: a second pass would issue its loads
+    // after item 0's, and waiting for them would wait for the item too
+    StageQuant<T, MR, NORM, false, (MR >= 2 ? 2 : 1)> sq{x_f32, k, {}};
     StageCopy<T, MR> sc{qs, xs, xb, k, {}, {}, {}};
     __shared__ float norm_part[16];
     if constexpr (NORM) {
