@@ -1251,9 +1251,10 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_b
     };
 
     const ActLds a = act_layout<T, MR>(lds, k);
-    // several rows stage two slots per thread up front: a second pass would issue its loads
-    // after item 0's, and waiting for them would wait for the item too
-    StageQuant<T, MR, NORM, false, (MR >= 2 ? 2 : 1)> sq{x_f32, k, {}};
+    // several rows, or rows longer than 8192, stage two slots per thread up front: a second
+    // pass would issue its loads after item 0's, and waiting for them would wait for the item
+    // too (the RMSNorm staging takes rows of at most 4096)
+    StageQuant<T, MR, NORM, false, ((MR >= 2 || XR == 0) && !NORM ? 2 : 1)> sq{x_f32, k, {}};
     StageCopy<T, MR> sc{qs, xs, xb, k, {}, {}, {}};
     __shared__ float norm_part[16];
     if constexpr (NORM) {
