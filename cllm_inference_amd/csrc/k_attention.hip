@@ -73,7 +73,8 @@ constexpr int kAttnCounters = 1024;  // (row, KV head) pairs a split launch may 
 constexpr int kMaxSplits = 256;      // sequence splits per (row, KV head)
 
 // HD = head_dim (multiple of 64, at most 256). Partials of split z for query head hq of row
-// t: part[((t * n_head + hq) * S + z) * (HD + 2) + ...] = unnormalised output [HD], max, sum.
+// t: part[((t * n_head + hq) * S + z) * (HD + 4) + ...] = unnormalised output [HD], max, sum
+// (two floats of padding keep every row 16-byte aligned for the combine's vector loads).
 // With one split, the normalised output goes straight to out.
 //
 // rope_base > 0 (one query row, a decode step): the queries and the key row at pos0 arrive
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void k_attention(
     for (int o = threadIdx.x; o < n_rep * HD; o += kThreads) {
         const int r = o / HD, d = o - r * HD;
         const float v = (wpart[0][o] + wpart[1][o]) + (wpart[2][o] + wpart[3][o]);
-        float* pp = part + (((size_t)t * n_head + kvh * n_rep + r) * S + z) * (HD + 2);
+        float* pp = part + (((size_t)t * n_head + kvh * n_rep + r) * S + z) * (HD + 4);
         __hip_atomic_store(pp + d, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (d == 0) {
             __hip_atomic_store(pp + HD, m_run[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -319,7 +320,7 @@ __global__ __launch_bounds__(kThreads) void k_attention(
     float* mz = &wpart[0][0];  // the wave partials are consumed: reuse as [kMaxRep][S] maxima
     for (int i = threadIdx.x; i < n_rep * S; i += kThreads) {
         const int r = i / S, zz = i - r * S;
-        const float* pz = part + (((size_t)t * n_head + kvh * n_rep + r) * S + zz) * (HD + 2);
+        const float* pz = part + (((size_t)t * n_head + kvh * n_rep + r) * S + zz) * (HD + 4);
         mz[r * S + zz] = ld(pz + HD);
         wz[r][zz] = ld(pz + HD + 1);  // the sums for now
     }
@@ -338,27 +339,51 @@ __global__ __launch_bounds__(kThreads) void k_attention(
         lsum[r] = den;
     }
     __syncthreads();
-    for (int o = threadIdx.x; o < n_rep * HD; o += kThreads) {
-        const int r = o / HD, d = o - r * HD;
-        const float* pp = part + ((size_t)t * n_head + kvh * n_rep + r) * S * (HD + 2) + d;
-        float num = 0.0f;
+    // Each thread takes four consecutive dims of one head and reads them as one 16-byte
+    // load per split: a buffer load with the SC1 bit, the same device-scope cache policy as
+    // the agent-scope atomic loads above, over this (row, KV head)'s partial rows. Sixteen
+    // splits at a time are in flight; per output the additions are in split order.
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    const float* pg = part + ((size_t)t * n_head + kvh * n_rep) * S * (HD + 4);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)pg, (short)0, (int)((size_t)n_rep * S * (HD + 4) * sizeof(float)), 0x00020000);
+    auto ld4 = [&](uint32_t off) {
+        return __builtin_bit_cast(f32x4v, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, 16));
+    };
+    constexpr int Q = HD / 4;
+    for (int o = threadIdx.x; o < n_rep * Q; o += kThreads) {
+        const int r = o / Q, d = 4 * (o - r * Q);
+        const uint32_t off0 = (uint32_t)((r * S * (HD + 4) + d) * sizeof(float));
+        const uint32_t zstep = (uint32_t)((HD + 4) * sizeof(float));
+        f32x4v num = {0.0f, 0.0f, 0.0f, 0.0f};
+        auto add = [&](float wgt, f32x4v v) {
+            num.x = __builtin_fmaf(wgt, v.x, num.x);
+            num.y = __builtin_fmaf(wgt, v.y, num.y);
+            num.z = __builtin_fmaf(wgt, v.z, num.z);
+            num.w = __builtin_fmaf(wgt, v.w, num.w);
+        };
         int zz = 0;
         for (; zz + 16 <= S; zz += 16) {
-            float v[16];
+            f32x4v v[16];
 #pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = ld(pp + (size_t)(zz + u) * (HD + 2));
+            for (int u = 0; u < 16; ++u) v[u] = ld4(off0 + (uint32_t)(zz + u) * zstep);
 #pragma unroll
-            for (int u = 0; u < 16; ++u) num = __builtin_fmaf(wz[r][zz + u], v[u], num);
+            for (int u = 0; u < 16; ++u) add(wz[r][zz + u], v[u]);
         }
         if (zz < S) {  // the last S % 16, also loaded together (one round trip, same order)
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) v[u] = zz + u < S ? ld(pp + (size_t)(zz + u) * (HD + 2)) : 0.0f;
+            f32x4v v[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u)
-                if (zz + u < S) num = __builtin_fmaf(wz[r][zz + u], v[u], num);
+                v[u] = zz + u < S ? ld4(off0 + (uint32_t)(zz + u) * zstep) : f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int u = 0; u < 16; ++u)
+                if (zz + u < S) add(wz[r][zz + u], v[u]);
         }
-        out[((size_t)t * n_head + kvh * n_rep + r) * HD + d] = __fdiv_rn(num, lsum[r]);
+        float* op = out + ((size_t)t * n_head + kvh * n_rep + r) * HD + d;
+        op[0] = __fdiv_rn(num.x, lsum[r]);
+        op[1] = __fdiv_rn(num.y, lsum[r]);
+        op[2] = __fdiv_rn(num.z, lsum[r]);
+        op[3] = __fdiv_rn(num.w, lsum[r]);
     }
 }
 
@@ -382,7 +407,7 @@ hipError_t launch_attention_hd(const float* q, const float* kc, const float* vc,
                                hipStream_t stream) {
     const int L_max = pos0 + rows;
     int S = attention_splits(rows, pos0, n_kv);
-    if ((size_t)rows * n_head * S * (HD + 2) > part_floats || !counters) S = 1;
+    if ((size_t)rows * n_head * S * (HD + 4) > part_floats || !counters) S = 1;
     const int split_len = ((L_max + S - 1) / S + kChunk - 1) / kChunk * kChunk;
     S = (L_max + split_len - 1) / split_len;
     const float scale = 1.0f / std::sqrt((float)HD);  // engine.cpp:121, IEEE on the host
@@ -695,7 +720,7 @@ hipError_t launch_rope_neox(float* x, int rows, int n_heads, float* x2, int n_he
 size_t attention_workspace_bytes(int rows, int n_head, int head_dim) {
     // at most 1024 / (n_kv * rows) + 1 splits, n_kv >= 1
     const size_t splits = (size_t)(1024 / std::max(rows, 1) + 1);
-    return kAttnCounters * sizeof(int) + (size_t)rows * n_head * splits * (head_dim + 2) * sizeof(float);
+    return kAttnCounters * sizeof(int) + (size_t)rows * n_head * splits * (head_dim + 4) * sizeof(float);
 }
 
 namespace {
