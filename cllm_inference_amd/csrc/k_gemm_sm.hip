@@ -91,7 +91,8 @@ __device__ __forceinline__ long as_long(u32x2 v) { return __builtin_bit_cast(lon
 
 // FUSED: x holds fp32 activation rows [m][k], quantized here (q8_quant_quad, bit for bit as
 // quantize_row_q8_0); else qs / xs / xb hold the Q8_0 batch. Activation rows past m are zeros.
-template <uint32_t T, int MT, bool FUSED>
+// LATE (from a quantized batch, one item per wave): item 0 is issued after the staging.
+template <uint32_t T, int MT, bool FUSED, bool LATE>
 __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
     const uint8_t* __restrict__ w, int64_t row_bytes, int k, int n, int m, int kc, int kp,
     const float* __restrict__ x, const int8_t* __restrict__ qs, const float* __restrict__ xs,
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
             bv[j] = KQ ? xb[(size_t)t * (k / 32) + k0 / 32 + b] : 0;
         }
         dep = opaque_zero(qs, xs, xb);
-        load_item(0, dep);
+        if constexpr (!LATE) load_item(0, dep);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int i = threadIdx.x + 1024 * j;
@@ -229,6 +230,11 @@ __global__ __launch_bounds__(64 * kSmWaves) void k_gemm_sm(
                 if constexpr (KQ) axm[t * nb + b] = t < m ? dv[j] * (float)bv[j] : 0.0f;
             }
         }
+        // LATE (one item per wave): its weights go out once the activations are in. Issued
+        // beside them they share the first burst's queues, and the staging, which every wave
+        // waits for, returns later. With more items the early item 0 starts the wave's chain
+        // of round trips sooner.
+        if constexpr (LATE) load_item(0, dep);
     }
     sm_barrier();
 
@@ -615,21 +621,21 @@ size_t sm_slices_bytes(const SmPlan& p, int n) {
     return (size_t)p.splits * ((n + 15) / 16) * p.mt * 1024;
 }
 
-template <uint32_t T, int MT, bool FUSED>
+template <uint32_t T, int MT, bool FUSED, bool LATE>
 hipError_t launch_sm_k(const uint8_t* w, int k, int n, int m, const SmPlan& p, const float* x,
                         const int8_t* qs, const float* xs, const int32_t* xb, const float* bias,
                         float* y, float* part, int* counters, hipStream_t stream) {
     const size_t shmem = sm_layout<T, MT>(p.kc).total;
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_sm<T, MT, FUSED>,
+        const hipError_t e = hipFuncSetAttribute((const void*)k_gemm_sm<T, MT, FUSED, LATE>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)sm_layout<T, MT>(kSmActBytes / (16 * MT)).total);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const int64_t row_bytes = (int64_t)(k / block_elems(T)) * block_bytes(T);
-    hipLaunchKernelGGL((k_gemm_sm<T, MT, FUSED>), dim3((unsigned)p.grid_x, (unsigned)p.splits),
+    hipLaunchKernelGGL((k_gemm_sm<T, MT, FUSED, LATE>), dim3((unsigned)p.grid_x, (unsigned)p.splits),
                        dim3(64 * kSmWaves), shmem, stream, w, row_bytes, k, n, m, p.kc, p.kp, x, qs,
                        xs, xb, bias, y, part, counters);
     return hipGetLastError();
@@ -640,11 +646,25 @@ template <uint32_t T, bool FUSED>
 hipError_t launch_sm_mt(const uint8_t* w, int k, int n, int m, const SmPlan& p, const float* x,
                         const int8_t* qs, const float* xs, const int32_t* xb, const float* bias,
                         float* y, float* part, int* counters, hipStream_t stream) {
+    // from a quantized batch with one item per wave, item 0 goes out after the staging
+    // (Q8_0 4096x4096, us: 16 rows 11.71 -> 11.39, 64 rows 19.39 -> 19.06; with four items per
+    // wave, Q5_K 14336x4096 at 16 rows, the late issue lost: 17.94 -> 18.50)
+    if constexpr (!FUSED) {
+        if (p.kc <= 256 * p.kp) {
+            switch (p.mt) {
+                case 1: return launch_sm_k<T, 1, false, true>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+                case 2: return launch_sm_k<T, 2, false, true>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+                case 3: return launch_sm_k<T, 3, false, true>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+                case 4: return launch_sm_k<T, 4, false, true>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+                default: return hipErrorInvalidValue;
+            }
+        }
+    }
     switch (p.mt) {
-        case 1: return launch_sm_k<T, 1, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
-        case 2: return launch_sm_k<T, 2, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
-        case 3: return launch_sm_k<T, 3, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
-        case 4: return launch_sm_k<T, 4, FUSED>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+        case 1: return launch_sm_k<T, 1, FUSED, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+        case 2: return launch_sm_k<T, 2, FUSED, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+        case 3: return launch_sm_k<T, 3, FUSED, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
+        case 4: return launch_sm_k<T, 4, FUSED, false>(w, k, n, m, p, x, qs, xs, xb, bias, y, part, counters, stream);
         default: return hipErrorInvalidValue;
     }
 }
