@@ -1275,8 +1275,9 @@ __global__ __launch_bounds__(64 * WV) void k_gemv_str(GemvSegs sg, int64_t row_b
         sc.issue();
     // LATE: item 0 goes out once the activation is staged, so that the staging's loads do not
     // share the device's first burst of weight requests (the fused quantization, several
-    // rows, and rows longer than 8192 gained; one pre-quantized row of 4096 lost)
-    constexpr bool LATE = (FUSED || MR >= 2 || XR == 0) && !NORM;
+    // rows, and rows longer than 8192 gained; one pre-quantized row of 4096 lost, and so did
+    // one fused Q5_K row of 4096 by 0.1 us)
+    constexpr bool LATE = (FUSED || MR >= 2 || XR == 0) && !NORM && !(T == T_Q5_K && MR == 1 && XR > 0);
     const uint32_t dep0 = FUSED ? opaque_zero(x_f32, sg.norm_w) : opaque_zero(qs, xs, xb);
     if constexpr (!LATE) load_item(row >= 0 ? row : r0, 0, dep0);
     if constexpr (FUSED) {
